@@ -1,0 +1,238 @@
+#!/usr/bin/env python3
+"""Q4_K matvec effective HBM bandwidth on one MI355X.
+
+Workload: Q4_K weights 14336 x 4096 (the 8B-class gate/up projection) times
+one fp32 activation vector (decode, N = 1), plus the same matrix at N = 8
+(the small-N path) reported beside it. A step is one kernel launch over one
+weight matrix; weights and activations are resident in HBM before timing.
+
+- Enough distinct weight copies rotate to exceed twice the 256 MB Infinity
+  Cache, so every step streams its weights from HBM.
+- Launches are captured once into a HIP graph and replayed, so host launch
+  overhead cannot leave the GPU idle; HIP events on that stream bracket the
+  timed steps.
+- `value` = algorithmic bytes per step (packed weights + 4*cols*N +
+  4*rows*N) / average step time.
+- cpu_baseline: the reference CPU provider (built from the reference sources
+  into oracle/_ref) on the same weights, on this host's cores; else this
+  repository's C port of the scalar path.
+
+Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+from fyodor_amd import Q4_K, storage_bytes, synth  # noqa: E402
+from fyodor_amd.hip import Kernels, Runtime  # noqa: E402
+
+METRIC = "Q4_K matvec effective HBM GB/s (% of peak), 14336x4096, N=1 and N=8"
+ROWS, COLS = 14336, 4096
+PEAK_HBM_GBS = 8000.0
+MALL_BYTES = 256 * 1024 * 1024
+
+
+def algorithmic_bytes(rows: int, cols: int, batch: int) -> int:
+    return storage_bytes(Q4_K, rows, cols) + 4 * cols * batch + 4 * rows * batch
+
+
+class Graph:
+    """A captured sequence of launches on one stream (hipGraph)."""
+
+    def __init__(self, rt: Runtime, stream: int, launches):
+        L = rt.lib
+        vp = ctypes.c_void_p
+        L.hipStreamBeginCapture.argtypes = [vp, ctypes.c_int]
+        L.hipStreamEndCapture.argtypes = [vp, ctypes.POINTER(vp)]
+        L.hipGraphInstantiate.argtypes = [ctypes.POINTER(vp), vp, vp, vp, ctypes.c_size_t]
+        L.hipGraphLaunch.argtypes = [vp, vp]
+        L.hipGraphExecDestroy.argtypes = [vp]
+        L.hipGraphDestroy.argtypes = [vp]
+        self.rt, self.stream = rt, stream
+        rt.check(L.hipStreamBeginCapture(stream, 0), "hipStreamBeginCapture")
+        try:
+            for launch in launches:
+                launch()
+        finally:
+            graph = vp()
+            rt.check(L.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
+        self.graph = graph
+        self.exec = vp()
+        rt.check(L.hipGraphInstantiate(ctypes.byref(self.exec), graph, None, None, 0), "hipGraphInstantiate")
+
+    def launch(self):
+        self.rt.check(self.rt.lib.hipGraphLaunch(self.exec, self.stream), "hipGraphLaunch")
+
+    def close(self):
+        self.rt.lib.hipGraphExecDestroy(self.exec)
+        self.rt.lib.hipGraphDestroy(self.graph)
+
+
+def time_steps(rt, kern, stream, weights, x_dev, y_dev, batch, steps, warmup, mode):
+    """Average milliseconds per step over `steps` timed launches."""
+    copies = len(weights)
+
+    def launch(i):
+        return lambda: kern.matmul(weights[i % copies], Q4_K, ROWS, COLS, x_dev, y_dev, batch, 0, 0, stream)
+
+    start, end = rt.event(), rt.event()
+    if mode == "graph":
+        warm = Graph(rt, stream, [launch(i) for i in range(max(warmup, 1))])
+        timed = Graph(rt, stream, [launch(i) for i in range(steps)])
+        warm.launch()
+        rt.sync(stream)
+        rt.record(start, stream)
+        timed.launch()
+        rt.record(end, stream)
+        ms = rt.elapsed_ms(start, end)
+        warm.close()
+        timed.close()
+    else:
+        for i in range(warmup):
+            launch(i)()
+        rt.sync(stream)
+        rt.record(start, stream)
+        for i in range(steps):
+            launch(i)()
+        rt.record(end, stream)
+        ms = rt.elapsed_ms(start, end)
+    rt.sync(stream)
+    return ms / steps
+
+
+def cpu_baseline(weights_host: np.ndarray, x: np.ndarray, y_gpu: np.ndarray, seconds: float) -> dict:
+    """The reference CPU provider (or the C port) on the same workload."""
+    sys.path.insert(0, str(REPO))
+    from oracle import Oracle, Reference  # the checker; only this leg uses it
+
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    os.environ["NYA_CPU_THREADS"] = str(threads)
+    copies = [weights_host] + [weights_host.copy() for _ in range(3)]  # > any L3
+    y = np.empty(ROWS, dtype=np.float32)
+    times = []
+    if Reference.available():
+        ref = Reference()
+        ctx = ref.cpu_provider()
+        kind = "reference"
+
+        def run(w):
+            ref.provider_matmul(ctx, w, Q4_K, x, ROWS, COLS, 1, y)
+    else:
+        orc = Oracle()
+        kind, ctx = "port", None
+
+        def run(w):
+            y[:] = orc.matmul(w, Q4_K, x, ROWS, COLS, 1, threads=threads)[0]
+    run(copies[0])
+    parity = float(np.linalg.norm(y_gpu.astype(np.float64) - y) / np.linalg.norm(y.astype(np.float64)))
+    run(copies[1])
+    began = time.perf_counter()
+    i = 0
+    while (time.perf_counter() - began < seconds or len(times) < 5) and len(times) < 5000:
+        t0 = time.perf_counter()
+        run(copies[i % len(copies)])
+        times.append(time.perf_counter() - t0)
+        i += 1
+    if ctx is not None:
+        ref.free(ctx)
+    med = float(np.median(times))
+    gbs = algorithmic_bytes(ROWS, COLS, 1) / med / 1e9
+    return {
+        "value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": kind,
+        "sample": f"{len(times)} Q4_K 14336x4096 N=1 matvecs over 4 rotating host copies of the same "
+                  f"synthetic weights, median time {med * 1e3:.3f} ms"
+                  + (" (reference backend/core/cpu_backend.c provider, NYA_CPU_THREADS)" if kind == "reference"
+                     else " (scalar C port, rows split over threads)"),
+        "parity_rel_l2_vs_gpu": parity,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--launch", choices=["graph", "stream"], default="graph")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (rows would be sharded "
+              "across GPUs with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    rt = Runtime()
+    kern = Kernels()
+    stream = rt.stream()
+    wbytes = storage_bytes(Q4_K, ROWS, COLS)
+    copies = max(2, math.ceil(2 * MALL_BYTES / wbytes) + 2)
+    host_w = synth.weights(Q4_K, ROWS, COLS, seed=1234)
+    dev_w = kern.device_weights(host_w, Q4_K, ROWS, COLS)
+    weights = []
+    for _ in range(copies):
+        p = rt.malloc(wbytes)
+        rt.upload(p, dev_w)
+        weights.append(p)
+    x8 = synth.activations(8, COLS, seed=1234)
+    x_dev = rt.malloc(x8.nbytes)
+    rt.upload(x_dev, x8)
+    y_dev = rt.malloc(8 * ROWS * 4)
+
+    results = {}
+    for batch in (1, 8):
+        ms = time_steps(rt, kern, stream, weights, x_dev, y_dev, batch, args.steps, args.warmup, args.launch)
+        nbytes = algorithmic_bytes(ROWS, COLS, batch)
+        results[batch] = (ms, nbytes / (ms * 1e-3) / 1e9, nbytes)
+
+    # One plain N=1 call for the parity figure next to the CPU baseline.
+    kern.matmul(weights[0], Q4_K, ROWS, COLS, x_dev, y_dev, 1, 0, 0, stream)
+    rt.sync(stream)
+    y1 = rt.download(y_dev, np.empty(ROWS, dtype=np.float32))
+
+    ms1, gbs1, bytes1 = results[1]
+    ms8, gbs8, bytes8 = results[8]
+    line = {
+        "metric": METRIC,
+        "value": round(gbs1, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms1, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded Q4_K blocks, x ~ N(0,1))",
+        "config": {"workload": "Q4_K matvec 14336x4096, N=1 (decode)", "rows": ROWS, "cols": COLS,
+                   "batch": 1, "weight_copies": copies, "launch": args.launch,
+                   "kernel": kern.kernel_name(Q4_K, ROWS, COLS, 1), "device": rt.device_name()},
+        "roofline": {"bound": "hbm", "achieved": round(gbs1, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs1 / PEAK_HBM_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": bytes1},
+        "n8": {"value": round(gbs8, 2), "unit": "GB/s", "ms_per_step": round(ms8, 6),
+               "frac": round(gbs8 / PEAK_HBM_GBS, 4), "algorithmic_bytes": bytes8,
+               "kernel": kern.kernel_name(Q4_K, ROWS, COLS, 8)},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(host_w, x8[0].copy(), y1, args.cpu_seconds)
+    for p in weights:
+        rt.free(p)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

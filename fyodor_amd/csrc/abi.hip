@@ -1,0 +1,97 @@
+// extern "C" entry points of libfyodor_hip.so (declared in include/fyodor_hip.h).
+#include <limits.h>
+#include <stdint.h>
+#include <string.h>
+#include "../../include/fyodor_hip.h"
+#include "formats.h"
+#include "kernels.h"
+
+namespace {
+
+using namespace fy;
+
+// Same acceptance rules as the provider's request validation
+// (backend/core/vendor.c:59-80) applied to packed storage.
+bool storage_bytes(unsigned type, size_t rows, size_t cols, size_t *bytes)
+{
+    format_info f;
+    if (!format_of(type, &f)) return false;
+    if (!rows || !cols || rows > INT_MAX || cols > INT_MAX || cols % f.block) return false;
+    const size_t blocks = cols / f.block;
+    if (blocks > SIZE_MAX / f.bytes) return false;
+    const size_t row = blocks * f.bytes;
+    if (rows > SIZE_MAX / row) return false;
+    *bytes = rows * row;
+    return true;
+}
+
+int status(hipError_t e)
+{
+    return e == hipSuccess ? 0 : -(int)(e > 0 ? e : 1);
+}
+
+}  // namespace
+
+extern "C" {
+
+NYA_HIP_EXPORT unsigned nya_hip_abi_version(void) { return NYA_HIP_ABI_VERSION; }
+
+NYA_HIP_EXPORT int nya_hip_weight_bytes(unsigned type, size_t rows, size_t cols, size_t *bytes)
+{
+    size_t b;
+    if (!bytes || !storage_bytes(type, rows, cols, &b)) return 1;
+    *bytes = b;
+    return 0;
+}
+
+NYA_HIP_EXPORT int nya_hip_weight_layout(unsigned type)
+{
+    format_info f;
+    if (!format_of(type, &f)) return -1;
+    return type == Q4_0 || type == Q8_0 || type == Q6_K ? 1 : 0;
+}
+
+NYA_HIP_EXPORT int nya_hip_weight_pack(void *dst, const void *src, unsigned type, size_t rows, size_t cols)
+{
+    size_t b;
+    if (!dst || !src || !storage_bytes(type, rows, cols, &b)) return 1;
+    pack_planes((uint8_t *)dst, (const uint8_t *)src, type, rows, cols);
+    return 0;
+}
+
+NYA_HIP_EXPORT int nya_hip_workspace_bytes(unsigned type, size_t rows, size_t cols, size_t batch, size_t *bytes)
+{
+    size_t b;
+    if (!bytes || !batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return 1;
+    *bytes = 0;
+    return 0;
+}
+
+NYA_HIP_EXPORT int nya_hip_matmul(uintptr_t w, unsigned type, size_t rows, size_t cols,
+    uintptr_t x, uintptr_t y, size_t batch, uintptr_t workspace, size_t workspace_bytes, uintptr_t stream)
+{
+    (void)workspace; (void)workspace_bytes;
+    size_t b;
+    if (!w || !x || !y || !batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return 1;
+    // 16-byte weight loads and 4-byte activation/output accesses.
+    if ((w & 15u) || (x & 3u) || (y & 3u)) return 1;
+    hipStream_t s = (hipStream_t)stream;
+    const uint8_t *wp = (const uint8_t *)w;
+    for (size_t done = 0; done < batch; done += 8) {
+        const int n = (int)(batch - done < 8 ? batch - done : 8);
+        const float *xp = (const float *)x + done * cols;
+        float *yp = (float *)y + done * rows;
+        const int st = status(launch_skinny(type, wp, xp, yp, (int)rows, (int)cols, n, s));
+        if (st) return st;
+    }
+    return 0;
+}
+
+NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_t cols, size_t batch)
+{
+    size_t b;
+    if (!batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return NULL;
+    return skinny_name(type, batch < 8 ? (int)batch : 8);
+}
+
+}  // extern "C"

@@ -1,0 +1,100 @@
+/* Caller-facing compute API of the quantized matrix path.
+ *
+ * This header restates the consumer contract of the engine's compute layer
+ * (backend/include/compute.h:1-90) so that the ROCm provider in
+ * fyodor_amd/rocm/rocm.c compiles unchanged both here and inside the
+ * reference tree. Every type below has the same tag, field order and
+ * enumerator values as the reference because provider and engine exchange
+ * them by address.
+ *
+ * A context is used by one thread at a time and must be freed before the
+ * borrowed weight memory it has cached is released
+ * (backend/include/compute.h:6-8). */
+#ifndef NYA_COMPUTE_H
+#define NYA_COMPUTE_H
+
+#include <stddef.h>
+
+typedef struct nya_compute_context nya_compute_context;
+
+/* backend/include/compute.h:10 */
+typedef enum nya_backend_type {
+    NYA_BACKEND_CPU, NYA_BACKEND_CUDA, NYA_BACKEND_VULKAN, NYA_BACKEND_ROCM, NYA_BACKEND_MLX
+} nya_backend_type;
+
+/* Capability bits, backend/include/compute.h:11-12. */
+enum {
+    NYA_COMPUTE_MATVEC = 1U,
+    NYA_COMPUTE_QUANTIZED = 2U,
+    NYA_COMPUTE_RESIDENT = 4U,
+    NYA_COMPUTE_MATMUL = 8U
+};
+
+/* Resource and dispatch counters, backend/include/compute.h:13-22.
+ * external_matmul_kind: 0 native kernels, 1 cuBLAS, 2 CUTLASS 3xTF32,
+ * 3 rocBLAS F32, 4 MLX F32. This provider reports 0 (its own kernels). */
+typedef struct nya_compute_stats {
+    size_t weights_bytes, kv_bytes, scratch_bytes, prefill_batch;
+    size_t external_matmul_bytes;
+    unsigned long long kernel_launches, uploads, downloads, synchronizations;
+    unsigned long long external_matmul_calls;
+    unsigned long long graph_captures, graph_replays;
+    unsigned external_matmul_kind;
+    unsigned long long cutlass_matmul_calls;
+    unsigned long long tiled_attention_calls;
+} nya_compute_stats;
+
+/* Host F32 attention view, backend/include/compute.h:28-33. Only its
+ * address crosses the provider vtable; this provider does not implement it. */
+typedef struct nya_compute_attention {
+    const float *query, *keys, *values;
+    float *output;
+    size_t batch, heads, kv_heads, width, capacity, position, window;
+    float scale;
+} nya_compute_attention;
+
+typedef struct nya_compute_plan nya_compute_plan;
+struct nya_llm_context;
+
+/* Provider selection (backend/include/compute.h:53-62). NULL selects the
+ * provider named by NYA_COMPUTE; a NULL result leaves the caller on its CPU
+ * kernels. */
+nya_compute_context *nya_compute_create(void);
+nya_compute_context *nya_compute_create_for(const char *provider);
+int nya_compute_backend_known(const char *provider);
+int nya_compute_backend_compiled(const char *provider);
+void nya_compute_context_stats(const nya_compute_context *context, nya_compute_stats *stats);
+void nya_compute_free(nya_compute_context *context);
+unsigned nya_compute_capabilities(const nya_compute_context *context);
+/* Name of the provider that is actually active: "cpu" once a provider has
+ * failed (backend/include/compute.h:85-86). */
+const char *nya_compute_name(const nya_compute_context *context);
+
+/* Row-major matrix times vector (backend/include/compute.h:68-79).
+ * Returns 0 when output is ready and -1 when the caller must run its CPU
+ * kernel instead. Weights are borrowed and immutable for the context's life. */
+int nya_compute_matvec(nya_compute_context *context, const void *weights,
+    size_t rows, size_t columns, const float *input, float *output);
+int nya_compute_matvec_typed(nya_compute_context *context, const void *weights,
+    size_t rows, size_t columns, unsigned int type, const float *input, float *output);
+/* Batch-major activations [batch][columns] and output [batch][rows]
+ * (backend/include/compute.h:80-83). */
+int nya_compute_matmul_typed(nya_compute_context *context, const void *weights,
+    size_t rows, size_t columns, unsigned type, const float *input, float *output, size_t batch);
+
+/* Resident plans and attention (backend/include/compute.h:34-51). The ROCm
+ * provider has no RESIDENT capability, so these dispatch to NULL entries and
+ * report "unavailable" (NULL / -1), exactly as for the reference provider. */
+int nya_compute_attention_f32(nya_compute_context *context, const nya_compute_attention *attention);
+nya_compute_plan *nya_compute_plan_create(nya_compute_context *context,
+    const struct nya_llm_context *model, size_t capacity);
+void nya_compute_plan_free(nya_compute_plan *plan);
+int nya_compute_plan_token(nya_compute_plan *plan, unsigned int token, size_t position,
+    int logits, float *output);
+int nya_compute_plan_prefill(nya_compute_plan *plan, const unsigned int *tokens,
+    size_t count, size_t position, float *output);
+void nya_compute_plan_stats(const nya_compute_plan *plan, nya_compute_stats *stats);
+int nya_compute_plan_read_kv(nya_compute_plan *plan, size_t layer, size_t position,
+    size_t count, float *keys, float *values, size_t elements);
+
+#endif

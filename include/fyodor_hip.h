@@ -1,0 +1,95 @@
+/* C ABI of the gfx950 quantized matrix kernel library (libfyodor_hip.so).
+ *
+ * The ROCm provider (fyodor_amd/rocm/rocm.c) resolves these symbols with
+ * dlopen/dlsym, the same way the reference provider resolves the HIP runtime
+ * and rocBLAS (rocm/rocm.c:155-166, rocm/abi.h:8-26). They replace the one
+ * rocBLAS call on the reference path, rocblas_sgemm(T,N) over host-expanded
+ * F32 weights (rocm/rocm.c:123-128), with kernels that read the GGUF block
+ * formats directly.
+ *
+ * Conventions follow the reference's versioned GPU-library bridge
+ * (CUDA/cutlass/bridge.h:1-23): device addresses and the stream are passed as
+ * uintptr_t and stay owned by the caller; the library never allocates,
+ * frees or synchronizes them. Return codes:
+ *     0  enqueued on the stream (or, for queries, answered);
+ *     1  declined before anything was enqueued (unsupported type or shape);
+ *    <0  HIP failure after a possible enqueue; the caller must treat its
+ *        device state as failed and recompute the whole request elsewhere.
+ *
+ * Layouts (backend/include/compute.h:80-83, rocm/rocm.c:124-126):
+ *     W  [rows][cols] in the device weight layout produced by
+ *        nya_hip_weight_prepare from GGUF row-major block storage;
+ *     X  [batch][cols] fp32, each batch entry contiguous;
+ *     Y  [batch][rows] fp32.
+ */
+#ifndef FYODOR_HIP_H
+#define FYODOR_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define NYA_HIP_EXPORT __attribute__((visibility("default")))
+#else
+#define NYA_HIP_EXPORT
+#endif
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NYA_HIP_ABI_VERSION 1U
+
+/* GGML storage type IDs (backend/core/llm_internal.h:11-19). */
+enum {
+    NYA_HIP_F32 = 0, NYA_HIP_F16 = 1, NYA_HIP_Q4_0 = 2, NYA_HIP_Q8_0 = 8,
+    NYA_HIP_Q4_K = 12, NYA_HIP_Q6_K = 14, NYA_HIP_BF16 = 30
+};
+
+/* Version handshake, as nya_cutlass_abi_version (CUDA/cutlass/bridge.h:17).
+ * Returns NYA_HIP_ABI_VERSION. */
+NYA_HIP_EXPORT unsigned nya_hip_abi_version(void);
+
+/* Device bytes of a [rows][cols] matrix of `type`. This always equals its
+ * GGUF storage size: the device layout only moves bytes. Replaces the F32
+ * size from nya_vendor_matrix (backend/core/vendor.c:59-80), which the
+ * reference uploads after host expansion. Returns 0, or 1 for an unsupported
+ * type or shape (cols not a multiple of the block, a zero or
+ * above-INT_MAX dimension, or a size_t overflow). */
+NYA_HIP_EXPORT int nya_hip_weight_bytes(unsigned type, size_t rows, size_t cols, size_t *bytes);
+
+/* Whether the device layout of `type` differs from GGUF storage:
+ * 0 the GGUF bytes are uploaded as they are (F32, F16, BF16, Q4_K);
+ * 1 they must first pass through nya_hip_weight_pack (Q4_0, Q8_0, Q6_K,
+ *   whose 18/34/210-byte blocks are split into 16-byte aligned planes);
+ * -1 unsupported type. */
+NYA_HIP_EXPORT int nya_hip_weight_layout(unsigned type);
+
+/* Host-side (CPU) conversion of GGUF bytes `src` into the device layout at
+ * `dst`, both host memory of nya_hip_weight_bytes bytes, not overlapping.
+ * Replaces the host F32 decode of the reference weight upload
+ * (rocm/rocm.c:90-94, backend/core/vendor.c:81-85) with a byte
+ * permutation of the same size. Returns 0, or 1 when unsupported. */
+NYA_HIP_EXPORT int nya_hip_weight_pack(void *dst, const void *src, unsigned type,
+    size_t rows, size_t cols);
+
+/* Device workspace that nya_hip_matmul needs for this request (0 when none).
+ * Returns 0, or 1 when the request is unsupported. */
+NYA_HIP_EXPORT int nya_hip_workspace_bytes(unsigned type, size_t rows, size_t cols,
+    size_t batch, size_t *bytes);
+
+/* Enqueue Y = X * W^T for batch >= 1 (replaces rocm/rocm.c:127-128).
+ * batch 1 is the decode matvec, batch 2..8 the small-N path and larger
+ * batches the prefill GEMM. `workspace` holds at least the bytes reported
+ * by nya_hip_workspace_bytes for the same arguments (it may be 0 then). */
+NYA_HIP_EXPORT int nya_hip_matmul(uintptr_t w, unsigned type, size_t rows, size_t cols,
+    uintptr_t x, uintptr_t y, size_t batch, uintptr_t workspace, size_t workspace_bytes,
+    uintptr_t stream);
+
+/* Name of the main kernel nya_hip_matmul launches for these arguments, as it
+ * appears in a rocprofv3 kernel trace, or NULL when unsupported. Diagnostic
+ * only; it launches nothing. */
+NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_t cols, size_t batch);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

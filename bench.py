@@ -159,6 +159,20 @@ def cpu_baseline(weights_host: np.ndarray, x: np.ndarray, y_gpu: np.ndarray, sec
     }
 
 
+def calibrate_copy(rt, kern, stream, steps: int) -> int:
+    """Copies of a known size: rocprofv3 FETCH_SIZE / WRITE_SIZE per
+    dispatch divided into these bytes give the counters' scale factor."""
+    nbytes = 256 << 20
+    src, dst = rt.malloc(nbytes), rt.malloc(nbytes)
+    for _ in range(steps):
+        kern.copy(dst, src, nbytes, stream)
+    rt.sync(stream)
+    rt.free(src)
+    rt.free(dst)
+    print(json.dumps({"calibration": "nya_hip_copy", "read_bytes": nbytes, "write_bytes": nbytes, "launches": steps}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -167,6 +181,8 @@ def main() -> int:
     ap.add_argument("--launch", choices=["graph", "stream"], default="graph")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only the plain 256 MiB device copy used to calibrate HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (rows would be sharded "
@@ -176,6 +192,8 @@ def main() -> int:
     rt = Runtime()
     kern = Kernels()
     stream = rt.stream()
+    if args.calibrate_copy:
+        return calibrate_copy(rt, kern, stream, max(args.steps, 1))
     wbytes = storage_bytes(Q4_K, ROWS, COLS)
     copies = max(2, math.ceil(2 * MALL_BYTES / wbytes) + 2)
     host_w = synth.weights(Q4_K, ROWS, COLS, seed=1234)

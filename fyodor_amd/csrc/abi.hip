@@ -48,7 +48,7 @@ NYA_HIP_EXPORT int nya_hip_weight_layout(unsigned type)
 {
     format_info f;
     if (!format_of(type, &f)) return -1;
-    return type == Q4_0 || type == Q8_0 || type == Q6_K ? 1 : 0;
+    return type == F32 || type == F16 || type == BF16 ? 0 : 1;
 }
 
 NYA_HIP_EXPORT int nya_hip_weight_pack(void *dst, const void *src, unsigned type, size_t rows, size_t cols)
@@ -73,15 +73,17 @@ NYA_HIP_EXPORT int nya_hip_matmul(uintptr_t w, unsigned type, size_t rows, size_
     (void)workspace; (void)workspace_bytes;
     size_t b;
     if (!w || !x || !y || !batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return 1;
-    // 16-byte weight loads and 4-byte activation/output accesses.
-    if ((w & 15u) || (x & 3u) || (y & 3u)) return 1;
+    // 16-byte weight and activation loads, 4-byte outputs.
+    if ((w & 15u) || (x & 15u) || (y & 3u)) return 1;
+    const bool dense = type == F32 || type == F16 || type == BF16;
     hipStream_t s = (hipStream_t)stream;
     const uint8_t *wp = (const uint8_t *)w;
     for (size_t done = 0; done < batch; done += 8) {
         const int n = (int)(batch - done < 8 ? batch - done : 8);
         const float *xp = (const float *)x + done * cols;
         float *yp = (float *)y + done * rows;
-        const int st = status(launch_skinny(type, wp, xp, yp, (int)rows, (int)cols, n, s));
+        const int st = status(dense ? launch_dense(type, wp, xp, yp, (int)rows, (int)cols, n, s)
+                                    : launch_quant_matvec(type, wp, xp, yp, (int)rows, (int)cols, n, s));
         if (st) return st;
     }
     return 0;
@@ -91,7 +93,13 @@ NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_
 {
     size_t b;
     if (!batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return NULL;
-    return skinny_name(type, batch < 8 ? (int)batch : 8);
+    return type == F32 || type == F16 || type == BF16 ? "skinny_dense" : "quant_matvec";
+}
+
+NYA_HIP_EXPORT int nya_hip_copy(uintptr_t dst, uintptr_t src, size_t bytes, uintptr_t stream)
+{
+    if (!dst || !src || (dst & 15u) || (src & 15u) || (bytes & 15u)) return 1;
+    return status(launch_copy((uint4 *)dst, (const uint4 *)src, bytes / 16, (hipStream_t)stream));
 }
 
 }  // extern "C"

@@ -14,15 +14,21 @@
 //             | (((qh[32h + l] >> 2q) & 3) << 4),
 //        w = d * sc[n/16] * (q6 - 32).
 //
-// Device layouts keep exactly the GGUF byte count. F32/F16/BF16 and Q4_K
-// (144 = 9 x 16 bytes) are uploaded unchanged. Q4_0, Q8_0 and Q6_K blocks are
-// not multiples of 16 bytes, so their matrices are split into planes, each
-// row-major over all rows and 16-byte aligned:
-//   Q8_0: [quants rows*nb*32][d rows*nb*2]
-//   Q4_0: [quants rows*nb*16][d rows*nb*2]
-//   Q6_K: [ql|qh rows*ns*192][sc rows*ns*16][d rows*ns*2]
-// where nb = cols/32 and ns = cols/256. Inside a plane the bytes of a block
-// keep their GGUF order.
+// Device layouts keep exactly the GGUF byte count. F32/F16/BF16 are uploaded
+// unchanged. For the block formats the kernels give each lane one "unit" of
+// a row (64 elements of a K-quant superblock, or one 32-element Q8_0/Q4_0
+// block), so the matrix is stored as field planes indexed by (row, unit):
+// lane u's slice of a field sits at (row * U + u) * size, and the 64 lanes of
+// a wavefront read one contiguous span per load instruction. U = units per
+// row. Planes, each over all rows:
+//   Q4_K (U = cols/64, unit 4s+p): qa 16 B = qs[32p..+16), qb 16 B =
+//        qs[32p+16..+16), slice 4 B = sc(2p) | m(2p)<<6 | sc(2p+1)<<12 |
+//        m(2p+1)<<18 | byte p of (d, dmin) << 24
+//   Q6_K (U = cols/64, unit 4s+2h+l16): a = ql[64h+16*l16..+16),
+//        b = ql[64h+32+16*l16..+16), c = qh[32h+16*l16..+16) (16 B each),
+//        sc 4 B (byte q = sc[8h+2q+l16]), then d 2 B per superblock
+//   Q8_0 (U = cols/32): qa = qs[0..16), qb = qs[16..32), d 2 B
+//   Q4_0 (U = cols/32): q = qs[0..16), d 2 B
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
@@ -49,7 +55,7 @@ inline bool format_of(unsigned type, format_info *f)
     }
 }
 
-// Host-side byte permutation GGUF -> device layout (see the header comment).
+// Host-side byte permutation GGUF -> device layout (see the header comment); pack.cpp.
 void pack_planes(uint8_t *dst, const uint8_t *src, unsigned type, size_t rows, size_t cols);
 
 }  // namespace fy

@@ -7,9 +7,15 @@
 namespace fy {
 
 // Y[n][rows] = sum_k W[row][k] * X[n][k] for n < batch, batch 1..8, W in the
-// device layout. Reads every weight byte once per call.
-hipError_t launch_skinny(unsigned type, const uint8_t *w, const float *x, float *y,
+// device layout. Each reads every weight byte once per call.
+// F32 / F16 / BF16 weights (dense.hip).
+hipError_t launch_dense(unsigned type, const uint8_t *w, const float *x, float *y,
     int rows, int cols, int batch, hipStream_t stream);
-const char *skinny_name(unsigned type, int batch);
+// Q4_0 / Q8_0 / Q4_K / Q6_K weights (matvec.hip); x must be 16-byte aligned.
+hipError_t launch_quant_matvec(unsigned type, const uint8_t *w, const float *x, float *y,
+    int rows, int cols, int batch, hipStream_t stream);
+
+// Plain 16-byte-per-thread device copy (dense.hip), for counter calibration.
+hipError_t launch_copy(uint4 *dst, const uint4 *src, size_t count, hipStream_t stream);
 
 }  // namespace fy

@@ -17,8 +17,8 @@
  *        device state as failed and recompute the whole request elsewhere.
  *
  * Layouts (backend/include/compute.h:80-83, rocm/rocm.c:124-126):
- *     W  [rows][cols] in the device weight layout produced by
- *        nya_hip_weight_prepare from GGUF row-major block storage;
+ *     W  [rows][cols] in the device weight layout: the GGUF row-major
+ *        block storage itself, or its nya_hip_weight_pack permutation;
  *     X  [batch][cols] fp32, each batch entry contiguous;
  *     Y  [batch][rows] fp32.
  */
@@ -57,9 +57,10 @@ NYA_HIP_EXPORT unsigned nya_hip_abi_version(void);
 NYA_HIP_EXPORT int nya_hip_weight_bytes(unsigned type, size_t rows, size_t cols, size_t *bytes);
 
 /* Whether the device layout of `type` differs from GGUF storage:
- * 0 the GGUF bytes are uploaded as they are (F32, F16, BF16, Q4_K);
- * 1 they must first pass through nya_hip_weight_pack (Q4_0, Q8_0, Q6_K,
- *   whose 18/34/210-byte blocks are split into 16-byte aligned planes);
+ * 0 the GGUF bytes are uploaded as they are (F32, F16, BF16);
+ * 1 they must first pass through nya_hip_weight_pack (Q4_0, Q8_0, Q4_K,
+ *   Q6_K, whose blocks are regrouped into per-lane field planes so that
+ *   every kernel load instruction reads one contiguous span);
  * -1 unsupported type. */
 NYA_HIP_EXPORT int nya_hip_weight_layout(unsigned type);
 
@@ -88,6 +89,12 @@ NYA_HIP_EXPORT int nya_hip_matmul(uintptr_t w, unsigned type, size_t rows, size_
  * appears in a rocprofv3 kernel trace, or NULL when unsupported. Diagnostic
  * only; it launches nothing. */
 NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_t cols, size_t batch);
+
+/* Diagnostics, no counterpart in the reference: enqueue a plain device copy
+ * of `bytes` (a multiple of 16, 16-byte aligned pointers) with one 16-byte
+ * load and one 16-byte store per element, used to calibrate HBM read/write
+ * byte counters (rocprofv3 FETCH_SIZE / WRITE_SIZE) against a known size. */
+NYA_HIP_EXPORT int nya_hip_copy(uintptr_t dst, uintptr_t src, size_t bytes, uintptr_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,128 @@
+/* Test-only stand-in for the HIP runtime and libfyodor_hip.so, used to test
+ * the C provider's ownership, layout, error propagation and cache behaviour
+ * on the CPU (the reference tests its provider the same way:
+ * backend/tests/mock_vendor.c, backend/tests/test_vendor.c).
+ *
+ * "Device" memory is host memory. Every fallible call can be made to fail
+ * once with nya_mock_fail_after(n) (the n-th fallible call from now fails);
+ * nya_mock_live() counts allocations and streams not yet released. The
+ * matmul computes in double from GGUF element values (the oracle's decoder).
+ * Its Q8_0 device layout XORs every byte with 0x5A, so a provider that
+ * uploads GGUF bytes where the packed copy belongs produces wrong results. */
+#include <stddef.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define API __attribute__((visibility("default")))
+
+typedef int hipError_t;
+typedef void *hipStream_t;
+
+float orc_value(const unsigned char *data, unsigned type, size_t index);
+
+static int live, countdown, device, calls;
+
+static int fail(void) { ++calls; return countdown > 0 && --countdown == 0; }
+static void *allocate(size_t bytes) { void *p = calloc(1, bytes ? bytes : 1); if (p) ++live; return p; }
+static void release(void *p) { if (p) { --live; free(p); } }
+
+API void nya_mock_fail_after(int n) { countdown = n; }
+API int nya_mock_live(void) { return live; }
+API int nya_mock_calls(void) { return calls; }
+
+API hipError_t hipInit(unsigned flags) { return flags || fail(); }
+API hipError_t hipGetDeviceCount(int *n) { *n = 1; return fail(); }
+API hipError_t hipGetDevice(int *n) { *n = device; return fail(); }
+API hipError_t hipSetDevice(int n) { if (fail() || n) return 1; device = n; return 0; }
+API hipError_t hipMemGetInfo(size_t *free_bytes, size_t *total) { *free_bytes = *total = (size_t)1 << 30; return fail(); }
+API hipError_t hipMalloc(void **p, size_t n) { if (fail()) return 2; *p = allocate(n); return *p ? 0 : 2; }
+API hipError_t hipFree(void *p) { release(p); return 0; }
+API hipError_t hipMemcpyAsync(void *dst, const void *src, size_t n, int kind, hipStream_t stream)
+{
+    if (fail() || !stream || (kind != 1 && kind != 2)) return 1;
+    memcpy(dst, src, n);
+    return 0;
+}
+API hipError_t hipStreamCreateWithFlags(hipStream_t *p, unsigned flags)
+{
+    if (fail() || flags != 1) return 1;
+    *p = allocate(1);
+    return *p ? 0 : 2;
+}
+API hipError_t hipStreamDestroy(hipStream_t p) { release(p); return 0; }
+API hipError_t hipStreamSynchronize(hipStream_t p) { return !p || fail(); }
+
+/* ---- kernel library ---- */
+static int blocks(unsigned type, size_t *block, size_t *bytes)
+{
+    switch (type) {
+    case 0: *block = 1; *bytes = 4; return 0;
+    case 1: case 30: *block = 1; *bytes = 2; return 0;
+    case 2: *block = 32; *bytes = 18; return 0;
+    case 8: *block = 32; *bytes = 34; return 0;
+    case 12: *block = 256; *bytes = 144; return 0;
+    case 14: *block = 256; *bytes = 210; return 0;
+    default: return -1;
+    }
+}
+
+API unsigned nya_hip_abi_version(void) { return 1; }
+API int nya_hip_weight_bytes(unsigned type, size_t rows, size_t cols, size_t *out)
+{
+    size_t block, bytes;
+    if (!out || blocks(type, &block, &bytes) || !rows || !cols || cols % block) return 1;
+    *out = rows * (cols / block) * bytes;
+    return 0;
+}
+API int nya_hip_weight_layout(unsigned type)
+{
+    size_t block, bytes;
+    if (blocks(type, &block, &bytes)) return -1;
+    return type == 8 ? 1 : 0;
+}
+API int nya_hip_weight_pack(void *dst, const void *src, unsigned type, size_t rows, size_t cols)
+{
+    size_t n;
+    if (fail() || nya_hip_weight_bytes(type, rows, cols, &n)) return 1;
+    for (size_t i = 0; i < n; ++i) ((unsigned char *)dst)[i] = ((const unsigned char *)src)[i] ^ 0x5A;
+    return 0;
+}
+API int nya_hip_workspace_bytes(unsigned type, size_t rows, size_t cols, size_t batch, size_t *out)
+{
+    size_t n;
+    if (!out || !batch || nya_hip_weight_bytes(type, rows, cols, &n)) return 1;
+    *out = 0;
+    return 0;
+}
+API int nya_hip_matmul(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x, uintptr_t y,
+    size_t batch, uintptr_t workspace, size_t workspace_bytes, uintptr_t stream)
+{
+    (void)workspace; (void)workspace_bytes;
+    size_t n;
+    if (!w || !x || !y || !stream || nya_hip_weight_bytes(type, rows, cols, &n)) return 1;
+    if (fail()) return -1;
+    const unsigned char *data = (const unsigned char *)w;
+    unsigned char *plain = NULL;
+    if (type == 8) {
+        plain = malloc(n);
+        if (!plain) return -2;
+        for (size_t i = 0; i < n; ++i) plain[i] = data[i] ^ 0x5A;
+        data = plain;
+    }
+    const float *in = (const float *)x;
+    float *out = (float *)y;
+    for (size_t b = 0; b < batch; ++b)
+        for (size_t r = 0; r < rows; ++r) {
+            double sum = 0;
+            for (size_t k = 0; k < cols; ++k) sum += (double)orc_value(data, type, r * cols + k) * in[b * cols + k];
+            out[b * rows + r] = (float)sum;
+        }
+    free(plain);
+    return 0;
+}
+API const char *nya_hip_kernel_name(unsigned type, size_t rows, size_t cols, size_t batch)
+{
+    (void)type; (void)rows; (void)cols; (void)batch;
+    return "mock_matmul";
+}

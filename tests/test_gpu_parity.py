@@ -10,44 +10,13 @@ shapes at relative L2 <= 1e-5 against the scalar oracle on seeded data.
 import numpy as np
 import pytest
 
-from fyodor_amd import BF16, F16, F32, Q4_0, Q4_K, Q6_K, Q8_0, TYPE_NAMES, storage_bytes, synth
+from fyodor_amd import BF16, F16, F32, Q4_0, Q4_K, Q6_K, Q8_0, TYPE_NAMES, synth
+from patterns import batch_inputs, pass_input, pattern_matrix
 
 pytestmark = pytest.mark.gpu
 
 ALL_TYPES = [F32, F16, BF16, Q4_0, Q8_0, Q4_K, Q6_K]
 REL_L2 = 1e-5   # fp32 activations, reordered fp32 accumulation
-
-
-def pattern_matrix(type_id: int, rows: int, cols: int) -> np.ndarray:
-    """The byte/value pattern of backend/tests/test_quant_kernels.c:154-172."""
-    n = storage_bytes(type_id, rows, cols)
-    i = np.arange(n, dtype=np.int64)
-    data = ((i * 73 + i // 17 + 31) & 255).astype(np.uint8)
-    if type_id in (F32, F16, BF16):
-        k = np.arange(rows * cols, dtype=np.int64)
-        value = ((k % 127) - 63).astype(np.float32) / np.float32(64)
-        if type_id == F32:
-            data = value.view(np.uint8).copy()
-        elif type_id == BF16:
-            data = (value.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).copy()
-        else:
-            v = (0x3000 + (k % 1024) + np.where(k % 2 == 1, 0x8000, 0)).astype(np.uint16)
-            data = v.view(np.uint8).copy()
-    else:
-        block = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}[type_id]
-        scale = 208 if type_id == Q6_K else 0
-        starts = np.arange(0, n, block)
-        data[starts + scale] = 0
-        data[starts + scale + 1] = 0x28
-        if type_id == Q4_K:
-            data[starts + 2] = 0
-            data[starts + 3] = 0x24
-    return data
-
-
-def pass_input(cols: int, p: int) -> np.ndarray:
-    i = np.arange(cols)
-    return (((i + p * 3) % 97) - 48).astype(np.float32) / np.float32(49)
 
 
 def check_rows(oracle, w, t, x, rows, cols, actual, scalar=None, first_rows=0):
@@ -68,7 +37,7 @@ def test_reference_kernel_contract(compute, oracle, type_id):
         x = pass_input(cols, p)
         y = compute.matvec_typed(w, rows, cols, type_id, x)
         check_rows(oracle, w, type_id, x, rows, cols, y, oracle.matvec(w, type_id, x, rows, cols), 17)
-    inputs = (((np.arange(65 * cols) % 61) - 30).astype(np.float32) / np.float32(31)).reshape(65, cols)
+    inputs = batch_inputs(65, cols)
     for batch in (3, 17, 65, 32, 8):
         out = np.full(batch * rows + 2, 12345, dtype=np.float32)
         compute.matmul_typed(w, rows, cols, type_id, inputs[:batch], batch, out=out[1:1 + batch * rows])

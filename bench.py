@@ -44,6 +44,21 @@ PEAK_HBM_GBS = 8000.0
 MALL_BYTES = 256 * 1024 * 1024
 
 
+TRAFFIC_PROFILE = REPO / "profiles" / "q4k_matvec_14336x4096_traffic.md"
+
+
+def measured_traffic(batch: int):
+    """HBM bytes per launch from the committed rocprofv3 counter summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of known size), or None."""
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            if line.startswith(f"traffic_n{batch}_bytes:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def algorithmic_bytes(rows: int, cols: int, batch: int) -> int:
     return storage_bytes(Q4_K, rows, cols) + 4 * cols * batch + 4 * rows * batch
 
@@ -238,10 +253,10 @@ def main() -> int:
                    "batch": 1, "weight_copies": copies, "launch": args.launch,
                    "kernel": kern.kernel_name(Q4_K, ROWS, COLS, 1), "device": rt.device_name()},
         "roofline": {"bound": "hbm", "achieved": round(gbs1, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs1 / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(gbs1 / PEAK_HBM_GBS, 4), "traffic": measured_traffic(1),
                      "algorithmic_bytes": bytes1},
         "n8": {"value": round(gbs8, 2), "unit": "GB/s", "ms_per_step": round(ms8, 6),
-               "frac": round(gbs8 / PEAK_HBM_GBS, 4), "algorithmic_bytes": bytes8,
+               "frac": round(gbs8 / PEAK_HBM_GBS, 4), "algorithmic_bytes": bytes8, "traffic": measured_traffic(8),
                "kernel": kern.kernel_name(Q4_K, ROWS, COLS, 8)},
     }
     if not args.no_cpu_baseline:

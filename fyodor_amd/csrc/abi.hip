@@ -93,7 +93,8 @@ NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_
 {
     size_t b;
     if (!batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return NULL;
-    return type == F32 || type == F16 || type == BF16 ? "skinny_dense" : "quant_matvec";
+    if (type == F32 || type == F16 || type == BF16) return "skinny_dense";
+    return quant_matvec_kernel(type, (int)rows, (int)cols, batch < 8 ? (int)batch : 8);
 }
 
 NYA_HIP_EXPORT int nya_hip_copy(uintptr_t dst, uintptr_t src, size_t bytes, uintptr_t stream)

@@ -15,6 +15,8 @@ hipError_t launch_dense(unsigned type, const uint8_t *w, const float *x, float *
 hipError_t launch_quant_matvec(unsigned type, const uint8_t *w, const float *x, float *y,
     int rows, int cols, int batch, hipStream_t stream);
 
+// Name of the kernel launch_quant_matvec uses for these arguments.
+const char *quant_matvec_kernel(unsigned type, int rows, int cols, int batch);
 // Plain 16-byte-per-thread device copy (dense.hip), for counter calibration.
 hipError_t launch_copy(uint4 *dst, const uint4 *src, size_t count, hipStream_t stream);
 

@@ -674,6 +674,15 @@ hipError_t launch_type(const uint8_t *w, const float *x, float *y, int rows, int
 
 }  // namespace
 
+const char *quant_matvec_kernel(unsigned type, int rows, int cols, int batch)
+{
+    (void)rows;
+    const int elems = type == Q8_0 || type == Q4_0 ? 32 : 64;
+    const int split = (cols / elems + 63) / 64;
+    const size_t shared = (size_t)4 * batch * cols + sizeof(float) * 8 * 8 * batch;
+    return split <= kWaves && shared <= (size_t)lds_limit() ? "quant_rows" : "quant_chunked";
+}
+
 hipError_t launch_quant_matvec(unsigned type, const uint8_t *w, const float *x, float *y,
     int rows, int cols, int batch, hipStream_t s)
 {

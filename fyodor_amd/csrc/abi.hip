@@ -25,6 +25,13 @@ bool storage_bytes(unsigned type, size_t rows, size_t cols, size_t *bytes)
     return true;
 }
 
+// Batches above the small-N kernels' 8 columns go to the MFMA GEMM when the
+// type allows it.
+bool use_gemm(unsigned type, size_t cols, size_t batch)
+{
+    return batch > 8 && gemm_supported(type, (int)cols);
+}
+
 int status(hipError_t e)
 {
     return e == hipSuccess ? 0 : -(int)(e > 0 ? e : 1);
@@ -63,14 +70,13 @@ NYA_HIP_EXPORT int nya_hip_workspace_bytes(unsigned type, size_t rows, size_t co
 {
     size_t b;
     if (!bytes || !batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return 1;
-    *bytes = 0;
+    *bytes = use_gemm(type, cols, batch) ? gemm_workspace((int)cols, (int)batch) : 0;
     return 0;
 }
 
 NYA_HIP_EXPORT int nya_hip_matmul(uintptr_t w, unsigned type, size_t rows, size_t cols,
     uintptr_t x, uintptr_t y, size_t batch, uintptr_t workspace, size_t workspace_bytes, uintptr_t stream)
 {
-    (void)workspace; (void)workspace_bytes;
     size_t b;
     if (!w || !x || !y || !batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return 1;
     // 16-byte weight and activation loads, 4-byte outputs.
@@ -78,6 +84,12 @@ NYA_HIP_EXPORT int nya_hip_matmul(uintptr_t w, unsigned type, size_t rows, size_
     const bool dense = type == F32 || type == F16 || type == BF16;
     hipStream_t s = (hipStream_t)stream;
     const uint8_t *wp = (const uint8_t *)w;
+    // The GEMM needs its workspace; without one (or a short one) the batch is
+    // run 8 columns at a time instead.
+    if (use_gemm(type, cols, batch) && workspace && !(workspace & 15u) &&
+        workspace_bytes >= gemm_workspace((int)cols, (int)batch))
+        return status(launch_gemm(type, wp, (const float *)x, (float *)y, (int)rows, (int)cols, (int)batch,
+                                  (void *)workspace, s));
     for (size_t done = 0; done < batch; done += 8) {
         const int n = (int)(batch - done < 8 ? batch - done : 8);
         const float *xp = (const float *)x + done * cols;
@@ -94,6 +106,7 @@ NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_
     size_t b;
     if (!batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return NULL;
     if (type == F32 || type == F16 || type == BF16) return "skinny_dense";
+    if (use_gemm(type, cols, batch)) return "gemm_tile";
     return quant_matvec_kernel(type, (int)rows, (int)cols, batch < 8 ? (int)batch : 8);
 }
 

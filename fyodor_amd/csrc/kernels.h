@@ -15,6 +15,15 @@ hipError_t launch_dense(unsigned type, const uint8_t *w, const float *x, float *
 hipError_t launch_quant_matvec(unsigned type, const uint8_t *w, const float *x, float *y,
     int rows, int cols, int batch, hipStream_t stream);
 
+// Batches above 8 with quantized weights (gemm.hip): MFMA tiles over the
+// whole batch, weights read once per 128 batch rows. gemm_supported says
+// whether the type and width qualify; the launch needs gemm_workspace bytes
+// of 16-byte-aligned device scratch.
+bool gemm_supported(unsigned type, int cols);
+size_t gemm_workspace(int cols, int batch);
+hipError_t launch_gemm(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols, int batch,
+    void *workspace, hipStream_t stream);
+
 // Name of the kernel launch_quant_matvec uses for these arguments.
 const char *quant_matvec_kernel(unsigned type, int rows, int cols, int batch);
 // Plain 16-byte-per-thread device copy (dense.hip), for counter calibration.

@@ -121,3 +121,19 @@ def test_pack_is_the_specified_permutation(kernels, t):
     dev = kernels.device_weights(w, t, rows, cols)
     assert dev.nbytes == w.nbytes and not np.shares_memory(dev, w)
     assert np.array_equal(unpack_reference(dev, t, rows, cols), w)
+
+
+def test_gemm_dispatch_and_workspace():
+    """Batches above 8 of the quantized types ask for the activation pieces'
+    workspace and name the MFMA GEMM; dense types and small batches need
+    none (nothing is launched)."""
+    kern = Kernels()
+    for t in (Q4_0, Q8_0, Q4_K, Q6_K):
+        assert kern.workspace_bytes(t, 4096, 4096, 8) == 0
+        assert kern.workspace_bytes(t, 4096, 4096, 9) == 6 * 4096 * 9
+        assert kern.workspace_bytes(t, 4096, 4096, 512) == 6 * 4096 * 512
+        assert kern.kernel_name(t, 4096, 4096, 512) == "gemm_tile"
+        assert kern.kernel_name(t, 4096, 4096, 8) != "gemm_tile"
+    for t in (F32, BF16):
+        assert kern.workspace_bytes(t, 4096, 4096, 512) == 0
+        assert kern.kernel_name(t, 4096, 4096, 512) == "skinny_dense"

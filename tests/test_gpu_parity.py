@@ -4,29 +4,21 @@ Restates the reference kernel contract backend/tests/test_quant_kernels.c:
 138-213 (all seven storage types, 65 rows, three input passes, a double
 oracle bound of 1e-6 * (1 + sum |w x|) per row, the first 17 rows within
 1.5e-4 * (1 + |y|) of the scalar kernel, matmul batches {3, 17, 65, 32, 8}
-with canaries on both sides of the output), then checks the benchmark
-shapes at relative L2 <= 1e-5 against the scalar oracle on seeded data.
+with canaries on both sides of the output; batches above 8 of the quantized
+types run the MFMA prefill GEMM), then checks the benchmark shapes at
+relative L2 <= 1e-5 against the scalar oracle on seeded data.
 """
 import numpy as np
 import pytest
 
 from fyodor_amd import BF16, F16, F32, Q4_0, Q4_K, Q6_K, Q8_0, TYPE_NAMES, synth
+from checks import check_rows, rel_l2
 from patterns import batch_inputs, pass_input, pattern_matrix
 
 pytestmark = pytest.mark.gpu
 
 ALL_TYPES = [F32, F16, BF16, Q4_0, Q8_0, Q4_K, Q6_K]
 REL_L2 = 1e-5   # fp32 activations, reordered fp32 accumulation
-
-
-def check_rows(oracle, w, t, x, rows, cols, actual, scalar=None, first_rows=0):
-    s, m = oracle.matvec_double(w, t, x, rows, cols)
-    err = np.abs(actual.astype(np.float64) - s)
-    bad = ~np.isfinite(actual) | (err > 1e-6 * (1 + m))
-    assert not bad.any(), f"{TYPE_NAMES[t]} rows {np.nonzero(bad)[0][:5]}: {actual[bad][:3]} vs {s[bad][:3]}"
-    if scalar is not None and first_rows:
-        a, e = actual[:first_rows], scalar[:first_rows]
-        assert np.all(np.abs(a - e) <= np.float32(0.00015) * (1 + np.abs(e)))
 
 
 @pytest.mark.parametrize("type_id", ALL_TYPES, ids=lambda t: TYPE_NAMES[t])
@@ -57,11 +49,6 @@ def test_long_rows(compute, oracle, type_id):
     for p in range(3):
         x = pass_input(cols, p)
         check_rows(oracle, w, type_id, x, rows, cols, compute.matvec_typed(w, rows, cols, type_id, x))
-
-
-def rel_l2(a, b):
-    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
-    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
 
 
 CONFIG_SHAPES = [

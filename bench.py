@@ -12,7 +12,8 @@ weight matrix; weights and activations are resident in HBM before timing.
   overhead cannot leave the GPU idle; HIP events on that stream bracket the
   timed steps.
 - `value` = algorithmic bytes per step (packed weights + 4*cols*N +
-  4*rows*N) / average step time.
+  4*rows*N) / average step time. At N = 8 a step is two launches: the
+  activation quantization and the matmul.
 - cpu_baseline: the reference CPU provider (built from the reference sources
   into oracle/_ref) on the same weights, on this host's cores; else this
   repository's C port of the scalar path.
@@ -95,12 +96,13 @@ class Graph:
         self.rt.lib.hipGraphDestroy(self.graph)
 
 
-def time_steps(rt, kern, stream, weights, x_dev, y_dev, batch, steps, warmup, mode):
+def time_steps(rt, kern, stream, weights, x_dev, y_dev, batch, steps, warmup, mode, work, work_bytes):
     """Average milliseconds per step over `steps` timed launches."""
     copies = len(weights)
 
     def launch(i):
-        return lambda: kern.matmul(weights[i % copies], Q4_K, ROWS, COLS, x_dev, y_dev, batch, 0, 0, stream)
+        return lambda: kern.matmul(weights[i % copies], Q4_K, ROWS, COLS, x_dev, y_dev, batch, work, work_bytes,
+                                   stream)
 
     start, end = rt.event(), rt.event()
     if mode == "graph":
@@ -222,10 +224,13 @@ def main() -> int:
     x_dev = rt.malloc(x8.nbytes)
     rt.upload(x_dev, x8)
     y_dev = rt.malloc(8 * ROWS * 4)
+    work_bytes = max(kern.workspace_bytes(Q4_K, ROWS, COLS, b) for b in (1, 8))
+    work = rt.malloc(max(work_bytes, 16))
 
     results = {}
     for batch in (1, 8):
-        ms = time_steps(rt, kern, stream, weights, x_dev, y_dev, batch, args.steps, args.warmup, args.launch)
+        ms = time_steps(rt, kern, stream, weights, x_dev, y_dev, batch, args.steps, args.warmup, args.launch,
+                        work, kern.workspace_bytes(Q4_K, ROWS, COLS, batch))
         nbytes = algorithmic_bytes(ROWS, COLS, batch)
         results[batch] = (ms, nbytes / (ms * 1e-3) / 1e9, nbytes)
 
@@ -261,7 +266,7 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(host_w, x8[0].copy(), y1, args.cpu_seconds)
-    for p in weights:
+    for p in weights + [work]:
         rt.free(p)
     print(json.dumps(line), flush=True)
     return 0

@@ -19,7 +19,7 @@ ROOT = Path(__file__).resolve().parent
 REPO = ROOT.parent
 LIB = ROOT / "lib"
 CSRC = ROOT / "csrc"
-HIP_SOURCES = ["abi.hip", "dense.hip", "matvec.hip", "gemm.hip", "pack.cpp"]
+HIP_SOURCES = ["abi.hip", "dense.hip", "smalln.hip", "gemm.hip", "pack.cpp"]
 C_SOURCES = ["core/compute.c", "core/vendor.c", "rocm/rocm.c"]
 
 HIPCC_FLAGS = [

@@ -62,7 +62,7 @@ NYA_HIP_EXPORT int nya_hip_weight_pack(void *dst, const void *src, unsigned type
 {
     size_t b;
     if (!dst || !src || !storage_bytes(type, rows, cols, &b)) return 1;
-    pack_planes((uint8_t *)dst, (const uint8_t *)src, type, rows, cols);
+    pack_tiles((uint8_t *)dst, (const uint8_t *)src, type, rows, cols);
     return 0;
 }
 
@@ -70,7 +70,9 @@ NYA_HIP_EXPORT int nya_hip_workspace_bytes(unsigned type, size_t rows, size_t co
 {
     size_t b;
     if (!bytes || !batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return 1;
-    *bytes = use_gemm(type, cols, batch) ? gemm_workspace((int)cols, (int)batch) : 0;
+    const bool dense = type == F32 || type == F16 || type == BF16;
+    *bytes = use_gemm(type, cols, batch) ? gemm_workspace((int)cols, (int)batch)
+           : dense ? 0 : smalln_workspace((int)cols, batch < 8 ? (int)batch : 8);
     return 0;
 }
 
@@ -84,19 +86,30 @@ NYA_HIP_EXPORT int nya_hip_matmul(uintptr_t w, unsigned type, size_t rows, size_
     const bool dense = type == F32 || type == F16 || type == BF16;
     hipStream_t s = (hipStream_t)stream;
     const uint8_t *wp = (const uint8_t *)w;
+    const bool fits = workspace && !(workspace & 15u);
     // The GEMM needs its workspace; without one (or a short one) the batch is
     // run 8 columns at a time instead.
-    if (use_gemm(type, cols, batch) && workspace && !(workspace & 15u) &&
-        workspace_bytes >= gemm_workspace((int)cols, (int)batch))
+    if (use_gemm(type, cols, batch) && fits && workspace_bytes >= gemm_workspace((int)cols, (int)batch))
         return status(launch_gemm(type, wp, (const float *)x, (float *)y, (int)rows, (int)cols, (int)batch,
                                   (void *)workspace, s));
     for (size_t done = 0; done < batch; done += 8) {
         const int n = (int)(batch - done < 8 ? batch - done : 8);
         const float *xp = (const float *)x + done * cols;
         float *yp = (float *)y + done * rows;
-        const int st = status(dense ? launch_dense(type, wp, xp, yp, (int)rows, (int)cols, n, s)
-                                    : launch_quant_matvec(type, wp, xp, yp, (int)rows, (int)cols, n, s));
-        if (st) return st;
+        if (dense) {
+            const int st = status(launch_dense(type, wp, xp, yp, (int)rows, (int)cols, n, s));
+            if (st) return st;
+        } else if (n == 1 || (fits && workspace_bytes >= smalln_workspace((int)cols, n))) {
+            const int st = status(launch_smalln(type, wp, xp, yp, (int)rows, (int)cols, n, (void *)workspace, s));
+            if (st) return st;
+        } else {
+            // No room for the activation digits of several tokens: one at a time.
+            for (int k = 0; k < n; ++k) {
+                const int st = status(launch_smalln(type, wp, xp + (size_t)k * cols, yp + (size_t)k * rows,
+                                                    (int)rows, (int)cols, 1, nullptr, s));
+                if (st) return st;
+            }
+        }
     }
     return 0;
 }
@@ -107,7 +120,7 @@ NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_
     if (!batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return NULL;
     if (type == F32 || type == F16 || type == BF16) return "skinny_dense";
     if (use_gemm(type, cols, batch)) return "gemm_tile";
-    return quant_matvec_kernel(type, (int)rows, (int)cols, batch < 8 ? (int)batch : 8);
+    return "smalln_mfma";
 }
 
 NYA_HIP_EXPORT int nya_hip_copy(uintptr_t dst, uintptr_t src, size_t bytes, uintptr_t stream)

@@ -15,20 +15,31 @@
 //        w = d * sc[n/16] * (q6 - 32).
 //
 // Device layouts keep exactly the GGUF byte count. F32/F16/BF16 are uploaded
-// unchanged. For the block formats the kernels give each lane one "unit" of
-// a row (64 elements of a K-quant superblock, or one 32-element Q8_0/Q4_0
-// block), so the matrix is stored as field planes indexed by (row, unit):
-// lane u's slice of a field sits at (row * U + u) * size, and the 64 lanes of
-// a wavefront read one contiguous span per load instruction. U = units per
-// row. Planes, each over all rows:
-//   Q4_K (U = cols/64, unit 4s+p): qa 16 B = qs[32p..+16), qb 16 B =
-//        qs[32p+16..+16), slice 4 B = sc(2p) | m(2p)<<6 | sc(2p+1)<<12 |
-//        m(2p+1)<<18 | byte p of (d, dmin) << 24
-//   Q6_K (U = cols/64, unit 4s+2h+l16): a = ql[64h+16*l16..+16),
-//        b = ql[64h+32+16*l16..+16), c = qh[32h+16*l16..+16) (16 B each),
-//        sc 4 B (byte q = sc[8h+2q+l16]), then d 2 B per superblock
-//   Q8_0 (U = cols/32): qa = qs[0..16), qb = qs[16..32), d 2 B
-//   Q4_0 (U = cols/32): q = qs[0..16), d 2 B
+// unchanged. The block formats are stored in tiles of 32 rows, the M (or N)
+// extent of one gfx950 MFMA: tile t holds rows 32t.. (R rows, R = 32 except
+// possibly in the last tile) at byte 32 * t * row_bytes. A tile is a sequence
+// of column groups of 256 (a K-quant superblock, or eight Q8_0/Q4_0 blocks;
+// the last Q8_0/Q4_0 group may hold nb < 8 blocks), group g at
+// g * group_bytes * R. Inside a group every field is stored row-minor
+// ([field][row]), so the 64 lanes of a wavefront that own 32 rows x 2
+// halves read one contiguous 1 KiB span per 16-byte load. Row r of the tile:
+//   Q4_K (144 R): for units p < 4 (sub-blocks 2p, 2p+1): qa at 32R p + 16r
+//        = qs[32p..+16), qb at 32R p + 16R + 16r = qs[32p+16..+16); slices at
+//        128R + 16r, four words, word p = sc(2p) | m(2p)<<6 | sc(2p+1)<<12 |
+//        m(2p+1)<<18 | byte p of (d, dmin) << 24.
+//   Q6_K (210 R; the 16-byte fields of group g at 208R g, the d values of
+//        all groups after them): for units p = 2h + l16 < 4 (elements
+//        128h + 32q + 16 l16 + i, q < 4, i < 16): la at 48R p + 16r =
+//        ql[64h+16 l16..+16), lb at 48R p + 16R + 16r = ql[64h+32+16 l16..+16),
+//        qh at 48R p + 32R + 16r = qh[32h+16 l16..+16); sc at 192R + 16r, word
+//        p byte q = sc[8h + 2q + l16]; d of group g at 208R G + 2R g + 2r
+//        (G groups per row).
+//   Q8_0 (34 R nb): qs of block j at 32R j + 32r, then d of block j at
+//        32R nb + 2R j + 2r.
+//   Q4_0 (18 R nb): qs of block j at 16R j + 16r, then d at 16R nb + 2R j +
+//        2r.
+// Every 16-byte field starts 16-byte aligned (tile and group offsets are
+// multiples of 16); 2-byte scales are read one per lane.
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
@@ -55,7 +66,31 @@ inline bool format_of(unsigned type, format_info *f)
     }
 }
 
+constexpr int kTileRows = 32;
+constexpr int kGroupCols = 256;
+
+// Bytes per row of one column group (a full one; a short last Q8_0/Q4_0
+// group has nb * block bytes).
+inline unsigned group_row_bytes(unsigned type)
+{
+    switch (type) {
+    case Q4_K: return 144;
+    case Q6_K: return 210;
+    case Q8_0: return 8 * 34;
+    case Q4_0: return 8 * 18;
+    default: return 0;
+    }
+}
+
+// GGUF bytes per row, usable in device code.
+template <unsigned T>
+constexpr size_t tiled_row_bytes(int cols)
+{
+    return T == Q4_K ? (size_t)(cols / 256) * 144 : T == Q6_K ? (size_t)(cols / 256) * 210
+         : T == Q8_0 ? (size_t)(cols / 32) * 34 : (size_t)(cols / 32) * 18;
+}
+
 // Host-side byte permutation GGUF -> device layout (see the header comment); pack.cpp.
-void pack_planes(uint8_t *dst, const uint8_t *src, unsigned type, size_t rows, size_t cols);
+void pack_tiles(uint8_t *dst, const uint8_t *src, unsigned type, size_t rows, size_t cols);
 
 }  // namespace fy

@@ -99,24 +99,28 @@ template <unsigned T>
 __device__ __forceinline__ void load_w(WRaw &r, const uint8_t *__restrict__ w, int rows, int cols, int row,
     int step, int half)
 {
+    // The tiled layout of formats.h: tile of 32 rows, 256-column groups.
+    const int tile = row / kTileRows, rr = row % kTileRows;
+    const int R = rows - kTileRows * tile < kTileRows ? rows - kTileRows * tile : kTileRows;
+    const uint8_t *tb = w + (size_t)kTileRows * tile * tiled_row_bytes<T>(cols);
     if constexpr (T == Q4_K) {
-        const size_t U = (size_t)(cols / 64), n = (size_t)rows * U, at = (size_t)row * U + (step >> 1);
-        r.q = ((const u32x4 *)(w + 16 * n * half))[at];    // qa (half 0) or qb (half 1)
-        r.c = ((const u32x4 *)(w + 32 * n))[at >> 2];        // the superblock's four slices
+        const int g = step >> 3, p = (step >> 1) & 3;
+        const uint8_t *b = tb + (size_t)144 * R * g;
+        r.q = *(const u32x4 *)(b + 32 * R * p + 16 * R * half + 16 * rr);   // qa (half 0) or qb (half 1)
+        r.c = *(const u32x4 *)(b + 128 * R + 16 * rr);                      // the superblock's four slices
     } else if constexpr (T == Q6_K) {
-        const size_t U = (size_t)(cols / 64), n = (size_t)rows * U, at = (size_t)row * U + (step >> 1);
-        r.q = ((const u32x4 *)(w + 16 * n * half))[at];    // ql of scale groups 0,2 (a) or 1,3 (b)
-        r.c = ((const u32x4 *)(w + 32 * n))[at];             // qh
-        r.e = ((const uint32_t *)(w + 48 * n))[at];          // sc of scale groups 0..3
-        r.f = ((const uint16_t *)(w + 52 * n))[at >> 2];     // d
-    } else if constexpr (T == Q8_0) {
-        const size_t U = (size_t)(cols / 32), n = (size_t)rows * U, at = (size_t)row * U + step;
-        r.q = ((const u32x4 *)(w + 16 * n * half))[at];    // qs[0..16) or qs[16..32)
-        r.e = ((const uint16_t *)(w + 32 * n))[at];
+        const int u = step >> 1, g = u >> 2, p = u & 3;
+        const uint8_t *b = tb + (size_t)208 * R * g;
+        r.q = *(const u32x4 *)(b + 48 * R * p + 16 * R * half + 16 * rr);   // ql of scale groups 0,2 (la) or 1,3 (lb)
+        r.c = *(const u32x4 *)(b + 48 * R * p + 32 * R + 16 * rr);          // qh
+        r.e = *(const uint32_t *)(b + 192 * R + 16 * rr + 4 * p);           // sc of scale groups 0..3
+        r.f = *(const uint16_t *)(tb + (size_t)208 * R * ((cols + 255) / 256) + 2 * R * g + 2 * rr);   // d
     } else {
-        const size_t U = (size_t)(cols / 32), n = (size_t)rows * U, at = (size_t)row * U + step;
-        r.q = ((const u32x4 *)w)[at];
-        r.e = ((const uint16_t *)(w + 16 * n))[at];
+        constexpr int quant = T == Q8_0 ? 32 : 16;
+        const int g = step >> 3, j = step & 7, left = cols / 32 - 8 * g, nb = left < 8 ? left : 8;
+        const uint8_t *b = tb + (size_t)(quant + 2) * 8 * R * g;
+        r.q = *(const u32x4 *)(b + quant * R * j + quant * rr + (T == Q8_0 ? 16 * half : 0));
+        r.e = *(const uint16_t *)(b + quant * R * nb + 2 * R * j + 2 * rr);
     }
 }
 

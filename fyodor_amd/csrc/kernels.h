@@ -6,14 +6,17 @@
 
 namespace fy {
 
-// Y[n][rows] = sum_k W[row][k] * X[n][k] for n < batch, batch 1..8, W in the
-// device layout. Each reads every weight byte once per call.
+// Y[n][rows] = sum_k W[row][k] * X[n][k] for n < batch, W in the device
+// layout.
 // F32 / F16 / BF16 weights (dense.hip).
 hipError_t launch_dense(unsigned type, const uint8_t *w, const float *x, float *y,
     int rows, int cols, int batch, hipStream_t stream);
-// Q4_0 / Q8_0 / Q4_K / Q6_K weights (matvec.hip); x must be 16-byte aligned.
-hipError_t launch_quant_matvec(unsigned type, const uint8_t *w, const float *x, float *y,
-    int rows, int cols, int batch, hipStream_t stream);
+// Q4_0 / Q8_0 / Q4_K / Q6_K weights in the tiled layout (smalln.hip), batch
+// 1..8; x must be 16-byte aligned. Batches of 2..8 need smalln_workspace
+// bytes of 16-byte-aligned device scratch (batch 1 needs none).
+size_t smalln_workspace(int cols, int batch);
+hipError_t launch_smalln(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols, int batch,
+    void *workspace, hipStream_t stream);
 
 // Batches above 8 with quantized weights (gemm.hip): MFMA tiles over the
 // whole batch, weights read once per 128 batch rows. gemm_supported says
@@ -24,8 +27,6 @@ size_t gemm_workspace(int cols, int batch);
 hipError_t launch_gemm(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols, int batch,
     void *workspace, hipStream_t stream);
 
-// Name of the kernel launch_quant_matvec uses for these arguments.
-const char *quant_matvec_kernel(unsigned type, int rows, int cols, int batch);
 // Plain 16-byte-per-thread device copy (dense.hip), for counter calibration.
 hipError_t launch_copy(uint4 *dst, const uint4 *src, size_t count, hipStream_t stream);
 

@@ -66,57 +66,65 @@ def test_queries(kernels):
     assert L.nya_hip_weight_bytes(Q8_0, 0, 32, ctypes.byref(b)) == 1
     assert L.nya_hip_weight_bytes(Q8_0, 1 << 31, 32, ctypes.byref(b)) == 1
     assert L.nya_hip_matmul(0, Q8_0, 3, 32, 16, 16, 1, 0, 0, 0) == 1          # declined, nothing enqueued
-    assert kernels.kernel_name(Q4_K, 14336, 4096, 1) == "quant_rows"
+    assert kernels.kernel_name(Q4_K, 14336, 4096, 1) == "smalln_mfma"
 
 
 def unpack_reference(dev: np.ndarray, t: int, rows: int, cols: int) -> np.ndarray:
-    """Inverse of the device layout, written from its specification."""
-    out = np.empty(storage_bytes(t, rows, cols), dtype=np.uint8)
-    if t in (Q8_0, Q4_0):
-        n = rows * cols // 32
-        q = 32 if t == Q8_0 else 16
-        blk = out.reshape(n, q + 2)
-        blk[:, 0:2] = dev[q * n:].reshape(n, 2)
-        blk[:, 2:18] = dev[:16 * n].reshape(n, 16)
-        if t == Q8_0:
-            blk[:, 18:34] = dev[16 * n:32 * n].reshape(n, 16)
-    elif t == Q4_K:
-        U, ns = cols // 64, cols // 256
-        n = rows * U
-        qa, qb = dev[:16 * n].reshape(rows, ns, 4, 16), dev[16 * n:32 * n].reshape(rows, ns, 4, 16)
-        sl = dev[32 * n:].view(np.uint32).reshape(rows, ns, 4)
-        blk = out.reshape(rows, ns, 144)
-        for p in range(4):
-            blk[:, :, 16 + 32 * p:32 + 32 * p] = qa[:, :, p]
-            blk[:, :, 32 + 32 * p:48 + 32 * p] = qb[:, :, p]
-            blk[:, :, p] = (sl[:, :, p] >> 24).astype(np.uint8)
-        sc = [(sl[:, :, g // 2] >> (12 * (g % 2))) & 63 for g in range(8)]
-        mn = [(sl[:, :, g // 2] >> (12 * (g % 2) + 6)) & 63 for g in range(8)]
-        for g in range(4):
-            blk[:, :, 4 + g] = sc[g] | ((sc[g + 4] >> 4) << 6)
-            blk[:, :, 8 + g] = mn[g] | ((mn[g + 4] >> 4) << 6)
-            blk[:, :, 12 + g] = (sc[g + 4] & 15) | ((mn[g + 4] & 15) << 4)
-    else:
-        ns = cols // 256
-        U, n = 4 * ns, rows * cols // 64
-        a, b, c = (dev[i * 16 * n:(i + 1) * 16 * n].reshape(rows, ns, 2, 2, 16) for i in range(3))
-        sc = dev[48 * n:52 * n].reshape(rows, ns, 2, 2, 4)
-        d = dev[52 * n:].reshape(rows, ns, 2)
-        blk = out.reshape(rows, ns, 210)
-        for h in range(2):
-            for l16 in range(2):
-                blk[:, :, 64 * h + 16 * l16:64 * h + 16 * l16 + 16] = a[:, :, h, l16]
-                blk[:, :, 64 * h + 32 + 16 * l16:64 * h + 48 + 16 * l16] = b[:, :, h, l16]
-                blk[:, :, 128 + 32 * h + 16 * l16:128 + 32 * h + 16 * l16 + 16] = c[:, :, h, l16]
-                for q in range(4):
-                    blk[:, :, 192 + 8 * h + 2 * q + l16] = sc[:, :, h, l16, q]
-        blk[:, :, 208:210] = d
-    return out
+    """Inverse of the tiled device layout, written from its specification:
+    tiles of 32 rows, 256-column groups, fields stored [field][row]."""
+    block, nbytes = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}[t]
+    row_bytes = cols // block * nbytes
+    out = np.empty((rows, row_bytes), dtype=np.uint8)
+    groups = -(-cols // 256)
+    for t0 in range(0, rows, 32):
+        R = min(32, rows - t0)
+        tile = dev[t0 * row_bytes:(t0 + R) * row_bytes]
+        for g in range(groups):
+            if t == Q4_K:
+                grp = tile[144 * R * g:144 * R * (g + 1)]
+                blk = out[t0:t0 + R, 144 * g:144 * (g + 1)]
+                sl = grp[128 * R:144 * R].reshape(R, 16).view(np.uint32)   # [R, 4]
+                for p in range(4):
+                    blk[:, 16 + 32 * p:32 + 32 * p] = grp[32 * R * p:32 * R * p + 16 * R].reshape(R, 16)
+                    blk[:, 32 + 32 * p:48 + 32 * p] = grp[32 * R * p + 16 * R:32 * R * (p + 1)].reshape(R, 16)
+                    blk[:, p] = (sl[:, p] >> 24).astype(np.uint8)
+                sc = [(sl[:, g2 // 2] >> (12 * (g2 % 2))) & 63 for g2 in range(8)]
+                mn = [(sl[:, g2 // 2] >> (12 * (g2 % 2) + 6)) & 63 for g2 in range(8)]
+                for k in range(4):
+                    blk[:, 4 + k] = sc[k] | ((sc[k + 4] >> 4) << 6)
+                    blk[:, 8 + k] = mn[k] | ((mn[k + 4] >> 4) << 6)
+                    blk[:, 12 + k] = (sc[k + 4] & 15) | ((mn[k + 4] & 15) << 4)
+            elif t == Q6_K:
+                grp = tile[208 * R * g:208 * R * (g + 1)]
+                blk = out[t0:t0 + R, 210 * g:210 * (g + 1)]
+                sc = grp[192 * R:208 * R].reshape(R, 4, 4)
+                for h in range(2):
+                    for l16 in range(2):
+                        p = 2 * h + l16
+                        f = grp[48 * R * p:48 * R * (p + 1)].reshape(3, R, 16)
+                        blk[:, 64 * h + 16 * l16:64 * h + 16 * l16 + 16] = f[0]
+                        blk[:, 64 * h + 32 + 16 * l16:64 * h + 48 + 16 * l16] = f[1]
+                        blk[:, 128 + 32 * h + 16 * l16:128 + 32 * h + 16 * l16 + 16] = f[2]
+                        for q in range(4):
+                            blk[:, 192 + 8 * h + 2 * q + l16] = sc[:, p, q]
+                d = tile[208 * R * groups + 2 * R * g:208 * R * groups + 2 * R * (g + 1)].reshape(R, 2)
+                blk[:, 208:210] = d
+            else:
+                quant = 32 if t == Q8_0 else 16
+                nb = min(8, cols // 32 - 8 * g)
+                grp = tile[(quant + 2) * 8 * R * g:(quant + 2) * 8 * R * g + (quant + 2) * nb * R]
+                for j in range(nb):
+                    c0 = (quant + 2) * (8 * g + j)
+                    out[t0:t0 + R, c0 + 2:c0 + 2 + quant] = grp[quant * R * j:quant * R * (j + 1)].reshape(R, quant)
+                    out[t0:t0 + R, c0:c0 + 2] = grp[quant * R * nb + 2 * R * j:quant * R * nb + 2 * R * (j + 1)].reshape(R, 2)
+    return out.reshape(-1)
 
 
 @pytest.mark.parametrize("t", [Q4_0, Q8_0, Q4_K, Q6_K])
-def test_pack_is_the_specified_permutation(kernels, t):
-    rows, cols = 5, 1024
+@pytest.mark.parametrize("rows,cols", [(5, 1024), (70, 768), (33, 256), (9, 800)])
+def test_pack_is_the_specified_permutation(kernels, t, rows, cols):
+    if cols % {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}[t]:
+        pytest.skip("shape not representable")
     w = synth.weights(t, rows, cols, 21)   # random scale bytes: every 12-byte pattern
     dev = kernels.device_weights(w, t, rows, cols)
     assert dev.nbytes == w.nbytes and not np.shares_memory(dev, w)
@@ -129,11 +137,13 @@ def test_gemm_dispatch_and_workspace():
     none (nothing is launched)."""
     kern = Kernels()
     for t in (Q4_0, Q8_0, Q4_K, Q6_K):
-        assert kern.workspace_bytes(t, 4096, 4096, 8) == 0
+        assert kern.workspace_bytes(t, 4096, 4096, 1) == 0
+        assert kern.workspace_bytes(t, 4096, 4096, 8) == 4096 // 32 * 136 * 8
+        assert kern.workspace_bytes(t, 4096, 4096, 3) == 4096 // 32 * 136 * 4
         assert kern.workspace_bytes(t, 4096, 4096, 9) == 6 * 4096 * 9
         assert kern.workspace_bytes(t, 4096, 4096, 512) == 6 * 4096 * 512
         assert kern.kernel_name(t, 4096, 4096, 512) == "gemm_tile"
-        assert kern.kernel_name(t, 4096, 4096, 8) != "gemm_tile"
+        assert kern.kernel_name(t, 4096, 4096, 8) == "smalln_mfma"
     for t in (F32, BF16):
         assert kern.workspace_bytes(t, 4096, 4096, 512) == 0
         assert kern.kernel_name(t, 4096, 4096, 512) == "skinny_dense"

@@ -27,6 +27,9 @@ HIPCC_FLAGS = [
     # Packed FP32 arithmetic is kept out of every kernel.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
+# Per-source additions. The small-N kernels read every MFMA result at once in
+# VALU code: results in VGPRs (not AGPRs) save a copy per register.
+EXTRA_FLAGS = {"smalln.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 C_FLAGS = [
     "-std=c17", "-O2", "-fPIC", "-Wall", "-Wextra", "-Wpedantic", "-Wshadow",
     "-D_POSIX_C_SOURCE=200809L",
@@ -61,7 +64,7 @@ def build_kernels() -> Path:
     def compile_one(pair):
         src, obj = pair
         lang = ["-x", "hip"] if src.suffix == ".hip" else []
-        _run([cc, *HIPCC_FLAGS, *inc, *lang, "-c", str(src), "-o", str(obj)])
+        _run([cc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), *inc, *lang, "-c", str(src), "-o", str(obj)])
 
     with ThreadPoolExecutor(max_workers=min(8, len(sources))) as pool:
         list(pool.map(compile_one, zip(sources, objects)))

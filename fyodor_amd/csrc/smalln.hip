@@ -45,8 +45,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kChunkCols = 16384;   // columns per launch (bounds the LDS copy of x)
 constexpr int kSlotBytes = 32;      // one digit of one token over a 32-column group
 
-__device__ __forceinline__ int sext8(int v) { return (int)(int8_t)(v & 0xFF); }
-
 // Bytes v < 128 minus c (c <= 64) as signed 8-bit values, four at once.
 __device__ __forceinline__ uint32_t bytes_minus(uint32_t v, uint32_t c4)
 {
@@ -59,45 +57,55 @@ __device__ __forceinline__ i32x4 as_i32x4(u32x4 v) { return __builtin_bit_cast(i
 // Group g (32 columns) of a chunk: digits at dig + g * 128 * np, slot 4t + d
 // (32 bytes), meta[g * np + t] = {2^(e-22), (float)sum(X) * 2^(e-22)}.
 
+// Byte b of each of four words, packed into one word.
+__device__ __forceinline__ uint32_t gather_byte(const int (&v)[8], int k, int b)
+{
+    const uint32_t sel = 0x0c0c0000u | (uint32_t)(4 + b) << 8 | (uint32_t)b;
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)v[k + 1], (uint32_t)v[k], sel);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)v[k + 3], (uint32_t)v[k + 2], sel);
+    return lo | hi << 16;
+}
+
 // Item `item` = 8 consecutive values of token t (4 items per group). The four
-// lanes of a group are consecutive and must call this together.
+// lanes of a group are consecutive and must call this together. The signed
+// digits of X are byte 0 of X, byte 1 of X + 2^7 and byte 2 of X + 2^7 + 2^15
+// (a1 = sext8((X + 128) >> 8), a2 = (X + 32896) >> 16).
 __device__ __forceinline__ void quantize8(float4 v0, float4 v1, int np, int t, int item, uint8_t *dig, float2 *meta)
 {
     const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-    float m = 0.f;
-    int bad = 0;
+    float m = 0.f, z = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         m = fmaxf(m, fabsf(v[j]));
-        bad |= !(fabsf(v[j]) <= 3.4028235e38f);   // inf or NaN
+        z = __builtin_fmaf(v[j], 0.f, z);   // NaN iff some value is inf or NaN
     }
     m = fmaxf(m, __shfl_xor(m, 1, 64));
     m = fmaxf(m, __shfl_xor(m, 2, 64));
-    bad |= __shfl_xor(bad, 1, 64);
-    bad |= __shfl_xor(bad, 2, 64);
+    z += __shfl_xor(z, 1, 64);
+    z += __shfl_xor(z, 2, 64);
     int ex = 0;
     (void)__builtin_frexpf(m, &ex);
-    const bool finite = !bad;
+    const bool finite = z == z;
     const int shift = m > 0.f && finite ? 22 - ex : 0;
     const float scale = !finite ? __builtin_nanf("") : m > 0.f ? __builtin_ldexpf(1.f, ex - 22) : 0.f;
-    uint32_t pk[3][2] = {{0, 0}, {0, 0}, {0, 0}};
+    int X[8], X1[8], X2[8];
     int sx = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int X = finite ? (int)__builtin_rintf(__builtin_ldexpf(v[j], shift)) : 0;
-        const int a0 = sext8(X), r1 = (X - a0) >> 8, a1 = sext8(r1), a2 = (r1 - a1) >> 8;
-        sx += X;
-        pk[0][j >> 2] |= (uint32_t)(a0 & 0xFF) << (8 * (j & 3));
-        pk[1][j >> 2] |= (uint32_t)(a1 & 0xFF) << (8 * (j & 3));
-        pk[2][j >> 2] |= (uint32_t)(a2 & 0xFF) << (8 * (j & 3));
+        // A non-finite group's digits are never used: its scale is NaN.
+        X[j] = (int)__builtin_rintf(__builtin_ldexpf(v[j], shift));
+        X1[j] = X[j] + 128;
+        X2[j] = X[j] + 32896;
+        sx += X[j];
     }
     sx += __shfl_xor(sx, 1, 64);
     sx += __shfl_xor(sx, 2, 64);
     const int g = item >> 2, part = item & 3;
     uint8_t *dst = dig + (size_t)g * 4 * kSlotBytes * np + kSlotBytes * 4 * t + 8 * part;
-#pragma unroll
-    for (int d = 0; d < 3; ++d) *(uint2 *)(dst + kSlotBytes * d) = make_uint2(pk[d][0], pk[d][1]);
-    *(uint2 *)(dst + kSlotBytes * 3) = make_uint2(0, 0);
+    *(uint2 *)dst = make_uint2(gather_byte(X, 0, 0), gather_byte(X, 4, 0));
+    *(uint2 *)(dst + kSlotBytes) = make_uint2(gather_byte(X1, 0, 1), gather_byte(X1, 4, 1));
+    *(uint2 *)(dst + 2 * kSlotBytes) = make_uint2(gather_byte(X2, 0, 2), gather_byte(X2, 4, 2));
+    *(uint2 *)(dst + 3 * kSlotBytes) = make_uint2(0, 0);
     if (part == 0) meta[(size_t)g * np + t] = make_float2(scale, (float)sx * scale);
 }
 
@@ -122,6 +130,11 @@ template <> struct WStage<Q4_0> { u32x4 q[8]; uint32_t d[8]; };
 
 // MFMAs per 256-column group, and how many activation operands each needs.
 template <unsigned T, int NP> constexpr int kTokenHalves = (T == Q6_K && NP > 4) ? 2 : 1;
+// Weight stages in flight per wavefront (a third one measured slower).
+template <unsigned T, int NP> constexpr int kRing = 2;
+// Accumulators per lane: Q6_K lanes hold every token, the others every
+// second one.
+template <unsigned T, int NP> constexpr int kAcc = T == Q6_K ? NP : (NP + 1) / 2;
 
 template <unsigned T, int NP, bool G>
 struct Stage {
@@ -174,24 +187,23 @@ __device__ __forceinline__ void load_weights(WStage<T> &w, const Lane &L, int g)
     }
 }
 
-// Activation operand of MFMA j (token half th) of chunk-local group gl:
-// returns the byte offset into the digit array, and whether the lane's
-// A-row is live for n tokens.
+// Byte offset of the activation operand of MFMA j (token half th) of
+// chunk-local group gl in the digit array. Lanes whose A-row is not live for
+// n tokens read slot 3 of token 0, which is always zero.
 template <unsigned T, int NP>
-__device__ __forceinline__ int a_offset(const Lane &L, int gl, int j, int th, int n, int nb, bool &live)
+__device__ __forceinline__ int a_offset(const Lane &L, int gl, int j, int th, int n, int nb)
 {
     const int row_bytes = 4 * kSlotBytes * NP;
     if constexpr (T == Q6_K) {
         const int p = j >> 1, m = j & 1;
         const int t = (L.slot >> 3) + 4 * th, c = (L.slot >> 2) & 1, d = L.slot & 3;
-        live = c == L.h && d < 3 && t < n;
+        const bool live = c == L.h && d < 3 && t < n;
         const int xg = 8 * gl + 4 * (p >> 1) + 2 * m + L.h;
-        return xg * row_bytes + kSlotBytes * (4 * (t < NP ? t : 0) + d) + 16 * (p & 1);
+        return xg * row_bytes + kSlotBytes * (live ? 4 * t + d : 3) + 16 * (p & 1);
     } else {
         const int jj = j < nb ? j : nb - 1;
-        const int t = L.slot >> 2;
-        live = t < n;
-        return (8 * gl + jj) * row_bytes + kSlotBytes * (t < NP ? L.slot : 0) + 16 * L.h;
+        const bool live = (L.slot >> 2) < n;
+        return (8 * gl + jj) * row_bytes + kSlotBytes * (live ? L.slot : 3) + 16 * L.h;
     }
 }
 
@@ -204,11 +216,8 @@ __device__ __forceinline__ void load_stage(Stage<T, NP, G> &st, const Lane &L, i
 #pragma unroll
         for (int th = 0; th < kTokenHalves<T, NP>; ++th)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                bool live;
-                const int off = a_offset<T, NP>(L, g - g0c, j, th, n, nb, live);
-                st.a[8 * th + j] = *(const i32x4 *)(dig + off);
-            }
+            for (int j = 0; j < 8; ++j)
+                st.a[8 * th + j] = *(const i32x4 *)(dig + a_offset<T, NP>(L, g - g0c, j, th, n, nb));
     }
     load_weights<T>(st.w, L, g);
 }
@@ -226,34 +235,31 @@ __device__ __forceinline__ float recombine(int d0, int d1, int d2)
 
 // The block dot products of one stage (group g) into acc. Q4_K/Q8_0/Q4_0:
 // acc[k] belongs to token 2k + h; Q6_K: acc[t] to token t (this lane half's
-// scale groups).
+// scale groups). The K-quant superblock scales d and dmin multiply the
+// group's sums once: sum_j (d sc_j q - dmin m_j) x = d sum_j sc_j (q.x)_j -
+// dmin sum_j m_j (sum x)_j.
 template <unsigned T, int NP, bool G>
-__device__ __forceinline__ void compute_stage(float (&acc)[8], const Stage<T, NP, G> &st, const Lane &L, int g,
-    int g0c, const uint8_t *dig, const float2 *meta, int n)
+__device__ __forceinline__ void compute_stage(float (&acc)[(kAcc<T, NP>)], const Stage<T, NP, G> &st, const Lane &L,
+    int g, int g0c, const uint8_t *dig, const float2 *meta, int n)
 {
+    constexpr int NA = kAcc<T, NP>;
     const int h = L.h;
     const int nb = (T == Q8_0 || T == Q4_0) ? group_blocks(L, g) : 8;
-    float d = 0.f, dmin = 0.f;
-    if constexpr (T == Q4_K) {
-        const uint32_t dd = (st.w.sl.x >> 24) | ((st.w.sl.y >> 24) << 8) | ((st.w.sl.z >> 24) << 16) |
-            ((st.w.sl.w >> 24) << 24);
-        d = f16_to_f32(dd & 0xFFFFu);
-        dmin = f16_to_f32(dd >> 16);
-    } else if constexpr (T == Q6_K) {
-        d = f16_to_f32(st.w.d);
-    }
+    float sum_s[NA], sum_m[NA];
+#pragma unroll
+    for (int k = 0; k < NA; ++k) sum_s[k] = sum_m[k] = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         if ((T == Q8_0 || T == Q4_0) && j >= nb) break;
         i32x4 b;
-        float factor, bias = 0.f;
+        float sc, mn = 0.f;   // per-block multiplier of q.x and of sum x
         int xg;
         if constexpr (T == Q4_K) {
             const int p = j >> 1, nib = j & 1;
             b = as_i32x4((st.w.q[p] >> (4 * nib)) & 0x0F0F0F0Fu);
             const uint32_t own = st.w.sl[p];
-            factor = d * (float)((own >> (12 * nib)) & 63u);
-            bias = dmin * (float)((own >> (12 * nib + 6)) & 63u);
+            sc = (float)((own >> (12 * nib)) & 63u);
+            mn = (float)((own >> (12 * nib + 6)) & 63u);
             xg = 8 * (g - g0c) + j;
         } else if constexpr (T == Q6_K) {
             const int p = j >> 1, m = j & 1, q = 2 * m + h;
@@ -263,49 +269,55 @@ __device__ __forceinline__ void compute_stage(float (&acc)[8], const Stage<T, NP
                 u[k] = bytes_minus(((st.w.ql[p][k] >> (4 * m)) & 0x0F0F0F0Fu) |
                     (((st.w.qh[p][k] >> (2 * q)) & 0x03030303u) << 4), 0x20202020u);
             b = as_i32x4(u);
-            factor = d * (float)(int8_t)((st.w.sc[p] >> (8 * q)) & 0xFFu);
+            sc = (float)(int8_t)((st.w.sc[p] >> (8 * q)) & 0xFFu);
             xg = 8 * (g - g0c) + 4 * (p >> 1) + q;
         } else if constexpr (T == Q8_0) {
             b = as_i32x4(st.w.q[j]);
-            factor = f16_to_f32(st.w.d[j]);
+            sc = f16_to_f32(st.w.d[j]);
             xg = 8 * (g - g0c) + j;
         } else {
             u32x4 u;
 #pragma unroll
             for (int k = 0; k < 4; ++k) u[k] = bytes_minus((st.w.q[j][k] >> (4 * h)) & 0x0F0F0F0Fu, 0x08080808u);
             b = as_i32x4(u);
-            factor = f16_to_f32(st.w.d[j]);
+            sc = f16_to_f32(st.w.d[j]);
             xg = 8 * (g - g0c) + j;
         }
 #pragma unroll
         for (int th = 0; th < kTokenHalves<T, NP>; ++th) {
-            bool live;
-            const int off = a_offset<T, NP>(L, g - g0c, j, th, n, nb, live);
             i32x4 a;
             if constexpr (G) a = st.a[8 * th + j];
-            else a = *(const i32x4 *)(dig + off);
-            if (!live) a = (i32x4){0, 0, 0, 0};
+            else a = *(const i32x4 *)(dig + a_offset<T, NP>(L, g - g0c, j, th, n, nb));
             const i32x16 D = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, (i32x16){}, 0, 0, 0);
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
+                const int t = T == Q6_K ? k + 4 * th : 2 * k + h;
+                const int slot = T == Q6_K ? k + 4 * th : k;   // accumulator
+                if (slot >= NA) continue;
                 const float Gs = recombine<T>(D[4 * k], D[4 * k + 1], D[4 * k + 2]);
-                if constexpr (T == Q6_K) {
-                    const int t = k + 4 * th;
-                    if (t < NP) {
-                        const float2 mt = meta[xg * NP + t];
-                        acc[t] += mt.x * (factor * Gs);
-                    }
-                } else if (2 * k < NP) {
-                    const int t = 2 * k + h < NP ? 2 * k + h : 0;
-                    const float2 mt = meta[xg * NP + t];
-                    if constexpr (T == Q4_K) acc[k] += mt.x * (factor * Gs) - bias * mt.y;
-                    else acc[k] += mt.x * (factor * Gs);
+                const float2 mt = meta[xg * NP + (t < NP ? t : 0)];
+                if constexpr (T == Q8_0 || T == Q4_0) {
+                    acc[slot] += mt.x * (sc * Gs);
+                } else {
+                    sum_s[slot] += sc * (Gs * mt.x);
+                    if constexpr (T == Q4_K) sum_m[slot] += mn * mt.y;
                 }
             }
         }
         // Keep each sub-block's MFMA next to its epilogue (bounds the live
-        // accumulator registers).
+        // result registers).
         __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (T == Q4_K) {
+        const uint32_t dd = (st.w.sl.x >> 24) | ((st.w.sl.y >> 24) << 8) | ((st.w.sl.z >> 24) << 16) |
+            ((st.w.sl.w >> 24) << 24);
+        const float d = f16_to_f32(dd & 0xFFFFu), dmin = f16_to_f32(dd >> 16);
+#pragma unroll
+        for (int k = 0; k < NA; ++k) acc[k] += d * sum_s[k] - dmin * sum_m[k];
+    } else if constexpr (T == Q6_K) {
+        const float d = f16_to_f32(st.w.d);
+#pragma unroll
+        for (int k = 0; k < NA; ++k) acc[k] += d * sum_s[k];
     }
 }
 
@@ -318,7 +330,7 @@ __global__ __launch_bounds__(64 * KS) void smalln_mfma(const uint8_t *__restrict
     int g0c, int ngc, int n, int accumulate)
 {
     extern __shared__ __align__(16) uint8_t lds[];
-    __shared__ float red[KS][8][64];
+    __shared__ float red[KS][(kAcc<T, NP>)][64];
     const int ccols = (g0c + ngc) * kGroupCols < cols ? ngc * kGroupCols : cols - g0c * kGroupCols;
     const int xgroups = ccols / 32;
     float2 *smeta = (float2 *)lds;                               // [xgroup][NP]
@@ -335,22 +347,27 @@ __global__ __launch_bounds__(64 * KS) void smalln_mfma(const uint8_t *__restrict
     L.slot = lane & 31;
     L.groups = (cols + kGroupCols - 1) / kGroupCols;
     L.blocks = cols / 32;
-    // This wave's groups [s0, s1) of the chunk.
-    const int s0 = g0c + wave * ngc / KS, s1 = g0c + (wave + 1) * ngc / KS, ns = s1 - s0;
-    const int last = ns > 0 ? s1 - 1 : g0c;
-    auto clamp = [&](int g) { return g <= last ? g : last; };
+    // This wave's groups: g0c + wave + KS k for k < ns (the workgroup's
+    // wavefronts read adjacent groups at the same time). Past the last one a
+    // stage repeats it.
+    const int ns = wave < ngc ? (ngc - wave + KS - 1) / KS : 0;
+    auto group_of = [&](int k) { return g0c + (ns > 0 ? wave + KS * (k < ns ? k : ns - 1) : 0); };
+    // N = 1: item idx (8 values) of this wave's columns of x, as a chunk
+    // item, or -1 past the end (whole 4-lane groups agree).
+    auto item_of = [&](int idx) {
+        const int k = idx >> 5, it = 32 * (wave + KS * k) + (idx & 31);
+        return k < ns && it < 4 * xgroups ? it : -1;
+    };
 
     // 1. Activations first.
     constexpr int kPre = 2;   // x items (8 values) per lane issued ahead (N = 1)
-    const int i0 = 32 * (s0 - g0c);
-    const int items = ns > 0 ? (32 * s1 < 4 * xgroups + 32 * g0c ? 32 * ns : 4 * xgroups - i0) : 0;
     float4 px[kPre][2];
     float2 pm[2];
     if constexpr (!G) {
 #pragma unroll
         for (int k = 0; k < kPre; ++k) {
-            const int it = i0 + (lane + 64 * k < items ? lane + 64 * k : 0);
-            const float4 *src = (const float4 *)x + 2 * (it < 4 * xgroups ? it : 0);
+            const int it = item_of(lane + 64 * k);
+            const float4 *src = (const float4 *)x + 2 * (it >= 0 ? it : 0);
             px[k][0] = src[0];
             px[k][1] = src[1];
         }
@@ -362,25 +379,29 @@ __global__ __launch_bounds__(64 * KS) void smalln_mfma(const uint8_t *__restrict
         }
     }
     asm volatile("" ::: "memory");
-    // 2. Both weight stages.
-    Stage<T, NP, G> st0, st1;
-    load_stage<T, NP, G>(st0, L, clamp(s0), g0c, gdig, n);
-    load_stage<T, NP, G>(st1, L, clamp(s0 + 1), g0c, gdig, n);
+    // 2. The first RING weight stages.
+    constexpr int RING = kRing<T, NP>;
+    Stage<T, NP, G> st[RING];
+#pragma unroll
+    for (int k = 0; k < RING; ++k) load_stage<T, NP, G>(st[k], L, group_of(k), g0c, gdig, n);
     // 3. Activations into LDS (waits for them only).
     if constexpr (!G) {
 #pragma unroll
         for (int k = 0; k < kPre; ++k)
             asm volatile("" : "+v"(px[k][0].x), "+v"(px[k][0].y), "+v"(px[k][0].z), "+v"(px[k][0].w),
                          "+v"(px[k][1].x), "+v"(px[k][1].y), "+v"(px[k][1].z), "+v"(px[k][1].w) :: "memory");
-        // Items are whole 4-lane groups: lanes of one group share validity.
 #pragma unroll
-        for (int k = 0; k < kPre; ++k)
-            if (lane + 64 * k < items) quantize8(px[k][0], px[k][1], 1, 0, i0 + lane + 64 * k, sdig, smeta);
-        for (int k = 64 * kPre; k < items; k += 64)
-            if (lane + k < items) {
-                const float4 *src = (const float4 *)x + 2 * (i0 + lane + k);
-                quantize8(src[0], src[1], 1, 0, i0 + lane + k, sdig, smeta);
+        for (int k = 0; k < kPre; ++k) {
+            const int it = item_of(lane + 64 * k);
+            if (it >= 0) quantize8(px[k][0], px[k][1], 1, 0, it, sdig, smeta);
+        }
+        for (int k = 64 * kPre; k < 32 * ns; k += 64) {
+            const int it = item_of(lane + k);
+            if (it >= 0) {
+                const float4 *src = (const float4 *)x + 2 * it;
+                quantize8(src[0], src[1], 1, 0, it, sdig, smeta);
             }
+        }
         // Each wave reads back only the groups it wrote.
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -397,31 +418,34 @@ __global__ __launch_bounds__(64 * KS) void smalln_mfma(const uint8_t *__restrict
     }
     const uint8_t *dig = G ? gdig : sdig;
 
-    // 4. Two-stage ring, branch-free: an odd count computes its last stage
-    //    twice and drops the copy.
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int i = 0; i < ns; i += 2) {
-        float part[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        compute_stage<T, NP, G>(part, st0, L, clamp(s0 + i), g0c, dig, smeta, n);
-        load_stage<T, NP, G>(st0, L, clamp(s0 + i + 2), g0c, gdig, n);
+    // 4. The ring, branch-free: past the wave's last group a stage repeats
+    //    that group and its sums are dropped.
+    constexpr int NA = kAcc<T, NP>;
+    float acc[NA];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) acc[k] += part[k];
-        float part1[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        compute_stage<T, NP, G>(part1, st1, L, clamp(s0 + i + 1), g0c, dig, smeta, n);
-        load_stage<T, NP, G>(st1, L, clamp(s0 + i + 3), g0c, gdig, n);
-        const float keep = i + 1 < ns ? 1.f : 0.f;
+    for (int k = 0; k < NA; ++k) acc[k] = 0.f;
+    for (int i = 0; i < ns; i += RING) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) acc[k] += keep * part1[k];
+        for (int k = 0; k < RING; ++k) {
+            float part[NA];
+#pragma unroll
+            for (int q = 0; q < NA; ++q) part[q] = 0.f;
+            compute_stage<T, NP, G>(part, st[k], L, group_of(i + k), g0c, dig, smeta, n);
+            load_stage<T, NP, G>(st[k], L, group_of(i + k + RING), g0c, gdig, n);
+            const float keep = i + k < ns ? 1.f : 0.f;
+#pragma unroll
+            for (int q = 0; q < NA; ++q) acc[q] += keep * part[q];
+        }
     }
 
     // 5. Partial sums of the KS waves, added in wave order.
 #pragma unroll
-    for (int k = 0; k < 8; ++k) red[wave][k][lane] = acc[k];
+    for (int k = 0; k < NA; ++k) red[wave][k][lane] = acc[k];
     __syncthreads();
     if (wave != 0) return;
-    float v[8];
+    float v[NA];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < NA; ++k) {
         v[k] = red[0][k][lane];
         for (int q = 1; q < KS; ++q) v[k] += red[q][k][lane];
     }
@@ -430,7 +454,7 @@ __global__ __launch_bounds__(64 * KS) void smalln_mfma(const uint8_t *__restrict
     if constexpr (T == Q6_K) {
         // The two lane halves hold the two scale groups of each 32 columns.
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] += __shfl_xor(v[k], 32, 64);
+        for (int k = 0; k < NA; ++k) v[k] += __shfl_xor(v[k], 32, 64);
 #pragma unroll
         for (int k = 0; k < NP; ++k)
             if (own && k < n && (k & 1) == L.h) {
@@ -439,9 +463,9 @@ __global__ __launch_bounds__(64 * KS) void smalln_mfma(const uint8_t *__restrict
             }
     } else {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < NA; ++k) {
             const int tok = 2 * k + L.h;
-            if (own && 2 * k < NP && tok < n) {
+            if (own && tok < n) {
                 float *dst = y + (size_t)tok * rows + row;
                 *dst = accumulate ? *dst + v[k] : v[k];
             }

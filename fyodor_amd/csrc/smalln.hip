@@ -248,64 +248,80 @@ __device__ __forceinline__ void compute_stage(float (&acc)[(kAcc<T, NP>)], const
     float sum_s[NA], sum_m[NA];
 #pragma unroll
     for (int k = 0; k < NA; ++k) sum_s[k] = sum_m[k] = 0.f;
+    // PAIR blocks at a time: both MFMAs issue before either epilogue reads a
+    // result, so the second covers the first's latency (one at a time when a
+    // block already takes two MFMAs).
+    constexpr int PAIR = kTokenHalves<T, NP> == 1 ? 2 : 1;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        if ((T == Q8_0 || T == Q4_0) && j >= nb) break;
-        i32x4 b;
-        float sc, mn = 0.f;   // per-block multiplier of q.x and of sum x
-        int xg;
-        if constexpr (T == Q4_K) {
-            const int p = j >> 1, nib = j & 1;
-            b = as_i32x4((st.w.q[p] >> (4 * nib)) & 0x0F0F0F0Fu);
-            const uint32_t own = st.w.sl[p];
-            sc = (float)((own >> (12 * nib)) & 63u);
-            mn = (float)((own >> (12 * nib + 6)) & 63u);
-            xg = 8 * (g - g0c) + j;
-        } else if constexpr (T == Q6_K) {
-            const int p = j >> 1, m = j & 1, q = 2 * m + h;
-            u32x4 u;
+    for (int j0 = 0; j0 < 8; j0 += PAIR) {
+        if ((T == Q8_0 || T == Q4_0) && j0 >= nb) break;
+        i32x16 D[PAIR][kTokenHalves<T, NP>];
+        float sc[PAIR], mn[PAIR];   // per-block multipliers of q.x and of sum x
+        int xg[PAIR];
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                u[k] = bytes_minus(((st.w.ql[p][k] >> (4 * m)) & 0x0F0F0F0Fu) |
-                    (((st.w.qh[p][k] >> (2 * q)) & 0x03030303u) << 4), 0x20202020u);
-            b = as_i32x4(u);
-            sc = (float)(int8_t)((st.w.sc[p] >> (8 * q)) & 0xFFu);
-            xg = 8 * (g - g0c) + 4 * (p >> 1) + q;
-        } else if constexpr (T == Q8_0) {
-            b = as_i32x4(st.w.q[j]);
-            sc = f16_to_f32(st.w.d[j]);
-            xg = 8 * (g - g0c) + j;
-        } else {
-            u32x4 u;
+        for (int jj = 0; jj < PAIR; ++jj) {
+            const int j = j0 + jj;
+            i32x4 b;
+            mn[jj] = 0.f;
+            if constexpr (T == Q4_K) {
+                const int p = j >> 1, nib = j & 1;
+                b = as_i32x4((st.w.q[p] >> (4 * nib)) & 0x0F0F0F0Fu);
+                const uint32_t own = st.w.sl[p];
+                sc[jj] = (float)((own >> (12 * nib)) & 63u);
+                mn[jj] = (float)((own >> (12 * nib + 6)) & 63u);
+                xg[jj] = 8 * (g - g0c) + j;
+            } else if constexpr (T == Q6_K) {
+                const int p = j >> 1, m = j & 1, q = 2 * m + h;
+                u32x4 u;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) u[k] = bytes_minus((st.w.q[j][k] >> (4 * h)) & 0x0F0F0F0Fu, 0x08080808u);
-            b = as_i32x4(u);
-            sc = f16_to_f32(st.w.d[j]);
-            xg = 8 * (g - g0c) + j;
-        }
+                for (int k = 0; k < 4; ++k)
+                    u[k] = bytes_minus(((st.w.ql[p][k] >> (4 * m)) & 0x0F0F0F0Fu) |
+                        (((st.w.qh[p][k] >> (2 * q)) & 0x03030303u) << 4), 0x20202020u);
+                b = as_i32x4(u);
+                sc[jj] = (float)(int8_t)((st.w.sc[p] >> (8 * q)) & 0xFFu);
+                xg[jj] = 8 * (g - g0c) + 4 * (p >> 1) + q;
+            } else if constexpr (T == Q8_0) {
+                b = as_i32x4(st.w.q[j]);
+                sc[jj] = f16_to_f32(st.w.d[j]);
+                xg[jj] = 8 * (g - g0c) + j;
+            } else {
+                u32x4 u;
 #pragma unroll
-        for (int th = 0; th < kTokenHalves<T, NP>; ++th) {
-            i32x4 a;
-            if constexpr (G) a = st.a[8 * th + j];
-            else a = *(const i32x4 *)(dig + a_offset<T, NP>(L, g - g0c, j, th, n, nb));
-            const i32x16 D = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, (i32x16){}, 0, 0, 0);
+                for (int k = 0; k < 4; ++k) u[k] = bytes_minus((st.w.q[j][k] >> (4 * h)) & 0x0F0F0F0Fu, 0x08080808u);
+                b = as_i32x4(u);
+                sc[jj] = f16_to_f32(st.w.d[j]);
+                xg[jj] = 8 * (g - g0c) + j;
+            }
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int t = T == Q6_K ? k + 4 * th : 2 * k + h;
-                const int slot = T == Q6_K ? k + 4 * th : k;   // accumulator
-                if (slot >= NA) continue;
-                const float Gs = recombine<T>(D[4 * k], D[4 * k + 1], D[4 * k + 2]);
-                const float2 mt = meta[xg * NP + (t < NP ? t : 0)];
-                if constexpr (T == Q8_0 || T == Q4_0) {
-                    acc[slot] += mt.x * (sc * Gs);
-                } else {
-                    sum_s[slot] += sc * (Gs * mt.x);
-                    if constexpr (T == Q4_K) sum_m[slot] += mn * mt.y;
-                }
+            for (int th = 0; th < kTokenHalves<T, NP>; ++th) {
+                i32x4 a;
+                if constexpr (G) a = st.a[8 * th + j];
+                else a = *(const i32x4 *)(dig + a_offset<T, NP>(L, g - g0c, j, th, n, nb));
+                D[jj][th] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, (i32x16){}, 0, 0, 0);
             }
         }
-        // Keep each sub-block's MFMA next to its epilogue (bounds the live
-        // result registers).
+#pragma unroll
+        for (int jj = 0; jj < PAIR; ++jj) {
+            // A short last Q8_0/Q4_0 group drops its padding block.
+            if ((T == Q8_0 || T == Q4_0) && j0 + jj >= nb) break;
+#pragma unroll
+            for (int th = 0; th < kTokenHalves<T, NP>; ++th)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int t = T == Q6_K ? k + 4 * th : 2 * k + h;
+                    const int slot = T == Q6_K ? k + 4 * th : k;   // accumulator
+                    if (slot >= NA) continue;
+                    const float Gs = recombine<T>(D[jj][th][4 * k], D[jj][th][4 * k + 1], D[jj][th][4 * k + 2]);
+                    const float2 mt = meta[xg[jj] * NP + (t < NP ? t : 0)];
+                    if constexpr (T == Q8_0 || T == Q4_0) {
+                        acc[slot] += mt.x * (sc[jj] * Gs);
+                    } else {
+                        sum_s[slot] += sc[jj] * (Gs * mt.x);
+                        if constexpr (T == Q4_K) sum_m[slot] += mn[jj] * mt.y;
+                    }
+                }
+        }
+        // Bounds the live result registers to one pair.
         __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (T == Q4_K) {

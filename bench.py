@@ -17,6 +17,9 @@ weight matrix; weights and activations are resident in HBM before timing.
 - cpu_baseline: the reference CPU provider (built from the reference sources
   into oracle/_ref) on the same weights, on this host's cores; else this
   repository's C port of the scalar path.
+- prefill: the same matrix times 512 tokens through the MFMA prefill GEMM
+  (one call = activation split + GEMM tiles), in useful TFLOP/s against the
+  dense bf16 MFMA peak.
 
 Prints one JSON line.
 """
@@ -42,6 +45,8 @@ from fyodor_amd.hip import Kernels, Runtime  # noqa: E402
 METRIC = "Q4_K matvec effective HBM GB/s (% of peak), 14336x4096, N=1 and N=8"
 ROWS, COLS = 14336, 4096
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0      # dense MFMA, MI355X
+PREFILL_TOKENS = 512
 MALL_BYTES = 256 * 1024 * 1024
 
 
@@ -176,6 +181,42 @@ def cpu_baseline(weights_host: np.ndarray, x: np.ndarray, y_gpu: np.ndarray, sec
     }
 
 
+def prefill(rt, kern, stream, weights, host_w, steps: int) -> dict:
+    """Q4_K 14336x4096 times PREFILL_TOKENS tokens on the prefill GEMM."""
+    m = PREFILL_TOKENS
+    x = synth.activations(m, COLS, seed=99)
+    x_dev, y_dev = rt.malloc(x.nbytes), rt.malloc(4 * ROWS * m)
+    rt.upload(x_dev, x)
+    need = kern.workspace_bytes(Q4_K, ROWS, COLS, m)
+    work = rt.malloc(need)
+    copies = len(weights)
+
+    def launch(i):
+        return lambda: kern.matmul(weights[i % copies], Q4_K, ROWS, COLS, x_dev, y_dev, m, work, need, stream)
+
+    warm = Graph(rt, stream, [launch(i) for i in range(2)])
+    timed = Graph(rt, stream, [launch(i) for i in range(steps)])
+    warm.launch()
+    rt.sync(stream)
+    start, end = rt.event(), rt.event()
+    rt.record(start, stream)
+    timed.launch()
+    rt.record(end, stream)
+    ms = rt.elapsed_ms(start, end) / steps
+    warm.close()
+    timed.close()
+    for p in (x_dev, y_dev, work):
+        rt.free(p)
+    tflops = 2.0 * ROWS * COLS * m / (ms * 1e-3) / 1e12
+    return {
+        "workload": f"Q4_K {ROWS}x{COLS} x {m} tokens (prefill GEMM)", "kernel": kern.kernel_name(Q4_K, ROWS, COLS, m),
+        "ms_per_call": round(ms, 5), "calls": steps,
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                     "frac_of_fp32_accurate_ceiling": round(tflops / (PEAK_BF16_TFLOPS / 6), 4)},
+    }
+
+
 def calibrate_copy(rt, kern, stream, steps: int) -> int:
     """Copies of a known size: rocprofv3 FETCH_SIZE / WRITE_SIZE per
     dispatch divided into these bytes give the counters' scale factor."""
@@ -200,6 +241,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only the plain 256 MiB device copy used to calibrate HBM byte counters")
+    ap.add_argument("--prefill-steps", type=int, default=20, help="timed prefill GEMM calls (0: skip)")
+    ap.add_argument("--prefill-only", action="store_true", help="run only the prefill GEMM measurement")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (rows would be sharded "
@@ -226,6 +269,13 @@ def main() -> int:
     y_dev = rt.malloc(8 * ROWS * 4)
     work_bytes = max(kern.workspace_bytes(Q4_K, ROWS, COLS, b) for b in (1, 8))
     work = rt.malloc(max(work_bytes, 16))
+
+    if args.prefill_only:
+        print(json.dumps({"prefill": prefill(rt, kern, stream, weights, host_w, max(args.prefill_steps, 1))}),
+              flush=True)
+        for p in weights + [work]:
+            rt.free(p)
+        return 0
 
     results = {}
     for batch in (1, 8):
@@ -264,6 +314,8 @@ def main() -> int:
                "frac": round(gbs8 / PEAK_HBM_GBS, 4), "algorithmic_bytes": bytes8, "traffic": measured_traffic(8),
                "kernel": kern.kernel_name(Q4_K, ROWS, COLS, 8)},
     }
+    if args.prefill_steps > 0:
+        line["prefill"] = prefill(rt, kern, stream, weights, host_w, args.prefill_steps)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(host_w, x8[0].copy(), y1, args.cpu_seconds)
     for p in weights + [work]:

@@ -19,7 +19,7 @@ ROOT = Path(__file__).resolve().parent
 REPO = ROOT.parent
 LIB = ROOT / "lib"
 CSRC = ROOT / "csrc"
-HIP_SOURCES = ["abi.hip", "dense.hip", "smalln.hip", "gemm.hip", "pack.cpp"]
+HIP_SOURCES = ["abi.hip", "dense.hip", "smalln.hip", "prefill.hip", "pack.cpp"]
 C_SOURCES = ["core/compute.c", "core/vendor.c", "rocm/rocm.c"]
 
 HIPCC_FLAGS = [
@@ -27,9 +27,9 @@ HIPCC_FLAGS = [
     # Packed FP32 arithmetic is kept out of every kernel.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-# Per-source additions. The small-N kernels read every MFMA result at once in
-# VALU code: results in VGPRs (not AGPRs) save a copy per register.
-EXTRA_FLAGS = {"smalln.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Per-source additions. The int8 block-dot kernels read every MFMA result at
+# once in VALU code: results in VGPRs (not AGPRs) save a copy per register.
+EXTRA_FLAGS = {f: ["-mllvm", "-amdgpu-mfma-vgpr-form"] for f in ("smalln.hip", "prefill.hip")}
 C_FLAGS = [
     "-std=c17", "-O2", "-fPIC", "-Wall", "-Wextra", "-Wpedantic", "-Wshadow",
     "-D_POSIX_C_SOURCE=200809L",

@@ -25,11 +25,12 @@ bool storage_bytes(unsigned type, size_t rows, size_t cols, size_t *bytes)
     return true;
 }
 
-// Batches above the small-N kernels' 8 columns go to the MFMA GEMM when the
-// type allows it.
-bool use_gemm(unsigned type, size_t cols, size_t batch)
+// Batches above the small-N kernels' 8 columns go to the prefill GEMM
+// (every block format).
+bool use_prefill(unsigned type, size_t cols, size_t batch)
 {
-    return batch > 8 && gemm_supported(type, (int)cols);
+    (void)cols;
+    return batch > 8 && (type == Q4_K || type == Q6_K || type == Q8_0 || type == Q4_0);
 }
 
 int status(hipError_t e)
@@ -71,7 +72,7 @@ NYA_HIP_EXPORT int nya_hip_workspace_bytes(unsigned type, size_t rows, size_t co
     size_t b;
     if (!bytes || !batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return 1;
     const bool dense = type == F32 || type == F16 || type == BF16;
-    *bytes = use_gemm(type, cols, batch) ? gemm_workspace((int)cols, (int)batch)
+    *bytes = use_prefill(type, cols, batch) ? prefill_workspace((int)cols, (int)batch)
            : dense ? 0 : smalln_workspace((int)cols, batch < 8 ? (int)batch : 8);
     return 0;
 }
@@ -89,9 +90,9 @@ NYA_HIP_EXPORT int nya_hip_matmul(uintptr_t w, unsigned type, size_t rows, size_
     const bool fits = workspace && !(workspace & 15u);
     // The GEMM needs its workspace; without one (or a short one) the batch is
     // run 8 columns at a time instead.
-    if (use_gemm(type, cols, batch) && fits && workspace_bytes >= gemm_workspace((int)cols, (int)batch))
-        return status(launch_gemm(type, wp, (const float *)x, (float *)y, (int)rows, (int)cols, (int)batch,
-                                  (void *)workspace, s));
+    if (use_prefill(type, cols, batch) && fits && workspace_bytes >= prefill_workspace((int)cols, (int)batch))
+        return status(launch_prefill(type, wp, (const float *)x, (float *)y, (int)rows, (int)cols, (int)batch,
+                                     (void *)workspace, s));
     for (size_t done = 0; done < batch; done += 8) {
         const int n = (int)(batch - done < 8 ? batch - done : 8);
         const float *xp = (const float *)x + done * cols;
@@ -119,7 +120,7 @@ NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_
     size_t b;
     if (!batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return NULL;
     if (type == F32 || type == F16 || type == BF16) return "skinny_dense";
-    if (use_gemm(type, cols, batch)) return "gemm_tile";
+    if (use_prefill(type, cols, batch)) return "prefill_mfma";
     return "smalln_mfma";
 }
 

@@ -18,13 +18,15 @@ size_t smalln_workspace(int cols, int batch);
 hipError_t launch_smalln(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols, int batch,
     void *workspace, hipStream_t stream);
 
-// Batches above 8 with quantized weights (gemm.hip): MFMA tiles over the
-// whole batch, weights read once per 128 batch rows. gemm_supported says
-// whether the type and width qualify; the launch needs gemm_workspace bytes
-// of 16-byte-aligned device scratch.
-bool gemm_supported(unsigned type, int cols);
-size_t gemm_workspace(int cols, int batch);
-hipError_t launch_gemm(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols, int batch,
+// Activation digits of `batch` tokens x `cols` columns (row stride ldx) in
+// the layout of blockdot.h for np token slots (smalln.hip).
+hipError_t launch_quantize_x(const float *x, int ldx, int cols, int batch, int np, uint8_t *dig, float2 *meta,
+    hipStream_t stream);
+
+// Batches above 8 with quantized weights on int8 MFMA (prefill.hip): needs
+// prefill_workspace bytes of 16-byte-aligned device scratch.
+size_t prefill_workspace(int cols, int batch);
+hipError_t launch_prefill(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols, int batch,
     void *workspace, hipStream_t stream);
 
 // Plain 16-byte-per-thread device copy (dense.hip), for counter calibration.

@@ -31,83 +31,13 @@
 // columns of x into LDS; N >= 2 reads digits written once per call by
 // quantize_x into the workspace. Columns beyond kChunkCols run as further
 // launches that add into y.
-#include "device.h"
-#include "formats.h"
+#include "blockdot.h"
 #include "kernels.h"
 
 namespace fy {
 namespace {
 
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-typedef int i32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
 constexpr int kChunkCols = 16384;   // columns per launch (bounds the LDS copy of x)
-constexpr int kSlotBytes = 32;      // one digit of one token over a 32-column group
-
-// Bytes v < 128 minus c (c <= 64) as signed 8-bit values, four at once.
-__device__ __forceinline__ uint32_t bytes_minus(uint32_t v, uint32_t c4)
-{
-    return ((v | 0x80808080u) - c4) ^ 0x80808080u;
-}
-
-__device__ __forceinline__ i32x4 as_i32x4(u32x4 v) { return __builtin_bit_cast(i32x4, v); }
-
-// ---- activation digits ---------------------------------------------------
-// Group g (32 columns) of a chunk: digits at dig + g * 128 * np, slot 4t + d
-// (32 bytes), meta[g * np + t] = {2^(e-22), (float)sum(X) * 2^(e-22)}.
-
-// Byte b of each of four words, packed into one word.
-__device__ __forceinline__ uint32_t gather_byte(const int (&v)[8], int k, int b)
-{
-    const uint32_t sel = 0x0c0c0000u | (uint32_t)(4 + b) << 8 | (uint32_t)b;
-    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)v[k + 1], (uint32_t)v[k], sel);
-    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)v[k + 3], (uint32_t)v[k + 2], sel);
-    return lo | hi << 16;
-}
-
-// Item `item` = 8 consecutive values of token t (4 items per group). The four
-// lanes of a group are consecutive and must call this together. The signed
-// digits of X are byte 0 of X, byte 1 of X + 2^7 and byte 2 of X + 2^7 + 2^15
-// (a1 = sext8((X + 128) >> 8), a2 = (X + 32896) >> 16).
-__device__ __forceinline__ void quantize8(float4 v0, float4 v1, int np, int t, int item, uint8_t *dig, float2 *meta)
-{
-    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-    float m = 0.f, z = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        m = fmaxf(m, fabsf(v[j]));
-        z = __builtin_fmaf(v[j], 0.f, z);   // NaN iff some value is inf or NaN
-    }
-    m = fmaxf(m, __shfl_xor(m, 1, 64));
-    m = fmaxf(m, __shfl_xor(m, 2, 64));
-    z += __shfl_xor(z, 1, 64);
-    z += __shfl_xor(z, 2, 64);
-    int ex = 0;
-    (void)__builtin_frexpf(m, &ex);
-    const bool finite = z == z;
-    const int shift = m > 0.f && finite ? 22 - ex : 0;
-    const float scale = !finite ? __builtin_nanf("") : m > 0.f ? __builtin_ldexpf(1.f, ex - 22) : 0.f;
-    int X[8], X1[8], X2[8];
-    int sx = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        // A non-finite group's digits are never used: its scale is NaN.
-        X[j] = (int)__builtin_rintf(__builtin_ldexpf(v[j], shift));
-        X1[j] = X[j] + 128;
-        X2[j] = X[j] + 32896;
-        sx += X[j];
-    }
-    sx += __shfl_xor(sx, 1, 64);
-    sx += __shfl_xor(sx, 2, 64);
-    const int g = item >> 2, part = item & 3;
-    uint8_t *dst = dig + (size_t)g * 4 * kSlotBytes * np + kSlotBytes * 4 * t + 8 * part;
-    *(uint2 *)dst = make_uint2(gather_byte(X, 0, 0), gather_byte(X, 4, 0));
-    *(uint2 *)(dst + kSlotBytes) = make_uint2(gather_byte(X1, 0, 1), gather_byte(X1, 4, 1));
-    *(uint2 *)(dst + 2 * kSlotBytes) = make_uint2(gather_byte(X2, 0, 2), gather_byte(X2, 4, 2));
-    *(uint2 *)(dst + 3 * kSlotBytes) = make_uint2(0, 0);
-    if (part == 0) meta[(size_t)g * np + t] = make_float2(scale, (float)sx * scale);
-}
 
 // Digits of n tokens x cols columns (row stride ldx) for a batch of np slots.
 __global__ __launch_bounds__(256) void quantize_x(const float *__restrict__ x, int ldx, int cols, int n, int np,
@@ -120,13 +50,6 @@ __global__ __launch_bounds__(256) void quantize_x(const float *__restrict__ x, i
     const float4 *src = (const float4 *)(x + (size_t)t * ldx) + 2 * item;
     quantize8(src[0], src[1], np, t, item, dig, meta);
 }
-
-// ---- weight stages -------------------------------------------------------
-template <unsigned T> struct WStage;
-template <> struct WStage<Q4_K> { u32x4 q[4]; u32x4 sl; };
-template <> struct WStage<Q6_K> { u32x4 ql[4], qh[4]; u32x4 sc; uint32_t d; };
-template <> struct WStage<Q8_0> { u32x4 q[8]; uint32_t d[8]; };
-template <> struct WStage<Q4_0> { u32x4 q[8]; uint32_t d[8]; };
 
 // MFMAs per 256-column group, and how many activation operands each needs.
 template <unsigned T, int NP> constexpr int kTokenHalves = (T == Q6_K && NP > 4) ? 2 : 1;
@@ -141,51 +64,6 @@ struct Stage {
     WStage<T> w;
     i32x4 a[G ? 8 * kTokenHalves<T, NP> : 1];
 };
-
-// The lane's place in the tile.
-struct Lane {
-    const uint8_t *tile;
-    int R, r, h, slot;
-    int groups, blocks;   // per row: 256-column groups, 32-column blocks
-};
-
-// Blocks in group g (Q8_0/Q4_0 last group may be short).
-__device__ __forceinline__ int group_blocks(const Lane &L, int g)
-{
-    const int nb = L.blocks - 8 * g;
-    return nb < 8 ? nb : 8;
-}
-
-template <unsigned T>
-__device__ __forceinline__ void load_weights(WStage<T> &w, const Lane &L, int g)
-{
-    const int R = L.R, r = L.r, h = L.h;
-    if constexpr (T == Q4_K) {
-        const uint8_t *b = L.tile + (size_t)144 * R * g;
-#pragma unroll
-        for (int p = 0; p < 4; ++p) w.q[p] = *(const u32x4 *)(b + 32 * R * p + 16 * R * h + 16 * r);
-        w.sl = *(const u32x4 *)(b + 128 * R + 16 * r);
-    } else if constexpr (T == Q6_K) {
-        const uint8_t *b = L.tile + (size_t)208 * R * g;
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            w.ql[p] = *(const u32x4 *)(b + 48 * R * p + 16 * R * h + 16 * r);
-            w.qh[p] = *(const u32x4 *)(b + 48 * R * p + 32 * R + 16 * r);
-        }
-        w.sc = *(const u32x4 *)(b + 192 * R + 16 * r);
-        w.d = *(const uint16_t *)(L.tile + (size_t)208 * R * L.groups + 2 * R * g + 2 * r);
-    } else {
-        constexpr int quant = T == Q8_0 ? 32 : 16;
-        const int nb = group_blocks(L, g);
-        const uint8_t *b = L.tile + (size_t)(quant + 2) * 8 * R * g;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int jj = j < nb ? j : nb - 1;
-            w.q[j] = *(const u32x4 *)(b + quant * R * jj + quant * r + (T == Q8_0 ? 16 * h : 0));
-            w.d[j] = *(const uint16_t *)(b + quant * R * nb + 2 * R * jj + 2 * r);
-        }
-    }
-}
 
 // Byte offset of the activation operand of MFMA j (token half th) of
 // chunk-local group gl in the digit array. Lanes whose A-row is not live for
@@ -222,17 +100,6 @@ __device__ __forceinline__ void load_stage(Stage<T, NP, G> &st, const Lane &L, i
     load_weights<T>(st.w, L, g);
 }
 
-// sum q * X of one 32-column block from its three digit sums. Q4_K (q <= 15)
-// and Q4_0 (|q| <= 8): |D2| <= 32 * 15 * 64, so the whole sum fits int32.
-// Q8_0 (|q| <= 128) and Q6_K (|q| <= 32) can reach 2^34: the low two digits
-// (below 2^27) combine in int32, the top one in float.
-template <unsigned T>
-__device__ __forceinline__ float recombine(int d0, int d1, int d2)
-{
-    if constexpr (T == Q4_K || T == Q4_0) return (float)(d2 * 65536 + d1 * 256 + d0);
-    else return (float)d2 * 65536.f + (float)(d1 * 256 + d0);
-}
-
 // The block dot products of one stage (group g) into acc. Q4_K/Q8_0/Q4_0:
 // acc[k] belongs to token 2k + h; Q6_K: acc[t] to token t (this lane half's
 // scale groups). The K-quant superblock scales d and dmin multiply the
@@ -261,37 +128,9 @@ __device__ __forceinline__ void compute_stage(float (&acc)[(kAcc<T, NP>)], const
 #pragma unroll
         for (int jj = 0; jj < PAIR; ++jj) {
             const int j = j0 + jj;
-            i32x4 b;
-            mn[jj] = 0.f;
-            if constexpr (T == Q4_K) {
-                const int p = j >> 1, nib = j & 1;
-                b = as_i32x4((st.w.q[p] >> (4 * nib)) & 0x0F0F0F0Fu);
-                const uint32_t own = st.w.sl[p];
-                sc[jj] = (float)((own >> (12 * nib)) & 63u);
-                mn[jj] = (float)((own >> (12 * nib + 6)) & 63u);
-                xg[jj] = 8 * (g - g0c) + j;
-            } else if constexpr (T == Q6_K) {
-                const int p = j >> 1, m = j & 1, q = 2 * m + h;
-                u32x4 u;
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    u[k] = bytes_minus(((st.w.ql[p][k] >> (4 * m)) & 0x0F0F0F0Fu) |
-                        (((st.w.qh[p][k] >> (2 * q)) & 0x03030303u) << 4), 0x20202020u);
-                b = as_i32x4(u);
-                sc[jj] = (float)(int8_t)((st.w.sc[p] >> (8 * q)) & 0xFFu);
-                xg[jj] = 8 * (g - g0c) + 4 * (p >> 1) + q;
-            } else if constexpr (T == Q8_0) {
-                b = as_i32x4(st.w.q[j]);
-                sc[jj] = f16_to_f32(st.w.d[j]);
-                xg[jj] = 8 * (g - g0c) + j;
-            } else {
-                u32x4 u;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) u[k] = bytes_minus((st.w.q[j][k] >> (4 * h)) & 0x0F0F0F0Fu, 0x08080808u);
-                b = as_i32x4(u);
-                sc[jj] = f16_to_f32(st.w.d[j]);
-                xg[jj] = 8 * (g - g0c) + j;
-            }
+            int xgl;
+            const i32x4 b = block_operand<T>(st.w, j, h, sc[jj], mn[jj], xgl);
+            xg[jj] = 8 * (g - g0c) + xgl;
 #pragma unroll
             for (int th = 0; th < kTokenHalves<T, NP>; ++th) {
                 i32x4 a;
@@ -324,16 +163,11 @@ __device__ __forceinline__ void compute_stage(float (&acc)[(kAcc<T, NP>)], const
         // Bounds the live result registers to one pair.
         __builtin_amdgcn_sched_barrier(0);
     }
-    if constexpr (T == Q4_K) {
-        const uint32_t dd = (st.w.sl.x >> 24) | ((st.w.sl.y >> 24) << 8) | ((st.w.sl.z >> 24) << 16) |
-            ((st.w.sl.w >> 24) << 24);
-        const float d = f16_to_f32(dd & 0xFFFFu), dmin = f16_to_f32(dd >> 16);
+    if constexpr (T == Q4_K || T == Q6_K) {
+        float d, dmin;
+        group_scales<T>(st.w, d, dmin);
 #pragma unroll
-        for (int k = 0; k < NA; ++k) acc[k] += d * sum_s[k] - dmin * sum_m[k];
-    } else if constexpr (T == Q6_K) {
-        const float d = f16_to_f32(st.w.d);
-#pragma unroll
-        for (int k = 0; k < NA; ++k) acc[k] += d * sum_s[k];
+        for (int k = 0; k < NA; ++k) acc[k] += T == Q4_K ? d * sum_s[k] - dmin * sum_m[k] : d * sum_s[k];
     }
 }
 
@@ -536,6 +370,15 @@ int padded_tokens(int n)
 
 }  // namespace
 
+hipError_t launch_quantize_x(const float *x, int ldx, int cols, int batch, int np, uint8_t *dig, float2 *meta,
+    hipStream_t s)
+{
+    const int total = batch * (cols / 8);
+    hipLaunchKernelGGL(quantize_x, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, x, ldx, cols, batch, np,
+        dig, meta);
+    return hipGetLastError();
+}
+
 size_t smalln_workspace(int cols, int batch)
 {
     const int np = padded_tokens(batch);
@@ -555,10 +398,7 @@ hipError_t launch_smalln(unsigned type, const uint8_t *w, const float *x, float 
         uint8_t *dig = (uint8_t *)workspace;
         float2 *meta = dig ? (float2 *)(dig + (size_t)ccols / 32 * 4 * kSlotBytes * np) : nullptr;
         if (np > 1) {
-            const int total = batch * ccols / 8;
-            hipLaunchKernelGGL(quantize_x, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
-                x + c0, cols, ccols, batch, np, dig, meta);
-            const hipError_t e = hipGetLastError();
+            const hipError_t e = launch_quantize_x(x + c0, cols, ccols, batch, np, dig, meta, s);
             if (e != hipSuccess) return e;
         }
         hipError_t e;

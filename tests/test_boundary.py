@@ -131,18 +131,19 @@ def test_pack_is_the_specified_permutation(kernels, t, rows, cols):
     assert np.array_equal(unpack_reference(dev, t, rows, cols), w)
 
 
-def test_gemm_dispatch_and_workspace():
-    """Batches above 8 of the quantized types ask for the activation pieces'
-    workspace and name the MFMA GEMM; dense types and small batches need
-    none (nothing is launched)."""
+def test_prefill_dispatch_and_workspace():
+    """Batch 1 needs no workspace; batches of 2..8 need the activation digits
+    of a padded token count, batches above 8 those of the prefill GEMM
+    (tokens rounded up to 32); dense types need none (nothing is
+    launched)."""
     kern = Kernels()
     for t in (Q4_0, Q8_0, Q4_K, Q6_K):
         assert kern.workspace_bytes(t, 4096, 4096, 1) == 0
         assert kern.workspace_bytes(t, 4096, 4096, 8) == 4096 // 32 * 136 * 8
         assert kern.workspace_bytes(t, 4096, 4096, 3) == 4096 // 32 * 136 * 4
-        assert kern.workspace_bytes(t, 4096, 4096, 9) == 6 * 4096 * 9
-        assert kern.workspace_bytes(t, 4096, 4096, 512) == 6 * 4096 * 512
-        assert kern.kernel_name(t, 4096, 4096, 512) == "gemm_tile"
+        assert kern.workspace_bytes(t, 4096, 4096, 9) == 4096 // 32 * 136 * 32
+        assert kern.workspace_bytes(t, 4096, 4096, 512) == 4096 // 32 * 136 * 512
+        assert kern.kernel_name(t, 4096, 4096, 512) == "prefill_mfma"
         assert kern.kernel_name(t, 4096, 4096, 8) == "smalln_mfma"
     for t in (F32, BF16):
         assert kern.workspace_bytes(t, 4096, 4096, 512) == 0

@@ -1,4 +1,4 @@
-"""The MFMA prefill GEMM (batches above 8 of Q4_0 / Q8_0 / Q4_K / Q6_K).
+"""The int8-MFMA prefill GEMM (batches above 8 of Q4_0 / Q8_0 / Q4_K / Q6_K).
 
 - prefill shapes of the 8B-class projections at batch 128..512: sampled
   tokens (both tile edges included) against the double-precision oracle
@@ -7,8 +7,8 @@
 - batch and row tails (batch 9, 127..129, 257; 200 rows = one full and one
   partial weight tile) with canaries on both sides of the output;
 - through the kernel library's C ABI: the GEMM (workspace given) against the
-  same request run 8 columns at a time (no workspace), and the workspace size
-  it asks for.
+  same request run through the small-N path (same integer block sums,
+  different fp32 summation order), and the workspace size it asks for.
 """
 import numpy as np
 import pytest
@@ -66,14 +66,14 @@ def hip():
 
 
 @pytest.mark.parametrize("type_id", QUANT, ids=lambda t: TYPE_NAMES[t])
-def test_gemm_matches_tiled_path(hip, type_id):
+def test_prefill_matches_tiled_path(hip, type_id):
     rt, kern, stream = hip
     rows, cols, batch = 384, 2048, 40
     w = synth.weights(type_id, rows, cols, 77 + type_id)
     x = synth.activations(batch, cols, 78 + type_id)
     need = kern.workspace_bytes(type_id, rows, cols, batch)
-    assert need == 6 * cols * batch
-    assert kern.kernel_name(type_id, rows, cols, batch) == "gemm_tile"
+    assert need == cols // 32 * 136 * 64          # batch rounded up to 32 tokens
+    assert kern.kernel_name(type_id, rows, cols, batch) == "prefill_mfma"
     wdev, xdev = rt.malloc(storage_bytes(type_id, rows, cols)), rt.malloc(x.nbytes)
     ydev, work = rt.malloc(4 * rows * batch), rt.malloc(need)
     try:
@@ -81,11 +81,11 @@ def test_gemm_matches_tiled_path(hip, type_id):
         rt.upload(xdev, x)
         kern.matmul(wdev, type_id, rows, cols, xdev, ydev, batch, work, need, stream)
         rt.sync(stream)
-        gemm = rt.download(ydev, np.empty((batch, rows), dtype=np.float32))
+        pre = rt.download(ydev, np.empty((batch, rows), dtype=np.float32))
         kern.matmul(wdev, type_id, rows, cols, xdev, ydev, batch, 0, 0, stream)
         rt.sync(stream)
         tiled = rt.download(ydev, np.empty((batch, rows), dtype=np.float32))
-        # A workspace one byte short is refused by the GEMM: tiled again.
+        # A workspace one byte short is refused by the prefill GEMM: tiled again.
         kern.matmul(wdev, type_id, rows, cols, xdev, ydev, batch, work, need - 1, stream)
         rt.sync(stream)
         short = rt.download(ydev, np.empty((batch, rows), dtype=np.float32))
@@ -93,4 +93,4 @@ def test_gemm_matches_tiled_path(hip, type_id):
         for p in (wdev, xdev, ydev, work):
             rt.free(p)
     assert np.array_equal(short, tiled)
-    assert rel_l2(gemm, tiled) <= 2e-6
+    assert rel_l2(pre, tiled) <= 2e-6

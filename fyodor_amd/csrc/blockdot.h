@@ -142,11 +142,21 @@ __device__ __forceinline__ void load_weights(WStage<T> &w, const Lane &L, int g)
 // and Q4_0 (|q| <= 8): |D2| <= 32 * 15 * 64, so the whole sum fits int32.
 // Q8_0 (|q| <= 128) and Q6_K (|q| <= 32) can reach 2^34: the low two digits
 // (below 2^27) combine in int32, the top one in float.
+// The int32 form is evaluated as (d2 * 2^8 + d1) * 2^8 + d0, two shift-adds;
+// the empty asm keeps the compiler from re-associating it into two shifts
+// and a three-input add. (It touches no register the MFMA writes: those are
+// read only by compiler-visible code, which keeps the MFMA result hazards
+// under the compiler's control.)
 template <unsigned T>
 __device__ __forceinline__ float recombine(int d0, int d1, int d2)
 {
-    if constexpr (T == Q4_K || T == Q4_0) return (float)(d2 * 65536 + d1 * 256 + d0);
-    else return (float)d2 * 65536.f + (float)(d1 * 256 + d0);
+    if constexpr (T == Q4_K || T == Q4_0) {
+        int u = d2 * 256 + d1;
+        asm("" : "+v"(u));
+        return (float)(u * 256 + d0);
+    } else {
+        return (float)d2 * 65536.f + (float)(d1 * 256 + d0);
+    }
 }
 
 // Block j (32 columns) of one group for this lane (half h): the B operand

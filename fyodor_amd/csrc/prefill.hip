@@ -20,6 +20,8 @@
 namespace fy {
 namespace {
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
 constexpr int kRowTiles = 4;   // 32-row tiles per workgroup (one per wavefront)
 
 // Tokens per workgroup: 32 (four MFMA token blocks of 8); Q6_K, whose blocks
@@ -34,12 +36,26 @@ template <unsigned T> constexpr int kDigitLoads = kGroupDigits<T> / (16 * 256); 
 template <unsigned T> constexpr int kHalves = T == Q6_K ? 2 : 1;   // MFMAs per token block
 template <unsigned T> constexpr int kLaneTokens = T == Q6_K ? 8 : 4; // accumulators per token block
 
-// Every thread stores one scale pair per group (branch-free); entries past
-// kGroupMeta are duplicates nobody reads.
+// LDS staging of one group, double-buffered. Every thread stores one digit
+// chunk per load and one scale pair (branch-free; for Q6_K the entries past
+// kGroupMeta are duplicates nobody reads).
+//
+// 32-token types: token block tb, digit slot s (= 4 * token + digit within
+// the block) and column half h of block j sit at
+// 4096 j + 1024 tb + 512 h + 16 (s ^ 8 h): the sixteen lanes that one LDS
+// cycle serves read 256 contiguous bytes, and the staging stores (h
+// alternating with the thread index) land on both halves of the banks.
+// Activation scales are stored token-permuted, mx[32 j + i] for token tau(i),
+// tau(i) = 8 (i / 8) + 2 (i % 4) + (i / 4) % 2: lane half h reads its four
+// tokens 8 tb + 2 k + h (k = 0..3) as one 16-byte load at 32 j + 8 tb + 4 h.
+// Q4_K also stores the block sums of x as the A operand of the min-term MFMA:
+// my[4 l + s] = sum x of block 2 s + l / 32 for token tau(l % 32).
+// Q6_K keeps tokens in order: mx[kTokens * j + t].
 template <unsigned T>
 struct Staging {
     uint8_t dig[2][kGroupDigits<T>];
-    float2 meta[2][kGroupMeta<T> > 256 ? kGroupMeta<T> : 256];
+    float mx[2][256];
+    float my[T == Q4_K ? 2 : 1][T == Q4_K ? 256 : 1];
 };
 
 // This thread's share of group g's digits and scales.
@@ -69,18 +85,32 @@ __device__ __forceinline__ void fetch_group(AFetch<T> &f, const uint8_t *__restr
     f.m = meta[(size_t)xg * np + m0 + e % kTokens<T>];
 }
 
+// Position of token t (0..31) in the permuted scale order.
+__device__ __forceinline__ int tau_inv(int t) { return 8 * (t >> 3) + 4 * (t & 1) + ((t >> 1) & 3); }
+
 template <unsigned T>
 __device__ __forceinline__ void store_group(Staging<T> &s, int buf, const AFetch<T> &f)
 {
     const int tid = threadIdx.x;
+    if constexpr (T == Q6_K) {
 #pragma unroll
-    for (int k = 0; k < kDigitLoads<T>; ++k) *(u32x4 *)(s.dig[buf] + 16 * (tid + 256 * k)) = f.d[k];
-    s.meta[buf][tid] = f.m;
+        for (int k = 0; k < kDigitLoads<T>; ++k) *(u32x4 *)(s.dig[buf] + 16 * (tid + 256 * k)) = f.d[k];
+        s.mx[buf][tid] = f.m.x;
+    } else {
+        // Chunk tid of block k: slot tid / 2 (token block tid / 64), half tid % 2.
+        const int slot = (tid >> 1) & 31, h = tid & 1;
+        const int at = 1024 * (tid >> 6) + 512 * h + 16 * (slot ^ (8 * h));
+#pragma unroll
+        for (int k = 0; k < kDigitLoads<T>; ++k) *(u32x4 *)(s.dig[buf] + kBlockDigits<T> * k + at) = f.d[k];
+        const int j = tid >> 5, i = tau_inv(tid & 31);
+        s.mx[buf][32 * j + i] = f.m.x;
+        if constexpr (T == Q4_K) s.my[buf][4 * (32 * (j & 1) + i) + (j >> 1)] = f.m.y;
+    }
 }
 
 // LDS offset of the A operand of block j, token block tb, token half th for
-// this lane (chunk-local: x group xgl of the group), or of token 0's zero
-// slot when the lane's A-row is not live for the n tokens left.
+// this lane (chunk-local: x group xgl of the group), or of a zero slot when
+// the lane's A-row is not live for the n tokens left.
 template <unsigned T>
 __device__ __forceinline__ int a_lds(const Lane &L, int xgl, int j, int tb, int th, int n)
 {
@@ -91,7 +121,8 @@ __device__ __forceinline__ int a_lds(const Lane &L, int xgl, int j, int tb, int 
         return kBlockDigits<T> * xgl + (live ? 128 * (8 * tb + t) + kSlotBytes * d : kSlotBytes * 3) + 16 * (p & 1);
     } else {
         const bool live = 8 * tb + (L.slot >> 2) < n;
-        return kBlockDigits<T> * xgl + (live ? 1024 * tb + kSlotBytes * L.slot : kSlotBytes * 3) + 16 * L.h;
+        const int slot = live ? L.slot : 3;   // token 0's zero slot
+        return kBlockDigits<T> * xgl + (live ? 1024 * tb : 0) + 512 * L.h + 16 * (slot ^ (8 * L.h));
     }
 }
 
@@ -138,13 +169,13 @@ __global__ __launch_bounds__(256) void prefill_mfma(const uint8_t *__restrict__ 
 
     for (int g = 0; g < groups; ++g) {
         const uint8_t *sd = S.dig[g & 1];
-        const float2 *sm = S.meta[g & 1];
+        const float *smx = S.mx[g & 1];
         const int nb = (T == Q8_0 || T == Q4_0) ? group_blocks(L, g) : 8;
-        float sum_s[TBN][NL], sum_m[TBN][NL];
+        float sum_s[TBN][NL];
 #pragma unroll
         for (int tb = 0; tb < TBN; ++tb)
 #pragma unroll
-            for (int k = 0; k < NL; ++k) sum_s[tb][k] = sum_m[tb][k] = 0.f;
+            for (int k = 0; k < NL; ++k) sum_s[tb][k] = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             if ((T == Q8_0 || T == Q4_0) && j >= nb) break;
@@ -165,34 +196,57 @@ __global__ __launch_bounds__(256) void prefill_mfma(const uint8_t *__restrict__ 
                         D[q][th] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, (i32x16){}, 0, 0, 0);
                     }
 #pragma unroll
-                for (int q = 0; q < TBS; ++q)
+                for (int q = 0; q < TBS; ++q) {
+                    const int tb = tb0 + q;
+                    if constexpr (T == Q6_K) {
 #pragma unroll
-                    for (int th = 0; th < kHalves<T>; ++th)
+                        for (int th = 0; th < kHalves<T>; ++th)
+#pragma unroll
+                            for (int k = 0; k < 4; ++k) {
+                                const float Gs = recombine<T>(D[q][th][4 * k], D[q][th][4 * k + 1], D[q][th][4 * k + 2]);
+                                sum_s[tb][k + 4 * th] += sc * (Gs * smx[TOK * xgl + 8 * tb + k + 4 * th]);
+                            }
+                    } else {
+                        // Scales of tokens 8 tb + 2 k + h, k = 0..3.
+                        const float4 mx = *(const float4 *)(smx + 32 * xgl + 8 * tb + 4 * L.h);
+                        const float m4[4] = {mx.x, mx.y, mx.z, mx.w};
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
-                            const int tb = tb0 + q;
-                            const int t = T == Q6_K ? k + 4 * th : 2 * k + L.h;   // token within the block
-                            const int slot = T == Q6_K ? k + 4 * th : k;
-                            const float Gs = recombine<T>(D[q][th][4 * k], D[q][th][4 * k + 1], D[q][th][4 * k + 2]);
-                            const float2 mt = sm[TOK * xgl + 8 * tb + t];
-                            if constexpr (T == Q8_0 || T == Q4_0) {
-                                sum_s[tb][slot] += mt.x * (sc * Gs);
-                            } else {
-                                sum_s[tb][slot] += sc * (Gs * mt.x);
-                                if constexpr (T == Q4_K) sum_m[tb][slot] += mn * mt.y;
-                            }
+                            const float Gs = recombine<T>(D[q][0][4 * k], D[q][0][4 * k + 1], D[q][0][4 * k + 2]);
+                            if constexpr (T == Q4_K) sum_s[tb][k] += sc * (Gs * m4[k]);
+                            else sum_s[tb][k] += m4[k] * (sc * Gs);
                         }
+                    }
+                }
                 __builtin_amdgcn_sched_barrier(0);
             }
+            (void)mn;
         }
         float d, dmin;
         group_scales<T>(st[0], d, dmin);
+        if constexpr (T == Q4_K) {
+            // Min term sum_j m_j * (sum x over block j) for the 32 rows x 32
+            // tokens: A = block sums (lane l: blocks 2s + l / 32 of token
+            // tau(l % 32)), B = the rows' 6-bit minimums; D row i is token
+            // tau(i), the token of acc[i / 8][i % 4] in lane half (i / 4) % 2.
+            const float4 ys = *(const float4 *)(S.my[g & 1] + 4 * lane);
+            const float ya[4] = {ys.x, ys.y, ys.z, ys.w};
+            f32x16 M = {};
 #pragma unroll
-        for (int tb = 0; tb < TBN; ++tb)
+            for (int s2 = 0; s2 < 4; ++s2) {
+                const float m = (float)((st[0].sl[s2] >> (12 * L.h + 6)) & 63u);
+                M = __builtin_amdgcn_mfma_f32_32x32x2f32(ya[s2], m, M, 0, 0, 0);
+            }
 #pragma unroll
-            for (int k = 0; k < NL; ++k)
-                acc[tb][k] += T == Q4_K ? d * sum_s[tb][k] - dmin * sum_m[tb][k]
-                            : T == Q6_K ? d * sum_s[tb][k] : sum_s[tb][k];
+            for (int tb = 0; tb < TBN; ++tb)
+#pragma unroll
+                for (int k = 0; k < NL; ++k) acc[tb][k] += d * sum_s[tb][k] - dmin * M[4 * tb + k];
+        } else {
+#pragma unroll
+            for (int tb = 0; tb < TBN; ++tb)
+#pragma unroll
+                for (int k = 0; k < NL; ++k) acc[tb][k] += T == Q6_K ? d * sum_s[tb][k] : sum_s[tb][k];
+        }
         // Group g + 1's activations into the other buffer (its readers passed
         // the last barrier), fetch group g + 2, and rotate the weight ring.
         store_group(S, (g + 1) & 1, af);

@@ -72,7 +72,7 @@ NYA_HIP_EXPORT int nya_hip_workspace_bytes(unsigned type, size_t rows, size_t co
     size_t b;
     if (!bytes || !batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return 1;
     const bool dense = type == F32 || type == F16 || type == BF16;
-    *bytes = use_prefill(type, cols, batch) ? prefill_workspace((int)cols, (int)batch)
+    *bytes = use_prefill(type, cols, batch) ? prefill_workspace(type, (int)cols, (int)batch)
            : dense ? 0 : smalln_workspace((int)cols, batch < 8 ? (int)batch : 8);
     return 0;
 }
@@ -90,7 +90,7 @@ NYA_HIP_EXPORT int nya_hip_matmul(uintptr_t w, unsigned type, size_t rows, size_
     const bool fits = workspace && !(workspace & 15u);
     // The GEMM needs its workspace; without one (or a short one) the batch is
     // run 8 columns at a time instead.
-    if (use_prefill(type, cols, batch) && fits && workspace_bytes >= prefill_workspace((int)cols, (int)batch))
+    if (use_prefill(type, cols, batch) && fits && workspace_bytes >= prefill_workspace(type, (int)cols, (int)batch))
         return status(launch_prefill(type, wp, (const float *)x, (float *)y, (int)rows, (int)cols, (int)batch,
                                      (void *)workspace, s));
     for (size_t done = 0; done < batch; done += 8) {
@@ -120,7 +120,7 @@ NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_
     size_t b;
     if (!batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return NULL;
     if (type == F32 || type == F16 || type == BF16) return "skinny_dense";
-    if (use_prefill(type, cols, batch)) return "prefill_mfma";
+    if (use_prefill(type, cols, batch)) return prefill_kernel(type);
     return "smalln_mfma";
 }
 

@@ -23,11 +23,19 @@ hipError_t launch_smalln(unsigned type, const uint8_t *w, const float *x, float 
 hipError_t launch_quantize_x(const float *x, int ldx, int cols, int batch, int np, uint8_t *dig, float2 *meta,
     hipStream_t stream);
 
-// Batches above 8 with quantized weights on int8 MFMA (prefill.hip): needs
-// prefill_workspace bytes of 16-byte-aligned device scratch.
-size_t prefill_workspace(int cols, int batch);
+// Batches above 8 with quantized weights: Q4_K / Q8_0 / Q4_0 on fp16 MFMA
+// (prefill_f16.hip), Q6_K on int8 MFMA (prefill.hip). The launch needs
+// prefill_workspace bytes of 16-byte-aligned device scratch; prefill_kernel
+// names the GEMM kernel.
+size_t prefill_workspace(unsigned type, int cols, int batch);
 hipError_t launch_prefill(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols, int batch,
     void *workspace, hipStream_t stream);
+const char *prefill_kernel(unsigned type);
+
+bool prefill_f16_supported(unsigned type);
+size_t prefill_f16_workspace(int cols, int batch);
+hipError_t launch_prefill_f16(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,
+    int batch, void *workspace, hipStream_t stream);
 
 // Plain 16-byte-per-thread device copy (dense.hip), for counter calibration.
 hipError_t launch_copy(uint4 *dst, const uint4 *src, size_t count, hipStream_t stream);

@@ -278,15 +278,19 @@ __global__ __launch_bounds__(256) void prefill_mfma(const uint8_t *__restrict__ 
 
 }  // namespace
 
-size_t prefill_workspace(int cols, int batch)
+size_t prefill_workspace(unsigned type, int cols, int batch)
 {
+    if (prefill_f16_supported(type)) return prefill_f16_workspace(cols, batch);
     const size_t np = ((size_t)batch + 31) / 32 * 32;   // a multiple of every kTokens
     return (size_t)(cols / 32) * (4 * kSlotBytes + 8) * np;
 }
 
+const char *prefill_kernel(unsigned type) { return prefill_f16_supported(type) ? "prefill_f16" : "prefill_mfma"; }
+
 hipError_t launch_prefill(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols, int batch,
     void *workspace, hipStream_t s)
 {
+    if (prefill_f16_supported(type)) return launch_prefill_f16(type, w, x, y, rows, cols, batch, workspace, s);
     const int np = (batch + 31) / 32 * 32;
     uint8_t *dig = (uint8_t *)workspace;
     float2 *meta = (float2 *)(dig + (size_t)(cols / 32) * 4 * kSlotBytes * np);
@@ -296,13 +300,8 @@ hipError_t launch_prefill(unsigned type, const uint8_t *w, const float *x, float
     const unsigned gx = (unsigned)((tiles + kRowTiles - 1) / kRowTiles);
     // Token blocks that hold at least one token.
     auto gy = [&](int tok) { return (unsigned)((batch + tok - 1) / tok); };
-    switch (type) {
-    case Q4_K: hipLaunchKernelGGL(prefill_mfma<Q4_K>, dim3(gx, gy(32)), dim3(256), 0, s, w, dig, meta, y, rows, cols, batch, np); break;
-    case Q6_K: hipLaunchKernelGGL(prefill_mfma<Q6_K>, dim3(gx, gy(16)), dim3(256), 0, s, w, dig, meta, y, rows, cols, batch, np); break;
-    case Q8_0: hipLaunchKernelGGL(prefill_mfma<Q8_0>, dim3(gx, gy(32)), dim3(256), 0, s, w, dig, meta, y, rows, cols, batch, np); break;
-    case Q4_0: hipLaunchKernelGGL(prefill_mfma<Q4_0>, dim3(gx, gy(32)), dim3(256), 0, s, w, dig, meta, y, rows, cols, batch, np); break;
-    default: return hipErrorInvalidValue;
-    }
+    if (type != Q6_K) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(prefill_mfma<Q6_K>, dim3(gx, gy(16)), dim3(256), 0, s, w, dig, meta, y, rows, cols, batch, np);
     return hipGetLastError();
 }
 

@@ -1,0 +1,347 @@
+// Prefill GEMM Y[m][row] = sum_k W[row][k] * X[m][k] for batches above 8 on
+// gfx950 fp16 MFMA (v_mfma_f32_32x32x16_f16), Q4_K / Q8_0 / Q4_0 weights.
+//
+// Numbers. The weights enter the MFMA as exact fp16 integers: Q4_K sc * q
+// (<= 63 * 15 = 945), Q8_0 q, Q4_0 q - 8. Each token's activations are scaled
+// by one power of two s = 2^(14 - E) (2^(E-1) <= max |x| < 2^E over the
+// token) and split into two fp16 pieces, x s = hi + lo + e with hi = fp16(x s)
+// and lo = fp16(x s - hi): |e| <= 2^-22 |x s|, or 2^-25 absolute where lo is
+// subnormal. The MFMA multiplies fp16 pairs exactly and accumulates in fp32,
+// so a block dot is sum (sc q)(hi + lo) with fp32 accumulation error only.
+// What remains for the VALU is the superblock scale d per 256 columns (Q4_K;
+// the 6-bit minimums go through an fp32 MFMA against the per-block sums of
+// x s) or the fp16 block scale per 32 columns (Q8_0, Q4_0), and 1/s once per
+// output. A token holding a non-finite value gets NaN pieces: its outputs are
+// NaN.
+//
+// Column order. A lane of the weight tile holds 16 consecutive columns of a
+// block (tiled layout, formats.h); the cheapest fp16 conversion of its bytes
+// yields columns in the order c0 c2 c1 c3 per 4 bytes. The MFMA sums over its
+// 16 K slots in any order, so the activation pieces are stored in the same
+// order: within every 8 columns, position s holds column pi(s),
+// pi = 0 2 1 3 4 6 5 7.
+//
+// Work split. A workgroup of four wavefronts owns 128 weight rows (one 32-row
+// tile per wavefront) and 32 tokens (the A rows of the MFMA). K advances one
+// 256-column group per step: both pieces of the 32 tokens (32 KiB) are staged
+// in LDS, double-buffered with one barrier per step, rows padded to 528 bytes
+// so the sixteen lanes of one LDS cycle hit distinct banks. The weights of
+// each wavefront's tile stream through the two-stage register ring of
+// blockdot.h.
+#include "blockdot.h"
+#include "kernels.h"
+
+namespace fy {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+constexpr int kRowTiles = 4;      // 32-row tiles per workgroup (one per wavefront)
+constexpr int kTokens = 32;       // tokens per workgroup = MFMA A rows
+constexpr int kPitch = 528;       // LDS bytes per token row of one piece (256 fp16 + 16)
+constexpr int kPieceBytes = kTokens * kPitch;
+
+// ---- activation pieces ---------------------------------------------------
+// Workspace for np tokens (np a multiple of 32): hi[np][cols], lo[np][cols]
+// (fp16, permuted as above), bsum[np][cols / 32] (fp32 sum of x s over each
+// 32-column block) and inv[np] (1 / s, or NaN).
+struct Pieces {
+    _Float16 *hi, *lo;
+    float *bsum, *inv;
+};
+
+__host__ __device__ inline Pieces pieces_of(void *ws, int cols, int np)
+{
+    Pieces p;
+    p.hi = (_Float16 *)ws;
+    p.lo = p.hi + (size_t)np * cols;
+    p.bsum = (float *)(p.lo + (size_t)np * cols);
+    p.inv = p.bsum + (size_t)np * (cols / 32);
+    return p;
+}
+
+__device__ __forceinline__ float block_max(float v, float *red)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    return v;
+}
+
+// One workgroup per token; cols % 32 == 0.
+__global__ __launch_bounds__(256) void split_x(const float *__restrict__ x, int cols, Pieces out)
+{
+    __shared__ float red[4];
+    const int t = blockIdx.x;
+    const float *row = x + (size_t)t * cols;
+    const int chunks = cols / 8;
+    float m = 0.f, z = 0.f;
+    for (int c = threadIdx.x; c < chunks; c += 256) {
+        const float4 a = *(const float4 *)(row + 8 * c), b = *(const float4 *)(row + 8 * c + 4);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+        // NaN iff some value is inf or NaN.
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) z = __builtin_fmaf(v[i], 0.f, z);
+    }
+    m = block_max(m, red);
+    z = block_max(z != z ? 1.f : 0.f, red);
+    const bool finite = z == 0.f;
+    int e = 0;
+    (void)__builtin_frexpf(m, &e);
+    const int shift = m > 0.f ? 14 - e : 0;
+    if (threadIdx.x == 0)
+        out.inv[t] = finite ? __builtin_ldexpf(1.f, -shift) : __builtin_nanf("");
+    for (int c = threadIdx.x; c < chunks; c += 256) {
+        const float4 a = *(const float4 *)(row + 8 * c), b = *(const float4 *)(row + 8 * c + 4);
+        float v[8] = {a.x, a.z, a.y, a.w, b.x, b.z, b.y, b.w};   // columns in pi order
+        float s = 0.f;
+        h8 hi, lo;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[i] = finite ? __builtin_ldexpf(v[i], shift) : __builtin_nanf("");
+            s += v[i];
+            hi[i] = (_Float16)v[i];
+            lo[i] = (_Float16)(v[i] - (float)hi[i]);
+        }
+        *(h8 *)(out.hi + (size_t)t * cols + 8 * c) = hi;
+        *(h8 *)(out.lo + (size_t)t * cols + 8 * c) = lo;
+        // Four consecutive chunks form a 32-column block (256 is a multiple of 4).
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        if ((c & 3) == 0) out.bsum[(size_t)t * (cols / 32) + c / 4] = s;
+    }
+}
+
+// ---- GEMM ---------------------------------------------------------------
+struct Staging {
+    uint8_t x[2][2][kPieceBytes];   // [buffer][piece][token row]
+    float bs[2][256];               // Q4_K block sums: [4 l + s] = block 2s + l/32 of token l % 32
+};
+
+// This thread's share of one group: eight 16-byte chunks and one block sum.
+struct XFetch {
+    u32x4 d[8];
+    float s;
+};
+
+// Chunk c = tid + 256 k: piece c / 1024, token (c / 32) % 32, columns
+// 8 (c % 32) .. of the group. The last group of a Q8_0/Q4_0 row may be short:
+// columns past the row are clamped (their blocks are skipped).
+__device__ __forceinline__ void fetch_x(XFetch &f, const Pieces &p, int cols, int m0, int g, bool sums)
+{
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int c = tid + 256 * k;
+        const _Float16 *plane = (c >> 10) ? p.lo : p.hi;
+        const int tok = (c >> 5) & 31;
+        int col = 256 * g + 8 * (c & 31);
+        col = col < cols ? col : cols - 8;
+        f.d[k] = *(const u32x4 *)(plane + (size_t)(m0 + tok) * cols + col);
+    }
+    if (sums) {
+        const int blocks = cols / 32;
+        const int j = tid >> 5, tok = tid & 31;
+        const int b = 8 * g + j < blocks ? 8 * g + j : blocks - 1;
+        f.s = p.bsum[(size_t)(m0 + tok) * blocks + b];
+    }
+}
+
+__device__ __forceinline__ void store_x(Staging &S, int buf, const XFetch &f, bool sums)
+{
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int c = tid + 256 * k;
+        *(u32x4 *)(S.x[buf][c >> 10] + kPitch * ((c >> 5) & 31) + 16 * (c & 31)) = f.d[k];
+    }
+    if (sums) {
+        const int j = tid >> 5, tok = tid & 31;
+        S.bs[buf][4 * (32 * (j & 1) + tok) + (j >> 1)] = f.s;
+    }
+}
+
+__device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+
+// fp16 pairs 1024 + (byte 0, byte 2) and 1024 + (byte 1, byte 3) of v (bytes
+// below 2^10 - 1024 = 0x3ff: the byte becomes the low mantissa bits under
+// the exponent byte 0x64).
+__device__ __forceinline__ h2 pair02(uint32_t v) { return as_h2(__builtin_amdgcn_perm(0x64646464u, v, 0x04020400u)); }
+__device__ __forceinline__ h2 pair13(uint32_t v) { return as_h2(__builtin_amdgcn_perm(0x64646464u, v, 0x04030401u)); }
+
+// B operand of block j, K slice kappa (columns 16h + 8 kappa .. of the block,
+// in pi order) for this lane. Q4_K folds the 6-bit sub-block scale in:
+// (1024 + q) sc - 1024 sc = q sc exactly (one fused rounding of an integer
+// below 2^11), with sc2 = (sc, sc) and nsc2 = (-1024 sc, -1024 sc).
+template <unsigned T>
+__device__ __forceinline__ h8 b_operand(const WStage<T> &w, int j, int kappa, int h, h2 sc2, h2 nsc2)
+{
+    uint32_t v[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        if constexpr (T == Q4_K) {
+            const uint32_t word = w.q[j >> 1][2 * kappa + i];
+            const uint32_t nib = ((j & 1) ? word >> 4 : word) & 0x0F0F0F0Fu;
+            v[2 * i] = as_u32(__builtin_elementwise_fma(pair02(nib), sc2, nsc2));
+            v[2 * i + 1] = as_u32(__builtin_elementwise_fma(pair13(nib), sc2, nsc2));
+        } else if constexpr (T == Q4_0) {
+            const uint32_t nib = (w.q[j][2 * kappa + i] >> (4 * h)) & 0x0F0F0F0Fu;
+            const h2 off = {(_Float16)1032, (_Float16)1032};   // 1024 + 8
+            v[2 * i] = as_u32(pair02(nib) - off);
+            v[2 * i + 1] = as_u32(pair13(nib) - off);
+        } else {
+            const uint32_t u = w.q[j][2 * kappa + i] ^ 0x80808080u;   // q + 128 per byte
+            const h2 off = {(_Float16)1152, (_Float16)1152};          // 1024 + 128
+            v[2 * i] = as_u32(pair02(u) - off);
+            v[2 * i + 1] = as_u32(pair13(u) - off);
+        }
+    }
+    (void)sc2;
+    (void)nsc2;
+    (void)h;
+    return __builtin_bit_cast(h8, (u32x4){v[0], v[1], v[2], v[3]});
+}
+
+template <unsigned T>
+__global__ __launch_bounds__(256) void prefill_f16(const uint8_t *__restrict__ w, Pieces p, float *__restrict__ y,
+    int rows, int cols, int batch)
+{
+    __shared__ __align__(16) Staging S;
+    constexpr bool sums = T == Q4_K;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tiles = (rows + kTileRows - 1) / kTileRows;
+    const int tile_raw = kRowTiles * blockIdx.x + wave;
+    const int tile = tile_raw < tiles ? tile_raw : tiles - 1;
+    const int m0 = kTokens * blockIdx.y, n = batch - m0;   // tokens left (> 0)
+    const int R = rows - kTileRows * tile < kTileRows ? rows - kTileRows * tile : kTileRows;
+    Lane L;
+    L.tile = w + (size_t)kTileRows * tile * tiled_row_bytes<T>(cols);
+    L.R = R;
+    L.r = (lane & 31) < R ? (lane & 31) : R - 1;
+    L.h = lane >> 5;
+    L.slot = lane & 31;
+    L.groups = (cols + kGroupCols - 1) / kGroupCols;
+    L.blocks = cols / 32;
+    const int groups = L.groups;
+    auto clampg = [&](int g) { return g < groups ? g : groups - 1; };
+
+    XFetch xf;
+    fetch_x(xf, p, cols, m0, 0, sums);
+    WStage<T> st[2];
+    load_weights<T>(st[0], L, 0);
+    store_x(S, 0, xf, sums);
+    fetch_x(xf, p, cols, m0, clampg(1), sums);
+    load_weights<T>(st[1], L, clampg(1));
+    __syncthreads();
+
+    // A operand of token row lane % 32: columns 16h + 8 kappa of block j.
+    const int a_off = kPitch * (lane & 31) + 32 * L.h;
+    f32x16 acc = {};
+    for (int g = 0; g < groups; ++g) {
+        const uint8_t *xh = S.x[g & 1][0], *xl = S.x[g & 1][1];
+        if constexpr (T == Q4_K) {
+            f32x16 C = {};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t own = st[0].sl[j >> 1];
+                const float scf = (float)((own >> (12 * (j & 1))) & 63u);
+                const h2 sc2 = {(_Float16)scf, (_Float16)scf};
+                const h2 nsc2 = {(_Float16)(-1024.f * scf), (_Float16)(-1024.f * scf)};
+#pragma unroll
+                for (int kappa = 0; kappa < 2; ++kappa) {
+                    const h8 b = b_operand<T>(st[0], j, kappa, L.h, sc2, nsc2);
+                    const int off = a_off + 64 * j + 16 * kappa;
+                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xh + off), b, C, 0, 0, 0);
+                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xl + off), b, C, 0, 0, 0);
+                }
+            }
+            float d, dmin;
+            group_scales<T>(st[0], d, dmin);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[r] += d * C[r];
+            // Minimums: acc -= dmin * sum_j m_j * (sum of x s over block j), on
+            // an fp32 MFMA accumulating into acc (lane l: A = the sum over
+            // block 2s + l/32 of token l % 32, B = -dmin * m of that block for
+            // row l % 32).
+            const float4 ys = *(const float4 *)(S.bs[g & 1] + 4 * lane);
+            const float ya[4] = {ys.x, ys.y, ys.z, ys.w};
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                const float m = (float)((st[0].sl[s2] >> (12 * L.h + 6)) & 63u);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ya[s2], -dmin * m, acc, 0, 0, 0);
+            }
+        } else {
+            const int nb = group_blocks(L, g);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (j >= nb) break;
+                f32x16 C = {};
+#pragma unroll
+                for (int kappa = 0; kappa < 2; ++kappa) {
+                    const h8 b = b_operand<T>(st[0], j, kappa, L.h, (h2){}, (h2){});
+                    const int off = a_off + 64 * j + 16 * kappa;
+                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xh + off), b, C, 0, 0, 0);
+                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xl + off), b, C, 0, 0, 0);
+                }
+                const float dj = f16_to_f32(st[0].d[j]);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[r] += dj * C[r];
+            }
+        }
+        // Group g + 1's pieces into the other buffer (its readers passed the
+        // last barrier), fetch group g + 2, rotate the weight ring.
+        store_x(S, (g + 1) & 1, xf, sums);
+        fetch_x(xf, p, cols, m0, clampg(g + 2), sums);
+        st[0] = st[1];
+        load_weights<T>(st[1], L, clampg(g + 2));
+        __syncthreads();
+    }
+
+    if (tile_raw >= tiles || (lane & 31) >= R) return;
+    const int row = kTileRows * tile + (lane & 31);
+    // D register r of lane l is token 8 (r / 4) + 4 (l / 32) + r % 4.
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int t = 8 * (r >> 2) + 4 * L.h + (r & 3);
+        if (t < n) y[(size_t)(m0 + t) * rows + row] = acc[r] * p.inv[m0 + t];
+    }
+}
+
+}  // namespace
+
+bool prefill_f16_supported(unsigned type) { return type == Q4_K || type == Q8_0 || type == Q4_0; }
+
+size_t prefill_f16_workspace(int cols, int batch)
+{
+    const size_t np = ((size_t)batch + kTokens - 1) / kTokens * kTokens;
+    return np * ((size_t)4 * cols + (size_t)(cols / 32) * 4 + 4);
+}
+
+hipError_t launch_prefill_f16(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,
+    int batch, void *workspace, hipStream_t s)
+{
+    const int np = (batch + kTokens - 1) / kTokens * kTokens;
+    const Pieces p = pieces_of(workspace, cols, np);
+    hipLaunchKernelGGL(split_x, dim3((unsigned)batch), dim3(256), 0, s, x, cols, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int tiles = (rows + kTileRows - 1) / kTileRows;
+    const dim3 grid((unsigned)((tiles + kRowTiles - 1) / kRowTiles), (unsigned)(np / kTokens));
+    switch (type) {
+    case Q4_K: hipLaunchKernelGGL(prefill_f16<Q4_K>, grid, dim3(256), 0, s, w, p, y, rows, cols, batch); break;
+    case Q8_0: hipLaunchKernelGGL(prefill_f16<Q8_0>, grid, dim3(256), 0, s, w, p, y, rows, cols, batch); break;
+    case Q4_0: hipLaunchKernelGGL(prefill_f16<Q4_0>, grid, dim3(256), 0, s, w, p, y, rows, cols, batch); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace fy

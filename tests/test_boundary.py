@@ -133,18 +133,28 @@ def test_pack_is_the_specified_permutation(kernels, t, rows, cols):
 
 def test_prefill_dispatch_and_workspace():
     """Batch 1 needs no workspace; batches of 2..8 need the activation digits
-    of a padded token count, batches above 8 those of the prefill GEMM
-    (tokens rounded up to 32); dense types need none (nothing is
-    launched)."""
+    of a padded token count; batches above 8 go to the prefill GEMM: fp16
+    activation pieces for Q4_K/Q8_0/Q4_0 (per token, rounded up to 32
+    tokens: two fp16 planes, the 32-column block sums and the scale), int8
+    digits for Q6_K; dense types need none (nothing is launched)."""
     kern = Kernels()
+
+    def pieces(cols, batch):
+        np_ = -(-batch // 32) * 32
+        return np_ * (4 * cols + cols // 32 * 4 + 4)
+
     for t in (Q4_0, Q8_0, Q4_K, Q6_K):
         assert kern.workspace_bytes(t, 4096, 4096, 1) == 0
         assert kern.workspace_bytes(t, 4096, 4096, 8) == 4096 // 32 * 136 * 8
         assert kern.workspace_bytes(t, 4096, 4096, 3) == 4096 // 32 * 136 * 4
-        assert kern.workspace_bytes(t, 4096, 4096, 9) == 4096 // 32 * 136 * 32
-        assert kern.workspace_bytes(t, 4096, 4096, 512) == 4096 // 32 * 136 * 512
-        assert kern.kernel_name(t, 4096, 4096, 512) == "prefill_mfma"
         assert kern.kernel_name(t, 4096, 4096, 8) == "smalln_mfma"
+    for t in (Q4_0, Q8_0, Q4_K):
+        assert kern.workspace_bytes(t, 4096, 4096, 9) == pieces(4096, 9)
+        assert kern.workspace_bytes(t, 4096, 4096, 512) == pieces(4096, 512)
+        assert kern.kernel_name(t, 4096, 4096, 512) == "prefill_f16"
+    assert kern.workspace_bytes(Q6_K, 4096, 4096, 9) == 4096 // 32 * 136 * 32
+    assert kern.workspace_bytes(Q6_K, 4096, 4096, 512) == 4096 // 32 * 136 * 512
+    assert kern.kernel_name(Q6_K, 4096, 4096, 512) == "prefill_mfma"
     for t in (F32, BF16):
         assert kern.workspace_bytes(t, 4096, 4096, 512) == 0
         assert kern.kernel_name(t, 4096, 4096, 512) == "skinny_dense"

@@ -1,4 +1,5 @@
-"""The int8-MFMA prefill GEMM (batches above 8 of Q4_0 / Q8_0 / Q4_K / Q6_K).
+"""The prefill GEMM (batches above 8): fp16 MFMA for Q4_0 / Q8_0 / Q4_K,
+int8 MFMA for Q6_K.
 
 - prefill shapes of the 8B-class projections at batch 128..512: sampled
   tokens (both tile edges included) against the double-precision oracle
@@ -7,8 +8,9 @@
 - batch and row tails (batch 9, 127..129, 257; 200 rows = one full and one
   partial weight tile) with canaries on both sides of the output;
 - through the kernel library's C ABI: the GEMM (workspace given) against the
-  same request run through the small-N path (same integer block sums,
-  different fp32 summation order), and the workspace size it asks for.
+  same request run through the small-N path (int8 activation digits; both
+  represent x to about 2^-22 and differ in fp32 summation order), and the
+  workspace size it asks for.
 """
 import numpy as np
 import pytest
@@ -72,8 +74,12 @@ def test_prefill_matches_tiled_path(hip, type_id):
     w = synth.weights(type_id, rows, cols, 77 + type_id)
     x = synth.activations(batch, cols, 78 + type_id)
     need = kern.workspace_bytes(type_id, rows, cols, batch)
-    assert need == cols // 32 * 136 * 64          # batch rounded up to 32 tokens
-    assert kern.kernel_name(type_id, rows, cols, batch) == "prefill_mfma"
+    if type_id == Q6_K:
+        assert need == cols // 32 * 136 * 64      # digits, batch rounded up to 32 tokens
+        assert kern.kernel_name(type_id, rows, cols, batch) == "prefill_mfma"
+    else:
+        assert need == 64 * (4 * cols + cols // 32 * 4 + 4)   # fp16 pieces of 64 tokens
+        assert kern.kernel_name(type_id, rows, cols, batch) == "prefill_f16"
     wdev, xdev = rt.malloc(storage_bytes(type_id, rows, cols)), rt.malloc(x.nbytes)
     ydev, work = rt.malloc(4 * rows * batch), rt.malloc(need)
     try:

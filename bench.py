@@ -17,10 +17,10 @@ weight matrix; weights and activations are resident in HBM before timing.
 - cpu_baseline: the reference CPU provider (built from the reference sources
   into oracle/_ref) on the same weights, on this host's cores; else this
   repository's C port of the scalar path.
-- prefill: the same matrix times 512 tokens through the int8-MFMA prefill
-  GEMM (one call = activation quantization + GEMM): model TFLOP/s, and the
-  int8 operations the matrix cores issue (four digit rows per token) against
-  the dense int8 MFMA peak.
+- prefill: the same matrix times 512 tokens through the fp16-MFMA prefill
+  GEMM (one call = activation split + GEMM): model TFLOP/s, and the fp16
+  flops the matrix cores issue (two activation pieces per token) against the
+  dense fp16 MFMA peak.
 
 Prints one JSON line.
 """
@@ -46,10 +46,11 @@ from fyodor_amd.hip import Kernels, Runtime  # noqa: E402
 METRIC = "Q4_K matvec effective HBM GB/s (% of peak), 14336x4096, N=1 and N=8"
 ROWS, COLS = 14336, 4096
 PEAK_HBM_GBS = 8000.0
-PEAK_INT8_TOPS = 5000.0        # dense int8 MFMA, MI355X
-# The prefill GEMM multiplies each token's three signed activation digits
-# (plus a zero fourth slot) by the int8 weights: four MFMA rows per token.
-PREFILL_MFMA_ROWS_PER_TOKEN = 4
+PEAK_FP16_TFLOPS = 2500.0      # dense fp16 MFMA, MI355X
+# The prefill GEMM multiplies each token's activations as two fp16 pieces
+# (hi + lo) by exact fp16 integer weights: two MFMA products per useful
+# multiply-add.
+PREFILL_PIECES = 2
 PREFILL_TOKENS = 512
 MALL_BYTES = 256 * 1024 * 1024
 
@@ -212,12 +213,12 @@ def prefill(rt, kern, stream, weights, host_w, steps: int) -> dict:
     for p in (x_dev, y_dev, work):
         rt.free(p)
     useful = 2.0 * ROWS * COLS * m / (ms * 1e-3) / 1e12          # model TFLOP/s
-    issued = useful * PREFILL_MFMA_ROWS_PER_TOKEN                  # int8 TOP/s on the matrix cores
+    issued = useful * PREFILL_PIECES                               # fp16 TFLOP/s on the matrix cores
     return {
         "workload": f"Q4_K {ROWS}x{COLS} x {m} tokens (prefill GEMM)", "kernel": kern.kernel_name(Q4_K, ROWS, COLS, m),
         "ms_per_call": round(ms, 5), "calls": steps, "useful_tflops": round(useful, 2),
-        "roofline": {"bound": "mfma", "achieved": round(issued, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
-                     "frac": round(issued / PEAK_INT8_TOPS, 4)},
+        "roofline": {"bound": "mfma", "achieved": round(issued, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(issued / PEAK_FP16_TFLOPS, 4)},
     }
 
 

@@ -245,26 +245,42 @@ __global__ __launch_bounds__(256) void prefill_f16(const uint8_t *__restrict__ w
     // A operand of token row lane % 32: columns 16h + 8 kappa of block j.
     const int a_off = kPitch * (lane & 31) + 32 * L.h;
     f32x16 acc = {};
-    for (int g = 0; g < groups; ++g) {
+    // One 256-column group: compute it from `cur`, then refill `cur` with
+    // group g + 2. The loop below alternates the two stages, so no register
+    // copy (which would wait for the loads just issued) rotates the ring.
+    auto step = [&](WStage<T> &cur, int g) {
         const uint8_t *xh = S.x[g & 1][0], *xl = S.x[g & 1][1];
+        // A operands (hi and lo of K slices 0 and 1) of block j, read one
+        // block ahead so the LDS latency hides behind the previous MFMAs.
+        auto read_a = [&](h8 (&a)[4], int j) {
+#pragma unroll
+            for (int kappa = 0; kappa < 2; ++kappa) {
+                const int off = a_off + 64 * j + 16 * kappa;
+                a[2 * kappa] = *(const h8 *)(xh + off);
+                a[2 * kappa + 1] = *(const h8 *)(xl + off);
+            }
+        };
+        h8 A[2][4];
+        read_a(A[0], 0);
         if constexpr (T == Q4_K) {
             f32x16 C = {};
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const uint32_t own = st[0].sl[j >> 1];
+                if (j + 1 < 8) read_a(A[(j + 1) & 1], j + 1);
+                __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of this block's MFMAs
+                const uint32_t own = cur.sl[j >> 1];
                 const float scf = (float)((own >> (12 * (j & 1))) & 63u);
                 const h2 sc2 = {(_Float16)scf, (_Float16)scf};
                 const h2 nsc2 = {(_Float16)(-1024.f * scf), (_Float16)(-1024.f * scf)};
 #pragma unroll
                 for (int kappa = 0; kappa < 2; ++kappa) {
-                    const h8 b = b_operand<T>(st[0], j, kappa, L.h, sc2, nsc2);
-                    const int off = a_off + 64 * j + 16 * kappa;
-                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xh + off), b, C, 0, 0, 0);
-                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xl + off), b, C, 0, 0, 0);
+                    const h8 b = b_operand<T>(cur, j, kappa, L.h, sc2, nsc2);
+                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[j & 1][2 * kappa], b, C, 0, 0, 0);
+                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[j & 1][2 * kappa + 1], b, C, 0, 0, 0);
                 }
             }
             float d, dmin;
-            group_scales<T>(st[0], d, dmin);
+            group_scales<T>(cur, d, dmin);
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[r] += d * C[r];
             // Minimums: acc -= dmin * sum_j m_j * (sum of x s over block j), on
@@ -275,7 +291,7 @@ __global__ __launch_bounds__(256) void prefill_f16(const uint8_t *__restrict__ w
             const float ya[4] = {ys.x, ys.y, ys.z, ys.w};
 #pragma unroll
             for (int s2 = 0; s2 < 4; ++s2) {
-                const float m = (float)((st[0].sl[s2] >> (12 * L.h + 6)) & 63u);
+                const float m = (float)((cur.sl[s2] >> (12 * L.h + 6)) & 63u);
                 acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ya[s2], -dmin * m, acc, 0, 0, 0);
             }
         } else {
@@ -283,26 +299,30 @@ __global__ __launch_bounds__(256) void prefill_f16(const uint8_t *__restrict__ w
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 if (j >= nb) break;
+                if (j + 1 < 8) read_a(A[(j + 1) & 1], j + 1);
+                __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of this block's MFMAs
                 f32x16 C = {};
 #pragma unroll
                 for (int kappa = 0; kappa < 2; ++kappa) {
-                    const h8 b = b_operand<T>(st[0], j, kappa, L.h, (h2){}, (h2){});
-                    const int off = a_off + 64 * j + 16 * kappa;
-                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xh + off), b, C, 0, 0, 0);
-                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xl + off), b, C, 0, 0, 0);
+                    const h8 b = b_operand<T>(cur, j, kappa, L.h, (h2){}, (h2){});
+                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[j & 1][2 * kappa], b, C, 0, 0, 0);
+                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[j & 1][2 * kappa + 1], b, C, 0, 0, 0);
                 }
-                const float dj = f16_to_f32(st[0].d[j]);
+                const float dj = f16_to_f32(cur.d[j]);
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[r] += dj * C[r];
             }
         }
         // Group g + 1's pieces into the other buffer (its readers passed the
-        // last barrier), fetch group g + 2, rotate the weight ring.
+        // last barrier), fetch group g + 2 and its weights.
         store_x(S, (g + 1) & 1, xf, sums);
         fetch_x(xf, p, cols, m0, clampg(g + 2), sums);
-        st[0] = st[1];
-        load_weights<T>(st[1], L, clampg(g + 2));
+        load_weights<T>(cur, L, clampg(g + 2));
         __syncthreads();
+    };
+    for (int g = 0; g < groups; g += 2) {
+        step(st[0], g);
+        if (g + 1 < groups) step(st[1], g + 1);
     }
 
     if (tile_raw >= tiles || (lane & 31) >= R) return;

@@ -21,13 +21,18 @@
 // order: within every 8 columns, position s holds column pi(s),
 // pi = 0 2 1 3 4 6 5 7.
 //
-// Work split. A workgroup of four wavefronts owns 128 weight rows (one 32-row
-// tile per wavefront) and 32 tokens (the A rows of the MFMA). K advances one
-// 256-column group per step: both pieces of the 32 tokens (32 KiB) are staged
-// in LDS, double-buffered with one barrier per step, rows padded to 528 bytes
-// so the sixteen lanes of one LDS cycle hit distinct banks. The weights of
-// each wavefront's tile stream through the two-stage register ring of
-// blockdot.h.
+// Work split. A workgroup of eight wavefronts (four for Q8_0/Q4_0 and for
+// grids too small to fill the chip twice) owns 256 weight rows (one 32-row
+// tile per wavefront) and 32 tokens (the A rows of the MFMA); the token block
+// varies fastest over the grid, so workgroups that share a row group run
+// side by side on one XCD and its L2. K advances one 256-column group per
+// step. Both pieces of the 32 tokens (32 KiB) go straight from global memory
+// into LDS (global_load_lds, no staging registers), double-buffered: step g
+// issues group g + 1's copies and weights, computes group g, waits for its
+// own copies and meets the others at one barrier. LDS rows are paired: the
+// 1 KiB copy of tokens 2q and 2q + 1 interleaves them per 16 bytes at a
+// 1056-byte pair pitch, so the sixteen lanes of one LDS cycle (tokens r..r+15,
+// same columns) hit distinct banks with immediate offsets only.
 #include "blockdot.h"
 #include "kernels.h"
 
@@ -38,15 +43,18 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
-constexpr int kRowTiles = 4;      // 32-row tiles per workgroup (one per wavefront)
 constexpr int kTokens = 32;       // tokens per workgroup = MFMA A rows
-constexpr int kPitch = 528;       // LDS bytes per token row of one piece (256 fp16 + 16)
-constexpr int kPieceBytes = kTokens * kPitch;
+constexpr int kPairPitch = 1056;  // LDS bytes per token pair of one piece (1 KiB + 32)
+constexpr int kPieceBytes = kTokens / 2 * kPairPitch;
+constexpr int kSumBytes = 1024;   // Q4_K block sums of one group: 32 tokens x 2 halves x 16 bytes
+constexpr int kBufBytes = 2 * kPieceBytes + kSumBytes;
 
 // ---- activation pieces ---------------------------------------------------
 // Workspace for np tokens (np a multiple of 32): hi[np][cols], lo[np][cols]
-// (fp16, permuted as above), bsum[np][cols / 32] (fp32 sum of x s over each
-// 32-column block) and inv[np] (1 / s, or NaN).
+// (fp16, permuted as above), bsum[np][cols / 256][2][4] (fp32 sum of x s over
+// 32-column block 2s + h of each 256-column group at [h][s], the operand
+// order of the minimum-term MFMA; written when cols % 256 == 0) and inv[np]
+// (1 / s, or NaN).
 struct Pieces {
     _Float16 *hi, *lo;
     float *bsum, *inv;
@@ -115,56 +123,58 @@ __global__ __launch_bounds__(256) void split_x(const float *__restrict__ x, int 
         // Four consecutive chunks form a 32-column block (256 is a multiple of 4).
         s += __shfl_xor(s, 1, 64);
         s += __shfl_xor(s, 2, 64);
-        if ((c & 3) == 0) out.bsum[(size_t)t * (cols / 32) + c / 4] = s;
+        if ((c & 3) == 0 && cols % 256 == 0) {
+            const int b = c / 4, j = b & 7;
+            out.bsum[(size_t)t * (cols / 32) + (b & ~7) + 4 * (j & 1) + (j >> 1)] = s;
+        }
     }
 }
 
 // ---- GEMM ---------------------------------------------------------------
-struct Staging {
-    uint8_t x[2][2][kPieceBytes];   // [buffer][piece][token row]
-    float bs[2][256];               // Q4_K block sums: [4 l + s] = block 2s + l/32 of token l % 32
-};
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
-// This thread's share of one group: eight 16-byte chunks and one block sum.
-struct XFetch {
-    u32x4 d[8];
-    float s;
-};
-
-// Chunk c = tid + 256 k: piece c / 1024, token (c / 32) % 32, columns
-// 8 (c % 32) .. of the group. The last group of a Q8_0/Q4_0 row may be short:
-// columns past the row are clamped (their blocks are skipped).
-__device__ __forceinline__ void fetch_x(XFetch &f, const Pieces &p, int cols, int m0, int g, bool sums)
+// Workgroup barrier without the memory-model fences of __syncthreads (whose
+// release side waits for every outstanding vector load): the kernel orders
+// its LDS traffic itself (explicit s_waitcnt before each barrier); the empty
+// asm statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void barrier()
 {
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const int c = tid + 256 * k;
-        const _Float16 *plane = (c >> 10) ? p.lo : p.hi;
-        const int tok = (c >> 5) & 31;
-        int col = 256 * g + 8 * (c & 31);
-        col = col < cols ? col : cols - 8;
-        f.d[k] = *(const u32x4 *)(plane + (size_t)(m0 + tok) * cols + col);
-    }
-    if (sums) {
-        const int blocks = cols / 32;
-        const int j = tid >> 5, tok = tid & 31;
-        const int b = 8 * g + j < blocks ? 8 * g + j : blocks - 1;
-        f.s = p.bsum[(size_t)(m0 + tok) * blocks + b];
-    }
+    asm volatile("" : : : "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" : : : "memory");
 }
 
-__device__ __forceinline__ void store_x(Staging &S, int buf, const XFetch &f, bool sums)
+// 16 bytes per lane from global memory straight into LDS: lane l's bytes land
+// at dst + 16 l (dst uniform over the wavefront).
+__device__ __forceinline__ void lds_copy16(const void *src, lds_u8 *dst)
 {
-    const int tid = threadIdx.x;
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+}
+
+// Copies of group g into LDS buffer `buf` issued by this wavefront (one of RT):
+// token pairs (16 / RT) wave .. (16 / RT) wave + 16 / RT - 1 of both pieces (lane l: token 2q + (l & 1),
+// 16-byte chunk l >> 1 of the group's row, to byte 16 l of the pair), and for
+// Q4_K (wavefront 0) the 32 tokens' block sums (lane l: token l % 32, half
+// l / 32). Columns past a short last Q8_0/Q4_0 group are clamped (those
+// blocks are skipped).
+template <int RT>
+__device__ __forceinline__ void copy_group(lds_u8 *__restrict__ buf, const Pieces &p, int cols, int m0, int g, bool sums)
+{
+    constexpr int kPairs = 16 / RT;   // token pairs per wavefront
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int col = 256 * g + 8 * (lane >> 1);
+    col = col < cols ? col : cols - 8;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const int c = tid + 256 * k;
-        *(u32x4 *)(S.x[buf][c >> 10] + kPitch * ((c >> 5) & 31) + 16 * (c & 31)) = f.d[k];
-    }
-    if (sums) {
-        const int j = tid >> 5, tok = tid & 31;
-        S.bs[buf][4 * (32 * (j & 1) + tok) + (j >> 1)] = f.s;
+    for (int piece = 0; piece < 2; ++piece)
+#pragma unroll
+        for (int k = 0; k < kPairs; ++k) {
+            const int q = kPairs * wave + k;
+            const _Float16 *src = (piece ? p.lo : p.hi) + (size_t)(m0 + 2 * q + (lane & 1)) * cols + col;
+            lds_copy16(src, buf + piece * kPieceBytes + q * kPairPitch);
+        }
+    if (sums && wave == 0) {
+        const float *src = p.bsum + ((size_t)(m0 + (lane & 31)) * (cols / 256) + g) * 8 + 4 * (lane >> 5);
+        lds_copy16(src, buf + 2 * kPieceBytes);
     }
 }
 
@@ -210,17 +220,97 @@ __device__ __forceinline__ h8 b_operand(const WStage<T> &w, int j, int kappa, in
     return __builtin_bit_cast(h8, (u32x4){v[0], v[1], v[2], v[3]});
 }
 
-template <unsigned T>
-__global__ __launch_bounds__(256) void prefill_f16(const uint8_t *__restrict__ w, Pieces p, float *__restrict__ y,
-    int rows, int cols, int batch)
+// Step g of prefill_f16: copy group g + 1 into the other buffer (its readers
+// passed the last barrier), compute group g from `cur` (loaded two steps
+// earlier), refill `cur` with group g + 2, wait for this wavefront's copies,
+// barrier. Copies and loads are unconditional (clamped to the last group): a
+// branch would leave a path with another count of loads in flight. The two
+// buffers come in as restrict pointers, which lets the compiler see that this
+// step's LDS reads do not depend on the copies it issues.
+template <unsigned T, int RT>
+__device__ __forceinline__ void group_step(WStage<T> &cur, f32x16 &acc, lds_u8 *__restrict__ buf,
+    lds_u8 *__restrict__ nbuf, const Pieces &p, const Lane &L, int a_off, int cols, int m0, int g, int groups)
 {
-    __shared__ __align__(16) Staging S;
     constexpr bool sums = T == Q4_K;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int kWeightLoads = T == Q4_K ? 5 : 16;
+    constexpr int kWaitCopies = (kWeightLoads & 15) | ((kWeightLoads >> 4) << 14) | (7 << 4) | (15 << 8);
+    const int lane = threadIdx.x & 63;
+    copy_group<RT>(nbuf, p, cols, m0, g + 1 < groups ? g + 1 : g, sums);
+    const lds_u8 *xh = buf + a_off, *xl = xh + kPieceBytes;
+    if constexpr (T == Q4_K) {
+        f32x16 C = {};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t own = cur.sl[j >> 1];
+            const float scf = (float)((own >> (12 * (j & 1))) & 63u);
+            const h2 sc2 = {(_Float16)scf, (_Float16)scf};
+            const h2 nsc2 = {(_Float16)(-1024.f * scf), (_Float16)(-1024.f * scf)};
+#pragma unroll
+            for (int kappa = 0; kappa < 2; ++kappa) {
+                const h8 b = b_operand<T>(cur, j, kappa, L.h, sc2, nsc2);
+                const int off = 128 * j + 32 * kappa;
+                C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xh + off), b, C, 0, 0, 0);
+                C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xl + off), b, C, 0, 0, 0);
+            }
+        }
+        float d, dmin;
+        group_scales<T>(cur, d, dmin);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] += d * C[r];
+        // Minimums: acc -= dmin * sum_j m_j * (sum of x s over block j), on
+        // an fp32 MFMA accumulating into acc (lane l: A = the sum over
+        // block 2s + l/32 of token l % 32, B = -dmin * m of that block for
+        // row l % 32).
+        const float4 ys = *(const float4 *)(buf + 2 * kPieceBytes + 16 * lane);
+        const float ya[4] = {ys.x, ys.y, ys.z, ys.w};
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+            const float m = (float)((cur.sl[s2] >> (12 * L.h + 6)) & 63u);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ya[s2], -dmin * m, acc, 0, 0, 0);
+        }
+    } else {
+        const int nb = group_blocks(L, g);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (j >= nb) break;
+            f32x16 C = {};
+#pragma unroll
+            for (int kappa = 0; kappa < 2; ++kappa) {
+                const h8 b = b_operand<T>(cur, j, kappa, L.h, (h2){}, (h2){});
+                const int off = 128 * j + 32 * kappa;
+                C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xh + off), b, C, 0, 0, 0);
+                C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xl + off), b, C, 0, 0, 0);
+            }
+            const float dj = f16_to_f32(cur.d[j]);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[r] += dj * C[r];
+        }
+    }
+    load_weights<T>(cur, L, g + 2 < groups ? g + 2 : groups - 1);
+    // This wavefront's copies are complete; then every wavefront's are,
+    // past the barrier.
+    __builtin_amdgcn_s_waitcnt(kWaitCopies);
+    barrier();
+}
+
+// RT wavefronts (32-row tiles) per workgroup: 8 (two workgroups per CU, four
+// wavefronts per SIMD, at most 128 VGPRs) for Q4_K when the grid fills the
+// chip, else 4 (twice the workgroups).
+template <unsigned T, int RT>
+__global__ __launch_bounds__(64 * RT) __attribute__((amdgpu_waves_per_eu(RT / 2, RT / 2))) void prefill_f16(const uint8_t *__restrict__ w, Pieces p, float *__restrict__ y,
+    int rows, int cols, int batch, int token_blocks)
+{
+    __shared__ __align__(16) uint8_t smem0[kBufBytes], smem1[kBufBytes];
+    lds_u8 *const B0 = (lds_u8 *)smem0, *const B1 = (lds_u8 *)smem1;
+    constexpr bool sums = T == Q4_K;
+    // The wavefront index is uniform: keeping it scalar keeps the tile base
+    // and the copy addresses in SGPRs.
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tiles = (rows + kTileRows - 1) / kTileRows;
-    const int tile_raw = kRowTiles * blockIdx.x + wave;
+    const int by = blockIdx.x % token_blocks, bx = blockIdx.x / token_blocks;
+    const int tile_raw = RT * bx + wave;
     const int tile = tile_raw < tiles ? tile_raw : tiles - 1;
-    const int m0 = kTokens * blockIdx.y, n = batch - m0;   // tokens left (> 0)
+    const int m0 = kTokens * by, n = batch - m0;   // tokens left (> 0)
     const int R = rows - kTileRows * tile < kTileRows ? rows - kTileRows * tile : kTileRows;
     Lane L;
     L.tile = w + (size_t)kTileRows * tile * tiled_row_bytes<T>(cols);
@@ -231,98 +321,30 @@ __global__ __launch_bounds__(256) void prefill_f16(const uint8_t *__restrict__ w
     L.groups = (cols + kGroupCols - 1) / kGroupCols;
     L.blocks = cols / 32;
     const int groups = L.groups;
-    auto clampg = [&](int g) { return g < groups ? g : groups - 1; };
 
-    XFetch xf;
-    fetch_x(xf, p, cols, m0, 0, sums);
+    // Vector memory instructions of one load_weights call: the wait before
+    // each barrier leaves exactly these (the next-but-one group's weights) in
+    // flight and so covers every copy issued before them.
+    constexpr int kWeightLoads = T == Q4_K ? 5 : 16;
+    // s_waitcnt immediate: vmcnt = kWeightLoads (bits 3:0 and 15:14), expcnt
+    // and lgkmcnt at their maxima (no wait).
+    constexpr int kWaitCopies = (kWeightLoads & 15) | ((kWeightLoads >> 4) << 14) | (7 << 4) | (15 << 8);
+    static_assert(kWeightLoads < 64, "vmcnt field");
+
     WStage<T> st[2];
+    copy_group<RT>(B0, p, cols, m0, 0, sums);
     load_weights<T>(st[0], L, 0);
-    store_x(S, 0, xf, sums);
-    fetch_x(xf, p, cols, m0, clampg(1), sums);
-    load_weights<T>(st[1], L, clampg(1));
-    __syncthreads();
+    load_weights<T>(st[1], L, groups > 1 ? 1 : 0);
+    __builtin_amdgcn_s_waitcnt(kWaitCopies);
+    barrier();
 
-    // A operand of token row lane % 32: columns 16h + 8 kappa of block j.
-    const int a_off = kPitch * (lane & 31) + 32 * L.h;
+    // A operand of token r = lane % 32: columns 32j + 16h + 8kappa of the
+    // group sit at pair r / 2, byte 32 (4j + 2h + kappa) + 16 (r & 1).
+    const int a_off = kPairPitch * ((lane & 31) >> 1) + 16 * (lane & 1) + 64 * L.h;
     f32x16 acc = {};
-    // One 256-column group: compute it from `cur`, then refill `cur` with
-    // group g + 2. The loop below alternates the two stages, so no register
-    // copy (which would wait for the loads just issued) rotates the ring.
-    auto step = [&](WStage<T> &cur, int g) {
-        const uint8_t *xh = S.x[g & 1][0], *xl = S.x[g & 1][1];
-        // A operands (hi and lo of K slices 0 and 1) of block j, read one
-        // block ahead so the LDS latency hides behind the previous MFMAs.
-        auto read_a = [&](h8 (&a)[4], int j) {
-#pragma unroll
-            for (int kappa = 0; kappa < 2; ++kappa) {
-                const int off = a_off + 64 * j + 16 * kappa;
-                a[2 * kappa] = *(const h8 *)(xh + off);
-                a[2 * kappa + 1] = *(const h8 *)(xl + off);
-            }
-        };
-        h8 A[2][4];
-        read_a(A[0], 0);
-        if constexpr (T == Q4_K) {
-            f32x16 C = {};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                if (j + 1 < 8) read_a(A[(j + 1) & 1], j + 1);
-                __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of this block's MFMAs
-                const uint32_t own = cur.sl[j >> 1];
-                const float scf = (float)((own >> (12 * (j & 1))) & 63u);
-                const h2 sc2 = {(_Float16)scf, (_Float16)scf};
-                const h2 nsc2 = {(_Float16)(-1024.f * scf), (_Float16)(-1024.f * scf)};
-#pragma unroll
-                for (int kappa = 0; kappa < 2; ++kappa) {
-                    const h8 b = b_operand<T>(cur, j, kappa, L.h, sc2, nsc2);
-                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[j & 1][2 * kappa], b, C, 0, 0, 0);
-                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[j & 1][2 * kappa + 1], b, C, 0, 0, 0);
-                }
-            }
-            float d, dmin;
-            group_scales<T>(cur, d, dmin);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[r] += d * C[r];
-            // Minimums: acc -= dmin * sum_j m_j * (sum of x s over block j), on
-            // an fp32 MFMA accumulating into acc (lane l: A = the sum over
-            // block 2s + l/32 of token l % 32, B = -dmin * m of that block for
-            // row l % 32).
-            const float4 ys = *(const float4 *)(S.bs[g & 1] + 4 * lane);
-            const float ya[4] = {ys.x, ys.y, ys.z, ys.w};
-#pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) {
-                const float m = (float)((cur.sl[s2] >> (12 * L.h + 6)) & 63u);
-                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ya[s2], -dmin * m, acc, 0, 0, 0);
-            }
-        } else {
-            const int nb = group_blocks(L, g);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                if (j >= nb) break;
-                if (j + 1 < 8) read_a(A[(j + 1) & 1], j + 1);
-                __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of this block's MFMAs
-                f32x16 C = {};
-#pragma unroll
-                for (int kappa = 0; kappa < 2; ++kappa) {
-                    const h8 b = b_operand<T>(cur, j, kappa, L.h, (h2){}, (h2){});
-                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[j & 1][2 * kappa], b, C, 0, 0, 0);
-                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[j & 1][2 * kappa + 1], b, C, 0, 0, 0);
-                }
-                const float dj = f16_to_f32(cur.d[j]);
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[r] += dj * C[r];
-            }
-        }
-        // Group g + 1's pieces into the other buffer (its readers passed the
-        // last barrier), fetch group g + 2 and its weights.
-        store_x(S, (g + 1) & 1, xf, sums);
-        fetch_x(xf, p, cols, m0, clampg(g + 2), sums);
-        load_weights<T>(cur, L, clampg(g + 2));
-        __syncthreads();
-    };
     for (int g = 0; g < groups; g += 2) {
-        step(st[0], g);
-        if (g + 1 < groups) step(st[1], g + 1);
+        group_step<T, RT>(st[0], acc, B0, B1, p, L, a_off, cols, m0, g, groups);
+        if (g + 1 < groups) group_step<T, RT>(st[1], acc, B1, B0, p, L, a_off, cols, m0, g + 1, groups);
     }
 
     if (tile_raw >= tiles || (lane & 31) >= R) return;
@@ -354,11 +376,18 @@ hipError_t launch_prefill_f16(unsigned type, const uint8_t *w, const float *x, f
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int tiles = (rows + kTileRows - 1) / kTileRows;
-    const dim3 grid((unsigned)((tiles + kRowTiles - 1) / kRowTiles), (unsigned)(np / kTokens));
+    const int tb = np / kTokens;
+    // Q8_0/Q4_0 stages (16 loads) do not fit 128 VGPRs without spilling:
+    // four-wavefront workgroups only.
+    const bool wide = type == Q4_K && (tiles + 7) / 8 * tb >= 256;
+    const dim3 grid((unsigned)((tiles + (wide ? 7 : 3)) / (wide ? 8 : 4) * tb));
     switch (type) {
-    case Q4_K: hipLaunchKernelGGL(prefill_f16<Q4_K>, grid, dim3(256), 0, s, w, p, y, rows, cols, batch); break;
-    case Q8_0: hipLaunchKernelGGL(prefill_f16<Q8_0>, grid, dim3(256), 0, s, w, p, y, rows, cols, batch); break;
-    case Q4_0: hipLaunchKernelGGL(prefill_f16<Q4_0>, grid, dim3(256), 0, s, w, p, y, rows, cols, batch); break;
+    case Q4_K:
+        if (wide) hipLaunchKernelGGL((prefill_f16<Q4_K, 8>), grid, dim3(512), 0, s, w, p, y, rows, cols, batch, tb);
+        else hipLaunchKernelGGL((prefill_f16<Q4_K, 4>), grid, dim3(256), 0, s, w, p, y, rows, cols, batch, tb);
+        break;
+    case Q8_0: hipLaunchKernelGGL((prefill_f16<Q8_0, 4>), grid, dim3(256), 0, s, w, p, y, rows, cols, batch, tb); break;
+    case Q4_0: hipLaunchKernelGGL((prefill_f16<Q4_0, 4>), grid, dim3(256), 0, s, w, p, y, rows, cols, batch, tb); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -126,16 +126,40 @@ __device__ __forceinline__ void load_weights(WStage<T> &w, const Lane &L, int g)
         w.sc = *(const u32x4 *)(b + 192 * R + 16 * r);
         w.d = *(const uint16_t *)(L.tile + (size_t)208 * R * L.groups + 2 * R * g + 2 * r);
     } else {
+        // A full group: Q4_0 units of two blocks (q[0..3]) or Q8_0 blocks, and
+        // the row's eight scales as one 16-byte load (d[0..3], two per word).
+        // A short last group: block by block, one scale per word.
         constexpr int quant = T == Q8_0 ? 32 : 16;
         const int nb = group_blocks(L, g);
         const uint8_t *b = L.tile + (size_t)(quant + 2) * 8 * R * g;
+        if (nb == 8) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int jj = j < nb ? j : nb - 1;
-            w.q[j] = *(const u32x4 *)(b + quant * R * jj + quant * r + (T == Q8_0 ? 16 * h : 0));
-            w.d[j] = *(const uint16_t *)(b + quant * R * nb + 2 * R * jj + 2 * r);
+            for (int j = 0; j < 8; ++j) {
+                if (T == Q4_0 && j >= 4) w.q[j] = (u32x4){};
+                else w.q[j] = T == Q4_0 ? *(const u32x4 *)(b + 32 * R * j + 16 * R * h + 16 * r)
+                                        : *(const u32x4 *)(b + 32 * R * j + 32 * r + 16 * h);
+            }
+            const u32x4 d = *(const u32x4 *)(b + 8 * quant * R + 16 * r);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) w.d[k] = k < 4 ? d[k] : 0u;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int jj = j < nb ? j : nb - 1;
+                w.q[j] = *(const u32x4 *)(b + quant * R * jj + quant * r + (T == Q8_0 ? 16 * h : 0));
+                w.d[j] = *(const uint16_t *)(b + quant * R * nb + 2 * R * jj + 2 * r);
+            }
         }
     }
+}
+
+// fp16 bits of the scale of block j of a Q8_0/Q4_0 stage (FULL: a full group,
+// two scales per word; else one per word).
+template <bool FULL, unsigned T>
+__device__ __forceinline__ uint32_t block_d(const WStage<T> &w, int j)
+{
+    if constexpr (FULL) return (w.d[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+    else return w.d[j];
 }
 
 // sum q * X of one 32-column block from its three digit sums. Q4_K (q <= 15)
@@ -164,7 +188,7 @@ __device__ __forceinline__ float recombine(int d0, int d1, int d2)
 // minimums; 0 otherwise), and which of the group's eight 32-column x groups
 // the lane's A-rows cover. K-quant superblock scales are left to
 // group_scales (backend/core/llm_quant.c:70-142).
-template <unsigned T>
+template <unsigned T, bool FULL = true>
 __device__ __forceinline__ i32x4 block_operand(const WStage<T> &w, int j, int h, float &sc, float &mn, int &xgl)
 {
     mn = 0.f;
@@ -186,14 +210,18 @@ __device__ __forceinline__ i32x4 block_operand(const WStage<T> &w, int j, int h,
         xgl = 4 * (p >> 1) + q;
         return as_i32x4(u);
     } else if constexpr (T == Q8_0) {
-        sc = f16_to_f32(w.d[j]);
+        sc = f16_to_f32(block_d<FULL>(w, j));
         xgl = j;
         return as_i32x4(w.q[j]);
     } else {
+        // Full group: nibble j & 1 of unit j >> 1 (this lane's 16 columns);
+        // short group: nibble h of block j.
         u32x4 u;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) u[k] = bytes_minus((w.q[j][k] >> (4 * h)) & 0x0F0F0F0Fu, 0x08080808u);
-        sc = f16_to_f32(w.d[j]);
+        for (int k = 0; k < 4; ++k)
+            u[k] = bytes_minus(((FULL ? w.q[j >> 1][k] >> (4 * (j & 1)) : w.q[j][k] >> (4 * h))) & 0x0F0F0F0Fu,
+                               0x08080808u);
+        sc = f16_to_f32(block_d<FULL>(w, j));
         xgl = j;
         return as_i32x4(u);
     }

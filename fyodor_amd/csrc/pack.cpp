@@ -51,9 +51,34 @@ void pack_q6k(uint8_t *g, uint8_t *dd, const uint8_t *b, size_t R, size_t r)
     memcpy(dd + 2 * r, b + 208, 2);
 }
 
-// Q8_0 / Q4_0: `b` holds nb consecutive GGUF blocks of the row.
+// Q8_0 / Q4_0: `b` holds nb consecutive GGUF blocks of the row. A full group
+// (nb = 8) stores Q4_0 quants in units of two blocks (byte n of half h of
+// unit p: element 16h + n of block 2p in the low nibble, of block 2p + 1 in
+// the high one) and the row's eight scales together; a short group keeps
+// each block's bytes and the scales block by block.
 void pack_q8q4(uint8_t *g, const uint8_t *b, size_t R, size_t r, size_t nb, size_t quant)
 {
+    if (nb == 8) {
+        for (size_t j = 0; j < 8; ++j) {
+            const uint8_t *blk = b + j * (quant + 2);
+            memcpy(g + 8 * quant * R + 16 * r + 2 * j, blk, 2);
+            if (quant == 32) memcpy(g + 32 * R * j + 32 * r, blk + 2, 32);
+        }
+        if (quant == 16) {
+            // Element e of a Q4_0 block: low nibble of qs[e] (e < 16), else the
+            // high nibble of qs[e - 16].
+            auto nib = [&](size_t j, size_t e) -> uint8_t {
+                const uint8_t *qs = b + j * 18 + 2;
+                return e < 16 ? (qs[e] & 15) : (qs[e - 16] >> 4);
+            };
+            for (size_t p = 0; p < 4; ++p)
+                for (size_t h = 0; h < 2; ++h)
+                    for (size_t n = 0; n < 16; ++n)
+                        g[32 * R * p + 16 * R * h + 16 * r + n] =
+                            (uint8_t)(nib(2 * p, 16 * h + n) | nib(2 * p + 1, 16 * h + n) << 4);
+        }
+        return;
+    }
     for (size_t j = 0; j < nb; ++j) {
         const uint8_t *blk = b + j * (quant + 2);
         memcpy(g + quant * R * j + quant * r, blk + 2, quant);

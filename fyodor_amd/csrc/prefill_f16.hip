@@ -33,6 +33,8 @@
 // 1 KiB copy of tokens 2q and 2q + 1 interleaves them per 16 bytes at a
 // 1056-byte pair pitch, so the sixteen lanes of one LDS cycle (tokens r..r+15,
 // same columns) hit distinct banks with immediate offsets only.
+#include <type_traits>
+
 #include "blockdot.h"
 #include "kernels.h"
 
@@ -191,7 +193,7 @@ __device__ __forceinline__ h2 pair13(uint32_t v) { return as_h2(__builtin_amdgcn
 // in pi order) for this lane. Q4_K folds the 6-bit sub-block scale in:
 // (1024 + q) sc - 1024 sc = q sc exactly (one fused rounding of an integer
 // below 2^11), with sc2 = (sc, sc) and nsc2 = (-1024 sc, -1024 sc).
-template <unsigned T>
+template <unsigned T, bool FULL = true>
 __device__ __forceinline__ h8 b_operand(const WStage<T> &w, int j, int kappa, int h, h2 sc2, h2 nsc2)
 {
     uint32_t v[4];
@@ -203,7 +205,10 @@ __device__ __forceinline__ h8 b_operand(const WStage<T> &w, int j, int kappa, in
             v[2 * i] = as_u32(__builtin_elementwise_fma(pair02(nib), sc2, nsc2));
             v[2 * i + 1] = as_u32(__builtin_elementwise_fma(pair13(nib), sc2, nsc2));
         } else if constexpr (T == Q4_0) {
-            const uint32_t nib = (w.q[j][2 * kappa + i] >> (4 * h)) & 0x0F0F0F0Fu;
+            // Full group: nibble j & 1 of unit j >> 1; short group: nibble h of
+            // block j (formats.h).
+            const uint32_t nib = (FULL ? w.q[j >> 1][2 * kappa + i] >> (4 * (j & 1)) : w.q[j][2 * kappa + i] >> (4 * h)) &
+                                 0x0F0F0F0Fu;
             const h2 off = {(_Float16)1032, (_Float16)1032};   // 1024 + 8
             v[2 * i] = as_u32(pair02(nib) - off);
             v[2 * i + 1] = as_u32(pair13(nib) - off);
@@ -269,22 +274,28 @@ __device__ __forceinline__ void group_step(WStage<T> &cur, f32x16 &acc, lds_u8 *
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ya[s2], -dmin * m, acc, 0, 0, 0);
         }
     } else {
-        const int nb = group_blocks(L, g);
+        // Per-block scales; a short last group has its own layout (formats.h).
+        auto blocks = [&](auto full) {
+            constexpr bool FULL = decltype(full)::value;
+            const int nb = group_blocks(L, g);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if (j >= nb) break;
-            f32x16 C = {};
+            for (int j = 0; j < 8; ++j) {
+                if (j >= nb) break;
+                f32x16 C = {};
 #pragma unroll
-            for (int kappa = 0; kappa < 2; ++kappa) {
-                const h8 b = b_operand<T>(cur, j, kappa, L.h, (h2){}, (h2){});
-                const int off = 128 * j + 32 * kappa;
-                C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xh + off), b, C, 0, 0, 0);
-                C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xl + off), b, C, 0, 0, 0);
+                for (int kappa = 0; kappa < 2; ++kappa) {
+                    const h8 b = b_operand<T, FULL>(cur, j, kappa, L.h, (h2){}, (h2){});
+                    const int off = 128 * j + 32 * kappa;
+                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xh + off), b, C, 0, 0, 0);
+                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xl + off), b, C, 0, 0, 0);
+                }
+                const float dj = f16_to_f32(block_d<FULL>(cur, j));
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[r] += dj * C[r];
             }
-            const float dj = f16_to_f32(cur.d[j]);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[r] += dj * C[r];
-        }
+        };
+        if (group_blocks(L, g) == 8) blocks(std::true_type{});
+        else blocks(std::false_type{});
     }
     load_weights<T>(cur, L, g + 2 < groups ? g + 2 : groups - 1);
     // This wavefront's copies are complete; then every wavefront's are,

@@ -105,7 +105,7 @@ __device__ __forceinline__ void load_stage(Stage<T, NP, G> &st, const Lane &L, i
 // scale groups). The K-quant superblock scales d and dmin multiply the
 // group's sums once: sum_j (d sc_j q - dmin m_j) x = d sum_j sc_j (q.x)_j -
 // dmin sum_j m_j (sum x)_j.
-template <unsigned T, int NP, bool G>
+template <unsigned T, int NP, bool G, bool FULL>
 __device__ __forceinline__ void compute_stage(float (&acc)[(kAcc<T, NP>)], const Stage<T, NP, G> &st, const Lane &L,
     int g, int g0c, const uint8_t *dig, const float2 *meta, int n)
 {
@@ -129,7 +129,7 @@ __device__ __forceinline__ void compute_stage(float (&acc)[(kAcc<T, NP>)], const
         for (int jj = 0; jj < PAIR; ++jj) {
             const int j = j0 + jj;
             int xgl;
-            const i32x4 b = block_operand<T>(st.w, j, h, sc[jj], mn[jj], xgl);
+            const i32x4 b = block_operand<T, FULL>(st.w, j, h, sc[jj], mn[jj], xgl);
             xg[jj] = 8 * (g - g0c) + xgl;
 #pragma unroll
             for (int th = 0; th < kTokenHalves<T, NP>; ++th) {
@@ -280,7 +280,12 @@ __global__ __launch_bounds__(64 * KS) void smalln_mfma(const uint8_t *__restrict
             float part[NA];
 #pragma unroll
             for (int q = 0; q < NA; ++q) part[q] = 0.f;
-            compute_stage<T, NP, G>(part, st[k], L, group_of(i + k), g0c, dig, smeta, n);
+            // A short last Q8_0/Q4_0 group has its own layout (formats.h).
+            const int gk = group_of(i + k);
+            if ((T == Q8_0 || T == Q4_0) && group_blocks(L, gk) < 8)
+                compute_stage<T, NP, G, false>(part, st[k], L, gk, g0c, dig, smeta, n);
+            else
+                compute_stage<T, NP, G, true>(part, st[k], L, gk, g0c, dig, smeta, n);
             load_stage<T, NP, G>(st[k], L, group_of(i + k + RING), g0c, gdig, n);
             const float keep = i + k < ns ? 1.f : 0.f;
 #pragma unroll

@@ -113,10 +113,27 @@ def unpack_reference(dev: np.ndarray, t: int, rows: int, cols: int) -> np.ndarra
                 quant = 32 if t == Q8_0 else 16
                 nb = min(8, cols // 32 - 8 * g)
                 grp = tile[(quant + 2) * 8 * R * g:(quant + 2) * 8 * R * g + (quant + 2) * nb * R]
-                for j in range(nb):
-                    c0 = (quant + 2) * (8 * g + j)
-                    out[t0:t0 + R, c0 + 2:c0 + 2 + quant] = grp[quant * R * j:quant * R * (j + 1)].reshape(R, quant)
-                    out[t0:t0 + R, c0:c0 + 2] = grp[quant * R * nb + 2 * R * j:quant * R * nb + 2 * R * (j + 1)].reshape(R, 2)
+                if nb == 8:
+                    # Full group: the row's eight scales together; Q4_0 quants in
+                    # units of two blocks (low nibble block 2p, high 2p + 1).
+                    dd = grp[8 * quant * R:8 * quant * R + 16 * R].reshape(R, 8, 2)
+                    for j in range(8):
+                        c0 = (quant + 2) * (8 * g + j)
+                        out[t0:t0 + R, c0:c0 + 2] = dd[:, j]
+                        if t == Q8_0:
+                            out[t0:t0 + R, c0 + 2:c0 + 34] = grp[32 * R * j:32 * R * (j + 1)].reshape(R, 32)
+                    if t == Q4_0:
+                        for p in range(4):
+                            u = grp[32 * R * p:32 * R * (p + 1)].reshape(2, R, 16)   # [half][row][n]
+                            for m in range(2):
+                                e = (u >> (4 * m)) & 15                              # element 16h + n of block 2p + m
+                                c0 = 18 * (8 * g + 2 * p + m)
+                                out[t0:t0 + R, c0 + 2:c0 + 18] = e[0] | (e[1] << 4)
+                else:
+                    for j in range(nb):
+                        c0 = (quant + 2) * (8 * g + j)
+                        out[t0:t0 + R, c0 + 2:c0 + 2 + quant] = grp[quant * R * j:quant * R * (j + 1)].reshape(R, quant)
+                        out[t0:t0 + R, c0:c0 + 2] = grp[quant * R * nb + 2 * R * j:quant * R * nb + 2 * R * (j + 1)].reshape(R, 2)
     return out.reshape(-1)
 
 

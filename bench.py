@@ -41,7 +41,7 @@ REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO))
 
 from fyodor_amd import Q4_K, storage_bytes, synth  # noqa: E402
-from fyodor_amd.hip import Kernels, Runtime  # noqa: E402
+from fyodor_amd.hip import Graph, Kernels, Runtime  # noqa: E402
 
 METRIC = "Q4_K matvec effective HBM GB/s (% of peak), 14336x4096, N=1 and N=8"
 ROWS, COLS = 14336, 4096
@@ -72,38 +72,6 @@ def measured_traffic(batch: int):
 
 def algorithmic_bytes(rows: int, cols: int, batch: int) -> int:
     return storage_bytes(Q4_K, rows, cols) + 4 * cols * batch + 4 * rows * batch
-
-
-class Graph:
-    """A captured sequence of launches on one stream (hipGraph)."""
-
-    def __init__(self, rt: Runtime, stream: int, launches):
-        L = rt.lib
-        vp = ctypes.c_void_p
-        L.hipStreamBeginCapture.argtypes = [vp, ctypes.c_int]
-        L.hipStreamEndCapture.argtypes = [vp, ctypes.POINTER(vp)]
-        L.hipGraphInstantiate.argtypes = [ctypes.POINTER(vp), vp, vp, vp, ctypes.c_size_t]
-        L.hipGraphLaunch.argtypes = [vp, vp]
-        L.hipGraphExecDestroy.argtypes = [vp]
-        L.hipGraphDestroy.argtypes = [vp]
-        self.rt, self.stream = rt, stream
-        rt.check(L.hipStreamBeginCapture(stream, 0), "hipStreamBeginCapture")
-        try:
-            for launch in launches:
-                launch()
-        finally:
-            graph = vp()
-            rt.check(L.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
-        self.graph = graph
-        self.exec = vp()
-        rt.check(L.hipGraphInstantiate(ctypes.byref(self.exec), graph, None, None, 0), "hipGraphInstantiate")
-
-    def launch(self):
-        self.rt.check(self.rt.lib.hipGraphLaunch(self.exec, self.stream), "hipGraphLaunch")
-
-    def close(self):
-        self.rt.lib.hipGraphExecDestroy(self.exec)
-        self.rt.lib.hipGraphDestroy(self.graph)
 
 
 def time_steps(rt, kern, stream, weights, x_dev, y_dev, batch, steps, warmup, mode, work, work_bytes):

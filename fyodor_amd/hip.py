@@ -149,3 +149,35 @@ class Kernels:
     def kernel_name(self, type_id: int, rows: int, cols: int, batch: int) -> str:
         name = self.lib.nya_hip_kernel_name(type_id, rows, cols, batch)
         return name.decode() if name else ""
+
+
+class Graph:
+    """A captured sequence of launches on one stream (hipGraph)."""
+
+    def __init__(self, rt: Runtime, stream: int, launches):
+        L = rt.lib
+        vp = ctypes.c_void_p
+        L.hipStreamBeginCapture.argtypes = [vp, ctypes.c_int]
+        L.hipStreamEndCapture.argtypes = [vp, ctypes.POINTER(vp)]
+        L.hipGraphInstantiate.argtypes = [ctypes.POINTER(vp), vp, vp, vp, ctypes.c_size_t]
+        L.hipGraphLaunch.argtypes = [vp, vp]
+        L.hipGraphExecDestroy.argtypes = [vp]
+        L.hipGraphDestroy.argtypes = [vp]
+        self.rt, self.stream = rt, stream
+        rt.check(L.hipStreamBeginCapture(stream, 0), "hipStreamBeginCapture")
+        try:
+            for launch in launches:
+                launch()
+        finally:
+            graph = vp()
+            rt.check(L.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
+        self.graph = graph
+        self.exec = vp()
+        rt.check(L.hipGraphInstantiate(ctypes.byref(self.exec), graph, None, None, 0), "hipGraphInstantiate")
+
+    def launch(self):
+        self.rt.check(self.rt.lib.hipGraphLaunch(self.exec, self.stream), "hipGraphLaunch")
+
+    def close(self):
+        self.rt.lib.hipGraphExecDestroy(self.exec)
+        self.rt.lib.hipGraphDestroy(self.graph)

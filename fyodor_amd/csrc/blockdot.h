@@ -22,12 +22,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kSlotBytes = 32;      // one digit of one token over a 32-column group
 
-// Bytes v < 128 minus c (c <= 64) as signed 8-bit values, four at once.
-__device__ __forceinline__ uint32_t bytes_minus(uint32_t v, uint32_t c4)
-{
-    return ((v | 0x80808080u) - c4) ^ 0x80808080u;
-}
-
 __device__ __forceinline__ i32x4 as_i32x4(u32x4 v) { return __builtin_bit_cast(i32x4, v); }
 
 // ---- activation digits ---------------------------------------------------
@@ -162,10 +156,11 @@ __device__ __forceinline__ uint32_t block_d(const WStage<T> &w, int j)
     else return w.d[j];
 }
 
-// sum q * X of one 32-column block from its three digit sums. Q4_K (q <= 15)
-// and Q4_0 (|q| <= 8): |D2| <= 32 * 15 * 64, so the whole sum fits int32.
-// Q8_0 (|q| <= 128) and Q6_K (|q| <= 32) can reach 2^34: the low two digits
-// (below 2^27) combine in int32, the top one in float.
+// sum q * X of one 32-column block from its three digit sums. Q4_K
+// (q <= 15): |D2| <= 32 * 15 * 64, so the whole sum fits int32. Q8_0, and
+// Q6_K and Q4_0 in their scaled forms (|q| <= 128, see block_operand), can
+// reach 2^34: the low two digits (below 2^27) combine in int32, the top one
+// in float.
 // The int32 form is evaluated as (d2 * 2^8 + d1) * 2^8 + d0, two shift-adds;
 // the empty asm keeps the compiler from re-associating it into two shifts
 // and a three-input add. (It touches no register the MFMA writes: those are
@@ -174,7 +169,7 @@ __device__ __forceinline__ uint32_t block_d(const WStage<T> &w, int j)
 template <unsigned T>
 __device__ __forceinline__ float recombine(int d0, int d1, int d2)
 {
-    if constexpr (T == Q4_K || T == Q4_0) {
+    if constexpr (T == Q4_K) {
         int u = d2 * 256 + d1;
         asm("" : "+v"(u));
         return (float)(u * 256 + d0);
@@ -188,6 +183,11 @@ __device__ __forceinline__ float recombine(int d0, int d1, int d2)
 // minimums; 0 otherwise), and which of the group's eight 32-column x groups
 // the lane's A-rows cover. K-quant superblock scales are left to
 // group_scales (backend/core/llm_quant.c:70-142).
+//
+// The offset weights enter the MFMA scaled so that a byte needs no per-byte
+// subtraction: Q6_K as 4 (q6 - 32) = (q6 << 2) ^ 0x80 (the 6-bit value in
+// bits 2..7, its top bit flipped), Q4_0 as 16 (q - 8) = (q << 4) ^ 0x80; the
+// factor returns through the scale (exactly: a power of two).
 template <unsigned T, bool FULL = true>
 __device__ __forceinline__ i32x4 block_operand(const WStage<T> &w, int j, int h, float &sc, float &mn, int &xgl)
 {
@@ -203,9 +203,11 @@ __device__ __forceinline__ i32x4 block_operand(const WStage<T> &w, int j, int h,
         const int p = j >> 1, m = j & 1, q = 2 * m + h;
         u32x4 u;
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-            u[k] = bytes_minus(((w.ql[p][k] >> (4 * m)) & 0x0F0F0F0Fu) |
-                (((w.qh[p][k] >> (2 * q)) & 0x03030303u) << 4), 0x20202020u);
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t lo = m ? w.ql[p][k] >> 2 : w.ql[p][k] << 2;   // nibble to bits 2..5
+            const uint32_t hi = w.qh[p][k] << (6 - 2 * q);                // two bits to 6..7
+            u[k] = (lo & 0x3C3C3C3Cu) | ((hi & 0xC0C0C0C0u) ^ 0x80808080u);
+        }
         sc = (float)(int8_t)((w.sc[p] >> (8 * q)) & 0xFFu);
         xgl = 4 * (p >> 1) + q;
         return as_i32x4(u);
@@ -215,13 +217,14 @@ __device__ __forceinline__ i32x4 block_operand(const WStage<T> &w, int j, int h,
         return as_i32x4(w.q[j]);
     } else {
         // Full group: nibble j & 1 of unit j >> 1 (this lane's 16 columns);
-        // short group: nibble h of block j.
+        // short group: nibble h of block j. The nibble goes to bits 4..7.
         u32x4 u;
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-            u[k] = bytes_minus(((FULL ? w.q[j >> 1][k] >> (4 * (j & 1)) : w.q[j][k] >> (4 * h))) & 0x0F0F0F0Fu,
-                               0x08080808u);
-        sc = f16_to_f32(block_d<FULL>(w, j));
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t v = FULL ? w.q[j >> 1][k] << (4 - 4 * (j & 1)) : w.q[j][k] << (4 - 4 * h);
+            u[k] = (v & 0xF0F0F0F0u) ^ 0x80808080u;
+        }
+        sc = f16_to_f32(block_d<FULL>(w, j)) * 0.0625f;
         xgl = j;
         return as_i32x4(u);
     }
@@ -237,7 +240,7 @@ __device__ __forceinline__ void group_scales(const WStage<T> &w, float &d, float
         d = f16_to_f32(dd & 0xFFFFu);
         dmin = f16_to_f32(dd >> 16);
     } else if constexpr (T == Q6_K) {
-        d = f16_to_f32(w.d);
+        d = f16_to_f32(w.d) * 0.25f;   // the weights entered as 4 (q6 - 32)
     }
 }
 

@@ -11,7 +11,8 @@
 // float work applies the block scales as the reference decodes them
 // (backend/core/llm_quant.c:70-142): Q4_K (d*sc)*q - dmin*m, Q6_K
 // (d*sc)*(q6-32), Q8_0 d*q, Q4_0 d*(q-8); the Q6_K and Q4_0 offsets are folded
-// into signed 8-bit weights before the MFMA.
+// into signed 8-bit weights before the MFMA (scaled by 4 and 16, which the
+// block scales take back).
 //
 // MFMA mapping (v_mfma_i32_32x32x32_i8). A = activation digits, 32 rows:
 // row 4t + d holds digit d of token t (row 4t + 3 is zero). B = 32 weight
@@ -24,13 +25,15 @@
 // of its own scale group for tokens 0..3 (a second MFMA covers tokens 4..7).
 //
 // Work split. One workgroup per 32-row tile. Its KS wavefronts split the
-// tile's 256-column groups; each streams its groups through a two-stage
-// register ring, all loads of a stage issued one stage ahead (vector loads
-// retire in order, so activations are requested before weights), and the
+// tile's 256-column groups; each streams its groups' weights through a
+// two-stage register ring (a stage's loads issued two groups ahead), and the
 // partial sums meet in LDS at the end. N = 1 quantizes each wavefront's own
 // columns of x into LDS; N >= 2 reads digits written once per call by
-// quantize_x into the workspace. Columns beyond kChunkCols run as further
-// launches that add into y.
+// quantize_x into the workspace, one group ahead: the operand registers of a
+// block are reloaded with the next group's as soon as the block's MFMA has
+// issued (L2 hits need less lead than HBM weights, and one set of operand
+// registers instead of one per stage keeps the wavefront within its register
+// budget). Columns beyond kChunkCols run as further launches that add into y.
 #include "blockdot.h"
 #include "kernels.h"
 
@@ -59,11 +62,9 @@ template <unsigned T, int NP> constexpr int kRing = 2;
 // second one.
 template <unsigned T, int NP> constexpr int kAcc = T == Q6_K ? NP : (NP + 1) / 2;
 
-template <unsigned T, int NP, bool G>
-struct Stage {
-    WStage<T> w;
-    i32x4 a[G ? 8 * kTokenHalves<T, NP> : 1];
-};
+// Activation operands of one group (N >= 2): MFMA j, token half th at
+// 8 th + j.
+template <unsigned T, int NP, bool G> constexpr int kActs = G ? 8 * kTokenHalves<T, NP> : 1;
 
 // Byte offset of the activation operand of MFMA j (token half th) of
 // chunk-local group gl in the digit array. Lanes whose A-row is not live for
@@ -85,33 +86,36 @@ __device__ __forceinline__ int a_offset(const Lane &L, int gl, int j, int th, in
     }
 }
 
+// Activation operands j0 .. j0 + cnt - 1 (every token half) of group g.
 template <unsigned T, int NP, bool G>
-__device__ __forceinline__ void load_stage(Stage<T, NP, G> &st, const Lane &L, int g, int g0c,
-    const uint8_t *__restrict__ dig, int n)
+__device__ __forceinline__ void load_acts(i32x4 (&a)[(kActs<T, NP, G>)], const Lane &L, int g, int g0c, int j0,
+    int cnt, const uint8_t *__restrict__ dig, int n)
 {
     if constexpr (G) {
         const int nb = (T == Q8_0 || T == Q4_0) ? group_blocks(L, g) : 8;
 #pragma unroll
         for (int th = 0; th < kTokenHalves<T, NP>; ++th)
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                st.a[8 * th + j] = *(const i32x4 *)(dig + a_offset<T, NP>(L, g - g0c, j, th, n, nb));
+            for (int j = j0; j < j0 + cnt; ++j)
+                a[8 * th + j] = *(const i32x4 *)(dig + a_offset<T, NP>(L, g - g0c, j, th, n, nb));
     }
-    load_weights<T>(st.w, L, g);
 }
 
 // The block dot products of one stage (group g) into acc. Q4_K/Q8_0/Q4_0:
 // acc[k] belongs to token 2k + h; Q6_K: acc[t] to token t (this lane half's
 // scale groups). The K-quant superblock scales d and dmin multiply the
 // group's sums once: sum_j (d sc_j q - dmin m_j) x = d sum_j sc_j (q.x)_j -
-// dmin sum_j m_j (sum x)_j.
+// dmin sum_j m_j (sum x)_j. N >= 2: a holds group g's activation operands;
+// each is reloaded with group gn's as soon as its MFMA has issued, so one set
+// of operand registers serves the whole ring.
 template <unsigned T, int NP, bool G, bool FULL>
-__device__ __forceinline__ void compute_stage(float (&acc)[(kAcc<T, NP>)], const Stage<T, NP, G> &st, const Lane &L,
-    int g, int g0c, const uint8_t *dig, const float2 *meta, int n)
+__device__ __forceinline__ void compute_stage(float (&acc)[(kAcc<T, NP>)], const WStage<T> &w,
+    i32x4 (&acts)[(kActs<T, NP, G>)], const Lane &L, int g, int gn, int g0c, const uint8_t *dig, const float2 *meta,
+    int n)
 {
     constexpr int NA = kAcc<T, NP>;
     const int h = L.h;
-    const int nb = (T == Q8_0 || T == Q4_0) ? group_blocks(L, g) : 8;
+    const int nb = (T == Q8_0 || T == Q4_0) && !FULL ? group_blocks(L, g) : 8;
     float sum_s[NA], sum_m[NA];
 #pragma unroll
     for (int k = 0; k < NA; ++k) sum_s[k] = sum_m[k] = 0.f;
@@ -121,7 +125,12 @@ __device__ __forceinline__ void compute_stage(float (&acc)[(kAcc<T, NP>)], const
     constexpr int PAIR = kTokenHalves<T, NP> == 1 ? 2 : 1;
 #pragma unroll
     for (int j0 = 0; j0 < 8; j0 += PAIR) {
-        if ((T == Q8_0 || T == Q4_0) && j0 >= nb) break;
+        // A short last Q8_0/Q4_0 group skips its missing blocks (their
+        // operands are still reloaded for the next group).
+        if ((T == Q8_0 || T == Q4_0) && !FULL && j0 >= nb) {
+            load_acts<T, NP, G>(acts, L, gn, g0c, j0, PAIR, dig, n);
+            continue;
+        }
         i32x16 D[PAIR][kTokenHalves<T, NP>];
         float sc[PAIR], mn[PAIR];   // per-block multipliers of q.x and of sum x
         int xg[PAIR];
@@ -129,16 +138,17 @@ __device__ __forceinline__ void compute_stage(float (&acc)[(kAcc<T, NP>)], const
         for (int jj = 0; jj < PAIR; ++jj) {
             const int j = j0 + jj;
             int xgl;
-            const i32x4 b = block_operand<T, FULL>(st.w, j, h, sc[jj], mn[jj], xgl);
+            const i32x4 b = block_operand<T, FULL>(w, j, h, sc[jj], mn[jj], xgl);
             xg[jj] = 8 * (g - g0c) + xgl;
 #pragma unroll
             for (int th = 0; th < kTokenHalves<T, NP>; ++th) {
                 i32x4 a;
-                if constexpr (G) a = st.a[8 * th + j];
+                if constexpr (G) a = acts[8 * th + j];
                 else a = *(const i32x4 *)(dig + a_offset<T, NP>(L, g - g0c, j, th, n, nb));
                 D[jj][th] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, (i32x16){}, 0, 0, 0);
             }
         }
+        load_acts<T, NP, G>(acts, L, gn, g0c, j0, PAIR, dig, n);
 #pragma unroll
         for (int jj = 0; jj < PAIR; ++jj) {
             // A short last Q8_0/Q4_0 group drops its padding block.
@@ -165,7 +175,7 @@ __device__ __forceinline__ void compute_stage(float (&acc)[(kAcc<T, NP>)], const
     }
     if constexpr (T == Q4_K || T == Q6_K) {
         float d, dmin;
-        group_scales<T>(st.w, d, dmin);
+        group_scales<T>(w, d, dmin);
 #pragma unroll
         for (int k = 0; k < NA; ++k) acc[k] += T == Q4_K ? d * sum_s[k] - dmin * sum_m[k] : d * sum_s[k];
     }
@@ -175,7 +185,7 @@ __device__ __forceinline__ void compute_stage(float (&acc)[(kAcc<T, NP>)], const
 // column chunk). N = 1 (G false): x is this chunk's columns of the single
 // token; otherwise dig/meta hold the chunk's digits for np = NP slots.
 template <unsigned T, int NP, int KS, bool G>
-__global__ __launch_bounds__(64 * KS) void smalln_mfma(const uint8_t *__restrict__ w, const float *__restrict__ x,
+__global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) void smalln_mfma(const uint8_t *__restrict__ w, const float *__restrict__ x,
     const uint8_t *__restrict__ gdig, const float2 *__restrict__ gmeta, float *__restrict__ y, int rows, int cols,
     int g0c, int ngc, int n, int accumulate)
 {
@@ -229,11 +239,14 @@ __global__ __launch_bounds__(64 * KS) void smalln_mfma(const uint8_t *__restrict
         }
     }
     asm volatile("" ::: "memory");
-    // 2. The first RING weight stages.
+    // 2. The first group's activation operands (N >= 2), then the first RING
+    //    weight stages.
     constexpr int RING = kRing<T, NP>;
-    Stage<T, NP, G> st[RING];
+    i32x4 acts[kActs<T, NP, G>];
+    load_acts<T, NP, G>(acts, L, group_of(0), g0c, 0, 8, gdig, n);
+    WStage<T> st[RING];
 #pragma unroll
-    for (int k = 0; k < RING; ++k) load_stage<T, NP, G>(st[k], L, group_of(k), g0c, gdig, n);
+    for (int k = 0; k < RING; ++k) load_weights<T>(st[k], L, group_of(k));
     // 3. Activations into LDS (waits for them only).
     if constexpr (!G) {
 #pragma unroll
@@ -281,12 +294,12 @@ __global__ __launch_bounds__(64 * KS) void smalln_mfma(const uint8_t *__restrict
 #pragma unroll
             for (int q = 0; q < NA; ++q) part[q] = 0.f;
             // A short last Q8_0/Q4_0 group has its own layout (formats.h).
-            const int gk = group_of(i + k);
+            const int gk = group_of(i + k), gn = group_of(i + k + 1);
             if ((T == Q8_0 || T == Q4_0) && group_blocks(L, gk) < 8)
-                compute_stage<T, NP, G, false>(part, st[k], L, gk, g0c, dig, smeta, n);
+                compute_stage<T, NP, G, false>(part, st[k], acts, L, gk, gn, g0c, dig, smeta, n);
             else
-                compute_stage<T, NP, G, true>(part, st[k], L, gk, g0c, dig, smeta, n);
-            load_stage<T, NP, G>(st[k], L, group_of(i + k + RING), g0c, gdig, n);
+                compute_stage<T, NP, G, true>(part, st[k], acts, L, gk, gn, g0c, dig, smeta, n);
+            load_weights<T>(st[k], L, group_of(i + k + RING));
             const float keep = i + k < ns ? 1.f : 0.f;
 #pragma unroll
             for (int q = 0; q < NA; ++q) acc[q] += keep * part[q];

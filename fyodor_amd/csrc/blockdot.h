@@ -101,23 +101,32 @@ __device__ __forceinline__ int group_blocks(const Lane &L, int g)
     return nb < 8 ? nb : 8;
 }
 
-template <unsigned T>
+// One 16-byte weight load; NT marks it non-temporal (weights are streamed
+// once; the callers choose where that measured faster).
+template <bool NT>
+__device__ __forceinline__ u32x4 load16(const uint8_t *p)
+{
+    if constexpr (NT) return __builtin_nontemporal_load((const u32x4 *)p);
+    else return *(const u32x4 *)p;
+}
+
+template <unsigned T, bool NT = false>
 __device__ __forceinline__ void load_weights(WStage<T> &w, const Lane &L, int g)
 {
     const int R = L.R, r = L.r, h = L.h;
     if constexpr (T == Q4_K) {
         const uint8_t *b = L.tile + (size_t)144 * R * g;
 #pragma unroll
-        for (int p = 0; p < 4; ++p) w.q[p] = *(const u32x4 *)(b + 32 * R * p + 16 * R * h + 16 * r);
-        w.sl = *(const u32x4 *)(b + 128 * R + 16 * r);
+        for (int p = 0; p < 4; ++p) w.q[p] = load16<NT>(b + 32 * R * p + 16 * R * h + 16 * r);
+        w.sl = load16<NT>(b + 128 * R + 16 * r);
     } else if constexpr (T == Q6_K) {
         const uint8_t *b = L.tile + (size_t)208 * R * g;
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-            w.ql[p] = *(const u32x4 *)(b + 48 * R * p + 16 * R * h + 16 * r);
-            w.qh[p] = *(const u32x4 *)(b + 48 * R * p + 32 * R + 16 * r);
+            w.ql[p] = load16<NT>(b + 48 * R * p + 16 * R * h + 16 * r);
+            w.qh[p] = load16<NT>(b + 48 * R * p + 32 * R + 16 * r);
         }
-        w.sc = *(const u32x4 *)(b + 192 * R + 16 * r);
+        w.sc = load16<NT>(b + 192 * R + 16 * r);
         w.d = *(const uint16_t *)(L.tile + (size_t)208 * R * L.groups + 2 * R * g + 2 * r);
     } else {
         // A full group: Q4_0 units of two blocks (q[0..3]) or Q8_0 blocks, and
@@ -130,17 +139,16 @@ __device__ __forceinline__ void load_weights(WStage<T> &w, const Lane &L, int g)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 if (T == Q4_0 && j >= 4) w.q[j] = (u32x4){};
-                else w.q[j] = T == Q4_0 ? *(const u32x4 *)(b + 32 * R * j + 16 * R * h + 16 * r)
-                                        : *(const u32x4 *)(b + 32 * R * j + 32 * r + 16 * h);
+                else w.q[j] = load16<NT>(b + 32 * R * j + 16 * R * h + 16 * r);
             }
-            const u32x4 d = *(const u32x4 *)(b + 8 * quant * R + 16 * r);
+            const u32x4 d = load16<NT>(b + 8 * quant * R + 16 * r);
 #pragma unroll
             for (int k = 0; k < 8; ++k) w.d[k] = k < 4 ? d[k] : 0u;
         } else {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int jj = j < nb ? j : nb - 1;
-                w.q[j] = *(const u32x4 *)(b + quant * R * jj + quant * r + (T == Q8_0 ? 16 * h : 0));
+                w.q[j] = load16<NT>(b + quant * R * jj + (T == Q8_0 ? 16 * R * h : 0) + 16 * r);
                 w.d[j] = *(const uint16_t *)(b + quant * R * nb + 2 * R * jj + 2 * r);
             }
         }

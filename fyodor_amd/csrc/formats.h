@@ -34,9 +34,9 @@
 //        qh at 48R p + 32R + 16r = qh[32h+16 l16..+16); sc at 192R + 16r, word
 //        p byte q = sc[8h + 2q + l16]; d of group g at 208R G + 2R g + 2r
 //        (G groups per row).
-//   Q8_0 (34 R nb): qs of block j at 32R j + 32r; then a full group (nb = 8)
-//        stores row r's eight d at 256R + 16r, a short one d of block j at
-//        32R nb + 2R j + 2r.
+//   Q8_0 (34 R nb): qs[16h..16h+16) of block j at 32R j + 16R h + 16r; then
+//        a full group (nb = 8) stores row r's eight d at 256R + 16r, a short
+//        one d of block j at 32R nb + 2R j + 2r.
 //   Q4_0 (18 R nb): a full group stores units p < 4 (blocks 2p, 2p+1) like
 //        Q4_K: half h at 32R p + 16R h + 16r, byte n = element 16h + n of
 //        block 2p (low nibble) | of block 2p + 1 (high nibble), then row r's

@@ -52,17 +52,19 @@ void pack_q6k(uint8_t *g, uint8_t *dd, const uint8_t *b, size_t R, size_t r)
 }
 
 // Q8_0 / Q4_0: `b` holds nb consecutive GGUF blocks of the row. A full group
-// (nb = 8) stores Q4_0 quants in units of two blocks (byte n of half h of
-// unit p: element 16h + n of block 2p in the low nibble, of block 2p + 1 in
-// the high one) and the row's eight scales together; a short group keeps
-// each block's bytes and the scales block by block.
+// (nb = 8) stores Q8_0 quants block by block in two halves of 16 columns,
+// Q4_0 quants in units of two blocks (byte n of half h of unit p: element
+// 16h + n of block 2p in the low nibble, of block 2p + 1 in the high one),
+// and the row's eight scales together; a short group keeps each block's
+// bytes (Q8_0 again in halves) and the scales block by block.
 void pack_q8q4(uint8_t *g, const uint8_t *b, size_t R, size_t r, size_t nb, size_t quant)
 {
     if (nb == 8) {
         for (size_t j = 0; j < 8; ++j) {
             const uint8_t *blk = b + j * (quant + 2);
             memcpy(g + 8 * quant * R + 16 * r + 2 * j, blk, 2);
-            if (quant == 32) memcpy(g + 32 * R * j + 32 * r, blk + 2, 32);
+            if (quant == 32)
+                for (size_t h = 0; h < 2; ++h) memcpy(g + 32 * R * j + 16 * R * h + 16 * r, blk + 2 + 16 * h, 16);
         }
         if (quant == 16) {
             // Element e of a Q4_0 block: low nibble of qs[e] (e < 16), else the
@@ -81,7 +83,10 @@ void pack_q8q4(uint8_t *g, const uint8_t *b, size_t R, size_t r, size_t nb, size
     }
     for (size_t j = 0; j < nb; ++j) {
         const uint8_t *blk = b + j * (quant + 2);
-        memcpy(g + quant * R * j + quant * r, blk + 2, quant);
+        if (quant == 32)
+            for (size_t h = 0; h < 2; ++h) memcpy(g + 32 * R * j + 16 * R * h + 16 * r, blk + 2 + 16 * h, 16);
+        else
+            memcpy(g + 16 * R * j + 16 * r, blk + 2, 16);
         memcpy(g + quant * R * nb + 2 * R * j + 2 * r, blk, 2);
     }
 }

@@ -120,8 +120,9 @@ def unpack_reference(dev: np.ndarray, t: int, rows: int, cols: int) -> np.ndarra
                     for j in range(8):
                         c0 = (quant + 2) * (8 * g + j)
                         out[t0:t0 + R, c0:c0 + 2] = dd[:, j]
-                        if t == Q8_0:
-                            out[t0:t0 + R, c0 + 2:c0 + 34] = grp[32 * R * j:32 * R * (j + 1)].reshape(R, 32)
+                        if t == Q8_0:   # two halves of 16 columns, each [row][16]
+                            halves = grp[32 * R * j:32 * R * (j + 1)].reshape(2, R, 16)
+                            out[t0:t0 + R, c0 + 2:c0 + 34] = np.concatenate([halves[0], halves[1]], axis=1)
                     if t == Q4_0:
                         for p in range(4):
                             u = grp[32 * R * p:32 * R * (p + 1)].reshape(2, R, 16)   # [half][row][n]
@@ -132,7 +133,10 @@ def unpack_reference(dev: np.ndarray, t: int, rows: int, cols: int) -> np.ndarra
                 else:
                     for j in range(nb):
                         c0 = (quant + 2) * (8 * g + j)
-                        out[t0:t0 + R, c0 + 2:c0 + 2 + quant] = grp[quant * R * j:quant * R * (j + 1)].reshape(R, quant)
+                        q = grp[quant * R * j:quant * R * (j + 1)]
+                        if t == Q8_0:
+                            q = np.concatenate(list(q.reshape(2, R, 16)), axis=1)
+                        out[t0:t0 + R, c0 + 2:c0 + 2 + quant] = q.reshape(R, quant)
                         out[t0:t0 + R, c0:c0 + 2] = grp[quant * R * nb + 2 * R * j:quant * R * nb + 2 * R * (j + 1)].reshape(R, 2)
     return out.reshape(-1)
 

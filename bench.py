@@ -40,7 +40,7 @@ import numpy as np
 REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO))
 
-from fyodor_amd import Q4_K, storage_bytes, synth  # noqa: E402
+from fyodor_amd import Q4_0, Q4_K, Q6_K, Q8_0, TYPE_NAMES, storage_bytes, synth  # noqa: E402
 from fyodor_amd.hip import Graph, Kernels, Runtime  # noqa: E402
 
 METRIC = "Q4_K matvec effective HBM GB/s (% of peak), 14336x4096, N=1 and N=8"
@@ -68,6 +68,12 @@ def measured_traffic(batch: int):
     except OSError:
         pass
     return None
+
+
+def device(rt) -> str:
+    """The device's name, or its compute-unit count when it reports none."""
+    name = rt.device_name()
+    return name if name else f"gfx950, {rt.attribute(63)} CUs"   # 63: hipDeviceAttributeMultiprocessorCount
 
 
 def algorithmic_bytes(rows: int, cols: int, batch: int) -> int:
@@ -190,6 +196,76 @@ def prefill(rt, kern, stream, weights, host_w, steps: int) -> dict:
     }
 
 
+# The measured configurations: decode and small-N shapes (type, rows, cols,
+# batches), then prefill GEMM shapes (type, rows, cols, tokens).
+SWEEP_MATVEC = [
+    (Q4_K, 14336, 4096, (1, 2, 4, 8)), (Q4_K, 4096, 4096, (1, 2, 4, 8)), (Q4_K, 1024, 4096, (1, 8)),
+    (Q8_0, 4096, 4096, (1, 8)), (Q4_0, 4096, 4096, (1, 8)), (Q4_0, 11008, 4096, (1, 8)),
+    (Q4_0, 4096, 11008, (1, 8)), (Q6_K, 4096, 14336, (1, 8)), (Q6_K, 128256, 4096, (1, 8)),
+]
+SWEEP_PREFILL = [(t, rows, 4096, m) for t in (Q4_K, Q8_0) for rows in (4096, 14336) for m in (512, 2048)]
+
+
+def time_case(rt, kern, stream, t, rows, cols, batch, steps):
+    """Milliseconds per call of one matmul shape: graph replay over enough
+    rotating weight copies that every call streams its weights from HBM."""
+    wbytes = storage_bytes(t, rows, cols)
+    copies = max(2, math.ceil(2 * MALL_BYTES / wbytes) + 1)
+    dev = kern.device_weights(synth.weights(t, rows, cols, seed=7), t, rows, cols)
+    weights = []
+    for _ in range(copies):
+        p = rt.malloc(wbytes)
+        rt.upload(p, dev)
+        weights.append(p)
+    x = synth.activations(batch, cols, seed=8)
+    x_dev, y_dev = rt.malloc(x.nbytes), rt.malloc(4 * rows * batch)
+    rt.upload(x_dev, x)
+    need = kern.workspace_bytes(t, rows, cols, batch)
+    work = rt.malloc(max(need, 16))
+
+    def launch(i):
+        return lambda: kern.matmul(weights[i % copies], t, rows, cols, x_dev, y_dev, batch, work, need, stream)
+
+    warm = Graph(rt, stream, [launch(i) for i in range(min(copies, 8))])
+    timed = Graph(rt, stream, [launch(i) for i in range(steps)])
+    warm.launch()
+    rt.sync(stream)
+    start, end = rt.event(), rt.event()
+    rt.record(start, stream)
+    timed.launch()
+    rt.record(end, stream)
+    ms = rt.elapsed_ms(start, end) / steps
+    warm.close()
+    timed.close()
+    for p in weights + [x_dev, y_dev, work]:
+        rt.free(p)
+    return ms
+
+
+def sweep(rt, kern, stream) -> int:
+    """One JSON line per configuration: matvec / small-N effective HBM GB/s,
+    prefill useful TFLOP/s (2 M N K per call)."""
+    for t, rows, cols, batches in SWEEP_MATVEC:
+        wbytes = storage_bytes(t, rows, cols)
+        for batch in batches:
+            steps = max(40, min(2000, int(4e9 / wbytes)))
+            ms = time_case(rt, kern, stream, t, rows, cols, batch, steps)
+            nbytes = wbytes + 4 * cols * batch + 4 * rows * batch
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            print(json.dumps({"sweep": "matvec", "type": TYPE_NAMES[t], "rows": rows, "cols": cols, "batch": batch,
+                              "kernel": kern.kernel_name(t, rows, cols, batch), "calls": steps,
+                              "us_per_call": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                              "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}), flush=True)
+    for t, rows, cols, m in SWEEP_PREFILL:
+        ms = time_case(rt, kern, stream, t, rows, cols, m, 20)
+        useful = 2.0 * rows * cols * m / (ms * 1e-3) / 1e12
+        print(json.dumps({"sweep": "prefill", "type": TYPE_NAMES[t], "rows": rows, "cols": cols, "tokens": m,
+                          "kernel": kern.kernel_name(t, rows, cols, m), "calls": 20,
+                          "us_per_call": round(ms * 1e3, 2), "useful_tflops": round(useful, 1),
+                          "frac_fp16": round(useful * PREFILL_PIECES / PEAK_FP16_TFLOPS, 4)}), flush=True)
+    return 0
+
+
 def calibrate_copy(rt, kern, stream, steps: int) -> int:
     """Copies of a known size: rocprofv3 FETCH_SIZE / WRITE_SIZE per
     dispatch divided into these bytes give the counters' scale factor."""
@@ -216,10 +292,12 @@ def main() -> int:
                     help="run only the plain 256 MiB device copy used to calibrate HBM byte counters")
     ap.add_argument("--prefill-steps", type=int, default=20, help="timed prefill GEMM calls (0: skip)")
     ap.add_argument("--prefill-only", action="store_true", help="run only the prefill GEMM measurement")
+    ap.add_argument("--sweep", action="store_true",
+                    help="time every decode, small-N and prefill configuration instead (one JSON line each)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (rows would be sharded "
-              "across GPUs with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (a matrix's rows would be "
+              "sharded across GPUs with no exchange between them). Run with --gpus 1.", file=sys.stderr)
         return 2
 
     rt = Runtime()
@@ -227,6 +305,8 @@ def main() -> int:
     stream = rt.stream()
     if args.calibrate_copy:
         return calibrate_copy(rt, kern, stream, max(args.steps, 1))
+    if args.sweep:
+        return sweep(rt, kern, stream)
     wbytes = storage_bytes(Q4_K, ROWS, COLS)
     copies = max(2, math.ceil(2 * MALL_BYTES / wbytes) + 2)
     host_w = synth.weights(Q4_K, ROWS, COLS, seed=1234)
@@ -279,7 +359,7 @@ def main() -> int:
         "data": "synthetic (seeded Q4_K blocks, x ~ N(0,1))",
         "config": {"workload": "Q4_K matvec 14336x4096, N=1 (decode)", "rows": ROWS, "cols": COLS,
                    "batch": 1, "weight_copies": copies, "launch": args.launch,
-                   "kernel": kern.kernel_name(Q4_K, ROWS, COLS, 1), "device": rt.device_name()},
+                   "kernel": kern.kernel_name(Q4_K, ROWS, COLS, 1), "device": device(rt)},
         "roofline": {"bound": "hbm", "achieved": round(gbs1, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs1 / PEAK_HBM_GBS, 4), "traffic": measured_traffic(1),
                      "algorithmic_bytes": bytes1},

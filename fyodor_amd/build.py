@@ -19,7 +19,7 @@ ROOT = Path(__file__).resolve().parent
 REPO = ROOT.parent
 LIB = ROOT / "lib"
 CSRC = ROOT / "csrc"
-HIP_SOURCES = ["abi.hip", "dense.hip", "smalln.hip", "prefill.hip", "prefill_f16.hip", "pack.cpp"]
+HIP_SOURCES = ["abi.hip", "dense.hip", "smalln.hip", "matvec.hip", "prefill.hip", "prefill_f16.hip", "pack.cpp"]
 C_SOURCES = ["core/compute.c", "core/vendor.c", "rocm/rocm.c"]
 
 HIPCC_FLAGS = [
@@ -29,7 +29,7 @@ HIPCC_FLAGS = [
 ]
 # Per-source additions. The int8 block-dot kernels read every MFMA result at
 # once in VALU code: results in VGPRs (not AGPRs) save a copy per register.
-EXTRA_FLAGS = {f: ["-mllvm", "-amdgpu-mfma-vgpr-form"] for f in ("smalln.hip", "prefill.hip", "prefill_f16.hip")}
+EXTRA_FLAGS = {f: ["-mllvm", "-amdgpu-mfma-vgpr-form"] for f in ("smalln.hip", "matvec.hip", "prefill.hip", "prefill_f16.hip")}
 C_FLAGS = [
     "-std=c17", "-O2", "-fPIC", "-Wall", "-Wextra", "-Wpedantic", "-Wshadow",
     "-D_POSIX_C_SOURCE=200809L",

@@ -38,6 +38,14 @@ int status(hipError_t e)
     return e == hipSuccess ? 0 : -(int)(e > 0 ? e : 1);
 }
 
+// One token of a quantized matrix: the batch-1 matvec where it exists, else
+// the small-N kernel at batch 1.
+hipError_t launch_token(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols, hipStream_t s)
+{
+    if (matvec_supported(type)) return launch_matvec(type, w, x, y, rows, cols, s);
+    return launch_smalln(type, w, x, y, rows, cols, 1, nullptr, s);
+}
+
 }  // namespace
 
 extern "C" {
@@ -100,14 +108,17 @@ NYA_HIP_EXPORT int nya_hip_matmul(uintptr_t w, unsigned type, size_t rows, size_
         if (dense) {
             const int st = status(launch_dense(type, wp, xp, yp, (int)rows, (int)cols, n, s));
             if (st) return st;
-        } else if (n == 1 || (fits && workspace_bytes >= smalln_workspace((int)cols, n))) {
+        } else if (n == 1) {
+            const int st = status(launch_token(type, wp, xp, yp, (int)rows, (int)cols, s));
+            if (st) return st;
+        } else if ((fits && workspace_bytes >= smalln_workspace((int)cols, n))) {
             const int st = status(launch_smalln(type, wp, xp, yp, (int)rows, (int)cols, n, (void *)workspace, s));
             if (st) return st;
         } else {
             // No room for the activation digits of several tokens: one at a time.
             for (int k = 0; k < n; ++k) {
-                const int st = status(launch_smalln(type, wp, xp + (size_t)k * cols, yp + (size_t)k * rows,
-                                                    (int)rows, (int)cols, 1, nullptr, s));
+                const int st = status(launch_token(type, wp, xp + (size_t)k * cols, yp + (size_t)k * rows,
+                                                   (int)rows, (int)cols, s));
                 if (st) return st;
             }
         }
@@ -121,7 +132,7 @@ NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_
     if (!batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return NULL;
     if (type == F32 || type == F16 || type == BF16) return "skinny_dense";
     if (use_prefill(type, cols, batch)) return prefill_kernel(type);
-    return "smalln_mfma";
+    return batch == 1 && matvec_supported(type) ? matvec_kernel(type) : "smalln_mfma";
 }
 
 NYA_HIP_EXPORT int nya_hip_copy(uintptr_t dst, uintptr_t src, size_t bytes, uintptr_t stream)

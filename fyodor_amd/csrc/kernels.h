@@ -18,6 +18,14 @@ size_t smalln_workspace(int cols, int batch);
 hipError_t launch_smalln(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols, int batch,
     void *workspace, hipStream_t stream);
 
+// Batch-1 matvec with the eight block dots of a 256-column group chained
+// through one MFMA accumulator (matvec.hip); matvec_supported tells which
+// types it takes (the others run on launch_smalln). x must be 16-byte aligned.
+bool matvec_supported(unsigned type);
+const char *matvec_kernel(unsigned type);
+hipError_t launch_matvec(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,
+    hipStream_t stream);
+
 // Activation digits of `batch` tokens x `cols` columns (row stride ldx) in
 // the layout of blockdot.h for np token slots (smalln.hip).
 hipError_t launch_quantize_x(const float *x, int ldx, int cols, int batch, int np, uint8_t *dig, float2 *meta,

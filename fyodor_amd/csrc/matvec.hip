@@ -1,0 +1,325 @@
+// Batch-1 matvec y = W x (token decode) for Q4_K weights in the tiled layout
+// of formats.h, with the block dot products on gfx950 int8 MFMA.
+//
+// Activations. Each 32-column block of x is written as X * 2^(e-21) with
+// 2^(e-1) <= max |x| < 2^e over the block and X integer, |X| <= 2^21, split
+// into signed bytes X = a0 + 2^8 a1 + 2^16 a2. The conversion is one ldexp
+// and one float add per digit: t = x 2^(21-e) + 1.5 * 2^23 (+ 128) rounds to
+// the integer X (X + 128) in the low mantissa bits, whose bytes are the
+// digits. Block dot products sum q * a_d are exact in int32.
+//
+// One token leaves most of an MFMA's 32 A-rows empty. Instead of one MFMA
+// result per 32-column block, the eight blocks of a 256-column group share ONE
+// accumulator: block k's digits sit in A-rows 4k .. 4k+2 (every other A-row of
+// that MFMA reads zeros), and the eight v_mfma_i32_32x32x32_i8 of a group
+// chain through the accumulator. D lane l, register r holds A-row
+// 8(r/4) + 4(l/32) + r%4 for weight row l%32, so after the chain lane half h
+// holds blocks 2m + h (m = 0..3) in registers 4m .. 4m+2 and every epilogue
+// instruction serves two blocks. The A operand of block k is read from LDS at
+// a per-lane address fixed for the whole kernel.
+//
+// Weights. A Q4_K byte holds element l of sub-block 2p (low nibble) and of
+// sub-block 2p + 1 (high nibble). The low nibble enters the MFMA as q & 15;
+// the high one in place as the signed byte (q & 0xF0) ^ 0x80 = 16 q - 128,
+// one instruction per word. Its block sum is 16 G - 128 sum X; the scale data
+// of odd blocks carries the factor 1/16 and the correction 8 sum x, so both
+// halves share one epilogue: (d sc) (G s + c) - dmin m sum x per block, as the
+// reference decodes Q4_K (backend/core/llm_quant.c:70-89: w = d sc q - dmin m).
+// A non-finite x makes its block sum non-finite, and with it every output.
+//
+// The lane halves hold disjoint blocks of the same rows; their sums and those
+// of the KS wavefronts of a tile are added in LDS in a fixed order.
+#include "blockdot.h"
+#include "kernels.h"
+
+namespace fy {
+namespace {
+
+constexpr int kChunkCols = 16384;   // columns per launch (bounds the LDS copy of x)
+constexpr int kMetaBytes = 16;      // per 32-column block: {s, c, sum x, 0}
+
+// A-operand byte offsets within a group's 1 KiB of digits, per lane and
+// block k: lane l supplies A-row l%32 = 4 kl + dd and K-half h = l/32; it is
+// live for block kl's digit dd < 3 and reads slot 3 (zero) of every other
+// block.
+struct AoffTable {
+    int v[64][8];
+};
+constexpr AoffTable make_aoff()
+{
+    AoffTable t{};
+    for (int l = 0; l < 64; ++l)
+        for (int k = 0; k < 8; ++k) {
+            const int kl = (l & 31) >> 2, dd = l & 3;
+            t.v[l][k] = 128 * k + 16 * (l >> 5) + 32 * (kl == k && dd < 3 ? dd : 3);
+        }
+    return t;
+}
+__constant__ AoffTable kAoff = make_aoff();
+
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 8 lanes of an aligned half-row (quad swaps, then the
+// half-row mirror); every lane receives the result.
+__device__ __forceinline__ float sum8(float v)
+{
+    v += dppf<0xB1>(v);
+    v += dppf<0x4E>(v);
+    return v + dppf<0x141>(v);
+}
+
+__device__ __forceinline__ uint32_t fbits(float v) { return __builtin_bit_cast(uint32_t, v); }
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dppu(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t max8u(uint32_t v)
+{
+    v = __builtin_elementwise_max(v, dppu<0xB1>(v));
+    v = __builtin_elementwise_max(v, dppu<0x4E>(v));
+    return __builtin_elementwise_max(v, dppu<0x141>(v));
+}
+
+// Bytes b of four words, packed into one word (word i -> byte i).
+__device__ __forceinline__ uint32_t pack_byte(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, int b)
+{
+    const uint32_t sel = 0x0c0c0000u | (uint32_t)(4 + b) << 8 | (uint32_t)b;
+    return __builtin_amdgcn_perm(w1, w0, sel) | __builtin_amdgcn_perm(w3, w2, sel) << 16;
+}
+
+// One 256-column group gl of x (chunk-local) into LDS: lane l holds columns
+// 4l .. 4l+3, lanes 8b .. 8b+7 block b. Digit slot d of block xg at
+// dig + 128 xg + 32 d (slot 3 zero); meta[xg] = {s', c, sum x, 0} with
+// s' = 2^(e-21) (/16 for odd blocks) and c = 8 sum x for odd blocks, else 0.
+__device__ __forceinline__ void quantize_group(float4 v, int gl, int lane, float odd_scale, float odd_corr,
+    uint8_t *__restrict__ dig, float4 *__restrict__ meta)
+{
+    // Largest magnitude of the block (integer order of |x| bit patterns).
+    const uint32_t ma = fbits(v.x) & 0x7FFFFFFFu, mb = fbits(v.y) & 0x7FFFFFFFu;
+    const uint32_t mc = fbits(v.z) & 0x7FFFFFFFu, md = fbits(v.w) & 0x7FFFFFFFu;
+    const uint32_t mx = max8u(__builtin_elementwise_max(__builtin_elementwise_max(ma, mb), __builtin_elementwise_max(mc, md)));
+    // x 2^sh with sh = 21 - e (capped where 2^sh would not be a float: such
+    // blocks keep fewer digits of values below 2^-106).
+    const int e = __builtin_amdgcn_frexp_expf(__builtin_bit_cast(float, mx));
+    const int sh = 21 - e < 127 ? 21 - e : 127;
+    const float scale = __builtin_bit_cast(float, (uint32_t)(sh + 127) << 23);
+    // |x 2^sh| <= 2^21: x 2^sh + 1.5 * 2^23 stays in [2^23, 2^24), where the
+    // float spacing is 1, so one fma rounds to the integer X and leaves the
+    // bit pattern 0x4B400000 + X. Byte 0 of it is byte 0 of X; byte 1 of the
+    // pattern with 128 more is byte 1 of X + 128; byte 2 of the pattern minus
+    // 0x400000 - 32896 is byte 2 of X + 32896: the signed digits.
+    constexpr float M0 = 12582912.f, M1 = 12583040.f;
+    constexpr uint32_t K2 = 32896u - 0x400000u;
+    const uint32_t a0 = fbits(__builtin_fmaf(v.x, scale, M0)), a1 = fbits(__builtin_fmaf(v.y, scale, M0));
+    const uint32_t a2 = fbits(__builtin_fmaf(v.z, scale, M0)), a3 = fbits(__builtin_fmaf(v.w, scale, M0));
+    const uint32_t w0 = pack_byte(a0, a1, a2, a3, 0);
+    const uint32_t w1 = pack_byte(fbits(__builtin_fmaf(v.x, scale, M1)), fbits(__builtin_fmaf(v.y, scale, M1)),
+                                  fbits(__builtin_fmaf(v.z, scale, M1)), fbits(__builtin_fmaf(v.w, scale, M1)), 1);
+    const uint32_t w2 = pack_byte(a0 + K2, a1 + K2, a2 + K2, a3 + K2, 2);
+    const float sx = sum8((v.x + v.y) + (v.z + v.w));
+    const int xg = 8 * gl + (lane >> 3);
+    uint8_t *dst = dig + 128 * xg + 4 * (lane & 7);
+    *(uint32_t *)dst = w0;
+    *(uint32_t *)(dst + 32) = w1;
+    *(uint32_t *)(dst + 64) = w2;
+    *(uint32_t *)(dst + 96) = 0u;
+    if ((lane & 7) == 0)
+        meta[xg] = make_float4(__builtin_amdgcn_ldexpf(odd_scale, -sh), odd_corr * sx, sx, 0.f);
+}
+
+// One 256-column group: the eight block dots chained through one
+// accumulator, then the scales. a points at this lane's A operand of block 0
+// of the group, mt at its meta of block h; returns this lane half's share of
+// the group's sum for weight row l%32.
+__device__ __forceinline__ float q4k_group(const WStage<Q4_K> &w, const uint8_t *__restrict__ a,
+    const int (&aoff)[8], const float4 *__restrict__ mt, int h)
+{
+    i32x16 D = {};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const u32x4 q = w.q[k >> 1];
+        const i32x4 b = as_i32x4((k & 1) ? (q & 0xF0F0F0F0u) ^ 0x80808080u : q & 0x0F0F0F0Fu);
+        D = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const i32x4 *)(a + aoff[k]), b, D, 0, 0, 0);
+    }
+    // Lane half h: blocks 2m + h. Slice word m packs sc and m of blocks 2m
+    // (bits 0..11) and 2m + 1 (bits 12..23).
+    const int sh = 12 * h;
+    float sum_s = 0.f, sum_m = 0.f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        // Odd blocks reach |sum| = 2^34: the top digit joins in float.
+        const float G = __builtin_fmaf((float)D[4 * m + 2], 65536.f, (float)(D[4 * m + 1] * 256 + D[4 * m]));
+        const float4 md = mt[2 * m];
+        const float sc = (float)__builtin_amdgcn_ubfe(w.sl[m], sh, 6);
+        const float mn = (float)__builtin_amdgcn_ubfe(w.sl[m], sh + 6, 6);
+        sum_s = __builtin_fmaf(sc, __builtin_fmaf(G, md.x, md.y), sum_s);
+        sum_m = __builtin_fmaf(mn, md.z, sum_m);
+    }
+    float d, dmin;
+    group_scales<Q4_K>(w, d, dmin);
+    return d * sum_s - dmin * sum_m;
+}
+
+// Buffer resource over `bytes` bytes at p (raw loads, out-of-range reads
+// return zero).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void *p, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// 16 bytes at voff + soff; NT: non-temporal (weights are streamed once).
+template <bool NT>
+__device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, int voff, int soff)
+{
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, NT ? 2 : 0));
+}
+
+// Weights of group g of the tile (buffer r over the tile): q[p] at
+// 32R p + 16R h + 16 r, slices at 128R + 16 r. The lane part (vq, vs) stays
+// in vector registers, the group part in scalar offsets.
+__device__ __forceinline__ void load_q4k(WStage<Q4_K> &w, __amdgpu_buffer_rsrc_t tile, int R, int g, int vq, int vs)
+{
+    const int base = 144 * R * g;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) w.q[p] = bload16<true>(tile, vq, base + 32 * R * p);
+    w.sl = bload16<true>(tile, vs, base + 128 * R);
+}
+
+// One workgroup per 32-row tile, KS wavefronts splitting its groups
+// [g0c, g0c + ngc) (one column chunk); wavefront w takes chunk groups
+// w, w + KS, ... through a RING-stage register ring.
+template <int KS, int RING>
+__global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) void matvec_q4k(
+    const uint8_t *__restrict__ w, const float *__restrict__ x, float *__restrict__ y, int rows, int cols, int g0c,
+    int ngc, int accumulate)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ float red[KS][64];
+    const int ccols = (g0c + ngc) * kGroupCols < cols ? ngc * kGroupCols : cols - g0c * kGroupCols;
+    const int xgroups = ccols / 32;
+    uint8_t *sdig = lds;                                        // [xgroup][4 slots][32 B]
+    float4 *smeta = (float4 *)(lds + (size_t)128 * xgroups);    // [xgroup]
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int t = blockIdx.x, R = rows - kTileRows * t < kTileRows ? rows - kTileRows * t : kTileRows;
+    const int h = lane >> 5, r = (lane & 31) < R ? (lane & 31) : R - 1;
+    const size_t row_bytes = tiled_row_bytes<Q4_K>(cols);
+    const __amdgpu_buffer_rsrc_t tile = buffer_of(w + (size_t)kTileRows * t * row_bytes, (uint32_t)(R * row_bytes));
+    const __amdgpu_buffer_rsrc_t xb = buffer_of(x, (uint32_t)ccols * 4u);
+    const int vq = 16 * R * h + 16 * r, vs = 16 * r, vx = 16 * lane;
+    // This wave's chunk groups: wave + KS k for k < ns.
+    const int ns = wave < ngc ? (ngc - wave + KS - 1) / KS : 0;
+    auto xload = [&](int gl) { return __builtin_bit_cast(float4, bload16<false>(xb, vx, 1024 * gl)); };
+
+    // 1. The A-operand offset table and x of the first RING groups, then
+    //    the weights (loads complete in order: what the quantization needs
+    //    comes first).
+    int4 ao0 = ((const int4 *)kAoff.v[lane])[0], ao1 = ((const int4 *)kAoff.v[lane])[1];
+    float4 px[RING];
+    // Unconditional: past the chunk the buffer range check returns zeros.
+#pragma unroll
+    for (int k = 0; k < RING; ++k) px[k] = xload(wave + KS * k);
+    asm volatile("" ::: "memory");
+    WStage<Q4_K> st[RING];
+#pragma unroll
+    for (int k = 0; k < RING; ++k) load_q4k(st[k], tile, R, g0c + wave + KS * k, vq, vs);
+    asm volatile("" : "+v"(ao0.x), "+v"(ao0.y), "+v"(ao0.z), "+v"(ao0.w), "+v"(ao1.x), "+v"(ao1.y), "+v"(ao1.z),
+                 "+v"(ao1.w) :: "memory");
+
+    // 2. Digits of this wave's groups into LDS.
+    const bool odd = (lane >> 3) & 1;
+    const float odd_scale = odd ? 0.0625f : 1.f, odd_corr = odd ? 8.f : 0.f;
+#pragma unroll
+    for (int k = 0; k < RING; ++k) {
+        asm volatile("" : "+v"(px[k].x), "+v"(px[k].y), "+v"(px[k].z), "+v"(px[k].w) :: "memory");
+        if (k < ns) quantize_group(px[k], wave + KS * k, lane, odd_scale, odd_corr, sdig, smeta);
+    }
+    for (int k = RING; k < ns; ++k)
+        quantize_group(xload(wave + KS * k), wave + KS * k, lane, odd_scale, odd_corr, sdig, smeta);
+    // Each wave reads back only the groups it wrote.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // 3. A-operand offsets (per lane, fixed for the kernel; loaded with x).
+    int aoff[8] = {ao0.x, ao0.y, ao0.z, ao0.w, ao1.x, ao1.y, ao1.z, ao1.w};
+    const uint8_t *abase = sdig + 1024 * wave;
+    const float4 *mbase = smeta + 8 * wave + h;
+
+    // 4. The ring: stage k holds group i + k; after computing it, it loads
+    //    group i + k + RING. Loads are unconditional (static wait counts):
+    //    past the matrix the buffer range check returns zeros.
+    float acc = 0.f;
+    auto pass = [&](int i) {
+#pragma unroll
+        for (int k = 0; k < RING; ++k) {
+            if (i + k < ns) {
+                const int gl = KS * (i + k);
+                acc += q4k_group(st[k], abase + 1024 * gl, aoff, mbase + 8 * gl, h);
+            }
+            load_q4k(st[k], tile, R, g0c + wave + KS * (i + k + RING), vq, vs);
+        }
+    };
+    pass(0);
+    for (int i = RING; i < ns; i += RING) pass(i);
+
+    // 5. Lane halves and wavefronts, in a fixed order.
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0 || lane >= R) return;
+    float v = red[0][lane] + red[0][lane + 32];
+#pragma unroll
+    for (int q = 1; q < KS; ++q) v += red[q][lane] + red[q][lane + 32];
+    float *dst = y + kTileRows * t + lane;
+    *dst = accumulate ? *dst + v : v;
+}
+
+size_t matvec_lds(int ccols)
+{
+    return (size_t)ccols / 32 * (128 + kMetaBytes);
+}
+
+}  // namespace
+
+bool matvec_supported(unsigned type)
+{
+    return type == Q4_K;
+}
+
+const char *matvec_kernel(unsigned type)
+{
+    return type == Q4_K ? "matvec_q4k" : nullptr;
+}
+
+hipError_t launch_matvec(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,
+    hipStream_t s)
+{
+    if (type != Q4_K) return hipErrorInvalidValue;
+    const int groups = cols / kGroupCols;
+    const unsigned tiles = (unsigned)((rows + kTileRows - 1) / kTileRows);
+    for (int g0 = 0; g0 < groups; g0 += kChunkCols / kGroupCols) {
+        const int ng = groups - g0 < kChunkCols / kGroupCols ? groups - g0 : kChunkCols / kGroupCols;
+        const float *xc = x + (size_t)g0 * kGroupCols;
+        const size_t lds = matvec_lds(ng * kGroupCols);
+        // At least one tile per CU: eight wavefronts per tile, two groups
+        // each in flight. Fewer tiles than CUs: sixteen wavefronts per tile
+        // (measured: 14336 x 4096 7.8 us vs 8.0 us with sixteen; 4096 x 4096
+        // 4.26 us vs 4.34 us with eight).
+        if (tiles >= 256)
+            hipLaunchKernelGGL((matvec_q4k<8, 2>), dim3(tiles), dim3(512), lds, s, w, xc, y, rows, cols, g0, ng, g0 > 0);
+        else
+            hipLaunchKernelGGL((matvec_q4k<16, 1>), dim3(tiles), dim3(1024), lds, s, w, xc, y, rows, cols, g0, ng, g0 > 0);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace fy

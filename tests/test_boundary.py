@@ -66,7 +66,8 @@ def test_queries(kernels):
     assert L.nya_hip_weight_bytes(Q8_0, 0, 32, ctypes.byref(b)) == 1
     assert L.nya_hip_weight_bytes(Q8_0, 1 << 31, 32, ctypes.byref(b)) == 1
     assert L.nya_hip_matmul(0, Q8_0, 3, 32, 16, 16, 1, 0, 0, 0) == 1          # declined, nothing enqueued
-    assert kernels.kernel_name(Q4_K, 14336, 4096, 1) == "smalln_mfma"
+    assert kernels.kernel_name(Q4_K, 14336, 4096, 1) == "matvec_q4k"
+    assert kernels.kernel_name(Q4_K, 14336, 4096, 8) == "smalln_mfma"
 
 
 def unpack_reference(dev: np.ndarray, t: int, rows: int, cols: int) -> np.ndarray:

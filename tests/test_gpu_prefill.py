@@ -98,5 +98,11 @@ def test_prefill_matches_tiled_path(hip, type_id):
     finally:
         for p in (wdev, xdev, ydev, work):
             rt.free(p)
-    assert np.array_equal(short, tiled)
+    # Without a workspace tokens run one at a time: on the batch-1 matvec
+    # where the type has one (its own rounding), else on the same small-N
+    # kernel as the batches of 8 the short workspace gets.
+    if kern.kernel_name(type_id, rows, cols, 1) == "smalln_mfma":
+        assert np.array_equal(short, tiled)
+    else:
+        assert rel_l2(short, tiled) <= 2e-6
     assert rel_l2(pre, tiled) <= 2e-6

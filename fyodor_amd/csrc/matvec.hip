@@ -133,37 +133,54 @@ __device__ __forceinline__ void quantize_group(float4 v, int gl, int lane, float
         meta[xg] = make_float4(__builtin_amdgcn_ldexpf(odd_scale, -sh), odd_corr * sx, sx, 0.f);
 }
 
-// One 256-column group: the eight block dots chained through one
-// accumulator, then the scales. a points at this lane's A operand of block 0
-// of the group, mt at its meta of block h; returns this lane half's share of
-// the group's sum for weight row l%32.
-__device__ __forceinline__ float q4k_group(const WStage<Q4_K> &w, const uint8_t *__restrict__ a,
-    const int (&aoff)[8], const float4 *__restrict__ mt, int h)
+// One 256-column group of VT 32-row tiles: for each tile the eight block dots
+// chained through one accumulator (the tiles' chains interleaved, sharing
+// each A operand), then the scales. a points at this lane's A operand of
+// block 0 of the group, mt at its meta of block h; part[v] receives this lane
+// half's share of the group's sum for row l%32 of tile v.
+template <int VT>
+__device__ __forceinline__ void q4k_group(float (&part)[VT], const WStage<Q4_K> (&w)[VT],
+    const uint8_t *__restrict__ a, const int (&aoff)[8], const float4 *__restrict__ mt, int h)
 {
-    i32x16 D = {};
+    i32x16 D[VT];
+#pragma unroll
+    for (int v = 0; v < VT; ++v) D[v] = (i32x16){};
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        const u32x4 q = w.q[k >> 1];
-        const i32x4 b = as_i32x4((k & 1) ? (q & 0xF0F0F0F0u) ^ 0x80808080u : q & 0x0F0F0F0Fu);
-        D = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const i32x4 *)(a + aoff[k]), b, D, 0, 0, 0);
+        const i32x4 av = *(const i32x4 *)(a + aoff[k]);
+#pragma unroll
+        for (int v = 0; v < VT; ++v) {
+            const u32x4 q = w[v].q[k >> 1];
+            const i32x4 b = as_i32x4((k & 1) ? (q & 0xF0F0F0F0u) ^ 0x80808080u : q & 0x0F0F0F0Fu);
+            D[v] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b, D[v], 0, 0, 0);
+        }
     }
     // Lane half h: blocks 2m + h. Slice word m packs sc and m of blocks 2m
     // (bits 0..11) and 2m + 1 (bits 12..23).
     const int sh = 12 * h;
-    float sum_s = 0.f, sum_m = 0.f;
+    float sum_s[VT], sum_m[VT];
+#pragma unroll
+    for (int v = 0; v < VT; ++v) sum_s[v] = sum_m[v] = 0.f;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-        // Odd blocks reach |sum| = 2^34: the top digit joins in float.
-        const float G = __builtin_fmaf((float)D[4 * m + 2], 65536.f, (float)(D[4 * m + 1] * 256 + D[4 * m]));
         const float4 md = mt[2 * m];
-        const float sc = (float)__builtin_amdgcn_ubfe(w.sl[m], sh, 6);
-        const float mn = (float)__builtin_amdgcn_ubfe(w.sl[m], sh + 6, 6);
-        sum_s = __builtin_fmaf(sc, __builtin_fmaf(G, md.x, md.y), sum_s);
-        sum_m = __builtin_fmaf(mn, md.z, sum_m);
+#pragma unroll
+        for (int v = 0; v < VT; ++v) {
+            // Odd blocks reach |sum| = 2^34: the top digit joins in float.
+            const float G = __builtin_fmaf((float)D[v][4 * m + 2], 65536.f,
+                                           (float)(D[v][4 * m + 1] * 256 + D[v][4 * m]));
+            const float sc = (float)__builtin_amdgcn_ubfe(w[v].sl[m], sh, 6);
+            const float mn = (float)__builtin_amdgcn_ubfe(w[v].sl[m], sh + 6, 6);
+            sum_s[v] = __builtin_fmaf(sc, __builtin_fmaf(G, md.x, md.y), sum_s[v]);
+            sum_m[v] = __builtin_fmaf(mn, md.z, sum_m[v]);
+        }
     }
-    float d, dmin;
-    group_scales<Q4_K>(w, d, dmin);
-    return d * sum_s - dmin * sum_m;
+#pragma unroll
+    for (int v = 0; v < VT; ++v) {
+        float d, dmin;
+        group_scales<Q4_K>(w[v], d, dmin);
+        part[v] = d * sum_s[v] - dmin * sum_m[v];
+    }
 }
 
 // Buffer resource over `bytes` bytes at p (raw loads, out-of-range reads
@@ -262,7 +279,9 @@ __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) vo
         for (int k = 0; k < RING; ++k) {
             if (i + k < ns) {
                 const int gl = KS * (i + k);
-                acc += q4k_group(st[k], abase + 1024 * gl, aoff, mbase + 8 * gl, h);
+                float part[1];
+                q4k_group<1>(part, *(const WStage<Q4_K>(*)[1])&st[k], abase + 1024 * gl, aoff, mbase + 8 * gl, h);
+                acc += part[0];
             }
             load_q4k(st[k], tile, R, g0c + wave + KS * (i + k + RING), vq, vs);
         }
@@ -279,6 +298,155 @@ __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) vo
     for (int q = 1; q < KS; ++q) v += red[q][lane] + red[q][lane + 32];
     float *dst = y + kTileRows * t + lane;
     *dst = accumulate ? *dst + v : v;
+}
+
+// Weights of group g for the lanes of one 32-row virtual tile in the whole
+// matrix's buffer wb. A lane's row sits in packed tile tb (byte offset of its
+// 32-row tile), at r with R rows in that tile: q[p] at tb + R(144 g + 32 p +
+// 16 h) + 16 r, slices at tb + R(144 g + 128) + 16 r. FULL (R = 32 for every
+// lane of the workgroup): the group and field parts are scalar offsets.
+template <bool FULL>
+__device__ __forceinline__ void load_q4k_rows(WStage<Q4_K> &w, __amdgpu_buffer_rsrc_t wb, int vq, int vs, int R, int g)
+{
+    if constexpr (FULL) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) w.q[p] = bload16<true>(wb, vq, 4608 * g + 1024 * p);
+        w.sl = bload16<true>(wb, vs, 4608 * g + 4096);
+    } else {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) w.q[p] = bload16<true>(wb, vq + R * (144 * g + 32 * p), 0);
+        w.sl = bload16<true>(wb, vs + R * (144 * g + 128), 0);
+    }
+}
+
+// Row-balanced batch-1 matvec. One workgroup of sixteen wavefronts per CU
+// takes a contiguous range of rw rows (rw = ceil(rows / workgroups)) as VT
+// virtual 32-row tiles: lane l of virtual tile v owns row base + 32 v + l%32,
+// wherever that row sits in the packed 32-row tiles, so every CU streams the
+// same bytes whatever the row count. Wavefront w takes chunk groups
+// w, w + 16, ... of all VT tiles: it reads and quantizes only those groups of
+// x (no barrier before the dots), and each A operand it reads from LDS serves
+// the VT tiles' interleaved MFMA chains.
+template <int VT, int RING, bool FULL>
+__device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, const float *__restrict__ x,
+    float *__restrict__ y, int rows, int cols, int base, int live, int g0c, int ngc, int accumulate,
+    uint8_t *sdig, float4 *smeta, float (*red)[VT][64])
+{
+    constexpr int KS = 16;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = lane >> 5;
+    const size_t row_bytes = tiled_row_bytes<Q4_K>(cols);
+    const int tiles = (rows + kTileRows - 1) / kTileRows, rlast = rows - kTileRows * (tiles - 1);
+    const __amdgpu_buffer_rsrc_t wb = buffer_of(w, (uint32_t)((size_t)rows * row_bytes));
+    const __amdgpu_buffer_rsrc_t xb = buffer_of(x, (uint32_t)((g0c + ngc) * kGroupCols <= cols ? ngc : 0) * 1024u);
+    // Lane offsets per virtual tile; rows past this workgroup's repeat its
+    // last row (same addresses: no extra traffic).
+    int vq[VT], vs[VT], R[VT];
+#pragma unroll
+    for (int v = 0; v < VT; ++v) {
+        const int row = base + (kTileRows * v + (lane & 31) < live ? kTileRows * v + (lane & 31) : live - 1);
+        const int t = row / kTileRows, r = row - kTileRows * t;
+        R[v] = t == tiles - 1 ? rlast : kTileRows;
+        const int tb = (int)((size_t)kTileRows * t * row_bytes);
+        vq[v] = tb + 16 * R[v] * h + 16 * r;
+        vs[v] = tb + 16 * r;
+    }
+    // This wave's chunk groups: wave + KS k for k < ns.
+    const int ns = wave < ngc ? (ngc - wave + KS - 1) / KS : 0;
+    float acc[VT];
+#pragma unroll
+    for (int v = 0; v < VT; ++v) acc[v] = 0.f;
+    if (ns > 0) {
+        auto gl_of = [&](int k) { return wave + KS * (k < ns ? k : ns - 1); };
+        // 1. The A-operand offset table and x of the first RING groups, then
+        //    the weights (loads complete in order: what the quantization
+        //    needs comes first). Stages past the wave's last group repeat it.
+        int4 ao0 = ((const int4 *)kAoff.v[lane])[0], ao1 = ((const int4 *)kAoff.v[lane])[1];
+        float4 px[RING];
+#pragma unroll
+        for (int k = 0; k < RING; ++k)
+            px[k] = __builtin_bit_cast(float4, bload16<false>(xb, 16 * lane, 1024 * gl_of(k)));
+        asm volatile("" ::: "memory");
+        WStage<Q4_K> st[RING][VT];
+#pragma unroll
+        for (int k = 0; k < RING; ++k)
+#pragma unroll
+            for (int v = 0; v < VT; ++v) load_q4k_rows<FULL>(st[k][v], wb, vq[v], vs[v], R[v], g0c + gl_of(k));
+        asm volatile("" : "+v"(ao0.x), "+v"(ao0.y), "+v"(ao0.z), "+v"(ao0.w), "+v"(ao1.x), "+v"(ao1.y),
+                     "+v"(ao1.z), "+v"(ao1.w) :: "memory");
+
+        // 2. Digits of this wave's groups into LDS.
+        const bool odd = (lane >> 3) & 1;
+        const float odd_scale = odd ? 0.0625f : 1.f, odd_corr = odd ? 8.f : 0.f;
+#pragma unroll
+        for (int k = 0; k < RING; ++k) {
+            asm volatile("" : "+v"(px[k].x), "+v"(px[k].y), "+v"(px[k].z), "+v"(px[k].w) :: "memory");
+            if (k < ns) quantize_group(px[k], gl_of(k), lane, odd_scale, odd_corr, sdig, smeta);
+        }
+        for (int k = RING; k < ns; ++k)
+            quantize_group(__builtin_bit_cast(float4, bload16<false>(xb, 16 * lane, 1024 * gl_of(k))), gl_of(k), lane,
+                           odd_scale, odd_corr, sdig, smeta);
+        // Each wave reads back only the groups it wrote.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        // 3. The ring: stage k holds group i + k of every virtual tile; after
+        //    computing it, it loads group i + k + RING (while there is one).
+        const int aoff[8] = {ao0.x, ao0.y, ao0.z, ao0.w, ao1.x, ao1.y, ao1.z, ao1.w};
+        const uint8_t *abase = sdig + 1024 * wave;
+        const float4 *mbase = smeta + 8 * wave + h;
+        auto pass = [&](int i) {
+#pragma unroll
+            for (int k = 0; k < RING; ++k) {
+                if (i + k < ns) {
+                    const int gl = KS * (i + k);
+                    float part[VT];
+                    q4k_group<VT>(part, st[k], abase + 1024 * gl, aoff, mbase + 8 * gl, h);
+#pragma unroll
+                    for (int v = 0; v < VT; ++v) acc[v] += part[v];
+                    if (i + k + RING < ns)
+#pragma unroll
+                        for (int v = 0; v < VT; ++v)
+                            load_q4k_rows<FULL>(st[k][v], wb, vq[v], vs[v], R[v], g0c + wave + gl + KS * RING);
+                }
+            }
+        };
+        pass(0);
+        for (int i = RING; i < ns; i += RING) pass(i);
+    }
+
+    // 4. Lane halves and wavefronts, in a fixed order.
+#pragma unroll
+    for (int v = 0; v < VT; ++v) red[wave][v][lane] = acc[v];
+    __syncthreads();
+    if (wave >= VT || lane >= 32 || kTileRows * wave + lane >= live) return;
+    const int v = wave;
+    float s = red[0][v][lane] + red[0][v][lane + 32];
+#pragma unroll
+    for (int q = 1; q < KS; ++q) s += red[q][v][lane] + red[q][v][lane + 32];
+    float *dst = y + base + kTileRows * v + lane;
+    *dst = accumulate ? *dst + s : s;
+}
+
+template <int VT, int RING>
+__global__ __launch_bounds__(1024) void matvec_q4k_rows(const uint8_t *__restrict__ w, const float *__restrict__ x,
+    float *__restrict__ y, int rows, int cols, int rw, int g0c, int ngc, int accumulate)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ float red[16][VT][64];
+    const int ccols = (g0c + ngc) * kGroupCols < cols ? ngc * kGroupCols : cols - g0c * kGroupCols;
+    uint8_t *sdig = lds;                                              // [xgroup][4 slots][32 B]
+    float4 *smeta = (float4 *)(lds + (size_t)128 * (ccols / 32));     // [xgroup]
+    const int base = blockIdx.x * rw, live = rows - base < rw ? rows - base : rw;
+    // Every lane of the workgroup in a 32-row tile (only the last tile of the
+    // matrix may be shorter): group and field offsets are scalar.
+    const int tiles = (rows + kTileRows - 1) / kTileRows;
+    if (rows % kTileRows == 0 || base + live <= kTileRows * (tiles - 1))
+        matvec_rows_body<VT, RING, true>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig, smeta, red);
+    else
+        matvec_rows_body<VT, RING, false>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig, smeta, red);
 }
 
 size_t matvec_lds(int ccols)
@@ -298,24 +466,49 @@ const char *matvec_kernel(unsigned type)
     return type == Q4_K ? "matvec_q4k" : nullptr;
 }
 
+// Workgroups of the row-balanced kernel: one per CU (counted once per
+// device).
+int cu_count()
+{
+    static int counts[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!counts[dev]) {
+        int n = 0;
+        counts[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0
+            ? n : 256;
+    }
+    return counts[dev];
+}
+
 hipError_t launch_matvec(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,
     hipStream_t s)
 {
     if (type != Q4_K) return hipErrorInvalidValue;
     const int groups = cols / kGroupCols;
     const unsigned tiles = (unsigned)((rows + kTileRows - 1) / kTileRows);
+    const int cus = cu_count();
+    const int rw = (rows + cus - 1) / cus, wgs = (rows + rw - 1) / rw;
+    const bool balanced = rw <= 2 * kTileRows && (size_t)rows * tiled_row_bytes<Q4_K>(cols) < (1u << 31);
     for (int g0 = 0; g0 < groups; g0 += kChunkCols / kGroupCols) {
         const int ng = groups - g0 < kChunkCols / kGroupCols ? groups - g0 : kChunkCols / kGroupCols;
         const float *xc = x + (size_t)g0 * kGroupCols;
         const size_t lds = matvec_lds(ng * kGroupCols);
-        // At least one tile per CU: eight wavefronts per tile, two groups
-        // each in flight. Fewer tiles than CUs: sixteen wavefronts per tile
-        // (measured: 14336 x 4096 7.8 us vs 8.0 us with sixteen; 4096 x 4096
-        // 4.26 us vs 4.34 us with eight).
-        if (tiles >= 256)
-            hipLaunchKernelGGL((matvec_q4k<8, 2>), dim3(tiles), dim3(512), lds, s, w, xc, y, rows, cols, g0, ng, g0 > 0);
+        // One tile per CU: a second ring stage only where a wavefront has more
+        // than one group (a repeated stage would stream its group twice).
+        if (balanced && rw <= kTileRows && ng > 16)
+            hipLaunchKernelGGL((matvec_q4k_rows<1, 2>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng,
+                               g0 > 0);
+        else if (balanced && rw <= kTileRows)
+            hipLaunchKernelGGL((matvec_q4k_rows<1, 1>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng,
+                               g0 > 0);
+        else if (balanced)
+            hipLaunchKernelGGL((matvec_q4k_rows<2, 1>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng,
+                               g0 > 0);
+        // More than two 32-row tiles per CU: one workgroup per tile, eight
+        // wavefronts, two groups each in flight.
         else
-            hipLaunchKernelGGL((matvec_q4k<16, 1>), dim3(tiles), dim3(1024), lds, s, w, xc, y, rows, cols, g0, ng, g0 > 0);
+            hipLaunchKernelGGL((matvec_q4k<8, 2>), dim3(tiles), dim3(512), lds, s, w, xc, y, rows, cols, g0, ng, g0 > 0);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

@@ -42,7 +42,7 @@ int status(hipError_t e)
 // the small-N kernel at batch 1.
 hipError_t launch_token(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols, hipStream_t s)
 {
-    if (matvec_supported(type)) return launch_matvec(type, w, x, y, rows, cols, s);
+    if (matvec_supported(type, rows, cols)) return launch_matvec(type, w, x, y, rows, cols, s);
     return launch_smalln(type, w, x, y, rows, cols, 1, nullptr, s);
 }
 
@@ -132,7 +132,8 @@ NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_
     if (!batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return NULL;
     if (type == F32 || type == F16 || type == BF16) return "skinny_dense";
     if (use_prefill(type, cols, batch)) return prefill_kernel(type);
-    return batch == 1 && matvec_supported(type) ? matvec_kernel(type) : "smalln_mfma";
+    return batch == 1 && matvec_supported(type, (int)rows, (int)cols) ? matvec_kernel(type, (int)rows, (int)cols)
+                                                                      : "smalln_mfma";
 }
 
 NYA_HIP_EXPORT int nya_hip_copy(uintptr_t dst, uintptr_t src, size_t bytes, uintptr_t stream)

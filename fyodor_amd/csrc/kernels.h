@@ -20,9 +20,10 @@ hipError_t launch_smalln(unsigned type, const uint8_t *w, const float *x, float 
 
 // Batch-1 matvec with the eight block dots of a 256-column group chained
 // through one MFMA accumulator (matvec.hip); matvec_supported tells which
-// types it takes (the others run on launch_smalln). x must be 16-byte aligned.
-bool matvec_supported(unsigned type);
-const char *matvec_kernel(unsigned type);
+// requests it takes (the others run on launch_smalln). x must be 16-byte
+// aligned.
+bool matvec_supported(unsigned type, int rows, int cols);
+const char *matvec_kernel(unsigned type, int rows, int cols);
 hipError_t launch_matvec(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,
     hipStream_t stream);
 

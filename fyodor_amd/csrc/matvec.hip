@@ -1,12 +1,12 @@
-// Batch-1 matvec y = W x (token decode) for Q4_K weights in the tiled layout
-// of formats.h, with the block dot products on gfx950 int8 MFMA.
+// Batch-1 matvec y = W x (token decode) for Q4_K, Q4_0 and Q8_0 weights in the
+// tiled layout of formats.h, with the block dot products on gfx950 int8 MFMA.
 //
 // Activations. Each 32-column block of x is written as X * 2^(e-21) with
 // 2^(e-1) <= max |x| < 2^e over the block and X integer, |X| <= 2^21, split
-// into signed bytes X = a0 + 2^8 a1 + 2^16 a2. The conversion is one ldexp
-// and one float add per digit: t = x 2^(21-e) + 1.5 * 2^23 (+ 128) rounds to
-// the integer X (X + 128) in the low mantissa bits, whose bytes are the
-// digits. Block dot products sum q * a_d are exact in int32.
+// into signed bytes X = a0 + 2^8 a1 + 2^16 a2. The conversion is one fma per
+// digit: x 2^(21-e) + 1.5 * 2^23 (+ 128) rounds to the integer X (X + 128) in
+// the low mantissa bits, whose bytes are the digits. Block dot products
+// sum q * a_d are exact in int32.
 //
 // One token leaves most of an MFMA's 32 A-rows empty. Instead of one MFMA
 // result per 32-column block, the eight blocks of a 256-column group share ONE
@@ -18,17 +18,19 @@
 // instruction serves two blocks. The A operand of block k is read from LDS at
 // a per-lane address fixed for the whole kernel.
 //
-// Weights. A Q4_K byte holds element l of sub-block 2p (low nibble) and of
-// sub-block 2p + 1 (high nibble). The low nibble enters the MFMA as q & 15;
-// the high one in place as the signed byte (q & 0xF0) ^ 0x80 = 16 q - 128,
-// one instruction per word. Its block sum is 16 G - 128 sum X; the scale data
-// of odd blocks carries the factor 1/16 and the correction 8 sum x, so both
-// halves share one epilogue: (d sc) (G s + c) - dmin m sum x per block, as the
-// reference decodes Q4_K (backend/core/llm_quant.c:70-89: w = d sc q - dmin m).
-// A non-finite x makes its block sum non-finite, and with it every output.
+// Weights, as the reference decodes them (backend/core/llm_quant.c:70-142).
+// Q4_K and Q4_0 bytes hold element l of blocks 2p (low nibble) and 2p + 1
+// (high nibble); the low nibble enters the MFMA as q & 15, the high one in
+// place as the signed byte (q & 0xF0) ^ 0x80 = 16 (q - 8), one instruction
+// per word. Each block's activation data carries the factor and the
+// correction that turn those sums into the format's: Q4_K w = (d sc) q - dmin
+// m (odd blocks: 1/16 and + 8 sum x), Q4_0 w = d (q - 8) (even blocks: - 8
+// sum x; odd blocks: 1/16), Q8_0 w = d q (signed bytes as they are). A
+// non-finite x makes its block's sum of x, and with it every output,
+// non-finite.
 //
 // The lane halves hold disjoint blocks of the same rows; their sums and those
-// of the KS wavefronts of a tile are added in LDS in a fixed order.
+// of the wavefronts of a tile are added in LDS in a fixed order.
 #include "blockdot.h"
 #include "kernels.h"
 
@@ -95,9 +97,10 @@ __device__ __forceinline__ uint32_t pack_byte(uint32_t w0, uint32_t w1, uint32_t
 
 // One 256-column group gl of x (chunk-local) into LDS: lane l holds columns
 // 4l .. 4l+3, lanes 8b .. 8b+7 block b. Digit slot d of block xg at
-// dig + 128 xg + 32 d (slot 3 zero); meta[xg] = {s', c, sum x, 0} with
-// s' = 2^(e-21) (/16 for odd blocks) and c = 8 sum x for odd blocks, else 0.
-__device__ __forceinline__ void quantize_group(float4 v, int gl, int lane, float odd_scale, float odd_corr,
+// dig + 128 xg + 32 d (slot 3 zero); meta[xg] = {f 2^(e-21), c sum x,
+// sum x, 0} with this lane's block factor f and correction c (kept as a
+// product with sum x, so a non-finite sum stays non-finite).
+__device__ __forceinline__ void quantize_group(float4 v, int gl, int lane, float fmul, float fcorr,
     uint8_t *__restrict__ dig, float4 *__restrict__ meta)
 {
     // Largest magnitude of the block (integer order of |x| bit patterns).
@@ -130,56 +133,87 @@ __device__ __forceinline__ void quantize_group(float4 v, int gl, int lane, float
     *(uint32_t *)(dst + 64) = w2;
     *(uint32_t *)(dst + 96) = 0u;
     if ((lane & 7) == 0)
-        meta[xg] = make_float4(__builtin_amdgcn_ldexpf(odd_scale, -sh), odd_corr * sx, sx, 0.f);
+        meta[xg] = make_float4(__builtin_amdgcn_ldexpf(fmul, -sh), fcorr * sx, sx, 0.f);
+}
+
+// One 256-column group of one 32-row tile, per format: the quant loads (16
+// bytes each, lane half h holding columns 16h .. 16h+15 of a block) and the
+// 16-byte scale word of the row.
+template <unsigned T> struct MvStage;
+template <> struct MvStage<Q4_K> { u32x4 q[4]; u32x4 sl; };   // sl: 6-bit sc/m, d, dmin
+template <> struct MvStage<Q4_0> { u32x4 q[4]; u32x4 d; };    // d: eight fp16 block scales
+template <> struct MvStage<Q8_0> { u32x4 q[8]; u32x4 d; };
+template <unsigned T> constexpr int kQuantLoads = T == Q8_0 ? 8 : 4;
+template <unsigned T> constexpr int kGroupRowBytes = T == Q8_0 ? 272 : 144;   // per row, per group
+template <unsigned T> constexpr int kScaleOffset = T == Q8_0 ? 256 : 128;    // per row, in the group
+
+// Per-block activation factor and correction for lane l's block b = (l/8)%8
+// of a group (see the header).
+template <unsigned T> __device__ __forceinline__ float block_factor(int lane)
+{
+    return T != Q8_0 && ((lane >> 3) & 1) ? 0.0625f : 1.f;
+}
+template <unsigned T> __device__ __forceinline__ float block_correction(int lane)
+{
+    const bool odd = (lane >> 3) & 1;
+    return T == Q4_K ? (odd ? 8.f : 0.f) : T == Q4_0 ? (odd ? 0.f : -8.f) : 0.f;
+}
+
+// B operand of block k of a stage.
+template <unsigned T>
+__device__ __forceinline__ i32x4 block_b(const MvStage<T> &w, int k)
+{
+    if constexpr (T == Q8_0) {
+        return as_i32x4(w.q[k]);
+    } else {
+        const u32x4 q = w.q[k >> 1];
+        return as_i32x4((k & 1) ? (q & 0xF0F0F0F0u) ^ 0x80808080u : q & 0x0F0F0F0Fu);
+    }
 }
 
 // One 256-column group of VT 32-row tiles: for each tile the eight block dots
-// chained through one accumulator (the tiles' chains interleaved, sharing
-// each A operand), then the scales. a points at this lane's A operand of
-// block 0 of the group, mt at its meta of block h; part[v] receives this lane
-// half's share of the group's sum for row l%32 of tile v.
-template <int VT>
-__device__ __forceinline__ void q4k_group(float (&part)[VT], const WStage<Q4_K> (&w)[VT],
+// chained through one accumulator, then the scales. a points at this lane's
+// A operand of block 0 of the group, mt at its activation data of block h;
+// part[v] receives this lane half's share of the group's sum for row l%32 of
+// tile v.
+template <unsigned T, int VT>
+__device__ __forceinline__ void group_dots(float (&part)[VT], const MvStage<T> (&w)[VT],
     const uint8_t *__restrict__ a, const int (&aoff)[8], const float4 *__restrict__ mt, int h)
 {
-    i32x16 D[VT];
-#pragma unroll
-    for (int v = 0; v < VT; ++v) D[v] = (i32x16){};
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const i32x4 av = *(const i32x4 *)(a + aoff[k]);
-#pragma unroll
-        for (int v = 0; v < VT; ++v) {
-            const u32x4 q = w[v].q[k >> 1];
-            const i32x4 b = as_i32x4((k & 1) ? (q & 0xF0F0F0F0u) ^ 0x80808080u : q & 0x0F0F0F0Fu);
-            D[v] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b, D[v], 0, 0, 0);
-        }
-    }
-    // Lane half h: blocks 2m + h. Slice word m packs sc and m of blocks 2m
-    // (bits 0..11) and 2m + 1 (bits 12..23).
-    const int sh = 12 * h;
-    float sum_s[VT], sum_m[VT];
-#pragma unroll
-    for (int v = 0; v < VT; ++v) sum_s[v] = sum_m[v] = 0.f;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        const float4 md = mt[2 * m];
-#pragma unroll
-        for (int v = 0; v < VT; ++v) {
-            // Odd blocks reach |sum| = 2^34: the top digit joins in float.
-            const float G = __builtin_fmaf((float)D[v][4 * m + 2], 65536.f,
-                                           (float)(D[v][4 * m + 1] * 256 + D[v][4 * m]));
-            const float sc = (float)__builtin_amdgcn_ubfe(w[v].sl[m], sh, 6);
-            const float mn = (float)__builtin_amdgcn_ubfe(w[v].sl[m], sh + 6, 6);
-            sum_s[v] = __builtin_fmaf(sc, __builtin_fmaf(G, md.x, md.y), sum_s[v]);
-            sum_m[v] = __builtin_fmaf(mn, md.z, sum_m[v]);
-        }
-    }
+    // One tile at a time: its chain, then its epilogue (one accumulator live).
 #pragma unroll
     for (int v = 0; v < VT; ++v) {
-        float d, dmin;
-        group_scales<Q4_K>(w[v], d, dmin);
-        part[v] = d * sum_s[v] - dmin * sum_m[v];
+        i32x16 D = {};
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            D = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const i32x4 *)(a + aoff[k]), block_b<T>(w[v], k), D, 0, 0, 0);
+        // Lane half h: blocks 2m + h.
+        float sum_s = 0.f, sum_m = 0.f;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const float4 md = mt[2 * m];
+            // Sums reach 2^34: the top digit joins in float.
+            const float G = __builtin_fmaf((float)D[4 * m + 2], 65536.f, (float)(D[4 * m + 1] * 256 + D[4 * m]));
+            const float t = __builtin_fmaf(G, md.x, md.y);
+            if constexpr (T == Q4_K) {
+                // Slice word m packs sc and m of blocks 2m (bits 0..11) and
+                // 2m + 1 (bits 12..23).
+                const float sc = (float)__builtin_amdgcn_ubfe(w[v].sl[m], 12 * h, 6);
+                const float mn = (float)__builtin_amdgcn_ubfe(w[v].sl[m], 12 * h + 6, 6);
+                sum_s = __builtin_fmaf(sc, t, sum_s);
+                sum_m = __builtin_fmaf(mn, md.z, sum_m);
+            } else {
+                // Scale word m holds the fp16 d of blocks 2m and 2m + 1.
+                sum_s = __builtin_fmaf(f16_to_f32(w[v].d[m] >> (16 * h)), t, sum_s);
+            }
+        }
+        if constexpr (T == Q4_K) {
+            const u32x4 sl = w[v].sl;   // byte 3 of the four words: d, dmin
+            const uint32_t dd = (sl.x >> 24) | ((sl.y >> 24) << 8) | ((sl.z >> 24) << 16) | ((sl.w >> 24) << 24);
+            part[v] = f16_to_f32(dd & 0xFFFFu) * sum_s - f16_to_f32(dd >> 16) * sum_m;
+        } else {
+            part[v] = sum_s;
+        }
     }
 }
 
@@ -200,7 +234,7 @@ __device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, int voff, int
 // Weights of group g of the tile (buffer r over the tile): q[p] at
 // 32R p + 16R h + 16 r, slices at 128R + 16 r. The lane part (vq, vs) stays
 // in vector registers, the group part in scalar offsets.
-__device__ __forceinline__ void load_q4k(WStage<Q4_K> &w, __amdgpu_buffer_rsrc_t tile, int R, int g, int vq, int vs)
+__device__ __forceinline__ void load_q4k(MvStage<Q4_K> &w, __amdgpu_buffer_rsrc_t tile, int R, int g, int vq, int vs)
 {
     const int base = 144 * R * g;
 #pragma unroll
@@ -244,22 +278,21 @@ __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
     for (int k = 0; k < RING; ++k) px[k] = xload(wave + KS * k);
     asm volatile("" ::: "memory");
-    WStage<Q4_K> st[RING];
+    MvStage<Q4_K> st[RING];
 #pragma unroll
     for (int k = 0; k < RING; ++k) load_q4k(st[k], tile, R, g0c + wave + KS * k, vq, vs);
     asm volatile("" : "+v"(ao0.x), "+v"(ao0.y), "+v"(ao0.z), "+v"(ao0.w), "+v"(ao1.x), "+v"(ao1.y), "+v"(ao1.z),
                  "+v"(ao1.w) :: "memory");
 
     // 2. Digits of this wave's groups into LDS.
-    const bool odd = (lane >> 3) & 1;
-    const float odd_scale = odd ? 0.0625f : 1.f, odd_corr = odd ? 8.f : 0.f;
+    const float fmul = block_factor<Q4_K>(lane), fcorr = block_correction<Q4_K>(lane);
 #pragma unroll
     for (int k = 0; k < RING; ++k) {
         asm volatile("" : "+v"(px[k].x), "+v"(px[k].y), "+v"(px[k].z), "+v"(px[k].w) :: "memory");
-        if (k < ns) quantize_group(px[k], wave + KS * k, lane, odd_scale, odd_corr, sdig, smeta);
+        if (k < ns) quantize_group(px[k], wave + KS * k, lane, fmul, fcorr, sdig, smeta);
     }
     for (int k = RING; k < ns; ++k)
-        quantize_group(xload(wave + KS * k), wave + KS * k, lane, odd_scale, odd_corr, sdig, smeta);
+        quantize_group(xload(wave + KS * k), wave + KS * k, lane, fmul, fcorr, sdig, smeta);
     // Each wave reads back only the groups it wrote.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -280,7 +313,7 @@ __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) vo
             if (i + k < ns) {
                 const int gl = KS * (i + k);
                 float part[1];
-                q4k_group<1>(part, *(const WStage<Q4_K>(*)[1])&st[k], abase + 1024 * gl, aoff, mbase + 8 * gl, h);
+                group_dots<Q4_K, 1>(part, *(const MvStage<Q4_K>(*)[1])&st[k], abase + 1024 * gl, aoff, mbase + 8 * gl, h);
                 acc += part[0];
             }
             load_q4k(st[k], tile, R, g0c + wave + KS * (i + k + RING), vq, vs);
@@ -302,21 +335,27 @@ __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) vo
 
 // Weights of group g for the lanes of one 32-row virtual tile in the whole
 // matrix's buffer wb. A lane's row sits in packed tile tb (byte offset of its
-// 32-row tile), at r with R rows in that tile: q[p] at tb + R(144 g + 32 p +
-// 16 h) + 16 r, slices at tb + R(144 g + 128) + 16 r. FULL (R = 32 for every
-// lane of the workgroup): the group and field parts are scalar offsets.
-template <bool FULL>
-__device__ __forceinline__ void load_q4k_rows(WStage<Q4_K> &w, __amdgpu_buffer_rsrc_t wb, int vq, int vs, int R, int g)
+// 32-row tile), at r with R rows in that tile: quant load p at
+// tb + R(GB g + 32 p + 16 h) + 16 r, the scale word at tb + R(GB g + S) + 16 r
+// (GB, S: the format's group bytes and scale offset per row). FULL (R = 32
+// for every lane of the workgroup): the group and field parts are scalar
+// offsets.
+template <unsigned T, bool FULL>
+__device__ __forceinline__ void load_rows(MvStage<T> &w, __amdgpu_buffer_rsrc_t wb, int vq, int vs, int R, int g)
 {
+    constexpr int GB = kGroupRowBytes<T>, S = kScaleOffset<T>;
+    u32x4 sw;
     if constexpr (FULL) {
 #pragma unroll
-        for (int p = 0; p < 4; ++p) w.q[p] = bload16<true>(wb, vq, 4608 * g + 1024 * p);
-        w.sl = bload16<true>(wb, vs, 4608 * g + 4096);
+        for (int p = 0; p < kQuantLoads<T>; ++p) w.q[p] = bload16<true>(wb, vq, kTileRows * GB * g + 1024 * p);
+        sw = bload16<true>(wb, vs, kTileRows * (GB * g + S));
     } else {
 #pragma unroll
-        for (int p = 0; p < 4; ++p) w.q[p] = bload16<true>(wb, vq + R * (144 * g + 32 * p), 0);
-        w.sl = bload16<true>(wb, vs + R * (144 * g + 128), 0);
+        for (int p = 0; p < kQuantLoads<T>; ++p) w.q[p] = bload16<true>(wb, vq + R * (GB * g + 32 * p), 0);
+        sw = bload16<true>(wb, vs + R * (GB * g + S), 0);
     }
+    if constexpr (T == Q4_K) w.sl = sw;
+    else w.d = sw;
 }
 
 // Row-balanced batch-1 matvec. One workgroup of sixteen wavefronts per CU
@@ -327,7 +366,7 @@ __device__ __forceinline__ void load_q4k_rows(WStage<Q4_K> &w, __amdgpu_buffer_r
 // w, w + 16, ... of all VT tiles: it reads and quantizes only those groups of
 // x (no barrier before the dots), and each A operand it reads from LDS serves
 // the VT tiles' interleaved MFMA chains.
-template <int VT, int RING, bool FULL>
+template <unsigned T, int VT, int RING, bool FULL>
 __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, const float *__restrict__ x,
     float *__restrict__ y, int rows, int cols, int base, int live, int g0c, int ngc, int accumulate,
     uint8_t *sdig, float4 *smeta, float (*red)[VT][64])
@@ -336,7 +375,7 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = lane >> 5;
-    const size_t row_bytes = tiled_row_bytes<Q4_K>(cols);
+    const size_t row_bytes = tiled_row_bytes<T>(cols);
     const int tiles = (rows + kTileRows - 1) / kTileRows, rlast = rows - kTileRows * (tiles - 1);
     const __amdgpu_buffer_rsrc_t wb = buffer_of(w, (uint32_t)((size_t)rows * row_bytes));
     const __amdgpu_buffer_rsrc_t xb = buffer_of(x, (uint32_t)((g0c + ngc) * kGroupCols <= cols ? ngc : 0) * 1024u);
@@ -368,25 +407,24 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
         for (int k = 0; k < RING; ++k)
             px[k] = __builtin_bit_cast(float4, bload16<false>(xb, 16 * lane, 1024 * gl_of(k)));
         asm volatile("" ::: "memory");
-        WStage<Q4_K> st[RING][VT];
+        MvStage<T> st[RING][VT];
 #pragma unroll
         for (int k = 0; k < RING; ++k)
 #pragma unroll
-            for (int v = 0; v < VT; ++v) load_q4k_rows<FULL>(st[k][v], wb, vq[v], vs[v], R[v], g0c + gl_of(k));
+            for (int v = 0; v < VT; ++v) load_rows<T, FULL>(st[k][v], wb, vq[v], vs[v], R[v], g0c + gl_of(k));
         asm volatile("" : "+v"(ao0.x), "+v"(ao0.y), "+v"(ao0.z), "+v"(ao0.w), "+v"(ao1.x), "+v"(ao1.y),
                      "+v"(ao1.z), "+v"(ao1.w) :: "memory");
 
         // 2. Digits of this wave's groups into LDS.
-        const bool odd = (lane >> 3) & 1;
-        const float odd_scale = odd ? 0.0625f : 1.f, odd_corr = odd ? 8.f : 0.f;
+        const float fmul = block_factor<T>(lane), fcorr = block_correction<T>(lane);
 #pragma unroll
         for (int k = 0; k < RING; ++k) {
             asm volatile("" : "+v"(px[k].x), "+v"(px[k].y), "+v"(px[k].z), "+v"(px[k].w) :: "memory");
-            if (k < ns) quantize_group(px[k], gl_of(k), lane, odd_scale, odd_corr, sdig, smeta);
+            if (k < ns) quantize_group(px[k], gl_of(k), lane, fmul, fcorr, sdig, smeta);
         }
         for (int k = RING; k < ns; ++k)
             quantize_group(__builtin_bit_cast(float4, bload16<false>(xb, 16 * lane, 1024 * gl_of(k))), gl_of(k), lane,
-                           odd_scale, odd_corr, sdig, smeta);
+                           fmul, fcorr, sdig, smeta);
         // Each wave reads back only the groups it wrote.
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -403,13 +441,13 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
                 if (i + k < ns) {
                     const int gl = KS * (i + k);
                     float part[VT];
-                    q4k_group<VT>(part, st[k], abase + 1024 * gl, aoff, mbase + 8 * gl, h);
+                    group_dots<T, VT>(part, st[k], abase + 1024 * gl, aoff, mbase + 8 * gl, h);
 #pragma unroll
                     for (int v = 0; v < VT; ++v) acc[v] += part[v];
                     if (i + k + RING < ns)
 #pragma unroll
                         for (int v = 0; v < VT; ++v)
-                            load_q4k_rows<FULL>(st[k][v], wb, vq[v], vs[v], R[v], g0c + wave + gl + KS * RING);
+                            load_rows<T, FULL>(st[k][v], wb, vq[v], vs[v], R[v], g0c + wave + gl + KS * RING);
                 }
             }
         };
@@ -430,8 +468,8 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
     *dst = accumulate ? *dst + s : s;
 }
 
-template <int VT, int RING>
-__global__ __launch_bounds__(1024) void matvec_q4k_rows(const uint8_t *__restrict__ w, const float *__restrict__ x,
+template <unsigned T, int VT, int RING>
+__global__ __launch_bounds__(1024) void matvec_rows(const uint8_t *__restrict__ w, const float *__restrict__ x,
     float *__restrict__ y, int rows, int cols, int rw, int g0c, int ngc, int accumulate)
 {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -444,26 +482,14 @@ __global__ __launch_bounds__(1024) void matvec_q4k_rows(const uint8_t *__restric
     // matrix may be shorter): group and field offsets are scalar.
     const int tiles = (rows + kTileRows - 1) / kTileRows;
     if (rows % kTileRows == 0 || base + live <= kTileRows * (tiles - 1))
-        matvec_rows_body<VT, RING, true>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig, smeta, red);
+        matvec_rows_body<T, VT, RING, true>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig, smeta, red);
     else
-        matvec_rows_body<VT, RING, false>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig, smeta, red);
+        matvec_rows_body<T, VT, RING, false>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig, smeta, red);
 }
 
 size_t matvec_lds(int ccols)
 {
     return (size_t)ccols / 32 * (128 + kMetaBytes);
-}
-
-}  // namespace
-
-bool matvec_supported(unsigned type)
-{
-    return type == Q4_K;
-}
-
-const char *matvec_kernel(unsigned type)
-{
-    return type == Q4_K ? "matvec_q4k" : nullptr;
 }
 
 // Workgroups of the row-balanced kernel: one per CU (counted once per
@@ -481,34 +507,70 @@ int cu_count()
     return counts[dev];
 }
 
-hipError_t launch_matvec(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,
-    hipStream_t s)
+// Row-balanced layout: rows per workgroup (one workgroup per CU).
+int rows_per_workgroup(int rows)
 {
-    if (type != Q4_K) return hipErrorInvalidValue;
-    const int groups = cols / kGroupCols;
-    const unsigned tiles = (unsigned)((rows + kTileRows - 1) / kTileRows);
     const int cus = cu_count();
-    const int rw = (rows + cus - 1) / cus, wgs = (rows + rw - 1) / rw;
-    const bool balanced = rw <= 2 * kTileRows && (size_t)rows * tiled_row_bytes<Q4_K>(cols) < (1u << 31);
+    return (rows + cus - 1) / cus;
+}
+
+template <unsigned T>
+hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int cols, hipStream_t s)
+{
+    const int groups = cols / kGroupCols, rw = rows_per_workgroup(rows), wgs = (rows + rw - 1) / rw;
     for (int g0 = 0; g0 < groups; g0 += kChunkCols / kGroupCols) {
         const int ng = groups - g0 < kChunkCols / kGroupCols ? groups - g0 : kChunkCols / kGroupCols;
         const float *xc = x + (size_t)g0 * kGroupCols;
         const size_t lds = matvec_lds(ng * kGroupCols);
-        // One tile per CU: a second ring stage only where a wavefront has more
-        // than one group (a repeated stage would stream its group twice).
-        if (balanced && rw <= kTileRows && ng > 16)
-            hipLaunchKernelGGL((matvec_q4k_rows<1, 2>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng,
-                               g0 > 0);
-        else if (balanced && rw <= kTileRows)
-            hipLaunchKernelGGL((matvec_q4k_rows<1, 1>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng,
-                               g0 > 0);
-        else if (balanced)
-            hipLaunchKernelGGL((matvec_q4k_rows<2, 1>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng,
-                               g0 > 0);
-        // More than two 32-row tiles per CU: one workgroup per tile, eight
-        // wavefronts, two groups each in flight.
+        // One tile per CU: a second ring stage only where a wavefront has
+        // more than one group (a repeated stage would stream its group twice).
+        if (rw <= kTileRows && ng > 16)
+            hipLaunchKernelGGL((matvec_rows<T, 1, 2>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
+        else if (rw <= kTileRows)
+            hipLaunchKernelGGL((matvec_rows<T, 1, 1>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
         else
-            hipLaunchKernelGGL((matvec_q4k<8, 2>), dim3(tiles), dim3(512), lds, s, w, xc, y, rows, cols, g0, ng, g0 > 0);
+            hipLaunchKernelGGL((matvec_rows<T, 2, 1>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace
+
+// The row-balanced kernel takes up to two 32-row tiles per CU and whole
+// 256-column groups (Q8_0/Q4_0: rows of complete groups); Q4_K beyond two
+// tiles per CU runs one workgroup per tile.
+bool matvec_supported(unsigned type, int rows, int cols)
+{
+    if (type != Q4_K && type != Q4_0 && type != Q8_0) return false;
+    if (cols % kGroupCols) return false;
+    if (type == Q4_K) return true;
+    return rows_per_workgroup(rows) <= 2 * kTileRows;
+}
+
+const char *matvec_kernel(unsigned type, int rows, int cols)
+{
+    if (!matvec_supported(type, rows, cols)) return nullptr;
+    if (type == Q4_K && rows_per_workgroup(rows) > 2 * kTileRows) return "matvec_q4k";
+    return "matvec_rows";
+}
+
+hipError_t launch_matvec(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,
+    hipStream_t s)
+{
+    if (!matvec_supported(type, rows, cols)) return hipErrorInvalidValue;
+    if (type == Q4_0) return launch_rows<Q4_0>(w, x, y, rows, cols, s);
+    if (type == Q8_0) return launch_rows<Q8_0>(w, x, y, rows, cols, s);
+    if (rows_per_workgroup(rows) <= 2 * kTileRows) return launch_rows<Q4_K>(w, x, y, rows, cols, s);
+    // More than two 32-row tiles per CU: one workgroup per tile, eight
+    // wavefronts, two groups each in flight.
+    const int groups = cols / kGroupCols;
+    const unsigned tiles = (unsigned)((rows + kTileRows - 1) / kTileRows);
+    for (int g0 = 0; g0 < groups; g0 += kChunkCols / kGroupCols) {
+        const int ng = groups - g0 < kChunkCols / kGroupCols ? groups - g0 : kChunkCols / kGroupCols;
+        hipLaunchKernelGGL((matvec_q4k<8, 2>), dim3(tiles), dim3(512), matvec_lds(ng * kGroupCols), s, w,
+                           x + (size_t)g0 * kGroupCols, y, rows, cols, g0, ng, g0 > 0);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

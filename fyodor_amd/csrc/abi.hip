@@ -80,8 +80,9 @@ NYA_HIP_EXPORT int nya_hip_workspace_bytes(unsigned type, size_t rows, size_t co
     size_t b;
     if (!bytes || !batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return 1;
     const bool dense = type == F32 || type == F16 || type == BF16;
+    const int n = batch < 8 ? (int)batch : 8;
     *bytes = use_prefill(type, cols, batch) ? prefill_workspace(type, (int)cols, (int)batch)
-           : dense ? 0 : smalln_workspace((int)cols, batch < 8 ? (int)batch : 8);
+           : dense || smalln_rows_supported(type, (int)rows, (int)cols, n) ? 0 : smalln_workspace((int)cols, n);
     return 0;
 }
 
@@ -111,6 +112,9 @@ NYA_HIP_EXPORT int nya_hip_matmul(uintptr_t w, unsigned type, size_t rows, size_
         } else if (n == 1) {
             const int st = status(launch_token(type, wp, xp, yp, (int)rows, (int)cols, s));
             if (st) return st;
+        } else if (smalln_rows_supported(type, (int)rows, (int)cols, n)) {
+            const int st = status(launch_smalln_rows(type, wp, xp, yp, (int)rows, (int)cols, n, s));
+            if (st) return st;
         } else if ((fits && workspace_bytes >= smalln_workspace((int)cols, n))) {
             const int st = status(launch_smalln(type, wp, xp, yp, (int)rows, (int)cols, n, (void *)workspace, s));
             if (st) return st;
@@ -132,8 +136,8 @@ NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_
     if (!batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return NULL;
     if (type == F32 || type == F16 || type == BF16) return "skinny_dense";
     if (use_prefill(type, cols, batch)) return prefill_kernel(type);
-    return batch == 1 && matvec_supported(type, (int)rows, (int)cols) ? matvec_kernel(type, (int)rows, (int)cols)
-                                                                      : "smalln_mfma";
+    if (batch == 1 && matvec_supported(type, (int)rows, (int)cols)) return matvec_kernel(type, (int)rows, (int)cols);
+    return smalln_rows_supported(type, (int)rows, (int)cols, (int)batch) ? "smalln_rows" : "smalln_mfma";
 }
 
 NYA_HIP_EXPORT int nya_hip_copy(uintptr_t dst, uintptr_t src, size_t bytes, uintptr_t stream)

@@ -26,6 +26,11 @@ bool matvec_supported(unsigned type, int rows, int cols);
 const char *matvec_kernel(unsigned type, int rows, int cols);
 hipError_t launch_matvec(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,
     hipStream_t stream);
+// Batches of 2..8 on the same row-balanced layout, the activation digits made
+// inside the kernel (matvec.hip); no workspace. x must be 16-byte aligned.
+bool smalln_rows_supported(unsigned type, int rows, int cols, int batch);
+hipError_t launch_smalln_rows(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,
+    int batch, hipStream_t stream);
 
 // Activation digits of `batch` tokens x `cols` columns (row stride ldx) in
 // the layout of blockdot.h for np token slots (smalln.hip).

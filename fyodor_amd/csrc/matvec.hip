@@ -95,6 +95,16 @@ __device__ __forceinline__ uint32_t pack_byte(uint32_t w0, uint32_t w1, uint32_t
     return __builtin_amdgcn_perm(w1, w0, sel) | __builtin_amdgcn_perm(w3, w2, sel) << 16;
 }
 
+// Workgroup barrier that waits for no memory access: the empty asm keeps the
+// compiler from moving loads across it, so it orders the issue of the loads
+// before it ahead of those after it.
+__device__ __forceinline__ void issue_barrier()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // One 256-column group gl of x (chunk-local) into LDS: lane l holds columns
 // 4l .. 4l+3, lanes 8b .. 8b+7 block b. Digit slot d of block xg at
 // dig + 128 xg + 32 d (slot 3 zero); meta[xg] = {f 2^(e-21), c sum x,
@@ -396,17 +406,22 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
     float acc[VT];
 #pragma unroll
     for (int v = 0; v < VT; ++v) acc[v] = 0.f;
+    auto gl_of = [&](int k) { return wave + KS * (k < ns ? k : ns - 1); };
+    // 1. The A-operand offset table and x of the first RING groups, then the
+    //    weights (loads complete in order: what the quantization needs comes
+    //    first; the barrier puts every wavefront's x ahead of all weights).
+    //    Stages past the wave's last group repeat it.
+    int4 ao0 = {}, ao1 = {};
+    float4 px[RING];
     if (ns > 0) {
-        auto gl_of = [&](int k) { return wave + KS * (k < ns ? k : ns - 1); };
-        // 1. The A-operand offset table and x of the first RING groups, then
-        //    the weights (loads complete in order: what the quantization
-        //    needs comes first). Stages past the wave's last group repeat it.
-        int4 ao0 = ((const int4 *)kAoff.v[lane])[0], ao1 = ((const int4 *)kAoff.v[lane])[1];
-        float4 px[RING];
+        ao0 = ((const int4 *)kAoff.v[lane])[0];
+        ao1 = ((const int4 *)kAoff.v[lane])[1];
 #pragma unroll
         for (int k = 0; k < RING; ++k)
             px[k] = __builtin_bit_cast(float4, bload16<false>(xb, 16 * lane, 1024 * gl_of(k)));
-        asm volatile("" ::: "memory");
+    }
+    issue_barrier();
+    if (ns > 0) {
         MvStage<T> st[RING][VT];
 #pragma unroll
         for (int k = 0; k < RING; ++k)
@@ -536,7 +551,323 @@ hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int
     return hipSuccess;
 }
 
+// ---- batches of 2..8 ------------------------------------------------------
+//
+// Same row balance and weight loads as matvec_rows; the A rows of the MFMA
+// carry the tokens: A-row 4t + d holds digit d of token t (d = 3 reads a
+// zero slot), so D lane l, register 4j + d holds digit d of token 2j + l/32
+// for weight row l%32, and each block needs its own epilogue. To keep that
+// epilogue short the exponent is shared by a token's 256-column group:
+// X = x 2^(21-e) with 2^(e-1) <= max |x| < 2^e over the group (|X| <= 2^21,
+// error <= 2^-22 of the group's largest magnitude). Q4_K block scales are
+// then small integers that multiply the three digit sums in int32
+// (v_mad_i32_i24: |sc sum q a| < 2^22, eight blocks < 2^25), and the float
+// work per (row, token) is once per group: d s G - dmin sum_b m_b (sum x)_b
+// (the block sums of the quantized x, so the result is the exact dot with
+// the quantized x).
+// Q4_0 (as 16 (q - 8)) and Q8_0 keep one fma per block with its fp16 scale.
+//
+// Every wavefront takes one 256-column group (cols <= 4096) and quantizes all
+// eight token slots of it into its own LDS slot; tokens past the batch read
+// zeros (buffer range check), so their rows of the MFMA are zero.
+
+// One wavefront's LDS slot: digits [block][token][3 digits][32 B] (a 96-byte
+// token pitch puts the eight tokens of one digit word on distinct banks),
+// one 32-byte zero slot that the A rows of digit 3 read for every block, the
+// block sums of the quantized x sx[token][block] (Q4_K) and the token scales
+// s[4 (t & 1) + t / 2] (lane half h reads tokens h, 2 + h, 4 + h, 6 + h at
+// once).
+constexpr int kTokPitch = 96;
+constexpr int kTokBlockPitch = 8 * kTokPitch;
+constexpr int kSlotZero = 8 * kTokBlockPitch;
+constexpr int kSlotSx = kSlotZero + 32;
+constexpr int kSlotScale = kSlotSx + 8 * 8 * 4;
+constexpr int kWaveLds = kSlotScale + 8 * 4;
+constexpr int kRowsWaves = 16;
+static_assert(kWaveLds % 16 == 0, "16-byte LDS accesses");
+
+// Lane l quantizes columns 4j .. 4j+3 (j = l%8) of every block of token l/8
+// (v[i]: those of block i; one 128-byte line of the token per load);
+// SUMS: also the block sums of the quantized values (Q4_K minimums).
+template <bool SUMS>
+__device__ __forceinline__ void quantize_tokens(const float4 (&v)[8], int lane, uint8_t *__restrict__ slot)
+{
+    typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+    const int t = lane >> 3, j = lane & 7;
+    // Largest magnitude; the IEEE maximum keeps a NaN, so an inf or NaN
+    // anywhere in the group gives a bit pattern of at least 0x7F800000.
+    float mf = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        mf = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mf, __builtin_fabsf(v[i].x)), __builtin_fabsf(v[i].y));
+        mf = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mf, __builtin_fabsf(v[i].z)), __builtin_fabsf(v[i].w));
+    }
+    // The token's group maximum (lanes 8t .. 8t + 7).
+    const uint32_t m = max8u(fbits(mf) & 0x7FFFFFFFu);
+    const int e = __builtin_amdgcn_frexp_expf(__builtin_bit_cast(float, m));
+    const int sh = 21 - e < 127 ? 21 - e : 127;
+    const float scale = __builtin_bit_cast(float, (uint32_t)(sh + 127) << 23);
+    // As in quantize_group, one fma leaves a = 0x4B400000 + X. Its low half
+    // is X mod 2^16: two of them side by side take + 128 in one packed
+    // 16-bit add, whose odd bytes are then digit 1 (byte 1 of X + 128); the
+    // even bytes before the add are digit 0. Digit 2 is byte 2 of a + K2.
+    constexpr float M0 = 12582912.f;
+    constexpr uint32_t K2 = 32896u - 0x400000u;
+    uint8_t *rec = slot + kTokPitch * t + 4 * j;
+    int part[8];   // per block: the sum of this lane's four X
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 x = v[i];
+        const uint32_t a0 = fbits(__builtin_fmaf(x.x, scale, M0)), a1 = fbits(__builtin_fmaf(x.y, scale, M0));
+        const uint32_t a2 = fbits(__builtin_fmaf(x.z, scale, M0)), a3 = fbits(__builtin_fmaf(x.w, scale, M0));
+        const uint32_t p01 = __builtin_amdgcn_perm(a1, a0, 0x05040100u), p23 = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
+        const uint32_t q01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, p01) + (u16x2){128, 128});
+        const uint32_t q23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, p23) + (u16x2){128, 128});
+        uint32_t *w = (uint32_t *)(rec + kTokBlockPitch * i);
+        w[0] = __builtin_amdgcn_perm(p23, p01, 0x06040200u);
+        w[8] = __builtin_amdgcn_perm(q23, q01, 0x07050301u);
+        w[16] = pack_byte(a0 + K2, a1 + K2, a2 + K2, a3 + K2, 2);
+        // The four offsets 0x4B400000 wrap away.
+        if constexpr (SUMS) part[i] = (int)((a0 + a1) + (a2 + a3) - 4u * 0x4B400000u);
+    }
+    if (lane < 2) *(u32x4 *)(slot + kSlotZero + 16 * lane) = (u32x4){0u, 0u, 0u, 0u};
+    if constexpr (SUMS) {
+        // Block sums over the token's eight lanes, scattered so that lane j
+        // ends with block j: partners j and 7 - j (half-row mirror) keep
+        // blocks 4 (j / 4) .. +3, then j ^ 2 and j ^ 1 (quad swaps) halve
+        // again. |sum| <= 2^26.
+        int h4[4], h2[2];
+        const bool up4 = j & 4, up2 = j & 2, up1 = j & 1;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int keep = up4 ? part[k + 4] : part[k], send = up4 ? part[k] : part[k + 4];
+            h4[k] = keep + __builtin_amdgcn_update_dpp(0, send, 0x141, 0xF, 0xF, false);
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int keep = up2 ? h4[k + 2] : h4[k], send = up2 ? h4[k] : h4[k + 2];
+            h2[k] = keep + __builtin_amdgcn_update_dpp(0, send, 0x4E, 0xF, 0xF, false);
+        }
+        const int keep = up1 ? h2[1] : h2[0], send = up1 ? h2[0] : h2[1];
+        const int sum = keep + __builtin_amdgcn_update_dpp(0, send, 0xB1, 0xF, 0xF, false);
+        ((float *)(slot + kSlotSx))[8 * t + j] = __builtin_amdgcn_ldexpf((float)sum, -sh);
+    }
+    // s = 2^(e-21); NaN when the group holds an inf or NaN (then every
+    // output of the token is NaN).
+    if (j == 0)
+        ((float *)(slot + kSlotScale))[4 * (t & 1) + (t >> 1)] =
+            m < 0x7F800000u ? __builtin_amdgcn_ldexpf(1.f, -sh) : __builtin_nanf("");
+}
+
+// B operand of block k: Q4_K nibbles as they are (0..15), Q4_0 as
+// 16 (q - 8), Q8_0 bytes as they are.
+template <unsigned T>
+__device__ __forceinline__ i32x4 block_b_tokens(const MvStage<T> &w, int k)
+{
+    if constexpr (T == Q8_0) {
+        return as_i32x4(w.q[k]);
+    } else if constexpr (T == Q4_K) {
+        const u32x4 q = w.q[k >> 1];
+        return as_i32x4((k & 1) ? (q >> 4) & 0x0F0F0F0Fu : q & 0x0F0F0F0Fu);
+    } else {
+        const u32x4 q = w.q[k >> 1];
+        return as_i32x4(((k & 1) ? q & 0xF0F0F0F0u : (q << 4) & 0xF0F0F0F0u) ^ 0x80808080u);
+    }
+}
+
+// The group's dots for VT virtual tiles and eight token slots: y[v][j] +=
+// this group's share of token 2j + h, row l%32 of tile v. This lane's A
+// operand of block b sits at aoff + b astride in the slot.
+template <unsigned T, int VT>
+__device__ __forceinline__ void group_dots_tokens(float (&y)[VT][4], const MvStage<T> (&w)[VT],
+    const uint8_t *__restrict__ slot, int aoff, int astride, int h)
+{
+    const float4 sv = *(const float4 *)(slot + kSlotScale + 16 * h);
+    const float s4[4] = {sv.x, sv.y, sv.z, sv.w};
+    if constexpr (T == Q4_K) {
+        int acc[VT][4][3];
+#pragma unroll
+        for (int v = 0; v < VT; ++v)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[v][j][0] = acc[v][j][1] = acc[v][j][2] = 0;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const i32x4 a = *(const i32x4 *)(slot + aoff + astride * b);
+#pragma unroll
+            for (int v = 0; v < VT; ++v) {
+                const i32x16 D = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, block_b_tokens<T>(w[v], b), (i32x16){}, 0, 0, 0);
+                const int sc = (int)__builtin_amdgcn_ubfe(w[v].sl[b >> 1], 12 * (b & 1), 6);
+                // |D| < 2^16: the 24-bit multiply-add takes it whole. The
+                // empty asm keeps each sum a chain of multiply-adds (not
+                // products summed in threes); it names only the
+                // accumulators, never an MFMA result.
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int d = 0; d < 3; ++d) {
+                        acc[v][j][d] += ((D[4 * j + d] << 8) >> 8) * sc;
+                        asm("" : "+v"(acc[v][j][d]));
+                    }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 xa = *(const float4 *)(slot + kSlotSx + 32 * (2 * j + h));
+            const float4 xb = *(const float4 *)(slot + kSlotSx + 32 * (2 * j + h) + 16);
+            const float sx[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+            for (int v = 0; v < VT; ++v) {
+                const u32x4 sl = w[v].sl;   // byte 3 of the four words: d, dmin
+                const uint32_t dd = (sl.x >> 24) | ((sl.y >> 24) << 8) | ((sl.z >> 24) << 16) | ((sl.w >> 24) << 24);
+                float mterm = 0.f;
+#pragma unroll
+                for (int b = 0; b < 8; ++b)
+                    mterm = __builtin_fmaf((float)__builtin_amdgcn_ubfe(sl[b >> 1], 12 * (b & 1) + 6, 6), sx[b], mterm);
+                const float G = __builtin_fmaf((float)acc[v][j][2], 65536.f,
+                                               __builtin_fmaf((float)acc[v][j][1], 256.f, (float)acc[v][j][0]));
+                y[v][j] = __builtin_fmaf(-f16_to_f32(dd >> 16), mterm,
+                                         __builtin_fmaf(s4[j] * f16_to_f32(dd & 0xFFFFu), G, y[v][j]));
+            }
+        }
+    } else {
+        float acc[VT][4];
+#pragma unroll
+        for (int v = 0; v < VT; ++v)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[v][j] = 0.f;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const i32x4 a = *(const i32x4 *)(slot + aoff + astride * b);
+#pragma unroll
+            for (int v = 0; v < VT; ++v) {
+                const i32x16 D = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, block_b_tokens<T>(w[v], b), (i32x16){}, 0, 0, 0);
+                const float db = f16_to_f32((w[v].d[b >> 1] >> (16 * (b & 1))) & 0xFFFFu);
+                // Sums reach 2^34: the top digit joins in float.
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[v][j] = __builtin_fmaf(__builtin_fmaf((float)D[4 * j + 2], 65536.f,
+                                                              (float)(D[4 * j + 1] * 256 + D[4 * j])), db, acc[v][j]);
+            }
+        }
+        constexpr float kWeightFactor = T == Q4_0 ? 0.0625f : 1.f;
+#pragma unroll
+        for (int v = 0; v < VT; ++v)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) y[v][j] = __builtin_fmaf(s4[j] * kWeightFactor, acc[v][j], y[v][j]);
+    }
+}
+
+template <unsigned T, int VT, bool FULL>
+__device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, const float *__restrict__ x,
+    float *__restrict__ y, int rows, int cols, int n, int base, int live, uint8_t *lds)
+{
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = lane >> 5;
+    const int groups = cols / kGroupCols;
+    const size_t row_bytes = tiled_row_bytes<T>(cols);
+    const int tiles = (rows + kTileRows - 1) / kTileRows, rlast = rows - kTileRows * (tiles - 1);
+    const __amdgpu_buffer_rsrc_t wb = buffer_of(w, (uint32_t)((size_t)rows * row_bytes));
+    const __amdgpu_buffer_rsrc_t xb = buffer_of(x, (uint32_t)n * (uint32_t)cols * 4u);
+    float acc[VT][4];
+#pragma unroll
+    for (int v = 0; v < VT; ++v)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[v][j] = 0.f;
+    // x first, then the weights of every virtual tile (rows past this
+    // workgroup's repeat its last row). A CU's loads complete in order: the
+    // barrier puts every wavefront's x ahead of all weights, so no
+    // wavefront's quantization waits for another's weights.
+    const int vx = 4 * ((lane >> 3) * cols + 4 * (lane & 7));
+    float4 px[8];
+    if (wave < groups)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) px[i] = __builtin_bit_cast(float4, bload16<false>(xb, vx, 1024 * wave + 128 * i));
+    issue_barrier();
+    if (wave < groups) {
+        MvStage<T> st[VT];
+#pragma unroll
+        for (int v = 0; v < VT; ++v) {
+            const int row = base + (kTileRows * v + (lane & 31) < live ? kTileRows * v + (lane & 31) : live - 1);
+            const int t = row / kTileRows, r = row - kTileRows * t;
+            const int R = t == tiles - 1 ? rlast : kTileRows;
+            const int tb = (int)((size_t)kTileRows * t * row_bytes);
+            load_rows<T, FULL>(st[v], wb, tb + 16 * R * h + 16 * r, tb + 16 * r, R, wave);
+        }
+        uint8_t *slot = lds + kWaveLds * wave;
+        quantize_tokens<T == Q4_K>(px, lane, slot);
+        // Each wave reads back only its own slot.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // A-row 4t + d: digit d < 3 of token t, or the zero slot.
+        const bool digit = (lane & 3) < 3;
+        const int aoff = (digit ? kTokPitch * ((lane & 31) >> 2) + 32 * (lane & 3) : kSlotZero) + 16 * h;
+        group_dots_tokens<T, VT>(acc, st, slot, aoff, digit ? kTokBlockPitch : 0, h);
+    }
+
+    // Wavefronts' shares, in a fixed order (the slots are reused).
+    __syncthreads();
+    float *red = (float *)lds;   // [wave][VT][4][64]
+#pragma unroll
+    for (int v = 0; v < VT; ++v)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) red[((wave * VT + v) * 4 + j) * 64 + lane] = acc[v][j];
+    __syncthreads();
+    const int i = threadIdx.x;
+    if (i >= VT * 256) return;
+    const int v = i >> 8, t = (i >> 5) & 7, r = i & 31;
+    const int ln = r + 32 * (t & 1), nw = groups < kRowsWaves ? groups : kRowsWaves;
+    float s = 0.f;
+    for (int q = 0; q < nw; ++q) s += red[((q * VT + v) * 4 + (t >> 1)) * 64 + ln];
+    if (t < n && kTileRows * v + r < live) y[(size_t)t * rows + base + kTileRows * v + r] = s;
+}
+
+template <unsigned T, int VT>
+__global__ __launch_bounds__(64 * kRowsWaves) void smalln_rows(const uint8_t *__restrict__ w,
+    const float *__restrict__ x, float *__restrict__ y, int rows, int cols, int n, int rw)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int base = blockIdx.x * rw, live = rows - base < rw ? rows - base : rw;
+    const int tiles = (rows + kTileRows - 1) / kTileRows;
+    if (rows % kTileRows == 0 || base + live <= kTileRows * (tiles - 1))
+        smalln_rows_body<T, VT, true>(w, x, y, rows, cols, n, base, live, lds);
+    else
+        smalln_rows_body<T, VT, false>(w, x, y, rows, cols, n, base, live, lds);
+}
+
+template <unsigned T>
+hipError_t launch_tokens(const uint8_t *w, const float *x, float *y, int rows, int cols, int n, hipStream_t s)
+{
+    const int rw = rows_per_workgroup(rows), wgs = (rows + rw - 1) / rw;
+    const size_t lds = (size_t)kWaveLds * kRowsWaves;
+    if (rw <= kTileRows)
+        hipLaunchKernelGGL((smalln_rows<T, 1>), dim3(wgs), dim3(64 * kRowsWaves), lds, s, w, x, y, rows, cols, n, rw);
+    else
+        hipLaunchKernelGGL((smalln_rows<T, 2>), dim3(wgs), dim3(64 * kRowsWaves), lds, s, w, x, y, rows, cols, n, rw);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+// Batches of 2..8 on the row-balanced kernel: Q4_K, Q4_0 and Q8_0 rows of
+// at most 4096 columns in whole 256-column groups, up to two 32-row tiles
+// per CU.
+bool smalln_rows_supported(unsigned type, int rows, int cols, int batch)
+{
+    if (type != Q4_K && type != Q4_0 && type != Q8_0) return false;
+    if (batch < 2 || batch > 8 || cols % kGroupCols || cols > kRowsWaves * kGroupCols) return false;
+    return rows_per_workgroup(rows) <= 2 * kTileRows;
+}
+
+hipError_t launch_smalln_rows(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,
+    int batch, hipStream_t s)
+{
+    if (!smalln_rows_supported(type, rows, cols, batch)) return hipErrorInvalidValue;
+    if (type == Q4_K) return launch_tokens<Q4_K>(w, x, y, rows, cols, batch, s);
+    if (type == Q4_0) return launch_tokens<Q4_0>(w, x, y, rows, cols, batch, s);
+    return launch_tokens<Q8_0>(w, x, y, rows, cols, batch, s);
+}
 
 // The row-balanced kernel takes up to two 32-row tiles per CU and whole
 // 256-column groups (Q8_0/Q4_0: rows of complete groups); Q4_K beyond two

@@ -69,7 +69,9 @@ def test_queries(kernels):
     assert kernels.kernel_name(Q4_K, 14336, 4096, 1) == "matvec_rows"          # up to 64 rows per CU
     assert kernels.kernel_name(Q4_K, 57344, 4096, 1) == "matvec_q4k"           # one workgroup per tile
     assert kernels.kernel_name(Q8_0, 4096, 800, 1) == "smalln_mfma"            # a short last group
-    assert kernels.kernel_name(Q4_K, 14336, 4096, 8) == "smalln_mfma"
+    assert kernels.kernel_name(Q4_K, 14336, 4096, 8) == "smalln_rows"          # digits made in the kernel
+    assert kernels.kernel_name(Q4_K, 4096, 14336, 8) == "smalln_mfma"          # more than 4096 columns
+    assert kernels.kernel_name(Q6_K, 4096, 4096, 8) == "smalln_mfma"
 
 
 def unpack_reference(dev: np.ndarray, t: int, rows: int, cols: int) -> np.ndarray:
@@ -169,9 +171,13 @@ def test_prefill_dispatch_and_workspace():
 
     for t in (Q4_0, Q8_0, Q4_K, Q6_K):
         assert kern.workspace_bytes(t, 4096, 4096, 1) == 0
-        assert kern.workspace_bytes(t, 4096, 4096, 8) == 4096 // 32 * 136 * 8
-        assert kern.workspace_bytes(t, 4096, 4096, 3) == 4096 // 32 * 136 * 4
-        assert kern.kernel_name(t, 4096, 4096, 8) == "smalln_mfma"
+        # Rows of up to 4096 columns: the row-balanced kernel needs no
+        # workspace; Q6_K and wider rows keep digits for 8 or 4 slots.
+        rows_kernel = t != Q6_K
+        assert kern.workspace_bytes(t, 4096, 4096, 8) == (0 if rows_kernel else 4096 // 32 * 136 * 8)
+        assert kern.workspace_bytes(t, 4096, 4096, 3) == (0 if rows_kernel else 4096 // 32 * 136 * 4)
+        assert kern.workspace_bytes(t, 4096, 8192, 3) == 8192 // 32 * 136 * 4
+        assert kern.kernel_name(t, 4096, 4096, 8) == ("smalln_rows" if rows_kernel else "smalln_mfma")
     for t in (Q4_0, Q8_0, Q4_K):
         assert kern.workspace_bytes(t, 4096, 4096, 9) == pieces(4096, 9)
         assert kern.workspace_bytes(t, 4096, 4096, 512) == pieces(4096, 512)

@@ -98,10 +98,12 @@ def test_prefill_matches_tiled_path(hip, type_id):
     finally:
         for p in (wdev, xdev, ydev, work):
             rt.free(p)
-    # Without a workspace tokens run one at a time: on the batch-1 matvec
-    # where the type has one (its own rounding), else on the same small-N
+    # Without the GEMM's workspace the batch runs 8 tokens at a time: on the
+    # row-balanced small-N kernel where it takes the shape (no workspace
+    # either way); else without a workspace token by token, on the batch-1
+    # matvec where the type has one (its own rounding) or on the same small-N
     # kernel as the batches of 8 the short workspace gets.
-    if kern.kernel_name(type_id, rows, cols, 1) == "smalln_mfma":
+    if kern.kernel_name(type_id, rows, cols, 8) == "smalln_rows" or kern.kernel_name(type_id, rows, cols, 1) == "smalln_mfma":
         assert np.array_equal(short, tiled)
     else:
         assert rel_l2(short, tiled) <= 2e-6

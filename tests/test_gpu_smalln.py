@@ -8,7 +8,9 @@
   activation digits) they agree within 2e-6 of each row's magnitude;
 - matrices wider than one launch's column chunk (20480 columns) against the
   double-precision oracle under the reference kernel contract's per-row bound;
-- without a workspace the library runs a batch token by token, same result.
+- without a workspace the library runs a batch token by token, same result
+  (or, where the row-balanced kernel takes the shape, the batch itself: it
+  needs no workspace).
 """
 import numpy as np
 import pytest
@@ -60,7 +62,10 @@ def test_batches_equal_single_tokens(hip, t):
     else:
         scale = np.abs(single).max(axis=1, keepdims=True) + 1e-30
         assert np.all(np.abs(full - single) <= 2e-6 * scale)
-    assert np.array_equal(run(hip, w, t, rows, cols, x[:5], 5, workspace=False), single[:5])
+    # Without a workspace: the row-balanced kernel needs none; otherwise the
+    # tokens run one at a time.
+    y5 = run(hip, w, t, rows, cols, x[:5], 5, workspace=False)
+    assert np.array_equal(y5, full[:5] if hip[1].kernel_name(t, rows, cols, 5) == "smalln_rows" else single[:5])
 
 
 @pytest.mark.parametrize("t", QUANT, ids=lambda t: TYPE_NAMES[t])
@@ -73,3 +78,43 @@ def test_wide_rows_span_launches(hip, oracle, t, batch):
     for k in range(batch):
         check_rows(oracle, w, t, x[k], rows, cols, y[k])
         assert rel_l2(y[k], oracle.matvec(w, t, x[k], rows, cols)) <= 1e-5
+
+
+ROWS_TYPES = [Q4_0, Q8_0, Q4_K]
+
+
+@pytest.mark.parametrize("t", ROWS_TYPES, ids=lambda t: TYPE_NAMES[t])
+@pytest.mark.parametrize("rows,cols", [(200, 4096), (9000, 1024), (40, 256), (16384, 512)],
+                         ids=["partial-tile", "two-virtual-tiles-ragged", "one-group", "two-virtual-tiles"])
+def test_rows_kernel_against_oracle(hip, oracle, t, rows, cols):
+    """The row-balanced small-N kernel (activation digits made in the kernel,
+    one exponent per token and 256-column group) under the reference
+    contract's per-row bound, tokens spanning 2^-40 .. 2^44 in magnitude and
+    single groups 2^-20 below the rest of their token."""
+    assert hip[1].kernel_name(t, rows, cols, 8) == "smalln_rows"
+    w = synth.weights(t, rows, cols, 500 + t)
+    x = synth.activations(8, cols, 501 + t)
+    x *= np.float32(2.0) ** np.arange(-40, 56, 12, dtype=np.float32)[:, None]
+    x[3, 256:512] *= np.float32(2.0 ** -20)
+    y = run(hip, w, t, rows, cols, x, 8)
+    for k in range(8):
+        check_rows(oracle, w, t, x[k], rows, cols, y[k])
+        assert rel_l2(y[k], oracle.matvec(w, t, x[k], rows, cols)) <= 1e-5
+    assert np.array_equal(run(hip, w, t, rows, cols, x[:3], 3), y[:3])
+
+
+@pytest.mark.parametrize("t", ROWS_TYPES, ids=lambda t: TYPE_NAMES[t])
+def test_nonfinite_token(hip, t):
+    """An inf or NaN in one token's x makes every output of that token
+    non-finite and leaves the other tokens as they were."""
+    rows, cols = 256, 1024
+    w = synth.weights(t, rows, cols, 600 + t)
+    x = synth.activations(4, cols, 601 + t)
+    clean = run(hip, w, t, rows, cols, x, 4)
+    x[1, 300] = np.inf
+    x[2, 5] = np.nan
+    y = run(hip, w, t, rows, cols, x, 4)
+    assert not np.isfinite(y[1]).any() and not np.isfinite(y[2]).any()
+    assert np.array_equal(y[[0, 3]], clean[[0, 3]])
+    for k in (1, 2):
+        assert not np.isfinite(run(hip, w, t, rows, cols, x[k:k + 1], 1)).any()

@@ -567,43 +567,51 @@ hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int
 // the quantized x).
 // Q4_0 (as 16 (q - 8)) and Q8_0 keep one fma per block with its fp16 scale.
 //
-// Every wavefront takes one 256-column group (cols <= 4096) and quantizes all
-// eight token slots of it into its own LDS slot; tokens past the batch read
-// zeros (buffer range check), so their rows of the MFMA are zero.
+// Every wavefront takes one 256-column group (cols <= 4096) and quantizes its
+// 2, 4 or 8 token slots into its own LDS slot; slots past the batch read
+// zeros (buffer range check), and A rows past the slots read a zero slot.
 
-// One wavefront's LDS slot: digits [block][token][3 digits][32 B] (a 96-byte
-// token pitch puts the eight tokens of one digit word on distinct banks),
-// one 32-byte zero slot that the A rows of digit 3 read for every block, the
-// block sums of the quantized x sx[token][block] (Q4_K) and the token scales
-// s[4 (t & 1) + t / 2] (lane half h reads tokens h, 2 + h, 4 + h, 6 + h at
-// once).
+// One wavefront's LDS slot for NP token slots: digits [block][token][3
+// digits][32 B] (a 96-byte token pitch puts the tokens of one digit word on
+// distinct banks), one 32-byte zero slot that the A rows of digit 3 and of
+// tokens past NP read for every block, the block sums of the quantized x
+// sx[token][block] (Q4_K) and the token scales s[4 (t & 1) + t / 2] (lane
+// half h reads tokens h, 2 + h, 4 + h, 6 + h at once).
 constexpr int kTokPitch = 96;
-constexpr int kTokBlockPitch = 8 * kTokPitch;
-constexpr int kSlotZero = 8 * kTokBlockPitch;
-constexpr int kSlotSx = kSlotZero + 32;
-constexpr int kSlotScale = kSlotSx + 8 * 8 * 4;
-constexpr int kWaveLds = kSlotScale + 8 * 4;
 constexpr int kRowsWaves = 16;
-static_assert(kWaveLds % 16 == 0, "16-byte LDS accesses");
+template <int NP> struct RowsSlot {
+    static constexpr int kBlockPitch = NP * kTokPitch;
+    static constexpr int kZero = 8 * kBlockPitch;
+    static constexpr int kSx = kZero + 32;
+    static constexpr int kScale = kSx + NP * 8 * 4;
+    static constexpr int kBytes = kScale + 8 * 4;
+    static_assert(kBytes % 16 == 0, "16-byte LDS accesses");
+};
 
-// Lane l quantizes columns 4j .. 4j+3 (j = l%8) of every block of token l/8
-// (v[i]: those of block i; one 128-byte line of the token per load);
-// SUMS: also the block sums of the quantized values (Q4_K minimums).
-template <bool SUMS>
-__device__ __forceinline__ void quantize_tokens(const float4 (&v)[8], int lane, uint8_t *__restrict__ slot)
+// Token t of NP is quantized by the L = 64 / NP lanes t L .. t L + L - 1;
+// lane j of them takes columns 4 (j % 8) .. +3 of blocks k (L / 8) + j / 8
+// (v[k], k < NP): one load reads 16 L consecutive bytes of the token. SUMS:
+// also the block sums of the quantized values (Q4_K minimums).
+template <bool SUMS, int NP>
+__device__ __forceinline__ void quantize_tokens(const float4 (&v)[NP], int lane, uint8_t *__restrict__ slot)
 {
+    typedef RowsSlot<NP> S;
     typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
-    const int t = lane >> 3, j = lane & 7;
+    constexpr int L = 64 / NP;
+    const int t = lane / L, j = lane % L, p = j >> 3, jj = j & 7;
     // Largest magnitude; the IEEE maximum keeps a NaN, so an inf or NaN
     // anywhere in the group gives a bit pattern of at least 0x7F800000.
     float mf = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        mf = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mf, __builtin_fabsf(v[i].x)), __builtin_fabsf(v[i].y));
-        mf = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mf, __builtin_fabsf(v[i].z)), __builtin_fabsf(v[i].w));
+    for (int k = 0; k < NP; ++k) {
+        mf = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mf, __builtin_fabsf(v[k].x)), __builtin_fabsf(v[k].y));
+        mf = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mf, __builtin_fabsf(v[k].z)), __builtin_fabsf(v[k].w));
     }
-    // The token's group maximum (lanes 8t .. 8t + 7).
-    const uint32_t m = max8u(fbits(mf) & 0x7FFFFFFFu);
+    // The token's group maximum: eight lanes, then the mirrored half-row
+    // (16), then the other row of the pair (32).
+    uint32_t m = max8u(fbits(mf) & 0x7FFFFFFFu);
+    if constexpr (L >= 16) m = __builtin_elementwise_max(m, dppu<0x140>(m));
+    if constexpr (L >= 32) m = __builtin_elementwise_max(m, (uint32_t)__shfl_xor((int)m, 16, 64));
     const int e = __builtin_amdgcn_frexp_expf(__builtin_bit_cast(float, m));
     const int sh = 21 - e < 127 ? 21 - e : 127;
     const float scale = __builtin_bit_cast(float, (uint32_t)(sh + 127) << 23);
@@ -613,49 +621,70 @@ __device__ __forceinline__ void quantize_tokens(const float4 (&v)[8], int lane, 
     // even bytes before the add are digit 0. Digit 2 is byte 2 of a + K2.
     constexpr float M0 = 12582912.f;
     constexpr uint32_t K2 = 32896u - 0x400000u;
-    uint8_t *rec = slot + kTokPitch * t + 4 * j;
-    int part[8];   // per block: the sum of this lane's four X
+    uint8_t *rec = slot + kTokPitch * t + 4 * jj;
+    int part[NP];   // per block: the sum of this lane's four X
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 x = v[i];
+    for (int k = 0; k < NP; ++k) {
+        const float4 x = v[k];
         const uint32_t a0 = fbits(__builtin_fmaf(x.x, scale, M0)), a1 = fbits(__builtin_fmaf(x.y, scale, M0));
         const uint32_t a2 = fbits(__builtin_fmaf(x.z, scale, M0)), a3 = fbits(__builtin_fmaf(x.w, scale, M0));
         const uint32_t p01 = __builtin_amdgcn_perm(a1, a0, 0x05040100u), p23 = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
         const uint32_t q01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, p01) + (u16x2){128, 128});
         const uint32_t q23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, p23) + (u16x2){128, 128});
-        uint32_t *w = (uint32_t *)(rec + kTokBlockPitch * i);
+        uint32_t *w = (uint32_t *)(rec + S::kBlockPitch * (k * (L / 8) + p));
         w[0] = __builtin_amdgcn_perm(p23, p01, 0x06040200u);
         w[8] = __builtin_amdgcn_perm(q23, q01, 0x07050301u);
         w[16] = pack_byte(a0 + K2, a1 + K2, a2 + K2, a3 + K2, 2);
         // The four offsets 0x4B400000 wrap away.
-        if constexpr (SUMS) part[i] = (int)((a0 + a1) + (a2 + a3) - 4u * 0x4B400000u);
+        if constexpr (SUMS) part[k] = (int)((a0 + a1) + (a2 + a3) - 4u * 0x4B400000u);
     }
-    if (lane < 2) *(u32x4 *)(slot + kSlotZero + 16 * lane) = (u32x4){0u, 0u, 0u, 0u};
+    if (lane < 2) *(u32x4 *)(slot + S::kZero + 16 * lane) = (u32x4){0u, 0u, 0u, 0u};
     if constexpr (SUMS) {
-        // Block sums over the token's eight lanes, scattered so that lane j
-        // ends with block j: partners j and 7 - j (half-row mirror) keep
-        // blocks 4 (j / 4) .. +3, then j ^ 2 and j ^ 1 (quad swaps) halve
-        // again. |sum| <= 2^26.
-        int h4[4], h2[2];
-        const bool up4 = j & 4, up2 = j & 2, up1 = j & 1;
+        // Block sums over the eight lanes of a block (jj = 0..7), reduced
+        // and scattered: partners jj and 7 - jj (half-row mirror), then
+        // jj ^ 2 and jj ^ 1 (quad swaps); each step keeps half of the
+        // blocks while more than one is left, then sums in full. Lane jj
+        // ends with part index kf, written by the lanes that own it.
+        // |sum| <= 2^26.
+        const bool up4 = jj & 4, up2 = jj & 2, up1 = jj & 1;
+        int sum, kf;
+        bool writer;
+        if constexpr (NP == 8) {
+            int h4[4], h2[2];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int keep = up4 ? part[k + 4] : part[k], send = up4 ? part[k] : part[k + 4];
-            h4[k] = keep + __builtin_amdgcn_update_dpp(0, send, 0x141, 0xF, 0xF, false);
-        }
+            for (int k = 0; k < 4; ++k)
+                h4[k] = (up4 ? part[k + 4] : part[k]) +
+                        __builtin_amdgcn_update_dpp(0, up4 ? part[k] : part[k + 4], 0x141, 0xF, 0xF, false);
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int keep = up2 ? h4[k + 2] : h4[k], send = up2 ? h4[k] : h4[k + 2];
-            h2[k] = keep + __builtin_amdgcn_update_dpp(0, send, 0x4E, 0xF, 0xF, false);
+            for (int k = 0; k < 2; ++k)
+                h2[k] = (up2 ? h4[k + 2] : h4[k]) +
+                        __builtin_amdgcn_update_dpp(0, up2 ? h4[k] : h4[k + 2], 0x4E, 0xF, 0xF, false);
+            sum = (up1 ? h2[1] : h2[0]) + __builtin_amdgcn_update_dpp(0, up1 ? h2[0] : h2[1], 0xB1, 0xF, 0xF, false);
+            kf = jj;
+            writer = true;
+        } else if constexpr (NP == 4) {
+            int h2[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+                h2[k] = (up4 ? part[k + 2] : part[k]) +
+                        __builtin_amdgcn_update_dpp(0, up4 ? part[k] : part[k + 2], 0x141, 0xF, 0xF, false);
+            sum = (up2 ? h2[1] : h2[0]) + __builtin_amdgcn_update_dpp(0, up2 ? h2[0] : h2[1], 0x4E, 0xF, 0xF, false);
+            sum += __builtin_amdgcn_update_dpp(0, sum, 0xB1, 0xF, 0xF, false);
+            kf = 2 * up4 + up2;
+            writer = !up1;
+        } else {
+            sum = (up4 ? part[1] : part[0]) + __builtin_amdgcn_update_dpp(0, up4 ? part[0] : part[1], 0x141, 0xF, 0xF, false);
+            sum += __builtin_amdgcn_update_dpp(0, sum, 0x4E, 0xF, 0xF, false);
+            sum += __builtin_amdgcn_update_dpp(0, sum, 0xB1, 0xF, 0xF, false);
+            kf = up4;
+            writer = !up2 && !up1;
         }
-        const int keep = up1 ? h2[1] : h2[0], send = up1 ? h2[0] : h2[1];
-        const int sum = keep + __builtin_amdgcn_update_dpp(0, send, 0xB1, 0xF, 0xF, false);
-        ((float *)(slot + kSlotSx))[8 * t + j] = __builtin_amdgcn_ldexpf((float)sum, -sh);
+        if (writer) ((float *)(slot + S::kSx))[8 * t + kf * (L / 8) + p] = __builtin_amdgcn_ldexpf((float)sum, -sh);
     }
     // s = 2^(e-21); NaN when the group holds an inf or NaN (then every
     // output of the token is NaN).
     if (j == 0)
-        ((float *)(slot + kSlotScale))[4 * (t & 1) + (t >> 1)] =
+        ((float *)(slot + S::kScale))[4 * (t & 1) + (t >> 1)] =
             m < 0x7F800000u ? __builtin_amdgcn_ldexpf(1.f, -sh) : __builtin_nanf("");
 }
 
@@ -675,21 +704,23 @@ __device__ __forceinline__ i32x4 block_b_tokens(const MvStage<T> &w, int k)
     }
 }
 
-// The group's dots for VT virtual tiles and eight token slots: y[v][j] +=
-// this group's share of token 2j + h, row l%32 of tile v. This lane's A
-// operand of block b sits at aoff + b astride in the slot.
-template <unsigned T, int VT>
-__device__ __forceinline__ void group_dots_tokens(float (&y)[VT][4], const MvStage<T> (&w)[VT],
+// The group's dots for VT virtual tiles and NP token slots: y[v][j] += this
+// group's share of token 2j + h (j < NP / 2), row l%32 of tile v. This
+// lane's A operand of block b sits at aoff + b astride in the slot.
+template <unsigned T, int VT, int NP>
+__device__ __forceinline__ void group_dots_tokens(float (&y)[VT][NP / 2], const MvStage<T> (&w)[VT],
     const uint8_t *__restrict__ slot, int aoff, int astride, int h)
 {
-    const float4 sv = *(const float4 *)(slot + kSlotScale + 16 * h);
+    typedef RowsSlot<NP> S;
+    constexpr int J = NP / 2;
+    const float4 sv = *(const float4 *)(slot + S::kScale + 16 * h);
     const float s4[4] = {sv.x, sv.y, sv.z, sv.w};
     if constexpr (T == Q4_K) {
-        int acc[VT][4][3];
+        int acc[VT][J][3];
 #pragma unroll
         for (int v = 0; v < VT; ++v)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[v][j][0] = acc[v][j][1] = acc[v][j][2] = 0;
+            for (int j = 0; j < J; ++j) acc[v][j][0] = acc[v][j][1] = acc[v][j][2] = 0;
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
             const i32x4 a = *(const i32x4 *)(slot + aoff + astride * b);
@@ -702,7 +733,7 @@ __device__ __forceinline__ void group_dots_tokens(float (&y)[VT][4], const MvSta
                 // products summed in threes); it names only the
                 // accumulators, never an MFMA result.
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < J; ++j)
 #pragma unroll
                     for (int d = 0; d < 3; ++d) {
                         acc[v][j][d] += ((D[4 * j + d] << 8) >> 8) * sc;
@@ -711,9 +742,9 @@ __device__ __forceinline__ void group_dots_tokens(float (&y)[VT][4], const MvSta
             }
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float4 xa = *(const float4 *)(slot + kSlotSx + 32 * (2 * j + h));
-            const float4 xb = *(const float4 *)(slot + kSlotSx + 32 * (2 * j + h) + 16);
+        for (int j = 0; j < J; ++j) {
+            const float4 xa = *(const float4 *)(slot + S::kSx + 32 * (2 * j + h));
+            const float4 xb = *(const float4 *)(slot + S::kSx + 32 * (2 * j + h) + 16);
             const float sx[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
 #pragma unroll
             for (int v = 0; v < VT; ++v) {
@@ -730,11 +761,11 @@ __device__ __forceinline__ void group_dots_tokens(float (&y)[VT][4], const MvSta
             }
         }
     } else {
-        float acc[VT][4];
+        float acc[VT][J];
 #pragma unroll
         for (int v = 0; v < VT; ++v)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[v][j] = 0.f;
+            for (int j = 0; j < J; ++j) acc[v][j] = 0.f;
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
             const i32x4 a = *(const i32x4 *)(slot + aoff + astride * b);
@@ -744,7 +775,7 @@ __device__ __forceinline__ void group_dots_tokens(float (&y)[VT][4], const MvSta
                 const float db = f16_to_f32((w[v].d[b >> 1] >> (16 * (b & 1))) & 0xFFFFu);
                 // Sums reach 2^34: the top digit joins in float.
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < J; ++j)
                     acc[v][j] = __builtin_fmaf(__builtin_fmaf((float)D[4 * j + 2], 65536.f,
                                                               (float)(D[4 * j + 1] * 256 + D[4 * j])), db, acc[v][j]);
             }
@@ -753,14 +784,16 @@ __device__ __forceinline__ void group_dots_tokens(float (&y)[VT][4], const MvSta
 #pragma unroll
         for (int v = 0; v < VT; ++v)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) y[v][j] = __builtin_fmaf(s4[j] * kWeightFactor, acc[v][j], y[v][j]);
+            for (int j = 0; j < J; ++j) y[v][j] = __builtin_fmaf(s4[j] * kWeightFactor, acc[v][j], y[v][j]);
     }
 }
 
-template <unsigned T, int VT, bool FULL>
+template <unsigned T, int VT, int NP, bool FULL>
 __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, const float *__restrict__ x,
     float *__restrict__ y, int rows, int cols, int n, int base, int live, uint8_t *lds)
 {
+    typedef RowsSlot<NP> S;
+    constexpr int J = NP / 2, L = 64 / NP;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = lane >> 5;
@@ -769,20 +802,21 @@ __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, 
     const int tiles = (rows + kTileRows - 1) / kTileRows, rlast = rows - kTileRows * (tiles - 1);
     const __amdgpu_buffer_rsrc_t wb = buffer_of(w, (uint32_t)((size_t)rows * row_bytes));
     const __amdgpu_buffer_rsrc_t xb = buffer_of(x, (uint32_t)n * (uint32_t)cols * 4u);
-    float acc[VT][4];
+    float acc[VT][J];
 #pragma unroll
     for (int v = 0; v < VT; ++v)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[v][j] = 0.f;
+        for (int j = 0; j < J; ++j) acc[v][j] = 0.f;
     // x first, then the weights of every virtual tile (rows past this
     // workgroup's repeat its last row). A CU's loads complete in order: the
     // barrier puts every wavefront's x ahead of all weights, so no
-    // wavefront's quantization waits for another's weights.
-    const int vx = 4 * ((lane >> 3) * cols + 4 * (lane & 7));
-    float4 px[8];
+    // wavefront's quantization waits for another's weights. Tokens past n
+    // read zeros (buffer range check).
+    const int vx = 4 * (lane / L) * cols + 16 * (lane % L);
+    float4 px[NP];
     if (wave < groups)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) px[i] = __builtin_bit_cast(float4, bload16<false>(xb, vx, 1024 * wave + 128 * i));
+        for (int k = 0; k < NP; ++k) px[k] = __builtin_bit_cast(float4, bload16<false>(xb, vx, 1024 * wave + 16 * L * k));
     issue_barrier();
     if (wave < groups) {
         MvStage<T> st[VT];
@@ -794,36 +828,38 @@ __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, 
             const int tb = (int)((size_t)kTileRows * t * row_bytes);
             load_rows<T, FULL>(st[v], wb, tb + 16 * R * h + 16 * r, tb + 16 * r, R, wave);
         }
-        uint8_t *slot = lds + kWaveLds * wave;
-        quantize_tokens<T == Q4_K>(px, lane, slot);
+        uint8_t *slot = lds + S::kBytes * wave;
+        quantize_tokens<T == Q4_K, NP>(px, lane, slot);
         // Each wave reads back only its own slot.
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // A-row 4t + d: digit d < 3 of token t, or the zero slot.
-        const bool digit = (lane & 3) < 3;
-        const int aoff = (digit ? kTokPitch * ((lane & 31) >> 2) + 32 * (lane & 3) : kSlotZero) + 16 * h;
-        group_dots_tokens<T, VT>(acc, st, slot, aoff, digit ? kTokBlockPitch : 0, h);
+        // A-row 4t + d: digit d < 3 of token t < NP, or the zero slot.
+        const int at = (lane & 31) >> 2, ad = lane & 3;
+        const bool digit = at < NP && ad < 3;
+        const int aoff = (digit ? kTokPitch * at + 32 * ad : S::kZero) + 16 * h;
+        group_dots_tokens<T, VT, NP>(acc, st, slot, aoff, digit ? S::kBlockPitch : 0, h);
     }
 
     // Wavefronts' shares, in a fixed order (the slots are reused).
     __syncthreads();
-    float *red = (float *)lds;   // [wave][VT][4][64]
+    float *red = (float *)lds;   // [wave][VT][J][64]
 #pragma unroll
     for (int v = 0; v < VT; ++v)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) red[((wave * VT + v) * 4 + j) * 64 + lane] = acc[v][j];
+        for (int j = 0; j < J; ++j) red[((wave * VT + v) * J + j) * 64 + lane] = acc[v][j];
     __syncthreads();
     const int i = threadIdx.x;
     if (i >= VT * 256) return;
     const int v = i >> 8, t = (i >> 5) & 7, r = i & 31;
+    if (t >= n || kTileRows * v + r >= live) return;
     const int ln = r + 32 * (t & 1), nw = groups < kRowsWaves ? groups : kRowsWaves;
     float s = 0.f;
-    for (int q = 0; q < nw; ++q) s += red[((q * VT + v) * 4 + (t >> 1)) * 64 + ln];
-    if (t < n && kTileRows * v + r < live) y[(size_t)t * rows + base + kTileRows * v + r] = s;
+    for (int q = 0; q < nw; ++q) s += red[((q * VT + v) * J + (t >> 1)) * 64 + ln];
+    y[(size_t)t * rows + base + kTileRows * v + r] = s;
 }
 
-template <unsigned T, int VT>
+template <unsigned T, int VT, int NP>
 __global__ __launch_bounds__(64 * kRowsWaves) void smalln_rows(const uint8_t *__restrict__ w,
     const float *__restrict__ x, float *__restrict__ y, int rows, int cols, int n, int rw)
 {
@@ -831,21 +867,41 @@ __global__ __launch_bounds__(64 * kRowsWaves) void smalln_rows(const uint8_t *__
     const int base = blockIdx.x * rw, live = rows - base < rw ? rows - base : rw;
     const int tiles = (rows + kTileRows - 1) / kTileRows;
     if (rows % kTileRows == 0 || base + live <= kTileRows * (tiles - 1))
-        smalln_rows_body<T, VT, true>(w, x, y, rows, cols, n, base, live, lds);
+        smalln_rows_body<T, VT, NP, true>(w, x, y, rows, cols, n, base, live, lds);
     else
-        smalln_rows_body<T, VT, false>(w, x, y, rows, cols, n, base, live, lds);
+        smalln_rows_body<T, VT, NP, false>(w, x, y, rows, cols, n, base, live, lds);
 }
 
+// LDS of one smalln_rows workgroup: the wavefront slots, or the reduction
+// array [wave][VT][NP / 2][64] floats that reuses them, whichever is larger.
+template <int VT, int NP>
+constexpr size_t rows_lds()
+{
+    const size_t slots = (size_t)RowsSlot<NP>::kBytes * kRowsWaves;
+    const size_t red = (size_t)kRowsWaves * VT * (NP / 2) * 64 * 4;
+    return slots > red ? slots : red;
+}
+
+template <unsigned T, int NP>
+hipError_t launch_tokens_np(const uint8_t *w, const float *x, float *y, int rows, int cols, int n, hipStream_t s)
+{
+    const int rw = rows_per_workgroup(rows), wgs = (rows + rw - 1) / rw;
+    if (rw <= kTileRows)
+        hipLaunchKernelGGL((smalln_rows<T, 1, NP>), dim3(wgs), dim3(64 * kRowsWaves), (rows_lds<1, NP>()), s, w, x, y,
+                           rows, cols, n, rw);
+    else
+        hipLaunchKernelGGL((smalln_rows<T, 2, NP>), dim3(wgs), dim3(64 * kRowsWaves), (rows_lds<2, NP>()), s, w, x, y,
+                           rows, cols, n, rw);
+    return hipGetLastError();
+}
+
+// Token slots: 2, 4 or 8 (a token's quantization takes 64 / slots lanes).
 template <unsigned T>
 hipError_t launch_tokens(const uint8_t *w, const float *x, float *y, int rows, int cols, int n, hipStream_t s)
 {
-    const int rw = rows_per_workgroup(rows), wgs = (rows + rw - 1) / rw;
-    const size_t lds = (size_t)kWaveLds * kRowsWaves;
-    if (rw <= kTileRows)
-        hipLaunchKernelGGL((smalln_rows<T, 1>), dim3(wgs), dim3(64 * kRowsWaves), lds, s, w, x, y, rows, cols, n, rw);
-    else
-        hipLaunchKernelGGL((smalln_rows<T, 2>), dim3(wgs), dim3(64 * kRowsWaves), lds, s, w, x, y, rows, cols, n, rw);
-    return hipGetLastError();
+    if (n <= 2) return launch_tokens_np<T, 2>(w, x, y, rows, cols, n, s);
+    if (n <= 4) return launch_tokens_np<T, 4>(w, x, y, rows, cols, n, s);
+    return launch_tokens_np<T, 8>(w, x, y, rows, cols, n, s);
 }
 
 }  // namespace

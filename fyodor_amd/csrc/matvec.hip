@@ -1,5 +1,6 @@
-// Batch-1 matvec y = W x (token decode) for Q4_K, Q4_0 and Q8_0 weights in the
-// tiled layout of formats.h, with the block dot products on gfx950 int8 MFMA.
+// Batch-1 matvec y = W x (token decode) for Q4_K, Q4_0, Q8_0 and Q6_K weights
+// in the tiled layout of formats.h, with the block dot products on gfx950
+// int8 MFMA (and, further down, the batches of 2..8 on the same layout).
 //
 // Activations. Each 32-column block of x is written as X * 2^(e-21) with
 // 2^(e-1) <= max |x| < 2^e over the block and X integer, |X| <= 2^21, split
@@ -58,6 +59,26 @@ constexpr AoffTable make_aoff()
     return t;
 }
 __constant__ AoffTable kAoff = make_aoff();
+
+// Q6_K: lane half h of MFMA block j = 4c + j' (unit p = 2c + j'/2, nibble
+// m = j'%2) holds columns 16 (j'/2) .. +15 of x-block 4c + 2m + h, which has
+// its own 16-column scale. The halves get their own A rows: block j' of a
+// four-block chain sits in A-rows 8j' + 4h + d, digit d < 3 in K-half h only,
+// so D lane half h holds its own half's sums (registers 4j' .. 4j'+2) and
+// each group takes two chains (c = 0, 1).
+constexpr AoffTable make_aoff6()
+{
+    AoffTable t{};
+    for (int l = 0; l < 64; ++l)
+        for (int j = 0; j < 8; ++j) {
+            const int h = l >> 5, jr = (l & 31) >> 3, hr = ((l & 31) >> 2) & 1, dd = l & 3;
+            const int c = j >> 2, jp = j & 3, xb = 4 * c + 2 * (jp & 1) + h;
+            const bool live = jr == jp && hr == h && dd < 3;
+            t.v[l][j] = 128 * xb + 32 * (live ? dd : 3) + 16 * (jp >> 1);
+        }
+    return t;
+}
+__constant__ AoffTable kAoff6 = make_aoff6();
 
 template <int CTRL>
 __device__ __forceinline__ float dppf(float v)
@@ -153,6 +174,7 @@ template <unsigned T> struct MvStage;
 template <> struct MvStage<Q4_K> { u32x4 q[4]; u32x4 sl; };   // sl: 6-bit sc/m, d, dmin
 template <> struct MvStage<Q4_0> { u32x4 q[4]; u32x4 d; };    // d: eight fp16 block scales
 template <> struct MvStage<Q8_0> { u32x4 q[8]; u32x4 d; };
+template <> struct MvStage<Q6_K> { u32x4 ql[4], qh[4]; u32x4 sc; uint32_t d; };   // sc: int8 16-column scales
 template <unsigned T> constexpr int kQuantLoads = T == Q8_0 ? 8 : 4;
 template <unsigned T> constexpr int kGroupRowBytes = T == Q8_0 ? 272 : 144;   // per row, per group
 template <unsigned T> constexpr int kScaleOffset = T == Q8_0 ? 256 : 128;    // per row, in the group
@@ -161,6 +183,7 @@ template <unsigned T> constexpr int kScaleOffset = T == Q8_0 ? 256 : 128;    // 
 // of a group (see the header).
 template <unsigned T> __device__ __forceinline__ float block_factor(int lane)
 {
+    if constexpr (T == Q6_K) return 0.25f;   // the weights enter as 4 (q6 - 32)
     return T != Q8_0 && ((lane >> 3) & 1) ? 0.0625f : 1.f;
 }
 template <unsigned T> __device__ __forceinline__ float block_correction(int lane)
@@ -181,6 +204,22 @@ __device__ __forceinline__ i32x4 block_b(const MvStage<T> &w, int k)
     }
 }
 
+// Q6_K B operand of MFMA block j for lane half h: 4 (q6 - 32) =
+// (q6 << 2) ^ 0x80, from the nibble m = j%2 of unit p = j/2 (lane half h
+// loaded ql half h, elements q = 2m + h) and bits 2q, 2q+1 of qh.
+__device__ __forceinline__ i32x4 block_b6(const MvStage<Q6_K> &w, int j, int h)
+{
+    const int p = j >> 1, m = j & 1, q = 2 * m + h;
+    u32x4 u;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t lo = m ? w.ql[p][k] >> 2 : w.ql[p][k] << 2;   // nibble to bits 2..5
+        const uint32_t hi = w.qh[p][k] << (6 - 2 * q);                // two bits to 6..7
+        u[k] = (lo & 0x3C3C3C3Cu) | ((hi & 0xC0C0C0C0u) ^ 0x80808080u);
+    }
+    return as_i32x4(u);
+}
+
 // One 256-column group of VT 32-row tiles: for each tile the eight block dots
 // chained through one accumulator, then the scales. a points at this lane's
 // A operand of block 0 of the group, mt at its activation data of block h;
@@ -190,39 +229,72 @@ template <unsigned T, int VT>
 __device__ __forceinline__ void group_dots(float (&part)[VT], const MvStage<T> (&w)[VT],
     const uint8_t *__restrict__ a, const int (&aoff)[8], const float4 *__restrict__ mt, int h)
 {
-    // One tile at a time: its chain, then its epilogue (one accumulator live).
+    if constexpr (T == Q6_K) {
+        // Two chains of four blocks (see kAoff6); lane half h's block j' of
+        // chain c reads x-block 4c + 2 (j'%2) + h and the scale
+        // sc[8c + 2 q + j'/2] with q = 2 (j'%2) + h.
 #pragma unroll
-    for (int v = 0; v < VT; ++v) {
-        i32x16 D = {};
+        for (int v = 0; v < VT; ++v) {
+            float sum = 0.f;
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-            D = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const i32x4 *)(a + aoff[k]), block_b<T>(w[v], k), D, 0, 0, 0);
-        // Lane half h: blocks 2m + h.
-        float sum_s = 0.f, sum_m = 0.f;
+            for (int c = 0; c < 2; ++c) {
+                i32x16 D = {};
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const float4 md = mt[2 * m];
-            // Sums reach 2^34: the top digit joins in float.
-            const float G = __builtin_fmaf((float)D[4 * m + 2], 65536.f, (float)(D[4 * m + 1] * 256 + D[4 * m]));
-            const float t = __builtin_fmaf(G, md.x, md.y);
-            if constexpr (T == Q4_K) {
-                // Slice word m packs sc and m of blocks 2m (bits 0..11) and
-                // 2m + 1 (bits 12..23).
-                const float sc = (float)__builtin_amdgcn_ubfe(w[v].sl[m], 12 * h, 6);
-                const float mn = (float)__builtin_amdgcn_ubfe(w[v].sl[m], 12 * h + 6, 6);
-                sum_s = __builtin_fmaf(sc, t, sum_s);
-                sum_m = __builtin_fmaf(mn, md.z, sum_m);
-            } else {
-                // Scale word m holds the fp16 d of blocks 2m and 2m + 1.
-                sum_s = __builtin_fmaf(f16_to_f32(w[v].d[m] >> (16 * h)), t, sum_s);
+                for (int jp = 0; jp < 4; ++jp)
+                    D = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const i32x4 *)(a + aoff[4 * c + jp]),
+                                                              block_b6(w[v], 4 * c + jp, h), D, 0, 0, 0);
+#pragma unroll
+                for (int jp = 0; jp < 4; ++jp) {
+                    const float4 md = mt[4 * c + 2 * (jp & 1)];
+                    // Sums reach 2^34: the top digit joins in float.
+                    const float G = __builtin_fmaf((float)D[4 * jp + 2], 65536.f,
+                                                   (float)(D[4 * jp + 1] * 256 + D[4 * jp]));
+                    const float t = __builtin_fmaf(G, md.x, md.y);
+                    const int q = 2 * (jp & 1) + h;
+                    // The builtin's result type is unsigned: convert it as
+                    // the signed value it holds.
+                    const float sc = (float)(int)__builtin_amdgcn_sbfe((int)w[v].sc[2 * c + (jp >> 1)], 8 * q, 8);
+                    sum = __builtin_fmaf(sc, t, sum);
+                }
             }
+            part[v] = f16_to_f32(w[v].d & 0xFFFFu) * sum;
         }
-        if constexpr (T == Q4_K) {
-            const u32x4 sl = w[v].sl;   // byte 3 of the four words: d, dmin
-            const uint32_t dd = (sl.x >> 24) | ((sl.y >> 24) << 8) | ((sl.z >> 24) << 16) | ((sl.w >> 24) << 24);
-            part[v] = f16_to_f32(dd & 0xFFFFu) * sum_s - f16_to_f32(dd >> 16) * sum_m;
-        } else {
-            part[v] = sum_s;
+    } else {
+        // One tile at a time: its chain, then its epilogue (one accumulator
+        // live).
+#pragma unroll
+        for (int v = 0; v < VT; ++v) {
+            i32x16 D = {};
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                D = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const i32x4 *)(a + aoff[k]), block_b<T>(w[v], k), D, 0, 0, 0);
+            // Lane half h: blocks 2m + h.
+            float sum_s = 0.f, sum_m = 0.f;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const float4 md = mt[2 * m];
+                // Sums reach 2^34: the top digit joins in float.
+                const float G = __builtin_fmaf((float)D[4 * m + 2], 65536.f, (float)(D[4 * m + 1] * 256 + D[4 * m]));
+                const float t = __builtin_fmaf(G, md.x, md.y);
+                if constexpr (T == Q4_K) {
+                    // Slice word m packs sc and m of blocks 2m (bits 0..11) and
+                    // 2m + 1 (bits 12..23).
+                    const float sc = (float)__builtin_amdgcn_ubfe(w[v].sl[m], 12 * h, 6);
+                    const float mn = (float)__builtin_amdgcn_ubfe(w[v].sl[m], 12 * h + 6, 6);
+                    sum_s = __builtin_fmaf(sc, t, sum_s);
+                    sum_m = __builtin_fmaf(mn, md.z, sum_m);
+                } else {
+                    // Scale word m holds the fp16 d of blocks 2m and 2m + 1.
+                    sum_s = __builtin_fmaf(f16_to_f32(w[v].d[m] >> (16 * h)), t, sum_s);
+                }
+            }
+            if constexpr (T == Q4_K) {
+                const u32x4 sl = w[v].sl;   // byte 3 of the four words: d, dmin
+                const uint32_t dd = (sl.x >> 24) | ((sl.y >> 24) << 8) | ((sl.z >> 24) << 16) | ((sl.w >> 24) << 24);
+                part[v] = f16_to_f32(dd & 0xFFFFu) * sum_s - f16_to_f32(dd >> 16) * sum_m;
+            } else {
+                part[v] = sum_s;
+            }
         }
     }
 }
@@ -351,21 +423,45 @@ __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) vo
 // for every lane of the workgroup): the group and field parts are scalar
 // offsets.
 template <unsigned T, bool FULL>
-__device__ __forceinline__ void load_rows(MvStage<T> &w, __amdgpu_buffer_rsrc_t wb, int vq, int vs, int R, int g)
+__device__ __forceinline__ void load_rows(MvStage<T> &w, __amdgpu_buffer_rsrc_t wb, int vq, int vs, int R, int g,
+    int vd = 0, int G = 0)
 {
-    constexpr int GB = kGroupRowBytes<T>, S = kScaleOffset<T>;
-    u32x4 sw;
-    if constexpr (FULL) {
+    if constexpr (T == Q6_K) {
+        // Per group 208 R bytes: units p at 48 R p (ql half h at + 16 R h,
+        // qh at + 32 R), scales at 192 R; the d of all G groups after them
+        // (2 bytes per row at vd = tile + 2 r, group g at 208 R G + 2 R g).
 #pragma unroll
-        for (int p = 0; p < kQuantLoads<T>; ++p) w.q[p] = bload16<true>(wb, vq, kTileRows * GB * g + 1024 * p);
-        sw = bload16<true>(wb, vs, kTileRows * (GB * g + S));
+        for (int p = 0; p < 4; ++p) {
+            if constexpr (FULL) {
+                w.ql[p] = bload16<true>(wb, vq, kTileRows * (208 * g + 48 * p));
+                w.qh[p] = bload16<true>(wb, vs, kTileRows * (208 * g + 48 * p + 32));
+            } else {
+                w.ql[p] = bload16<true>(wb, vq + R * (208 * g + 48 * p), 0);
+                w.qh[p] = bload16<true>(wb, vs + R * (208 * g + 48 * p + 32), 0);
+            }
+        }
+        if constexpr (FULL) {
+            w.sc = bload16<true>(wb, vs, kTileRows * (208 * g + 192));
+            w.d = __builtin_amdgcn_raw_buffer_load_b16(wb, vd, kTileRows * (208 * G + 2 * g), 2);
+        } else {
+            w.sc = bload16<true>(wb, vs + R * (208 * g + 192), 0);
+            w.d = __builtin_amdgcn_raw_buffer_load_b16(wb, vd + R * (208 * G + 2 * g), 0, 2);
+        }
     } else {
+        constexpr int GB = kGroupRowBytes<T>, S = kScaleOffset<T>;
+        u32x4 sw;
+        if constexpr (FULL) {
 #pragma unroll
-        for (int p = 0; p < kQuantLoads<T>; ++p) w.q[p] = bload16<true>(wb, vq + R * (GB * g + 32 * p), 0);
-        sw = bload16<true>(wb, vs + R * (GB * g + S), 0);
+            for (int p = 0; p < kQuantLoads<T>; ++p) w.q[p] = bload16<true>(wb, vq, kTileRows * GB * g + 1024 * p);
+            sw = bload16<true>(wb, vs, kTileRows * (GB * g + S));
+        } else {
+#pragma unroll
+            for (int p = 0; p < kQuantLoads<T>; ++p) w.q[p] = bload16<true>(wb, vq + R * (GB * g + 32 * p), 0);
+            sw = bload16<true>(wb, vs + R * (GB * g + S), 0);
+        }
+        if constexpr (T == Q4_K) w.sl = sw;
+        else w.d = sw;
     }
-    if constexpr (T == Q4_K) w.sl = sw;
-    else w.d = sw;
 }
 
 // Row-balanced batch-1 matvec. One workgroup of sixteen wavefronts per CU
@@ -376,12 +472,11 @@ __device__ __forceinline__ void load_rows(MvStage<T> &w, __amdgpu_buffer_rsrc_t 
 // w, w + 16, ... of all VT tiles: it reads and quantizes only those groups of
 // x (no barrier before the dots), and each A operand it reads from LDS serves
 // the VT tiles' interleaved MFMA chains.
-template <unsigned T, int VT, int RING, bool FULL>
+template <unsigned T, int VT, int RING, int KS, bool FULL>
 __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, const float *__restrict__ x,
     float *__restrict__ y, int rows, int cols, int base, int live, int g0c, int ngc, int accumulate,
     uint8_t *sdig, float4 *smeta, float (*red)[VT][64])
 {
-    constexpr int KS = 16;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = lane >> 5;
@@ -391,7 +486,7 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
     const __amdgpu_buffer_rsrc_t xb = buffer_of(x, (uint32_t)((g0c + ngc) * kGroupCols <= cols ? ngc : 0) * 1024u);
     // Lane offsets per virtual tile; rows past this workgroup's repeat its
     // last row (same addresses: no extra traffic).
-    int vq[VT], vs[VT], R[VT];
+    int vq[VT], vs[VT], vd[VT], R[VT];
 #pragma unroll
     for (int v = 0; v < VT; ++v) {
         const int row = base + (kTileRows * v + (lane & 31) < live ? kTileRows * v + (lane & 31) : live - 1);
@@ -400,7 +495,9 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
         const int tb = (int)((size_t)kTileRows * t * row_bytes);
         vq[v] = tb + 16 * R[v] * h + 16 * r;
         vs[v] = tb + 16 * r;
+        vd[v] = tb + 2 * r;
     }
+    const int G = cols / kGroupCols;
     // This wave's chunk groups: wave + KS k for k < ns.
     const int ns = wave < ngc ? (ngc - wave + KS - 1) / KS : 0;
     float acc[VT];
@@ -414,8 +511,9 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
     int4 ao0 = {}, ao1 = {};
     float4 px[RING];
     if (ns > 0) {
-        ao0 = ((const int4 *)kAoff.v[lane])[0];
-        ao1 = ((const int4 *)kAoff.v[lane])[1];
+        const AoffTable &table = T == Q6_K ? kAoff6 : kAoff;
+        ao0 = ((const int4 *)table.v[lane])[0];
+        ao1 = ((const int4 *)table.v[lane])[1];
 #pragma unroll
         for (int k = 0; k < RING; ++k)
             px[k] = __builtin_bit_cast(float4, bload16<false>(xb, 16 * lane, 1024 * gl_of(k)));
@@ -426,7 +524,7 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
 #pragma unroll
         for (int k = 0; k < RING; ++k)
 #pragma unroll
-            for (int v = 0; v < VT; ++v) load_rows<T, FULL>(st[k][v], wb, vq[v], vs[v], R[v], g0c + gl_of(k));
+            for (int v = 0; v < VT; ++v) load_rows<T, FULL>(st[k][v], wb, vq[v], vs[v], R[v], g0c + gl_of(k), vd[v], G);
         asm volatile("" : "+v"(ao0.x), "+v"(ao0.y), "+v"(ao0.z), "+v"(ao0.w), "+v"(ao1.x), "+v"(ao1.y),
                      "+v"(ao1.z), "+v"(ao1.w) :: "memory");
 
@@ -462,7 +560,7 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
                     if (i + k + RING < ns)
 #pragma unroll
                         for (int v = 0; v < VT; ++v)
-                            load_rows<T, FULL>(st[k][v], wb, vq[v], vs[v], R[v], g0c + wave + gl + KS * RING);
+                            load_rows<T, FULL>(st[k][v], wb, vq[v], vs[v], R[v], g0c + wave + gl + KS * RING, vd[v], G);
                 }
             }
         };
@@ -483,12 +581,12 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
     *dst = accumulate ? *dst + s : s;
 }
 
-template <unsigned T, int VT, int RING>
-__global__ __launch_bounds__(1024) void matvec_rows(const uint8_t *__restrict__ w, const float *__restrict__ x,
+template <unsigned T, int VT, int RING, int KS>
+__global__ __launch_bounds__(64 * KS) void matvec_rows(const uint8_t *__restrict__ w, const float *__restrict__ x,
     float *__restrict__ y, int rows, int cols, int rw, int g0c, int ngc, int accumulate)
 {
     extern __shared__ __align__(16) uint8_t lds[];
-    __shared__ float red[16][VT][64];
+    __shared__ float red[KS][VT][64];
     const int ccols = (g0c + ngc) * kGroupCols < cols ? ngc * kGroupCols : cols - g0c * kGroupCols;
     uint8_t *sdig = lds;                                              // [xgroup][4 slots][32 B]
     float4 *smeta = (float4 *)(lds + (size_t)128 * (ccols / 32));     // [xgroup]
@@ -497,9 +595,9 @@ __global__ __launch_bounds__(1024) void matvec_rows(const uint8_t *__restrict__ 
     // matrix may be shorter): group and field offsets are scalar.
     const int tiles = (rows + kTileRows - 1) / kTileRows;
     if (rows % kTileRows == 0 || base + live <= kTileRows * (tiles - 1))
-        matvec_rows_body<T, VT, RING, true>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig, smeta, red);
+        matvec_rows_body<T, VT, RING, KS, true>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig, smeta, red);
     else
-        matvec_rows_body<T, VT, RING, false>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig, smeta, red);
+        matvec_rows_body<T, VT, RING, KS, false>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig, smeta, red);
 }
 
 size_t matvec_lds(int ccols)
@@ -538,13 +636,22 @@ hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int
         const float *xc = x + (size_t)g0 * kGroupCols;
         const size_t lds = matvec_lds(ng * kGroupCols);
         // One tile per CU: a second ring stage only where a wavefront has
-        // more than one group (a repeated stage would stream its group twice).
-        if (rw <= kTileRows && ng > 16)
-            hipLaunchKernelGGL((matvec_rows<T, 1, 2>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
-        else if (rw <= kTileRows)
-            hipLaunchKernelGGL((matvec_rows<T, 1, 1>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
-        else
-            hipLaunchKernelGGL((matvec_rows<T, 2, 1>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
+        // more than one group (a repeated stage would stream its group
+        // twice). Q6_K stages (37 registers) take eight wavefronts of up to
+        // 256 registers instead of sixteen of 128.
+        if constexpr (T == Q6_K) {
+            if (rw <= kTileRows)
+                hipLaunchKernelGGL((matvec_rows<T, 1, 2, 8>), dim3(wgs), dim3(512), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
+            else
+                hipLaunchKernelGGL((matvec_rows<T, 2, 1, 8>), dim3(wgs), dim3(512), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
+        } else {
+            if (rw <= kTileRows && ng > 16)
+                hipLaunchKernelGGL((matvec_rows<T, 1, 2, 16>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
+            else if (rw <= kTileRows)
+                hipLaunchKernelGGL((matvec_rows<T, 1, 1, 16>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
+            else
+                hipLaunchKernelGGL((matvec_rows<T, 2, 1, 16>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
+        }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -927,10 +1034,11 @@ hipError_t launch_smalln_rows(unsigned type, const uint8_t *w, const float *x, f
 
 // The row-balanced kernel takes up to two 32-row tiles per CU and whole
 // 256-column groups (Q8_0/Q4_0: rows of complete groups); Q4_K beyond two
-// tiles per CU runs one workgroup per tile.
+// tiles per CU runs one workgroup per tile, Q6_K there stays on the small-N
+// kernel.
 bool matvec_supported(unsigned type, int rows, int cols)
 {
-    if (type != Q4_K && type != Q4_0 && type != Q8_0) return false;
+    if (type != Q4_K && type != Q4_0 && type != Q8_0 && type != Q6_K) return false;
     if (cols % kGroupCols) return false;
     if (type == Q4_K) return true;
     return rows_per_workgroup(rows) <= 2 * kTileRows;
@@ -949,6 +1057,7 @@ hipError_t launch_matvec(unsigned type, const uint8_t *w, const float *x, float 
     if (!matvec_supported(type, rows, cols)) return hipErrorInvalidValue;
     if (type == Q4_0) return launch_rows<Q4_0>(w, x, y, rows, cols, s);
     if (type == Q8_0) return launch_rows<Q8_0>(w, x, y, rows, cols, s);
+    if (type == Q6_K) return launch_rows<Q6_K>(w, x, y, rows, cols, s);
     if (rows_per_workgroup(rows) <= 2 * kTileRows) return launch_rows<Q4_K>(w, x, y, rows, cols, s);
     // More than two 32-row tiles per CU: one workgroup per tile, eight
     // wavefronts, two groups each in flight.

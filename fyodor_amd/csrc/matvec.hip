@@ -630,18 +630,24 @@ int rows_per_workgroup(int rows)
 template <unsigned T>
 hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int cols, hipStream_t s)
 {
-    const int groups = cols / kGroupCols, rw = rows_per_workgroup(rows), wgs = (rows + rw - 1) / rw;
+    // Past two tiles per CU (Q6_K only): one workgroup per 32-row tile.
+    const int rpw = rows_per_workgroup(rows), rw = rpw > 2 * kTileRows ? kTileRows : rpw;
+    const int groups = cols / kGroupCols, wgs = (rows + rw - 1) / rw;
     for (int g0 = 0; g0 < groups; g0 += kChunkCols / kGroupCols) {
         const int ng = groups - g0 < kChunkCols / kGroupCols ? groups - g0 : kChunkCols / kGroupCols;
         const float *xc = x + (size_t)g0 * kGroupCols;
         const size_t lds = matvec_lds(ng * kGroupCols);
         // One tile per CU: a second ring stage only where a wavefront has
         // more than one group (a repeated stage would stream its group
-        // twice). Q6_K stages (37 registers) take eight wavefronts of up to
-        // 256 registers instead of sixteen of 128.
+        // twice). Q6_K (37-register stages): one stage per wavefront (two
+        // or three stages at eight wavefronts measured 13-17 % slower on
+        // 4096 x 14336); two tiles per CU take eight wavefronts of up to
+        // 256 registers.
         if constexpr (T == Q6_K) {
-            if (rw <= kTileRows)
-                hipLaunchKernelGGL((matvec_rows<T, 1, 2, 8>), dim3(wgs), dim3(512), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
+            if (rw <= kTileRows && rpw > 2 * kTileRows)   // one tile per workgroup (128256 x 4096: 84.7 -> 72.5 us)
+                hipLaunchKernelGGL((matvec_rows<T, 1, 1, 8>), dim3(wgs), dim3(512), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
+            else if (rw <= kTileRows)
+                hipLaunchKernelGGL((matvec_rows<T, 1, 1, 16>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
             else
                 hipLaunchKernelGGL((matvec_rows<T, 2, 1, 8>), dim3(wgs), dim3(512), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
         } else {
@@ -1033,14 +1039,14 @@ hipError_t launch_smalln_rows(unsigned type, const uint8_t *w, const float *x, f
 }
 
 // The row-balanced kernel takes up to two 32-row tiles per CU and whole
-// 256-column groups (Q8_0/Q4_0: rows of complete groups); Q4_K beyond two
-// tiles per CU runs one workgroup per tile, Q6_K there stays on the small-N
-// kernel.
+// 256-column groups (Q8_0/Q4_0: rows of complete groups); beyond two tiles
+// per CU, Q4_K and Q6_K run one workgroup per tile (matvec_q4k, or the row
+// kernel over single tiles).
 bool matvec_supported(unsigned type, int rows, int cols)
 {
     if (type != Q4_K && type != Q4_0 && type != Q8_0 && type != Q6_K) return false;
     if (cols % kGroupCols) return false;
-    if (type == Q4_K) return true;
+    if (type == Q4_K || type == Q6_K) return true;
     return rows_per_workgroup(rows) <= 2 * kTileRows;
 }
 

@@ -73,7 +73,7 @@ def test_queries(kernels):
     assert kernels.kernel_name(Q4_K, 4096, 14336, 8) == "smalln_mfma"          # more than 4096 columns
     assert kernels.kernel_name(Q6_K, 4096, 4096, 8) == "smalln_mfma"
     assert kernels.kernel_name(Q6_K, 4096, 14336, 1) == "matvec_rows"
-    assert kernels.kernel_name(Q6_K, 128256, 4096, 1) == "smalln_mfma"         # past two tiles per CU
+    assert kernels.kernel_name(Q6_K, 128256, 4096, 1) == "matvec_rows"         # one tile per workgroup
 
 
 def unpack_reference(dev: np.ndarray, t: int, rows: int, cols: int) -> np.ndarray:

@@ -680,8 +680,8 @@ hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int
 // the quantized x).
 // Q4_0 (as 16 (q - 8)) and Q8_0 keep one fma per block with its fp16 scale.
 //
-// Every wavefront takes one 256-column group (cols <= 4096) and quantizes its
-// 2, 4 or 8 token slots into its own LDS slot; slots past the batch read
+// Every wavefront takes 256-column groups w, w + 16, ... and quantizes each
+// for 2, 4 or 8 token slots into its own LDS slot; slots past the batch read
 // zeros (buffer range check), and A rows past the slots read a zero slot.
 
 // One wavefront's LDS slot for NP token slots: digits [block][token][3
@@ -901,7 +901,7 @@ __device__ __forceinline__ void group_dots_tokens(float (&y)[VT][NP / 2], const 
     }
 }
 
-template <unsigned T, int VT, int NP, bool FULL>
+template <unsigned T, int VT, int NP, bool LOOP, bool FULL>
 __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, const float *__restrict__ x,
     float *__restrict__ y, int rows, int cols, int n, int base, int live, uint8_t *lds)
 {
@@ -925,33 +925,66 @@ __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, 
     // barrier puts every wavefront's x ahead of all weights, so no
     // wavefront's quantization waits for another's weights. Tokens past n
     // read zeros (buffer range check).
+    // This wave's groups: wave + 16 k for k < ns (one slot, reused).
+    const int ns = wave < groups ? (groups - wave + kRowsWaves - 1) / kRowsWaves : 0;
     const int vx = 4 * (lane / L) * cols + 16 * (lane % L);
     float4 px[NP];
-    if (wave < groups)
+    auto load_x = [&](int g) {
 #pragma unroll
-        for (int k = 0; k < NP; ++k) px[k] = __builtin_bit_cast(float4, bload16<false>(xb, vx, 1024 * wave + 16 * L * k));
+        for (int k = 0; k < NP; ++k) px[k] = __builtin_bit_cast(float4, bload16<false>(xb, vx, 1024 * g + 16 * L * k));
+    };
+    if (ns > 0) load_x(wave);
     issue_barrier();
-    if (wave < groups) {
-        MvStage<T> st[VT];
-#pragma unroll
-        for (int v = 0; v < VT; ++v) {
-            const int row = base + (kTileRows * v + (lane & 31) < live ? kTileRows * v + (lane & 31) : live - 1);
-            const int t = row / kTileRows, r = row - kTileRows * t;
-            const int R = t == tiles - 1 ? rlast : kTileRows;
-            const int tb = (int)((size_t)kTileRows * t * row_bytes);
-            load_rows<T, FULL>(st[v], wb, tb + 16 * R * h + 16 * r, tb + 16 * r, R, wave);
-        }
+    if (ns > 0) {
         uint8_t *slot = lds + S::kBytes * wave;
-        quantize_tokens<T == Q4_K, NP>(px, lane, slot);
-        // Each wave reads back only its own slot.
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         // A-row 4t + d: digit d < 3 of token t < NP, or the zero slot.
         const int at = (lane & 31) >> 2, ad = lane & 3;
         const bool digit = at < NP && ad < 3;
         const int aoff = (digit ? kTokPitch * at + 32 * ad : S::kZero) + 16 * h;
-        group_dots_tokens<T, VT, NP>(acc, st, slot, aoff, digit ? S::kBlockPitch : 0, h);
+        MvStage<T> st[VT];
+        if constexpr (!LOOP) {
+            // One group per wavefront (cols <= 4096).
+#pragma unroll
+            for (int v = 0; v < VT; ++v) {
+                const int row = base + (kTileRows * v + (lane & 31) < live ? kTileRows * v + (lane & 31) : live - 1);
+                const int t = row / kTileRows, r = row - kTileRows * t;
+                const int R = t == tiles - 1 ? rlast : kTileRows;
+                const int tb = (int)((size_t)kTileRows * t * row_bytes);
+                load_rows<T, FULL>(st[v], wb, tb + 16 * R * h + 16 * r, tb + 16 * r, R, wave);
+            }
+            quantize_tokens<T == Q4_K, NP>(px, lane, slot);
+            // Each wave reads back only its own slot.
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            group_dots_tokens<T, VT, NP>(acc, st, slot, aoff, digit ? S::kBlockPitch : 0, h);
+        } else {
+            static_assert(VT == 1, "one virtual tile when looping over groups");
+            // Several groups per wavefront (one virtual tile): after each
+            // group's dots the next group's x, then its weights (no prefetch
+            // across the dots: x and a stage together would not fit the 128
+            // registers of sixteen wavefronts).
+            const int row = base + ((lane & 31) < live ? (lane & 31) : live - 1);
+            const int t = row / kTileRows, r = row - kTileRows * t;
+            const int R = t == tiles - 1 ? rlast : kTileRows;
+            const int tb = (int)((size_t)kTileRows * t * row_bytes);
+            const int vq = tb + 16 * R * h + 16 * r, vs = tb + 16 * r;
+            load_rows<T, FULL>(st[0], wb, vq, vs, R, wave);
+            for (int k = 0; k < ns; ++k) {
+                if (k > 0) {
+                    load_x(wave + kRowsWaves * k);
+                    load_rows<T, FULL>(st[0], wb, vq, vs, R, wave + kRowsWaves * k);
+                }
+                quantize_tokens<T == Q4_K, NP>(px, lane, slot);
+                // Each wave reads back only its own slot (and rewrites it
+                // only after this group's dots: a wave's LDS accesses
+                // complete in order).
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                group_dots_tokens<T, VT, NP>(acc, st, slot, aoff, digit ? S::kBlockPitch : 0, h);
+            }
+        }
     }
 
     // Wavefronts' shares, in a fixed order (the slots are reused).
@@ -972,7 +1005,7 @@ __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, 
     y[(size_t)t * rows + base + kTileRows * v + r] = s;
 }
 
-template <unsigned T, int VT, int NP>
+template <unsigned T, int VT, int NP, bool LOOP>
 __global__ __launch_bounds__(64 * kRowsWaves) void smalln_rows(const uint8_t *__restrict__ w,
     const float *__restrict__ x, float *__restrict__ y, int rows, int cols, int n, int rw)
 {
@@ -980,9 +1013,9 @@ __global__ __launch_bounds__(64 * kRowsWaves) void smalln_rows(const uint8_t *__
     const int base = blockIdx.x * rw, live = rows - base < rw ? rows - base : rw;
     const int tiles = (rows + kTileRows - 1) / kTileRows;
     if (rows % kTileRows == 0 || base + live <= kTileRows * (tiles - 1))
-        smalln_rows_body<T, VT, NP, true>(w, x, y, rows, cols, n, base, live, lds);
+        smalln_rows_body<T, VT, NP, LOOP, true>(w, x, y, rows, cols, n, base, live, lds);
     else
-        smalln_rows_body<T, VT, NP, false>(w, x, y, rows, cols, n, base, live, lds);
+        smalln_rows_body<T, VT, NP, LOOP, false>(w, x, y, rows, cols, n, base, live, lds);
 }
 
 // LDS of one smalln_rows workgroup: the wavefront slots, or the reduction
@@ -999,12 +1032,15 @@ template <unsigned T, int NP>
 hipError_t launch_tokens_np(const uint8_t *w, const float *x, float *y, int rows, int cols, int n, hipStream_t s)
 {
     const int rw = rows_per_workgroup(rows), wgs = (rows + rw - 1) / rw;
-    if (rw <= kTileRows)
-        hipLaunchKernelGGL((smalln_rows<T, 1, NP>), dim3(wgs), dim3(64 * kRowsWaves), (rows_lds<1, NP>()), s, w, x, y,
-                           rows, cols, n, rw);
+    if (cols > kRowsWaves * kGroupCols)   // several groups per wavefront (one tile per CU)
+        hipLaunchKernelGGL((smalln_rows<T, 1, NP, true>), dim3(wgs), dim3(64 * kRowsWaves), (rows_lds<1, NP>()), s, w,
+                           x, y, rows, cols, n, rw);
+    else if (rw <= kTileRows)
+        hipLaunchKernelGGL((smalln_rows<T, 1, NP, false>), dim3(wgs), dim3(64 * kRowsWaves), (rows_lds<1, NP>()), s, w,
+                           x, y, rows, cols, n, rw);
     else
-        hipLaunchKernelGGL((smalln_rows<T, 2, NP>), dim3(wgs), dim3(64 * kRowsWaves), (rows_lds<2, NP>()), s, w, x, y,
-                           rows, cols, n, rw);
+        hipLaunchKernelGGL((smalln_rows<T, 2, NP, false>), dim3(wgs), dim3(64 * kRowsWaves), (rows_lds<2, NP>()), s, w,
+                           x, y, rows, cols, n, rw);
     return hipGetLastError();
 }
 
@@ -1019,14 +1055,14 @@ hipError_t launch_tokens(const uint8_t *w, const float *x, float *y, int rows, i
 
 }  // namespace
 
-// Batches of 2..8 on the row-balanced kernel: Q4_K, Q4_0 and Q8_0 rows of
-// at most 4096 columns in whole 256-column groups, up to two 32-row tiles
-// per CU.
+// Batches of 2..8 on the row-balanced kernel: Q4_K, Q4_0 and Q8_0 rows in
+// whole 256-column groups, up to two 32-row tiles per CU (one where a
+// wavefront has more than one group).
 bool smalln_rows_supported(unsigned type, int rows, int cols, int batch)
 {
     if (type != Q4_K && type != Q4_0 && type != Q8_0) return false;
-    if (batch < 2 || batch > 8 || cols % kGroupCols || cols > kRowsWaves * kGroupCols) return false;
-    return rows_per_workgroup(rows) <= 2 * kTileRows;
+    if (batch < 2 || batch > 8 || cols % kGroupCols) return false;
+    return rows_per_workgroup(rows) <= (cols > kRowsWaves * kGroupCols ? 1 : 2) * kTileRows;
 }
 
 hipError_t launch_smalln_rows(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,

@@ -84,8 +84,9 @@ ROWS_TYPES = [Q4_0, Q8_0, Q4_K]
 
 
 @pytest.mark.parametrize("t", ROWS_TYPES, ids=lambda t: TYPE_NAMES[t])
-@pytest.mark.parametrize("rows,cols", [(200, 4096), (9000, 1024), (40, 256), (16384, 512)],
-                         ids=["partial-tile", "two-virtual-tiles-ragged", "one-group", "two-virtual-tiles"])
+@pytest.mark.parametrize("rows,cols", [(200, 4096), (9000, 1024), (40, 256), (16384, 512), (72, 11008)],
+                         ids=["partial-tile", "two-virtual-tiles-ragged", "one-group", "two-virtual-tiles",
+                              "groups-per-wave"])
 def test_rows_kernel_against_oracle(hip, oracle, t, rows, cols):
     """The row-balanced small-N kernel (activation digits made in the kernel,
     one exponent per token and 256-column group) under the reference

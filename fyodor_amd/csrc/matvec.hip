@@ -817,18 +817,80 @@ __device__ __forceinline__ i32x4 block_b_tokens(const MvStage<T> &w, int k)
     }
 }
 
+// Accumulators per lane and virtual tile: tokens 2j + h, or for Q6_K (each
+// lane half owns its own 16-column scale groups) every token.
+template <unsigned T, int NP> constexpr int kTokAcc = T == Q6_K ? NP : NP / 2;
+
 // The group's dots for VT virtual tiles and NP token slots: y[v][j] += this
-// group's share of token 2j + h (j < NP / 2), row l%32 of tile v. This
-// lane's A operand of block b sits at aoff + b astride in the slot.
+// group's share of token 2j + h (j < NP / 2; Q6_K: token j), row l%32 of
+// tile v. This lane's A operand of block b sits at aoff + b astride in the
+// slot (Q6_K: see below).
 template <unsigned T, int VT, int NP>
-__device__ __forceinline__ void group_dots_tokens(float (&y)[VT][NP / 2], const MvStage<T> (&w)[VT],
+__device__ __forceinline__ void group_dots_tokens(float (&y)[VT][(kTokAcc<T, NP>)], const MvStage<T> (&w)[VT],
     const uint8_t *__restrict__ slot, int aoff, int astride, int h)
 {
     typedef RowsSlot<NP> S;
     constexpr int J = NP / 2;
     const float4 sv = *(const float4 *)(slot + S::kScale + 16 * h);
     const float s4[4] = {sv.x, sv.y, sv.z, sv.w};
-    if constexpr (T == Q4_K) {
+    if constexpr (T == Q6_K) {
+        // MFMA block j = 4c + jp: lane half h holds columns 16 (jp / 2) .. +15
+        // of x-block 4c + 2 (jp % 2) + h with scale sc[8c + 2q + jp / 2],
+        // q = 2 (jp % 2) + h. A-row 8t' + 4h' + d: digit d of token t' + 4th
+        // in K-half h' only, so D lane half h holds its own half's sums of
+        // four tokens per MFMA (registers 4t' .. 4t'+2). aoff: this lane's
+        // A row in x-block h of the group for token half 0; bit th of
+        // astride: the row is live for token half th (else the zero slot).
+        constexpr int TH = NP > 4 ? 2 : 1, TT = NP < 4 ? NP : 4;
+        const float4 s0 = *(const float4 *)(slot + S::kScale), s1 = *(const float4 *)(slot + S::kScale + 16);
+        const float sraw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};   // token t at 4 (t & 1) + t / 2
+        int acc[VT][TH][TT][3];
+#pragma unroll
+        for (int v = 0; v < VT; ++v)
+#pragma unroll
+            for (int th = 0; th < TH; ++th)
+#pragma unroll
+                for (int t = 0; t < TT; ++t) acc[v][th][t][0] = acc[v][th][t][1] = acc[v][th][t][2] = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int c = j >> 2, jp = j & 3, q = 2 * (jp & 1) + h;
+            const int uoff = S::kBlockPitch * (4 * c + 2 * (jp & 1)) + 16 * (jp >> 1);
+#pragma unroll
+            for (int th = 0; th < TH; ++th) {
+                const int off = (astride >> th) & 1 ? aoff + 4 * kTokPitch * th + uoff : S::kZero;
+                const i32x4 a = *(const i32x4 *)(slot + off);
+#pragma unroll
+                for (int v = 0; v < VT; ++v) {
+                    const i32x16 D = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, block_b6(w[v], j, h), (i32x16){}, 0, 0, 0);
+                    const int sc = (int)__builtin_amdgcn_sbfe((int)w[v].sc[2 * c + (jp >> 1)], 8 * q, 8);
+                    // |D| < 2^18, |sc| <= 128: 24-bit multiply-adds, eight
+                    // blocks below 2^28.
+#pragma unroll
+                    for (int t = 0; t < TT; ++t)
+#pragma unroll
+                        for (int d = 0; d < 3; ++d) {
+                            acc[v][th][t][d] += ((D[4 * t + d] << 8) >> 8) * sc;
+                            asm("" : "+v"(acc[v][th][t][d]));
+                        }
+                }
+                // One MFMA result live at a time (register budget).
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < VT; ++v) {
+            const float d4 = 0.25f * f16_to_f32(w[v].d & 0xFFFFu);   // the weights entered as 4 (q6 - 32)
+#pragma unroll
+            for (int th = 0; th < TH; ++th)
+#pragma unroll
+                for (int t = 0; t < TT; ++t) {
+                    const int tok = 4 * th + t;
+                    const float G = __builtin_fmaf((float)acc[v][th][t][2], 65536.f,
+                                                   __builtin_fmaf((float)acc[v][th][t][1], 256.f, (float)acc[v][th][t][0]));
+                    y[v][tok] = __builtin_fmaf(sraw[4 * (tok & 1) + (tok >> 1)] * d4, G, y[v][tok]);
+                }
+        }
+    } else if constexpr (T == Q4_K) {
         int acc[VT][J][3];
 #pragma unroll
         for (int v = 0; v < VT; ++v)
@@ -906,7 +968,7 @@ __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, 
     float *__restrict__ y, int rows, int cols, int n, int base, int live, uint8_t *lds)
 {
     typedef RowsSlot<NP> S;
-    constexpr int J = NP / 2, L = 64 / NP;
+    constexpr int J = kTokAcc<T, NP>, L = 64 / NP;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = lane >> 5;
@@ -938,9 +1000,21 @@ __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, 
     if (ns > 0) {
         uint8_t *slot = lds + S::kBytes * wave;
         // A-row 4t + d: digit d < 3 of token t < NP, or the zero slot.
-        const int at = (lane & 31) >> 2, ad = lane & 3;
-        const bool digit = at < NP && ad < 3;
-        const int aoff = (digit ? kTokPitch * at + 32 * ad : S::kZero) + 16 * h;
+        int aoff, astride;
+        if constexpr (T == Q6_K) {
+            // A-row 8t' + 4h' + d: live in K-half h' = h for digit d < 3 of
+            // tokens t' (bit 0) and t' + 4 (bit 1) below NP.
+            const int tq = (lane & 31) >> 3, hq = ((lane & 31) >> 2) & 1, ad = lane & 3;
+            const bool row = hq == h && ad < 3;
+            aoff = S::kBlockPitch * h + kTokPitch * tq + 32 * ad;
+            astride = (row && tq < NP ? 1 : 0) | (row && tq + 4 < NP ? 2 : 0);
+        } else {
+            // A-row 4t + d: digit d < 3 of token t < NP, or the zero slot.
+            const int at = (lane & 31) >> 2, ad = lane & 3;
+            const bool digit = at < NP && ad < 3;
+            aoff = (digit ? kTokPitch * at + 32 * ad : S::kZero) + 16 * h;
+            astride = digit ? S::kBlockPitch : 0;
+        }
         MvStage<T> st[VT];
         if constexpr (!LOOP) {
             // One group per wavefront (cols <= 4096).
@@ -950,14 +1024,14 @@ __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, 
                 const int t = row / kTileRows, r = row - kTileRows * t;
                 const int R = t == tiles - 1 ? rlast : kTileRows;
                 const int tb = (int)((size_t)kTileRows * t * row_bytes);
-                load_rows<T, FULL>(st[v], wb, tb + 16 * R * h + 16 * r, tb + 16 * r, R, wave);
+                load_rows<T, FULL>(st[v], wb, tb + 16 * R * h + 16 * r, tb + 16 * r, R, wave, tb + 2 * r, groups);
             }
             quantize_tokens<T == Q4_K, NP>(px, lane, slot);
             // Each wave reads back only its own slot.
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            group_dots_tokens<T, VT, NP>(acc, st, slot, aoff, digit ? S::kBlockPitch : 0, h);
+            group_dots_tokens<T, VT, NP>(acc, st, slot, aoff, astride, h);
         } else {
             static_assert(VT == 1, "one virtual tile when looping over groups");
             // Several groups per wavefront (one virtual tile): after each
@@ -968,12 +1042,12 @@ __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, 
             const int t = row / kTileRows, r = row - kTileRows * t;
             const int R = t == tiles - 1 ? rlast : kTileRows;
             const int tb = (int)((size_t)kTileRows * t * row_bytes);
-            const int vq = tb + 16 * R * h + 16 * r, vs = tb + 16 * r;
-            load_rows<T, FULL>(st[0], wb, vq, vs, R, wave);
+            const int vq = tb + 16 * R * h + 16 * r, vs = tb + 16 * r, vd = tb + 2 * r;
+            load_rows<T, FULL>(st[0], wb, vq, vs, R, wave, vd, groups);
             for (int k = 0; k < ns; ++k) {
                 if (k > 0) {
                     load_x(wave + kRowsWaves * k);
-                    load_rows<T, FULL>(st[0], wb, vq, vs, R, wave + kRowsWaves * k);
+                    load_rows<T, FULL>(st[0], wb, vq, vs, R, wave + kRowsWaves * k, vd, groups);
                 }
                 quantize_tokens<T == Q4_K, NP>(px, lane, slot);
                 // Each wave reads back only its own slot (and rewrites it
@@ -982,7 +1056,10 @@ __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, 
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                group_dots_tokens<T, VT, NP>(acc, st, slot, aoff, digit ? S::kBlockPitch : 0, h);
+                group_dots_tokens<T, VT, NP>(acc, st, slot, aoff, astride, h);
+                // Keeps the next group's loads after these dots (their
+                // registers and those of the dots would not fit together).
+                asm volatile("" ::: "memory");
             }
         }
     }
@@ -999,9 +1076,15 @@ __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, 
     if (i >= VT * 256) return;
     const int v = i >> 8, t = (i >> 5) & 7, r = i & 31;
     if (t >= n || kTileRows * v + r >= live) return;
-    const int ln = r + 32 * (t & 1), nw = groups < kRowsWaves ? groups : kRowsWaves;
+    const int nw = groups < kRowsWaves ? groups : kRowsWaves;
     float s = 0.f;
-    for (int q = 0; q < nw; ++q) s += red[((q * VT + v) * J + (t >> 1)) * 64 + ln];
+    if constexpr (T == Q6_K) {
+        // Every lane holds every token: its lane half's columns.
+        for (int q = 0; q < nw; ++q) s += red[((q * VT + v) * J + t) * 64 + r] + red[((q * VT + v) * J + t) * 64 + r + 32];
+    } else {
+        const int ln = r + 32 * (t & 1);
+        for (int q = 0; q < nw; ++q) s += red[((q * VT + v) * J + (t >> 1)) * 64 + ln];
+    }
     y[(size_t)t * rows + base + kTileRows * v + r] = s;
 }
 
@@ -1019,12 +1102,13 @@ __global__ __launch_bounds__(64 * kRowsWaves) void smalln_rows(const uint8_t *__
 }
 
 // LDS of one smalln_rows workgroup: the wavefront slots, or the reduction
-// array [wave][VT][NP / 2][64] floats that reuses them, whichever is larger.
+// array [wave][VT][NP or NP / 2][64] floats that reuses them, whichever is
+// larger.
 template <int VT, int NP>
 constexpr size_t rows_lds()
 {
     const size_t slots = (size_t)RowsSlot<NP>::kBytes * kRowsWaves;
-    const size_t red = (size_t)kRowsWaves * VT * (NP / 2) * 64 * 4;
+    const size_t red = (size_t)kRowsWaves * VT * NP * 64 * 4;
     return slots > red ? slots : red;
 }
 
@@ -1032,13 +1116,13 @@ template <unsigned T, int NP>
 hipError_t launch_tokens_np(const uint8_t *w, const float *x, float *y, int rows, int cols, int n, hipStream_t s)
 {
     const int rw = rows_per_workgroup(rows), wgs = (rows + rw - 1) / rw;
-    if (cols > kRowsWaves * kGroupCols)   // several groups per wavefront (one tile per CU)
-        hipLaunchKernelGGL((smalln_rows<T, 1, NP, true>), dim3(wgs), dim3(64 * kRowsWaves), (rows_lds<1, NP>()), s, w,
+    if (cols > kRowsWaves * kGroupCols && !(T == Q6_K && NP == 8))   // several groups per wavefront (one tile per CU)
+        hipLaunchKernelGGL((smalln_rows<T, 1, NP, !(T == Q6_K && NP == 8)>), dim3(wgs), dim3(64 * kRowsWaves), (rows_lds<1, NP>()), s, w,
                            x, y, rows, cols, n, rw);
-    else if (rw <= kTileRows)
+    else if (T == Q6_K || rw <= kTileRows)
         hipLaunchKernelGGL((smalln_rows<T, 1, NP, false>), dim3(wgs), dim3(64 * kRowsWaves), (rows_lds<1, NP>()), s, w,
                            x, y, rows, cols, n, rw);
-    else
+    else if constexpr (T != Q6_K)
         hipLaunchKernelGGL((smalln_rows<T, 2, NP, false>), dim3(wgs), dim3(64 * kRowsWaves), (rows_lds<2, NP>()), s, w,
                            x, y, rows, cols, n, rw);
     return hipGetLastError();
@@ -1055,14 +1139,19 @@ hipError_t launch_tokens(const uint8_t *w, const float *x, float *y, int rows, i
 
 }  // namespace
 
-// Batches of 2..8 on the row-balanced kernel: Q4_K, Q4_0 and Q8_0 rows in
-// whole 256-column groups, up to two 32-row tiles per CU (one where a
-// wavefront has more than one group).
+// Batches of 2..8 on the row-balanced kernel: Q4_K, Q4_0, Q8_0 and Q6_K rows
+// in whole 256-column groups, up to two 32-row tiles per CU (one where a
+// wavefront has more than one group, and for Q6_K).
 bool smalln_rows_supported(unsigned type, int rows, int cols, int batch)
 {
-    if (type != Q4_K && type != Q4_0 && type != Q8_0) return false;
+    if (type != Q4_K && type != Q4_0 && type != Q8_0 && type != Q6_K) return false;
     if (batch < 2 || batch > 8 || cols % kGroupCols) return false;
-    return rows_per_workgroup(rows) <= (cols > kRowsWaves * kGroupCols ? 1 : 2) * kTileRows;
+    // Q6_K stages (37 registers): one virtual tile, and on rows of several
+    // groups per wavefront at most four token slots (eight would spill; two
+    // launches of four measured slower than the tile kernel).
+    const bool wide = cols > kRowsWaves * kGroupCols;
+    if (type == Q6_K && wide && batch > 4) return false;
+    return rows_per_workgroup(rows) <= (wide || type == Q6_K ? 1 : 2) * kTileRows;
 }
 
 hipError_t launch_smalln_rows(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,
@@ -1071,6 +1160,7 @@ hipError_t launch_smalln_rows(unsigned type, const uint8_t *w, const float *x, f
     if (!smalln_rows_supported(type, rows, cols, batch)) return hipErrorInvalidValue;
     if (type == Q4_K) return launch_tokens<Q4_K>(w, x, y, rows, cols, batch, s);
     if (type == Q4_0) return launch_tokens<Q4_0>(w, x, y, rows, cols, batch, s);
+    if (type == Q6_K) return launch_tokens<Q6_K>(w, x, y, rows, cols, batch, s);
     return launch_tokens<Q8_0>(w, x, y, rows, cols, batch, s);
 }
 

@@ -72,7 +72,8 @@ def test_queries(kernels):
     assert kernels.kernel_name(Q4_K, 14336, 4096, 8) == "smalln_rows"          # digits made in the kernel
     assert kernels.kernel_name(Q4_K, 4096, 14336, 8) == "smalln_rows"          # several groups per wavefront
     assert kernels.kernel_name(Q4_K, 14336, 8192, 8) == "smalln_mfma"          # that, at two tiles per CU
-    assert kernels.kernel_name(Q6_K, 4096, 4096, 8) == "smalln_mfma"
+    assert kernels.kernel_name(Q6_K, 4096, 4096, 8) == "smalln_rows"
+    assert kernels.kernel_name(Q6_K, 14336, 4096, 8) == "smalln_mfma"          # Q6_K rows kernel: one tile per CU
     assert kernels.kernel_name(Q6_K, 4096, 14336, 1) == "matvec_rows"
     assert kernels.kernel_name(Q6_K, 128256, 4096, 1) == "matvec_rows"         # one tile per workgroup
 
@@ -175,9 +176,9 @@ def test_prefill_dispatch_and_workspace():
     for t in (Q4_0, Q8_0, Q4_K, Q6_K):
         assert kern.workspace_bytes(t, 4096, 4096, 1) == 0
         # The row-balanced kernel needs no workspace (rows wider than 4096
-        # columns: one tile per CU); Q6_K and the others keep digits for 8 or
-        # 4 slots.
-        rows_kernel = t != Q6_K
+        # columns and Q6_K: one tile per CU); the tile kernel keeps digits for
+        # 8 or 4 slots.
+        rows_kernel = True
         assert kern.workspace_bytes(t, 4096, 4096, 8) == (0 if rows_kernel else 4096 // 32 * 136 * 8)
         assert kern.workspace_bytes(t, 4096, 4096, 3) == (0 if rows_kernel else 4096 // 32 * 136 * 4)
         assert kern.workspace_bytes(t, 4096, 8192, 3) == (0 if rows_kernel else 8192 // 32 * 136 * 4)

@@ -104,7 +104,27 @@ def test_rows_kernel_against_oracle(hip, oracle, t, rows, cols):
     assert np.array_equal(run(hip, w, t, rows, cols, x[:3], 3), y[:3])
 
 
-@pytest.mark.parametrize("t", ROWS_TYPES, ids=lambda t: TYPE_NAMES[t])
+@pytest.mark.parametrize("rows,cols", [(200, 4096), (40, 256), (72, 11008)],
+                         ids=["partial-tile", "one-group", "groups-per-wave"])
+def test_rows_kernel_q6k_against_oracle(hip, oracle, rows, cols):
+    """Q6_K on the row kernel (each lane half with its own 16-column
+    scales; rows wider than 4096 columns up to four tokens) under the
+    contract bound, tokens spanning 2^-40 .. 2^44."""
+    t = Q6_K
+    wide = cols > 4096
+    assert hip[1].kernel_name(t, rows, cols, 4 if wide else 8) == "smalln_rows"
+    assert hip[1].kernel_name(t, rows, cols, 8) == ("smalln_mfma" if wide else "smalln_rows")
+    w = synth.weights(t, rows, cols, 700)
+    x = synth.activations(8, cols, 701)
+    x *= np.float32(2.0) ** np.arange(-40, 56, 12, dtype=np.float32)[:, None]
+    for batch in ((4, 3) if wide else (8, 3)):
+        y = run(hip, w, t, rows, cols, x[:batch], batch)
+        for k in range(batch):
+            check_rows(oracle, w, t, x[k], rows, cols, y[k])
+            assert rel_l2(y[k], oracle.matvec(w, t, x[k], rows, cols)) <= 1e-5
+
+
+@pytest.mark.parametrize("t", ROWS_TYPES + [Q6_K], ids=lambda t: TYPE_NAMES[t])
 def test_nonfinite_token(hip, t):
     """An inf or NaN in one token's x makes every output of that token
     non-finite and leaves the other tokens as they were."""

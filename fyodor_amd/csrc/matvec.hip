@@ -1115,7 +1115,11 @@ constexpr size_t rows_lds()
 template <unsigned T, int NP>
 hipError_t launch_tokens_np(const uint8_t *w, const float *x, float *y, int rows, int cols, int n, hipStream_t s)
 {
-    const int rw = rows_per_workgroup(rows), wgs = (rows + rw - 1) / rw;
+    // Past two tiles per CU (Q6_K: past one), one workgroup per 32-row tile
+    // (each quantizes x again; Q6_K 128256 x 4096 N=2 98 -> 83 us, Q4_K
+    // 57344 x 4096 N=2 33 -> 24 us against the tile kernel).
+    const int rpw = rows_per_workgroup(rows);
+    const int rw = (T == Q6_K && rpw > kTileRows) || rpw > 2 * kTileRows ? kTileRows : rpw, wgs = (rows + rw - 1) / rw;
     if (cols > kRowsWaves * kGroupCols && !(T == Q6_K && NP == 8))   // several groups per wavefront (one tile per CU)
         hipLaunchKernelGGL((smalln_rows<T, 1, NP, !(T == Q6_K && NP == 8)>), dim3(wgs), dim3(64 * kRowsWaves), (rows_lds<1, NP>()), s, w,
                            x, y, rows, cols, n, rw);
@@ -1140,8 +1144,9 @@ hipError_t launch_tokens(const uint8_t *w, const float *x, float *y, int rows, i
 }  // namespace
 
 // Batches of 2..8 on the row-balanced kernel: Q4_K, Q4_0, Q8_0 and Q6_K rows
-// in whole 256-column groups, up to two 32-row tiles per CU (one where a
-// wavefront has more than one group, and for Q6_K).
+// in whole 256-column groups. Rows of up to 4096 columns take any row count
+// (past two tiles per CU, one for Q6_K: one workgroup per tile); wider rows,
+// where a wavefront has several groups, up to one tile per CU.
 bool smalln_rows_supported(unsigned type, int rows, int cols, int batch)
 {
     if (type != Q4_K && type != Q4_0 && type != Q8_0 && type != Q6_K) return false;
@@ -1151,7 +1156,7 @@ bool smalln_rows_supported(unsigned type, int rows, int cols, int batch)
     // launches of four measured slower than the tile kernel).
     const bool wide = cols > kRowsWaves * kGroupCols;
     if (type == Q6_K && wide && batch > 4) return false;
-    return rows_per_workgroup(rows) <= (wide || type == Q6_K ? 1 : 2) * kTileRows;
+    return !wide || rows_per_workgroup(rows) <= kTileRows;
 }
 
 hipError_t launch_smalln_rows(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,

@@ -84,9 +84,10 @@ ROWS_TYPES = [Q4_0, Q8_0, Q4_K]
 
 
 @pytest.mark.parametrize("t", ROWS_TYPES, ids=lambda t: TYPE_NAMES[t])
-@pytest.mark.parametrize("rows,cols", [(200, 4096), (9000, 1024), (40, 256), (16384, 512), (72, 11008)],
+@pytest.mark.parametrize("rows,cols", [(200, 4096), (9000, 1024), (40, 256), (16384, 512), (72, 11008),
+                                       (20000, 256)],
                          ids=["partial-tile", "two-virtual-tiles-ragged", "one-group", "two-virtual-tiles",
-                              "groups-per-wave"])
+                              "groups-per-wave", "tile-per-workgroup"])
 def test_rows_kernel_against_oracle(hip, oracle, t, rows, cols):
     """The row-balanced small-N kernel (activation digits made in the kernel,
     one exponent per token and 256-column group) under the reference
@@ -104,8 +105,8 @@ def test_rows_kernel_against_oracle(hip, oracle, t, rows, cols):
     assert np.array_equal(run(hip, w, t, rows, cols, x[:3], 3), y[:3])
 
 
-@pytest.mark.parametrize("rows,cols", [(200, 4096), (40, 256), (72, 11008)],
-                         ids=["partial-tile", "one-group", "groups-per-wave"])
+@pytest.mark.parametrize("rows,cols", [(200, 4096), (40, 256), (72, 11008), (9000, 512)],
+                         ids=["partial-tile", "one-group", "groups-per-wave", "tile-per-workgroup"])
 def test_rows_kernel_q6k_against_oracle(hip, oracle, rows, cols):
     """Q6_K on the row kernel (each lane half with its own 16-column
     scales; rows wider than 4096 columns up to four tokens) under the

@@ -637,12 +637,10 @@ hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int
         const int ng = groups - g0 < kChunkCols / kGroupCols ? groups - g0 : kChunkCols / kGroupCols;
         const float *xc = x + (size_t)g0 * kGroupCols;
         const size_t lds = matvec_lds(ng * kGroupCols);
-        // One tile per CU: a second ring stage only where a wavefront has
-        // more than one group (a repeated stage would stream its group
-        // twice). Q6_K (37-register stages): one stage per wavefront (two
-        // or three stages at eight wavefronts measured 13-17 % slower on
-        // 4096 x 14336); two tiles per CU take eight wavefronts of up to
-        // 256 registers.
+        // Q6_K (37-register stages): one stage per wavefront (two or three
+        // stages at eight wavefronts measured 13-17 % slower on 4096 x
+        // 14336); two tiles per CU take eight wavefronts of up to 256
+        // registers.
         if constexpr (T == Q6_K) {
             if (rw <= kTileRows && rpw > 2 * kTileRows)   // one tile per workgroup (128256 x 4096: 84.7 -> 72.5 us)
                 hipLaunchKernelGGL((matvec_rows<T, 1, 1, 8>), dim3(wgs), dim3(512), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
@@ -651,9 +649,10 @@ hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int
             else
                 hipLaunchKernelGGL((matvec_rows<T, 2, 1, 8>), dim3(wgs), dim3(512), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
         } else {
-            if (rw <= kTileRows && ng > 16)
-                hipLaunchKernelGGL((matvec_rows<T, 1, 2, 16>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
-            else if (rw <= kTileRows)
+            // One stage per wavefront also where it has several groups
+            // (two stages measured 2-10 % slower on 4096 x 11008 and
+            // 4096 x 14336).
+            if (rw <= kTileRows)
                 hipLaunchKernelGGL((matvec_rows<T, 1, 1, 16>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
             else
                 hipLaunchKernelGGL((matvec_rows<T, 2, 1, 16>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);

@@ -962,7 +962,7 @@ __device__ __forceinline__ void group_dots_tokens(float (&y)[VT][(kTokAcc<T, NP>
     }
 }
 
-template <unsigned T, int VT, int NP, bool LOOP, bool FULL>
+template <unsigned T, int VT, int NP, bool LOOP, int KS, bool FULL>
 __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, const float *__restrict__ x,
     float *__restrict__ y, int rows, int cols, int n, int base, int live, uint8_t *lds)
 {
@@ -987,7 +987,7 @@ __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, 
     // wavefront's quantization waits for another's weights. Tokens past n
     // read zeros (buffer range check).
     // This wave's groups: wave + 16 k for k < ns (one slot, reused).
-    const int ns = wave < groups ? (groups - wave + kRowsWaves - 1) / kRowsWaves : 0;
+    const int ns = wave < groups ? (groups - wave + KS - 1) / KS : 0;
     const int vx = 4 * (lane / L) * cols + 16 * (lane % L);
     float4 px[NP];
     auto load_x = [&](int g) {
@@ -1045,8 +1045,8 @@ __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, 
             load_rows<T, FULL>(st[0], wb, vq, vs, R, wave, vd, groups);
             for (int k = 0; k < ns; ++k) {
                 if (k > 0) {
-                    load_x(wave + kRowsWaves * k);
-                    load_rows<T, FULL>(st[0], wb, vq, vs, R, wave + kRowsWaves * k, vd, groups);
+                    load_x(wave + KS * k);
+                    load_rows<T, FULL>(st[0], wb, vq, vs, R, wave + KS * k, vd, groups);
                 }
                 quantize_tokens<T == Q4_K, NP>(px, lane, slot);
                 // Each wave reads back only its own slot (and rewrites it
@@ -1075,7 +1075,7 @@ __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, 
     if (i >= VT * 256) return;
     const int v = i >> 8, t = (i >> 5) & 7, r = i & 31;
     if (t >= n || kTileRows * v + r >= live) return;
-    const int nw = groups < kRowsWaves ? groups : kRowsWaves;
+    const int nw = groups < KS ? groups : KS;
     float s = 0.f;
     if constexpr (T == Q6_K) {
         // Every lane holds every token: its lane half's columns.
@@ -1087,27 +1087,27 @@ __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, 
     y[(size_t)t * rows + base + kTileRows * v + r] = s;
 }
 
-template <unsigned T, int VT, int NP, bool LOOP>
-__global__ __launch_bounds__(64 * kRowsWaves) void smalln_rows(const uint8_t *__restrict__ w,
+template <unsigned T, int VT, int NP, bool LOOP, int KS = kRowsWaves>
+__global__ __launch_bounds__(64 * KS) void smalln_rows(const uint8_t *__restrict__ w,
     const float *__restrict__ x, float *__restrict__ y, int rows, int cols, int n, int rw)
 {
     extern __shared__ __align__(16) uint8_t lds[];
     const int base = blockIdx.x * rw, live = rows - base < rw ? rows - base : rw;
     const int tiles = (rows + kTileRows - 1) / kTileRows;
     if (rows % kTileRows == 0 || base + live <= kTileRows * (tiles - 1))
-        smalln_rows_body<T, VT, NP, LOOP, true>(w, x, y, rows, cols, n, base, live, lds);
+        smalln_rows_body<T, VT, NP, LOOP, KS, true>(w, x, y, rows, cols, n, base, live, lds);
     else
-        smalln_rows_body<T, VT, NP, LOOP, false>(w, x, y, rows, cols, n, base, live, lds);
+        smalln_rows_body<T, VT, NP, LOOP, KS, false>(w, x, y, rows, cols, n, base, live, lds);
 }
 
 // LDS of one smalln_rows workgroup: the wavefront slots, or the reduction
 // array [wave][VT][NP or NP / 2][64] floats that reuses them, whichever is
 // larger.
-template <int VT, int NP>
+template <int VT, int NP, int KS = kRowsWaves>
 constexpr size_t rows_lds()
 {
-    const size_t slots = (size_t)RowsSlot<NP>::kBytes * kRowsWaves;
-    const size_t red = (size_t)kRowsWaves * VT * NP * 64 * 4;
+    const size_t slots = (size_t)RowsSlot<NP>::kBytes * KS;
+    const size_t red = (size_t)KS * VT * NP * 64 * 4;
     return slots > red ? slots : red;
 }
 
@@ -1119,7 +1119,16 @@ hipError_t launch_tokens_np(const uint8_t *w, const float *x, float *y, int rows
     // 57344 x 4096 N=2 33 -> 24 us against the tile kernel).
     const int rpw = rows_per_workgroup(rows);
     const int rw = (T == Q6_K && rpw > kTileRows) || rpw > 2 * kTileRows ? kTileRows : rpw, wgs = (rows + rw - 1) / rw;
-    if (cols > kRowsWaves * kGroupCols && !(T == Q6_K && NP == 8))   // several groups per wavefront (one tile per CU)
+    if constexpr (T == Q6_K && NP == 8) {
+        if (cols > kRowsWaves * kGroupCols) {
+            // Wide Q6_K rows at eight slots: eight wavefronts of up to 256
+            // registers (sixteen of 128 would spill).
+            hipLaunchKernelGGL((smalln_rows<T, 1, NP, true, 8>), dim3(wgs), dim3(512), (rows_lds<1, NP, 8>()), s, w, x,
+                               y, rows, cols, n, rw);
+            return hipGetLastError();
+        }
+    }
+    if (cols > kRowsWaves * kGroupCols)   // several groups per wavefront (one tile per CU)
         hipLaunchKernelGGL((smalln_rows<T, 1, NP, !(T == Q6_K && NP == 8)>), dim3(wgs), dim3(64 * kRowsWaves), (rows_lds<1, NP>()), s, w,
                            x, y, rows, cols, n, rw);
     else if (T == Q6_K || rw <= kTileRows)
@@ -1154,7 +1163,6 @@ bool smalln_rows_supported(unsigned type, int rows, int cols, int batch)
     // groups per wavefront at most four token slots (eight would spill; two
     // launches of four measured slower than the tile kernel).
     const bool wide = cols > kRowsWaves * kGroupCols;
-    if (type == Q6_K && wide && batch > 4) return false;
     return !wide || rows_per_workgroup(rows) <= kTileRows;
 }
 

@@ -74,7 +74,7 @@ def test_queries(kernels):
     assert kernels.kernel_name(Q4_K, 14336, 8192, 8) == "smalln_mfma"          # that, at two tiles per CU
     assert kernels.kernel_name(Q6_K, 4096, 4096, 8) == "smalln_rows"
     assert kernels.kernel_name(Q6_K, 14336, 4096, 8) == "smalln_rows"          # one workgroup per tile
-    assert kernels.kernel_name(Q6_K, 4096, 14336, 8) == "smalln_mfma"          # wide Q6_K rows, above four tokens
+    assert kernels.kernel_name(Q6_K, 4096, 14336, 8) == "smalln_rows"          # wide Q6_K rows: eight wavefronts
     assert kernels.kernel_name(Q6_K, 4096, 14336, 1) == "matvec_rows"
     assert kernels.kernel_name(Q6_K, 128256, 4096, 1) == "matvec_rows"         # one tile per workgroup
 

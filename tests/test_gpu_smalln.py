@@ -109,16 +109,14 @@ def test_rows_kernel_against_oracle(hip, oracle, t, rows, cols):
                          ids=["partial-tile", "one-group", "groups-per-wave", "tile-per-workgroup"])
 def test_rows_kernel_q6k_against_oracle(hip, oracle, rows, cols):
     """Q6_K on the row kernel (each lane half with its own 16-column
-    scales; rows wider than 4096 columns up to four tokens) under the
-    contract bound, tokens spanning 2^-40 .. 2^44."""
+    scales; rows wider than 4096 columns at eight slots on eight wavefronts)
+    under the contract bound, tokens spanning 2^-40 .. 2^44."""
     t = Q6_K
-    wide = cols > 4096
-    assert hip[1].kernel_name(t, rows, cols, 4 if wide else 8) == "smalln_rows"
-    assert hip[1].kernel_name(t, rows, cols, 8) == ("smalln_mfma" if wide else "smalln_rows")
+    assert hip[1].kernel_name(t, rows, cols, 8) == "smalln_rows"
     w = synth.weights(t, rows, cols, 700)
     x = synth.activations(8, cols, 701)
     x *= np.float32(2.0) ** np.arange(-40, 56, 12, dtype=np.float32)[:, None]
-    for batch in ((4, 3) if wide else (8, 3)):
+    for batch in (8, 3):
         y = run(hip, w, t, rows, cols, x[:batch], batch)
         for k in range(batch):
             check_rows(oracle, w, t, x[k], rows, cols, y[k])

@@ -116,6 +116,16 @@ __device__ __forceinline__ uint32_t pack_byte(uint32_t w0, uint32_t w1, uint32_t
     return __builtin_amdgcn_perm(w1, w0, sel) | __builtin_amdgcn_perm(w3, w2, sel) << 16;
 }
 
+// Workgroups are dispatched round-robin over the eight XCDs: block b runs on
+// XCD b % 8. Renumbered so that each XCD's blocks take one contiguous eighth
+// of the rows (measured 1-6 % faster on 14336 x 4096 N=8 and the 128256-row
+// Q6_K matvec; results are unchanged).
+__device__ __forceinline__ int xcd_block()
+{
+    const int nb = gridDim.x, b = blockIdx.x;
+    return nb % 8 ? b : (b % 8) * (nb / 8) + b / 8;
+}
+
 // Workgroup barrier that waits for no memory access: the empty asm keeps the
 // compiler from moving loads across it, so it orders the issue of the loads
 // before it ahead of those after it.
@@ -590,7 +600,7 @@ __global__ __launch_bounds__(64 * KS) void matvec_rows(const uint8_t *__restrict
     const int ccols = (g0c + ngc) * kGroupCols < cols ? ngc * kGroupCols : cols - g0c * kGroupCols;
     uint8_t *sdig = lds;                                              // [xgroup][4 slots][32 B]
     float4 *smeta = (float4 *)(lds + (size_t)128 * (ccols / 32));     // [xgroup]
-    const int base = blockIdx.x * rw, live = rows - base < rw ? rows - base : rw;
+    const int base = xcd_block() * rw, live = rows - base < rw ? rows - base : rw;
     // Every lane of the workgroup in a 32-row tile (only the last tile of the
     // matrix may be shorter): group and field offsets are scalar.
     const int tiles = (rows + kTileRows - 1) / kTileRows;
@@ -1092,7 +1102,7 @@ __global__ __launch_bounds__(64 * KS) void smalln_rows(const uint8_t *__restrict
     const float *__restrict__ x, float *__restrict__ y, int rows, int cols, int n, int rw)
 {
     extern __shared__ __align__(16) uint8_t lds[];
-    const int base = blockIdx.x * rw, live = rows - base < rw ? rows - base : rw;
+    const int base = xcd_block() * rw, live = rows - base < rw ? rows - base : rw;
     const int tiles = (rows + kTileRows - 1) / kTileRows;
     if (rows % kTileRows == 0 || base + live <= kTileRows * (tiles - 1))
         smalln_rows_body<T, VT, NP, LOOP, KS, true>(w, x, y, rows, cols, n, base, live, lds);

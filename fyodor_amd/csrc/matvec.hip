@@ -1169,9 +1169,9 @@ bool smalln_rows_supported(unsigned type, int rows, int cols, int batch)
 {
     if (type != Q4_K && type != Q4_0 && type != Q8_0 && type != Q6_K) return false;
     if (batch < 2 || batch > 8 || cols % kGroupCols) return false;
-    // Q6_K stages (37 registers): one virtual tile, and on rows of several
-    // groups per wavefront at most four token slots (eight would spill; two
-    // launches of four measured slower than the tile kernel).
+    // Rows of several 256-column groups per wavefront loop over the groups
+    // with one virtual tile per workgroup (two would spill); past 32 rows per
+    // CU such matrices run faster on the tile kernel.
     const bool wide = cols > kRowsWaves * kGroupCols;
     return !wide || rows_per_workgroup(rows) <= kTileRows;
 }

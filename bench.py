@@ -113,49 +113,80 @@ def time_steps(rt, kern, stream, weights, x_dev, y_dev, batch, steps, warmup, mo
     return ms / steps
 
 
+def host_cpu() -> tuple:
+    """CPU model name and the SIMD path the reference provider selects on it
+    (backend/core/cpu_kernels.c:91-100: AVX-512 F+BW, else AVX2+F16C, else
+    scalar)."""
+    model, flags = "unknown", set()
+    try:
+        for line in open("/proc/cpuinfo"):
+            key, _, value = line.partition(":")
+            if key.strip() == "model name" and model == "unknown":
+                model = value.strip()
+            elif key.strip() == "flags" and not flags:
+                flags = set(value.split())
+    except OSError:
+        pass
+    if {"avx2", "f16c"} <= flags:
+        return model, "avx512" if {"avx512f", "avx512bw"} <= flags else "avx2"
+    return model, "scalar"
+
+
 def cpu_baseline(weights_host: np.ndarray, x: np.ndarray, y_gpu: np.ndarray, seconds: float) -> dict:
-    """The reference CPU provider (or the C port) on the same workload."""
+    """The reference CPU provider (or the C port) on the same workload, at
+    the host's thread count and at one thread."""
     sys.path.insert(0, str(REPO))
     from oracle import Oracle, Reference  # the checker; only this leg uses it
 
     threads = min(len(os.sched_getaffinity(0)), 16)
-    os.environ["NYA_CPU_THREADS"] = str(threads)
     copies = [weights_host] + [weights_host.copy() for _ in range(3)]  # > any L3
     y = np.empty(ROWS, dtype=np.float32)
-    times = []
-    if Reference.available():
-        ref = Reference()
-        ctx = ref.cpu_provider()
-        kind = "reference"
+    kind = "reference" if Reference.available() else "port"
+    ref = Reference() if kind == "reference" else None
+    orc = None if ref else Oracle()
 
-        def run(w):
-            ref.provider_matmul(ctx, w, Q4_K, x, ROWS, COLS, 1, y)
-    else:
-        orc = Oracle()
-        kind, ctx = "port", None
+    def leg(n: int, budget: float, cap: int):
+        """Median seconds per matvec on n threads and the output of the first."""
+        ctx = None
+        if ref:
+            # The provider reads its thread count when created
+            # (backend/core/cpu_backend.c:147-151).
+            os.environ["NYA_CPU_THREADS"] = str(n)
+            ctx = ref.cpu_provider()
 
-        def run(w):
-            y[:] = orc.matmul(w, Q4_K, x, ROWS, COLS, 1, threads=threads)[0]
-    run(copies[0])
-    parity = float(np.linalg.norm(y_gpu.astype(np.float64) - y) / np.linalg.norm(y.astype(np.float64)))
-    run(copies[1])
-    began = time.perf_counter()
-    i = 0
-    while (time.perf_counter() - began < seconds or len(times) < 5) and len(times) < 5000:
-        t0 = time.perf_counter()
-        run(copies[i % len(copies)])
-        times.append(time.perf_counter() - t0)
-        i += 1
-    if ctx is not None:
-        ref.free(ctx)
-    med = float(np.median(times))
-    gbs = algorithmic_bytes(ROWS, COLS, 1) / med / 1e9
+            def run(w):
+                ref.provider_matmul(ctx, w, Q4_K, x, ROWS, COLS, 1, y)
+        else:
+            def run(w):
+                y[:] = orc.matmul(w, Q4_K, x, ROWS, COLS, 1, threads=n)[0]
+        run(copies[0])
+        first = y.copy()
+        run(copies[1])
+        times, i, began = [], 0, time.perf_counter()
+        while (time.perf_counter() - began < budget or len(times) < 5) and len(times) < cap:
+            t0 = time.perf_counter()
+            run(copies[i % len(copies)])
+            times.append(time.perf_counter() - t0)
+            i += 1
+        if ctx is not None:
+            ref.free(ctx)
+        return float(np.median(times)), len(times), first
+
+    med, count, y_cpu = leg(threads, seconds, 5000)
+    med1, count1, _ = leg(1, seconds / 4, 200)
+    parity = float(np.linalg.norm(y_gpu.astype(np.float64) - y_cpu) / np.linalg.norm(y_cpu.astype(np.float64)))
+    model, isa = host_cpu()
+    nbytes = algorithmic_bytes(ROWS, COLS, 1)
     return {
-        "value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": kind,
-        "sample": f"{len(times)} Q4_K 14336x4096 N=1 matvecs over 4 rotating host copies of the same "
+        "value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": kind,
+        "sample": f"{count} Q4_K 14336x4096 N=1 matvecs over 4 rotating host copies of the same "
                   f"synthetic weights, median time {med * 1e3:.3f} ms"
                   + (" (reference backend/core/cpu_backend.c provider, NYA_CPU_THREADS)" if kind == "reference"
                      else " (scalar C port, rows split over threads)"),
+        "one_thread": {"value": round(nbytes / med1 / 1e9, 2), "unit": "GB/s",
+                       "sample": f"{count1} matvecs of the same workload, median time {med1 * 1e3:.3f} ms"},
+        "isa": isa if kind == "reference" else "scalar",
+        "cpu_model": model,
         "parity_rel_l2_vs_gpu": parity,
     }
 

@@ -113,6 +113,33 @@ def time_steps(rt, kern, stream, weights, x_dev, y_dev, batch, steps, warmup, mo
     return ms / steps
 
 
+def call_latency(kern, rt, stream, weights, x_dev, y_dev, host_w: np.ndarray, x_host: np.ndarray,
+                 calls: int = 200) -> dict:
+    """Wall time of single N=1 calls, each waited for, at the two boundaries:
+    nya_hip_matmul on device buffers plus a stream synchronize, and the
+    provider's matvec on host buffers (rocm/rocm.c:111-139: x up, kernel,
+    y down, synchronize) with the weights already in its cache."""
+    abi = []
+    for i in range(calls + 5):
+        t0 = time.perf_counter()
+        kern.matmul(weights[i % len(weights)], Q4_K, ROWS, COLS, x_dev, y_dev, 1, 0, 0, stream)
+        rt.sync(stream)
+        abi.append(time.perf_counter() - t0)
+    from fyodor_amd import Compute
+    host = []
+    with Compute("rocm") as c:
+        c.matvec_typed(host_w, ROWS, COLS, Q4_K, x_host)          # uploads the packed weights once
+        for _ in range(calls + 5):
+            t0 = time.perf_counter()
+            c.matvec_typed(host_w, ROWS, COLS, Q4_K, x_host)
+            host.append(time.perf_counter() - t0)
+    med_abi, med_host = float(np.median(abi[5:])), float(np.median(host[5:]))
+    return {"abi_us": round(med_abi * 1e6, 2), "provider_host_us": round(med_host * 1e6, 2),
+            "provider_host_GBps": round(algorithmic_bytes(ROWS, COLS, 1) / med_host / 1e9, 2),
+            "sample": f"median of {calls} N=1 calls of each, one at a time; the ABI calls rotate over the "
+                      f"{len(weights)} weight copies, the provider reuses its one cached copy"}
+
+
 def host_cpu() -> tuple:
     """CPU model name and the SIMD path the reference provider selects on it
     (backend/core/cpu_kernels.c:91-100: AVX-512 F+BW, else AVX2+F16C, else
@@ -318,6 +345,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--launch", choices=["graph", "stream"], default="graph")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-call-latency", action="store_true",
+                    help="skip the per-call wall times at the C-ABI and provider boundaries")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only the plain 256 MiB device copy used to calibrate HBM byte counters")
@@ -398,6 +427,8 @@ def main() -> int:
                "frac": round(gbs8 / PEAK_HBM_GBS, 4), "algorithmic_bytes": bytes8, "traffic": measured_traffic(8),
                "kernel": kern.kernel_name(Q4_K, ROWS, COLS, 8)},
     }
+    if not args.no_call_latency:
+        line["call_latency"] = call_latency(kern, rt, stream, weights, x_dev, y_dev, host_w, x8[0].copy())
     if args.prefill_steps > 0:
         line["prefill"] = prefill(rt, kern, stream, weights, host_w, args.prefill_steps)
     if not args.no_cpu_baseline:

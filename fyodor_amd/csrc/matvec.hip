@@ -9,15 +9,21 @@
 // the low mantissa bits, whose bytes are the digits. Block dot products
 // sum q * a_d are exact in int32.
 //
-// One token leaves most of an MFMA's 32 A-rows empty. Instead of one MFMA
-// result per 32-column block, the eight blocks of a 256-column group share ONE
-// accumulator: block k's digits sit in A-rows 4k .. 4k+2 (every other A-row of
-// that MFMA reads zeros), and the eight v_mfma_i32_32x32x32_i8 of a group
-// chain through the accumulator. D lane l, register r holds A-row
-// 8(r/4) + 4(l/32) + r%4 for weight row l%32, so after the chain lane half h
-// holds blocks 2m + h (m = 0..3) in registers 4m .. 4m+2 and every epilogue
-// instruction serves two blocks. The A operand of block k is read from LDS at
-// a per-lane address fixed for the whole kernel.
+// One token leaves most of an MFMA's A-rows empty, so each block takes the
+// cheapest MFMA that still reads its whole 1 KiB weight operand as loaded:
+// v_mfma_i32_16x16x64_i8 (half the cycles of v_mfma_i32_32x32x32_i8). Its B
+// lane l holds column n = l%16 with K-chunk c = l/16; the weight load gives
+// lane l row l%32 and column half l/32 of a 32-column block, so chunk c
+// carries row half c%2 and column half c/2. A-rows 8 bsel + 4 rh + d hold
+// digit d of x in the chunks of row half rh only (zeros elsewhere), so D rows
+// 8 bsel + 4 rh .. +2 are the digit sums of rows 16 rh + n; blocks 2m and
+// 2m + 1 chain through accumulator m as bsel = 0, 1. D lane l, register i
+// holds D row 4(l/16) + i, column l%16, i.e. row l%32 of the weight tile and
+// block 2m + l/32: lane half h holds blocks 2m + h (m = 0..3) in registers
+// 0..2 of accumulator m and every epilogue instruction serves two blocks.
+// The A operand of block k is read from LDS at a per-lane address fixed for
+// the whole kernel. (Q6_K, whose lane halves carry different 16-column
+// scales, keeps v_mfma_i32_32x32x32_i8; see aoff6_of.)
 //
 // Weights, as the reference decodes them (backend/core/llm_quant.c:70-142).
 // Q4_K and Q4_0 bytes hold element l of blocks 2p (low nibble) and 2p + 1
@@ -41,24 +47,19 @@ namespace {
 constexpr int kChunkCols = 16384;   // columns per launch (bounds the LDS copy of x)
 constexpr int kMetaBytes = 16;      // per 32-column block: {s, c, sum x, 0}
 
-// A-operand byte offsets within a group's 1 KiB of digits, per lane and
-// block k: lane l supplies A-row l%32 = 4 kl + dd and K-half h = l/32; it is
-// live for block kl's digit dd < 3 and reads slot 3 (zero) of every other
-// block.
-struct AoffTable {
-    int v[64][8];
-};
-constexpr AoffTable make_aoff()
+// A-operand byte offsets within a group's 1 KiB of digits (digit slot d of
+// block k at 128 k + 32 d, column half at + 16, slot 3 zero), per lane and
+// block k = 2m + bsel of the 16x16x64 chain: lane l supplies A-row
+// l%16 = 8 b + 4 rh + d for K-chunk c = l/16; it is live for its own bsel,
+// row half c%2 == rh and digit d < 3, and reads the zero slot otherwise.
+// Computed in registers (a few instructions per lane, no memory access before
+// the weight loads).
+__device__ __forceinline__ int aoff_of(int l, int k)
 {
-    AoffTable t{};
-    for (int l = 0; l < 64; ++l)
-        for (int k = 0; k < 8; ++k) {
-            const int kl = (l & 31) >> 2, dd = l & 3;
-            t.v[l][k] = 128 * k + 16 * (l >> 5) + 32 * (kl == k && dd < 3 ? dd : 3);
-        }
-    return t;
+    const int m = l & 15, c = l >> 4, b = m >> 3, rh = (m >> 2) & 1, d = m & 3;
+    const bool live = b == (k & 1) && (c & 1) == rh && d < 3;
+    return 128 * k + 16 * (c >> 1) + 32 * (live ? d : 3);
 }
-__constant__ AoffTable kAoff = make_aoff();
 
 // Q6_K: lane half h of MFMA block j = 4c + j' (unit p = 2c + j'/2, nibble
 // m = j'%2) holds columns 16 (j'/2) .. +15 of x-block 4c + 2m + h, which has
@@ -66,19 +67,13 @@ __constant__ AoffTable kAoff = make_aoff();
 // four-block chain sits in A-rows 8j' + 4h + d, digit d < 3 in K-half h only,
 // so D lane half h holds its own half's sums (registers 4j' .. 4j'+2) and
 // each group takes two chains (c = 0, 1).
-constexpr AoffTable make_aoff6()
+__device__ __forceinline__ int aoff6_of(int l, int j)
 {
-    AoffTable t{};
-    for (int l = 0; l < 64; ++l)
-        for (int j = 0; j < 8; ++j) {
-            const int h = l >> 5, jr = (l & 31) >> 3, hr = ((l & 31) >> 2) & 1, dd = l & 3;
-            const int c = j >> 2, jp = j & 3, xb = 4 * c + 2 * (jp & 1) + h;
-            const bool live = jr == jp && hr == h && dd < 3;
-            t.v[l][j] = 128 * xb + 32 * (live ? dd : 3) + 16 * (jp >> 1);
-        }
-    return t;
+    const int h = l >> 5, jr = (l & 31) >> 3, hr = ((l & 31) >> 2) & 1, dd = l & 3;
+    const int c = j >> 2, jp = j & 3, xb = 4 * c + 2 * (jp & 1) + h;
+    const bool live = jr == jp && hr == h && dd < 3;
+    return 128 * xb + 32 * (live ? dd : 3) + 16 * (jp >> 1);
 }
-__constant__ AoffTable kAoff6 = make_aoff6();
 
 template <int CTRL>
 __device__ __forceinline__ float dppf(float v)
@@ -240,7 +235,7 @@ __device__ __forceinline__ void group_dots(float (&part)[VT], const MvStage<T> (
     const uint8_t *__restrict__ a, const int (&aoff)[8], const float4 *__restrict__ mt, int h)
 {
     if constexpr (T == Q6_K) {
-        // Two chains of four blocks (see kAoff6); lane half h's block j' of
+        // Two chains of four blocks (see aoff6_of); lane half h's block j' of
         // chain c reads x-block 4c + 2 (j'%2) + h and the scale
         // sc[8c + 2 q + j'/2] with q = 2 (j'%2) + h.
 #pragma unroll
@@ -270,21 +265,24 @@ __device__ __forceinline__ void group_dots(float (&part)[VT], const MvStage<T> (
             part[v] = f16_to_f32(w[v].d & 0xFFFFu) * sum;
         }
     } else {
-        // One tile at a time: its chain, then its epilogue (one accumulator
-        // live).
+        // One tile at a time: its four two-block chains, then its epilogue.
 #pragma unroll
         for (int v = 0; v < VT; ++v) {
-            i32x16 D = {};
+            i32x4 D[4];
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
-                D = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const i32x4 *)(a + aoff[k]), block_b<T>(w[v], k), D, 0, 0, 0);
+            for (int m = 0; m < 4; ++m) {
+                D[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(*(const i32x4 *)(a + aoff[2 * m]), block_b<T>(w[v], 2 * m),
+                                                             (i32x4){0, 0, 0, 0}, 0, 0, 0);
+                D[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(*(const i32x4 *)(a + aoff[2 * m + 1]),
+                                                             block_b<T>(w[v], 2 * m + 1), D[m], 0, 0, 0);
+            }
             // Lane half h: blocks 2m + h.
             float sum_s = 0.f, sum_m = 0.f;
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 const float4 md = mt[2 * m];
                 // Sums reach 2^34: the top digit joins in float.
-                const float G = __builtin_fmaf((float)D[4 * m + 2], 65536.f, (float)(D[4 * m + 1] * 256 + D[4 * m]));
+                const float G = __builtin_fmaf((float)D[m][2], 65536.f, (float)(D[m][1] * 256 + D[m][0]));
                 const float t = __builtin_fmaf(G, md.x, md.y);
                 if constexpr (T == Q4_K) {
                     // Slice word m packs sc and m of blocks 2m (bits 0..11) and
@@ -324,14 +322,15 @@ __device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, int voff, int
 }
 
 // Weights of group g of the tile (buffer r over the tile): q[p] at
-// 32R p + 16R h + 16 r, slices at 128R + 16 r. The lane part (vq, vs) stays
-// in vector registers, the group part in scalar offsets.
+// 32R p + 16R h + 16 r, slices at 128R + 16 r. The group offset joins the
+// vector offset, which the buffer range check covers: groups past the tile
+// (the ring's last stages) read zeros.
 __device__ __forceinline__ void load_q4k(MvStage<Q4_K> &w, __amdgpu_buffer_rsrc_t tile, int R, int g, int vq, int vs)
 {
     const int base = 144 * R * g;
 #pragma unroll
-    for (int p = 0; p < 4; ++p) w.q[p] = bload16<true>(tile, vq, base + 32 * R * p);
-    w.sl = bload16<true>(tile, vs, base + 128 * R);
+    for (int p = 0; p < 4; ++p) w.q[p] = bload16<true>(tile, vq + base, 32 * R * p);
+    w.sl = bload16<true>(tile, vs + base, 128 * R);
 }
 
 // One workgroup per 32-row tile, KS wavefronts splitting its groups
@@ -359,12 +358,12 @@ __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int vq = 16 * R * h + 16 * r, vs = 16 * r, vx = 16 * lane;
     // This wave's chunk groups: wave + KS k for k < ns.
     const int ns = wave < ngc ? (ngc - wave + KS - 1) / KS : 0;
-    auto xload = [&](int gl) { return __builtin_bit_cast(float4, bload16<false>(xb, vx, 1024 * gl)); };
+    // The group goes into the vector offset, which the buffer range check
+    // covers (the scalar offset is added after the check).
+    auto xload = [&](int gl) { return __builtin_bit_cast(float4, bload16<false>(xb, vx + 1024 * gl, 0)); };
 
-    // 1. The A-operand offset table and x of the first RING groups, then
-    //    the weights (loads complete in order: what the quantization needs
-    //    comes first).
-    int4 ao0 = ((const int4 *)kAoff.v[lane])[0], ao1 = ((const int4 *)kAoff.v[lane])[1];
+    // 1. x of the first RING groups, then the weights (loads complete in
+    //    order: what the quantization needs comes first).
     float4 px[RING];
     // Unconditional: past the chunk the buffer range check returns zeros.
 #pragma unroll
@@ -373,8 +372,6 @@ __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) vo
     MvStage<Q4_K> st[RING];
 #pragma unroll
     for (int k = 0; k < RING; ++k) load_q4k(st[k], tile, R, g0c + wave + KS * k, vq, vs);
-    asm volatile("" : "+v"(ao0.x), "+v"(ao0.y), "+v"(ao0.z), "+v"(ao0.w), "+v"(ao1.x), "+v"(ao1.y), "+v"(ao1.z),
-                 "+v"(ao1.w) :: "memory");
 
     // 2. Digits of this wave's groups into LDS.
     const float fmul = block_factor<Q4_K>(lane), fcorr = block_correction<Q4_K>(lane);
@@ -391,7 +388,9 @@ __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) vo
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // 3. A-operand offsets (per lane, fixed for the kernel; loaded with x).
-    int aoff[8] = {ao0.x, ao0.y, ao0.z, ao0.w, ao1.x, ao1.y, ao1.z, ao1.w};
+    int aoff[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) aoff[k] = aoff_of(lane, k);
     const uint8_t *abase = sdig + 1024 * wave;
     const float4 *mbase = smeta + 8 * wave + h;
 
@@ -481,8 +480,10 @@ __device__ __forceinline__ void load_rows(MvStage<T> &w, __amdgpu_buffer_rsrc_t 
 // same bytes whatever the row count. Wavefront w takes chunk groups
 // w, w + 16, ... of all VT tiles: it reads and quantizes only those groups of
 // x (no barrier before the dots), and each A operand it reads from LDS serves
-// the VT tiles' interleaved MFMA chains.
-template <unsigned T, int VT, int RING, int KS, bool FULL>
+// the VT tiles' interleaved MFMA chains. MULTI: some wavefront has more
+// groups than ring stages (rows wider than KS RING groups); without it the
+// ring is never refilled and that code is left out (it costs registers).
+template <unsigned T, int VT, int RING, int KS, bool FULL, bool MULTI>
 __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, const float *__restrict__ x,
     float *__restrict__ y, int rows, int cols, int base, int live, int g0c, int ngc, int accumulate,
     uint8_t *sdig, float4 *smeta, float (*red)[VT][64])
@@ -514,20 +515,18 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
 #pragma unroll
     for (int v = 0; v < VT; ++v) acc[v] = 0.f;
     auto gl_of = [&](int k) { return wave + KS * (k < ns ? k : ns - 1); };
-    // 1. The A-operand offset table and x of the first RING groups, then the
-    //    weights (loads complete in order: what the quantization needs comes
-    //    first; the barrier puts every wavefront's x ahead of all weights).
-    //    Stages past the wave's last group repeat it.
-    int4 ao0 = {}, ao1 = {};
+    // 1. x of the first RING groups, then the weights (loads complete in
+    //    order: what the quantization needs comes first; the barrier puts
+    //    every wavefront's x ahead of all weights). Stages past the wave's
+    //    last group repeat it. The x loads are unconditional, with the group
+    //    in the range-checked vector offset (a wave without groups reads
+    //    zeros): loaded under a condition, their registers would be merged
+    //    after it, and the merge waits for the loads, holding back every
+    //    weight load behind a full memory round trip.
     float4 px[RING];
-    if (ns > 0) {
-        const AoffTable &table = T == Q6_K ? kAoff6 : kAoff;
-        ao0 = ((const int4 *)table.v[lane])[0];
-        ao1 = ((const int4 *)table.v[lane])[1];
 #pragma unroll
-        for (int k = 0; k < RING; ++k)
-            px[k] = __builtin_bit_cast(float4, bload16<false>(xb, 16 * lane, 1024 * gl_of(k)));
-    }
+    for (int k = 0; k < RING; ++k)
+        px[k] = __builtin_bit_cast(float4, bload16<false>(xb, 16 * lane + 1024 * (ns > 0 ? gl_of(k) : wave), 0));
     issue_barrier();
     if (ns > 0) {
         MvStage<T> st[RING][VT];
@@ -535,8 +534,6 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
         for (int k = 0; k < RING; ++k)
 #pragma unroll
             for (int v = 0; v < VT; ++v) load_rows<T, FULL>(st[k][v], wb, vq[v], vs[v], R[v], g0c + gl_of(k), vd[v], G);
-        asm volatile("" : "+v"(ao0.x), "+v"(ao0.y), "+v"(ao0.z), "+v"(ao0.w), "+v"(ao1.x), "+v"(ao1.y),
-                     "+v"(ao1.z), "+v"(ao1.w) :: "memory");
 
         // 2. Digits of this wave's groups into LDS.
         const float fmul = block_factor<T>(lane), fcorr = block_correction<T>(lane);
@@ -545,9 +542,10 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
             asm volatile("" : "+v"(px[k].x), "+v"(px[k].y), "+v"(px[k].z), "+v"(px[k].w) :: "memory");
             if (k < ns) quantize_group(px[k], gl_of(k), lane, fmul, fcorr, sdig, smeta);
         }
-        for (int k = RING; k < ns; ++k)
-            quantize_group(__builtin_bit_cast(float4, bload16<false>(xb, 16 * lane, 1024 * gl_of(k))), gl_of(k), lane,
-                           fmul, fcorr, sdig, smeta);
+        if constexpr (MULTI)
+            for (int k = RING; k < ns; ++k)
+                quantize_group(__builtin_bit_cast(float4, bload16<false>(xb, 16 * lane, 1024 * gl_of(k))), gl_of(k),
+                               lane, fmul, fcorr, sdig, smeta);
         // Each wave reads back only the groups it wrote.
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -555,7 +553,9 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
 
         // 3. The ring: stage k holds group i + k of every virtual tile; after
         //    computing it, it loads group i + k + RING (while there is one).
-        const int aoff[8] = {ao0.x, ao0.y, ao0.z, ao0.w, ao1.x, ao1.y, ao1.z, ao1.w};
+        int aoff[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) aoff[k] = T == Q6_K ? aoff6_of(lane, k) : aoff_of(lane, k);
         const uint8_t *abase = sdig + 1024 * wave;
         const float4 *mbase = smeta + 8 * wave + h;
         auto pass = [&](int i) {
@@ -567,7 +567,7 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
                     group_dots<T, VT>(part, st[k], abase + 1024 * gl, aoff, mbase + 8 * gl, h);
 #pragma unroll
                     for (int v = 0; v < VT; ++v) acc[v] += part[v];
-                    if (i + k + RING < ns)
+                    if (MULTI && i + k + RING < ns)
 #pragma unroll
                         for (int v = 0; v < VT; ++v)
                             load_rows<T, FULL>(st[k][v], wb, vq[v], vs[v], R[v], g0c + wave + gl + KS * RING, vd[v], G);
@@ -575,23 +575,36 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
             }
         };
         pass(0);
-        for (int i = RING; i < ns; i += RING) pass(i);
+        if constexpr (MULTI)
+            for (int i = RING; i < ns; i += RING) pass(i);
     }
 
-    // 4. Lane halves and wavefronts, in a fixed order.
+    // 4. Lane halves and wavefronts, in a fixed order. Wave 0 sums: lane
+    //    l = 32 v + r takes row r of virtual tile v. All 2 KS partials are
+    //    read before the first add, so the reads cost one LDS round trip
+    //    (read, wait, add in turn measured 0.1 us slower at the end of every
+    //    launch).
 #pragma unroll
     for (int v = 0; v < VT; ++v) red[wave][v][lane] = acc[v];
     __syncthreads();
-    if (wave >= VT || lane >= 32 || kTileRows * wave + lane >= live) return;
-    const int v = wave;
-    float s = red[0][v][lane] + red[0][v][lane + 32];
+    if (wave != 0) return;
+    const int v = lane >> 5, r = lane & 31;
+    if (v >= VT || kTileRows * v + r >= live) return;
+    float p[2 * KS];
 #pragma unroll
-    for (int q = 1; q < KS; ++q) s += red[q][v][lane] + red[q][v][lane + 32];
-    float *dst = y + base + kTileRows * v + lane;
+    for (int q = 0; q < KS; ++q) {
+        p[2 * q] = red[q][v][r];
+        p[2 * q + 1] = red[q][v][r + 32];
+    }
+    asm volatile("" ::: "memory");
+    float s = p[0] + p[1];
+#pragma unroll
+    for (int q = 1; q < KS; ++q) s += p[2 * q] + p[2 * q + 1];
+    float *dst = y + base + kTileRows * v + r;
     *dst = accumulate ? *dst + s : s;
 }
 
-template <unsigned T, int VT, int RING, int KS>
+template <unsigned T, int VT, int RING, int KS, bool MULTI>
 __global__ __launch_bounds__(64 * KS) void matvec_rows(const uint8_t *__restrict__ w, const float *__restrict__ x,
     float *__restrict__ y, int rows, int cols, int rw, int g0c, int ngc, int accumulate)
 {
@@ -605,9 +618,11 @@ __global__ __launch_bounds__(64 * KS) void matvec_rows(const uint8_t *__restrict
     // matrix may be shorter): group and field offsets are scalar.
     const int tiles = (rows + kTileRows - 1) / kTileRows;
     if (rows % kTileRows == 0 || base + live <= kTileRows * (tiles - 1))
-        matvec_rows_body<T, VT, RING, KS, true>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig, smeta, red);
+        matvec_rows_body<T, VT, RING, KS, true, MULTI>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig, smeta,
+                                                      red);
     else
-        matvec_rows_body<T, VT, RING, KS, false>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig, smeta, red);
+        matvec_rows_body<T, VT, RING, KS, false, MULTI>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig, smeta,
+                                                       red);
 }
 
 size_t matvec_lds(int ccols)
@@ -637,6 +652,19 @@ int rows_per_workgroup(int rows)
     return (rows + cus - 1) / cus;
 }
 
+// One launch of matvec_rows over chunk groups [g0, g0 + ng).
+template <unsigned T, int VT, int RING, int KS>
+void launch_rows_kernel(int wgs, size_t lds, hipStream_t s, const uint8_t *w, const float *xc, float *y, int rows,
+    int cols, int rw, int g0, int ng)
+{
+    if ((ng + KS - 1) / KS > RING)
+        hipLaunchKernelGGL((matvec_rows<T, VT, RING, KS, true>), dim3(wgs), dim3(64 * KS), lds, s, w, xc, y, rows, cols,
+                           rw, g0, ng, g0 > 0);
+    else
+        hipLaunchKernelGGL((matvec_rows<T, VT, RING, KS, false>), dim3(wgs), dim3(64 * KS), lds, s, w, xc, y, rows, cols,
+                           rw, g0, ng, g0 > 0);
+}
+
 template <unsigned T>
 hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int cols, hipStream_t s)
 {
@@ -653,19 +681,19 @@ hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int
         // registers.
         if constexpr (T == Q6_K) {
             if (rw <= kTileRows && rpw > 2 * kTileRows)   // one tile per workgroup (128256 x 4096: 84.7 -> 72.5 us)
-                hipLaunchKernelGGL((matvec_rows<T, 1, 1, 8>), dim3(wgs), dim3(512), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
+                launch_rows_kernel<T, 1, 1, 8>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
             else if (rw <= kTileRows)
-                hipLaunchKernelGGL((matvec_rows<T, 1, 1, 16>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
+                launch_rows_kernel<T, 1, 1, 16>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
             else
-                hipLaunchKernelGGL((matvec_rows<T, 2, 1, 8>), dim3(wgs), dim3(512), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
+                launch_rows_kernel<T, 2, 1, 8>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
         } else {
             // One stage per wavefront also where it has several groups
             // (two stages measured 2-10 % slower on 4096 x 11008 and
             // 4096 x 14336).
             if (rw <= kTileRows)
-                hipLaunchKernelGGL((matvec_rows<T, 1, 1, 16>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
+                launch_rows_kernel<T, 1, 1, 16>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
             else
-                hipLaunchKernelGGL((matvec_rows<T, 2, 1, 16>), dim3(wgs), dim3(1024), lds, s, w, xc, y, rows, cols, rw, g0, ng, g0 > 0);
+                launch_rows_kernel<T, 2, 1, 16>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

@@ -48,6 +48,7 @@ class Oracle:
         lib.orc_matvec.argtypes = [_F, _B, ctypes.c_uint, _F, _S, _S]
         lib.orc_matvec_double.argtypes = [_D, _D, _B, ctypes.c_uint, _F, _S, _S]
         lib.orc_matmul.argtypes = [_F, _B, ctypes.c_uint, _F, _S, _S, _S, ctypes.c_int]
+        lib.orc_dequant.argtypes = [_F, _B, ctypes.c_uint, _S, _S, ctypes.c_int]
         self.lib = lib
 
     def half(self, bits: int) -> float:
@@ -79,6 +80,34 @@ class Oracle:
         y = np.empty(batch * rows, dtype=np.float32)
         self.lib.orc_matmul(_fp(y), w.ctypes.data, type_id, _fp(x), cols, rows, batch, threads)
         return y.reshape(batch, rows)
+
+    def dequant(self, w: np.ndarray, type_id: int, rows: int, cols: int, threads: int = 0) -> np.ndarray:
+        """[rows, cols] float32: every weight as the reference decodes it."""
+        out = np.empty((rows, cols), dtype=np.float32)
+        self.lib.orc_dequant(_fp(out), w.ctypes.data, type_id, rows, cols, threads or host_threads())
+        return out
+
+    def contract_sums(self, w: np.ndarray, type_id: int, x: np.ndarray, rows: int, cols: int):
+        """Per token and row, the double sum of decoded products and the sum
+        of their magnitudes (backend/tests/test_quant_kernels.c:13-25) for a
+        whole batch X [batch, cols]: [batch, rows] each, from the decoded
+        weights by float64 matrix products."""
+        wd = self.dequant(w, type_id, rows, cols).astype(np.float64)
+        xd = np.asarray(x, dtype=np.float64).reshape(-1, cols)
+        s = xd @ wd.T
+        np.abs(wd, out=wd)
+        m = np.abs(xd) @ wd.T
+        return s, m
+
+
+def host_threads() -> int:
+    """Threads for the oracle's threaded helpers: the CPUs this process may
+    run on, at most 16."""
+    import os
+    try:
+        return max(1, min(16, len(os.sched_getaffinity(0))))
+    except (AttributeError, OSError):
+        return max(1, min(16, os.cpu_count() or 1))
 
 
 class Reference:

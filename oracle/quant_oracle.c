@@ -20,7 +20,8 @@
  *  - orc_matvec: bit-exact against golden vectors written by the reference's
  *    own nya_llm_matvec compiled from its sources (tests/golden/), and
  *    against exact power-of-two dot products;
- *  - orc_matvec_double: brute-force double sums on tiny inputs. */
+ *  - orc_matvec_double: brute-force double sums on tiny inputs;
+ *  - orc_dequant: element for element equal to orc_value. */
 #include <math.h>
 #include <pthread.h>
 #include <stdint.h>
@@ -302,6 +303,48 @@ int orc_matmul(float *y, const unsigned char *w, unsigned type, const float *x, 
     }
     run_job(&jobs[0]);
     for (int t = started + 1; t < threads; ++t) run_job(&jobs[t]);
+    for (int t = 1; t <= started; ++t) pthread_join(ids[t], NULL);
+    return 0;
+}
+
+/* The decoded weights of a whole matrix, out[r * cols + k] = orc_value of
+ * element k of row r (backend/core/llm_quant.c:70-142), rows split over
+ * `threads` POSIX threads. The tests form the double-precision sums of the
+ * reference kernel contract (backend/tests/test_quant_kernels.c:13-25) for
+ * large batches from these values with a BLAS product. Returns 0. */
+typedef struct dequant_job {
+    float *out;
+    const unsigned char *w;
+    unsigned type;
+    size_t cols, begin, end;
+} dequant_job;
+
+static void *run_dequant(void *opaque)
+{
+    const dequant_job *j = opaque;
+    const size_t stride = row_bytes(j->type, j->cols);
+    for (size_t r = j->begin; r < j->end; ++r)
+        for (size_t k = 0; k < j->cols; ++k) j->out[r * j->cols + k] = orc_value(j->w + r * stride, j->type, k);
+    return NULL;
+}
+
+int orc_dequant(float *out, const unsigned char *w, unsigned type, size_t rows, size_t cols, int threads)
+{
+    if (threads < 1) threads = 1;
+    if ((size_t)threads > rows) threads = (int)rows;
+    if (threads > 256) threads = 256;
+    dequant_job jobs[256];
+    pthread_t ids[256];
+    for (int t = 0; t < threads; ++t)
+        jobs[t] = (dequant_job){out, w, type, cols, rows * (size_t)t / (size_t)threads,
+            rows * (size_t)(t + 1) / (size_t)threads};
+    int started = 0;
+    for (int t = 1; t < threads; ++t) {
+        if (pthread_create(&ids[t], NULL, run_dequant, &jobs[t])) break;
+        started = t;
+    }
+    run_dequant(&jobs[0]);
+    for (int t = started + 1; t < threads; ++t) run_dequant(&jobs[t]);
     for (int t = 1; t <= started; ++t) pthread_join(ids[t], NULL);
     return 0;
 }

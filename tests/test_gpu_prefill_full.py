@@ -1,0 +1,138 @@
+"""The prefill GEMM at every benchmark prefill configuration, every token.
+
+{Q8_0, Q4_K} x {4096 x 4096, 14336 x 4096} x M in {512, 2048} tokens
+through the provider (host buffers, the batched path that replaces
+CUDA/gemm.cu:53-96 and the reference CPU provider's batch >= 8 GEMM,
+backend/core/cpu_backend.c:64-74). Every output is checked:
+
+- against the double-precision sums of the reference kernel contract
+  (backend/tests/test_quant_kernels.c:13-25, :138-213): |y - S| <=
+  1e-6 * (1 + sum |w x|) per token and row, S from the decoded weights by a
+  float64 matrix product;
+- every token at relative L2 <= 1e-5 against the scalar oracle (the
+  reference's own operation order, threaded over rows).
+
+Also: tokens spanning 2^-40 .. 2^44 in magnitude (one 256-column group
+2^-20 below the rest of its token) through the prefill GEMM and the
+batch-1 matvec under the same two checks; activation outlier channels
+(2^12, 2^14) at batch 1, 8 and 40 within relative L2 1e-5 of the scalar
+oracle; rows whose last Q8_0/Q4_0 column group is short (800 columns =
+three full groups and one block) at batch 9 and 40.
+"""
+import numpy as np
+import pytest
+
+from fyodor_amd import Q4_0, Q4_K, Q6_K, Q8_0, TYPE_NAMES, synth
+from checks import rel_l2
+from oracle import host_threads
+
+pytestmark = pytest.mark.gpu
+
+CELLS = [(t, rows, 4096, m) for t in (Q8_0, Q4_K) for rows in (4096, 14336) for m in (512, 2048)]
+
+
+def check_all(oracle, w, t, x, rows, cols, y):
+    """Every token and row against the contract bound and the scalar oracle."""
+    batch = x.shape[0]
+    assert y.shape == (batch, rows) and np.all(np.isfinite(y))
+    s, m = oracle.contract_sums(w, t, x, rows, cols)
+    err = np.abs(y.astype(np.float64) - s)
+    bad = err > 1e-6 * (1 + m)
+    assert not bad.any(), f"{int(bad.sum())} outputs outside the contract bound, first at {np.argwhere(bad)[0]}"
+    scalar = oracle.matmul(w, t, x, rows, cols, batch, threads=host_threads())
+    num = np.linalg.norm(y.astype(np.float64) - scalar, axis=1)
+    den = np.linalg.norm(scalar.astype(np.float64), axis=1)
+    worst = int(np.argmax(num / den))
+    assert np.all(num <= 1e-5 * den), f"token {worst}: relative L2 {num[worst] / den[worst]:.3g}"
+
+
+@pytest.mark.parametrize("t,rows,cols,batch", CELLS, ids=[f"{TYPE_NAMES[t]}-{r}x{c}-m{b}" for t, r, c, b in CELLS])
+def test_prefill_cell_every_token(compute, oracle, t, rows, cols, batch):
+    seed = 31 * t + rows + batch
+    w = synth.weights(t, rows, cols, seed)
+    x = synth.activations(batch, cols, seed + 1)
+    y = compute.matmul_typed(w, rows, cols, t, x, batch)
+    check_all(oracle, w, t, x, rows, cols, y)
+
+
+def wide_range(batch, cols, seed):
+    """Tokens scaled by 2^-40 .. 2^44 in steps, one group of token 3 another
+    2^-20 down (each token, group and block keeps its own exponent)."""
+    x = synth.activations(batch, cols, seed)
+    x *= (np.float32(2.0) ** np.linspace(-40, 44, batch).round().astype(np.float32))[:, None]
+    x[3 % batch, 256:512] *= np.float32(2.0 ** -20)
+    return x
+
+
+def outlier_channels(batch, cols, seed, shift=12):
+    """Three channels 2^shift above the rest of every token, the few large
+    activation features of real decoder layers."""
+    x = synth.activations(batch, cols, seed)
+    x[:, [7, 1000, 2900]] *= np.float32(2.0 ** shift)
+    return x
+
+
+def check_rel_l2(oracle, w, t, x, rows, cols, y, bound=1e-5):
+    """Every token within relative L2 `bound` of the scalar oracle."""
+    assert np.all(np.isfinite(y))
+    scalar = oracle.matmul(w, t, x, rows, cols, x.shape[0], threads=host_threads())
+    num = np.linalg.norm(y.astype(np.float64) - scalar, axis=1)
+    den = np.linalg.norm(scalar.astype(np.float64), axis=1)
+    worst = int(np.argmax(num / den))
+    assert np.all(num <= bound * den), f"token {worst}: relative L2 {num[worst] / den[worst]:.3g}"
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K, Q6_K], ids=lambda t: TYPE_NAMES[t])
+def test_prefill_wide_range(compute, oracle, t):
+    rows, cols, batch = 512, 4096, 40
+    w = synth.weights(t, rows, cols, 90 + t)
+    x = wide_range(batch, cols, 91 + t)
+    y = compute.matmul_typed(w, rows, cols, t, x, batch)
+    check_all(oracle, w, t, x, rows, cols, y)
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K, Q6_K], ids=lambda t: TYPE_NAMES[t])
+@pytest.mark.parametrize("rows", [14336, 4096])
+def test_matvec_wide_range(compute, oracle, t, rows):
+    """The batch-1 matvec builds its own 21-bit digits per 32-column block
+    with a capped shift: single tokens across the whole exponent range."""
+    cols = 4096
+    w = synth.weights(t, rows, cols, 95 + t)
+    x = wide_range(12, cols, 96 + t)
+    y = np.stack([compute.matvec_typed(w, rows, cols, t, x[k]) for k in range(x.shape[0])])
+    check_all(oracle, w, t, x, rows, cols, y)
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K, Q6_K], ids=lambda t: TYPE_NAMES[t])
+@pytest.mark.parametrize("batch", [1, 8, 40])
+def test_outlier_channels(compute, oracle, t, batch):
+    """Activation outliers 2^12 and 2^14 above the rest of every token, at
+    batch 1 (matvec), 8 (small-N) and 40 (prefill GEMM): every token within
+    relative L2 1e-5 of the reference scalar order. x is represented to
+    2^-21 of its 32-column block's largest magnitude (matvec), 2^-22 of its
+    256-column group's (small-N) or its token's (prefill), so rows whose
+    products come mostly from elements far below an outlier they share a
+    block, group or token with can leave the per-row bound of the kernel
+    contract; the whole output stays at the reference's own distance from
+    the exact sums (measured 1.6e-6 to 3e-6 relative L2 up to 2^14)."""
+    rows, cols = 512, 4096
+    w = synth.weights(t, rows, cols, 92 + t)
+    for shift in (12, 14):
+        x = outlier_channels(batch, cols, 93 + t + shift, shift)
+        y = compute.matmul_typed(w, rows, cols, t, x, batch)
+        check_rel_l2(oracle, w, t, x, rows, cols, y.reshape(batch, rows))
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0], ids=lambda t: TYPE_NAMES[t])
+@pytest.mark.parametrize("batch", [9, 40])
+def test_short_last_group(compute, oracle, t, batch):
+    """800 columns: three full 256-column groups and a one-block group, the
+    prefill GEMM's short-group and column-clamp path; 300 rows (one partial
+    tile), canaries on both sides of the output."""
+    rows, cols = 300, 800
+    w = synth.weights(t, rows, cols, 97 + t + batch)
+    x = synth.activations(batch, cols, 98 + t)
+    out = np.full(batch * rows + 2, 12345, dtype=np.float32)
+    compute.matmul_typed(w, rows, cols, t, x, batch, out=out[1:-1])
+    assert out[0] == 12345 and out[-1] == 12345
+    check_all(oracle, w, t, x, rows, cols, out[1:-1].reshape(batch, rows))

@@ -130,3 +130,22 @@ def test_double_oracle_brute_force(oracle, type_id):
     prods = vals * x.astype(np.float64)
     assert np.allclose(s, prods.sum(axis=1), rtol=0, atol=1e-12 * (1 + np.abs(prods).sum()))
     assert np.allclose(m, np.abs(prods).sum(axis=1), rtol=1e-15)
+
+
+@pytest.mark.parametrize("type_id", ALL, ids=lambda t: TYPE_NAMES[t])
+def test_dequant_equals_values(oracle, type_id):
+    """orc_dequant (threaded, whole matrix) is element for element the pinned
+    orc_value, for every thread split, and contract_sums equals the per-row
+    double oracle."""
+    rows, cols = 7, 512
+    w = synth.weights(type_id, rows, cols, 21)
+    vals = oracle.values(w, type_id, rows * cols).reshape(rows, cols)
+    for threads in (1, 3, 16):
+        got = oracle.dequant(w, type_id, rows, cols, threads=threads)
+        assert np.array_equal(got.view(np.uint32), vals.view(np.uint32))
+    x = synth.activations(3, cols, 22)
+    s, m = oracle.contract_sums(w, type_id, x, rows, cols)
+    for k in range(3):
+        s1, m1 = oracle.matvec_double(w, type_id, x[k], rows, cols)
+        assert np.allclose(s[k], s1, rtol=0, atol=1e-12 * (1 + m1.max()))
+        assert np.allclose(m[k], m1, rtol=1e-13, atol=0)

@@ -53,7 +53,9 @@ NYA_HIP_EXPORT unsigned nya_hip_abi_version(void);
  * size from nya_vendor_matrix (backend/core/vendor.c:59-80), which the
  * reference uploads after host expansion. Returns 0, or 1 for an unsupported
  * type or shape (cols not a multiple of the block, a zero or
- * above-INT_MAX dimension, or a size_t overflow). */
+ * above-INT_MAX dimension, a size_t overflow, or a Q4_0/Q8_0/Q4_K/Q6_K
+ * matrix the kernels cannot address: above INT32_MAX bytes or rows above
+ * 2^26 columns). Every other entry point declines the same shapes. */
 NYA_HIP_EXPORT int nya_hip_weight_bytes(unsigned type, size_t rows, size_t cols, size_t *bytes);
 
 /* Whether the device layout of `type` differs from GGUF storage:

@@ -52,6 +52,30 @@ def kernels():
     return Kernels()
 
 
+@pytest.mark.parametrize("t,block_bytes", [(Q4_0, 18), (Q8_0, 34), (Q4_K, 144), (Q6_K, 210)])
+def test_unaddressable_block_matrices_decline(kernels, t, block_bytes):
+    """A block-format matrix above INT32_MAX bytes (the kernels' 32-bit
+    buffer range and tile offsets) or rows above 2^26 columns are declined
+    by every entry point before anything is enqueued; the largest one that
+    fits is accepted. Dense types are addressed with 64-bit offsets."""
+    L = kernels.lib
+    b = ctypes.c_size_t()
+    block = 32 if t in (Q4_0, Q8_0) else 256
+    cols = 4096
+    row = cols // block * block_bytes
+    fits = (2**31 - 1) // row
+    assert L.nya_hip_weight_bytes(t, fits, cols, ctypes.byref(b)) == 0 and b.value == fits * row <= 2**31 - 1
+    for rows, c in [(fits + 1, cols), (1, (1 << 26) + block)]:
+        assert L.nya_hip_weight_bytes(t, rows, c, ctypes.byref(b)) == 1
+        assert L.nya_hip_workspace_bytes(t, rows, c, 1, ctypes.byref(b)) == 1
+        assert L.nya_hip_weight_pack(16, 16, t, rows, c) == 1
+        assert L.nya_hip_kernel_name(t, rows, c, 1) is None
+        # Declined on the shape alone: the (never dereferenced) addresses are
+        # aligned, so nothing else would refuse the call.
+        assert L.nya_hip_matmul(1 << 20, t, rows, c, 1 << 20, 1 << 20, 1, 0, 0, 0) == 1
+    assert L.nya_hip_weight_bytes(F32, 40000, 20000, ctypes.byref(b)) == 0 and b.value == 40000 * 20000 * 4
+
+
 def test_queries(kernels):
     L = kernels.lib
     assert L.nya_hip_abi_version() == 1

@@ -2,6 +2,8 @@
 #include <limits.h>
 #include <stdint.h>
 #include <string.h>
+
+#include <mutex>
 #include "../../include/fyodor_hip.h"
 #include "formats.h"
 #include "kernels.h"
@@ -100,6 +102,44 @@ int matmul_impl(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t 
     return 0;
 }
 
+
+// ---- the allocation-free entry point ---------------------------------------
+//
+// Scratch of nya_hip_matmul_static: a fixed device array, one copy per GPU
+// (the runtime places it when it loads this library's code on the device and
+// keeps it until the process ends). In host code `scratch` names a host-side
+// stand-in, not device memory: its device address is looked up once per
+// device with hipGetSymbolAddress, with that device current, and only that
+// address is handed to kernels.
+constexpr size_t kStaticScratchBytes = NYA_HIP_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void *g_scratch[kMaxDevices];
+
+// The current device's copy of `scratch`, or nullptr if it cannot be found.
+void *static_scratch()
+{
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> hold(g_scratch_lock);
+    if (!g_scratch[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+        g_scratch[dev] = p;
+    }
+    return g_scratch[dev];
+}
+
+// Tokens per call of the prefill GEMM whose workspace fits the array (a
+// multiple of its 32-token tiles), or 0 if not even 32 do.
+size_t static_chunk_tokens(unsigned type, size_t cols)
+{
+    const size_t per32 = prefill_workspace(type, (int)cols, 32);
+    return per32 ? kStaticScratchBytes / per32 * 32 : 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -144,6 +184,39 @@ NYA_HIP_EXPORT int nya_hip_matmul(uintptr_t w, unsigned type, size_t rows, size_
     uintptr_t x, uintptr_t y, size_t batch, uintptr_t workspace, size_t workspace_bytes, uintptr_t stream)
 {
     return matmul_impl(w, type, rows, cols, x, y, batch, workspace, workspace_bytes, stream);
+}
+
+NYA_HIP_EXPORT int nya_hip_matmul_static(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
+    uintptr_t y, size_t batch, uintptr_t stream)
+{
+    size_t b;
+    if (!w || !x || !y || !batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return 1;
+    if ((w & 15u) || (x & 15u) || (y & 3u)) return 1;
+    void *ws = static_scratch();
+    if (!ws) return -(int)hipErrorInvalidSymbol;
+    // The prefill GEMM runs in token chunks whose workspace fits the array
+    // (every token is independent of the others): `parts` chunks of nearly
+    // equal size, each above half the array's capacity (at least 16 tokens),
+    // so every chunk stays on the GEMM and every token gets the same result
+    // as through nya_hip_matmul. Every other path needs at most a few hundred
+    // KiB (the small-N digits of one 16384-column chunk).
+    size_t parts = 1;
+    if (use_prefill(type, cols, batch)) {
+        const size_t fit = static_chunk_tokens(type, cols);
+        if (fit < 32) return NYA_HIP_STATUS_SCRATCH;
+        parts = (batch + fit - 1) / fit;
+    }
+    for (size_t part = 0, done = 0; part < parts; ++part) {
+        const size_t n = batch / parts + (part < batch % parts ? 1 : 0);
+        size_t need = 0;
+        if (nya_hip_workspace_bytes(type, rows, cols, n, &need)) return 1;
+        if (need > kStaticScratchBytes) return NYA_HIP_STATUS_SCRATCH;
+        const int st = matmul_impl(w, type, rows, cols, x + done * cols * sizeof(float),
+                                   y + done * rows * sizeof(float), n, (uintptr_t)ws, kStaticScratchBytes, stream);
+        if (st) return st;
+        done += n;
+    }
+    return 0;
 }
 
 NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_t cols, size_t batch)

@@ -113,6 +113,7 @@ class Kernels:
         L.nya_hip_weight_pack.argtypes = [_vp, _vp, _u, _sz, _sz]
         L.nya_hip_workspace_bytes.argtypes = [_u, _sz, _sz, _sz, ctypes.POINTER(_sz)]
         L.nya_hip_matmul.argtypes = [_up, _u, _sz, _sz, _up, _up, _sz, _up, _sz, _up]
+        L.nya_hip_matmul_static.argtypes = [_up, _u, _sz, _sz, _up, _up, _sz, _up]
         L.nya_hip_copy.argtypes = [_up, _up, _sz, _up]
         L.nya_hip_kernel_name.restype = ctypes.c_char_p
         L.nya_hip_kernel_name.argtypes = [_u, _sz, _sz, _sz]
@@ -140,6 +141,14 @@ class Kernels:
         status = self.lib.nya_hip_matmul(w, type_id, rows, cols, x, y, batch, workspace, workspace_bytes, stream)
         if status != 0:
             raise HipError(f"nya_hip_matmul returned {status}")
+
+    def matmul_static(self, w: int, type_id: int, rows: int, cols: int, x: int, y: int, batch: int,
+                      stream: int) -> None:
+        """The allocation-free entry point (scratch in the library's static
+        device array)."""
+        status = self.lib.nya_hip_matmul_static(w, type_id, rows, cols, x, y, batch, stream)
+        if status != 0:
+            raise HipError(f"nya_hip_matmul_static returned {status}")
 
     def copy(self, dst: int, src: int, nbytes: int, stream: int) -> None:
         status = self.lib.nya_hip_copy(dst, src, nbytes, stream)

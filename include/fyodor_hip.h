@@ -87,6 +87,25 @@ NYA_HIP_EXPORT int nya_hip_matmul(uintptr_t w, unsigned type, size_t rows, size_
     uintptr_t x, uintptr_t y, size_t batch, uintptr_t workspace, size_t workspace_bytes,
     uintptr_t stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): Y = X * W^T exactly as nya_hip_matmul with its
+ * workspace (same kernels, same results per token), but the kernels'
+ * scratch is a fixed device array of NYA_HIP_STATIC_SCRATCH_BYTES inside
+ * this library, one per GPU, held until the process ends; the call
+ * allocates and frees nothing. Prefill batches (above 8 tokens) run in
+ * token chunks whose scratch fits the array. Returns 0, 1 when declined
+ * (the rules of nya_hip_matmul), NYA_HIP_STATUS_SCRATCH when a request
+ * would need more scratch than the array holds (not reachable for rows of
+ * at most 2^26 columns), <0 on a HIP failure. Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (other streams, other
+ * threads) race and must be serialized by the caller; the array keeps the
+ * last call's contents, which no call reads before writing. */
+#define NYA_HIP_STATIC_SCRATCH_BYTES ((size_t)64 << 20)
+#define NYA_HIP_STATUS_SCRATCH 2
+NYA_HIP_EXPORT int nya_hip_matmul_static(uintptr_t w, unsigned type, size_t rows, size_t cols,
+    uintptr_t x, uintptr_t y, size_t batch, uintptr_t stream);
+
 /* Name of the main kernel nya_hip_matmul launches for these arguments, as it
  * appears in a rocprofv3 kernel trace, or NULL when unsupported. Diagnostic
  * only; it launches nothing. */

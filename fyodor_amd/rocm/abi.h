@@ -1,37 +1,42 @@
-/* Function table the C provider resolves at run time: the HIP runtime
- * members keep the names and C types of the reference table
- * (rocm/abi.h:8-19); the rocBLAS members (rocm/abi.h:20-25) are replaced by
- * the gfx950 kernel library declared in include/fyodor_hip.h. Neither a HIP
- * compiler nor HIP headers are needed to build the provider. */
+/* Entry points the ROCm provider resolves at run time, grouped by the shared
+ * library that exports them. The HIP members keep the runtime's own names
+ * and C types (the reference provider resolves the same ones,
+ * rocm/abi.h:8-19); the rocBLAS members of the reference table
+ * (rocm/abi.h:20-25) are replaced by the gfx950 kernel library of
+ * include/fyodor_hip.h. Building the provider needs neither a HIP compiler
+ * nor HIP headers. */
 #ifndef NYA_ROCM_ABI_H
 #define NYA_ROCM_ABI_H
 #include <stddef.h>
 #include <stdint.h>
 #include "types.h"
 
-typedef struct nya_rocm_api {
-    /* libamdhip64 */
+/* libamdhip64 */
+typedef struct nya_hip_runtime {
     hipError_t (*init)(unsigned);
     hipError_t (*device_count)(int *);
     hipError_t (*get_device)(int *);
     hipError_t (*set_device)(int);
     hipError_t (*memory_info)(size_t *, size_t *);
-    hipError_t (*allocate)(void **, size_t);
-    hipError_t (*deallocate)(void *);
+    hipError_t (*device_alloc)(void **, size_t);
+    hipError_t (*device_free)(void *);
+    hipError_t (*pinned_alloc)(void **, size_t, unsigned);
+    hipError_t (*pinned_free)(void *);
     hipError_t (*copy_async)(void *, const void *, size_t, hipMemcpyKind, hipStream_t);
     hipError_t (*stream_create)(hipStream_t *, unsigned);
     hipError_t (*stream_destroy)(hipStream_t);
-    hipError_t (*synchronize)(hipStream_t);
-    /* libfyodor_hip (include/fyodor_hip.h) */
-    unsigned (*kernel_version)(void);
+    hipError_t (*stream_wait)(hipStream_t);
+} nya_hip_runtime;
+
+/* libfyodor_hip (include/fyodor_hip.h) */
+typedef struct nya_kernel_library {
+    unsigned (*abi_version)(void);
     int (*weight_bytes)(unsigned, size_t, size_t, size_t *);
     int (*weight_layout)(unsigned);
     int (*weight_pack)(void *, const void *, unsigned, size_t, size_t);
     int (*workspace_bytes)(unsigned, size_t, size_t, size_t, size_t *);
     int (*matmul)(uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t, size_t, uintptr_t, size_t, uintptr_t);
-} nya_rocm_api;
+} nya_kernel_library;
 
-#define NYA_HIP_H2D hipMemcpyHostToDevice
-#define NYA_HIP_D2H hipMemcpyDeviceToHost
-#define NYA_HIP_KERNEL_ABI 1U
+#define NYA_KERNEL_ABI 1U
 #endif

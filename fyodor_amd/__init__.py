@@ -67,28 +67,34 @@ class ComputeDeclined(RuntimeError):
 _provider = None
 
 
+def compute_api(lib: ctypes.CDLL) -> ctypes.CDLL:
+    """Declares the engine's compute API (include/compute.h) on a loaded
+    library that exports it: this repository's provider library, or a
+    build of the engine's own dispatcher with this provider registered."""
+    vp, sz, fp = ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_float)
+    lib.nya_compute_create_for.restype = vp
+    lib.nya_compute_create_for.argtypes = [ctypes.c_char_p]
+    lib.nya_compute_free.argtypes = [vp]
+    lib.nya_compute_name.restype = ctypes.c_char_p
+    lib.nya_compute_name.argtypes = [vp]
+    lib.nya_compute_capabilities.restype = ctypes.c_uint
+    lib.nya_compute_capabilities.argtypes = [vp]
+    lib.nya_compute_matvec.argtypes = [vp, vp, sz, sz, fp, fp]
+    lib.nya_compute_matvec_typed.argtypes = [vp, vp, sz, sz, ctypes.c_uint, fp, fp]
+    lib.nya_compute_matmul_typed.argtypes = [vp, vp, sz, sz, ctypes.c_uint, fp, fp, sz]
+    lib.nya_compute_context_stats.argtypes = [vp, ctypes.POINTER(ComputeStats)]
+    lib.nya_compute_backend_known.argtypes = [ctypes.c_char_p]
+    lib.nya_compute_backend_compiled.argtypes = [ctypes.c_char_p]
+    return lib
+
+
 def provider_library() -> ctypes.CDLL:
     """Loads libfyodor_rocm.so; raises when it has not been built."""
     global _provider
     if _provider is None:
         if not PROVIDER_LIBRARY.exists():
             raise ProviderUnavailable(f"{PROVIDER_LIBRARY} is missing: run `python -m fyodor_amd.build`")
-        lib = ctypes.CDLL(str(PROVIDER_LIBRARY))
-        vp, sz, fp = ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_float)
-        lib.nya_compute_create_for.restype = vp
-        lib.nya_compute_create_for.argtypes = [ctypes.c_char_p]
-        lib.nya_compute_free.argtypes = [vp]
-        lib.nya_compute_name.restype = ctypes.c_char_p
-        lib.nya_compute_name.argtypes = [vp]
-        lib.nya_compute_capabilities.restype = ctypes.c_uint
-        lib.nya_compute_capabilities.argtypes = [vp]
-        lib.nya_compute_matvec.argtypes = [vp, vp, sz, sz, fp, fp]
-        lib.nya_compute_matvec_typed.argtypes = [vp, vp, sz, sz, ctypes.c_uint, fp, fp]
-        lib.nya_compute_matmul_typed.argtypes = [vp, vp, sz, sz, ctypes.c_uint, fp, fp, sz]
-        lib.nya_compute_context_stats.argtypes = [vp, ctypes.POINTER(ComputeStats)]
-        lib.nya_compute_backend_known.argtypes = [ctypes.c_char_p]
-        lib.nya_compute_backend_compiled.argtypes = [ctypes.c_char_p]
-        _provider = lib
+        _provider = compute_api(ctypes.CDLL(str(PROVIDER_LIBRARY)))
     return _provider
 
 

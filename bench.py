@@ -8,19 +8,24 @@ weight matrix; weights and activations are resident in HBM before timing.
 
 - Enough distinct weight copies rotate to exceed twice the 256 MB Infinity
   Cache, so every step streams its weights from HBM.
-- Launches are captured once into a HIP graph and replayed, so host launch
-  overhead cannot leave the GPU idle; HIP events on that stream bracket the
-  timed steps.
+- A 64 MiB device copy is enqueued just before the start event, so the
+  host has queued the timed launches before the GPU reaches them; HIP
+  events on that stream bracket the timed steps, so the span holds GPU work
+  only, also at the driver's 20 steps (a HIP graph of 20 launches measured
+  0.5 us per step slower to start; --launch graph times one).
 - `value` = algorithmic bytes per step (packed weights + 4*cols*N +
-  4*rows*N) / average step time. At N = 8 a step is two launches: the
-  activation quantization and the matmul.
+  4*rows*N) / average step time.
+- read_ceiling: a plain streaming read of the same weight bytes over the
+  same rotation and launch method (nya_hip_read), the time this matvec can
+  approach.
 - cpu_baseline: the reference CPU provider (built from the reference sources
-  into oracle/_ref) on the same weights, on this host's cores; else this
-  repository's C port of the scalar path.
+  into oracle/_ref) on the same weights, on this host's cores, at the
+  reference's default thread count, at the CPUs this process may use and at
+  one thread; else this repository's C port of the scalar path.
 - prefill: the same matrix times 512 tokens through the fp16-MFMA prefill
-  GEMM (one call = activation split + GEMM): model TFLOP/s, and the fp16
-  flops the matrix cores issue (two activation pieces per token) against the
-  dense fp16 MFMA peak.
+  GEMM (one call = activation split + GEMM): useful TFLOP/s (2 M N K) against
+  the dense fp16 MFMA peak, and the fp16 work the matrix cores issue (two
+  activation pieces per token) beside it.
 
 Prints one JSON line.
 """
@@ -80,45 +85,84 @@ def algorithmic_bytes(rows: int, cols: int, batch: int) -> int:
     return storage_bytes(Q4_K, rows, cols) + 4 * cols * batch + 4 * rows * batch
 
 
-def time_steps(rt, kern, stream, weights, x_dev, y_dev, batch, steps, warmup, mode, work, work_bytes):
+class Settle:
+    """A 64 MiB device copy enqueued before a start event: the GPU is busy
+    for tens of microseconds while the host submits what follows, so the
+    timed span starts with the first timed launch already queued."""
+
+    BYTES = 64 << 20
+
+    def __init__(self, rt, kern):
+        self.rt, self.kern = rt, kern
+        self.src, self.dst = rt.malloc(self.BYTES), rt.malloc(self.BYTES)
+
+    def __call__(self, stream):
+        self.kern.copy(self.dst, self.src, self.BYTES, stream)
+
+    def close(self):
+        self.rt.free(self.src)
+        self.rt.free(self.dst)
+
+
+def time_launches(rt, stream, settle, launch, steps: int, warm: int, mode: str) -> float:
+    """Milliseconds per launch over `steps` launches launch(0..steps-1),
+    after `warm` untimed ones, between HIP events that bracket GPU work only
+    (the settle copy runs before the start event while the host queues the
+    launches). mode "stream": direct launches; "graph": one HIP graph."""
+    graph = Graph(rt, stream, [lambda i=i: launch(i) for i in range(steps)]) if mode == "graph" else None
+    for i in range(warm):
+        launch(i)
+    rt.sync(stream)
+    start, end = rt.event(), rt.event()
+    settle(stream)
+    rt.record(start, stream)
+    if graph:
+        graph.launch()
+    else:
+        for i in range(steps):
+            launch(i)
+    rt.record(end, stream)
+    ms = rt.elapsed_ms(start, end)
+    rt.sync(stream)
+    if graph:
+        graph.close()
+    return ms / steps
+
+
+def time_steps(rt, kern, stream, settle, weights, x_dev, y_dev, batch, steps, warmup, mode, work, work_bytes):
     """Average milliseconds per step over `steps` timed launches."""
     copies = len(weights)
 
     def launch(i):
-        return lambda: kern.matmul(weights[i % copies], Q4_K, ROWS, COLS, x_dev, y_dev, batch, work, work_bytes,
-                                   stream)
+        kern.matmul(weights[i % copies], Q4_K, ROWS, COLS, x_dev, y_dev, batch, work, work_bytes, stream)
 
-    start, end = rt.event(), rt.event()
-    if mode == "graph":
-        warm = Graph(rt, stream, [launch(i) for i in range(max(warmup, 1))])
-        timed = Graph(rt, stream, [launch(i) for i in range(steps)])
-        warm.launch()
-        rt.sync(stream)
-        rt.record(start, stream)
-        timed.launch()
-        rt.record(end, stream)
-        ms = rt.elapsed_ms(start, end)
-        warm.close()
-        timed.close()
-    else:
-        for i in range(warmup):
-            launch(i)()
-        rt.sync(stream)
-        rt.record(start, stream)
-        for i in range(steps):
-            launch(i)()
-        rt.record(end, stream)
-        ms = rt.elapsed_ms(start, end)
-    rt.sync(stream)
-    return ms / steps
+    return time_launches(rt, stream, settle, launch, steps, warmup, mode)
+
+
+def read_ceiling(rt, kern, stream, settle, weights, steps, warmup, mode, matvec_ms) -> dict:
+    """The plain streaming read of the same weight bytes, same rotation and
+    launch method as the timed matvec steps."""
+    wbytes = storage_bytes(Q4_K, ROWS, COLS)
+    sink = rt.malloc(4096)
+    copies = len(weights)
+
+    def launch(i):
+        kern.read(weights[i % copies], wbytes, sink, stream)
+
+    ms = time_launches(rt, stream, settle, launch, steps, warmup, mode)
+    rt.free(sink)
+    return {"kernel": "read16 (nya_hip_read)", "bytes": wbytes, "us_per_step": round(ms * 1e3, 3),
+            "GBps": round(wbytes / (ms * 1e-3) / 1e9, 2), "frac": round(wbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "matvec_over_read": round(matvec_ms / ms, 4)}
 
 
 def call_latency(kern, rt, stream, weights, x_dev, y_dev, host_w: np.ndarray, x_host: np.ndarray,
                  calls: int = 200) -> dict:
     """Wall time of single N=1 calls, each waited for, at the two boundaries:
     nya_hip_matmul on device buffers plus a stream synchronize, and the
-    provider's matvec on host buffers (rocm/rocm.c:111-139: x up, kernel,
-    y down, synchronize) with the weights already in its cache."""
+    provider's matvec on host buffers (x staged and copied up, the kernel
+    writing y into pinned host memory, one synchronize; the engine's
+    contract, rocm/rocm.c:111-139) with the weights already in its cache."""
     abi = []
     for i in range(calls + 5):
         t0 = time.perf_counter()
@@ -140,52 +184,91 @@ def call_latency(kern, rt, stream, weights, x_dev, y_dev, host_w: np.ndarray, x_
                       f"{len(weights)} weight copies, the provider reuses its one cached copy"}
 
 
-def host_cpu() -> tuple:
-    """CPU model name and the SIMD path the reference provider selects on it
-    (backend/core/cpu_kernels.c:91-100: AVX-512 F+BW, else AVX2+F16C, else
-    scalar)."""
-    model, flags = "unknown", set()
+def host_cpu() -> dict:
+    """The host CPU as /proc/cpuinfo and sysfs describe it, and the SIMD path
+    the reference provider selects on it (backend/core/cpu_kernels.c:91-100:
+    AVX-512 F+BW, else AVX2+F16C, else scalar)."""
+    info, flags = {}, set()
     try:
         for line in open("/proc/cpuinfo"):
             key, _, value = line.partition(":")
-            if key.strip() == "model name" and model == "unknown":
-                model = value.strip()
-            elif key.strip() == "flags" and not flags:
+            key = key.strip()
+            if key in ("model name", "vendor_id", "cpu family", "model", "stepping") and key not in info:
+                info[key] = value.strip()
+            elif key == "flags" and not flags:
                 flags = set(value.split())
     except OSError:
         pass
+    isa = "scalar"
     if {"avx2", "f16c"} <= flags:
-        return model, "avx512" if {"avx512f", "avx512bw"} <= flags else "avx2"
-    return model, "scalar"
+        isa = "avx512" if {"avx512f", "avx512bw"} <= flags else "avx2"
+    model = info.get("model name", "unknown")
+    ident = "family {} model {} stepping {}".format(info.get("cpu family", "?"), info.get("model", "?"),
+                                                   info.get("stepping", "?"))
+    return {"model": f"{model} ({info.get('vendor_id', '?')}, {ident})", "isa": isa,
+            "online_cpus": os.cpu_count() or 1, "affinity_cpus": len(os.sched_getaffinity(0)),
+            "l3_bytes": l3_bytes()}
+
+
+def l3_bytes() -> int:
+    """Total last-level cache of the host: the sum over distinct L3
+    instances in sysfs (0 when sysfs does not say)."""
+    seen, total = set(), 0
+    base = Path("/sys/devices/system/cpu")
+    for cache in base.glob("cpu[0-9]*/cache/index[0-9]*"):
+        try:
+            if (cache / "level").read_text().strip() != "3":
+                continue
+            shared = (cache / "shared_cpu_list").read_text().strip()
+            if shared in seen:
+                continue
+            seen.add(shared)
+            size = (cache / "size").read_text().strip().upper()
+            total += int(size[:-1]) * {"K": 1 << 10, "M": 1 << 20}.get(size[-1], 1) if size[-1] in "KM" else int(size)
+        except (OSError, ValueError):
+            continue
+    return total
 
 
 def cpu_baseline(weights_host: np.ndarray, x: np.ndarray, y_gpu: np.ndarray, seconds: float) -> dict:
-    """The reference CPU provider (or the C port) on the same workload, at
-    the host's thread count and at one thread."""
+    """The reference CPU provider (or the C port) on the same workload: at
+    the reference's default thread count (NYA_CPU_THREADS unset: online
+    CPUs, at most 64, backend/core/cpu_backend.c:113-151), at the CPUs this
+    process may run on, and at one thread. The weights rotate over enough
+    host copies to exceed twice the host's L3."""
     sys.path.insert(0, str(REPO))
     from oracle import Oracle, Reference  # the checker; only this leg uses it
 
-    threads = min(len(os.sched_getaffinity(0)), 16)
-    copies = [weights_host] + [weights_host.copy() for _ in range(3)]  # > any L3
+    host = host_cpu()
+    default_threads = min(host["online_cpus"], 64)
+    affinity = host["affinity_cpus"]
+    n_copies = max(2, math.ceil(2 * host["l3_bytes"] / weights_host.nbytes) + 1)
+    copies = [weights_host] + [weights_host.copy() for _ in range(n_copies - 1)]
     y = np.empty(ROWS, dtype=np.float32)
     kind = "reference" if Reference.available() else "port"
     ref = Reference() if kind == "reference" else None
     orc = None if ref else Oracle()
 
-    def leg(n: int, budget: float, cap: int):
-        """Median seconds per matvec on n threads and the output of the first."""
+    def leg(n, budget: float, cap: int):
+        """Median seconds per matvec and the output of the first call; n None:
+        the provider's own default thread count."""
         ctx = None
         if ref:
             # The provider reads its thread count when created
             # (backend/core/cpu_backend.c:147-151).
-            os.environ["NYA_CPU_THREADS"] = str(n)
+            saved = os.environ.pop("NYA_CPU_THREADS", None)
+            if n is not None:
+                os.environ["NYA_CPU_THREADS"] = str(n)
             ctx = ref.cpu_provider()
+            os.environ.pop("NYA_CPU_THREADS", None)
+            if saved is not None:
+                os.environ["NYA_CPU_THREADS"] = saved
 
             def run(w):
                 ref.provider_matmul(ctx, w, Q4_K, x, ROWS, COLS, 1, y)
         else:
             def run(w):
-                y[:] = orc.matmul(w, Q4_K, x, ROWS, COLS, 1, threads=n)[0]
+                y[:] = orc.matmul(w, Q4_K, x, ROWS, COLS, 1, threads=n or default_threads)[0]
         run(copies[0])
         first = y.copy()
         run(copies[1])
@@ -199,26 +282,31 @@ def cpu_baseline(weights_host: np.ndarray, x: np.ndarray, y_gpu: np.ndarray, sec
             ref.free(ctx)
         return float(np.median(times)), len(times), first
 
-    med, count, y_cpu = leg(threads, seconds, 5000)
-    med1, count1, _ = leg(1, seconds / 4, 200)
-    parity = float(np.linalg.norm(y_gpu.astype(np.float64) - y_cpu) / np.linalg.norm(y_cpu.astype(np.float64)))
-    model, isa = host_cpu()
     nbytes = algorithmic_bytes(ROWS, COLS, 1)
+    med, count, y_cpu = leg(None, seconds * 0.5, 5000)
+    med_a, count_a, _ = leg(affinity, seconds * 0.3, 5000)
+    med1, count1, _ = leg(1, seconds * 0.2, 200)
+    parity = float(np.linalg.norm(y_gpu.astype(np.float64) - y_cpu) / np.linalg.norm(y_cpu.astype(np.float64)))
     return {
-        "value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": kind,
-        "sample": f"{count} Q4_K 14336x4096 N=1 matvecs over 4 rotating host copies of the same "
-                  f"synthetic weights, median time {med * 1e3:.3f} ms"
-                  + (" (reference backend/core/cpu_backend.c provider, NYA_CPU_THREADS)" if kind == "reference"
+        "value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": default_threads, "kind": kind,
+        "sample": f"{count} Q4_K 14336x4096 N=1 matvecs over {n_copies} rotating host copies of the same "
+                  f"synthetic weights (more than twice the host's {host['l3_bytes'] >> 20} MiB of L3), median "
+                  f"time {med * 1e3:.3f} ms, at the reference's default thread count (online CPUs capped at 64)"
+                  + (" (reference backend/core/cpu_backend.c provider)" if kind == "reference"
                      else " (scalar C port, rows split over threads)"),
-        "one_thread": {"value": round(nbytes / med1 / 1e9, 2), "unit": "GB/s",
+        "affinity": {"value": round(nbytes / med_a / 1e9, 2), "unit": "GB/s", "cores": affinity,
+                     "sample": f"{count_a} matvecs of the same workload on the {affinity} CPUs this process may "
+                               f"use, median time {med_a * 1e3:.3f} ms"},
+        "one_thread": {"value": round(nbytes / med1 / 1e9, 2), "unit": "GB/s", "cores": 1,
                        "sample": f"{count1} matvecs of the same workload, median time {med1 * 1e3:.3f} ms"},
-        "isa": isa if kind == "reference" else "scalar",
-        "cpu_model": model,
+        "isa": host["isa"] if kind == "reference" else "scalar",
+        "cpu_model": host["model"],
+        "online_cpus": host["online_cpus"],
         "parity_rel_l2_vs_gpu": parity,
     }
 
 
-def prefill(rt, kern, stream, weights, host_w, steps: int) -> dict:
+def prefill(rt, kern, stream, settle, weights, steps: int) -> dict:
     """Q4_K 14336x4096 times PREFILL_TOKENS tokens on the prefill GEMM."""
     m = PREFILL_TOKENS
     x = synth.activations(m, COLS, seed=99)
@@ -229,28 +317,20 @@ def prefill(rt, kern, stream, weights, host_w, steps: int) -> dict:
     copies = len(weights)
 
     def launch(i):
-        return lambda: kern.matmul(weights[i % copies], Q4_K, ROWS, COLS, x_dev, y_dev, m, work, need, stream)
+        kern.matmul(weights[i % copies], Q4_K, ROWS, COLS, x_dev, y_dev, m, work, need, stream)
 
-    warm = Graph(rt, stream, [launch(i) for i in range(2)])
-    timed = Graph(rt, stream, [launch(i) for i in range(steps)])
-    warm.launch()
-    rt.sync(stream)
-    start, end = rt.event(), rt.event()
-    rt.record(start, stream)
-    timed.launch()
-    rt.record(end, stream)
-    ms = rt.elapsed_ms(start, end) / steps
-    warm.close()
-    timed.close()
+    ms = time_launches(rt, stream, settle, launch, steps, 2, "stream")
     for p in (x_dev, y_dev, work):
         rt.free(p)
-    useful = 2.0 * ROWS * COLS * m / (ms * 1e-3) / 1e12          # model TFLOP/s
-    issued = useful * PREFILL_PIECES                               # fp16 TFLOP/s on the matrix cores
+    useful = 2.0 * ROWS * COLS * m / (ms * 1e-3) / 1e12          # 2 M N K per call
+    issued = useful * PREFILL_PIECES                               # fp16 work on the matrix cores
     return {
         "workload": f"Q4_K {ROWS}x{COLS} x {m} tokens (prefill GEMM)", "kernel": kern.kernel_name(Q4_K, ROWS, COLS, m),
         "ms_per_call": round(ms, 5), "calls": steps, "useful_tflops": round(useful, 2),
-        "roofline": {"bound": "mfma", "achieved": round(issued, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(issued / PEAK_FP16_TFLOPS, 4)},
+        "roofline": {"bound": "mfma", "achieved": round(useful, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(useful / PEAK_FP16_TFLOPS, 4)},
+        "issued": {"tflops": round(issued, 2), "frac": round(issued / PEAK_FP16_TFLOPS, 4),
+                   "note": "fp16 MFMA work including the second activation piece of every token"},
     }
 
 
@@ -264,9 +344,10 @@ SWEEP_MATVEC = [
 SWEEP_PREFILL = [(t, rows, 4096, m) for t in (Q4_K, Q8_0) for rows in (4096, 14336) for m in (512, 2048)]
 
 
-def time_case(rt, kern, stream, t, rows, cols, batch, steps):
-    """Milliseconds per call of one matmul shape: graph replay over enough
-    rotating weight copies that every call streams its weights from HBM."""
+def time_case(rt, kern, stream, settle, t, rows, cols, batch, steps):
+    """Milliseconds per call of one matmul shape: direct launches behind the
+    settle copy, over enough rotating weight copies that every call streams
+    its weights from HBM."""
     wbytes = storage_bytes(t, rows, cols)
     copies = max(2, math.ceil(2 * MALL_BYTES / wbytes) + 1)
     dev = kern.device_weights(synth.weights(t, rows, cols, seed=7), t, rows, cols)
@@ -282,32 +363,22 @@ def time_case(rt, kern, stream, t, rows, cols, batch, steps):
     work = rt.malloc(max(need, 16))
 
     def launch(i):
-        return lambda: kern.matmul(weights[i % copies], t, rows, cols, x_dev, y_dev, batch, work, need, stream)
+        kern.matmul(weights[i % copies], t, rows, cols, x_dev, y_dev, batch, work, need, stream)
 
-    warm = Graph(rt, stream, [launch(i) for i in range(min(copies, 8))])
-    timed = Graph(rt, stream, [launch(i) for i in range(steps)])
-    warm.launch()
-    rt.sync(stream)
-    start, end = rt.event(), rt.event()
-    rt.record(start, stream)
-    timed.launch()
-    rt.record(end, stream)
-    ms = rt.elapsed_ms(start, end) / steps
-    warm.close()
-    timed.close()
+    ms = time_launches(rt, stream, settle, launch, steps, min(copies, 8), "stream")
     for p in weights + [x_dev, y_dev, work]:
         rt.free(p)
     return ms
 
 
-def sweep(rt, kern, stream) -> int:
+def sweep(rt, kern, stream, settle) -> int:
     """One JSON line per configuration: matvec / small-N effective HBM GB/s,
     prefill useful TFLOP/s (2 M N K per call)."""
     for t, rows, cols, batches in SWEEP_MATVEC:
         wbytes = storage_bytes(t, rows, cols)
         for batch in batches:
             steps = max(40, min(2000, int(4e9 / wbytes)))
-            ms = time_case(rt, kern, stream, t, rows, cols, batch, steps)
+            ms = time_case(rt, kern, stream, settle, t, rows, cols, batch, steps)
             nbytes = wbytes + 4 * cols * batch + 4 * rows * batch
             gbs = nbytes / (ms * 1e-3) / 1e9
             print(json.dumps({"sweep": "matvec", "type": TYPE_NAMES[t], "rows": rows, "cols": cols, "batch": batch,
@@ -315,12 +386,13 @@ def sweep(rt, kern, stream) -> int:
                               "us_per_call": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
                               "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}), flush=True)
     for t, rows, cols, m in SWEEP_PREFILL:
-        ms = time_case(rt, kern, stream, t, rows, cols, m, 20)
+        ms = time_case(rt, kern, stream, settle, t, rows, cols, m, 20)
         useful = 2.0 * rows * cols * m / (ms * 1e-3) / 1e12
         print(json.dumps({"sweep": "prefill", "type": TYPE_NAMES[t], "rows": rows, "cols": cols, "tokens": m,
                           "kernel": kern.kernel_name(t, rows, cols, m), "calls": 20,
                           "us_per_call": round(ms * 1e3, 2), "useful_tflops": round(useful, 1),
-                          "frac_fp16": round(useful * PREFILL_PIECES / PEAK_FP16_TFLOPS, 4)}), flush=True)
+                          "frac_fp16": round(useful / PEAK_FP16_TFLOPS, 4),
+                          "issued_frac_fp16": round(useful * PREFILL_PIECES / PEAK_FP16_TFLOPS, 4)}), flush=True)
     return 0
 
 
@@ -343,7 +415,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--launch", choices=["graph", "stream"], default="graph")
+    ap.add_argument("--launch", choices=["stream", "graph"], default="stream",
+                    help="direct launches behind the settle copy (default), or one HIP graph per timed run")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-call-latency", action="store_true",
                     help="skip the per-call wall times at the C-ABI and provider boundaries")
@@ -365,8 +438,9 @@ def main() -> int:
     stream = rt.stream()
     if args.calibrate_copy:
         return calibrate_copy(rt, kern, stream, max(args.steps, 1))
+    settle = Settle(rt, kern)
     if args.sweep:
-        return sweep(rt, kern, stream)
+        return sweep(rt, kern, stream, settle)
     wbytes = storage_bytes(Q4_K, ROWS, COLS)
     copies = max(2, math.ceil(2 * MALL_BYTES / wbytes) + 2)
     host_w = synth.weights(Q4_K, ROWS, COLS, seed=1234)
@@ -384,7 +458,7 @@ def main() -> int:
     work = rt.malloc(max(work_bytes, 16))
 
     if args.prefill_only:
-        print(json.dumps({"prefill": prefill(rt, kern, stream, weights, host_w, max(args.prefill_steps, 1))}),
+        print(json.dumps({"prefill": prefill(rt, kern, stream, settle, weights, max(args.prefill_steps, 1))}),
               flush=True)
         for p in weights + [work]:
             rt.free(p)
@@ -392,7 +466,7 @@ def main() -> int:
 
     results = {}
     for batch in (1, 8):
-        ms = time_steps(rt, kern, stream, weights, x_dev, y_dev, batch, args.steps, args.warmup, args.launch,
+        ms = time_steps(rt, kern, stream, settle, weights, x_dev, y_dev, batch, args.steps, args.warmup, args.launch,
                         work, kern.workspace_bytes(Q4_K, ROWS, COLS, batch))
         nbytes = algorithmic_bytes(ROWS, COLS, batch)
         results[batch] = (ms, nbytes / (ms * 1e-3) / 1e9, nbytes)
@@ -427,14 +501,16 @@ def main() -> int:
                "frac": round(gbs8 / PEAK_HBM_GBS, 4), "algorithmic_bytes": bytes8, "traffic": measured_traffic(8),
                "kernel": kern.kernel_name(Q4_K, ROWS, COLS, 8)},
     }
+    line["read_ceiling"] = read_ceiling(rt, kern, stream, settle, weights, args.steps, args.warmup, args.launch, ms1)
     if not args.no_call_latency:
         line["call_latency"] = call_latency(kern, rt, stream, weights, x_dev, y_dev, host_w, x8[0].copy())
     if args.prefill_steps > 0:
-        line["prefill"] = prefill(rt, kern, stream, weights, host_w, args.prefill_steps)
+        line["prefill"] = prefill(rt, kern, stream, settle, weights, args.prefill_steps)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(host_w, x8[0].copy(), y1, args.cpu_seconds)
-    for p in weights + [work]:
+    for p in weights + [work, x_dev, y_dev]:
         rt.free(p)
+    settle.close()
     print(json.dumps(line), flush=True)
     return 0
 

@@ -235,4 +235,10 @@ NYA_HIP_EXPORT int nya_hip_copy(uintptr_t dst, uintptr_t src, size_t bytes, uint
     return status(launch_copy((uint4 *)dst, (const uint4 *)src, bytes / 16, (hipStream_t)stream));
 }
 
+NYA_HIP_EXPORT int nya_hip_read(uintptr_t src, size_t bytes, uintptr_t sink, uintptr_t stream)
+{
+    if (!src || !sink || !bytes || (src & 15u) || (sink & 3u) || (bytes & 15u)) return 1;
+    return status(launch_read((const uint4 *)src, bytes / 16, (unsigned *)sink, (hipStream_t)stream));
+}
+
 }  // extern "C"

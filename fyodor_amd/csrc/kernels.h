@@ -53,5 +53,11 @@ hipError_t launch_prefill_f16(unsigned type, const uint8_t *w, const float *x, f
 
 // Plain 16-byte-per-thread device copy (dense.hip), for counter calibration.
 hipError_t launch_copy(uint4 *dst, const uint4 *src, size_t count, hipStream_t stream);
+// Plain streaming read of `count` 16-byte elements, one workgroup per CU
+// (dense.hip); `sink` holds kReadSinkWords words.
+constexpr int kReadSinkWords = 1024;
+hipError_t launch_read(const uint4 *src, size_t count, unsigned *sink, hipStream_t stream);
+// Compute units of the current device (counted once per device).
+int device_cu_count();
 
 }  // namespace fy

@@ -630,9 +630,12 @@ size_t matvec_lds(int ccols)
     return (size_t)ccols / 32 * (128 + kMetaBytes);
 }
 
-// Workgroups of the row-balanced kernel: one per CU (counted once per
-// device).
-int cu_count()
+// Workgroups of the row-balanced kernel: one per CU.
+int cu_count() { return device_cu_count(); }
+
+}  // namespace
+
+int device_cu_count()
 {
     static int counts[64];
     int dev = 0;
@@ -644,6 +647,8 @@ int cu_count()
     }
     return counts[dev];
 }
+
+namespace {
 
 // Row-balanced layout: rows per workgroup (one workgroup per CU).
 int rows_per_workgroup(int rows)

@@ -115,6 +115,7 @@ class Kernels:
         L.nya_hip_matmul.argtypes = [_up, _u, _sz, _sz, _up, _up, _sz, _up, _sz, _up]
         L.nya_hip_matmul_static.argtypes = [_up, _u, _sz, _sz, _up, _up, _sz, _up]
         L.nya_hip_copy.argtypes = [_up, _up, _sz, _up]
+        L.nya_hip_read.argtypes = [_up, _sz, _up, _up]
         L.nya_hip_kernel_name.restype = ctypes.c_char_p
         L.nya_hip_kernel_name.argtypes = [_u, _sz, _sz, _sz]
 
@@ -154,6 +155,12 @@ class Kernels:
         status = self.lib.nya_hip_copy(dst, src, nbytes, stream)
         if status != 0:
             raise HipError(f"nya_hip_copy returned {status}")
+
+    def read(self, src: int, nbytes: int, sink: int, stream: int) -> None:
+        """Plain streaming read of nbytes (diagnostic HBM read ceiling)."""
+        status = self.lib.nya_hip_read(src, nbytes, sink, stream)
+        if status != 0:
+            raise HipError(f"nya_hip_read returned {status}")
 
     def kernel_name(self, type_id: int, rows: int, cols: int, batch: int) -> str:
         name = self.lib.nya_hip_kernel_name(type_id, rows, cols, batch)

@@ -117,6 +117,15 @@ NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_
  * byte counters (rocprofv3 FETCH_SIZE / WRITE_SIZE) against a known size. */
 NYA_HIP_EXPORT int nya_hip_copy(uintptr_t dst, uintptr_t src, size_t bytes, uintptr_t stream);
 
+/* Diagnostics, no counterpart in the reference: enqueue a plain streaming
+ * read of `bytes` (a multiple of 16, 16-byte aligned) with non-temporal
+ * 16-byte loads, one workgroup per compute unit over a contiguous share and
+ * nothing computed: the HBM read time a decode matvec of the same bytes can
+ * approach. `sink` (4-byte aligned, NYA_HIP_READ_SINK_BYTES) receives at most
+ * a few words and is otherwise left as it is. */
+#define NYA_HIP_READ_SINK_BYTES 4096
+NYA_HIP_EXPORT int nya_hip_read(uintptr_t src, size_t bytes, uintptr_t sink, uintptr_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,10 +11,12 @@ from oracle import Oracle  # noqa: E402
 
 
 def test_host_cpu_names_a_reference_isa():
-    model, isa = bench.host_cpu()
-    assert isinstance(model, str) and model
+    host = bench.host_cpu()
+    assert isinstance(host["model"], str) and "family" in host["model"]
     # backend/core/cpu_kernels.c:91-100 selects one of these three.
-    assert isa in ("avx512", "avx2", "scalar")
+    assert host["isa"] in ("avx512", "avx2", "scalar")
+    assert 1 <= host["affinity_cpus"] <= host["online_cpus"]
+    assert host["l3_bytes"] >= 0
 
 
 def test_cpu_baseline_fields(monkeypatch):
@@ -30,6 +32,8 @@ def test_cpu_baseline_fields(monkeypatch):
     assert line["kind"] in ("reference", "port")
     assert line["unit"] == "GB/s" and line["value"] > 0 and line["cores"] >= 1
     assert line["one_thread"]["value"] > 0 and line["one_thread"]["unit"] == "GB/s"
+    assert line["affinity"]["value"] > 0 and line["affinity"]["cores"] >= 1
+    assert "family" in line["cpu_model"] and line["online_cpus"] >= 1
     assert line["isa"] in ("avx512", "avx2", "scalar")
     # Both CPU paths are within float rounding of the scalar restatement.
     assert line["parity_rel_l2_vs_gpu"] < 1e-5

@@ -22,8 +22,10 @@
 // block 2m + l/32: lane half h holds blocks 2m + h (m = 0..3) in registers
 // 0..2 of accumulator m and every epilogue instruction serves two blocks.
 // The A operand of block k is read from LDS at a per-lane address fixed for
-// the whole kernel. (Q6_K, whose lane halves carry different 16-column
-// scales, keeps v_mfma_i32_32x32x32_i8; see aoff6_of.)
+// the whole kernel. Q6_K, whose lane halves carry different 16-column scales,
+// gives the column half the A-row bit of bsel: one block per MFMA, A-rows
+// 8 h + 4 rh + d, so D lane l holds the sums of its own row l%32 and its own
+// column half l/32 (see aoff6_of).
 //
 // Weights, as the reference decodes them (backend/core/llm_quant.c:70-142).
 // Q4_K and Q4_0 bytes hold element l of blocks 2p (low nibble) and 2p + 1
@@ -61,18 +63,17 @@ __device__ __forceinline__ int aoff_of(int l, int k)
     return 128 * k + 16 * (c >> 1) + 32 * (live ? d : 3);
 }
 
-// Q6_K: lane half h of MFMA block j = 4c + j' (unit p = 2c + j'/2, nibble
-// m = j'%2) holds columns 16 (j'/2) .. +15 of x-block 4c + 2m + h, which has
-// its own 16-column scale. The halves get their own A rows: block j' of a
-// four-block chain sits in A-rows 8j' + 4h + d, digit d < 3 in K-half h only,
-// so D lane half h holds its own half's sums (registers 4j' .. 4j'+2) and
-// each group takes two chains (c = 0, 1).
+// Q6_K: lane half h of block j (unit p = j/2, nibble m = j%2) holds columns
+// 16 p%2 .. +15 of x-block xb = 4 (j/4) + 2 m + h, which has its own
+// 16-column scale. Lane l supplies A-row l%16 = 8 hh + 4 rh + d for K-chunk
+// c = l/16 (row half c%2, lane half c/2): live for rh == c%2, hh == c/2 and
+// d < 3, reading digit d of x-block xb(j, hh); else the zero slot.
 __device__ __forceinline__ int aoff6_of(int l, int j)
 {
-    const int h = l >> 5, jr = (l & 31) >> 3, hr = ((l & 31) >> 2) & 1, dd = l & 3;
-    const int c = j >> 2, jp = j & 3, xb = 4 * c + 2 * (jp & 1) + h;
-    const bool live = jr == jp && hr == h && dd < 3;
-    return 128 * xb + 32 * (live ? dd : 3) + 16 * (jp >> 1);
+    const int m = l & 15, c = l >> 4, hh = m >> 3, rh = (m >> 2) & 1, d = m & 3;
+    const bool live = (c & 1) == rh && (c >> 1) == hh && d < 3;
+    const int xb = 4 * (j >> 2) + 2 * (j & 1) + (c >> 1);
+    return 128 * xb + 32 * (live ? d : 3) + 16 * ((j >> 1) & 1);
 }
 
 template <int CTRL>
@@ -235,32 +236,29 @@ __device__ __forceinline__ void group_dots(float (&part)[VT], const MvStage<T> (
     const uint8_t *__restrict__ a, const int (&aoff)[8], const float4 *__restrict__ mt, int h)
 {
     if constexpr (T == Q6_K) {
-        // Two chains of four blocks (see aoff6_of); lane half h's block j' of
-        // chain c reads x-block 4c + 2 (j'%2) + h and the scale
-        // sc[8c + 2 q + j'/2] with q = 2 (j'%2) + h.
+        // One MFMA per block (see aoff6_of); lane half h's block j reads
+        // x-block 4 (j/4) + 2 (j%2) + h and the scale in byte q = 2 (j%2) + h
+        // of scale word 2 (j/4) + (j/2)%2.
 #pragma unroll
         for (int v = 0; v < VT; ++v) {
+            i32x4 D[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                D[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(*(const i32x4 *)(a + aoff[j]), block_b6(w[v], j, h),
+                                                             (i32x4){0, 0, 0, 0}, 0, 0, 0);
             float sum = 0.f;
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                i32x16 D = {};
-#pragma unroll
-                for (int jp = 0; jp < 4; ++jp)
-                    D = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const i32x4 *)(a + aoff[4 * c + jp]),
-                                                              block_b6(w[v], 4 * c + jp, h), D, 0, 0, 0);
-#pragma unroll
-                for (int jp = 0; jp < 4; ++jp) {
-                    const float4 md = mt[4 * c + 2 * (jp & 1)];
-                    // Sums reach 2^34: the top digit joins in float.
-                    const float G = __builtin_fmaf((float)D[4 * jp + 2], 65536.f,
-                                                   (float)(D[4 * jp + 1] * 256 + D[4 * jp]));
-                    const float t = __builtin_fmaf(G, md.x, md.y);
-                    const int q = 2 * (jp & 1) + h;
-                    // The builtin's result type is unsigned: convert it as
-                    // the signed value it holds.
-                    const float sc = (float)(int)__builtin_amdgcn_sbfe((int)w[v].sc[2 * c + (jp >> 1)], 8 * q, 8);
-                    sum = __builtin_fmaf(sc, t, sum);
-                }
+            for (int j = 0; j < 8; ++j) {
+                const int c = j >> 2, jp = j & 3;
+                const float4 md = mt[4 * c + 2 * (jp & 1)];
+                // Sums reach 2^34: the top digit joins in float.
+                const float G = __builtin_fmaf((float)D[j][2], 65536.f, (float)(D[j][1] * 256 + D[j][0]));
+                const float t = __builtin_fmaf(G, md.x, md.y);
+                const int q = 2 * (jp & 1) + h;
+                // The builtin's result type is unsigned: convert it as the
+                // signed value it holds.
+                const float sc = (float)(int)__builtin_amdgcn_sbfe((int)w[v].sc[2 * c + (jp >> 1)], 8 * q, 8);
+                sum = __builtin_fmaf(sc, t, sum);
             }
             part[v] = f16_to_f32(w[v].d & 0xFFFFu) * sum;
         }
@@ -481,16 +479,30 @@ __device__ __forceinline__ void load_rows(MvStage<T> &w, __amdgpu_buffer_rsrc_t 
 // w, w + 16, ... of all VT tiles: it reads and quantizes only those groups of
 // x (no barrier before the dots), and each A operand it reads from LDS serves
 // the VT tiles' interleaved MFMA chains. MULTI: some wavefront has more
-// groups than ring stages (rows wider than KS RING groups); without it the
-// ring is never refilled and that code is left out (it costs registers).
-template <unsigned T, int VT, int RING, int KS, bool FULL, bool MULTI>
+// stages than its ring holds (rows wider than KS P RING groups); without it
+// the ring is never refilled and that code is left out (it costs registers).
+//
+// P = 2 (up to 16 rows per workgroup, VT = 1): a stage holds two of
+// the wavefront's groups, j = 2k and 2k + 1, for the same 16 rows. Lane l
+// takes row l%16 of group j = 2k + (l/16)%2, so every 1 KiB load carries
+// distinct bytes (with 32-row lanes, 16 of them would repeat the last row)
+// and a wavefront needs half the memory round trips. The MFMA sees the same
+// lane layout as at P = 1, with the second group where the second row half
+// was: B chunk c = l/16 and the A-row half rh select group 2k + c%2 (the
+// A operand of lanes with c odd is read from that group's digits), and D
+// lane l holds row l%16 of group 2k + (l/16)%2. A stage whose second group
+// is past the wavefront's last one repeats its first group in those lanes,
+// and their sums are dropped.
+template <unsigned T, int VT, int RING, int KS, int P, bool FULL, bool MULTI>
 __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, const float *__restrict__ x,
     float *__restrict__ y, int rows, int cols, int base, int live, int g0c, int ngc, int accumulate,
     uint8_t *sdig, float4 *smeta, float (*red)[VT][64])
 {
+    static_assert(P == 1 || (P == 2 && VT == 1), "two groups per stage: one 16-row virtual tile");
+    constexpr int RT = kTileRows / P;   // rows per virtual tile
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int h = lane >> 5;
+    const int h = lane >> 5, s = P == 2 ? (lane >> 4) & 1 : 0;
     const size_t row_bytes = tiled_row_bytes<T>(cols);
     const int tiles = (rows + kTileRows - 1) / kTileRows, rlast = rows - kTileRows * (tiles - 1);
     const __amdgpu_buffer_rsrc_t wb = buffer_of(w, (uint32_t)((size_t)rows * row_bytes));
@@ -500,7 +512,8 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
     int vq[VT], vs[VT], vd[VT], R[VT];
 #pragma unroll
     for (int v = 0; v < VT; ++v) {
-        const int row = base + (kTileRows * v + (lane & 31) < live ? kTileRows * v + (lane & 31) : live - 1);
+        const int rl = RT * v + (lane & (RT - 1));
+        const int row = base + (rl < live ? rl : live - 1);
         const int t = row / kTileRows, r = row - kTileRows * t;
         R[v] = t == tiles - 1 ? rlast : kTileRows;
         const int tb = (int)((size_t)kTileRows * t * row_bytes);
@@ -509,50 +522,69 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
         vd[v] = tb + 2 * r;
     }
     const int G = cols / kGroupCols;
-    // This wave's chunk groups: wave + KS k for k < ns.
+    // This wave's chunk groups: wave + KS j for j < ns, in nst stages of P.
     const int ns = wave < ngc ? (ngc - wave + KS - 1) / KS : 0;
+    const int nst = (ns + P - 1) / P;
+    // Stage k of lane half s: its own group P k + s while there is one, else
+    // the stage's first (and stages past the wave's last repeat that one).
+    auto full_of = [&](int k) { return P == 1 || P * k + 1 < ns; };
+    auto j_of = [&](int k) { const int kk = k < nst ? k : nst - 1; return P * kk + (full_of(kk) ? s : 0); };
+    // Lane half s = 1 of a full stage: one group (KS groups of the chunk) on,
+    // in the quant and scale fields (sq) and in Q6_K's d array (sd).
+    constexpr int GB = T == Q6_K ? 208 : kGroupRowBytes<T>;
+    int sq[VT], sd[VT];
+#pragma unroll
+    for (int v = 0; v < VT; ++v) {
+        sq[v] = P == 2 && s ? KS * R[v] * GB : 0;
+        sd[v] = P == 2 && s ? KS * R[v] * 2 : 0;
+    }
+    auto stage_load = [&](MvStage<T>(&st)[VT], int k) {
+        const int kk = k < nst ? k : nst - 1, add = full_of(kk);
+#pragma unroll
+        for (int v = 0; v < VT; ++v)
+            load_rows<T, FULL>(st[v], wb, vq[v] + (add ? sq[v] : 0), vs[v] + (add ? sq[v] : 0), R[v],
+                               g0c + wave + KS * P * kk, vd[v] + (add ? sd[v] : 0), G);
+    };
     float acc[VT];
 #pragma unroll
     for (int v = 0; v < VT; ++v) acc[v] = 0.f;
-    auto gl_of = [&](int k) { return wave + KS * (k < ns ? k : ns - 1); };
-    // 1. x of the first RING groups, then the weights (loads complete in
+    // 1. x of the first RING stages, then the weights (loads complete in
     //    order: what the quantization needs comes first; the barrier puts
-    //    every wavefront's x ahead of all weights). Stages past the wave's
-    //    last group repeat it. The x loads are unconditional, with the group
-    //    in the range-checked vector offset (a wave without groups reads
-    //    zeros): loaded under a condition, their registers would be merged
-    //    after it, and the merge waits for the loads, holding back every
-    //    weight load behind a full memory round trip.
-    float4 px[RING];
+    //    every wavefront's x ahead of all weights). Groups past the wave's
+    //    last repeat it. The x loads are unconditional, with the group in the
+    //    range-checked vector offset (a wave without groups reads zeros):
+    //    loaded under a condition, their registers would be merged after it,
+    //    and the merge waits for the loads, holding back every weight load
+    //    behind a full memory round trip.
+    auto xgroup = [&](int j) { return wave + KS * (j < ns ? j : ns - 1); };
+    float4 px[P * RING];
 #pragma unroll
-    for (int k = 0; k < RING; ++k)
-        px[k] = __builtin_bit_cast(float4, bload16<false>(xb, 16 * lane + 1024 * (ns > 0 ? gl_of(k) : wave), 0));
+    for (int j = 0; j < P * RING; ++j)
+        px[j] = __builtin_bit_cast(float4, bload16<false>(xb, 16 * lane + 1024 * (ns > 0 ? xgroup(j) : wave), 0));
     issue_barrier();
     if (ns > 0) {
         MvStage<T> st[RING][VT];
 #pragma unroll
-        for (int k = 0; k < RING; ++k)
-#pragma unroll
-            for (int v = 0; v < VT; ++v) load_rows<T, FULL>(st[k][v], wb, vq[v], vs[v], R[v], g0c + gl_of(k), vd[v], G);
+        for (int k = 0; k < RING; ++k) stage_load(st[k], k);
 
         // 2. Digits of this wave's groups into LDS.
         const float fmul = block_factor<T>(lane), fcorr = block_correction<T>(lane);
 #pragma unroll
-        for (int k = 0; k < RING; ++k) {
-            asm volatile("" : "+v"(px[k].x), "+v"(px[k].y), "+v"(px[k].z), "+v"(px[k].w) :: "memory");
-            if (k < ns) quantize_group(px[k], gl_of(k), lane, fmul, fcorr, sdig, smeta);
+        for (int j = 0; j < P * RING; ++j) {
+            asm volatile("" : "+v"(px[j].x), "+v"(px[j].y), "+v"(px[j].z), "+v"(px[j].w) :: "memory");
+            if (j < ns) quantize_group(px[j], xgroup(j), lane, fmul, fcorr, sdig, smeta);
         }
         if constexpr (MULTI)
-            for (int k = RING; k < ns; ++k)
-                quantize_group(__builtin_bit_cast(float4, bload16<false>(xb, 16 * lane, 1024 * gl_of(k))), gl_of(k),
+            for (int j = P * RING; j < ns; ++j)
+                quantize_group(__builtin_bit_cast(float4, bload16<false>(xb, 16 * lane, 1024 * xgroup(j))), xgroup(j),
                                lane, fmul, fcorr, sdig, smeta);
         // Each wave reads back only the groups it wrote.
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-        // 3. The ring: stage k holds group i + k of every virtual tile; after
-        //    computing it, it loads group i + k + RING (while there is one).
+        // 3. The ring: stage k holds stage i + k of every virtual tile; after
+        //    computing it, it loads stage i + k + RING (while there is one).
         int aoff[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) aoff[k] = T == Q6_K ? aoff6_of(lane, k) : aoff_of(lane, k);
@@ -561,35 +593,35 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
         auto pass = [&](int i) {
 #pragma unroll
             for (int k = 0; k < RING; ++k) {
-                if (i + k < ns) {
-                    const int gl = KS * (i + k);
+                if (i + k < nst) {
+                    const int gl = KS * j_of(i + k);
                     float part[VT];
                     group_dots<T, VT>(part, st[k], abase + 1024 * gl, aoff, mbase + 8 * gl, h);
+                    const bool keep = full_of(i + k) || s == 0;
 #pragma unroll
-                    for (int v = 0; v < VT; ++v) acc[v] += part[v];
-                    if (MULTI && i + k + RING < ns)
-#pragma unroll
-                        for (int v = 0; v < VT; ++v)
-                            load_rows<T, FULL>(st[k][v], wb, vq[v], vs[v], R[v], g0c + wave + gl + KS * RING, vd[v], G);
+                    for (int v = 0; v < VT; ++v) acc[v] += keep ? part[v] : 0.f;
+                    if (MULTI && i + k + RING < nst) stage_load(st[k], i + k + RING);
                 }
             }
         };
         pass(0);
         if constexpr (MULTI)
-            for (int i = RING; i < ns; i += RING) pass(i);
+            for (int i = RING; i < nst; i += RING) pass(i);
     }
 
     // 4. Lane halves and wavefronts, in a fixed order. Wave 0 sums: lane
-    //    l = 32 v + r takes row r of virtual tile v. All 2 KS partials are
+    //    l = RT v + r takes row r of virtual tile v. All 2 KS partials are
     //    read before the first add, so the reads cost one LDS round trip
     //    (read, wait, add in turn measured 0.1 us slower at the end of every
-    //    launch).
+    //    launch). At P = 2 the two groups of a stage are added first (lanes
+    //    l and l ^ 16).
+    if constexpr (P == 2) acc[0] += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, acc[0]), 0x401F));
 #pragma unroll
     for (int v = 0; v < VT; ++v) red[wave][v][lane] = acc[v];
     __syncthreads();
     if (wave != 0) return;
-    const int v = lane >> 5, r = lane & 31;
-    if (v >= VT || kTileRows * v + r >= live) return;
+    const int v = lane / RT, r = lane & (RT - 1);
+    if (v >= VT || RT * v + r >= live) return;
     float p[2 * KS];
 #pragma unroll
     for (int q = 0; q < KS; ++q) {
@@ -597,14 +629,14 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
         p[2 * q + 1] = red[q][v][r + 32];
     }
     asm volatile("" ::: "memory");
-    float s = p[0] + p[1];
+    float sum = p[0] + p[1];
 #pragma unroll
-    for (int q = 1; q < KS; ++q) s += p[2 * q] + p[2 * q + 1];
-    float *dst = y + base + kTileRows * v + r;
-    *dst = accumulate ? *dst + s : s;
+    for (int q = 1; q < KS; ++q) sum += p[2 * q] + p[2 * q + 1];
+    float *dst = y + base + RT * v + r;
+    *dst = accumulate ? *dst + sum : sum;
 }
 
-template <unsigned T, int VT, int RING, int KS, bool MULTI>
+template <unsigned T, int VT, int RING, int KS, int P, bool MULTI>
 __global__ __launch_bounds__(64 * KS) void matvec_rows(const uint8_t *__restrict__ w, const float *__restrict__ x,
     float *__restrict__ y, int rows, int cols, int rw, int g0c, int ngc, int accumulate)
 {
@@ -618,11 +650,11 @@ __global__ __launch_bounds__(64 * KS) void matvec_rows(const uint8_t *__restrict
     // matrix may be shorter): group and field offsets are scalar.
     const int tiles = (rows + kTileRows - 1) / kTileRows;
     if (rows % kTileRows == 0 || base + live <= kTileRows * (tiles - 1))
-        matvec_rows_body<T, VT, RING, KS, true, MULTI>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig, smeta,
-                                                      red);
+        matvec_rows_body<T, VT, RING, KS, P, true, MULTI>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig,
+                                                         smeta, red);
     else
-        matvec_rows_body<T, VT, RING, KS, false, MULTI>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig, smeta,
-                                                       red);
+        matvec_rows_body<T, VT, RING, KS, P, false, MULTI>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig,
+                                                          smeta, red);
 }
 
 size_t matvec_lds(int ccols)
@@ -658,16 +690,21 @@ int rows_per_workgroup(int rows)
 }
 
 // One launch of matvec_rows over chunk groups [g0, g0 + ng).
-template <unsigned T, int VT, int RING, int KS>
+template <unsigned T, int VT, int RING, int KS, int P = 1>
 void launch_rows_kernel(int wgs, size_t lds, hipStream_t s, const uint8_t *w, const float *xc, float *y, int rows,
     int cols, int rw, int g0, int ng)
 {
-    if ((ng + KS - 1) / KS > RING)
-        hipLaunchKernelGGL((matvec_rows<T, VT, RING, KS, true>), dim3(wgs), dim3(64 * KS), lds, s, w, xc, y, rows, cols,
-                           rw, g0, ng, g0 > 0);
-    else
-        hipLaunchKernelGGL((matvec_rows<T, VT, RING, KS, false>), dim3(wgs), dim3(64 * KS), lds, s, w, xc, y, rows, cols,
-                           rw, g0, ng, g0 > 0);
+    // A chunk has at most kChunkCols / kGroupCols groups: past KS P RING of
+    // them no wavefront needs the refill code.
+    if constexpr (KS * P * RING < kChunkCols / kGroupCols) {
+        if (((ng + KS - 1) / KS + P - 1) / P > RING) {
+            hipLaunchKernelGGL((matvec_rows<T, VT, RING, KS, P, true>), dim3(wgs), dim3(64 * KS), lds, s, w, xc, y, rows,
+                               cols, rw, g0, ng, g0 > 0);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((matvec_rows<T, VT, RING, KS, P, false>), dim3(wgs), dim3(64 * KS), lds, s, w, xc, y, rows, cols,
+                       rw, g0, ng, g0 > 0);
 }
 
 template <unsigned T>
@@ -680,22 +717,35 @@ hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int
         const int ng = groups - g0 < kChunkCols / kGroupCols ? groups - g0 : kChunkCols / kGroupCols;
         const float *xc = x + (size_t)g0 * kGroupCols;
         const size_t lds = matvec_lds(ng * kGroupCols);
-        // Q6_K (37-register stages): one stage per wavefront (two or three
-        // stages at eight wavefronts measured 13-17 % slower on 4096 x
-        // 14336); two tiles per CU take eight wavefronts of up to 256
-        // registers.
+        // Up to 16 rows per CU: two groups per stage (P = 2, 4096 x 11008
+        // Q4_0: 7.53 -> 7.07 us), and a second stage where a wavefront has
+        // three or more groups (4096 x 14336: Q4_K 8.84 -> 7.92 us, Q6_K
+        // 11.19 -> 10.75 us; with one or two it only adds loads). Eight
+        // wavefronts with three or four stages measured 5-12 % slower.
+        const bool deep = (ng + 15) / 16 >= 3;
+        // Q6_K (37-register stages) from 17 rows per CU: one stage per
+        // wavefront (two or three stages at eight wavefronts measured
+        // 13-17 % slower on 4096 x 14336); two tiles per CU take eight
+        // wavefronts of up to 256 registers.
         if constexpr (T == Q6_K) {
-            if (rw <= kTileRows && rpw > 2 * kTileRows)   // one tile per workgroup (128256 x 4096: 84.7 -> 72.5 us)
+            if (rw <= kTileRows / 2 && deep)
+                launch_rows_kernel<T, 1, 2, 16, 2>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
+            else if (rw <= kTileRows / 2)
+                launch_rows_kernel<T, 1, 1, 16, 2>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
+            else if (rw <= kTileRows && rpw > 2 * kTileRows)   // one tile per workgroup (128256 x 4096: 84.7 -> 72.5 us)
                 launch_rows_kernel<T, 1, 1, 8>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
             else if (rw <= kTileRows)
                 launch_rows_kernel<T, 1, 1, 16>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
             else
                 launch_rows_kernel<T, 2, 1, 8>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
         } else {
-            // One stage per wavefront also where it has several groups
-            // (two stages measured 2-10 % slower on 4096 x 11008 and
-            // 4096 x 14336).
-            if (rw <= kTileRows)
+            // One stage per wavefront from 17 rows per CU on, also where it
+            // has several groups (two stages measured 2-10 % slower).
+            if (rw <= kTileRows / 2 && deep)
+                launch_rows_kernel<T, 1, 2, 16, 2>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
+            else if (rw <= kTileRows / 2)
+                launch_rows_kernel<T, 1, 1, 16, 2>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
+            else if (rw <= kTileRows)
                 launch_rows_kernel<T, 1, 1, 16>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
             else
                 launch_rows_kernel<T, 2, 1, 16>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);

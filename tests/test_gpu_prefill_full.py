@@ -14,7 +14,8 @@ backend/core/cpu_backend.c:64-74). Every output is checked:
 
 Also: tokens spanning 2^-40 .. 2^44 in magnitude (one 256-column group
 2^-20 below the rest of its token) through the prefill GEMM and the
-batch-1 matvec under the same two checks; activation outlier channels
+batch-1 matvec (also at the row kernel's stage structures) under the same
+two checks; activation outlier channels
 (2^12, 2^14) at batch 1, 8 and 40 within relative L2 1e-5 of the scalar
 oracle; rows whose last Q8_0/Q4_0 column group is short (800 columns =
 three full groups and one block) at batch 9 and 40.
@@ -99,6 +100,26 @@ def test_matvec_wide_range(compute, oracle, t, rows):
     cols = 4096
     w = synth.weights(t, rows, cols, 95 + t)
     x = wide_range(12, cols, 96 + t)
+    y = np.stack([compute.matvec_typed(w, rows, cols, t, x[k]) for k in range(x.shape[0])])
+    check_all(oracle, w, t, x, rows, cols, y)
+
+
+STAGE_SHAPES = [(300, 11008), (4090, 14336), (1000, 20480), (4096, 8448), (4096, 8192)]
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K, Q6_K], ids=lambda t: TYPE_NAMES[t])
+@pytest.mark.parametrize("rows,cols", STAGE_SHAPES,
+                         ids=["two-rows-per-cu-odd-groups", "ragged-tile-mixed-stages", "chunked-columns",
+                              "thirty-three-groups", "thirty-two-groups"])
+def test_matvec_stage_shapes(compute, oracle, t, rows, cols):
+    """The batch-1 row kernel at up to 16 rows per CU, where a stage holds
+    two of a wavefront's column groups: wavefronts with an odd number of
+    groups (the last stage's second group absent), with one, two and three or
+    more groups (one stage, or two without a refill), a ragged last
+    workgroup and 32-row tile, and rows wider than one launch's column chunk;
+    single tokens across the whole exponent range."""
+    w = synth.weights(t, rows, cols, 97 + t)
+    x = wide_range(3, cols, 98 + t)
     y = np.stack([compute.matvec_typed(w, rows, cols, t, x[k]) for k in range(x.shape[0])])
     check_all(oracle, w, t, x, rows, cols, y)
 

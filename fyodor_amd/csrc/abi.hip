@@ -136,8 +136,9 @@ void *static_scratch()
 // multiple of its 32-token tiles), or 0 if not even 32 do.
 size_t static_chunk_tokens(unsigned type, size_t cols)
 {
-    const size_t per32 = prefill_workspace(type, (int)cols, 32);
-    return per32 ? kStaticScratchBytes / per32 * 32 : 0;
+    // Whole 64-token blocks: the workspace rounds the batch up to them.
+    const size_t per64 = prefill_workspace(type, (int)cols, 64);
+    return per64 ? kStaticScratchBytes / per64 * 64 : 0;
 }
 
 }  // namespace
@@ -196,14 +197,14 @@ NYA_HIP_EXPORT int nya_hip_matmul_static(uintptr_t w, unsigned type, size_t rows
     if (!ws) return -(int)hipErrorInvalidSymbol;
     // The prefill GEMM runs in token chunks whose workspace fits the array
     // (every token is independent of the others): `parts` chunks of nearly
-    // equal size, each above half the array's capacity (at least 16 tokens),
+    // equal size, each above half the array's capacity (at least 32 tokens),
     // so every chunk stays on the GEMM and every token gets the same result
     // as through nya_hip_matmul. Every other path needs at most a few hundred
     // KiB (the small-N digits of one 16384-column chunk).
     size_t parts = 1;
     if (use_prefill(type, cols, batch)) {
         const size_t fit = static_chunk_tokens(type, cols);
-        if (fit < 32) return NYA_HIP_STATUS_SCRATCH;
+        if (fit < 64) return NYA_HIP_STATUS_SCRATCH;
         parts = (batch + fit - 1) / fit;
     }
     for (size_t part = 0, done = 0; part < parts; ++part) {

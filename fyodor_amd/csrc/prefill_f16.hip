@@ -45,11 +45,13 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
-constexpr int kTokens = 32;       // tokens per workgroup = MFMA A rows
+constexpr int kTokens = 32;       // tokens per token tile = MFMA A rows
 constexpr int kPairPitch = 1056;  // LDS bytes per token pair of one piece (1 KiB + 32)
 constexpr int kPieceBytes = kTokens / 2 * kPairPitch;
 constexpr int kSumBytes = 1024;   // Q4_K block sums of one group: 32 tokens x 2 halves x 16 bytes
-constexpr int kBufBytes = 2 * kPieceBytes + kSumBytes;
+constexpr int kTileBytes = 2 * kPieceBytes + kSumBytes;   // one token tile of one group
+// One LDS buffer holds a group for the workgroup's TW token tiles.
+template <int TW> constexpr int kBufBytes = TW * kTileBytes;
 
 // ---- activation pieces ---------------------------------------------------
 // Workspace for np tokens (np a multiple of 32): hi[np][cols], lo[np][cols]
@@ -153,16 +155,18 @@ __device__ __forceinline__ void lds_copy16(const void *src, lds_u8 *dst)
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
 }
 
-// Copies of group g into LDS buffer `buf` issued by this wavefront (one of RT):
-// token pairs (16 / RT) wave .. (16 / RT) wave + 16 / RT - 1 of both pieces (lane l: token 2q + (l & 1),
-// 16-byte chunk l >> 1 of the group's row, to byte 16 l of the pair), and for
-// Q4_K (wavefront 0) the 32 tokens' block sums (lane l: token l % 32, half
-// l / 32). Columns past a short last Q8_0/Q4_0 group are clamped (those
-// blocks are skipped).
-template <int RT>
+// Copies of group g into LDS buffer `buf` issued by this wavefront (one of
+// RT), for each of the TW token tiles (tile tt at buf + kTileBytes tt):
+// token pairs 16 TW / RT per wavefront of both pieces (lane l: token
+// 2q + (l & 1), 16-byte chunk l >> 1 of the group's row, to byte 16 l of the
+// pair), and for Q4_K tile (wavefront % TW)'s block sums (lane l: token
+// l % 32, half l / 32). Columns past a short last Q8_0/Q4_0 group are
+// clamped (those blocks are skipped).
+template <int RT, int TW>
 __device__ __forceinline__ void copy_group(lds_u8 *__restrict__ buf, const Pieces &p, int cols, int m0, int g, bool sums)
 {
-    constexpr int kPairs = 16 / RT;   // token pairs per wavefront
+    constexpr int kPairs = 16 * TW / RT;   // token pairs per wavefront, over all token tiles
+    static_assert(kPairs >= 1 && 16 * TW % RT == 0, "whole token pairs per wavefront");
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int col = 256 * g + 8 * (lane >> 1);
     col = col < cols ? col : cols - 8;
@@ -170,13 +174,17 @@ __device__ __forceinline__ void copy_group(lds_u8 *__restrict__ buf, const Piece
     for (int piece = 0; piece < 2; ++piece)
 #pragma unroll
         for (int k = 0; k < kPairs; ++k) {
-            const int q = kPairs * wave + k;
-            const _Float16 *src = (piece ? p.lo : p.hi) + (size_t)(m0 + 2 * q + (lane & 1)) * cols + col;
-            lds_copy16(src, buf + piece * kPieceBytes + q * kPairPitch);
+            const int q = kPairs * wave + k, tt = q / 16, qq = q % 16;   // pair qq of token tile tt
+            const _Float16 *src = (piece ? p.lo : p.hi) + (size_t)(m0 + 32 * tt + 2 * qq + (lane & 1)) * cols + col;
+            lds_copy16(src, buf + kTileBytes * tt + piece * kPieceBytes + qq * kPairPitch);
         }
-    if (sums && wave == 0) {
-        const float *src = p.bsum + ((size_t)(m0 + (lane & 31)) * (cols / 256) + g) * 8 + 4 * (lane >> 5);
-        lds_copy16(src, buf + 2 * kPieceBytes);
+    if (sums) {
+        // Every wavefront copies (wavefronts past TW the same bytes to the
+        // same place again): a copy under a wavefront condition leaves a
+        // branch after which the compiler waits for every load.
+        const int tt = wave % TW;
+        const float *src = p.bsum + ((size_t)(m0 + 32 * tt + (lane & 31)) * (cols / 256) + g) * 8 + 4 * (lane >> 5);
+        lds_copy16(src, buf + kTileBytes * tt + 2 * kPieceBytes);
     }
 }
 
@@ -225,27 +233,113 @@ __device__ __forceinline__ h8 b_operand(const WStage<T> &w, int j, int kappa, in
     return __builtin_bit_cast(h8, (u32x4){v[0], v[1], v[2], v[3]});
 }
 
+// Weight loads of one stage (the layout of formats.h, as load_weights in
+// blockdot.h reads it), as raw buffer loads over the tile. FULLK (every
+// group of the row a full 256-column group): always exactly kWeightLoads of
+// them; the wait before each barrier leaves that many in flight and counts
+// on them being the last vector memory instructions, so that it covers every
+// copy issued before them. Rows with a short last Q8_0/Q4_0 group issue
+// another count for that group and wait for all loads before each barrier.
+template <unsigned T, bool FULLK>
+constexpr int kWeightLoads = !FULLK ? 0 : T == Q8_0 ? 9 : 5;
+
+template <unsigned T, bool FULLK>
+__device__ __forceinline__ void load_stage(WStage<T> &w, __amdgpu_buffer_rsrc_t rs, const Lane &L, int g)
+{
+    auto ld = [&](int off) { return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0)); };
+    const int R = L.R, r = L.r, h = L.h;
+    if constexpr (T == Q4_K) {
+        const int b = 144 * R * g;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) w.q[p] = ld(b + 32 * R * p + 16 * R * h + 16 * r);
+        w.sl = ld(b + 128 * R + 16 * r);
+    } else {
+        constexpr int quant = T == Q8_0 ? 32 : 16;
+        const int b = (quant + 2) * 8 * R * g;
+        auto full = [&]() {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (T == Q4_0 && j >= 4) w.q[j] = (u32x4){};
+                else w.q[j] = ld(b + 32 * R * j + 16 * R * h + 16 * r);
+            }
+            const u32x4 d = ld(b + 8 * quant * R + 16 * r);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) w.d[k] = k < 4 ? d[k] : 0u;
+        };
+        if constexpr (FULLK) {
+            full();
+        } else {
+            const int nb = group_blocks(L, g);
+            if (nb == 8) {
+                full();
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int jj = j < nb ? j : nb - 1;
+                    w.q[j] = ld(b + quant * R * jj + (T == Q8_0 ? 16 * R * h : 0) + 16 * r);
+                    w.d[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, b + quant * R * nb + 2 * R * jj + 2 * r, 0, 0);
+                }
+            }
+        }
+    }
+}
+
 // Step g of prefill_f16: copy group g + 1 into the other buffer (its readers
 // passed the last barrier), compute group g from `cur` (loaded two steps
 // earlier), refill `cur` with group g + 2, wait for this wavefront's copies,
-// barrier. Copies and loads are unconditional (clamped to the last group): a
-// branch would leave a path with another count of loads in flight. The two
-// buffers come in as restrict pointers, which lets the compiler see that this
-// step's LDS reads do not depend on the copies it issues.
-template <unsigned T, int RT>
-__device__ __forceinline__ void group_step(WStage<T> &cur, f32x16 &acc, lds_u8 *__restrict__ buf,
-    lds_u8 *__restrict__ nbuf, const Pieces &p, const Lane &L, int a_off, int cols, int m0, int g, int groups)
+// barrier. Each B operand made from the weights serves the TW token tiles
+// (two MFMAs each, one per activation piece). Copies and loads are
+// unconditional (clamped to the last group): a branch would leave a path
+// with another count of loads in flight. The two buffers come in as restrict
+// pointers, which lets the compiler see that this step's LDS reads do not
+// depend on the copies it issues.
+template <unsigned T, int RT, int TW, bool FULLK>
+__device__ __forceinline__ void group_step(WStage<T> &cur, f32x16 (&acc)[TW], lds_u8 *__restrict__ buf,
+    lds_u8 *__restrict__ nbuf, const Pieces &p, const Lane &L, __amdgpu_buffer_rsrc_t rs, int a_off, int cols, int m0,
+    int g, int groups)
 {
     constexpr bool sums = T == Q4_K;
-    constexpr int kWeightLoads = T == Q4_K ? 5 : 16;
-    constexpr int kWaitCopies = (kWeightLoads & 15) | ((kWeightLoads >> 4) << 14) | (7 << 4) | (15 << 8);
+    // s_waitcnt immediate: vmcnt = kLoads (bits 3:0 and 15:14), expcnt and
+    // lgkmcnt at their maxima (no wait).
+    constexpr int kLoads = kWeightLoads<T, FULLK>;
+    constexpr int kWaitCopies = (kLoads & 15) | ((kLoads >> 4) << 14) | (7 << 4) | (15 << 8);
+    static_assert(kLoads < 64, "vmcnt field");
     const int lane = threadIdx.x & 63;
-    copy_group<RT>(nbuf, p, cols, m0, g + 1 < groups ? g + 1 : g, sums);
-    const lds_u8 *xh = buf + a_off, *xl = xh + kPieceBytes;
+    copy_group<RT, TW>(nbuf, p, cols, m0, g + 1 < groups ? g + 1 : g, sums);
+    // The weight loads below stay after the copies, in the compiler's view of
+    // memory (the fence; the weights are not a restrict pointer) and in the
+    // schedule.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    const lds_u8 *xh = buf + a_off;
     if constexpr (T == Q4_K) {
-        f32x16 C = {};
+        f32x16 C[TW];
+#pragma unroll
+        for (int tt = 0; tt < TW; ++tt) C[tt] = (f32x16){};
+        // Two token tiles: the A operands of block j + 1 are read while block
+        // j's MFMAs run (xa[j % 2]: [token tile][K slice kappa][piece]). One
+        // token tile (128 registers at eight wavefronts) reads each block's
+        // operands in the block: the second set would spill.
+        constexpr int kAhead = TW == 2 ? 1 : 0;
+        h8 xa[2][TW][2][2];
+        auto read_a = [&](int j, h8 (&dst)[TW][2][2]) {
+#pragma unroll
+            for (int tt = 0; tt < TW; ++tt)
+#pragma unroll
+                for (int kappa = 0; kappa < 2; ++kappa)
+#pragma unroll
+                    for (int pc = 0; pc < 2; ++pc)
+                        dst[tt][kappa][pc] =
+                            *(const h8 *)(xh + kTileBytes * tt + 128 * j + 32 * kappa + kPieceBytes * pc);
+        };
+        if constexpr (kAhead) {
+            read_a(0, xa[0]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
+            if (!kAhead) read_a(j, xa[j & 1]);
+            else if (j < 7) read_a(j + 1, xa[(j + 1) & 1]);
             const uint32_t own = cur.sl[j >> 1];
             const float scf = (float)((own >> (12 * (j & 1))) & 63u);
             const h2 sc2 = {(_Float16)scf, (_Float16)scf};
@@ -253,25 +347,44 @@ __device__ __forceinline__ void group_step(WStage<T> &cur, f32x16 &acc, lds_u8 *
 #pragma unroll
             for (int kappa = 0; kappa < 2; ++kappa) {
                 const h8 b = b_operand<T>(cur, j, kappa, L.h, sc2, nsc2);
-                const int off = 128 * j + 32 * kappa;
-                C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xh + off), b, C, 0, 0, 0);
-                C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xl + off), b, C, 0, 0, 0);
+#pragma unroll
+                for (int tt = 0; tt < TW; ++tt) {
+                    C[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa[j & 1][tt][kappa][0], b, C[tt], 0, 0, 0);
+                    C[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa[j & 1][tt][kappa][1], b, C[tt], 0, 0, 0);
+                }
+            }
+            // Two token tiles: each MFMA followed by four VALU instructions
+            // (the next operands) and one LDS read of the next block
+            // (Q4_K 14336 x 4096 x 512: 172.6 -> 164.9 us; the compiler's own
+            // order reads two operands, waits for them, then issues one
+            // MFMA). One token tile keeps the compiler's order (this one
+            // measured 36 % slower on 4096 x 4096 x 512).
+            if constexpr (TW == 2) {
+#pragma unroll
+                for (int q = 0; q < 4 * TW; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
+                    if (j < 7) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
+                }
             }
         }
         float d, dmin;
         group_scales<T>(cur, d, dmin);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] += d * C[r];
         // Minimums: acc -= dmin * sum_j m_j * (sum of x s over block j), on
         // an fp32 MFMA accumulating into acc (lane l: A = the sum over
         // block 2s + l/32 of token l % 32, B = -dmin * m of that block for
         // row l % 32).
-        const float4 ys = *(const float4 *)(buf + 2 * kPieceBytes + 16 * lane);
-        const float ya[4] = {ys.x, ys.y, ys.z, ys.w};
+        float bm[4];
 #pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2) {
-            const float m = (float)((cur.sl[s2] >> (12 * L.h + 6)) & 63u);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ya[s2], -dmin * m, acc, 0, 0, 0);
+        for (int s2 = 0; s2 < 4; ++s2) bm[s2] = -dmin * (float)((cur.sl[s2] >> (12 * L.h + 6)) & 63u);
+#pragma unroll
+        for (int tt = 0; tt < TW; ++tt) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[tt][r] += d * C[tt][r];
+            const float4 ys = *(const float4 *)(buf + kTileBytes * tt + 2 * kPieceBytes + 16 * lane);
+            const float ya[4] = {ys.x, ys.y, ys.z, ys.w};
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) acc[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(ya[s2], bm[s2], acc[tt], 0, 0, 0);
         }
     } else {
         // Per-block scales; a short last group has its own layout (formats.h).
@@ -281,37 +394,50 @@ __device__ __forceinline__ void group_step(WStage<T> &cur, f32x16 &acc, lds_u8 *
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 if (j >= nb) break;
-                f32x16 C = {};
+                f32x16 C[TW];
+#pragma unroll
+                for (int tt = 0; tt < TW; ++tt) C[tt] = (f32x16){};
 #pragma unroll
                 for (int kappa = 0; kappa < 2; ++kappa) {
                     const h8 b = b_operand<T, FULL>(cur, j, kappa, L.h, (h2){}, (h2){});
                     const int off = 128 * j + 32 * kappa;
-                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xh + off), b, C, 0, 0, 0);
-                    C = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(xl + off), b, C, 0, 0, 0);
+#pragma unroll
+                    for (int tt = 0; tt < TW; ++tt) {
+                        const lds_u8 *x = xh + kTileBytes * tt + off;
+                        C[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)x, b, C[tt], 0, 0, 0);
+                        C[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const h8 *)(x + kPieceBytes), b, C[tt], 0, 0, 0);
+                    }
                 }
                 const float dj = f16_to_f32(block_d<FULL>(cur, j));
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[r] += dj * C[r];
+                for (int tt = 0; tt < TW; ++tt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[tt][r] += dj * C[tt][r];
             }
         };
-        if (group_blocks(L, g) == 8) blocks(std::true_type{});
+        if (FULLK || group_blocks(L, g) == 8) blocks(std::true_type{});
         else blocks(std::false_type{});
     }
-    load_weights<T>(cur, L, g + 2 < groups ? g + 2 : groups - 1);
+    load_stage<T, FULLK>(cur, rs, L, g + 2 < groups ? g + 2 : groups - 1);
     // This wavefront's copies are complete; then every wavefront's are,
-    // past the barrier.
+    // past the barrier. (The fence keeps the loads above before the wait.)
+    asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(kWaitCopies);
     barrier();
 }
 
-// RT wavefronts (32-row tiles) per workgroup: 8 (two workgroups per CU, four
-// wavefronts per SIMD, at most 128 VGPRs) for Q4_K when the grid fills the
-// chip, else 4 (twice the workgroups).
-template <unsigned T, int RT>
-__global__ __launch_bounds__(64 * RT) __attribute__((amdgpu_waves_per_eu(RT / 2, RT / 2))) void prefill_f16(const uint8_t *__restrict__ w, Pieces p, float *__restrict__ y,
-    int rows, int cols, int batch, int token_blocks)
+// RT wavefronts (32-row tiles) per workgroup, TW token tiles of 32 per
+// wavefront. TW = 1: 8 wavefronts (two workgroups per CU, four wavefronts
+// per SIMD, at most 128 VGPRs) for Q4_K when the grid fills the chip, else 4
+// (twice the workgroups). TW = 2: the 64 tokens' double buffer takes 139 KB
+// of LDS, one workgroup per CU, 8 wavefronts of up to 256 VGPRs.
+// The weights are deliberately not a restrict pointer: the compiler may
+// then not move their loads across the memory fences of group_step.
+template <unsigned T, int RT, int TW, bool FULLK>
+__global__ __launch_bounds__(64 * RT) __attribute__((amdgpu_waves_per_eu(TW == 1 ? RT / 2 : RT / 4, TW == 1 ? RT / 2 : RT / 4))) void prefill_f16(
+    const uint8_t *w, Pieces p, float *__restrict__ y, int rows, int cols, int batch, int token_blocks)
 {
-    __shared__ __align__(16) uint8_t smem0[kBufBytes], smem1[kBufBytes];
+    __shared__ __align__(16) uint8_t smem0[kBufBytes<TW>], smem1[kBufBytes<TW>];
     lds_u8 *const B0 = (lds_u8 *)smem0, *const B1 = (lds_u8 *)smem1;
     constexpr bool sums = T == Q4_K;
     // The wavefront index is uniform: keeping it scalar keeps the tile base
@@ -321,7 +447,7 @@ __global__ __launch_bounds__(64 * RT) __attribute__((amdgpu_waves_per_eu(RT / 2,
     const int by = blockIdx.x % token_blocks, bx = blockIdx.x / token_blocks;
     const int tile_raw = RT * bx + wave;
     const int tile = tile_raw < tiles ? tile_raw : tiles - 1;
-    const int m0 = kTokens * by, n = batch - m0;   // tokens left (> 0)
+    const int m0 = kTokens * TW * by, n = batch - m0;   // tokens left (> 0)
     const int R = rows - kTileRows * tile < kTileRows ? rows - kTileRows * tile : kTileRows;
     Lane L;
     L.tile = w + (size_t)kTileRows * tile * tiled_row_bytes<T>(cols);
@@ -332,75 +458,110 @@ __global__ __launch_bounds__(64 * RT) __attribute__((amdgpu_waves_per_eu(RT / 2,
     L.groups = (cols + kGroupCols - 1) / kGroupCols;
     L.blocks = cols / 32;
     const int groups = L.groups;
-
-    // Vector memory instructions of one load_weights call: the wait before
-    // each barrier leaves exactly these (the next-but-one group's weights) in
-    // flight and so covers every copy issued before them.
-    constexpr int kWeightLoads = T == Q4_K ? 5 : 16;
-    // s_waitcnt immediate: vmcnt = kWeightLoads (bits 3:0 and 15:14), expcnt
-    // and lgkmcnt at their maxima (no wait).
-    constexpr int kWaitCopies = (kWeightLoads & 15) | ((kWeightLoads >> 4) << 14) | (7 << 4) | (15 << 8);
-    static_assert(kWeightLoads < 64, "vmcnt field");
+    // The tile's bytes (below 2^31: the library declines larger matrices).
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(L.tile), (short)0, (int)((size_t)R * tiled_row_bytes<T>(cols)), 0x00020000);
 
     WStage<T> st[2];
-    copy_group<RT>(B0, p, cols, m0, 0, sums);
-    load_weights<T>(st[0], L, 0);
-    load_weights<T>(st[1], L, groups > 1 ? 1 : 0);
-    __builtin_amdgcn_s_waitcnt(kWaitCopies);
+    // Both stages and the first copies complete before the loop, so the
+    // first step reads only complete registers (after LDS copies are issued,
+    // the compiler waits for all vector memory, those copies included, before
+    // the first use of a register still loading; later steps read stages
+    // completed by an earlier step's wait).
+    copy_group<RT, TW>(B0, p, cols, m0, 0, sums);
+    asm volatile("" ::: "memory");
+    load_stage<T, FULLK>(st[0], rs, L, 0);
+    load_stage<T, FULLK>(st[1], rs, L, groups > 1 ? 1 : 0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0);
     barrier();
 
     // A operand of token r = lane % 32: columns 32j + 16h + 8kappa of the
     // group sit at pair r / 2, byte 32 (4j + 2h + kappa) + 16 (r & 1).
     const int a_off = kPairPitch * ((lane & 31) >> 1) + 16 * (lane & 1) + 64 * L.h;
-    f32x16 acc = {};
-    for (int g = 0; g < groups; g += 2) {
-        group_step<T, RT>(st[0], acc, B0, B1, p, L, a_off, cols, m0, g, groups);
-        if (g + 1 < groups) group_step<T, RT>(st[1], acc, B1, B0, p, L, a_off, cols, m0, g + 1, groups);
+    f32x16 acc[TW];
+#pragma unroll
+    for (int tt = 0; tt < TW; ++tt) acc[tt] = (f32x16){};
+    // Both steps of a pass unconditionally, an odd last group after the
+    // loop: with the second step under a condition, the loop header would
+    // merge a path on which stage 0's loads are still in flight, and the
+    // compiler would wait for every load (the next group's copies included)
+    // before each first step.
+    int g = 0;
+    for (; g + 1 < groups; g += 2) {
+        group_step<T, RT, TW, FULLK>(st[0], acc, B0, B1, p, L, rs, a_off, cols, m0, g, groups);
+        group_step<T, RT, TW, FULLK>(st[1], acc, B1, B0, p, L, rs, a_off, cols, m0, g + 1, groups);
     }
+    if (g < groups) group_step<T, RT, TW, FULLK>(st[0], acc, B0, B1, p, L, rs, a_off, cols, m0, g, groups);
 
     if (tile_raw >= tiles || (lane & 31) >= R) return;
     const int row = kTileRows * tile + (lane & 31);
-    // D register r of lane l is token 8 (r / 4) + 4 (l / 32) + r % 4.
+    // D register r of lane l is token 8 (r / 4) + 4 (l / 32) + r % 4 of its
+    // token tile.
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int t = 8 * (r >> 2) + 4 * L.h + (r & 3);
-        if (t < n) y[(size_t)(m0 + t) * rows + row] = acc[r] * p.inv[m0 + t];
-    }
+    for (int tt = 0; tt < TW; ++tt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = 32 * tt + 8 * (r >> 2) + 4 * L.h + (r & 3);
+            if (t < n) y[(size_t)(m0 + t) * rows + row] = acc[tt][r] * p.inv[m0 + t];
+        }
 }
 
 }  // namespace
 
 bool prefill_f16_supported(unsigned type) { return type == Q4_K || type == Q8_0 || type == Q4_0; }
 
+// The pieces of the batch rounded up to 64 tokens (whole token blocks of
+// either kernel shape).
 size_t prefill_f16_workspace(int cols, int batch)
 {
-    const size_t np = ((size_t)batch + kTokens - 1) / kTokens * kTokens;
+    const size_t np = ((size_t)batch + 2 * kTokens - 1) / (2 * kTokens) * (2 * kTokens);
     return np * ((size_t)4 * cols + (size_t)(cols / 32) * 4 + 4);
 }
 
 hipError_t launch_prefill_f16(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,
     int batch, void *workspace, hipStream_t s)
 {
-    const int np = (batch + kTokens - 1) / kTokens * kTokens;
+    const int np = (batch + 2 * kTokens - 1) / (2 * kTokens) * (2 * kTokens);
     const Pieces p = pieces_of(workspace, cols, np);
     hipLaunchKernelGGL(split_x, dim3((unsigned)batch), dim3(256), 0, s, x, cols, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int tiles = (rows + kTileRows - 1) / kTileRows;
-    const int tb = np / kTokens;
-    // Q8_0/Q4_0 stages (16 loads) do not fit 128 VGPRs without spilling:
-    // four-wavefront workgroups only.
+    const bool fullk = cols % kGroupCols == 0;
+    // Two token tiles per wavefront (each weight operand serves four MFMAs)
+    // where one workgroup per CU of 256 rows x 64 tokens fills the chip.
+    const int tb2 = (batch + 2 * kTokens - 1) / (2 * kTokens);
+    const int tb = (batch + kTokens - 1) / kTokens;
+    const bool pair = (tiles + 7) / 8 * tb2 >= 256;
+    // One token tile: Q8_0/Q4_0 stages (16 loads) do not fit 128 VGPRs
+    // without spilling: four-wavefront workgroups only.
     const bool wide = type == Q4_K && (tiles + 7) / 8 * tb >= 256;
+    const dim3 grid2((unsigned)((tiles + 7) / 8 * tb2));
     const dim3 grid((unsigned)((tiles + (wide ? 7 : 3)) / (wide ? 8 : 4) * tb));
+#define FY_PREFILL(TT, RTT, TWW, FK, G, TB) \
+    hipLaunchKernelGGL((prefill_f16<TT, RTT, TWW, FK>), G, dim3(64 * RTT), 0, s, w, p, y, rows, cols, batch, TB)
     switch (type) {
     case Q4_K:
-        if (wide) hipLaunchKernelGGL((prefill_f16<Q4_K, 8>), grid, dim3(512), 0, s, w, p, y, rows, cols, batch, tb);
-        else hipLaunchKernelGGL((prefill_f16<Q4_K, 4>), grid, dim3(256), 0, s, w, p, y, rows, cols, batch, tb);
+        if (pair) FY_PREFILL(Q4_K, 8, 2, true, grid2, tb2);
+        else if (wide) FY_PREFILL(Q4_K, 8, 1, true, grid, tb);
+        else FY_PREFILL(Q4_K, 4, 1, true, grid, tb);
         break;
-    case Q8_0: hipLaunchKernelGGL((prefill_f16<Q8_0, 4>), grid, dim3(256), 0, s, w, p, y, rows, cols, batch, tb); break;
-    case Q4_0: hipLaunchKernelGGL((prefill_f16<Q4_0, 4>), grid, dim3(256), 0, s, w, p, y, rows, cols, batch, tb); break;
+    case Q8_0:
+        if (pair && fullk) FY_PREFILL(Q8_0, 8, 2, true, grid2, tb2);
+        else if (pair) FY_PREFILL(Q8_0, 8, 2, false, grid2, tb2);
+        else if (fullk) FY_PREFILL(Q8_0, 4, 1, true, grid, tb);
+        else FY_PREFILL(Q8_0, 4, 1, false, grid, tb);
+        break;
+    case Q4_0:
+        if (pair && fullk) FY_PREFILL(Q4_0, 8, 2, true, grid2, tb2);
+        else if (pair) FY_PREFILL(Q4_0, 8, 2, false, grid2, tb2);
+        else if (fullk) FY_PREFILL(Q4_0, 4, 1, true, grid, tb);
+        else FY_PREFILL(Q4_0, 4, 1, false, grid, tb);
+        break;
     default: return hipErrorInvalidValue;
     }
+#undef FY_PREFILL
     return hipGetLastError();
 }
 

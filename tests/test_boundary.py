@@ -190,13 +190,14 @@ def test_pack_is_the_specified_permutation(kernels, t, rows, cols):
 def test_prefill_dispatch_and_workspace():
     """Batch 1 needs no workspace; batches of 2..8 need the activation digits
     of a padded token count; batches above 8 go to the prefill GEMM: fp16
-    activation pieces for Q4_K/Q8_0/Q4_0 (per token, rounded up to 32
+    activation pieces for Q4_K/Q8_0/Q4_0 (per token, rounded up to 64
     tokens: two fp16 planes, the 32-column block sums and the scale), int8
-    digits for Q6_K; dense types need none (nothing is launched)."""
+    digits for Q6_K (rounded up to 32 tokens); dense types need none
+    (nothing is launched)."""
     kern = Kernels()
 
     def pieces(cols, batch):
-        np_ = -(-batch // 32) * 32
+        np_ = -(-batch // 64) * 64
         return np_ * (4 * cols + cols // 32 * 4 + 4)
 
     for t in (Q4_0, Q8_0, Q4_K, Q6_K):

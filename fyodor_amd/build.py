@@ -19,7 +19,8 @@ ROOT = Path(__file__).resolve().parent
 REPO = ROOT.parent
 LIB = ROOT / "lib"
 CSRC = ROOT / "csrc"
-HIP_SOURCES = ["abi.hip", "dense.hip", "smalln.hip", "matvec.hip", "prefill.hip", "prefill_f16.hip", "pack.cpp"]
+HIP_SOURCES = ["abi.hip", "dense.hip", "smalln.hip", "matvec.hip", "prefill.hip", "prefill_f16.hip", "resident.hip",
+               "pack.cpp"]
 C_SOURCES = ["core/compute.c", "core/vendor.c", "rocm/rocm.c"]
 
 HIPCC_FLAGS = [

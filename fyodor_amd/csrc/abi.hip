@@ -242,4 +242,64 @@ NYA_HIP_EXPORT int nya_hip_read(uintptr_t src, size_t bytes, uintptr_t sink, uin
     return status(launch_read((const uint4 *)src, bytes / 16, (unsigned *)sink, (hipStream_t)stream));
 }
 
+// ---- resident decoder steps ----------------------------------------------
+
+// fp32 device vectors: non-null and 4-byte aligned.
+static bool vec(uintptr_t p) { return p && !(p & 3u); }
+static bool count_ok(size_t n) { return n && n <= (size_t)INT_MAX; }
+
+NYA_HIP_EXPORT int nya_hip_dequant_row(uintptr_t w, unsigned type, size_t rows, size_t cols, size_t row, uintptr_t out,
+    uintptr_t stream)
+{
+    format_info f;
+    if (!w || !vec(out) || !format_of(type, &f) || !count_ok(rows) || !count_ok(cols) || cols % f.block ||
+        row >= rows)
+        return 1;
+    const size_t row_bytes = cols / f.block * f.bytes;
+    return status(launch_dequant_row((const uint8_t *)w, type, row_bytes, row, (int)cols, (float *)out,
+                                     (hipStream_t)stream));
+}
+
+NYA_HIP_EXPORT int nya_hip_rms_norm(uintptr_t x, uintptr_t residual, uintptr_t weight, uintptr_t out, size_t n,
+    float epsilon, uintptr_t stream)
+{
+    if (!vec(x) || !vec(out) || (residual & 3u) || (weight & 3u) || !count_ok(n) || !(epsilon >= 0.f)) return 1;
+    return status(launch_rms_norm((float *)x, (const float *)residual, (const float *)weight, (float *)out, (int)n,
+                                  epsilon, (hipStream_t)stream));
+}
+
+NYA_HIP_EXPORT int nya_hip_rope(uintptr_t v, size_t heads, size_t width, uintptr_t frequencies, size_t position,
+    uintptr_t stream)
+{
+    if (!vec(v) || !vec(frequencies) || !count_ok(heads) || !count_ok(width) || width % 2 ||
+        heads > (size_t)INT_MAX / width || position > (size_t)INT_MAX)
+        return 1;
+    return status(launch_rope((float *)v, (int)heads, (int)width, (const float *)frequencies, (int)position,
+                              (hipStream_t)stream));
+}
+
+NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, uintptr_t keys, uintptr_t values, uintptr_t out, uintptr_t scores,
+    size_t heads, size_t kv_heads, size_t width, size_t length, float scale, uintptr_t stream)
+{
+    if (!vec(q) || !vec(keys) || !vec(values) || !vec(out) || !vec(scores) || !count_ok(heads) ||
+        !count_ok(kv_heads) || !count_ok(width) || !count_ok(length) || heads % kv_heads ||
+        kv_heads > (size_t)INT_MAX / width || heads > (size_t)INT_MAX / length)
+        return 1;
+    return status(launch_attention((const float *)q, (const float *)keys, (const float *)values, (float *)out,
+                                   (float *)scores, (int)heads, (int)kv_heads, (int)width, (int)length, scale,
+                                   (hipStream_t)stream));
+}
+
+NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, uintptr_t up, size_t n, uintptr_t stream)
+{
+    if (!vec(gate) || !vec(up) || !count_ok(n)) return 1;
+    return status(launch_silu_mul((float *)gate, (const float *)up, (int)n, (hipStream_t)stream));
+}
+
+NYA_HIP_EXPORT int nya_hip_add(uintptr_t x, uintptr_t r, size_t n, uintptr_t stream)
+{
+    if (!vec(x) || !vec(r) || !count_ok(n)) return 1;
+    return status(launch_add((float *)x, (const float *)r, (int)n, (hipStream_t)stream));
+}
+
 }  // extern "C"

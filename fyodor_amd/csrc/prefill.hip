@@ -85,8 +85,9 @@ __device__ __forceinline__ void fetch_group(AFetch<T> &f, const uint8_t *__restr
     f.m = meta[(size_t)xg * np + m0 + e % kTokens<T>];
 }
 
-// Position of token t (0..31) in the permuted scale order.
-__device__ __forceinline__ int tau_inv(int t) { return 8 * (t >> 3) + 4 * (t & 1) + ((t >> 1) & 3); }
+// Position of token t (0..31) in the permuted scale order (used by the
+// 32-token formats; only Q6_K is launched on this kernel now).
+[[maybe_unused]] __device__ __forceinline__ int tau_inv(int t) { return 8 * (t >> 3) + 4 * (t & 1) + ((t >> 1) & 3); }
 
 template <unsigned T>
 __device__ __forceinline__ void store_group(Staging<T> &s, int buf, const AFetch<T> &f)

@@ -126,6 +126,50 @@ NYA_HIP_EXPORT int nya_hip_copy(uintptr_t dst, uintptr_t src, size_t bytes, uint
 #define NYA_HIP_READ_SINK_BYTES 4096
 NYA_HIP_EXPORT int nya_hip_read(uintptr_t src, size_t bytes, uintptr_t sink, uintptr_t stream);
 
+/* ---- resident decoder steps ------------------------------------------------
+ * The vector steps of one decoder token, for a provider that keeps a whole
+ * model's token forward on the device (the resident plan of
+ * backend/include/compute.h:37-51; the reference's CUDA provider runs the
+ * same steps as its own kernels, CUDA/resident.inc:466-578). All vectors are
+ * fp32 device arrays (4-byte aligned); each call enqueues one kernel and
+ * returns 0, 1 when declined (null or misaligned pointers, zero or
+ * above-INT_MAX sizes), <0 on a HIP failure. Each restates one step of the
+ * engine's CPU token forward, backend/core/llm_cpu.c:424-578 (LLaMA). */
+
+/* out[cols] = row `row` of a [rows][cols] matrix of `type` in GGUF storage
+ * (not packed), decoded as nya_llm_tensor_value does
+ * (backend/core/llm_quant.c:70-142): the token embedding gather
+ * (backend/core/llm_cpu.c:71-80, :452-453). */
+NYA_HIP_EXPORT int nya_hip_dequant_row(uintptr_t w, unsigned type, size_t rows, size_t cols, size_t row,
+    uintptr_t out, uintptr_t stream);
+
+/* When residual is nonzero, x += residual first (x is written back); then
+ * out = x * s * weight with s = 1 / sqrt(sum x^2 / n + epsilon), the sum of
+ * squares in double, weight 0 meaning ones (backend/core/llm_cpu.c:83-104;
+ * the residual add of :514 folded in). */
+NYA_HIP_EXPORT int nya_hip_rms_norm(uintptr_t x, uintptr_t residual, uintptr_t weight, uintptr_t out, size_t n,
+    float epsilon, uintptr_t stream);
+
+/* Rotates the interleaved pairs (2j, 2j+1) of each of `heads` heads of
+ * `width` elements at v by the angle position * frequencies[j]
+ * (backend/core/llm_cpu.c:298-324, angles :429-432). */
+NYA_HIP_EXPORT int nya_hip_rope(uintptr_t v, size_t heads, size_t width, uintptr_t frequencies, size_t position,
+    uintptr_t stream);
+
+/* Causal attention of one query token: for each of `heads` heads (grouped
+ * onto kv_heads key/value heads), scores q.k_t * scale over the `length`
+ * cached positions of keys / values ([length][kv_heads * width] rows), a
+ * softmax, and out = sum_t p_t v_t (backend/core/llm_cpu.c:491-511).
+ * `scores` is scratch of heads * length floats. */
+NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, uintptr_t keys, uintptr_t values, uintptr_t out,
+    uintptr_t scores, size_t heads, size_t kv_heads, size_t width, size_t length, float scale, uintptr_t stream);
+
+/* gate = gate / (1 + e^-gate) * up (backend/core/llm_cpu.c:336-341, SiLU). */
+NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, uintptr_t up, size_t n, uintptr_t stream);
+
+/* x += r (the residual adds, backend/core/llm_cpu.c:514, :531). */
+NYA_HIP_EXPORT int nya_hip_add(uintptr_t x, uintptr_t r, size_t n, uintptr_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,149 @@
+"""A small random-weight LLaMA written as a GGUF v3 file, for inference
+parity tests of the resident plan against the engine's own CPU session.
+
+The file layout is the public GGUF v3 container: magic, version, tensor and
+metadata counts; metadata as (key, type, value); tensor directory entries
+(name, dimensions with the row length first, type, offset); then the tensor
+data, each tensor aligned to `general.alignment`. The metadata keys and
+tensor names are the ones the engine's loader binds for a dense LLaMA
+(backend/core/llm_gguf.c:595-644, :1069-1077): embedding, output norm and
+output, and per block the attention norm, q/k/v/output projections, the
+feed-forward norm and gate/up/down projections, with every tensor used.
+
+Weights come from fyodor_amd.synth (seeded GGUF blocks of real-model scale);
+norm weights are 1 + N(0, 0.1); the vocabulary is three control tokens and
+numbered pieces.
+"""
+from __future__ import annotations
+
+import struct
+from dataclasses import dataclass, field
+from pathlib import Path
+
+import numpy as np
+
+from fyodor_amd import F32, Q4_K, Q6_K, storage_bytes, synth
+
+# GGUF metadata value types.
+U32, I32, F32_META, BOOL, STRING, ARRAY = 4, 5, 6, 7, 8, 9
+ALIGNMENT = 32
+
+
+@dataclass
+class LlamaShape:
+    embedding: int = 256
+    heads: int = 4
+    kv_heads: int = 2
+    hidden: int = 512
+    blocks: int = 2
+    context: int = 64
+    vocabulary: int = 300
+    # GGML types of the embedding / output / attention / gate-up / down matrices.
+    types: dict = field(default_factory=lambda: {"embedding": Q4_K, "output": Q6_K, "attention": Q4_K,
+                                                 "gate_up": Q4_K, "down": Q6_K})
+    epsilon: float = 1e-5
+    rope_base: float = 10000.0
+    seed: int = 1
+
+
+def _string(s: str) -> bytes:
+    b = s.encode()
+    return struct.pack("<Q", len(b)) + b
+
+
+def _kv(key: str, kind: int, value) -> bytes:
+    out = _string(key) + struct.pack("<I", kind)
+    if kind == U32:
+        return out + struct.pack("<I", value)
+    if kind == F32_META:
+        return out + struct.pack("<f", value)
+    if kind == BOOL:
+        return out + struct.pack("<B", 1 if value else 0)
+    if kind == STRING:
+        return out + _string(value)
+    raise ValueError(kind)
+
+
+def _array(key: str, elem: int, values) -> bytes:
+    out = _string(key) + struct.pack("<IIQ", ARRAY, elem, len(values))
+    if elem == STRING:
+        return out + b"".join(_string(v) for v in values)
+    fmt = {F32_META: "<f", I32: "<i", U32: "<I"}[elem]
+    return out + b"".join(struct.pack(fmt, v) for v in values)
+
+
+def tensors(shape: LlamaShape) -> list[tuple[str, int, tuple[int, ...], np.ndarray]]:
+    """(name, type, dims with the row length first, bytes) for every tensor."""
+    d, h, v = shape.embedding, shape.hidden, shape.vocabulary
+    kv = shape.kv_heads * (d // shape.heads)
+    rng = np.random.default_rng(shape.seed)
+    seed = [shape.seed * 1000]
+
+    def matrix(kind: str, rows: int, cols: int):
+        seed[0] += 1
+        t = shape.types[kind]
+        return t, (cols, rows), synth.weights(t, rows, cols, seed[0])
+
+    def norm(n: int):
+        w = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+        return F32, (n,), w.view(np.uint8)
+
+    out = [("token_embd.weight", *matrix("embedding", v, d)), ("output_norm.weight", *norm(d)),
+           ("output.weight", *matrix("output", v, d))]
+    for b in range(shape.blocks):
+        out += [(f"blk.{b}.attn_norm.weight", *norm(d)),
+                (f"blk.{b}.attn_q.weight", *matrix("attention", d, d)),
+                (f"blk.{b}.attn_k.weight", *matrix("attention", kv, d)),
+                (f"blk.{b}.attn_v.weight", *matrix("attention", kv, d)),
+                (f"blk.{b}.attn_output.weight", *matrix("attention", d, d)),
+                (f"blk.{b}.ffn_norm.weight", *norm(d)),
+                (f"blk.{b}.ffn_gate.weight", *matrix("gate_up", h, d)),
+                (f"blk.{b}.ffn_down.weight", *matrix("down", d, h)),
+                (f"blk.{b}.ffn_up.weight", *matrix("gate_up", h, d))]
+    for name, t, dims, data in out:
+        rows = dims[1] if len(dims) > 1 else 1
+        assert data.nbytes == storage_bytes(t, rows, dims[0]), name
+    return out
+
+
+def write(path: Path, shape: LlamaShape) -> int:
+    """Writes the model; returns its size in bytes."""
+    pieces = ["<unk>", "<s>", "</s>"] + [f"p{i:04d}" for i in range(shape.vocabulary - 3)]
+    meta = [
+        _kv("general.architecture", STRING, "llama"),
+        _kv("tokenizer.ggml.model", STRING, "llama"),
+        _kv("llama.embedding_length", U32, shape.embedding),
+        _kv("llama.feed_forward_length", U32, shape.hidden),
+        _kv("llama.block_count", U32, shape.blocks),
+        _kv("llama.attention.head_count", U32, shape.heads),
+        _kv("llama.attention.head_count_kv", U32, shape.kv_heads),
+        _kv("llama.context_length", U32, shape.context),
+        _kv("llama.attention.layer_norm_rms_epsilon", F32_META, shape.epsilon),
+        _kv("llama.rope.freq_base", F32_META, shape.rope_base),
+        _kv("tokenizer.ggml.unknown_token_id", U32, 0),
+        _kv("tokenizer.ggml.bos_token_id", U32, 1),
+        _kv("tokenizer.ggml.eos_token_id", U32, 2),
+        _array("tokenizer.ggml.tokens", STRING, pieces),
+        _array("tokenizer.ggml.scores", F32_META, [0.0] * len(pieces)),
+        _array("tokenizer.ggml.token_type", I32, [3 if i in (1, 2) else 1 for i in range(len(pieces))]),
+        _kv("tokenizer.ggml.add_eos_token", BOOL, False),
+        _kv("general.alignment", U32, ALIGNMENT),
+    ]
+    ts = tensors(shape)
+    directory, offset = [], 0
+    for name, t, dims, data in ts:
+        directory.append(_string(name) + struct.pack("<I", len(dims)) +
+                         b"".join(struct.pack("<Q", n) for n in dims) + struct.pack("<IQ", t, offset))
+        offset = (offset + data.nbytes + ALIGNMENT - 1) // ALIGNMENT * ALIGNMENT
+    head = b"GGUF" + struct.pack("<IQQ", 3, len(ts), len(meta)) + b"".join(meta) + b"".join(directory)
+    start = (len(head) + ALIGNMENT - 1) // ALIGNMENT * ALIGNMENT
+    with open(path, "wb") as f:
+        f.write(head + b"\0" * (start - len(head)))
+        at = 0
+        for _, _, _, data in ts:
+            f.write(data.tobytes())
+            at += data.nbytes
+            pad = (at + ALIGNMENT - 1) // ALIGNMENT * ALIGNMENT - at
+            f.write(b"\0" * pad)
+            at += pad
+    return path.stat().st_size

@@ -31,7 +31,8 @@ def test_kernel_library_exports_its_header():
     want = declared("fyodor_hip.h")
     assert want == {"nya_hip_abi_version", "nya_hip_weight_bytes", "nya_hip_weight_layout", "nya_hip_weight_pack",
                     "nya_hip_workspace_bytes", "nya_hip_matmul", "nya_hip_matmul_static", "nya_hip_kernel_name",
-                    "nya_hip_copy", "nya_hip_read"}
+                    "nya_hip_copy", "nya_hip_read", "nya_hip_dequant_row", "nya_hip_rms_norm", "nya_hip_rope",
+                    "nya_hip_attention", "nya_hip_silu_mul", "nya_hip_add"}
     assert want <= exported(KERNEL_LIBRARY)
 
 
@@ -221,3 +222,41 @@ def test_prefill_dispatch_and_workspace():
     for t in (F32, BF16):
         assert kern.workspace_bytes(t, 4096, 4096, 512) == 0
         assert kern.kernel_name(t, 4096, 4096, 512) == "skinny_dense"
+
+
+def test_model_header_layout_matches_engine(tmp_path):
+    """fyodor_amd/core/llm_internal.h lays out the engine's model types as
+    backend/core/llm_internal.h does (the provider reads the engine's
+    nya_llm_context by address): every member the resident plan reads, and
+    the sizes of the structures, compiled against both headers."""
+    ref_core = Path("/root/reference/backend/core")
+    if not (ref_core / "llm_internal.h").exists():
+        pytest.skip("reference sources not mounted")
+    fields = {
+        "nya_llm_context": ["compute", "tensors", "tensor_count", "layers", "tokenizer", "token_embedding",
+                            "output_norm", "output", "embedding_length", "block_count", "context_length",
+                            "norm_epsilon", "rope_frequency_base", "is_gemma", "is_assistant",
+                            "per_layer_embedding_length", "expert_count", "final_logit_softcap", "cache_width",
+                            "sliding_value_dimension"],
+        "nya_llm_layer": ["attention_norm", "query", "key", "value", "attention_output", "feed_forward_norm",
+                          "feed_forward_gate", "feed_forward_down", "feed_forward_up", "query_norm", "key_norm",
+                          "attention_post_norm", "ffn_post_norm", "router", "ple_gate", "output_scale",
+                          "rope_factors", "head_count", "kv_head_count", "head_dimension", "hidden_length",
+                          "sliding_window", "kv_source", "cache_offset"],
+        "nya_llm_tensor": ["type", "dimension_count", "dimensions", "data", "data_size"],
+        "nya_llm_tokenizer": ["vocabulary_size", "suppressed_tokens", "suppressed_count"],
+    }
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "llm_internal.h"', "int main(void) {"]
+    for struct, names in fields.items():
+        lines.append(f'printf("{struct} %zu\\n", sizeof({struct}));')
+        lines += [f'printf("{struct}.{n} %zu\\n", offsetof({struct}, {n}));' for n in names]
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    out = {}
+    for name, inc in [("ours", [INCLUDE.parent / "fyodor_amd/core", INCLUDE]),
+                      ("engine", [ref_core, ref_core.parent / "include"])]:
+        exe = tmp_path / name
+        subprocess.run(["gcc", "-std=c17", *[f"-I{p}" for p in inc], str(src), "-o", str(exe)], check=True)
+        out[name] = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout
+    assert out["ours"] == out["engine"]

@@ -1,0 +1,55 @@
+"""The resident plan on an MI355X: the engine's own inference session and
+model loader (backend/core/llm_cpu.c, llm_gguf.c, built from the reference
+sources into oracle/_ref/libnya_dropin.so with this repository's provider
+registered) run a random-weight LLaMA GGUF (tests/gguf_model.py) with
+NYA_COMPUTE=rocm — the whole token forward on the GPU through the gfx950
+kernels — and every decode step's logits, the KV cache, and after a reset
+prefill chunks between decode steps, match the engine's scalar reference
+session within its own inference-test bounds
+(backend/tests/test_inference.c:9-33, :207-219): logits within
+5e-4 (1 + |ref|), K/V within 1.5e-4 (1 + |ref|)."""
+import ctypes
+
+import pytest
+
+from fyodor_amd import F16, KERNEL_LIBRARY, Q4_0, Q4_K, Q6_K, Q8_0
+from gguf_model import LlamaShape, write
+from resident_check import bind, compare
+from conftest import DROPIN_LIBRARY
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def session_lib():
+    """Built beforehand (make -C oracle dropin, where the reference sources
+    are); used as built here."""
+    if not DROPIN_LIBRARY.exists():
+        pytest.skip("oracle/_ref/libnya_dropin.so was not built (it needs the reference sources)")
+    return bind(ctypes.CDLL(str(DROPIN_LIBRARY)))
+
+
+@pytest.fixture()
+def rocm_env(monkeypatch):
+    monkeypatch.setenv("NYA_ROCM_KERNEL_LIBRARY", str(KERNEL_LIBRARY))
+    for v in ("NYA_ROCM_HIP_LIBRARY", "NYA_ROCM_CACHE_MIB", "NYA_INFERENCE_REFERENCE"):
+        monkeypatch.delenv(v, raising=False)
+
+
+TOKENS = [(i * 37 + 11) % 1000 for i in range(40)]
+
+
+@pytest.mark.parametrize("types", [
+    {"embedding": Q4_K, "output": Q6_K, "attention": Q4_K, "gate_up": Q4_K, "down": Q6_K},
+    {"embedding": F16, "output": Q8_0, "attention": Q8_0, "gate_up": Q4_0, "down": Q8_0},
+], ids=["k-quants", "q8-q4-f16"])
+def test_resident_plan_on_gpu(session_lib, rocm_env, tmp_path, types):
+    shape = LlamaShape(embedding=512, heads=8, kv_heads=2, hidden=1024, blocks=3, context=64, vocabulary=1000,
+                       types=types, seed=3)
+    path = tmp_path / "model.gguf"
+    write(path, shape)
+    out = compare(session_lib, path, shape, "rocm", TOKENS)
+    print(f"resident plan: worst scaled logit error {out['logit']:.3g}, KV {out['kv']:.3g}", flush=True)
+    assert out["execution"] == "resident"
+    s = out["stats"]
+    assert s.kernel_launches > 0 and s.external_matmul_calls > 0 and s.kv_bytes > 0

@@ -1,0 +1,65 @@
+"""The resident plan on the CPU, through the engine's own session and model
+loader (backend/core/llm_cpu.c, llm_gguf.c built from the reference sources
+with this repository's provider registered), against the mock HIP runtime
+and kernel library (tests/mock/mock_hip.c, whose resident steps compute in
+the engine's order on the host):
+
+- a random-weight LLaMA GGUF (tests/gguf_model.py) loads, the session runs
+  "resident" on the rocm provider, and every decode step's logits and the KV
+  cache match the engine's scalar reference session within the engine's own
+  inference-test bounds (backend/tests/test_inference.c:9-33, :207-219);
+  after a reset, prefill chunks (the plan's prefill) between decode steps
+  match too;
+- a kernel library without the resident steps declines the plan, and the
+  engine then runs its reference path (backend/core/llm_cpu.c:235-242) with
+  the same logits.
+The same comparison runs on an MI355X in tests/test_gpu_resident.py."""
+import subprocess
+
+import pytest
+
+from fyodor_amd import Q4_0, Q4_K, Q6_K, Q8_0, F16
+from gguf_model import LlamaShape, write
+from resident_check import bind, compare
+
+TOKENS = [5, 17, 200, 3, 42, 99, 250, 1, 7, 64, 128, 33]
+
+
+@pytest.fixture()
+def session_lib(dropin_library, mock_paths, monkeypatch):
+    good, _ = mock_paths
+    monkeypatch.setenv("NYA_ROCM_HIP_LIBRARY", str(good))
+    monkeypatch.setenv("NYA_ROCM_KERNEL_LIBRARY", str(good))
+    monkeypatch.delenv("NYA_ROCM_CACHE_MIB", raising=False)
+    monkeypatch.delenv("NYA_INFERENCE_REFERENCE", raising=False)
+    return bind(dropin_library)
+
+
+@pytest.mark.parametrize("types", [
+    {"embedding": Q4_K, "output": Q6_K, "attention": Q4_K, "gate_up": Q4_K, "down": Q6_K},
+    {"embedding": F16, "output": Q8_0, "attention": Q8_0, "gate_up": Q4_0, "down": Q8_0},
+], ids=["k-quants", "q8-q4-f16"])
+def test_resident_plan_matches_reference_session(session_lib, tmp_path, types):
+    shape = LlamaShape(types=types, context=32)
+    path = tmp_path / "model.gguf"
+    write(path, shape)
+    out = compare(session_lib, path, shape, "rocm", TOKENS)
+    assert out["execution"] == "resident"
+    s = out["stats"]
+    assert s.kernel_launches > 0 and s.external_matmul_calls > 0 and s.kv_bytes > 0 and s.weights_bytes > 0
+
+
+def test_plan_declined_without_resident_steps(session_lib, tmp_path, monkeypatch):
+    lib_dir = tmp_path / "mock"
+    lib_dir.mkdir()
+    plain = lib_dir / "libnya_mock_plain.so"
+    from conftest import REPO
+    src = [str(REPO / "tests/mock/mock_hip.c"), str(REPO / "oracle/quant_oracle.c")]
+    subprocess.run(["gcc", "-std=c17", "-O1", "-fPIC", "-shared", "-D_POSIX_C_SOURCE=200809L",
+                    "-Dnya_hip_rope=nya_mock_unused_rope", *src, "-o", str(plain), "-lm", "-lpthread"], check=True)
+    monkeypatch.setenv("NYA_ROCM_KERNEL_LIBRARY", str(plain))
+    shape = LlamaShape(context=16)
+    path = tmp_path / "model.gguf"
+    write(path, shape)
+    out = compare(session_lib, path, shape, "rocm", TOKENS[:6])
+    assert out["execution"] == "cpu-reference"

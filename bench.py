@@ -22,6 +22,11 @@ weight matrix; weights and activations are resident in HBM before timing.
   into oracle/_ref) on the same weights, on this host's cores, at the
   reference's default thread count, at the CPUs this process may use and at
   one thread; else this repository's C port of the scalar path.
+- resident: the provider's resident plan (a whole token forward on the GPU)
+  on synthetic dense LLaMAs of two shapes: an 8B-class model (tg: decode
+  tokens/s with logits every token, and its weight bytes per token over the
+  token time) and TinyLlama 1.1B (tg128 and pp512, the reference's published
+  end-to-end metrics).
 - prefill: the same matrix times 512 tokens through the fp16-MFMA prefill
   GEMM (one call = activation split + GEMM): useful TFLOP/s (2 M N K) against
   the dense fp16 MFMA peak, and the fp16 work the matrix cores issue (two
@@ -334,6 +339,86 @@ def prefill(rt, kern, stream, settle, weights, steps: int) -> dict:
     }
 
 
+# Resident plan workloads: dense LLaMAs with a Q4_K_M-like type mix (Q4_K
+# attention, gate and up; Q6_K down and output; Q4_K embedding).
+# "llama-8b": embedding 4096, 32 heads of 128 with 8 KV heads, feed-forward
+# 14336, 32 blocks, vocabulary 128256. "tinyllama-1.1b": embedding 2048, 32
+# heads of 64 with 4 KV heads, feed-forward 5632, 22 blocks, vocabulary
+# 32000 — the model of the reference's published end-to-end table
+# (backend/README.md:796-803: tg128 and pp512 tokens/s).
+RESIDENT_TYPES = {"embedding": Q4_K, "output": Q6_K, "attention": Q4_K, "gate_up": Q4_K, "down": Q6_K}
+RESIDENT_MODELS = {
+    "llama-8b": dict(embedding=4096, heads=32, kv_heads=8, hidden=14336, blocks=32, vocabulary=128256),
+    "tinyllama-1.1b": dict(embedding=2048, heads=32, kv_heads=4, hidden=5632, blocks=22, vocabulary=32000),
+}
+
+
+def resident(name: str, tg: int, pp: int, blocks: int | None = None) -> dict:
+    """The provider's resident plan on a synthetic model of `name`'s shape:
+    tg = tokens/s of `tg` decode steps from position 0 (each with its logits
+    downloaded and checked, as llama-bench's tg counts a generated token),
+    pp = tokens/s of one plan_prefill of `pp` prompt tokens from position 0
+    (logits of the last). Host wall clock around the plan calls; the plan
+    is warmed first. HBM figure: weight bytes a decode step reads (every
+    block's matrices, the output matrix, one embedding row) over its time."""
+    from fyodor_amd import Compute
+    from fyodor_amd.model import LlamaModel, LlamaShape, Plan, llama_tensors
+
+    shape_args = dict(RESIDENT_MODELS[name])
+    if blocks:
+        shape_args["blocks"] = blocks
+    shape = LlamaShape(**shape_args, context=max(tg, pp) + 8, types=RESIDENT_TYPES, seed=7)
+    model = LlamaModel(shape, llama_tensors(shape, shared_blocks=True))
+    ids = [(7 * i + 11) % shape.vocabulary for i in range(max(tg, pp))]
+    out = {"workload": (f"dense LLaMA, embedding {shape.embedding}, {shape.heads} heads / {shape.kv_heads} KV of "
+                        f"{shape.embedding // shape.heads}, feed-forward {shape.hidden}, {shape.blocks} blocks, "
+                        f"vocabulary {shape.vocabulary}, Q4_K attention/gate/up + Q6_K down/output")}
+    compute = Compute("rocm")
+    try:
+        t0 = time.perf_counter()
+        plan = Plan(compute, model, shape.context)
+        out["plan_open_s"] = round(time.perf_counter() - t0, 2)
+        try:
+            for i in range(8):
+                plan.token(ids[i], i)
+            if tg:
+                before = plan.stats()["kernel_launches"]
+                start = time.perf_counter()
+                for i in range(tg):
+                    plan.token(ids[i], i)
+                wall = time.perf_counter() - start
+                launches = (plan.stats()["kernel_launches"] - before) / tg
+                embd = next(a for a in model.arrays if a[0] == "token_embd.weight")
+                wbytes = sum(a[3].nbytes for a in model.arrays if a[0] != "token_embd.weight") + \
+                    embd[3].nbytes // shape.vocabulary
+                gbs = wbytes * tg / wall / 1e9
+                out[f"tg{tg}"] = {"tokens_per_s": round(tg / wall, 2), "us_per_token": round(wall / tg * 1e6, 1),
+                                  "weight_bytes_per_token": wbytes, "effective_gbs": round(gbs, 1),
+                                  "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "launches_per_token": round(launches, 1),
+                                  "logits_finite": bool(np.all(np.isfinite(plan.logits)))}
+            if pp:
+                plan.prefill(ids[:pp], 0)
+                start = time.perf_counter()
+                plan.prefill(ids[:pp], 0)
+                wall = time.perf_counter() - start
+                out[f"pp{pp}"] = {"tokens_per_s": round(pp / wall, 2), "ms": round(wall * 1e3, 2)}
+            out["device_weight_bytes"] = plan.stats()["weights_bytes"]
+        finally:
+            plan.close()
+    finally:
+        compute.close()
+    return out
+
+
+def resident_legs(tg: int, pp: int, blocks: int | None) -> dict:
+    legs = {name: resident(name, tg, 0 if name == "llama-8b" else pp, blocks) for name in RESIDENT_MODELS}
+    legs["reference_published"] = {
+        "tinyllama-1.1b": {"tg128": 205.48, "pp512": 1374.38, "hardware": "RTX 5060 Ti",
+                           "source": "backend/README.md:796-803 (Stage 2 Fyodor CUDA resident)"}}
+    legs["timing"] = "host wall clock around plan_token / plan_prefill calls; synthetic weights of the named shape"
+    return legs
+
+
 # The measured configurations: decode and small-N shapes (type, rows, cols,
 # batches), then prefill GEMM shapes (type, rows, cols, tokens).
 SWEEP_MATVEC = [
@@ -425,6 +510,10 @@ def main() -> int:
                     help="run only the plain 256 MiB device copy used to calibrate HBM byte counters")
     ap.add_argument("--prefill-steps", type=int, default=20, help="timed prefill GEMM calls (0: skip)")
     ap.add_argument("--prefill-only", action="store_true", help="run only the prefill GEMM measurement")
+    ap.add_argument("--resident-tg", type=int, default=128, help="timed decode tokens of the resident plans (0: skip)")
+    ap.add_argument("--resident-pp", type=int, default=512, help="prompt tokens of the timed resident prefill")
+    ap.add_argument("--resident-blocks", type=int, default=0, help="override the resident models' block count")
+    ap.add_argument("--resident-only", action="store_true", help="run only the resident plan measurements")
     ap.add_argument("--sweep", action="store_true",
                     help="time every decode, small-N and prefill configuration instead (one JSON line each)")
     args = ap.parse_args()
@@ -433,6 +522,10 @@ def main() -> int:
               "sharded across GPUs with no exchange between them). Run with --gpus 1.", file=sys.stderr)
         return 2
 
+    if args.resident_only:
+        print(json.dumps({"resident": resident_legs(args.resident_tg, args.resident_pp, args.resident_blocks or None)}),
+              flush=True)
+        return 0
     rt = Runtime()
     kern = Kernels()
     stream = rt.stream()
@@ -506,11 +599,13 @@ def main() -> int:
         line["call_latency"] = call_latency(kern, rt, stream, weights, x_dev, y_dev, host_w, x8[0].copy())
     if args.prefill_steps > 0:
         line["prefill"] = prefill(rt, kern, stream, settle, weights, args.prefill_steps)
-    if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(host_w, x8[0].copy(), y1, args.cpu_seconds)
     for p in weights + [work, x_dev, y_dev]:
         rt.free(p)
     settle.close()
+    if args.resident_tg > 0:
+        line["resident"] = resident_legs(args.resident_tg, args.resident_pp, args.resident_blocks or None)
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(host_w, x8[0].copy(), y1, args.cpu_seconds)
     print(json.dumps(line), flush=True)
     return 0
 

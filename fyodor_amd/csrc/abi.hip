@@ -268,21 +268,22 @@ NYA_HIP_EXPORT int nya_hip_rms_norm(uintptr_t x, uintptr_t residual, uintptr_t w
                                   epsilon, (hipStream_t)stream));
 }
 
-NYA_HIP_EXPORT int nya_hip_rope(uintptr_t v, size_t heads, size_t width, uintptr_t frequencies, size_t position,
-    uintptr_t stream)
+NYA_HIP_EXPORT int nya_hip_rope_qkv(uintptr_t qkv, size_t heads, size_t kv_heads, size_t width,
+    uintptr_t frequencies, size_t position, uintptr_t key, uintptr_t value, uintptr_t stream)
 {
-    if (!vec(v) || !vec(frequencies) || !count_ok(heads) || !count_ok(width) || width % 2 ||
-        heads > (size_t)INT_MAX / width || position > (size_t)INT_MAX)
+    if (!vec(qkv) || !vec(frequencies) || !vec(key) || !vec(value) || !count_ok(heads) || !count_ok(kv_heads) ||
+        !count_ok(width) || width % 2 || heads > (size_t)INT_MAX / 2 - kv_heads ||
+        heads + 2 * kv_heads > (size_t)INT_MAX / width || position > (size_t)INT_MAX)
         return 1;
-    return status(launch_rope((float *)v, (int)heads, (int)width, (const float *)frequencies, (int)position,
-                              (hipStream_t)stream));
+    return status(launch_rope_qkv((float *)qkv, (int)heads, (int)kv_heads, (int)width, (const float *)frequencies,
+                                  (int)position, (float *)key, (float *)value, (hipStream_t)stream));
 }
 
 NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, uintptr_t keys, uintptr_t values, uintptr_t out, uintptr_t scores,
     size_t heads, size_t kv_heads, size_t width, size_t length, float scale, uintptr_t stream)
 {
     if (!vec(q) || !vec(keys) || !vec(values) || !vec(out) || !vec(scores) || !count_ok(heads) ||
-        !count_ok(kv_heads) || !count_ok(width) || !count_ok(length) || heads % kv_heads ||
+        !count_ok(kv_heads) || !count_ok(width) || width > 256 || !count_ok(length) || heads % kv_heads ||
         kv_heads > (size_t)INT_MAX / width || heads > (size_t)INT_MAX / length)
         return 1;
     return status(launch_attention((const float *)q, (const float *)keys, (const float *)values, (float *)out,
@@ -294,12 +295,6 @@ NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, uintptr_t up, size_t n, uint
 {
     if (!vec(gate) || !vec(up) || !count_ok(n)) return 1;
     return status(launch_silu_mul((float *)gate, (const float *)up, (int)n, (hipStream_t)stream));
-}
-
-NYA_HIP_EXPORT int nya_hip_add(uintptr_t x, uintptr_t r, size_t n, uintptr_t stream)
-{
-    if (!vec(x) || !vec(r) || !count_ok(n)) return 1;
-    return status(launch_add((float *)x, (const float *)r, (int)n, (hipStream_t)stream));
 }
 
 }  // extern "C"

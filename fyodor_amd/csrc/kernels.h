@@ -60,17 +60,18 @@ hipError_t launch_read(const uint4 *src, size_t count, unsigned *sink, hipStream
 // Vector steps of a resident decoder token (resident.hip), fp32 device
 // vectors: one row of a GGUF-layout matrix decoded (row_bytes its stored
 // size); x += r (when r is given) then out = RMS-normalized x times w (w may
-// be null); rotary encoding of `heads` interleaved heads at `position`;
-// causal attention of `heads` query heads over `length` cached positions
-// (scores: heads x length scratch); gate = silu(gate) * up; x += r.
+// be null); rotary encoding at `position` of a fused q|k|v product (q rotated
+// in place, k rotated into `key`, v copied into `value`); causal attention of
+// `heads` query heads of width <= 256 over `length` cached positions (scores:
+// heads x length scratch, used beyond 8192 positions); gate = silu(gate) * up.
 hipError_t launch_dequant_row(const uint8_t *w, unsigned type, size_t row_bytes, size_t row, int cols, float *out,
     hipStream_t stream);
 hipError_t launch_rms_norm(float *x, const float *r, const float *w, float *out, int n, float eps, hipStream_t stream);
-hipError_t launch_rope(float *v, int heads, int width, const float *freq, int position, hipStream_t stream);
+hipError_t launch_rope_qkv(float *qkv, int heads, int kv_heads, int width, const float *freq, int position, float *key,
+    float *value, hipStream_t stream);
 hipError_t launch_attention(const float *q, const float *keys, const float *values, float *out, float *scores,
     int heads, int kv_heads, int width, int length, float scale, hipStream_t stream);
 hipError_t launch_silu_mul(float *gate, const float *up, int n, hipStream_t stream);
-hipError_t launch_add(float *x, const float *r, int n, hipStream_t stream);
 
 // Compute units of the current device (counted once per device).
 int device_cu_count();

@@ -82,9 +82,10 @@ int nya_compute_matvec_typed(nya_compute_context *context, const void *weights,
 int nya_compute_matmul_typed(nya_compute_context *context, const void *weights,
     size_t rows, size_t columns, unsigned type, const float *input, float *output, size_t batch);
 
-/* Resident plans and attention (backend/include/compute.h:34-51). The ROCm
- * provider has no RESIDENT capability, so these dispatch to NULL entries and
- * report "unavailable" (NULL / -1), exactly as for the reference provider. */
+/* Resident plans and attention (backend/include/compute.h:34-51). A provider
+ * without an entry reports "unavailable" (NULL / -1); the ROCm provider has
+ * the plan entries (a whole dense-LLaMA token forward on the GPU) and no
+ * attention_f32 entry. */
 int nya_compute_attention_f32(nya_compute_context *context, const nya_compute_attention *attention);
 nya_compute_plan *nya_compute_plan_create(nya_compute_context *context,
     const struct nya_llm_context *model, size_t capacity);

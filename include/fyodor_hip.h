@@ -150,25 +150,27 @@ NYA_HIP_EXPORT int nya_hip_dequant_row(uintptr_t w, unsigned type, size_t rows, 
 NYA_HIP_EXPORT int nya_hip_rms_norm(uintptr_t x, uintptr_t residual, uintptr_t weight, uintptr_t out, size_t n,
     float epsilon, uintptr_t stream);
 
-/* Rotates the interleaved pairs (2j, 2j+1) of each of `heads` heads of
- * `width` elements at v by the angle position * frequencies[j]
- * (backend/core/llm_cpu.c:298-324, angles :429-432). */
-NYA_HIP_EXPORT int nya_hip_rope(uintptr_t v, size_t heads, size_t width, uintptr_t frequencies, size_t position,
-    uintptr_t stream);
+/* The rotary step of one token on a fused q|k|v product at qkv (`heads`
+ * query heads, then `kv_heads` key heads and `kv_heads` value heads, each of
+ * `width` elements): the interleaved pairs (2j, 2j+1) of every q head are
+ * rotated in place and those of every k head into `key`, by the angle
+ * position * frequencies[j] (backend/core/llm_cpu.c:298-324, angles
+ * :429-432), and v is copied to `value` — the token's slots of the layer's
+ * KV cache (the cache writes of :433-436). */
+NYA_HIP_EXPORT int nya_hip_rope_qkv(uintptr_t qkv, size_t heads, size_t kv_heads, size_t width,
+    uintptr_t frequencies, size_t position, uintptr_t key, uintptr_t value, uintptr_t stream);
 
 /* Causal attention of one query token: for each of `heads` heads (grouped
- * onto kv_heads key/value heads), scores q.k_t * scale over the `length`
- * cached positions of keys / values ([length][kv_heads * width] rows), a
- * softmax, and out = sum_t p_t v_t (backend/core/llm_cpu.c:491-511).
- * `scores` is scratch of heads * length floats. */
+ * onto kv_heads key/value heads, width at most 256), scores q.k_t * scale
+ * over the `length` cached positions of keys / values
+ * ([length][kv_heads * width] rows), a softmax, and out = sum_t p_t v_t
+ * (backend/core/llm_cpu.c:491-511). `scores` is scratch of heads * length
+ * floats. */
 NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, uintptr_t keys, uintptr_t values, uintptr_t out,
     uintptr_t scores, size_t heads, size_t kv_heads, size_t width, size_t length, float scale, uintptr_t stream);
 
 /* gate = gate / (1 + e^-gate) * up (backend/core/llm_cpu.c:336-341, SiLU). */
 NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, uintptr_t up, size_t n, uintptr_t stream);
-
-/* x += r (the residual adds, backend/core/llm_cpu.c:514, :531). */
-NYA_HIP_EXPORT int nya_hip_add(uintptr_t x, uintptr_t r, size_t n, uintptr_t stream);
 
 #ifdef __cplusplus
 }

@@ -10,40 +10,20 @@ tensor names are the ones the engine's loader binds for a dense LLaMA
 output, and per block the attention norm, q/k/v/output projections, the
 feed-forward norm and gate/up/down projections, with every tensor used.
 
-Weights come from fyodor_amd.synth (seeded GGUF blocks of real-model scale);
-norm weights are 1 + N(0, 0.1); the vocabulary is three control tokens and
-numbered pieces.
+The shape and the tensors (seeded GGUF blocks of real-model scale, norm
+weights 1 + N(0, 0.1)) are fyodor_amd.model's LlamaShape / llama_tensors; the
+vocabulary is three control tokens and numbered pieces.
 """
 from __future__ import annotations
 
 import struct
-from dataclasses import dataclass, field
 from pathlib import Path
 
-import numpy as np
-
-from fyodor_amd import F32, Q4_K, Q6_K, storage_bytes, synth
+from fyodor_amd.model import LlamaShape, llama_tensors
 
 # GGUF metadata value types.
 U32, I32, F32_META, BOOL, STRING, ARRAY = 4, 5, 6, 7, 8, 9
 ALIGNMENT = 32
-
-
-@dataclass
-class LlamaShape:
-    embedding: int = 256
-    heads: int = 4
-    kv_heads: int = 2
-    hidden: int = 512
-    blocks: int = 2
-    context: int = 64
-    vocabulary: int = 300
-    # GGML types of the embedding / output / attention / gate-up / down matrices.
-    types: dict = field(default_factory=lambda: {"embedding": Q4_K, "output": Q6_K, "attention": Q4_K,
-                                                 "gate_up": Q4_K, "down": Q6_K})
-    epsilon: float = 1e-5
-    rope_base: float = 10000.0
-    seed: int = 1
 
 
 def _string(s: str) -> bytes:
@@ -72,38 +52,7 @@ def _array(key: str, elem: int, values) -> bytes:
     return out + b"".join(struct.pack(fmt, v) for v in values)
 
 
-def tensors(shape: LlamaShape) -> list[tuple[str, int, tuple[int, ...], np.ndarray]]:
-    """(name, type, dims with the row length first, bytes) for every tensor."""
-    d, h, v = shape.embedding, shape.hidden, shape.vocabulary
-    kv = shape.kv_heads * (d // shape.heads)
-    rng = np.random.default_rng(shape.seed)
-    seed = [shape.seed * 1000]
-
-    def matrix(kind: str, rows: int, cols: int):
-        seed[0] += 1
-        t = shape.types[kind]
-        return t, (cols, rows), synth.weights(t, rows, cols, seed[0])
-
-    def norm(n: int):
-        w = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
-        return F32, (n,), w.view(np.uint8)
-
-    out = [("token_embd.weight", *matrix("embedding", v, d)), ("output_norm.weight", *norm(d)),
-           ("output.weight", *matrix("output", v, d))]
-    for b in range(shape.blocks):
-        out += [(f"blk.{b}.attn_norm.weight", *norm(d)),
-                (f"blk.{b}.attn_q.weight", *matrix("attention", d, d)),
-                (f"blk.{b}.attn_k.weight", *matrix("attention", kv, d)),
-                (f"blk.{b}.attn_v.weight", *matrix("attention", kv, d)),
-                (f"blk.{b}.attn_output.weight", *matrix("attention", d, d)),
-                (f"blk.{b}.ffn_norm.weight", *norm(d)),
-                (f"blk.{b}.ffn_gate.weight", *matrix("gate_up", h, d)),
-                (f"blk.{b}.ffn_down.weight", *matrix("down", d, h)),
-                (f"blk.{b}.ffn_up.weight", *matrix("gate_up", h, d))]
-    for name, t, dims, data in out:
-        rows = dims[1] if len(dims) > 1 else 1
-        assert data.nbytes == storage_bytes(t, rows, dims[0]), name
-    return out
+tensors = llama_tensors
 
 
 def write(path: Path, shape: LlamaShape) -> int:

@@ -176,3 +176,44 @@ def compare(lib, path: Path, shape, provider: str, tokens: list[int]) -> dict:
         model.close()
         ref_model.close()
     return out
+
+
+def plan_against_engine(lib, tmp_path: Path, shape, tokens: list[int]) -> dict:
+    """Decode `tokens` on a plan that fyodor_amd.model builds (no engine
+    loader) through this repository's compute API, and on the engine's
+    reference session of the same model written as GGUF; then one prefill
+    chunk. Returns the worst scaled logit and KV errors."""
+    from fyodor_amd import Compute
+    from fyodor_amd import model as fm
+    from gguf_model import write
+    path = tmp_path / "model.gguf"
+    write(path, shape)
+    ref_model = Model(lib, path, None)
+    ref = Session(ref_model, shape.context)
+    compute = Compute("rocm")
+    plan = fm.Plan(compute, fm.LlamaModel(shape), shape.context)
+    worst = {"logit": 0.0, "kv": 0.0}
+    try:
+        for i, t in enumerate(tokens):
+            assert ref.run([t], True) == 0
+            got = plan.token(t, i)
+            worst["logit"] = max(worst["logit"], check_logits(ref.logits(shape.vocabulary), got, f"position {i}"))
+        chunk = [(7 * i + 3) % shape.vocabulary for i in range(4)]
+        assert ref.run(chunk, False) == 0
+        got = plan.prefill(chunk, len(tokens))
+        worst["logit"] = max(worst["logit"], check_logits(ref.logits(shape.vocabulary), got, "prefill chunk"))
+        width = shape.kv_heads * (shape.embedding // shape.heads)
+        n = len(tokens) + len(chunk)
+        for layer in range(shape.blocks):
+            for a, b in zip(ref.kv(layer, 0, n, width), plan.read_kv(layer, 0, n)):
+                scaled = np.abs(b.astype(np.float64) - a) / (1 + np.abs(a.astype(np.float64)))
+                assert scaled.max() <= KV_BOUND, f"layer {layer}: KV scaled error {scaled.max():.3g}"
+                worst["kv"] = max(worst["kv"], float(scaled.max()))
+        stats = plan.stats()
+        assert stats["kernel_launches"] > 0 and stats["weights_bytes"] > 0 and stats["kv_bytes"] > 0
+    finally:
+        plan.close()
+        compute.close()
+        ref.close()
+        ref_model.close()
+    return worst

@@ -14,7 +14,7 @@ import pytest
 
 from fyodor_amd import F16, KERNEL_LIBRARY, Q4_0, Q4_K, Q6_K, Q8_0
 from gguf_model import LlamaShape, write
-from resident_check import bind, compare
+from resident_check import bind, compare, plan_against_engine
 from conftest import DROPIN_LIBRARY
 
 pytestmark = pytest.mark.gpu
@@ -53,3 +53,13 @@ def test_resident_plan_on_gpu(session_lib, rocm_env, tmp_path, types):
     assert out["execution"] == "resident"
     s = out["stats"]
     assert s.kernel_launches > 0 and s.external_matmul_calls > 0 and s.kv_bytes > 0
+
+
+def test_python_model_plan_on_gpu(session_lib, rocm_env, tmp_path):
+    """The model description built by fyodor_amd.model (no engine loader),
+    planned through this repository's own compute API on the GPU, against
+    the engine's reference session of the same model."""
+    shape = LlamaShape(embedding=512, heads=8, kv_heads=2, hidden=1024, blocks=3, context=64, vocabulary=1000,
+                       seed=5)
+    out = plan_against_engine(session_lib, tmp_path, shape, TOKENS[:24])
+    print(f"python-built plan: worst scaled logit error {out['logit']:.3g}, KV {out['kv']:.3g}", flush=True)

@@ -56,7 +56,7 @@ def test_plan_declined_without_resident_steps(session_lib, tmp_path, monkeypatch
     from conftest import REPO
     src = [str(REPO / "tests/mock/mock_hip.c"), str(REPO / "oracle/quant_oracle.c")]
     subprocess.run(["gcc", "-std=c17", "-O1", "-fPIC", "-shared", "-D_POSIX_C_SOURCE=200809L",
-                    "-Dnya_hip_rope=nya_mock_unused_rope", *src, "-o", str(plain), "-lm", "-lpthread"], check=True)
+                    "-Dnya_hip_rope_qkv=nya_mock_unused_rope", *src, "-o", str(plain), "-lm", "-lpthread"], check=True)
     monkeypatch.setenv("NYA_ROCM_KERNEL_LIBRARY", str(plain))
     shape = LlamaShape(context=16)
     path = tmp_path / "model.gguf"

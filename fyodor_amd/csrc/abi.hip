@@ -247,54 +247,82 @@ NYA_HIP_EXPORT int nya_hip_read(uintptr_t src, size_t bytes, uintptr_t sink, uin
 // fp32 device vectors: non-null and 4-byte aligned.
 static bool vec(uintptr_t p) { return p && !(p & 3u); }
 static bool count_ok(size_t n) { return n && n <= (size_t)INT_MAX; }
+// Tokens per call: the second grid dimension.
+static bool tokens_ok(size_t count) { return count && count <= 65535; }
 
-NYA_HIP_EXPORT int nya_hip_dequant_row(uintptr_t w, unsigned type, size_t rows, size_t cols, size_t row, uintptr_t out,
-    uintptr_t stream)
+NYA_HIP_EXPORT int nya_hip_step(uintptr_t step, unsigned token, size_t position, uintptr_t stream)
+{
+    if (!vec(step) || position > (size_t)INT_MAX) return 1;
+    return status(launch_set_step((uint32_t *)step, token, (int)position, (hipStream_t)stream));
+}
+
+NYA_HIP_EXPORT int nya_hip_embed(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t tokens, size_t count,
+    uintptr_t out, uintptr_t stream)
 {
     format_info f;
-    if (!w || !vec(out) || !format_of(type, &f) || !count_ok(rows) || !count_ok(cols) || cols % f.block ||
-        row >= rows)
+    if (!w || !vec(tokens) || !vec(out) || !format_of(type, &f) || !count_ok(rows) || !count_ok(cols) ||
+        cols % f.block || !tokens_ok(count))
         return 1;
     const size_t row_bytes = cols / f.block * f.bytes;
-    return status(launch_dequant_row((const uint8_t *)w, type, row_bytes, row, (int)cols, (float *)out,
-                                     (hipStream_t)stream));
+    return status(launch_embed((const uint8_t *)w, type, row_bytes, (int)rows, (const uint32_t *)tokens, (int)count,
+                               (int)cols, (float *)out, (hipStream_t)stream));
 }
 
 NYA_HIP_EXPORT int nya_hip_rms_norm(uintptr_t x, uintptr_t residual, uintptr_t weight, uintptr_t out, size_t n,
-    float epsilon, uintptr_t stream)
+    size_t count, float epsilon, uintptr_t stream)
 {
-    if (!vec(x) || !vec(out) || (residual & 3u) || (weight & 3u) || !count_ok(n) || !(epsilon >= 0.f)) return 1;
+    if (!vec(x) || !vec(out) || (residual & 3u) || (weight & 3u) || !count_ok(n) || !tokens_ok(count) ||
+        !(epsilon >= 0.f))
+        return 1;
     return status(launch_rms_norm((float *)x, (const float *)residual, (const float *)weight, (float *)out, (int)n,
-                                  epsilon, (hipStream_t)stream));
+                                  (int)count, epsilon, (hipStream_t)stream));
 }
 
-NYA_HIP_EXPORT int nya_hip_rope_qkv(uintptr_t qkv, size_t heads, size_t kv_heads, size_t width,
-    uintptr_t frequencies, size_t position, uintptr_t key, uintptr_t value, uintptr_t stream)
+NYA_HIP_EXPORT int nya_hip_rope_qkv(uintptr_t q, size_t q_stride, uintptr_t k, size_t k_stride, uintptr_t v,
+    size_t v_stride, size_t count, size_t heads, size_t kv_heads, size_t width, uintptr_t frequencies,
+    uintptr_t positions, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream)
 {
-    if (!vec(qkv) || !vec(frequencies) || !vec(key) || !vec(value) || !count_ok(heads) || !count_ok(kv_heads) ||
-        !count_ok(width) || width % 2 || heads > (size_t)INT_MAX / 2 - kv_heads ||
-        heads + 2 * kv_heads > (size_t)INT_MAX / width || position > (size_t)INT_MAX)
+    if (!vec(q) || !vec(k) || !vec(v) || !vec(frequencies) || !vec(positions) || !vec(keys) || !vec(values) ||
+        !tokens_ok(count) || !count_ok(heads) || !count_ok(kv_heads) || !count_ok(width) || width % 2 ||
+        !count_ok(capacity) || heads > (size_t)INT_MAX / width || kv_heads > (size_t)INT_MAX / width ||
+        q_stride < heads * width || k_stride < kv_heads * width || v_stride < kv_heads * width ||
+        q_stride > (size_t)INT_MAX || k_stride > (size_t)INT_MAX || v_stride > (size_t)INT_MAX)
         return 1;
-    return status(launch_rope_qkv((float *)qkv, (int)heads, (int)kv_heads, (int)width, (const float *)frequencies,
-                                  (int)position, (float *)key, (float *)value, (hipStream_t)stream));
+    return status(launch_rope_qkv((float *)q, (int)q_stride, (const float *)k, (int)k_stride, (const float *)v,
+                                  (int)v_stride, (int)count, (int)heads, (int)kv_heads, (int)width,
+                                  (const float *)frequencies, (const int *)positions, (int)capacity, (float *)keys,
+                                  (float *)values, (hipStream_t)stream));
 }
 
-NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, uintptr_t keys, uintptr_t values, uintptr_t out, uintptr_t scores,
-    size_t heads, size_t kv_heads, size_t width, size_t length, float scale, uintptr_t stream)
+NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t keys, uintptr_t values, uintptr_t out,
+    uintptr_t scores, uintptr_t positions, size_t count, size_t heads, size_t kv_heads, size_t width,
+    size_t max_length, float scale, uintptr_t stream)
 {
-    if (!vec(q) || !vec(keys) || !vec(values) || !vec(out) || !vec(scores) || !count_ok(heads) ||
-        !count_ok(kv_heads) || !count_ok(width) || width > 256 || !count_ok(length) || heads % kv_heads ||
-        kv_heads > (size_t)INT_MAX / width || heads > (size_t)INT_MAX / length)
+    if (!vec(q) || !vec(keys) || !vec(values) || !vec(out) || !vec(positions) || (scores & 3u) ||
+        !tokens_ok(count) || !count_ok(heads) || !count_ok(kv_heads) || !count_ok(width) || width > 256 ||
+        !count_ok(max_length) || heads % kv_heads || kv_heads > (size_t)INT_MAX / width ||
+        q_stride < heads * width || q_stride > (size_t)INT_MAX || (max_length > 8192 && !scores) ||
+        heads > (size_t)INT_MAX / max_length)
         return 1;
-    return status(launch_attention((const float *)q, (const float *)keys, (const float *)values, (float *)out,
-                                   (float *)scores, (int)heads, (int)kv_heads, (int)width, (int)length, scale,
-                                   (hipStream_t)stream));
+    return status(launch_attention((const float *)q, (int)q_stride, (const float *)keys, (const float *)values,
+                                   (float *)out, (float *)scores, (const int *)positions, (int)count, (int)heads,
+                                   (int)kv_heads, (int)width, (int)max_length, scale, (hipStream_t)stream));
 }
 
-NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, uintptr_t up, size_t n, uintptr_t stream)
+NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, size_t gate_stride, uintptr_t up, size_t up_stride,
+    uintptr_t out, size_t n, size_t count, uintptr_t stream)
 {
-    if (!vec(gate) || !vec(up) || !count_ok(n)) return 1;
-    return status(launch_silu_mul((float *)gate, (const float *)up, (int)n, (hipStream_t)stream));
+    if (!vec(gate) || !vec(up) || !vec(out) || !count_ok(n) || !tokens_ok(count) || gate_stride < n ||
+        up_stride < n || gate_stride > (size_t)INT_MAX || up_stride > (size_t)INT_MAX)
+        return 1;
+    // One token may be rewritten in place (out = gate); across tokens the
+    // output must not overlap either input.
+    const size_t out_end = out + count * n * sizeof(float);
+    const size_t gate_end = gate + ((count - 1) * gate_stride + n) * sizeof(float);
+    const size_t up_end = up + ((count - 1) * up_stride + n) * sizeof(float);
+    if (count > 1 && ((out < gate_end && gate < out_end) || (out < up_end && up < out_end))) return 1;
+    return status(launch_silu_mul((const float *)gate, (int)gate_stride, (const float *)up, (int)up_stride,
+                                  (float *)out, (int)n, (int)count, (hipStream_t)stream));
 }
 
 }  // extern "C"

@@ -57,21 +57,30 @@ hipError_t launch_copy(uint4 *dst, const uint4 *src, size_t count, hipStream_t s
 // (dense.hip); `sink` holds kReadSinkWords words.
 constexpr int kReadSinkWords = 1024;
 hipError_t launch_read(const uint4 *src, size_t count, unsigned *sink, hipStream_t stream);
-// Vector steps of a resident decoder token (resident.hip), fp32 device
-// vectors: one row of a GGUF-layout matrix decoded (row_bytes its stored
-// size); x += r (when r is given) then out = RMS-normalized x times w (w may
-// be null); rotary encoding at `position` of a fused q|k|v product (q rotated
-// in place, k rotated into `key`, v copied into `value`); causal attention of
-// `heads` query heads of width <= 256 over `length` cached positions (scores:
-// heads x length scratch, used beyond 8192 positions); gate = silu(gate) * up.
-hipError_t launch_dequant_row(const uint8_t *w, unsigned type, size_t row_bytes, size_t row, int cols, float *out,
+// Vector steps of the resident decoder (resident.hip) over `count` tokens,
+// fp32 device vectors, token i's row at i times the row's stride (floats):
+// the decode step ids written (step[0] token, step[1] position); rows
+// tokens[i] of a GGUF-layout matrix decoded (row_bytes its stored size);
+// x += r (when r is given) then out = RMS-normalized x times w (w may be
+// null); rotary encoding at positions[i] (q rotated in place, k rotated into
+// its slot of `keys`, v copied into `values`, both
+// [capacity][kv_heads * width]); causal attention of each token's `heads`
+// query heads (width <= 256) over positions [0, positions[i]] (scores:
+// count x heads x max_length scratch, used past 8192 positions);
+// out = silu(gate) * up.
+hipError_t launch_set_step(uint32_t *step, uint32_t token, int position, hipStream_t stream);
+hipError_t launch_embed(const uint8_t *w, unsigned type, size_t row_bytes, int rows, const uint32_t *tokens, int count,
+    int cols, float *out, hipStream_t stream);
+hipError_t launch_rms_norm(float *x, const float *r, const float *w, float *out, int n, int count, float eps,
     hipStream_t stream);
-hipError_t launch_rms_norm(float *x, const float *r, const float *w, float *out, int n, float eps, hipStream_t stream);
-hipError_t launch_rope_qkv(float *qkv, int heads, int kv_heads, int width, const float *freq, int position, float *key,
-    float *value, hipStream_t stream);
-hipError_t launch_attention(const float *q, const float *keys, const float *values, float *out, float *scores,
-    int heads, int kv_heads, int width, int length, float scale, hipStream_t stream);
-hipError_t launch_silu_mul(float *gate, const float *up, int n, hipStream_t stream);
+hipError_t launch_rope_qkv(float *q, int q_stride, const float *k, int k_stride, const float *v, int v_stride,
+    int count, int heads, int kv_heads, int width, const float *freq, const int *positions, int capacity, float *keys,
+    float *values, hipStream_t stream);
+hipError_t launch_attention(const float *q, int q_stride, const float *keys, const float *values, float *out,
+    float *scores, const int *positions, int count, int heads, int kv_heads, int width, int max_length, float scale,
+    hipStream_t stream);
+hipError_t launch_silu_mul(const float *gate, int gate_stride, const float *up, int up_stride, float *out, int n,
+    int count, hipStream_t stream);
 
 // Compute units of the current device (counted once per device).
 int device_cu_count();

@@ -1,11 +1,15 @@
-// The vector operations of one decoder token kept on the device (the resident
-// plan of the ROCm provider): the embedding row, RMS normalization with the
-// residual add folded in, rotary position encoding with the KV cache store,
-// causal attention over the KV cache and the gated SiLU. Each restates one step of the engine's CPU token forward
+// The vector operations of the decoder kept on the device (the resident
+// plan of the ROCm provider), each over `count` tokens at once (one token
+// when decoding, a prompt chunk when prefilling): the embedding rows, RMS
+// normalization with the residual add folded in, rotary position encoding
+// with the KV cache store, causal attention over the KV cache and the gated
+// SiLU. Each restates one step of the engine's CPU token forward
 // (backend/core/llm_cpu.c:424-578, LLaMA branch) with the same operation
-// order per element; arithmetic is not contracted into fused multiply-adds
-// (the reference's C17 build does not contract either). The matrix products
-// between them are the library's quantized kernels.
+// order per element where the step is elementwise; arithmetic is not
+// contracted into fused multiply-adds (the reference's C17 build does not
+// contract either). The matrix products between them are the library's
+// quantized kernels. Token ids and positions are device arrays, so one
+// sequence of launches serves any token (and can be recorded once).
 #include <math.h>
 
 #include "kernels.h"
@@ -58,25 +62,34 @@ __device__ float element(const uint8_t *row, unsigned type, int i)
     }
 }
 
-__global__ __launch_bounds__(256) void dequant_row(const uint8_t *__restrict__ w, unsigned type, size_t row_bytes,
-    size_t row, int cols, float *__restrict__ out)
+// out[i][c] = element c of row tokens[i] (a token past the matrix gives a
+// zero row; the host checks ids first).
+__global__ __launch_bounds__(256) void embed(const uint8_t *__restrict__ w, unsigned type, size_t row_bytes,
+    int rows, const uint32_t *__restrict__ tokens, int cols, float *__restrict__ out)
 {
-    const uint8_t *r = w + row * row_bytes;
-    for (int i = blockIdx.x * 256 + threadIdx.x; i < cols; i += gridDim.x * 256) out[i] = element(r, type, i);
+    const uint32_t token = tokens[blockIdx.y];
+    float *o = out + (size_t)blockIdx.y * cols;
+    const uint8_t *r = w + (size_t)token * row_bytes;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < cols; i += gridDim.x * 256)
+        o[i] = token < (uint32_t)rows ? element(r, type, i) : 0.f;
 }
 
-// One workgroup of 1024 holding n <= 4096 K elements in registers (K float4
-// per thread; x, r and w all loaded before the first use). x += r first when
-// r is given (written back); then out = x * scale * w with
-// scale = 1 / sqrt(sum x^2 / n + eps), the sum of squares in double
-// (backend/core/llm_cpu.c:83-104; the order of the sum differs from the
-// reference's sequential one, in double either way).
+// One workgroup of 1024 per row (token), holding n <= 4096 K elements in
+// registers (K float4 per thread; x, r and w all loaded before the first
+// use). x += r first when r is given (written back); then
+// out = x * scale * w with scale = 1 / sqrt(sum x^2 / n + eps), the sum of
+// squares in double (backend/core/llm_cpu.c:83-104; the order of the sum
+// differs from the reference's sequential one, in double either way).
 template <int K>
 __global__ __launch_bounds__(1024) void rms_norm_regs(float4 *__restrict__ x, const float4 *__restrict__ r,
     const float4 *__restrict__ w, float4 *__restrict__ out, int n4, float eps)
 {
     __shared__ double part[16];
     const int t = threadIdx.x;
+    const size_t row = (size_t)blockIdx.x * n4;
+    x += row;
+    out += row;
+    if (r) r += row;
     float4 v[K], u[K], g[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -113,34 +126,24 @@ __global__ __launch_bounds__(1024) void rms_norm_regs(float4 *__restrict__ x, co
     }
 }
 
-// The same for any n and alignment: one workgroup of 256.
+// The same for any n and alignment: one workgroup of 256 per row.
 __global__ __launch_bounds__(256) void rms_norm(float *__restrict__ x, const float *__restrict__ r,
-    const float *__restrict__ w, float *__restrict__ out, int n, float eps, bool vector4)
+    const float *__restrict__ w, float *__restrict__ out, int n, float eps)
 {
     __shared__ double part[4];
     const int t = threadIdx.x;
+    const size_t row = (size_t)blockIdx.x * n;
+    x += row;
+    out += row;
+    if (r) r += row;
     double s = 0.0;
-    if (vector4) {
-        float4 *x4 = (float4 *)x;
-        const float4 *r4 = (const float4 *)r;
-        for (int i = t; i < n / 4; i += 256) {
-            float4 v = x4[i];
-            if (r) {
-                const float4 u = r4[i];
-                v = make_float4(v.x + u.x, v.y + u.y, v.z + u.z, v.w + u.w);
-                x4[i] = v;
-            }
-            s += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+    for (int i = t; i < n; i += 256) {
+        float v = x[i];
+        if (r) {
+            v = v + r[i];
+            x[i] = v;
         }
-    } else {
-        for (int i = t; i < n; i += 256) {
-            float v = x[i];
-            if (r) {
-                v = v + r[i];
-                x[i] = v;
-            }
-            s += (double)v * v;
-        }
+        s += (double)v * v;
     }
     for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
     if ((t & 63) == 0) part[t >> 6] = s;
@@ -150,30 +153,39 @@ __global__ __launch_bounds__(256) void rms_norm(float *__restrict__ x, const flo
     for (int i = t; i < n; i += 256) out[i] = x[i] * scale * (w ? w[i] : 1.0f);
 }
 
-// The rotary step of one token on the fused q|k|v product (q: heads * width,
-// then k and v: kv_heads * width each): every interleaved pair of q rotated
-// in place and of k rotated into the key cache slot, by angle
-// position * freq[j] (backend/core/llm_cpu.c:298-324, angles :429-432); v
-// copied into the value cache slot.
-__global__ __launch_bounds__(256) void rope_qkv(float *__restrict__ qkv, int heads, int kv_heads, int width,
-    const float *__restrict__ freq, int position, float *__restrict__ key, float *__restrict__ value)
+// The rotary step of token i = blockIdx.y at position positions[i]: its q
+// row (q + i q_stride, heads * width) rotated in place and its k row
+// (k + i k_stride, kv_heads * width) rotated into the key cache slot
+// keys + position * kv_heads * width, every interleaved pair by angle
+// position * freq[j] (backend/core/llm_cpu.c:298-324, angles :429-432); its
+// v row copied into the value cache slot. A position outside
+// [0, capacity) leaves the rows and the cache alone (the host checks
+// first).
+__global__ __launch_bounds__(256) void rope_qkv(float *__restrict__ q, int q_stride, const float *__restrict__ k,
+    int k_stride, const float *__restrict__ v, int v_stride, int heads, int kv_heads, int width,
+    const float *__restrict__ freq, const int *__restrict__ positions, int capacity, float *__restrict__ keys,
+    float *__restrict__ values)
 {
+    const int position = positions[blockIdx.y];
+    if (position < 0 || position >= capacity) return;
     const int pairs = width / 2, qn = heads * pairs, kn = kv_heads * pairs, vn = kv_heads * width;
-    const float *v_in = qkv + (size_t)(heads + kv_heads) * width;
+    float *qr = q + (size_t)blockIdx.y * q_stride;
+    const float *kr = k + (size_t)blockIdx.y * k_stride, *vr = v + (size_t)blockIdx.y * v_stride;
+    float *key = keys + (size_t)position * vn, *value = values + (size_t)position * vn;
     for (int i = blockIdx.x * 256 + threadIdx.x; i < qn + kn + vn; i += gridDim.x * 256) {
         if (i < qn + kn) {
             const bool is_q = i < qn;
             const int e = is_q ? i : i - qn, h = e / pairs, j = e % pairs;
             const float angle = (float)position * freq[j];
             const float c = cosf(angle), s = sinf(angle);
-            const float *src = qkv + (is_q ? 0 : (size_t)heads * width) + (size_t)h * width + 2 * j;
-            float *dst = (is_q ? qkv : key) + (size_t)h * width + 2 * j;
+            const float *src = (is_q ? qr : kr) + (size_t)h * width + 2 * j;
+            float *dst = (is_q ? qr : key) + (size_t)h * width + 2 * j;
             const float a = src[0], b = src[1];
             dst[0] = a * c - b * s;
             dst[1] = a * s + b * c;
         } else {
             const int e = i - qn - kn;
-            value[e] = v_in[e];
+            value[e] = vr[e];
         }
     }
 }
@@ -193,22 +205,44 @@ __device__ __forceinline__ float block_reduce(float v, float *red, bool maximum)
 }
 
 constexpr int kLdsScores = 8192;   // scores kept in LDS up to this length
-constexpr int kMaxWidth = 256;     // head width limit of the attention kernel
+constexpr int kMaxWidth = 256;     // head width limit of the attention kernels
 
-// One workgroup per query head, head width W (64, 128 or 256; q, keys and
-// values 16-byte aligned): scores q.k_t * scale for t < length, a softmax
-// over them, out = sum_t p_t v_t (backend/core/llm_cpu.c:491-511).
-// Scores: 16 lanes per key row, lane l16 holding float4 columns
-// l16 + 16 c of q and of the row; 64 rows in flight per workgroup (four per
-// 16 lanes), reduced across the 16 lanes. p_t = e^(s_t - max) / sum as in
-// the reference. Output: thread (g, c) sums float4 column c over
-// t = g, g + G, ... (G = 1024 / W groups), then the groups add up in order.
-// Scores in LDS up to kLdsScores positions, else in the [heads][length]
-// global scratch.
+// Attention of query token i = blockIdx.y, head blockIdx.x, over the cached
+// positions [0, positions[i]] (clamped to max_length): its q at
+// q + i * q_stride + head * W, its output at out + (i * heads + head) * W.
+struct AttentionRow {
+    int head, kvh, length;
+    size_t q, out, scores;
+};
+
+__device__ __forceinline__ AttentionRow attention_row(const int *positions, int heads, int kv_heads, int width,
+    int q_stride, int max_length)
+{
+    AttentionRow a;
+    a.head = blockIdx.x;
+    a.kvh = a.head / (heads / kv_heads);
+    const int p = positions[blockIdx.y];
+    a.length = p < 0 ? 0 : p >= max_length ? max_length : p + 1;
+    a.q = (size_t)blockIdx.y * q_stride + (size_t)a.head * width;
+    a.out = ((size_t)blockIdx.y * heads + a.head) * width;
+    a.scores = ((size_t)blockIdx.y * heads + a.head) * max_length;
+    return a;
+}
+
+// Head width W (64, 128 or 256; q, keys, values and out 16-byte aligned):
+// scores q.k_t * scale for t < length, a softmax over them,
+// out = sum_t p_t v_t (backend/core/llm_cpu.c:491-511). Scores: 16 lanes per
+// key row, lane l16 holding float4 columns l16 + 16 c of q and of the row;
+// 64 rows in flight per workgroup (four per 16 lanes), reduced across the
+// 16 lanes. p_t = e^(s_t - max) / sum as in the reference. Output: thread
+// (g, c) sums float4 column c over t = g, g + G, ... (G = 1024 / W groups),
+// then the groups add up in order. Scores in LDS (LDS: max_length <=
+// kLdsScores), else in the global scratch [count][heads][max_length].
 template <int W, bool LDS>
-__global__ __launch_bounds__(256) void attention_w(const float *__restrict__ q, const float *__restrict__ keys,
-    const float *__restrict__ values, float *__restrict__ out, float *__restrict__ scores, int heads, int kv_heads,
-    int length, float scale)
+__global__ __launch_bounds__(256) void attention_w(const float *__restrict__ q, int q_stride,
+    const float *__restrict__ keys, const float *__restrict__ values, float *__restrict__ out,
+    float *__restrict__ scores, const int *__restrict__ positions, int heads, int kv_heads, int max_length,
+    float scale)
 {
     constexpr int C = W / 64;            // float4 per lane per row
     constexpr int U = 4;                 // rows per 16 lanes in flight
@@ -216,15 +250,17 @@ __global__ __launch_bounds__(256) void attention_w(const float *__restrict__ q, 
     __shared__ float lds_scores[LDS ? kLdsScores : 1];
     __shared__ float4 part[256];
     __shared__ float red[4];
-    const int tid = threadIdx.x, head = blockIdx.x, kvh = head / (heads / kv_heads);
+    const AttentionRow a = attention_row(positions, heads, kv_heads, W, q_stride, max_length);
+    const int tid = threadIdx.x, length = a.length;
+    if (length == 0) return;
     const int kv4 = kv_heads * (W / 4);  // float4 per cached position
-    float *sc = LDS ? lds_scores : scores + (size_t)head * length;
+    float *sc = LDS ? lds_scores : scores + a.scores;
     const int l16 = tid & 15, row = tid >> 4;
-    const float4 *q4 = (const float4 *)q + (size_t)head * (W / 4);
+    const float4 *q4 = (const float4 *)(q + a.q);
     float4 qr[C];
 #pragma unroll
     for (int c = 0; c < C; ++c) qr[c] = q4[l16 + 16 * c];
-    const float4 *k4 = (const float4 *)keys + (size_t)kvh * (W / 4);
+    const float4 *k4 = (const float4 *)keys + (size_t)a.kvh * (W / 4);
     float m = -INFINITY;
     for (int t0 = 0; t0 < length; t0 += 16 * U) {
         float4 kr[U][C];
@@ -262,7 +298,7 @@ __global__ __launch_bounds__(256) void attention_w(const float *__restrict__ q, 
     for (int t = tid; t < length; t += 256) sc[t] = sc[t] / sum;
     __syncthreads();
     const int c = tid % (W / 4), g = tid / (W / 4);
-    const float4 *v4 = (const float4 *)values + (size_t)kvh * (W / 4) + c;
+    const float4 *v4 = (const float4 *)values + (size_t)a.kvh * (W / 4) + c;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int t0 = g; t0 < length; t0 += 4 * G) {
         float4 vr[4];
@@ -290,33 +326,33 @@ __global__ __launch_bounds__(256) void attention_w(const float *__restrict__ q, 
             const float4 b = part[k * (W / 4) + tid];
             o = make_float4(o.x + b.x, o.y + b.y, o.z + b.z, o.w + b.w);
         }
-        ((float4 *)out)[(size_t)head * (W / 4) + tid] = o;
+        ((float4 *)(out + a.out))[tid] = o;
     }
 }
 
-// The same for any even width up to kMaxWidth and any 4-byte alignment:
-// one workgroup per query head. Scores: 16 lanes per key row (a wave takes four rows at once, lanes
-// striding the width), reduced across the 16; p_t = e^(s_t - max) / sum as in
-// the reference. Output: 256 / width groups of threads each sum a strided
-// share of t per element, then the groups add up. keys / values:
-// [position][kv_heads * width] of one layer; scores in LDS, or in the
-// [heads][length] global scratch beyond kLdsScores.
+// The same for any even width up to kMaxWidth and any 4-byte alignment.
+// Scores: 16 lanes per key row (lanes striding the width), reduced across
+// the 16. Output: 256 / width groups of threads each sum a strided share of
+// t per element, then the groups add up.
 template <bool LDS>
-__global__ __launch_bounds__(256) void attention(const float *__restrict__ q, const float *__restrict__ keys,
-    const float *__restrict__ values, float *__restrict__ out, float *__restrict__ scores, int heads, int kv_heads,
-    int width, int length, float scale)
+__global__ __launch_bounds__(256) void attention(const float *__restrict__ q, int q_stride,
+    const float *__restrict__ keys, const float *__restrict__ values, float *__restrict__ out,
+    float *__restrict__ scores, const int *__restrict__ positions, int heads, int kv_heads, int width,
+    int max_length, float scale)
 {
     __shared__ float lds_scores[LDS ? kLdsScores : 1];
     __shared__ float qs[kMaxWidth];
     __shared__ float part[256];
     __shared__ float red[4];
-    const int tid = threadIdx.x, head = blockIdx.x, kvh = head / (heads / kv_heads);
+    const AttentionRow a = attention_row(positions, heads, kv_heads, width, q_stride, max_length);
+    const int tid = threadIdx.x, length = a.length;
+    if (length == 0) return;
     const size_t kvdim = (size_t)kv_heads * width;
-    float *sc = LDS ? lds_scores : scores + (size_t)head * length;
-    for (int j = tid; j < width; j += 256) qs[j] = q[(size_t)head * width + j];
+    float *sc = LDS ? lds_scores : scores + a.scores;
+    for (int j = tid; j < width; j += 256) qs[j] = q[a.q + j];
     __syncthreads();
     const int l16 = tid & 15, row = tid >> 4;   // 16 rows in flight per workgroup
-    const float *kb = keys + (size_t)kvh * width;
+    const float *kb = keys + (size_t)a.kvh * width;
     float m = -INFINITY;
     for (int t0 = 0; t0 < length; t0 += 16) {
         const int t = t0 + row;
@@ -345,7 +381,7 @@ __global__ __launch_bounds__(256) void attention(const float *__restrict__ q, co
     __syncthreads();
     const int groups = 256 / width, g = tid / width, j = tid % width;
     if (g < groups) {
-        const float *vb = values + (size_t)kvh * width + j;
+        const float *vb = values + (size_t)a.kvh * width + j;
         float acc = 0.f;
         for (int t = g; t < length; t += groups) acc += sc[t] * vb[(size_t)t * kvdim];
         part[tid] = acc;
@@ -354,26 +390,43 @@ __global__ __launch_bounds__(256) void attention(const float *__restrict__ q, co
     if (tid < width) {
         float acc = part[tid];
         for (int k = 1; k < groups; ++k) acc += part[k * width + tid];
-        out[(size_t)head * width + tid] = acc;
+        out[a.out + tid] = acc;
     }
 }
 
-// gate = silu(gate) * up, silu(x) = x / (1 + e^-x) (backend/core/llm_cpu.c:336-341):
-// four elements per thread (16-byte aligned, n a multiple of 4), else one.
+// out[i][j] = silu(gate[i][j]) * up[i][j] for token i = blockIdx.y (rows at
+// i times their strides), silu(x) = x / (1 + e^-x)
+// (backend/core/llm_cpu.c:336-341); four elements per thread where n and the
+// strides are multiples of 4 and the rows 16-byte aligned. out may be gate
+// itself for one token.
 __device__ __forceinline__ float silu_times(float x, float u) { return x / (1.0f + expf(-x)) * u; }
 
-__global__ __launch_bounds__(256) void silu_mul4(float4 *__restrict__ gate, const float4 *__restrict__ up, int n4)
+__global__ __launch_bounds__(256) void silu_mul4(const float4 *gate, int gate_stride4, const float4 *up,
+    int up_stride4, float4 *out, int n4)
 {
+    const float4 *g = gate + (size_t)blockIdx.y * gate_stride4, *u = up + (size_t)blockIdx.y * up_stride4;
+    float4 *o = out + (size_t)blockIdx.y * n4;
     for (int i = blockIdx.x * 256 + threadIdx.x; i < n4; i += gridDim.x * 256) {
-        const float4 g = gate[i], u = up[i];
-        gate[i] = make_float4(silu_times(g.x, u.x), silu_times(g.y, u.y), silu_times(g.z, u.z), silu_times(g.w, u.w));
+        const float4 a = g[i], b = u[i];
+        o[i] = make_float4(silu_times(a.x, b.x), silu_times(a.y, b.y), silu_times(a.z, b.z), silu_times(a.w, b.w));
     }
 }
 
-__global__ __launch_bounds__(256) void silu_mul(float *__restrict__ gate, const float *__restrict__ up, int n)
+__global__ __launch_bounds__(256) void silu_mul(const float *gate, int gate_stride, const float *up, int up_stride,
+    float *out, int n)
 {
-    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
-        gate[i] = silu_times(gate[i], up[i]);
+    const float *g = gate + (size_t)blockIdx.y * gate_stride, *u = up + (size_t)blockIdx.y * up_stride;
+    float *o = out + (size_t)blockIdx.y * n;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) o[i] = silu_times(g[i], u[i]);
+}
+
+// step[0] = token, step[1] = position: one decode token's ids, written on
+// the stream so that a recorded sequence of launches can read them.
+__global__ void set_step(uint32_t *step, uint32_t token, int position)
+{
+    if (threadIdx.x == 0) {
+        step[0] = token;
+        step[1] = (uint32_t)position;
     }
 }
 
@@ -381,79 +434,100 @@ unsigned grid_of(long n) { return (unsigned)(n < 256 * 1024 ? (n + 255) / 256 : 
 
 }  // namespace
 
-hipError_t launch_dequant_row(const uint8_t *w, unsigned type, size_t row_bytes, size_t row, int cols, float *out,
+hipError_t launch_set_step(uint32_t *step, uint32_t token, int position, hipStream_t s)
+{
+    hipLaunchKernelGGL(set_step, dim3(1), dim3(64), 0, s, step, token, position);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed(const uint8_t *w, unsigned type, size_t row_bytes, int rows, const uint32_t *tokens, int count,
+    int cols, float *out, hipStream_t s)
+{
+    hipLaunchKernelGGL(embed, dim3(grid_of(cols), (unsigned)count), dim3(256), 0, s, w, type, row_bytes, rows, tokens,
+                       cols, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm(float *x, const float *r, const float *w, float *out, int n, int count, float eps,
     hipStream_t s)
 {
-    hipLaunchKernelGGL(dequant_row, dim3(grid_of(cols)), dim3(256), 0, s, w, type, row_bytes, row, cols, out);
-    return hipGetLastError();
-}
-
-hipError_t launch_rms_norm(float *x, const float *r, const float *w, float *out, int n, float eps, hipStream_t s)
-{
-    const bool vector4 = (n & 3) == 0 && (((uintptr_t)x | (uintptr_t)r) & 15u) == 0;
-    const bool regs = vector4 && (((uintptr_t)w | (uintptr_t)out) & 15u) == 0 && n <= 4 * 4096;
+    const bool regs = (n & 3) == 0 && n <= 4 * 4096 &&
+                      (((uintptr_t)x | (uintptr_t)r | (uintptr_t)w | (uintptr_t)out) & 15u) == 0;
     const int n4 = n / 4;
+    const dim3 grid((unsigned)count);
     if (regs && n4 <= 1024)
-        hipLaunchKernelGGL(rms_norm_regs<1>, dim3(1), dim3(1024), 0, s, (float4 *)x, (const float4 *)r,
-                           (const float4 *)w, (float4 *)out, n4, eps);
+        hipLaunchKernelGGL(rms_norm_regs<1>, grid, dim3(1024), 0, s, (float4 *)x, (const float4 *)r, (const float4 *)w,
+                           (float4 *)out, n4, eps);
     else if (regs && n4 <= 2048)
-        hipLaunchKernelGGL(rms_norm_regs<2>, dim3(1), dim3(1024), 0, s, (float4 *)x, (const float4 *)r,
-                           (const float4 *)w, (float4 *)out, n4, eps);
+        hipLaunchKernelGGL(rms_norm_regs<2>, grid, dim3(1024), 0, s, (float4 *)x, (const float4 *)r, (const float4 *)w,
+                           (float4 *)out, n4, eps);
     else if (regs)
-        hipLaunchKernelGGL(rms_norm_regs<4>, dim3(1), dim3(1024), 0, s, (float4 *)x, (const float4 *)r,
-                           (const float4 *)w, (float4 *)out, n4, eps);
+        hipLaunchKernelGGL(rms_norm_regs<4>, grid, dim3(1024), 0, s, (float4 *)x, (const float4 *)r, (const float4 *)w,
+                           (float4 *)out, n4, eps);
     else
-        hipLaunchKernelGGL(rms_norm, dim3(1), dim3(256), 0, s, x, r, w, out, n, eps, vector4);
+        hipLaunchKernelGGL(rms_norm, grid, dim3(256), 0, s, x, r, w, out, n, eps);
     return hipGetLastError();
 }
 
-hipError_t launch_rope_qkv(float *qkv, int heads, int kv_heads, int width, const float *freq, int position, float *key,
-    float *value, hipStream_t s)
+hipError_t launch_rope_qkv(float *q, int q_stride, const float *k, int k_stride, const float *v, int v_stride,
+    int count, int heads, int kv_heads, int width, const float *freq, const int *positions, int capacity, float *keys,
+    float *values, hipStream_t s)
 {
     const long n = (long)(heads + kv_heads) * (width / 2) + (long)kv_heads * width;
-    hipLaunchKernelGGL(rope_qkv, dim3(grid_of(n)), dim3(256), 0, s, qkv, heads, kv_heads, width, freq, position, key,
-                       value);
+    hipLaunchKernelGGL(rope_qkv, dim3(grid_of(n), (unsigned)count), dim3(256), 0, s, q, q_stride, k, k_stride, v,
+                       v_stride, heads, kv_heads, width, freq, positions, capacity, keys, values);
     return hipGetLastError();
 }
 
 template <int W>
-void launch_attention_w(const float *q, const float *keys, const float *values, float *out, float *scores, int heads,
-    int kv_heads, int length, float scale, hipStream_t s)
+void launch_attention_w(const float *q, int q_stride, const float *keys, const float *values, float *out,
+    float *scores, const int *positions, int count, int heads, int kv_heads, int max_length, float scale,
+    hipStream_t s)
 {
-    if (length <= kLdsScores)
-        hipLaunchKernelGGL((attention_w<W, true>), dim3((unsigned)heads), dim3(256), 0, s, q, keys, values, out, scores,
-                           heads, kv_heads, length, scale);
+    const dim3 grid((unsigned)heads, (unsigned)count);
+    if (max_length <= kLdsScores)
+        hipLaunchKernelGGL((attention_w<W, true>), grid, dim3(256), 0, s, q, q_stride, keys, values, out, scores,
+                           positions, heads, kv_heads, max_length, scale);
     else
-        hipLaunchKernelGGL((attention_w<W, false>), dim3((unsigned)heads), dim3(256), 0, s, q, keys, values, out,
-                           scores, heads, kv_heads, length, scale);
+        hipLaunchKernelGGL((attention_w<W, false>), grid, dim3(256), 0, s, q, q_stride, keys, values, out, scores,
+                           positions, heads, kv_heads, max_length, scale);
 }
 
-hipError_t launch_attention(const float *q, const float *keys, const float *values, float *out, float *scores,
-    int heads, int kv_heads, int width, int length, float scale, hipStream_t s)
+hipError_t launch_attention(const float *q, int q_stride, const float *keys, const float *values, float *out,
+    float *scores, const int *positions, int count, int heads, int kv_heads, int width, int max_length, float scale,
+    hipStream_t s)
 {
     if (width > kMaxWidth) return hipErrorInvalidValue;
-    const bool aligned = (((uintptr_t)q | (uintptr_t)keys | (uintptr_t)values | (uintptr_t)out) & 15u) == 0;
+    const bool aligned = (q_stride & 3) == 0 &&
+                         (((uintptr_t)q | (uintptr_t)keys | (uintptr_t)values | (uintptr_t)out) & 15u) == 0;
+    const dim3 grid((unsigned)heads, (unsigned)count);
     if (aligned && width == 128)
-        launch_attention_w<128>(q, keys, values, out, scores, heads, kv_heads, length, scale, s);
+        launch_attention_w<128>(q, q_stride, keys, values, out, scores, positions, count, heads, kv_heads, max_length,
+                                scale, s);
     else if (aligned && width == 64)
-        launch_attention_w<64>(q, keys, values, out, scores, heads, kv_heads, length, scale, s);
+        launch_attention_w<64>(q, q_stride, keys, values, out, scores, positions, count, heads, kv_heads, max_length,
+                               scale, s);
     else if (aligned && width == 256)
-        launch_attention_w<256>(q, keys, values, out, scores, heads, kv_heads, length, scale, s);
-    else if (length <= kLdsScores)
-        hipLaunchKernelGGL(attention<true>, dim3((unsigned)heads), dim3(256), 0, s, q, keys, values, out, scores,
-                           heads, kv_heads, width, length, scale);
+        launch_attention_w<256>(q, q_stride, keys, values, out, scores, positions, count, heads, kv_heads, max_length,
+                                scale, s);
+    else if (max_length <= kLdsScores)
+        hipLaunchKernelGGL(attention<true>, grid, dim3(256), 0, s, q, q_stride, keys, values, out, scores, positions,
+                           heads, kv_heads, width, max_length, scale);
     else
-        hipLaunchKernelGGL(attention<false>, dim3((unsigned)heads), dim3(256), 0, s, q, keys, values, out, scores,
-                           heads, kv_heads, width, length, scale);
+        hipLaunchKernelGGL(attention<false>, grid, dim3(256), 0, s, q, q_stride, keys, values, out, scores, positions,
+                           heads, kv_heads, width, max_length, scale);
     return hipGetLastError();
 }
 
-hipError_t launch_silu_mul(float *gate, const float *up, int n, hipStream_t s)
+hipError_t launch_silu_mul(const float *gate, int gate_stride, const float *up, int up_stride, float *out, int n,
+    int count, hipStream_t s)
 {
-    if ((n & 3) == 0 && (((uintptr_t)gate | (uintptr_t)up) & 15u) == 0)
-        hipLaunchKernelGGL(silu_mul4, dim3(grid_of(n / 4)), dim3(256), 0, s, (float4 *)gate, (const float4 *)up, n / 4);
+    if (((n | gate_stride | up_stride) & 3) == 0 && (((uintptr_t)gate | (uintptr_t)up | (uintptr_t)out) & 15u) == 0)
+        hipLaunchKernelGGL(silu_mul4, dim3(grid_of(n / 4), (unsigned)count), dim3(256), 0, s, (const float4 *)gate,
+                           gate_stride / 4, (const float4 *)up, up_stride / 4, (float4 *)out, n / 4);
     else
-        hipLaunchKernelGGL(silu_mul, dim3(grid_of(n)), dim3(256), 0, s, gate, up, n);
+        hipLaunchKernelGGL(silu_mul, dim3(grid_of(n), (unsigned)count), dim3(256), 0, s, gate, gate_stride, up,
+                           up_stride, out, n);
     return hipGetLastError();
 }
 

@@ -98,7 +98,9 @@ class LlamaShape:
     blocks: int = 2
     context: int = 64
     vocabulary: int = 300
-    # GGML types of the embedding / output / attention / gate-up / down matrices.
+    # GGML types of the embedding / output / attention / gate-up / down
+    # matrices; optional "value" and "up" entries override the attention
+    # type for v and the gate-up type for up.
     types: dict = field(default_factory=lambda: {"embedding": Q4_K, "output": Q6_K, "attention": Q4_K,
                                                  "gate_up": Q4_K, "down": Q6_K})
     epsilon: float = 1e-5
@@ -119,7 +121,7 @@ def llama_tensors(shape: LlamaShape, shared_blocks: bool = False) -> list[tuple[
 
     def matrix(kind: str, rows: int, cols: int):
         seed[0] += 1
-        t = shape.types[kind]
+        t = shape.types[kind] if kind in shape.types else shape.types["attention" if kind == "value" else "gate_up"]
         return t, (cols, rows), synth.weights(t, rows, cols, seed[0])
 
     def norm(n: int):
@@ -132,12 +134,12 @@ def llama_tensors(shape: LlamaShape, shared_blocks: bool = False) -> list[tuple[
         out += [(f"blk.{b}.attn_norm.weight", *norm(d)),
                 (f"blk.{b}.attn_q.weight", *matrix("attention", d, d)),
                 (f"blk.{b}.attn_k.weight", *matrix("attention", kv, d)),
-                (f"blk.{b}.attn_v.weight", *matrix("attention", kv, d)),
+                (f"blk.{b}.attn_v.weight", *matrix("value", kv, d)),
                 (f"blk.{b}.attn_output.weight", *matrix("attention", d, d)),
                 (f"blk.{b}.ffn_norm.weight", *norm(d)),
                 (f"blk.{b}.ffn_gate.weight", *matrix("gate_up", h, d)),
                 (f"blk.{b}.ffn_down.weight", *matrix("down", d, h)),
-                (f"blk.{b}.ffn_up.weight", *matrix("gate_up", h, d))]
+                (f"blk.{b}.ffn_up.weight", *matrix("up", h, d))]
     if shared_blocks:
         first = out[3:]
         for b in range(1, shape.blocks):

@@ -41,12 +41,14 @@ typedef struct nya_kernel_library {
 /* libfyodor_hip's resident decoder steps (include/fyodor_hip.h). Optional:
  * without them the provider still multiplies matrices and declines plans. */
 typedef struct nya_resident_ops {
-    int (*dequant_row)(uintptr_t, unsigned, size_t, size_t, size_t, uintptr_t, uintptr_t);
-    int (*rms_norm)(uintptr_t, uintptr_t, uintptr_t, uintptr_t, size_t, float, uintptr_t);
-    int (*rope_qkv)(uintptr_t, size_t, size_t, size_t, uintptr_t, size_t, uintptr_t, uintptr_t, uintptr_t);
-    int (*attention)(uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, size_t, size_t, size_t, size_t, float,
-        uintptr_t);
-    int (*silu_mul)(uintptr_t, uintptr_t, size_t, uintptr_t);
+    int (*step)(uintptr_t, unsigned, size_t, uintptr_t);
+    int (*embed)(uintptr_t, unsigned, size_t, size_t, uintptr_t, size_t, uintptr_t, uintptr_t);
+    int (*rms_norm)(uintptr_t, uintptr_t, uintptr_t, uintptr_t, size_t, size_t, float, uintptr_t);
+    int (*rope_qkv)(uintptr_t, size_t, uintptr_t, size_t, uintptr_t, size_t, size_t, size_t, size_t, size_t,
+        uintptr_t, uintptr_t, size_t, uintptr_t, uintptr_t, uintptr_t);
+    int (*attention)(uintptr_t, size_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, size_t, size_t, size_t,
+        size_t, size_t, float, uintptr_t);
+    int (*silu_mul)(uintptr_t, size_t, uintptr_t, size_t, uintptr_t, size_t, size_t, uintptr_t);
 } nya_resident_ops;
 
 #define NYA_KERNEL_ABI 1U

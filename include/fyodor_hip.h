@@ -126,51 +126,71 @@ NYA_HIP_EXPORT int nya_hip_copy(uintptr_t dst, uintptr_t src, size_t bytes, uint
 #define NYA_HIP_READ_SINK_BYTES 4096
 NYA_HIP_EXPORT int nya_hip_read(uintptr_t src, size_t bytes, uintptr_t sink, uintptr_t stream);
 
-/* ---- resident decoder steps ------------------------------------------------
- * The vector steps of one decoder token, for a provider that keeps a whole
- * model's token forward on the device (the resident plan of
- * backend/include/compute.h:37-51; the reference's CUDA provider runs the
- * same steps as its own kernels, CUDA/resident.inc:466-578). All vectors are
- * fp32 device arrays (4-byte aligned); each call enqueues one kernel and
- * returns 0, 1 when declined (null or misaligned pointers, zero or
- * above-INT_MAX sizes), <0 on a HIP failure. Each restates one step of the
- * engine's CPU token forward, backend/core/llm_cpu.c:424-578 (LLaMA). */
+/* The vector steps of the decoder over `count` tokens (1..65535) at once,
+ * for a provider that keeps a whole model's token forward on the device (the
+ * resident plan of backend/include/compute.h:37-51; the reference's CUDA
+ * provider runs the same steps as its own kernels,
+ * CUDA/resident.inc:466-578). All vectors are fp32 device arrays (4-byte
+ * aligned), token i's row at i times the row length; token ids (uint32) and
+ * positions (int32) are device arrays, so the same calls serve every token.
+ * Each call enqueues one kernel and returns 0, 1 when declined (null or
+ * misaligned pointers, zero or out-of-range sizes), <0 on a HIP failure.
+ * Each restates one step of the engine's CPU token forward,
+ * backend/core/llm_cpu.c:424-578 (LLaMA). */
 
-/* out[cols] = row `row` of a [rows][cols] matrix of `type` in GGUF storage
- * (not packed), decoded as nya_llm_tensor_value does
+/* step[0] = token (uint32), step[1] = position (int32), written on the
+ * stream: the ids of one decode token for the calls below (tokens = step,
+ * positions = step + 4 bytes, count 1), so a recorded sequence of those
+ * calls serves every token. No counterpart in the reference (its CUDA plan
+ * passes them as kernel arguments, CUDA/resident.inc:466-578). */
+NYA_HIP_EXPORT int nya_hip_step(uintptr_t step, unsigned token, size_t position, uintptr_t stream);
+
+/* out[i][cols] = row tokens[i] of a [rows][cols] matrix of `type` in GGUF
+ * storage (not packed), decoded as nya_llm_tensor_value does
  * (backend/core/llm_quant.c:70-142): the token embedding gather
- * (backend/core/llm_cpu.c:71-80, :452-453). */
-NYA_HIP_EXPORT int nya_hip_dequant_row(uintptr_t w, unsigned type, size_t rows, size_t cols, size_t row,
-    uintptr_t out, uintptr_t stream);
+ * (backend/core/llm_cpu.c:71-80, :452-453). An id past the matrix gives a
+ * zero row. */
+NYA_HIP_EXPORT int nya_hip_embed(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t tokens,
+    size_t count, uintptr_t out, uintptr_t stream);
 
-/* When residual is nonzero, x += residual first (x is written back); then
- * out = x * s * weight with s = 1 / sqrt(sum x^2 / n + epsilon), the sum of
- * squares in double, weight 0 meaning ones (backend/core/llm_cpu.c:83-104;
- * the residual add of :514 folded in). */
+/* Per token row of n: when residual is nonzero, x += residual first (x is
+ * written back); then out = x * s * weight with
+ * s = 1 / sqrt(sum x^2 / n + epsilon), the sum of squares in double, weight
+ * 0 meaning ones (backend/core/llm_cpu.c:83-104; the residual add of :514
+ * folded in). */
 NYA_HIP_EXPORT int nya_hip_rms_norm(uintptr_t x, uintptr_t residual, uintptr_t weight, uintptr_t out, size_t n,
-    float epsilon, uintptr_t stream);
+    size_t count, float epsilon, uintptr_t stream);
 
-/* The rotary step of one token on a fused q|k|v product at qkv (`heads`
- * query heads, then `kv_heads` key heads and `kv_heads` value heads, each of
- * `width` elements): the interleaved pairs (2j, 2j+1) of every q head are
- * rotated in place and those of every k head into `key`, by the angle
- * position * frequencies[j] (backend/core/llm_cpu.c:298-324, angles
- * :429-432), and v is copied to `value` — the token's slots of the layer's
- * KV cache (the cache writes of :433-436). */
-NYA_HIP_EXPORT int nya_hip_rope_qkv(uintptr_t qkv, size_t heads, size_t kv_heads, size_t width,
-    uintptr_t frequencies, size_t position, uintptr_t key, uintptr_t value, uintptr_t stream);
+/* The rotary step of each token i at position p = positions[i]: its q row
+ * (q + i q_stride floats, `heads` heads of `width`) has the interleaved
+ * pairs (2j, 2j+1) of every head rotated in place, and its k row
+ * (k + i k_stride, kv_heads heads) rotated into keys + p kv_heads width, by
+ * the angle p * frequencies[j] (backend/core/llm_cpu.c:298-324, angles
+ * :429-432); its v row (v + i v_stride) is copied to
+ * values + p kv_heads width — the token's slots of the layer's KV cache
+ * ([capacity][kv_heads * width] each; the cache writes of :433-436). A
+ * position outside [0, capacity) leaves the rows and the cache alone. */
+NYA_HIP_EXPORT int nya_hip_rope_qkv(uintptr_t q, size_t q_stride, uintptr_t k, size_t k_stride, uintptr_t v,
+    size_t v_stride, size_t count, size_t heads, size_t kv_heads, size_t width, uintptr_t frequencies,
+    uintptr_t positions, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream);
 
-/* Causal attention of one query token: for each of `heads` heads (grouped
- * onto kv_heads key/value heads, width at most 256), scores q.k_t * scale
- * over the `length` cached positions of keys / values
- * ([length][kv_heads * width] rows), a softmax, and out = sum_t p_t v_t
- * (backend/core/llm_cpu.c:491-511). `scores` is scratch of heads * length
- * floats. */
-NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, uintptr_t keys, uintptr_t values, uintptr_t out,
-    uintptr_t scores, size_t heads, size_t kv_heads, size_t width, size_t length, float scale, uintptr_t stream);
+/* Causal attention of each token (its q at q + i q_stride): for each of
+ * `heads` heads (grouped onto kv_heads key/value heads, width at most 256),
+ * scores q.k_t * scale over the cached positions t = 0 .. positions[i]
+ * (at most max_length) of keys / values ([max_length][kv_heads * width]
+ * rows), a softmax, and out[i] = sum_t p_t v_t (backend/core/llm_cpu.c:491-511).
+ * `scores` is scratch of count * heads * max_length floats, needed (and
+ * used) only when max_length exceeds 8192. */
+NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t keys, uintptr_t values, uintptr_t out,
+    uintptr_t scores, uintptr_t positions, size_t count, size_t heads, size_t kv_heads, size_t width,
+    size_t max_length, float scale, uintptr_t stream);
 
-/* gate = gate / (1 + e^-gate) * up (backend/core/llm_cpu.c:336-341, SiLU). */
-NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, uintptr_t up, size_t n, uintptr_t stream);
+/* out[i][j] = g / (1 + e^-g) * u with g = gate[i gate_stride + j],
+ * u = up[i up_stride + j], out rows of n (backend/core/llm_cpu.c:336-341,
+ * SiLU of the gate times the up product). For one token out may be gate
+ * itself; for several it must not overlap either input. */
+NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, size_t gate_stride, uintptr_t up, size_t up_stride,
+    uintptr_t out, size_t n, size_t count, uintptr_t stream);
 
 #ifdef __cplusplus
 }

@@ -143,10 +143,12 @@ def check_kv(ref: Session, got: Session, layers: int, width: int, count: int):
     return worst
 
 
-def compare(lib, path: Path, shape, provider: str, tokens: list[int]) -> dict:
+def compare(lib, path: Path, shape, provider: str, tokens: list[int], chunks=(5, 1, 1, 7, 1)) -> dict:
     """Token-by-token decode, then (after a reset) prefill chunks mixed with
-    decode steps, on the reference and on `provider`; every step's logits and
-    the final KV caches compared. Returns the worst scaled errors."""
+    decode steps (`chunks`: tokens per session run; runs of more than one
+    token are the plan's prefill), on the reference and on `provider`; every
+    step's logits and the final KV caches compared. Returns the worst scaled
+    errors."""
     ref_model, model = Model(lib, path, None), Model(lib, path, provider)
     assert model.provider() == provider
     ref, got = Session(ref_model, shape.context), Session(model, shape.context)
@@ -161,7 +163,7 @@ def compare(lib, path: Path, shape, provider: str, tokens: list[int]) -> dict:
         # Reset, then prefill chunks (the plan's prefill) between decode steps.
         ref.reset()
         got.reset()
-        at, chunks = 0, [5, 1, 1, 7, 1]
+        at = 0
         for n in chunks:
             part = [(i * 7 + 3) % shape.vocabulary for i in range(at, at + n)]
             assert ref.run(part, n == 1) == 0 and got.run(part, n == 1) == 0

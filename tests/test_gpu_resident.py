@@ -4,7 +4,8 @@ sources into oracle/_ref/libnya_dropin.so with this repository's provider
 registered) run a random-weight LLaMA GGUF (tests/gguf_model.py) with
 NYA_COMPUTE=rocm — the whole token forward on the GPU through the gfx950
 kernels — and every decode step's logits, the KV cache, and after a reset
-prefill chunks between decode steps, match the engine's scalar reference
+prompt chunks (batched through the prefill GEMM and the small-N kernels)
+between decode steps, match the engine's scalar reference
 session within its own inference-test bounds
 (backend/tests/test_inference.c:9-33, :207-219): logits within
 5e-4 (1 + |ref|), K/V within 1.5e-4 (1 + |ref|)."""
@@ -42,13 +43,17 @@ TOKENS = [(i * 37 + 11) % 1000 for i in range(40)]
 @pytest.mark.parametrize("types", [
     {"embedding": Q4_K, "output": Q6_K, "attention": Q4_K, "gate_up": Q4_K, "down": Q6_K},
     {"embedding": F16, "output": Q8_0, "attention": Q8_0, "gate_up": Q4_0, "down": Q8_0},
-], ids=["k-quants", "q8-q4-f16"])
+    # v and up of other types than q/k and gate: the products run as separate parts.
+    {"embedding": Q4_K, "output": Q6_K, "attention": Q4_K, "value": Q6_K, "gate_up": Q4_K, "up": Q8_0, "down": Q6_K},
+], ids=["k-quants", "q8-q4-f16", "split-products"])
 def test_resident_plan_on_gpu(session_lib, rocm_env, tmp_path, types):
     shape = LlamaShape(embedding=512, heads=8, kv_heads=2, hidden=1024, blocks=3, context=64, vocabulary=1000,
                        types=types, seed=3)
     path = tmp_path / "model.gguf"
     write(path, shape)
-    out = compare(session_lib, path, shape, "rocm", TOKENS)
+    # Prompt chunks of 37 and 13 tokens run the batched forward on the
+    # prefill GEMM; 5 on the small-N kernels; single tokens decode.
+    out = compare(session_lib, path, shape, "rocm", TOKENS, chunks=(37, 1, 5, 1, 13, 1))
     print(f"resident plan: worst scaled logit error {out['logit']:.3g}, KV {out['kv']:.3g}", flush=True)
     assert out["execution"] == "resident"
     s = out["stats"]

@@ -1,17 +1,22 @@
 """The resident decoder steps of libfyodor_hip.so (include/fyodor_hip.h),
-each called through the C-ABI on an MI355X and compared with a float64
-numpy statement of the engine's step (backend/core/llm_cpu.c:71-104,
-:298-341, :429-436, :491-511) on seeded inputs:
+each called through the C-ABI on an MI355X over one and several tokens, and
+compared with a float64 numpy statement of the engine's step
+(backend/core/llm_cpu.c:71-104, :298-341, :429-436, :491-511) on seeded
+inputs:
 
-- dequant_row: bit-exact against the oracle's GGUF decoder, every type;
-- rms_norm (with and without the residual add, on the vector and scalar
-  paths): within 2e-6 (1 + |ref|);
-- rope_qkv (q rotated in place, k rotated into the key slot, v copied):
-  within 2e-6 (1 + |ref|), the v copy exact;
+- step: the decode slot holds the token id and position;
+- embed: bit-exact against the oracle's GGUF decoder, every type; an id past
+  the matrix gives a zero row;
+- rms_norm (with and without the residual add, vector and scalar paths,
+  several rows): within 2e-6 (1 + |ref|);
+- rope_qkv (fused q|k|v rows and separate q / k,v blocks; q rotated in place,
+  k rotated into its cache slot, v copied; a position past the cache leaves
+  everything alone): within 2e-6 (1 + |ref|), the v copy exact;
 - attention at head widths 64 / 80 / 128 / 256, grouped and ungrouped heads,
-  lengths from 1 through the LDS limit (8192) into the global-scratch path:
-  within 1e-5 (1 + |ref|);
-- silu_mul: within 2e-6 (1 + |ref|).
+  one query and causal runs of several, lengths from 1 through the LDS limit
+  (8192) into the global-scratch path: within 1e-5 (1 + |ref|);
+- silu_mul (fused [gate | up] rows, separate blocks, in place for one
+  token): within 2e-6 (1 + |ref|).
 The bounds are fp32 rounding over these sums, far inside the engine's own
 inference bounds (logits 5e-4 (1 + |ref|))."""
 import ctypes
@@ -19,23 +24,24 @@ import ctypes
 import numpy as np
 import pytest
 
-from fyodor_amd import BF16, F16, F32, Q4_0, Q4_K, Q6_K, Q8_0, storage_bytes, synth
+from fyodor_amd import BF16, F16, F32, Q4_0, Q4_K, Q6_K, Q8_0, synth
 from fyodor_amd.hip import Kernels, Runtime
 
 pytestmark = pytest.mark.gpu
 
-_up, _sz = ctypes.c_uint64, ctypes.c_size_t
+_up, _sz, _u, _f = ctypes.c_uint64, ctypes.c_size_t, ctypes.c_uint, ctypes.c_float
 
 
 @pytest.fixture(scope="module")
 def env():
     rt, kern = Runtime(), Kernels()
     L = kern.lib
-    L.nya_hip_dequant_row.argtypes = [_up, ctypes.c_uint, _sz, _sz, _sz, _up, _up]
-    L.nya_hip_rms_norm.argtypes = [_up, _up, _up, _up, _sz, ctypes.c_float, _up]
-    L.nya_hip_rope_qkv.argtypes = [_up, _sz, _sz, _sz, _up, _sz, _up, _up, _up]
-    L.nya_hip_attention.argtypes = [_up, _up, _up, _up, _up, _sz, _sz, _sz, _sz, ctypes.c_float, _up]
-    L.nya_hip_silu_mul.argtypes = [_up, _up, _sz, _up]
+    L.nya_hip_step.argtypes = [_up, _u, _sz, _up]
+    L.nya_hip_embed.argtypes = [_up, _u, _sz, _sz, _up, _sz, _up, _up]
+    L.nya_hip_rms_norm.argtypes = [_up, _up, _up, _up, _sz, _sz, _f, _up]
+    L.nya_hip_rope_qkv.argtypes = [_up, _sz, _up, _sz, _up, _sz, _sz, _sz, _sz, _sz, _up, _up, _sz, _up, _up, _up]
+    L.nya_hip_attention.argtypes = [_up, _sz, _up, _up, _up, _up, _up, _sz, _sz, _sz, _sz, _sz, _f, _up]
+    L.nya_hip_silu_mul.argtypes = [_up, _sz, _up, _sz, _up, _sz, _sz, _up]
     stream = rt.stream()
     yield rt, L, stream
     rt.sync(stream)
@@ -70,41 +76,59 @@ def scaled_error(got, ref):
     return float(np.max(np.abs(got.astype(np.float64) - ref) / (1 + np.abs(ref))))
 
 
-@pytest.mark.parametrize("type_id", [F32, F16, BF16, Q8_0, Q4_0, Q4_K, Q6_K])
-def test_dequant_row_exact(env, oracle, type_id):
+def test_step_slot(env):
     rt, L, stream = env
-    rows, cols = 7, 512
-    w = synth.weights(type_id, rows, cols, seed=40 + type_id)
-    ref = oracle.dequant(w, type_id, rows, cols).reshape(rows, cols)
     dev = Dev(rt)
     try:
-        wd, out = dev.put(w), dev.empty(4 * cols)
-        for row in (0, 3, rows - 1):
-            assert L.nya_hip_dequant_row(wd, type_id, rows, cols, row, out, stream) == 0
-            rt.sync(stream)
-            got = dev.get(out, np.empty(cols, np.float32))
-            assert np.array_equal(got.view(np.uint32), ref[row].view(np.uint32)), f"row {row}"
-        assert L.nya_hip_dequant_row(wd, type_id, rows, cols, rows, out, stream) == 1   # row out of range
+        slot = dev.empty(8)
+        assert L.nya_hip_step(slot, 31999, 1234, stream) == 0
+        rt.sync(stream)
+        assert dev.get(slot, np.empty(2, np.uint32)).tolist() == [31999, 1234]
+        assert L.nya_hip_step(slot + 2, 1, 0, stream) == 1   # misaligned
     finally:
         dev.close()
 
 
-@pytest.mark.parametrize("n,offset", [(4096, 0), (4098, 0), (4096, 4)], ids=["vector", "ragged", "misaligned"])
+@pytest.mark.parametrize("type_id", [F32, F16, BF16, Q8_0, Q4_0, Q4_K, Q6_K])
+def test_embed_exact(env, oracle, type_id):
+    rt, L, stream = env
+    rows, cols = 7, 512
+    w = synth.weights(type_id, rows, cols, seed=40 + type_id)
+    ref = oracle.dequant(w, type_id, rows, cols).reshape(rows, cols)
+    tokens = np.array([3, 0, rows - 1, rows + 5, 3], np.uint32)   # one id past the matrix
+    dev = Dev(rt)
+    try:
+        wd, td, out = dev.put(w), dev.put(tokens), dev.empty(4 * cols * len(tokens))
+        assert L.nya_hip_embed(wd, type_id, rows, cols, td, len(tokens), out, stream) == 0
+        rt.sync(stream)
+        got = dev.get(out, np.empty((len(tokens), cols), np.float32))
+        for i, t in enumerate(tokens):
+            want = ref[t] if t < rows else np.zeros(cols, np.float32)
+            assert np.array_equal(got[i].view(np.uint32), want.view(np.uint32)), f"token {i} (id {t})"
+        assert L.nya_hip_embed(wd, type_id, rows, cols, td, 0, out, stream) == 1      # no tokens
+    finally:
+        dev.close()
+
+
+@pytest.mark.parametrize("n,offset", [(4096, 0), (2048, 0), (4098, 0), (4096, 4), (16384, 0)],
+                         ids=["vector", "half", "ragged", "misaligned", "wide"])
 @pytest.mark.parametrize("residual", [False, True])
 def test_rms_norm(env, n, offset, residual):
     rt, L, stream = env
+    count = 3
     rng = np.random.default_rng(n + offset)
-    x, r = rng.standard_normal(n).astype(np.float32), rng.standard_normal(n).astype(np.float32)
+    x = rng.standard_normal((count, n)).astype(np.float32)
+    r = rng.standard_normal((count, n)).astype(np.float32)
     w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
     eps = 1e-5
     xs32 = (x + r if residual else x).astype(np.float32)
     xs = xs32.astype(np.float64)
-    scale = 1.0 / np.sqrt(np.sum(xs * xs) / n + eps)
-    ref = xs32.astype(np.float64) * np.float32(scale) * w
+    scale = 1.0 / np.sqrt(np.sum(xs * xs, axis=1, keepdims=True) / n + eps)
+    ref = xs * scale.astype(np.float32) * w
     dev = Dev(rt)
     try:
-        xd, rd, wd, od = dev.put(x, offset), dev.put(r, offset), dev.put(w), dev.empty(4 * n)
-        assert L.nya_hip_rms_norm(xd, rd if residual else 0, wd, od, n, eps, stream) == 0
+        xd, rd, wd, od = dev.put(x, offset), dev.put(r, offset), dev.put(w), dev.empty(4 * n * count)
+        assert L.nya_hip_rms_norm(xd, rd if residual else 0, wd, od, n, count, eps, stream) == 0
         rt.sync(stream)
         assert scaled_error(dev.get(od, x), ref) <= 2e-6
         assert np.array_equal(dev.get(xd, x), xs32)      # the residual add written back (or x untouched)
@@ -112,34 +136,66 @@ def test_rms_norm(env, n, offset, residual):
         dev.close()
 
 
+def rotate(v, c, s, pairs):
+    v = v.reshape(-1, pairs, 2).astype(np.float64)
+    a, b = v[..., 0], v[..., 1]
+    return np.stack([a * c - b * s, a * s + b * c], -1).reshape(-1)
+
+
+@pytest.mark.parametrize("layout", ["fused", "split"])
 @pytest.mark.parametrize("heads,kv_heads,width", [(32, 8, 128), (4, 4, 64), (6, 2, 80)])
-def test_rope_qkv(env, heads, kv_heads, width):
+def test_rope_qkv(env, heads, kv_heads, width, layout):
     rt, L, stream = env
+    count, capacity = 4, 2000
+    positions = np.array([1234, 1235, 1236, capacity + 3], np.int32)   # the last is outside the cache
+    qd, kvd = heads * width, kv_heads * width
     rng = np.random.default_rng(heads * width)
-    qkv = rng.standard_normal((heads + 2 * kv_heads) * width).astype(np.float32)
     pairs = width // 2
     freq = (10000.0 ** (-np.arange(pairs) / pairs)).astype(np.float32)
-    position = 1234
-    angle = (np.float32(position) * freq).astype(np.float64)
-    c, s = np.cos(angle), np.sin(angle)
-
-    def rotate(v):
-        v = v.reshape(-1, pairs, 2).astype(np.float64)
-        a, b = v[..., 0], v[..., 1]
-        return np.stack([a * c - b * s, a * s + b * c], -1).reshape(-1)
-
-    q, k, v = np.split(qkv, [heads * width, (heads + kv_heads) * width])
+    if layout == "fused":
+        rows = rng.standard_normal((count, qd + 2 * kvd)).astype(np.float32)
+        qs = ks = vs = qd + 2 * kvd
+        q_at, k_at, v_at = 0, qd, qd + kvd
+        blocks = [rows]
+    else:   # q in one block, k|v in another (types that differ)
+        qb = rng.standard_normal((count, qd)).astype(np.float32)
+        kvb = rng.standard_normal((count, 2 * kvd)).astype(np.float32)
+        qs, ks, vs = qd, 2 * kvd, 2 * kvd
+        blocks = [qb, kvb]
+    keys0 = rng.standard_normal((capacity, kvd)).astype(np.float32)
+    values0 = rng.standard_normal((capacity, kvd)).astype(np.float32)
     dev = Dev(rt)
     try:
-        qd, fd = dev.put(qkv), dev.put(freq)
-        kd, vd = dev.empty(k.nbytes), dev.empty(v.nbytes)
-        assert L.nya_hip_rope_qkv(qd, heads, kv_heads, width, fd, position, kd, vd, stream) == 0
+        ptrs = [dev.put(b) for b in blocks]
+        if layout == "fused":
+            q, k, v = ptrs[0] + 4 * q_at, ptrs[0] + 4 * k_at, ptrs[0] + 4 * v_at
+        else:
+            q, k, v = ptrs[0], ptrs[1], ptrs[1] + 4 * kvd
+        fd, pd, kd, vd = dev.put(freq), dev.put(positions), dev.put(keys0), dev.put(values0)
+        assert L.nya_hip_rope_qkv(q, qs, k, ks, v, vs, count, heads, kv_heads, width, fd, pd, capacity, kd, vd,
+                                  stream) == 0
         rt.sync(stream)
-        out = dev.get(qd, qkv)
-        assert scaled_error(out[:q.size], rotate(q)) <= 2e-6
-        assert np.array_equal(out[q.size:], qkv[q.size:])                 # k and v left in place
-        assert scaled_error(dev.get(kd, k), rotate(k)) <= 2e-6
-        assert np.array_equal(dev.get(vd, v), v)
+        got = [dev.get(p, b) for p, b in zip(ptrs, blocks)]
+        keys, values = dev.get(kd, keys0), dev.get(vd, values0)
+        for i, pos in enumerate(positions):
+            if layout == "fused":
+                qin, kin, vin = blocks[0][i, :qd], blocks[0][i, qd:qd + kvd], blocks[0][i, qd + kvd:]
+                qout, kvout = got[0][i, :qd], got[0][i, qd:]
+            else:
+                qin, kin, vin = blocks[0][i], blocks[1][i, :kvd], blocks[1][i, kvd:]
+                qout, kvout = got[0][i], got[1][i]
+            assert np.array_equal(kvout, np.concatenate([kin, vin]))          # k and v rows left in place
+            if pos >= capacity:
+                assert np.array_equal(qout, qin)
+                continue
+            angle = (np.float32(pos) * freq).astype(np.float64)
+            c, s = np.cos(angle), np.sin(angle)
+            assert scaled_error(qout, rotate(qin, c, s, pairs)) <= 2e-6
+            assert scaled_error(keys[pos], rotate(kin, c, s, pairs)) <= 2e-6
+            assert np.array_equal(values[pos], vin)
+        untouched = np.setdiff1d(np.arange(capacity), positions[positions < capacity])
+        assert np.array_equal(keys[untouched], keys0[untouched])
+        assert np.array_equal(values[untouched], values0[untouched])
     finally:
         dev.close()
 
@@ -158,53 +214,74 @@ def attention_ref(q, keys, values, heads, kv_heads, width, length, scale):
     return out.reshape(-1)
 
 
-@pytest.mark.parametrize("heads,kv_heads,width,length", [
-    (32, 8, 128, 1), (32, 8, 128, 37), (32, 8, 128, 1000), (8, 8, 64, 300), (6, 2, 80, 129), (4, 1, 256, 513),
-    (8, 2, 128, 8192), (8, 2, 128, 9000),
+@pytest.mark.parametrize("heads,kv_heads,width,length,count", [
+    (32, 8, 128, 1, 1), (32, 8, 128, 37, 1), (32, 8, 128, 1000, 1), (8, 8, 64, 300, 1), (6, 2, 80, 129, 1),
+    (4, 1, 256, 513, 1), (8, 2, 128, 8192, 1), (8, 2, 128, 9000, 1),
+    (32, 4, 64, 64, 64), (8, 2, 128, 300, 5), (6, 2, 80, 40, 7), (4, 2, 128, 8300, 3),
 ])
-def test_attention(env, heads, kv_heads, width, length):
+def test_attention(env, heads, kv_heads, width, length, count):
+    """`count` causal queries ending at position length - 1, the query rows
+    strided past the fused k|v part as in the plan's buffers."""
     rt, L, stream = env
-    rng = np.random.default_rng(length * 7 + width)
-    capacity = length + 5
-    q = rng.standard_normal(heads * width).astype(np.float32)
-    keys = rng.standard_normal((capacity, kv_heads * width)).astype(np.float32)
-    values = rng.standard_normal((capacity, kv_heads * width)).astype(np.float32)
+    rng = np.random.default_rng(length * 7 + width + count)
+    max_length = length + 5
+    q_stride = (heads + 2 * kv_heads) * width
+    q = rng.standard_normal((count, q_stride)).astype(np.float32)
+    keys = rng.standard_normal((max_length, kv_heads * width)).astype(np.float32)
+    values = rng.standard_normal((max_length, kv_heads * width)).astype(np.float32)
+    positions = np.arange(length - count, length, dtype=np.int32)
     scale = float(1 / np.sqrt(np.float32(width)))
-    ref = attention_ref(q, keys, values, heads, kv_heads, width, length, np.float32(scale))
+    ref = np.concatenate([attention_ref(q[i, :heads * width], keys, values, heads, kv_heads, width, int(p) + 1,
+                                        np.float32(scale)) for i, p in enumerate(positions)])
     dev = Dev(rt)
     try:
-        qd, kd, vd = dev.put(q), dev.put(keys), dev.put(values)
-        od, sd = dev.empty(q.nbytes), dev.empty(4 * heads * length)
-        assert L.nya_hip_attention(qd, kd, vd, od, sd, heads, kv_heads, width, length, scale, stream) == 0
+        qd, kd, vd, pd = dev.put(q), dev.put(keys), dev.put(values), dev.put(positions)
+        od = dev.empty(4 * count * heads * width)
+        sd = dev.empty(4 * count * heads * max_length) if max_length > 8192 else 0
+        assert L.nya_hip_attention(qd, q_stride, kd, vd, od, sd, pd, count, heads, kv_heads, width, max_length, scale,
+                                   stream) == 0
         rt.sync(stream)
-        err = scaled_error(dev.get(od, q), ref)
-        print(f"attention {heads}/{kv_heads} x {width}, length {length}: scaled error {err:.3g}", flush=True)
+        err = scaled_error(dev.get(od, np.empty(count * heads * width, np.float32)), ref)
+        print(f"attention {heads}/{kv_heads} x {width}, length {length}, {count} queries: scaled error {err:.3g}",
+              flush=True)
         assert err <= 1e-5
     finally:
         dev.close()
 
 
-def test_attention_declines_wide_heads(env):
+def test_attention_declines(env):
     rt, L, stream = env
     dev = Dev(rt)
     try:
         p = dev.empty(4 * 4 * 512)
-        assert L.nya_hip_attention(p, p, p, p, p, 2, 2, 512, 1, 1.0, stream) == 1
+        assert L.nya_hip_attention(p, 1024, p, p, p, p, p, 1, 2, 2, 512, 1, 1.0, stream) == 1   # width > 256
+        assert L.nya_hip_attention(p, 256, p, p, p, 0, p, 1, 2, 2, 128, 9000, 1.0, stream) == 1  # scratch needed
     finally:
         dev.close()
 
 
-def test_silu_mul(env):
+@pytest.mark.parametrize("layout", ["fused", "split", "in-place"])
+def test_silu_mul(env, layout):
     rt, L, stream = env
     rng = np.random.default_rng(5)
     n = 14336
-    g, u = (4 * rng.standard_normal(n)).astype(np.float32), rng.standard_normal(n).astype(np.float32)
+    count = 1 if layout == "in-place" else 3
+    g = (4 * rng.standard_normal((count, n))).astype(np.float32)
+    u = rng.standard_normal((count, n)).astype(np.float32)
     ref = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u
     dev = Dev(rt)
     try:
-        gd, ud = dev.put(g), dev.put(u)
-        assert L.nya_hip_silu_mul(gd, ud, n, stream) == 0
+        if layout == "split":
+            gd, ud = dev.put(g), dev.put(u)
+            gs = us = n
+        else:
+            gu = dev.put(np.concatenate([g, u], axis=1))
+            gd, ud, gs, us = gu, gu + 4 * n, 2 * n, 2 * n
+        out = gd if layout == "in-place" else dev.empty(4 * n * count)
+        assert L.nya_hip_silu_mul(gd, gs, ud, us, out, n, count, stream) == 0
         rt.sync(stream)
-        assert scaled_error(dev.get(gd, g), ref) <= 2e-6
+        assert scaled_error(dev.get(out, g), ref) <= 2e-6
+        if layout != "in-place":
+            assert L.nya_hip_silu_mul(gd, gs, ud, us, gd, n, count, stream) == 1   # overlapping output
     finally:
         dev.close()

@@ -38,7 +38,8 @@ def session_lib(dropin_library, mock_paths, monkeypatch):
 @pytest.mark.parametrize("types", [
     {"embedding": Q4_K, "output": Q6_K, "attention": Q4_K, "gate_up": Q4_K, "down": Q6_K},
     {"embedding": F16, "output": Q8_0, "attention": Q8_0, "gate_up": Q4_0, "down": Q8_0},
-], ids=["k-quants", "q8-q4-f16"])
+    {"embedding": Q4_K, "output": Q6_K, "attention": Q4_K, "value": Q6_K, "gate_up": Q4_K, "up": Q8_0, "down": Q6_K},
+], ids=["k-quants", "q8-q4-f16", "split-products"])
 def test_resident_plan_matches_reference_session(session_lib, tmp_path, types):
     shape = LlamaShape(types=types, context=32)
     path = tmp_path / "model.gguf"

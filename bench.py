@@ -8,8 +8,10 @@ weight matrix; weights and activations are resident in HBM before timing.
 
 - Enough distinct weight copies rotate to exceed twice the 256 MB Infinity
   Cache, so every step streams its weights from HBM.
-- A 64 MiB device copy is enqueued just before the start event, so the
-  host has queued the timed launches before the GPU reaches them; HIP
+- Every weight copy is read once before timing (its pages mapped and
+  translated), then a 64 MiB device copy is enqueued just before the start
+  event, so the host has queued the timed launches before the GPU reaches
+  them; HIP
   events on that stream bracket the timed steps, so the span holds GPU work
   only, also at the driver's 20 steps (a HIP graph of 20 launches measured
   0.5 us per step slower to start; --launch graph times one).
@@ -93,30 +95,41 @@ def algorithmic_bytes(rows: int, cols: int, batch: int) -> int:
 class Settle:
     """A 64 MiB device copy enqueued before a start event: the GPU is busy
     for tens of microseconds while the host submits what follows, so the
-    timed span starts with the first timed launch already queued."""
+    timed span starts with the first timed launch already queued. Before it,
+    touch() reads every weight copy once (nya_hip_read), so the pages of all
+    inputs are mapped and translated when timing starts, also where the
+    timed steps outnumber the warmup steps (a larger copy here measured
+    slower at 20 steps: it displaced those translations)."""
 
     BYTES = 64 << 20
 
     def __init__(self, rt, kern):
         self.rt, self.kern = rt, kern
         self.src, self.dst = rt.malloc(self.BYTES), rt.malloc(self.BYTES)
+        self.sink = rt.malloc(1 << 20)
+
+    def touch(self, buffers, stream):
+        for p, nbytes in buffers:
+            self.kern.read(p, nbytes, self.sink, stream)
 
     def __call__(self, stream):
         self.kern.copy(self.dst, self.src, self.BYTES, stream)
 
     def close(self):
-        self.rt.free(self.src)
-        self.rt.free(self.dst)
+        for p in (self.src, self.dst, self.sink):
+            self.rt.free(p)
 
 
-def time_launches(rt, stream, settle, launch, steps: int, warm: int, mode: str) -> float:
+def time_launches(rt, stream, settle, launch, steps: int, warm: int, mode: str, touch=()) -> float:
     """Milliseconds per launch over `steps` launches launch(0..steps-1),
     after `warm` untimed ones, between HIP events that bracket GPU work only
     (the settle copy runs before the start event while the host queues the
-    launches). mode "stream": direct launches; "graph": one HIP graph."""
+    launches; `touch`: (pointer, bytes) of the input buffers, read once
+    before it). mode "stream": direct launches; "graph": one HIP graph."""
     graph = Graph(rt, stream, [lambda i=i: launch(i) for i in range(steps)]) if mode == "graph" else None
     for i in range(warm):
         launch(i)
+    settle.touch(touch, stream)
     rt.sync(stream)
     start, end = rt.event(), rt.event()
     settle(stream)
@@ -141,7 +154,8 @@ def time_steps(rt, kern, stream, settle, weights, x_dev, y_dev, batch, steps, wa
     def launch(i):
         kern.matmul(weights[i % copies], Q4_K, ROWS, COLS, x_dev, y_dev, batch, work, work_bytes, stream)
 
-    return time_launches(rt, stream, settle, launch, steps, warmup, mode)
+    wbytes = storage_bytes(Q4_K, ROWS, COLS)
+    return time_launches(rt, stream, settle, launch, steps, warmup, mode, [(p, wbytes) for p in weights])
 
 
 def read_ceiling(rt, kern, stream, settle, weights, steps, warmup, mode, matvec_ms) -> dict:
@@ -154,7 +168,7 @@ def read_ceiling(rt, kern, stream, settle, weights, steps, warmup, mode, matvec_
     def launch(i):
         kern.read(weights[i % copies], wbytes, sink, stream)
 
-    ms = time_launches(rt, stream, settle, launch, steps, warmup, mode)
+    ms = time_launches(rt, stream, settle, launch, steps, warmup, mode, [(p, wbytes) for p in weights])
     rt.free(sink)
     return {"kernel": "read16 (nya_hip_read)", "bytes": wbytes, "us_per_step": round(ms * 1e3, 3),
             "GBps": round(wbytes / (ms * 1e-3) / 1e9, 2), "frac": round(wbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
@@ -324,7 +338,8 @@ def prefill(rt, kern, stream, settle, weights, steps: int) -> dict:
     def launch(i):
         kern.matmul(weights[i % copies], Q4_K, ROWS, COLS, x_dev, y_dev, m, work, need, stream)
 
-    ms = time_launches(rt, stream, settle, launch, steps, 2, "stream")
+    wbytes = storage_bytes(Q4_K, ROWS, COLS)
+    ms = time_launches(rt, stream, settle, launch, steps, 2, "stream", [(p, wbytes) for p in weights])
     for p in (x_dev, y_dev, work):
         rt.free(p)
     useful = 2.0 * ROWS * COLS * m / (ms * 1e-3) / 1e12          # 2 M N K per call
@@ -450,7 +465,7 @@ def time_case(rt, kern, stream, settle, t, rows, cols, batch, steps):
     def launch(i):
         kern.matmul(weights[i % copies], t, rows, cols, x_dev, y_dev, batch, work, need, stream)
 
-    ms = time_launches(rt, stream, settle, launch, steps, min(copies, 8), "stream")
+    ms = time_launches(rt, stream, settle, launch, steps, min(copies, 8), "stream", [(p, wbytes) for p in weights])
     for p in weights + [x_dev, y_dev, work]:
         rt.free(p)
     return ms

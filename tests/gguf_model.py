@@ -55,8 +55,10 @@ def _array(key: str, elem: int, values) -> bytes:
 tensors = llama_tensors
 
 
-def write(path: Path, shape: LlamaShape) -> int:
-    """Writes the model; returns its size in bytes."""
+def write(path: Path, shape: LlamaShape, shared_blocks: bool = False) -> int:
+    """Writes the model; returns its size in bytes. With `shared_blocks`
+    every block stores block 0's tensor bytes (a many-block file in the
+    generation time of one block)."""
     pieces = ["<unk>", "<s>", "</s>"] + [f"p{i:04d}" for i in range(shape.vocabulary - 3)]
     meta = [
         _kv("general.architecture", STRING, "llama"),
@@ -78,7 +80,7 @@ def write(path: Path, shape: LlamaShape) -> int:
         _kv("tokenizer.ggml.add_eos_token", BOOL, False),
         _kv("general.alignment", U32, ALIGNMENT),
     ]
-    ts = tensors(shape)
+    ts = tensors(shape, shared_blocks=shared_blocks)
     directory, offset = [], 0
     for name, t, dims, data in ts:
         directory.append(_string(name) + struct.pack("<I", len(dims)) +

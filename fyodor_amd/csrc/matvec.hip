@@ -261,6 +261,9 @@ __device__ __forceinline__ void group_dots(float (&part)[VT], const MvStage<T> (
                 sum = __builtin_fmaf(sc, t, sum);
             }
             part[v] = f16_to_f32(w[v].d & 0xFFFFu) * sum;
+            // Tiles in load order (not interleaved by the scheduler): each
+            // tile's work waits only for its own loads.
+            __builtin_amdgcn_sched_barrier(0);
         }
     } else {
         // One tile at a time: its four two-block chains, then its epilogue.
@@ -301,6 +304,7 @@ __device__ __forceinline__ void group_dots(float (&part)[VT], const MvStage<T> (
             } else {
                 part[v] = sum_s;
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 }
@@ -429,6 +433,13 @@ __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) vo
 // (GB, S: the format's group bytes and scale offset per row). FULL (R = 32
 // for every lane of the workgroup): the group and field parts are scalar
 // offsets.
+//
+// Issue order is fixed (the empty asm statements keep the compiler from
+// reordering the loads): the scale words first, then the quants in the order
+// the dots use them. A wavefront's loads return in order, so each block's
+// dots wait only for the loads before its own, and the work left after the
+// last load of a stage is one block's (left to the compiler, the scale word
+// went last and every scale multiply waited for the whole stage).
 template <unsigned T, bool FULL>
 __device__ __forceinline__ void load_rows(MvStage<T> &w, __amdgpu_buffer_rsrc_t wb, int vq, int vs, int R, int g,
     int vd = 0, int G = 0)
@@ -437,8 +448,16 @@ __device__ __forceinline__ void load_rows(MvStage<T> &w, __amdgpu_buffer_rsrc_t 
         // Per group 208 R bytes: units p at 48 R p (ql half h at + 16 R h,
         // qh at + 32 R), scales at 192 R; the d of all G groups after them
         // (2 bytes per row at vd = tile + 2 r, group g at 208 R G + 2 R g).
+        if constexpr (FULL) {
+            w.sc = bload16<true>(wb, vs, kTileRows * (208 * g + 192));
+            w.d = __builtin_amdgcn_raw_buffer_load_b16(wb, vd, kTileRows * (208 * G + 2 * g), 2);
+        } else {
+            w.sc = bload16<true>(wb, vs + R * (208 * g + 192), 0);
+            w.d = __builtin_amdgcn_raw_buffer_load_b16(wb, vd + R * (208 * G + 2 * g), 0, 2);
+        }
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
+            asm volatile("" ::: "memory");
             if constexpr (FULL) {
                 w.ql[p] = bload16<true>(wb, vq, kTileRows * (208 * g + 48 * p));
                 w.qh[p] = bload16<true>(wb, vs, kTileRows * (208 * g + 48 * p + 32));
@@ -447,28 +466,24 @@ __device__ __forceinline__ void load_rows(MvStage<T> &w, __amdgpu_buffer_rsrc_t 
                 w.qh[p] = bload16<true>(wb, vs + R * (208 * g + 48 * p + 32), 0);
             }
         }
-        if constexpr (FULL) {
-            w.sc = bload16<true>(wb, vs, kTileRows * (208 * g + 192));
-            w.d = __builtin_amdgcn_raw_buffer_load_b16(wb, vd, kTileRows * (208 * G + 2 * g), 2);
-        } else {
-            w.sc = bload16<true>(wb, vs + R * (208 * g + 192), 0);
-            w.d = __builtin_amdgcn_raw_buffer_load_b16(wb, vd + R * (208 * G + 2 * g), 0, 2);
-        }
     } else {
         constexpr int GB = kGroupRowBytes<T>, S = kScaleOffset<T>;
         u32x4 sw;
-        if constexpr (FULL) {
-#pragma unroll
-            for (int p = 0; p < kQuantLoads<T>; ++p) w.q[p] = bload16<true>(wb, vq, kTileRows * GB * g + 1024 * p);
-            sw = bload16<true>(wb, vs, kTileRows * (GB * g + S));
-        } else {
-#pragma unroll
-            for (int p = 0; p < kQuantLoads<T>; ++p) w.q[p] = bload16<true>(wb, vq + R * (GB * g + 32 * p), 0);
-            sw = bload16<true>(wb, vs + R * (GB * g + S), 0);
-        }
+        if constexpr (FULL) sw = bload16<true>(wb, vs, kTileRows * (GB * g + S));
+        else sw = bload16<true>(wb, vs + R * (GB * g + S), 0);
         if constexpr (T == Q4_K) w.sl = sw;
         else w.d = sw;
+#pragma unroll
+        for (int p = 0; p < kQuantLoads<T>; ++p) {
+            asm volatile("" ::: "memory");
+            if constexpr (FULL) w.q[p] = bload16<true>(wb, vq, kTileRows * GB * g + 1024 * p);
+            else w.q[p] = bload16<true>(wb, vq + R * (GB * g + 32 * p), 0);
+        }
     }
+    // Nothing after the loads is scheduled among them (an activation
+    // instruction placed there waited for the x loads and held back the rest
+    // of the stage).
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 // Row-balanced batch-1 matvec. One workgroup of sixteen wavefronts per CU
@@ -986,16 +1001,35 @@ __device__ __forceinline__ void group_dots_tokens(float (&y)[VT][(kTokAcc<T, NP>
                 }
         }
     } else if constexpr (T == Q4_K) {
-        int acc[VT][J][3];
+        // The minimum term sum_b m_b (sum x)_b first: it needs only the scale
+        // words (each tile's first load) and the block sums in LDS, so it runs
+        // while the quants stream in.
+        float mterm[VT][J];
 #pragma unroll
-        for (int v = 0; v < VT; ++v)
-#pragma unroll
-            for (int j = 0; j < J; ++j) acc[v][j][0] = acc[v][j][1] = acc[v][j][2] = 0;
-#pragma unroll
-        for (int b = 0; b < 8; ++b) {
-            const i32x4 a = *(const i32x4 *)(slot + aoff + astride * b);
+        for (int j = 0; j < J; ++j) {
+            const float4 xa = *(const float4 *)(slot + S::kSx + 32 * (2 * j + h));
+            const float4 xb = *(const float4 *)(slot + S::kSx + 32 * (2 * j + h) + 16);
+            const float sx[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
 #pragma unroll
             for (int v = 0; v < VT; ++v) {
+                float m = 0.f;
+#pragma unroll
+                for (int b = 0; b < 8; ++b)
+                    m = __builtin_fmaf((float)__builtin_amdgcn_ubfe(w[v].sl[b >> 1], 12 * (b & 1) + 6, 6), sx[b], m);
+                mterm[v][j] = m;
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // Then tile by tile, in load order: each block's dots wait only for
+        // its own quant word.
+#pragma unroll
+        for (int v = 0; v < VT; ++v) {
+            int acc[J][3];
+#pragma unroll
+            for (int j = 0; j < J; ++j) acc[j][0] = acc[j][1] = acc[j][2] = 0;
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+                const i32x4 a = *(const i32x4 *)(slot + aoff + astride * b);
                 const i32x16 D = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, block_b_tokens<T>(w[v], b), (i32x16){}, 0, 0, 0);
                 const int sc = (int)__builtin_amdgcn_ubfe(w[v].sl[b >> 1], 12 * (b & 1), 6);
                 // |D| < 2^16: the 24-bit multiply-add takes it whole. The
@@ -1006,55 +1040,42 @@ __device__ __forceinline__ void group_dots_tokens(float (&y)[VT][(kTokAcc<T, NP>
                 for (int j = 0; j < J; ++j)
 #pragma unroll
                     for (int d = 0; d < 3; ++d) {
-                        acc[v][j][d] += ((D[4 * j + d] << 8) >> 8) * sc;
-                        asm("" : "+v"(acc[v][j][d]));
+                        acc[j][d] += ((D[4 * j + d] << 8) >> 8) * sc;
+                        asm("" : "+v"(acc[j][d]));
                     }
             }
-        }
+            const u32x4 sl = w[v].sl;   // byte 3 of the four words: d, dmin
+            const uint32_t dd = (sl.x >> 24) | ((sl.y >> 24) << 8) | ((sl.z >> 24) << 16) | ((sl.w >> 24) << 24);
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const float4 xa = *(const float4 *)(slot + S::kSx + 32 * (2 * j + h));
-            const float4 xb = *(const float4 *)(slot + S::kSx + 32 * (2 * j + h) + 16);
-            const float sx[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-#pragma unroll
-            for (int v = 0; v < VT; ++v) {
-                const u32x4 sl = w[v].sl;   // byte 3 of the four words: d, dmin
-                const uint32_t dd = (sl.x >> 24) | ((sl.y >> 24) << 8) | ((sl.z >> 24) << 16) | ((sl.w >> 24) << 24);
-                float mterm = 0.f;
-#pragma unroll
-                for (int b = 0; b < 8; ++b)
-                    mterm = __builtin_fmaf((float)__builtin_amdgcn_ubfe(sl[b >> 1], 12 * (b & 1) + 6, 6), sx[b], mterm);
-                const float G = __builtin_fmaf((float)acc[v][j][2], 65536.f,
-                                               __builtin_fmaf((float)acc[v][j][1], 256.f, (float)acc[v][j][0]));
-                y[v][j] = __builtin_fmaf(-f16_to_f32(dd >> 16), mterm,
+            for (int j = 0; j < J; ++j) {
+                const float G = __builtin_fmaf((float)acc[j][2], 65536.f,
+                                               __builtin_fmaf((float)acc[j][1], 256.f, (float)acc[j][0]));
+                y[v][j] = __builtin_fmaf(-f16_to_f32(dd >> 16), mterm[v][j],
                                          __builtin_fmaf(s4[j] * f16_to_f32(dd & 0xFFFFu), G, y[v][j]));
             }
         }
     } else {
-        float acc[VT][J];
+        // Tile by tile, in load order (the scale word first).
+        constexpr float kWeightFactor = T == Q4_0 ? 0.0625f : 1.f;
 #pragma unroll
-        for (int v = 0; v < VT; ++v)
+        for (int v = 0; v < VT; ++v) {
+            float acc[J];
 #pragma unroll
-            for (int j = 0; j < J; ++j) acc[v][j] = 0.f;
+            for (int j = 0; j < J; ++j) acc[j] = 0.f;
 #pragma unroll
-        for (int b = 0; b < 8; ++b) {
-            const i32x4 a = *(const i32x4 *)(slot + aoff + astride * b);
-#pragma unroll
-            for (int v = 0; v < VT; ++v) {
+            for (int b = 0; b < 8; ++b) {
+                const i32x4 a = *(const i32x4 *)(slot + aoff + astride * b);
                 const i32x16 D = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, block_b_tokens<T>(w[v], b), (i32x16){}, 0, 0, 0);
                 const float db = f16_to_f32((w[v].d[b >> 1] >> (16 * (b & 1))) & 0xFFFFu);
                 // Sums reach 2^34: the top digit joins in float.
 #pragma unroll
                 for (int j = 0; j < J; ++j)
-                    acc[v][j] = __builtin_fmaf(__builtin_fmaf((float)D[4 * j + 2], 65536.f,
-                                                              (float)(D[4 * j + 1] * 256 + D[4 * j])), db, acc[v][j]);
+                    acc[j] = __builtin_fmaf(__builtin_fmaf((float)D[4 * j + 2], 65536.f,
+                                                           (float)(D[4 * j + 1] * 256 + D[4 * j])), db, acc[j]);
             }
+#pragma unroll
+            for (int j = 0; j < J; ++j) y[v][j] = __builtin_fmaf(s4[j] * kWeightFactor, acc[j], y[v][j]);
         }
-        constexpr float kWeightFactor = T == Q4_0 ? 0.0625f : 1.f;
-#pragma unroll
-        for (int v = 0; v < VT; ++v)
-#pragma unroll
-            for (int j = 0; j < J; ++j) y[v][j] = __builtin_fmaf(s4[j] * kWeightFactor, acc[v][j], y[v][j]);
     }
 }
 
@@ -1171,14 +1192,29 @@ __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, 
     if (i >= VT * 256) return;
     const int v = i >> 8, t = (i >> 5) & 7, r = i & 31;
     if (t >= n || kTileRows * v + r >= live) return;
-    const int nw = groups < KS ? groups : KS;
+    // Every wavefront wrote its share (zero for a wavefront without groups).
+    // All KS partials are read before the first add: one LDS round trip, not
+    // one per partial.
     float s = 0.f;
     if constexpr (T == Q6_K) {
         // Every lane holds every token: its lane half's columns.
-        for (int q = 0; q < nw; ++q) s += red[((q * VT + v) * J + t) * 64 + r] + red[((q * VT + v) * J + t) * 64 + r + 32];
+        float p[2 * KS];
+#pragma unroll
+        for (int q = 0; q < KS; ++q) {
+            p[2 * q] = red[((q * VT + v) * J + t) * 64 + r];
+            p[2 * q + 1] = red[((q * VT + v) * J + t) * 64 + r + 32];
+        }
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int q = 0; q < KS; ++q) s += p[2 * q] + p[2 * q + 1];
     } else {
         const int ln = r + 32 * (t & 1);
-        for (int q = 0; q < nw; ++q) s += red[((q * VT + v) * J + (t >> 1)) * 64 + ln];
+        float p[KS];
+#pragma unroll
+        for (int q = 0; q < KS; ++q) p[q] = red[((q * VT + v) * J + (t >> 1)) * 64 + ln];
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int q = 0; q < KS; ++q) s += p[q];
     }
     y[(size_t)t * rows + base + kTileRows * v + r] = s;
 }

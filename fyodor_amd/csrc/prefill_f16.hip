@@ -8,10 +8,10 @@
 // and lo = fp16(x s - hi): |e| <= 2^-22 |x s|, or 2^-25 absolute where lo is
 // subnormal. The MFMA multiplies fp16 pairs exactly and accumulates in fp32,
 // so a block dot is sum (sc q)(hi + lo) with fp32 accumulation error only.
-// What remains for the VALU is the superblock scale d per 256 columns (Q4_K;
-// the 6-bit minimums go through an fp32 MFMA against the per-block sums of
-// x s) or the fp16 block scale per 32 columns (Q8_0, Q4_0), and 1/s once per
-// output. A token holding a non-finite value gets NaN pieces: its outputs are
+// What remains for the VALU is the superblock scales d and dmin per 256
+// columns (Q4_K; the 6-bit minimums meet the per-block sums of x s on one
+// more fp16 MFMA, the sums split into two pieces like x) or the fp16 block
+// scale per 32 columns (Q8_0, Q4_0), and 1/s once per output. A token holding a non-finite value gets NaN pieces: its outputs are
 // NaN.
 //
 // Column order. A lane of the weight tile holds 16 consecutive columns of a
@@ -55,13 +55,14 @@ template <int TW> constexpr int kBufBytes = TW * kTileBytes;
 
 // ---- activation pieces ---------------------------------------------------
 // Workspace for np tokens (np a multiple of 32): hi[np][cols], lo[np][cols]
-// (fp16, permuted as above), bsum[np][cols / 256][2][4] (fp32 sum of x s over
-// 32-column block 2s + h of each 256-column group at [h][s], the operand
-// order of the minimum-term MFMA; written when cols % 256 == 0) and inv[np]
-// (1 / s, or NaN).
+// (fp16, permuted as above), bsum[np][cols / 256][2][8] (the sum of x s over
+// 32-column block j of each 256-column group, times 2^-5, as two fp16
+// pieces: [0][j] hi, [1][j] lo; |sum| < 2^19, so the scaled sum is below the
+// fp16 range limit; written when cols % 256 == 0) and inv[np] (1 / s, or
+// NaN).
 struct Pieces {
-    _Float16 *hi, *lo;
-    float *bsum, *inv;
+    _Float16 *hi, *lo, *bsum;
+    float *inv;
 };
 
 __host__ __device__ inline Pieces pieces_of(void *ws, int cols, int np)
@@ -69,8 +70,8 @@ __host__ __device__ inline Pieces pieces_of(void *ws, int cols, int np)
     Pieces p;
     p.hi = (_Float16 *)ws;
     p.lo = p.hi + (size_t)np * cols;
-    p.bsum = (float *)(p.lo + (size_t)np * cols);
-    p.inv = p.bsum + (size_t)np * (cols / 32);
+    p.bsum = p.lo + (size_t)np * cols;
+    p.inv = (float *)(p.bsum + (size_t)np * (cols / 16));
     return p;
 }
 
@@ -129,7 +130,11 @@ __global__ __launch_bounds__(256) void split_x(const float *__restrict__ x, int 
         s += __shfl_xor(s, 2, 64);
         if ((c & 3) == 0 && cols % 256 == 0) {
             const int b = c / 4, j = b & 7;
-            out.bsum[(size_t)t * (cols / 32) + (b & ~7) + 4 * (j & 1) + (j >> 1)] = s;
+            const float sv = s * 0.03125f;
+            const _Float16 shi = (_Float16)sv;
+            _Float16 *dst = out.bsum + (size_t)t * (cols / 16) + 2 * (b & ~7) + j;
+            dst[0] = shi;
+            dst[8] = (_Float16)(sv - (float)shi);
         }
     }
 }
@@ -183,7 +188,7 @@ __device__ __forceinline__ void copy_group(lds_u8 *__restrict__ buf, const Piece
         // same place again): a copy under a wavefront condition leaves a
         // branch after which the compiler waits for every load.
         const int tt = wave % TW;
-        const float *src = p.bsum + ((size_t)(m0 + 32 * tt + (lane & 31)) * (cols / 256) + g) * 8 + 4 * (lane >> 5);
+        const _Float16 *src = p.bsum + ((size_t)(m0 + 32 * tt + (lane & 31)) * (cols / 256) + g) * 16 + 8 * (lane >> 5);
         lds_copy16(src, buf + kTileBytes * tt + 2 * kPieceBytes);
     }
 }
@@ -370,21 +375,21 @@ __device__ __forceinline__ void group_step(WStage<T> &cur, f32x16 (&acc)[TW], ld
         }
         float d, dmin;
         group_scales<T>(cur, d, dmin);
-        // Minimums: acc -= dmin * sum_j m_j * (sum of x s over block j), on
-        // an fp32 MFMA accumulating into acc (lane l: A = the sum over
-        // block 2s + l/32 of token l % 32, B = -dmin * m of that block for
-        // row l % 32).
-        float bm[4];
+        // Minimums: M = sum_j m_j * 2^-5 (sum of x s over block j) on one
+        // fp16 MFMA per token tile, exact products: lane l supplies A = piece
+        // l/32 (hi, lo) of the eight scaled block sums of token l % 32, and
+        // B = m_j for row l % 32, j = 0..7 in both K halves. Then
+        // acc += d C - 32 dmin M.
+        h8 bm;
 #pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2) bm[s2] = -dmin * (float)((cur.sl[s2] >> (12 * L.h + 6)) & 63u);
+        for (int j = 0; j < 8; ++j) bm[j] = (_Float16)(int)((cur.sl[j >> 1] >> (12 * (j & 1) + 6)) & 63u);
+        const float ndmin = -32.f * dmin;
 #pragma unroll
         for (int tt = 0; tt < TW; ++tt) {
+            const h8 ys = *(const h8 *)(buf + kTileBytes * tt + 2 * kPieceBytes + 16 * lane);
+            const f32x16 M = __builtin_amdgcn_mfma_f32_32x32x16_f16(ys, bm, (f32x16){}, 0, 0, 0);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[tt][r] += d * C[tt][r];
-            const float4 ys = *(const float4 *)(buf + kTileBytes * tt + 2 * kPieceBytes + 16 * lane);
-            const float ya[4] = {ys.x, ys.y, ys.z, ys.w};
-#pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) acc[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(ya[s2], bm[s2], acc[tt], 0, 0, 0);
+            for (int r = 0; r < 16; ++r) acc[tt][r] = __builtin_fmaf(d, C[tt][r], __builtin_fmaf(ndmin, M[r], acc[tt][r]));
         }
     } else {
         // Per-block scales; a short last group has its own layout (formats.h).

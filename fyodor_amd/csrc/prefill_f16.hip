@@ -153,11 +153,20 @@ __device__ __forceinline__ void barrier()
     asm volatile("" : : : "memory");
 }
 
-// 16 bytes per lane from global memory straight into LDS: lane l's bytes land
-// at dst + 16 l (dst uniform over the wavefront).
-__device__ __forceinline__ void lds_copy16(const void *src, lds_u8 *dst)
+// 16 bytes per lane from a buffer straight into LDS: lane l's bytes (at
+// voff + soff in the buffer) land at dst + 16 l (dst uniform over the
+// wavefront). Buffer loads take a per-lane 32-bit offset fixed for the kernel
+// and a scalar one: no vector address arithmetic per copy (global_load_lds
+// needed four to five VALU instructions of 64-bit address math each).
+__device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t r, int voff, int soff, lds_u8 *dst)
 {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)dst, 16, voff, soff, 0, 0);
+}
+
+// Buffer resource over `bytes` bytes at p (out-of-range reads return zero).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void *p, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
 }
 
 // Copies of group g into LDS buffer `buf` issued by this wavefront (one of
@@ -165,31 +174,35 @@ __device__ __forceinline__ void lds_copy16(const void *src, lds_u8 *dst)
 // token pairs 16 TW / RT per wavefront of both pieces (lane l: token
 // 2q + (l & 1), 16-byte chunk l >> 1 of the group's row, to byte 16 l of the
 // pair), and for Q4_K tile (wavefront % TW)'s block sums (lane l: token
-// l % 32, half l / 32). Columns past a short last Q8_0/Q4_0 group are
-// clamped (those blocks are skipped).
+// l % 32, half l / 32). Each copy reads through a resource over its own two
+// token rows (rebased in scalar registers, so every offset stays far below
+// 2^31 at the widest rows the library accepts); past a short last Q8_0/Q4_0
+// group a lane reads the next row's columns or zeros, into LDS slots of
+// blocks that are skipped.
 template <int RT, int TW>
 __device__ __forceinline__ void copy_group(lds_u8 *__restrict__ buf, const Pieces &p, int cols, int m0, int g, bool sums)
 {
     constexpr int kPairs = 16 * TW / RT;   // token pairs per wavefront, over all token tiles
     static_assert(kPairs >= 1 && 16 * TW % RT == 0, "whole token pairs per wavefront");
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    int col = 256 * g + 8 * (lane >> 1);
-    col = col < cols ? col : cols - 8;
+    const int vpair = 2 * ((lane & 1) * cols + 8 * (lane >> 1));   // bytes within the pair's two rows
 #pragma unroll
     for (int piece = 0; piece < 2; ++piece)
 #pragma unroll
         for (int k = 0; k < kPairs; ++k) {
             const int q = kPairs * wave + k, tt = q / 16, qq = q % 16;   // pair qq of token tile tt
-            const _Float16 *src = (piece ? p.lo : p.hi) + (size_t)(m0 + 32 * tt + 2 * qq + (lane & 1)) * cols + col;
-            lds_copy16(src, buf + kTileBytes * tt + piece * kPieceBytes + qq * kPairPitch);
+            const _Float16 *rows2 = (piece ? p.lo : p.hi) + (size_t)(m0 + 32 * tt + 2 * qq) * cols;
+            lds_copy16(rsrc_of(rows2, 4u * (uint32_t)cols), vpair, 512 * g,
+                       buf + kTileBytes * tt + piece * kPieceBytes + qq * kPairPitch);
         }
     if (sums) {
         // Every wavefront copies (wavefronts past TW the same bytes to the
         // same place again): a copy under a wavefront condition leaves a
         // branch after which the compiler waits for every load.
-        const int tt = wave % TW;
-        const _Float16 *src = p.bsum + ((size_t)(m0 + 32 * tt + (lane & 31)) * (cols / 256) + g) * 16 + 8 * (lane >> 5);
-        lds_copy16(src, buf + kTileBytes * tt + 2 * kPieceBytes);
+        const int tt = wave % TW, gs = cols / 256;
+        const _Float16 *first = p.bsum + ((size_t)(m0 + 32 * tt) * gs + g) * 16;   // token 0 of the tile
+        lds_copy16(rsrc_of(first, 1024u * (uint32_t)gs), 2 * (16 * gs * (lane & 31) + 8 * (lane >> 5)), 0,
+                   buf + kTileBytes * tt + 2 * kPieceBytes);
     }
 }
 

@@ -309,6 +309,14 @@ NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t key
                                    (int)kv_heads, (int)width, (int)max_length, scale, (hipStream_t)stream));
 }
 
+NYA_HIP_EXPORT int nya_hip_greedy(uintptr_t logits, size_t n, size_t count, uintptr_t mask, uintptr_t ids,
+    uintptr_t stream)
+{
+    if (!vec(logits) || !vec(ids) || (mask & 3u) || !count_ok(n) || !tokens_ok(count)) return 1;
+    return status(launch_greedy((const float *)logits, (int)n, (int)count, (const uint32_t *)mask, (uint32_t *)ids,
+                                (hipStream_t)stream));
+}
+
 NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, size_t gate_stride, uintptr_t up, size_t up_stride,
     uintptr_t out, size_t n, size_t count, uintptr_t stream)
 {

@@ -81,6 +81,11 @@ hipError_t launch_attention(const float *q, int q_stride, const float *keys, con
     hipStream_t stream);
 hipError_t launch_silu_mul(const float *gate, int gate_stride, const float *up, int up_stride, float *out, int n,
     int count, hipStream_t stream);
+// The greedy choice of each of `count` rows of n logits (first largest among
+// the entries not masked; 0xFFFFFFFF for a row with a NaN or +inf, or
+// without a finite candidate).
+hipError_t launch_greedy(const float *logits, int n, int count, const uint32_t *mask, uint32_t *ids,
+    hipStream_t stream);
 
 // Compute units of the current device (counted once per device).
 int device_cu_count();

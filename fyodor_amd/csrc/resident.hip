@@ -432,6 +432,59 @@ __global__ void set_step(uint32_t *step, uint32_t token, int position)
 
 unsigned grid_of(long n) { return (unsigned)(n < 256 * 1024 ? (n + 255) / 256 : 1024); }
 
+// The greedy choice of each of `count` rows of n logits, as the engine's
+// sampler makes it at temperature 0 (backend/core/llm_cpu.c:896-904) after
+// the suppressed tokens are masked (backend/core/llm_cpu.c:570-574): the
+// first index of the largest value among the entries whose bit in `mask` is
+// clear (one bit per index, word i / 32, bit i % 32; null: none masked).
+// 0xFFFFFFFF when the row holds a non-finite value anywhere (the engine
+// rejects non-finite model output before it masks), or when every entry is
+// masked. One workgroup per row: each thread scans
+// its indices in increasing order (a later equal value never replaces an
+// earlier one), then the pairs (value, index) meet with the larger value, or
+// on equal values the smaller index, winning.
+__global__ __launch_bounds__(1024) void greedy(const float *__restrict__ logits, int n,
+    const uint32_t *__restrict__ mask, uint32_t *__restrict__ ids)
+{
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const float *row = logits + (size_t)blockIdx.x * n;
+    float best = -INFINITY;
+    int at = 0x7FFFFFFF;
+    int bad = 0;
+    for (int i = threadIdx.x; i < n; i += 1024) {
+        const float v = row[i];
+        bad |= !(__builtin_fabsf(v) <= 3.40282347e38f);
+        const bool masked = mask && ((mask[i >> 5] >> (i & 31)) & 1u);
+        if (!masked && v > best) {
+            best = v;
+            at = i;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(at, o, 64);
+        if (ov > best || (ov == best && oi < at)) {
+            best = ov;
+            at = oi;
+        }
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        sv[wave] = best;
+        si[wave] = at;
+    }
+    bad = __syncthreads_or(bad);
+    if (threadIdx.x != 0) return;
+    for (int q = 1; q < 16; ++q)
+        if (sv[q] > best || (sv[q] == best && si[q] < at)) {
+            best = sv[q];
+            at = si[q];
+        }
+    ids[blockIdx.x] = bad || !(best > -INFINITY) ? 0xFFFFFFFFu : (uint32_t)at;
+}
+
 }  // namespace
 
 hipError_t launch_set_step(uint32_t *step, uint32_t token, int position, hipStream_t s)
@@ -516,6 +569,12 @@ hipError_t launch_attention(const float *q, int q_stride, const float *keys, con
     else
         hipLaunchKernelGGL(attention<false>, grid, dim3(256), 0, s, q, q_stride, keys, values, out, scores, positions,
                            heads, kv_heads, width, max_length, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_greedy(const float *logits, int n, int count, const uint32_t *mask, uint32_t *ids, hipStream_t s)
+{
+    hipLaunchKernelGGL(greedy, dim3((unsigned)count), dim3(1024), 0, s, logits, n, mask, ids);
     return hipGetLastError();
 }
 

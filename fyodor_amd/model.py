@@ -246,7 +246,57 @@ class Plan:
         self.lib.nya_compute_plan_stats(self.ptr, ctypes.byref(s))
         return s.as_dict()
 
+    @property
+    def verify_limit(self) -> int:
+        self.lib.nya_compute_plan_verify_limit.restype = ctypes.c_size_t
+        self.lib.nya_compute_plan_verify_limit.argtypes = [ctypes.c_void_p]
+        return int(self.lib.nya_compute_plan_verify_limit(self.ptr))
+
+    def verify(self, tokens, position: int, logits: bool = False):
+        """Tokens [position, position + len(tokens)) in one batch
+        (nya_compute_plan_verify): the target's greedy choice after each, and
+        with `logits` the rows of logits too ([len(tokens)][vocabulary])."""
+        n = len(tokens)
+        arr = (ctypes.c_uint * n)(*tokens)
+        ids = (ctypes.c_uint * n)()
+        rows = np.empty((n, self.model.shape.vocabulary), np.float32) if logits else None
+        fp = ctypes.POINTER(ctypes.c_float)
+        self.lib.nya_compute_plan_verify.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint), ctypes.c_size_t,
+                                                     ctypes.c_size_t, ctypes.POINTER(ctypes.c_uint), fp]
+        if self.lib.nya_compute_plan_verify(self.ptr, arr, n, position, ids,
+                                            rows.ctypes.data_as(fp) if logits else None):
+            raise RuntimeError(f"resident verification failed at position {position} ({n} tokens)")
+        return (list(ids), rows) if logits else list(ids)
+
     def close(self):
         if self.ptr:
             self.lib.nya_compute_plan_free(self.ptr)
             self.ptr = None
+
+
+class Speculation(ctypes.Structure):
+    """nya_compute_speculation (include/compute.h)."""
+    _fields_ = [(name, ctypes.c_size_t) for name in
+                ("generated", "rounds", "draft_tokens", "accepted", "target_tokens", "draft_steps")]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+def generate_greedy(target: Plan, draft: Plan | None, prompt, limit: int, window: int = 4, stops=()):
+    """Greedy generation on `target` with batched speculative verification
+    against `draft` (nya_compute_generate_greedy): (tokens, counters). Both
+    plans must be empty and hold len(prompt) + limit positions."""
+    lib = target.lib
+    u = ctypes.POINTER(ctypes.c_uint)
+    lib.nya_compute_generate_greedy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, u, ctypes.c_size_t, ctypes.c_size_t,
+                                                ctypes.c_size_t, u, ctypes.c_size_t, u,
+                                                ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(Speculation)]
+    p = (ctypes.c_uint * len(prompt))(*prompt)
+    st = (ctypes.c_uint * max(len(stops), 1))(*stops)
+    out = (ctypes.c_uint * limit)()
+    count, stats = ctypes.c_size_t(), Speculation()
+    if lib.nya_compute_generate_greedy(target.ptr, draft.ptr if draft else None, p, len(prompt), window, limit, st,
+                                       len(stops), out, ctypes.byref(count), ctypes.byref(stats)):
+        raise RuntimeError("greedy generation failed")
+    return list(out[:count.value]), stats.as_dict()

@@ -49,6 +49,7 @@ typedef struct nya_resident_ops {
     int (*attention)(uintptr_t, size_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, size_t, size_t, size_t,
         size_t, size_t, float, uintptr_t);
     int (*silu_mul)(uintptr_t, size_t, uintptr_t, size_t, uintptr_t, size_t, size_t, uintptr_t);
+    int (*greedy)(uintptr_t, size_t, size_t, uintptr_t, uintptr_t, uintptr_t);
 } nya_resident_ops;
 
 #define NYA_KERNEL_ABI 1U

@@ -98,4 +98,47 @@ void nya_compute_plan_stats(const nya_compute_plan *plan, nya_compute_stats *sta
 int nya_compute_plan_read_kv(nya_compute_plan *plan, size_t layer, size_t position,
     size_t count, float *keys, float *values, size_t elements);
 
+/* No counterpart in the reference: greedy speculative decoding with batched
+ * verification. The engine's speculative path proposes with a draft model
+ * and checks each proposal with one target step
+ * (backend/core/llm_cpu.c:1146-1320); its comment at :1150-1152 leaves the
+ * throughput of batched verification open.
+ *
+ * nya_compute_plan_verify runs tokens [position, position + count) through
+ * the plan in one batch and returns the greedy choice after each (ids[i] is
+ * the target's token for position + i + 1, the first largest logit outside
+ * the suppressed tokens, as the engine's sampler at temperature 0), and the
+ * count rows of logits when `logits` is not NULL. Earlier positions may be
+ * run again (a rejected proposal's cache entry is overwritten). Returns 0,
+ * or -1 (count above nya_compute_plan_verify_limit, or the plan retired). */
+int nya_compute_plan_verify(nya_compute_plan *plan, const unsigned int *tokens, size_t count,
+    size_t position, unsigned int *ids, float *logits);
+size_t nya_compute_plan_verify_limit(const nya_compute_plan *plan);
+
+/* Counters of one nya_compute_generate_greedy call. */
+typedef struct nya_compute_speculation {
+    size_t generated;        /* tokens emitted */
+    size_t rounds;           /* target verifications after the prompt */
+    size_t draft_tokens;     /* proposals made */
+    size_t accepted;         /* proposals equal to the target's choice */
+    size_t target_tokens;    /* tokens run through the target, prompt included */
+    size_t draft_steps;      /* draft runs, prompt included */
+} nya_compute_speculation;
+
+/* Greedy generation of up to `limit` tokens after `prompt` (prompt_count >= 1)
+ * on `target`, stopping after a token of `stops` is emitted; the emitted
+ * tokens (written to out, their number to *out_count) are the target's own
+ * greedy decode. With a `draft` plan of the same vocabulary and window >= 1
+ * (at most 32), each round the draft proposes up to `window` tokens and one
+ * nya_compute_plan_verify of the target checks them all (the engine's
+ * temperature-0 rule, backend/core/llm_cpu.c:1274-1317: the target's choice
+ * is emitted, a proposal equal to it lets the round continue, and after all
+ * proposals the target's next choice is emitted too). Both plans need
+ * capacity for prompt_count + limit positions and start empty. Returns 0 or
+ * -1; `stats` may be NULL. */
+int nya_compute_generate_greedy(nya_compute_plan *target, nya_compute_plan *draft,
+    const unsigned int *prompt, size_t prompt_count, size_t window, size_t limit,
+    const unsigned int *stops, size_t stop_count, unsigned int *out, size_t *out_count,
+    nya_compute_speculation *stats);
+
 #endif

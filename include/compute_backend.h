@@ -29,7 +29,21 @@ typedef struct nya_backend_interface {
 } nya_backend_interface;
 
 /* The ROCm provider's table (replaces rocm/rocm.c:193-199). Capabilities are
- * MATVEC | QUANTIZED | MATMUL; plan and attention entries are NULL. */
+ * MATVEC | QUANTIZED | MATMUL | RESIDENT; the attention entry is NULL. */
 const nya_backend_interface *nya_rocm_backend(void);
+
+/* Entries of the ROCm provider that the engine's table has no slot for; they
+ * take the handle its plan_create returned. Batched verification of draft
+ * tokens: the forward of tokens [position, position + count) in one run and
+ * the target's greedy choice after each (ids[i] for position + i + 1), the
+ * count rows of logits too when `logits` is not NULL; 0 or -1 (the plan
+ * retires, as after a failed plan_token). The most tokens one verification
+ * takes; the plan's vocabulary size. No counterpart in the reference, whose
+ * speculative decoding verifies with serial target steps
+ * (backend/core/llm_cpu.c:1274-1305). */
+int nya_rocm_plan_verify(void *plan, const uint32_t *tokens, size_t count, size_t position, uint32_t *ids,
+    float *logits);
+size_t nya_rocm_plan_verify_limit(const void *plan);
+size_t nya_rocm_plan_vocabulary(const void *plan);
 
 #endif

@@ -192,6 +192,19 @@ NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t key
 NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, size_t gate_stride, uintptr_t up, size_t up_stride,
     uintptr_t out, size_t n, size_t count, uintptr_t stream);
 
+/* ids[i] = the greedy choice of row i of `count` rows of n fp32 logits
+ * (logits + i n), as backend/core/llm_cpu.c:896-904 (nya_llm_sample at
+ * temperature 0) picks it after the suppressed tokens are masked
+ * (backend/core/llm_cpu.c:570-574): the first index of the largest value
+ * among the entries whose bit in `mask` is clear (uint32 words, bit j % 32
+ * of word j / 32; 0: none masked); 0xFFFFFFFF for a row holding a
+ * non-finite value anywhere (the engine rejects non-finite model output
+ * before masking) or with every entry masked. The resident plan's batched
+ * verification of draft tokens downloads these ids instead of `count` rows
+ * of logits. */
+NYA_HIP_EXPORT int nya_hip_greedy(uintptr_t logits, size_t n, size_t count, uintptr_t mask, uintptr_t ids,
+    uintptr_t stream);
+
 #ifdef __cplusplus
 }
 #endif

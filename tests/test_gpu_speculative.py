@@ -1,0 +1,64 @@
+"""Batched verification and greedy speculative decoding on an MI355X
+(the checks of tests/speculative_check.py, which also run on the mock HIP
+runtime in tests/test_speculative.py), through this repository's compute API
+on the gfx950 kernels:
+
+- nya_compute_plan_verify over chunks of 5 (the vocabulary product on the
+  small-N kernels), 20 and 33 tokens (the prefill GEMM) gives the logits of
+  one plan_token per token within the engine's logit bound
+  (backend/tests/test_inference.c:214-219) and its greedy choices; earlier
+  positions run again follow the new tokens;
+- nya_compute_generate_greedy emits the target's serial greedy decode with
+  drafts that disagree, agree, or agree at some positions only (proposals
+  both accepted and rejected), and without a draft;
+- the device greedy choice skips suppressed tokens."""
+import pytest
+
+from fyodor_amd import Q4_K, Q6_K, Q8_0
+from fyodor_amd import model as fm
+from speculative_check import (generation_equals_target_decode, suppressed_tokens_are_skipped,
+                               verify_matches_steps)
+
+pytestmark = pytest.mark.gpu
+
+PROMPT = [5, 17, 200, 3, 42]
+
+
+@pytest.fixture(autouse=True)
+def rocm_env(monkeypatch):
+    from fyodor_amd import KERNEL_LIBRARY
+    monkeypatch.setenv("NYA_ROCM_KERNEL_LIBRARY", str(KERNEL_LIBRARY))
+    for v in ("NYA_ROCM_HIP_LIBRARY", "NYA_ROCM_CACHE_MIB"):
+        monkeypatch.delenv(v, raising=False)
+
+
+@pytest.mark.parametrize("chunk", [5, 20, 33])
+def test_verify_matches_serial_steps(chunk):
+    shape = fm.LlamaShape(embedding=512, heads=8, kv_heads=2, hidden=1024, blocks=3, context=96, vocabulary=1000,
+                          seed=3)
+    tokens = [(i * 37 + 11) % shape.vocabulary for i in range(2 * chunk + 3)]
+    worst = verify_matches_steps(shape, tokens, chunk)
+    print(f"chunk {chunk}: worst scaled logit error {worst:.3g}", flush=True)
+
+
+@pytest.mark.parametrize("draft", ["other", "same", "swapped", "none"])
+def test_generation_equals_target_decode(draft):
+    types = {"embedding": Q4_K, "output": Q6_K, "attention": Q4_K, "gate_up": Q4_K, "down": Q6_K}
+    target = fm.LlamaShape(embedding=512, heads=8, kv_heads=2, hidden=1024, blocks=3, context=96, vocabulary=1000,
+                           types=types, seed=5 if draft == "swapped" else 3)
+    other = fm.LlamaShape(embedding=256, heads=4, kv_heads=2, hidden=512, blocks=1, context=96, vocabulary=1000,
+                          types={**types, "output": Q8_0}, seed=11)
+    if draft == "swapped":
+        # This shape's decode alternates two tokens (seed 5): a draft with
+        # one of them swapped is right at every other position.
+        target = fm.LlamaShape(context=96, types=types, seed=5)
+    runs = generation_equals_target_decode(target, other if draft == "other" else None, PROMPT, limit=24,
+                                           windows=(1, 4, 8), same_draft=draft == "same", swap=draft == "swapped")
+    print(draft, runs, flush=True)
+    if draft == "swapped":
+        assert any(0 < stats["accepted"] < stats["draft_tokens"] for _, stats in runs), runs
+
+
+def test_suppressed_tokens_are_skipped():
+    suppressed_tokens_are_skipped(fm.LlamaShape(embedding=512, heads=8, kv_heads=2, hidden=1024, blocks=2, context=32,
+                                                vocabulary=1000, seed=3), PROMPT)

@@ -28,7 +28,8 @@ weight matrix; weights and activations are resident in HBM before timing.
   on synthetic dense LLaMAs of two shapes: an 8B-class model (tg: decode
   tokens/s with logits every token, and its weight bytes per token over the
   token time) and TinyLlama 1.1B (tg128 and pp512, the reference's published
-  end-to-end metrics).
+  end-to-end metrics); on the 8B-class model also batched verification of
+  k draft tokens (one nya_compute_plan_verify) against k decode steps.
 - prefill: the same matrix times 512 tokens through the fp16-MFMA prefill
   GEMM (one call = activation split + GEMM): useful TFLOP/s (2 M N K) against
   the dense fp16 MFMA peak, and the fp16 work the matrix cores issue (two
@@ -368,7 +369,10 @@ RESIDENT_MODELS = {
 }
 
 
-def resident(name: str, tg: int, pp: int, blocks: int | None = None) -> dict:
+VERIFY_TOKENS = (1, 2, 4, 8, 16, 33)
+
+
+def resident(name: str, tg: int, pp: int, blocks: int | None = None, verify=()) -> dict:
     """The provider's resident plan on a synthetic model of `name`'s shape:
     tg = tokens/s of `tg` decode steps from position 0 (each with its logits
     downloaded and checked, as llama-bench's tg counts a generated token),
@@ -411,6 +415,24 @@ def resident(name: str, tg: int, pp: int, blocks: int | None = None) -> dict:
                                   "weight_bytes_per_token": wbytes, "effective_gbs": round(gbs, 1),
                                   "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "launches_per_token": round(launches, 1),
                                   "logits_finite": bool(np.all(np.isfinite(plan.logits)))}
+            if verify:
+                # Batched verification (nya_compute_plan_verify): the target
+                # runs k draft tokens at once and returns its greedy choice
+                # after each; serial verification is k decode steps.
+                step_us = out[f"tg{tg}"]["us_per_token"] if tg else None
+                out["verify"] = {}
+                for k in verify:
+                    toks = ids[8:8 + k]
+                    plan.verify(toks, 8)
+                    reps = 20
+                    start = time.perf_counter()
+                    for _ in range(reps):
+                        plan.verify(toks, 8)
+                    wall = (time.perf_counter() - start) / reps
+                    leg = {"us_per_call": round(wall * 1e6, 1), "target_tokens_per_s": round(k / wall, 1)}
+                    if step_us:
+                        leg["speedup_vs_serial_steps"] = round(k * step_us / (wall * 1e6), 2)
+                    out["verify"][str(k)] = leg
             if pp:
                 plan.prefill(ids[:pp], 0)
                 start = time.perf_counter()
@@ -426,7 +448,8 @@ def resident(name: str, tg: int, pp: int, blocks: int | None = None) -> dict:
 
 
 def resident_legs(tg: int, pp: int, blocks: int | None) -> dict:
-    legs = {name: resident(name, tg, 0 if name == "llama-8b" else pp, blocks) for name in RESIDENT_MODELS}
+    legs = {name: resident(name, tg, 0 if name == "llama-8b" else pp, blocks,
+                           VERIFY_TOKENS if name == "llama-8b" else ()) for name in RESIDENT_MODELS}
     legs["reference_published"] = {
         "tinyllama-1.1b": {"tg128": 205.48, "pp512": 1374.38, "hardware": "RTX 5060 Ti",
                            "source": "backend/README.md:796-803 (Stage 2 Fyodor CUDA resident)"}}

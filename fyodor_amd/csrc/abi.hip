@@ -37,12 +37,23 @@ bool storage_bytes(unsigned type, size_t rows, size_t cols, size_t *bytes)
     return true;
 }
 
-// Batches above the small-N kernels' 8 columns go to the prefill GEMM
-// (every block format).
-bool use_prefill(unsigned type, size_t cols, size_t batch)
+// Batches above the small-N kernels' 8 columns go to the prefill GEMM (every
+// block format), except small batches of matrices the row-balanced small-N
+// kernel takes: those stay memory-bound, and launches of 8 tokens each beat
+// the GEMM's activation split and sparse grid up to a batch measured per
+// shape (MI355X, 50 calls over rotating weights, GEMM / 8-token launches):
+// Q4_K 14336 x 4096 at 16 tokens 32.0 / 22.3 us, at 24 32.6 / 33.0; Q4_K and
+// Q8_0 4096 x 4096 at 32 31.4 / 26.2 and 40.7 / 25.6, at 40 31.1 / 32.6;
+// Q6_K 4096 x 14336 (its int8 GEMM starts slow on wide rows) at 48
+// 203.9 / 152.7, at 64 203.9 / 201.9. The Q6_K output head (128256 x 4096)
+// keeps the GEMM from 9 tokens on (173 / 198 us).
+bool use_prefill(unsigned type, size_t rows, size_t cols, size_t batch)
 {
-    (void)cols;
-    return batch > 8 && (type == Q4_K || type == Q6_K || type == Q8_0 || type == Q4_0);
+    if (batch <= 8 || !(type == Q4_K || type == Q6_K || type == Q8_0 || type == Q4_0)) return false;
+    size_t chunked = 0;
+    if (type == Q6_K) chunked = cols > 4096 ? 56 : 0;
+    else chunked = rows >= 8192 ? 20 : 32;
+    return batch > chunked || !smalln_rows_supported(type, (int)rows, (int)cols, 8);
 }
 
 int status(hipError_t e)
@@ -71,7 +82,7 @@ int matmul_impl(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t 
     const bool fits = workspace && !(workspace & 15u);
     // The GEMM needs its workspace; without one (or a short one) the batch is
     // run 8 columns at a time instead.
-    if (use_prefill(type, cols, batch) && fits && workspace_bytes >= prefill_workspace(type, (int)cols, (int)batch))
+    if (use_prefill(type, rows, cols, batch) && fits && workspace_bytes >= prefill_workspace(type, (int)cols, (int)batch))
         return status(launch_prefill(type, wp, (const float *)x, (float *)y, (int)rows, (int)cols, (int)batch,
                                      (void *)workspace, s));
     for (size_t done = 0; done < batch; done += 8) {
@@ -176,7 +187,7 @@ NYA_HIP_EXPORT int nya_hip_workspace_bytes(unsigned type, size_t rows, size_t co
     if (!bytes || !batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return 1;
     const bool dense = type == F32 || type == F16 || type == BF16;
     const int n = batch < 8 ? (int)batch : 8;
-    *bytes = use_prefill(type, cols, batch) ? prefill_workspace(type, (int)cols, (int)batch)
+    *bytes = use_prefill(type, rows, cols, batch) ? prefill_workspace(type, (int)cols, (int)batch)
            : dense || smalln_rows_supported(type, (int)rows, (int)cols, n) ? 0 : smalln_workspace((int)cols, n);
     return 0;
 }
@@ -202,7 +213,7 @@ NYA_HIP_EXPORT int nya_hip_matmul_static(uintptr_t w, unsigned type, size_t rows
     // as through nya_hip_matmul. Every other path needs at most a few hundred
     // KiB (the small-N digits of one 16384-column chunk).
     size_t parts = 1;
-    if (use_prefill(type, cols, batch)) {
+    if (use_prefill(type, rows, cols, batch)) {
         const size_t fit = static_chunk_tokens(type, cols);
         if (fit < 64) return NYA_HIP_STATUS_SCRATCH;
         parts = (batch + fit - 1) / fit;
@@ -225,9 +236,11 @@ NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_
     size_t b;
     if (!batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return NULL;
     if (type == F32 || type == F16 || type == BF16) return "skinny_dense";
-    if (use_prefill(type, cols, batch)) return prefill_kernel(type);
+    if (use_prefill(type, rows, cols, batch)) return prefill_kernel(type);
     if (batch == 1 && matvec_supported(type, (int)rows, (int)cols)) return matvec_kernel(type, (int)rows, (int)cols);
-    return smalln_rows_supported(type, (int)rows, (int)cols, (int)batch) ? "smalln_rows" : "smalln_mfma";
+    // Batches above 8 outside the GEMM run 8 tokens per launch.
+    const int n = batch < 8 ? (int)batch : 8;
+    return smalln_rows_supported(type, (int)rows, (int)cols, n) ? "smalln_rows" : "smalln_mfma";
 }
 
 NYA_HIP_EXPORT int nya_hip_copy(uintptr_t dst, uintptr_t src, size_t bytes, uintptr_t stream)

@@ -194,8 +194,11 @@ def test_prefill_dispatch_and_workspace():
     of a padded token count; batches above 8 go to the prefill GEMM: fp16
     activation pieces for Q4_K/Q8_0/Q4_0 (per token, rounded up to 64
     tokens: two fp16 planes, the 32-column block sums and the scale), int8
-    digits for Q6_K (rounded up to 32 tokens); dense types need none
-    (nothing is launched)."""
+    digits for Q6_K (rounded up to 32 tokens) -- except small batches of
+    matrices the row-balanced small-N kernel takes, which run 8 tokens per
+    launch up to a break-even batch (20 tokens from 8192 rows on, else 32;
+    Q6_K only on rows wider than 4096 columns, up to 56); dense types need
+    none (nothing is launched)."""
     kern = Kernels()
 
     def pieces(cols, batch):
@@ -214,9 +217,18 @@ def test_prefill_dispatch_and_workspace():
         assert kern.workspace_bytes(t, 16384, 8192, 3) == 8192 // 32 * 136 * 4
         assert kern.kernel_name(t, 4096, 4096, 8) == ("smalln_rows" if rows_kernel else "smalln_mfma")
     for t in (Q4_0, Q8_0, Q4_K):
-        assert kern.workspace_bytes(t, 4096, 4096, 9) == pieces(4096, 9)
+        for batch in (9, 32):
+            assert kern.workspace_bytes(t, 4096, 4096, batch) == 0
+            assert kern.kernel_name(t, 4096, 4096, batch) == "smalln_rows"
+        assert kern.workspace_bytes(t, 4096, 4096, 33) == pieces(4096, 33)
+        assert kern.workspace_bytes(t, 14336, 4096, 20) == 0
+        assert kern.workspace_bytes(t, 14336, 4096, 21) == pieces(4096, 21)
+        assert kern.kernel_name(t, 14336, 4096, 21) == "prefill_f16"
         assert kern.workspace_bytes(t, 4096, 4096, 512) == pieces(4096, 512)
         assert kern.kernel_name(t, 4096, 4096, 512) == "prefill_f16"
+    assert kern.workspace_bytes(Q6_K, 4096, 14336, 56) == 0
+    assert kern.kernel_name(Q6_K, 4096, 14336, 56) == "smalln_rows"
+    assert kern.kernel_name(Q6_K, 4096, 14336, 57) == "prefill_mfma"
     assert kern.workspace_bytes(Q6_K, 4096, 4096, 9) == 4096 // 32 * 136 * 32
     assert kern.workspace_bytes(Q6_K, 4096, 4096, 512) == 4096 // 32 * 136 * 512
     assert kern.kernel_name(Q6_K, 4096, 4096, 512) == "prefill_mfma"

@@ -434,30 +434,34 @@ __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) vo
 // for every lane of the workgroup): the group and field parts are scalar
 // offsets.
 //
-// Issue order is fixed (the empty asm statements keep the compiler from
-// reordering the loads): the scale words first, then the quants in the order
-// the dots use them. A wavefront's loads return in order, so each block's
-// dots wait only for the loads before its own, and the work left after the
-// last load of a stage is one block's (left to the compiler, the scale word
-// went last and every scale multiply waited for the whole stage).
+// A stage is loaded field by field: field 0 is the scale word (Q6_K: the
+// 16-column scales and d), field 1 + p quant word p (Q6_K: ql and qh of unit
+// p), in the order the dots use them. Issue order is fixed (the empty asm
+// statements keep the compiler from reordering the loads) and a wavefront's
+// loads return in order, so each block's dots wait only for the loads before
+// its own, and the work left after the last load of a stage is one block's
+// (left to the compiler, the scale word went last and every scale multiply
+// waited for the whole stage).
+template <unsigned T> constexpr int kFields = 1 + (T == Q6_K ? 4 : kQuantLoads<T>);
+
 template <unsigned T, bool FULL>
-__device__ __forceinline__ void load_rows(MvStage<T> &w, __amdgpu_buffer_rsrc_t wb, int vq, int vs, int R, int g,
-    int vd = 0, int G = 0)
+__device__ __forceinline__ void load_field(MvStage<T> &w, __amdgpu_buffer_rsrc_t wb, int vq, int vs, int R, int g,
+    int vd, int G, int f)
 {
     if constexpr (T == Q6_K) {
         // Per group 208 R bytes: units p at 48 R p (ql half h at + 16 R h,
         // qh at + 32 R), scales at 192 R; the d of all G groups after them
         // (2 bytes per row at vd = tile + 2 r, group g at 208 R G + 2 R g).
-        if constexpr (FULL) {
-            w.sc = bload16<true>(wb, vs, kTileRows * (208 * g + 192));
-            w.d = __builtin_amdgcn_raw_buffer_load_b16(wb, vd, kTileRows * (208 * G + 2 * g), 2);
+        if (f == 0) {
+            if constexpr (FULL) {
+                w.sc = bload16<true>(wb, vs, kTileRows * (208 * g + 192));
+                w.d = __builtin_amdgcn_raw_buffer_load_b16(wb, vd, kTileRows * (208 * G + 2 * g), 2);
+            } else {
+                w.sc = bload16<true>(wb, vs + R * (208 * g + 192), 0);
+                w.d = __builtin_amdgcn_raw_buffer_load_b16(wb, vd + R * (208 * G + 2 * g), 0, 2);
+            }
         } else {
-            w.sc = bload16<true>(wb, vs + R * (208 * g + 192), 0);
-            w.d = __builtin_amdgcn_raw_buffer_load_b16(wb, vd + R * (208 * G + 2 * g), 0, 2);
-        }
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            asm volatile("" ::: "memory");
+            const int p = f - 1;
             if constexpr (FULL) {
                 w.ql[p] = bload16<true>(wb, vq, kTileRows * (208 * g + 48 * p));
                 w.qh[p] = bload16<true>(wb, vs, kTileRows * (208 * g + 48 * p + 32));
@@ -468,21 +472,48 @@ __device__ __forceinline__ void load_rows(MvStage<T> &w, __amdgpu_buffer_rsrc_t 
         }
     } else {
         constexpr int GB = kGroupRowBytes<T>, S = kScaleOffset<T>;
-        u32x4 sw;
-        if constexpr (FULL) sw = bload16<true>(wb, vs, kTileRows * (GB * g + S));
-        else sw = bload16<true>(wb, vs + R * (GB * g + S), 0);
-        if constexpr (T == Q4_K) w.sl = sw;
-        else w.d = sw;
-#pragma unroll
-        for (int p = 0; p < kQuantLoads<T>; ++p) {
-            asm volatile("" ::: "memory");
+        if (f == 0) {
+            u32x4 sw;
+            if constexpr (FULL) sw = bload16<true>(wb, vs, kTileRows * (GB * g + S));
+            else sw = bload16<true>(wb, vs + R * (GB * g + S), 0);
+            if constexpr (T == Q4_K) w.sl = sw;
+            else w.d = sw;
+        } else {
+            const int p = f - 1;
             if constexpr (FULL) w.q[p] = bload16<true>(wb, vq, kTileRows * GB * g + 1024 * p);
             else w.q[p] = bload16<true>(wb, vq + R * (GB * g + 32 * p), 0);
         }
     }
+}
+
+template <unsigned T, bool FULL>
+__device__ __forceinline__ void load_rows(MvStage<T> &w, __amdgpu_buffer_rsrc_t wb, int vq, int vs, int R, int g,
+    int vd = 0, int G = 0)
+{
+#pragma unroll
+    for (int f = 0; f < kFields<T>; ++f) {
+        load_field<T, FULL>(w, wb, vq, vs, R, g, vd, G, f);
+        asm volatile("" ::: "memory");
+    }
     // Nothing after the loads is scheduled among them (an activation
     // instruction placed there waited for the x loads and held back the rest
     // of the stage).
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// The same for VT virtual tiles at once, field by field (field f of every
+// tile before field f + 1): for dots that take block b of every tile
+// together.
+template <unsigned T, bool FULL, int VT>
+__device__ __forceinline__ void load_rows_fields(MvStage<T> (&w)[VT], __amdgpu_buffer_rsrc_t wb, const int (&vq)[VT],
+    const int (&vs)[VT], const int (&R)[VT], int g, const int (&vd)[VT], int G)
+{
+#pragma unroll
+    for (int f = 0; f < kFields<T>; ++f) {
+#pragma unroll
+        for (int v = 0; v < VT; ++v) load_field<T, FULL>(w[v], wb, vq[v], vs[v], R[v], g, vd[v], G, f);
+        asm volatile("" ::: "memory");
+    }
     __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -1020,16 +1051,19 @@ __device__ __forceinline__ void group_dots_tokens(float (&y)[VT][(kTokAcc<T, NP>
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        // Then tile by tile, in load order: each block's dots wait only for
-        // its own quant word.
+        // Then block by block, each block's two MFMAs (one per tile) and their
+        // scale multiply-adds interleaved: the loads come field by field, so
+        // block pair p waits only for quant word p of each tile.
+        int acc[VT][J][3];
 #pragma unroll
-        for (int v = 0; v < VT; ++v) {
-            int acc[J][3];
+        for (int v = 0; v < VT; ++v)
 #pragma unroll
-            for (int j = 0; j < J; ++j) acc[j][0] = acc[j][1] = acc[j][2] = 0;
+            for (int j = 0; j < J; ++j) acc[v][j][0] = acc[v][j][1] = acc[v][j][2] = 0;
 #pragma unroll
-            for (int b = 0; b < 8; ++b) {
-                const i32x4 a = *(const i32x4 *)(slot + aoff + astride * b);
+        for (int b = 0; b < 8; ++b) {
+            const i32x4 a = *(const i32x4 *)(slot + aoff + astride * b);
+#pragma unroll
+            for (int v = 0; v < VT; ++v) {
                 const i32x16 D = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, block_b_tokens<T>(w[v], b), (i32x16){}, 0, 0, 0);
                 const int sc = (int)__builtin_amdgcn_ubfe(w[v].sl[b >> 1], 12 * (b & 1), 6);
                 // |D| < 2^16: the 24-bit multiply-add takes it whole. The
@@ -1040,42 +1074,49 @@ __device__ __forceinline__ void group_dots_tokens(float (&y)[VT][(kTokAcc<T, NP>
                 for (int j = 0; j < J; ++j)
 #pragma unroll
                     for (int d = 0; d < 3; ++d) {
-                        acc[j][d] += ((D[4 * j + d] << 8) >> 8) * sc;
-                        asm("" : "+v"(acc[j][d]));
+                        acc[v][j][d] += ((D[4 * j + d] << 8) >> 8) * sc;
+                        asm("" : "+v"(acc[v][j][d]));
                     }
             }
+        }
+#pragma unroll
+        for (int v = 0; v < VT; ++v) {
             const u32x4 sl = w[v].sl;   // byte 3 of the four words: d, dmin
             const uint32_t dd = (sl.x >> 24) | ((sl.y >> 24) << 8) | ((sl.z >> 24) << 16) | ((sl.w >> 24) << 24);
 #pragma unroll
             for (int j = 0; j < J; ++j) {
-                const float G = __builtin_fmaf((float)acc[j][2], 65536.f,
-                                               __builtin_fmaf((float)acc[j][1], 256.f, (float)acc[j][0]));
+                const float G = __builtin_fmaf((float)acc[v][j][2], 65536.f,
+                                               __builtin_fmaf((float)acc[v][j][1], 256.f, (float)acc[v][j][0]));
                 y[v][j] = __builtin_fmaf(-f16_to_f32(dd >> 16), mterm[v][j],
                                          __builtin_fmaf(s4[j] * f16_to_f32(dd & 0xFFFFu), G, y[v][j]));
             }
         }
     } else {
-        // Tile by tile, in load order (the scale word first).
-        constexpr float kWeightFactor = T == Q4_0 ? 0.0625f : 1.f;
+        // Block by block over the tiles, as for Q4_K.
+        float acc[VT][J];
 #pragma unroll
-        for (int v = 0; v < VT; ++v) {
-            float acc[J];
+        for (int v = 0; v < VT; ++v)
 #pragma unroll
-            for (int j = 0; j < J; ++j) acc[j] = 0.f;
+            for (int j = 0; j < J; ++j) acc[v][j] = 0.f;
 #pragma unroll
-            for (int b = 0; b < 8; ++b) {
-                const i32x4 a = *(const i32x4 *)(slot + aoff + astride * b);
+        for (int b = 0; b < 8; ++b) {
+            const i32x4 a = *(const i32x4 *)(slot + aoff + astride * b);
+#pragma unroll
+            for (int v = 0; v < VT; ++v) {
                 const i32x16 D = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, block_b_tokens<T>(w[v], b), (i32x16){}, 0, 0, 0);
                 const float db = f16_to_f32((w[v].d[b >> 1] >> (16 * (b & 1))) & 0xFFFFu);
                 // Sums reach 2^34: the top digit joins in float.
 #pragma unroll
                 for (int j = 0; j < J; ++j)
-                    acc[j] = __builtin_fmaf(__builtin_fmaf((float)D[4 * j + 2], 65536.f,
-                                                           (float)(D[4 * j + 1] * 256 + D[4 * j])), db, acc[j]);
+                    acc[v][j] = __builtin_fmaf(__builtin_fmaf((float)D[4 * j + 2], 65536.f,
+                                                              (float)(D[4 * j + 1] * 256 + D[4 * j])), db, acc[v][j]);
             }
-#pragma unroll
-            for (int j = 0; j < J; ++j) y[v][j] = __builtin_fmaf(s4[j] * kWeightFactor, acc[j], y[v][j]);
         }
+        constexpr float kWeightFactor = T == Q4_0 ? 0.0625f : 1.f;
+#pragma unroll
+        for (int v = 0; v < VT; ++v)
+#pragma unroll
+            for (int j = 0; j < J; ++j) y[v][j] = __builtin_fmaf(s4[j] * kWeightFactor, acc[v][j], y[v][j]);
     }
 }
 
@@ -1133,15 +1174,20 @@ __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, 
         }
         MvStage<T> st[VT];
         if constexpr (!LOOP) {
-            // One group per wavefront (cols <= 4096).
+            // One group per wavefront (cols <= 4096); the dots take block b
+            // of every tile together, so the tiles load field by field.
+            int vq[VT], vs[VT], vd[VT], R[VT];
 #pragma unroll
             for (int v = 0; v < VT; ++v) {
                 const int row = base + (kTileRows * v + (lane & 31) < live ? kTileRows * v + (lane & 31) : live - 1);
                 const int t = row / kTileRows, r = row - kTileRows * t;
-                const int R = t == tiles - 1 ? rlast : kTileRows;
+                R[v] = t == tiles - 1 ? rlast : kTileRows;
                 const int tb = (int)((size_t)kTileRows * t * row_bytes);
-                load_rows<T, FULL>(st[v], wb, tb + 16 * R * h + 16 * r, tb + 16 * r, R, wave, tb + 2 * r, groups);
+                vq[v] = tb + 16 * R[v] * h + 16 * r;
+                vs[v] = tb + 16 * r;
+                vd[v] = tb + 2 * r;
             }
+            load_rows_fields<T, FULL, VT>(st, wb, vq, vs, R, wave, vd, groups);
             quantize_tokens<T == Q4_K, NP>(px, lane, slot);
             // Each wave reads back only its own slot.
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

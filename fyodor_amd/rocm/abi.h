@@ -28,6 +28,17 @@ typedef struct nya_hip_runtime {
     hipError_t (*stream_wait)(hipStream_t);
 } nya_hip_runtime;
 
+/* libamdhip64's stream capture and graphs. Optional: without them the
+ * resident plan launches every step of a token itself. */
+typedef struct nya_hip_graphs {
+    hipError_t (*begin_capture)(hipStream_t, hipStreamCaptureMode);
+    hipError_t (*end_capture)(hipStream_t, hipGraph_t *);
+    hipError_t (*instantiate)(hipGraphExec_t *, hipGraph_t, unsigned long long);
+    hipError_t (*launch)(hipGraphExec_t, hipStream_t);
+    hipError_t (*exec_destroy)(hipGraphExec_t);
+    hipError_t (*destroy)(hipGraph_t);
+} nya_hip_graphs;
+
 /* libfyodor_hip (include/fyodor_hip.h) */
 typedef struct nya_kernel_library {
     unsigned (*abi_version)(void);

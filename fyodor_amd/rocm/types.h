@@ -26,6 +26,14 @@ typedef enum hipMemcpyKind {
 } hipMemcpyKind;
 
 typedef struct ihipStream_t *hipStream_t;
+typedef struct ihipGraph *hipGraph_t;
+typedef struct hipGraphExec *hipGraphExec_t;
+
+typedef enum hipStreamCaptureMode {
+    hipStreamCaptureModeGlobal = 0,
+    hipStreamCaptureModeThreadLocal = 1,
+    hipStreamCaptureModeRelaxed = 2
+} hipStreamCaptureMode;
 
 /* hipStreamNonBlocking: the stream does not synchronize with the null
  * stream (rocm/rocm.c:179 passes 1). */

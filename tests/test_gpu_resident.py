@@ -68,3 +68,46 @@ def test_python_model_plan_on_gpu(session_lib, rocm_env, tmp_path):
                        seed=5)
     out = plan_against_engine(session_lib, tmp_path, shape, TOKENS[:24])
     print(f"python-built plan: worst scaled logit error {out['logit']:.3g}, KV {out['kv']:.3g}", flush=True)
+
+
+def test_decode_graph_replays_match_direct_launches(monkeypatch):
+    """A decode token's launches replayed as a captured HIP graph give the
+    same logits, bit for bit, as the same launches issued one by one
+    (NYA_ROCM_GRAPHS=0), over many replays of both graphs (with and without
+    logits) with eager prompt chunks and host waits between them."""
+    import numpy as np
+    from fyodor_amd import Compute
+    from fyodor_amd import model as fm
+    monkeypatch.setenv("NYA_ROCM_KERNEL_LIBRARY", str(KERNEL_LIBRARY))
+    monkeypatch.delenv("NYA_ROCM_HIP_LIBRARY", raising=False)
+    shape = fm.LlamaShape(embedding=512, heads=8, kv_heads=2, hidden=1024, blocks=3, context=64, vocabulary=1000,
+                          seed=3)
+    model = fm.LlamaModel(shape)
+    tokens = [(i * 37 + 11) % shape.vocabulary for i in range(40)]
+
+    def decode(graphs: bool):
+        monkeypatch.setenv("NYA_ROCM_GRAPHS", "1" if graphs else "0")
+        compute = Compute("rocm")
+        plan = fm.Plan(compute, model, shape.context)
+        rows = []
+        try:
+            rows.append(plan.prefill(tokens[:5], 0).copy())
+            for i in range(5, 30):
+                if i % 4 == 3:
+                    plan.token(tokens[i], i, logits=False)
+                else:
+                    rows.append(plan.token(tokens[i], i).copy())
+            rows.append(plan.prefill(tokens[30:37], 30).copy())
+            for i in range(37, 40):
+                rows.append(plan.token(tokens[i], i).copy())
+            return rows, plan.stats()
+        finally:
+            plan.close()
+            compute.close()
+
+    graphed, g = decode(True)
+    direct, d = decode(False)
+    assert g["graph_captures"] == 2 and g["graph_replays"] == 28 and d["graph_replays"] == 0
+    assert g["kernel_launches"] == d["kernel_launches"] and g["external_matmul_calls"] == d["external_matmul_calls"]
+    for i, (a, b) in enumerate(zip(graphed, direct)):
+        assert np.array_equal(a, b), f"row {i}"

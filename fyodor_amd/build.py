@@ -81,7 +81,7 @@ def build_provider() -> Path:
     out = LIB / "libfyodor_rocm.so"
     tmp = LIB / "libfyodor_rocm.so.tmp"
     _run(["gcc", *C_FLAGS, f"-I{REPO / 'include'}", f"-I{ROOT / 'core'}", f"-I{ROOT / 'rocm'}",
-          *[str(ROOT / s) for s in C_SOURCES], "-shared", "-ldl", "-o", str(tmp)])
+          *[str(ROOT / s) for s in C_SOURCES], "-shared", "-ldl", "-lm", "-o", str(tmp)])
     os.replace(tmp, out)
     return out
 

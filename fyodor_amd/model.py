@@ -300,3 +300,33 @@ def generate_greedy(target: Plan, draft: Plan | None, prompt, limit: int, window
                                        len(stops), out, ctypes.byref(count), ctypes.byref(stats)):
         raise RuntimeError("greedy generation failed")
     return list(out[:count.value]), stats.as_dict()
+
+
+class Sampling(ctypes.Structure):
+    """nya_compute_sampling (include/compute.h)."""
+    _fields_ = [("temperature", ctypes.c_float), ("top_p", ctypes.c_float), ("top_k", ctypes.c_size_t),
+                ("seed", ctypes.c_uint64)]
+
+
+def generate_sampled(target: Plan, draft: Plan | None, prompt, limit: int, temperature: float, top_p: float = 1.0,
+                     top_k: int = 0, seed: int = 0, window: int = 4, stops=()):
+    """Generation at `temperature` with the engine's exact speculative
+    sampling over batched verification (nya_compute_generate_sampled):
+    (tokens, counters). Both plans must be empty and hold len(prompt) + limit
+    positions."""
+    lib = target.lib
+    u = ctypes.POINTER(ctypes.c_uint)
+    lib.nya_compute_generate_sampled.argtypes = [ctypes.c_void_p, ctypes.c_void_p, u, ctypes.c_size_t,
+                                                 ctypes.c_size_t, ctypes.c_size_t, ctypes.POINTER(Sampling), u,
+                                                 ctypes.c_size_t, u, ctypes.POINTER(ctypes.c_size_t),
+                                                 ctypes.POINTER(Speculation)]
+    p = (ctypes.c_uint * len(prompt))(*prompt)
+    st = (ctypes.c_uint * max(len(stops), 1))(*stops)
+    out = (ctypes.c_uint * limit)()
+    count, stats = ctypes.c_size_t(), Speculation()
+    s = Sampling(temperature, top_p, top_k, seed)
+    if lib.nya_compute_generate_sampled(target.ptr, draft.ptr if draft else None, p, len(prompt), window, limit,
+                                        ctypes.byref(s), st, len(stops), out, ctypes.byref(count),
+                                        ctypes.byref(stats)):
+        raise RuntimeError("sampled generation failed")
+    return list(out[:count.value]), stats.as_dict()

@@ -14,6 +14,7 @@
 #define NYA_COMPUTE_H
 
 #include <stddef.h>
+#include <stdint.h>
 
 typedef struct nya_compute_context nya_compute_context;
 
@@ -140,5 +141,33 @@ int nya_compute_generate_greedy(nya_compute_plan *target, nya_compute_plan *draf
     const unsigned int *prompt, size_t prompt_count, size_t window, size_t limit,
     const unsigned int *stops, size_t stop_count, unsigned int *out, size_t *out_count,
     nya_compute_speculation *stats);
+
+/* Sampling controls of the engine's generation request
+ * (backend/include/generation.h:22-44). */
+typedef struct nya_compute_sampling {
+    float temperature;   /* 0: greedy; else at most 5 */
+    float top_p;         /* nucleus mass, in (0, 1] */
+    size_t top_k;        /* 0: no top-k filter */
+    uint64_t seed;       /* 0: the engine's default stream */
+} nya_compute_sampling;
+
+/* Generation at temperature > 0 with the engine's exact speculative sampling
+ * (backend/core/llm_cpu.c:1146-1317, ordinary draft): the draft samples up to
+ * `window` proposals from its own distribution (its own random stream), one
+ * nya_compute_plan_verify of the target returns the target's rows for all of
+ * them, and each proposal x is accepted with probability min(1, p(x)/q(x));
+ * the first rejection emits a draw from max(p - q, 0) instead and ends the
+ * round; after all proposals the target samples one more token. p and q are
+ * the distributions after temperature, top-k and top-p, as the engine builds
+ * them (llm_cpu.c:847-888), and the random streams, their seeds and the order
+ * of their draws are the engine's, so equal logits give equal tokens. Without
+ * a draft (or window 0) it is the engine's plain sampling loop
+ * (llm_cpu.c:1036-1075). Temperature 0 is nya_compute_generate_greedy.
+ * Other arguments and the return value as there; `stats->accepted` counts
+ * accepted proposals. */
+int nya_compute_generate_sampled(nya_compute_plan *target, nya_compute_plan *draft,
+    const unsigned int *prompt, size_t prompt_count, size_t window, size_t limit,
+    const nya_compute_sampling *sampling, const unsigned int *stops, size_t stop_count,
+    unsigned int *out, size_t *out_count, nya_compute_speculation *stats);
 
 #endif

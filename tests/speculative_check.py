@@ -7,15 +7,23 @@ The oracle is the target plan's own serial decode: one nya_compute_plan_token
 per token, with the engine's greedy rule applied to its logits (the first
 largest value, backend/core/llm_cpu.c:896-904; numpy's argmax picks the first
 of equal maxima). Greedy speculative decoding must emit exactly that
-sequence, whatever the draft proposes (backend/core/llm_cpu.c:1274-1317)."""
+sequence, whatever the draft proposes (backend/core/llm_cpu.c:1274-1317).
+
+Sampled generation (nya_compute_generate_sampled) is checked against
+oracle/speculative.py, the engine's sampler and speculative sampling loop
+restated (itself pinned to the engine's nya_llm_generate_draft in
+tests/test_sampling_oracle.py), fed by a second pair of plans that make the
+same provider calls as the C loop: equal logits, so equal tokens."""
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 
 import numpy as np
 
 from fyodor_amd import Compute, storage_bytes
 from fyodor_amd import model as fm
+from oracle import speculative as spec
 from resident_check import LOGIT_BOUND
 
 
@@ -194,3 +202,120 @@ def suppressed_tokens_are_skipped(shape: fm.LlamaShape, prompt):
         plan.close()
         compute.close()
         del keep
+
+
+class PlanSource:
+    """Logits for the sampling oracle from a plan, through the calls
+    nya_compute_generate_sampled makes: positions of the prefix not yet in
+    the plan's cache (the first mismatch on) run as one catch-up (plan_token
+    for one token, plan_prefill for more), then one verification of the
+    batch returns its rows."""
+
+    def __init__(self, plan: fm.Plan):
+        self.plan, self.cache = plan, []
+
+    def rows(self, prefix, batch):
+        k = 0
+        while k < min(len(self.cache), len(prefix)) and self.cache[k] == prefix[k]:
+            k += 1
+        part = list(prefix[k:])
+        if len(part) == 1:
+            self.plan.token(part[0], k, logits=False)
+        elif part:
+            self.plan.prefill(part, k)
+        _, rows = self.plan.verify(list(batch), len(prefix), logits=True)
+        self.cache = list(prefix) + list(batch)
+        return rows
+
+    def row(self, prefix, token):
+        return self.rows(prefix, [token])[0]
+
+
+def sampled_generation_matches_oracle(target_shape: fm.LlamaShape, draft: str, prompt, limit: int, cases,
+                                      stops=()):
+    """nya_compute_generate_sampled for each (window, temperature, top_p,
+    top_k, seed) of `cases` emits the oracle's tokens, with its counts of
+    proposals and accepted proposals; `draft` is "other" (other weights),
+    "same" (the target's weights) or "none". Returns the counters."""
+    compute = Compute("rocm")
+    target_model = fm.LlamaModel(target_shape)
+    draft_model = {"other": lambda: fm.LlamaModel(dataclasses.replace(target_shape, seed=11, blocks=1)),
+                   "same": lambda: target_model, "none": lambda: None}[draft]()
+    capacity = len(prompt) + limit
+    out = []
+    try:
+        for window, temperature, top_p, top_k, seed in cases:
+            plans = [fm.Plan(compute, target_model, capacity)]
+            if draft_model is not None:
+                plans.append(fm.Plan(compute, draft_model, capacity))
+            try:
+                got, stats = fm.generate_sampled(plans[0], plans[1] if len(plans) > 1 else None, prompt, limit,
+                                                 temperature, top_p, top_k, seed, window=window, stops=stops)
+                sources = [PlanSource(fm.Plan(compute, target_model, capacity))]
+                if draft_model is not None:
+                    sources.append(PlanSource(fm.Plan(compute, draft_model, capacity)))
+                try:
+                    ref, counts = spec.generate(sources[0].rows, sources[1].row if len(sources) > 1 else None, prompt,
+                                                limit, window, temperature, top_p, top_k, seed, stops)
+                finally:
+                    for src in sources:
+                        src.plan.close()
+            finally:
+                for plan in plans:
+                    plan.close()
+            where = f"window {window} T {temperature} top_p {top_p} top_k {top_k} seed {seed}"
+            assert got == ref, f"{where}: {got} != {ref}"
+            assert stats["generated"] == len(got)
+            assert stats["accepted"] == counts["accepted"], where
+            assert stats["draft_tokens"] == counts["draft_tokens"], where
+            out.append(stats)
+    finally:
+        compute.close()
+    return out
+
+
+def first_token_follows_target(target_shape: fm.LlamaShape, prompt, runs: int, window: int = 4):
+    """The engine's distribution check (backend/tests/test_generation.c
+    :345-365) on this build: with top-k 2, a temperature giving the leading
+    candidate p = 3/4, and a draft favouring the other candidate, the
+    first token over `runs` seeds follows the target's two-candidate
+    distribution (within five standard deviations), and both acceptance and
+    rejection happen; with top_p below the leading probability only the
+    leading token comes out (:377-387). Returns (p, count of the leading
+    token, accepted proposals)."""
+    compute = Compute("rocm")
+    target_model = fm.LlamaModel(target_shape)
+    capacity = len(prompt) + 1
+    probe = fm.Plan(compute, target_model, capacity)
+    try:
+        row = probe.prefill(list(prompt), 0).copy()
+    finally:
+        probe.close()
+    # The temperature that gives the leading candidate p = 3/4 of the two:
+    # draws of the target's distribution and of the reversed draft's then
+    # differ by half the runs.
+    top2 = np.sort(row)[-2:]
+    temperature = float(np.float32((top2[1] - top2[0]) / np.log(3.0))) if top2[1] > top2[0] else 1.0
+    dense, cand = spec.distribution(row, temperature, 1.0, 2)
+    lead, p = cand[0]
+    # As the engine's test does, a draft that reverses the two candidates:
+    # the target's weights with their output rows swapped.
+    draft_model = fm.LlamaModel(target_shape, swapped_output(target_shape, target_model.arrays, lead, cand[1][0]))
+    target, draft = fm.Plan(compute, target_model, capacity), fm.Plan(compute, draft_model, capacity)
+    try:
+        count = accepted = 0
+        for seed in range(1, runs + 1):
+            got, stats = fm.generate_sampled(target, draft, prompt, 1, temperature, 1.0, 2, seed, window=window)
+            count += got[0] == lead
+            accepted += stats["accepted"]
+        sigma = (runs * p * (1 - p)) ** 0.5
+        assert abs(count - runs * p) <= 4.5 * sigma, (count, runs, p)
+        assert 0 < accepted < runs, accepted
+        for seed in range(1, 33):
+            got, _ = fm.generate_sampled(target, draft, prompt, 1, temperature, 0.9 * p, 2, seed, window=window)
+            assert got == [lead], (seed, got, lead, p)
+    finally:
+        target.close()
+        draft.close()
+        compute.close()
+    return p, count, accepted

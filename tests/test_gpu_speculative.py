@@ -11,13 +11,20 @@ on the gfx950 kernels:
 - nya_compute_generate_greedy emits the target's serial greedy decode with
   drafts that disagree, agree, or agree at some positions only (proposals
   both accepted and rejected), and without a draft;
+- nya_compute_generate_sampled emits the tokens of the engine's speculative
+  sampling loop restated (oracle/speculative.py, pinned to the engine in
+  tests/test_sampling_oracle.py) fed by plans making the same calls, with
+  drafts of other weights, the target's own, and none; the first token
+  follows the target's distribution over 400 seeds and top-p below the
+  leading probability keeps only the leading token
+  (backend/tests/test_generation.c:345-387);
 - the device greedy choice skips suppressed tokens."""
 import pytest
 
 from fyodor_amd import Q4_K, Q6_K, Q8_0
 from fyodor_amd import model as fm
-from speculative_check import (generation_equals_target_decode, suppressed_tokens_are_skipped,
-                               verify_matches_steps)
+from speculative_check import (first_token_follows_target, generation_equals_target_decode,
+                               sampled_generation_matches_oracle, suppressed_tokens_are_skipped, verify_matches_steps)
 
 pytestmark = pytest.mark.gpu
 
@@ -62,3 +69,24 @@ def test_generation_equals_target_decode(draft):
 def test_suppressed_tokens_are_skipped():
     suppressed_tokens_are_skipped(fm.LlamaShape(embedding=512, heads=8, kv_heads=2, hidden=1024, blocks=2, context=32,
                                                 vocabulary=1000, seed=3), PROMPT)
+
+
+SAMPLED_CASES = [(4, 1.0, 1.0, 0, 1), (1, 0.7, 0.9, 0, 7), (8, 1.5, 1.0, 5, 123), (5, 1.0, 0.5, 40, 99),
+                 (16, 0.5, 1.0, 0, 3)]
+
+
+@pytest.mark.parametrize("draft", ["other", "same", "none"])
+def test_sampled_generation_matches_oracle(draft):
+    types = {"embedding": Q4_K, "output": Q6_K, "attention": Q4_K, "gate_up": Q4_K, "down": Q6_K}
+    target = fm.LlamaShape(embedding=512, heads=8, kv_heads=2, hidden=1024, blocks=3, context=96, vocabulary=1000,
+                           types=types, seed=3)
+    runs = sampled_generation_matches_oracle(target, draft, PROMPT, 24, SAMPLED_CASES)
+    print(draft, runs, flush=True)
+    if draft == "same":
+        # The target's weights on the same kernels: equal distributions.
+        assert all(r["accepted"] == r["draft_tokens"] for r in runs), runs
+
+
+def test_sampled_first_token_distribution():
+    p, count, accepted = first_token_follows_target(fm.LlamaShape(context=64, seed=3), PROMPT[:1], runs=400)
+    print(f"p {p:.4f}: {count} of 400 leading, {accepted} accepted", flush=True)

@@ -11,14 +11,21 @@ holds the checks, which also run on an MI355X (tests/test_gpu_speculative.py):
   rows of the output matrix swapped (some accepted, some rejected), and
   without a draft, at several windows; a stop token ends it after the token
   is emitted;
+- nya_compute_generate_sampled emits the tokens of the engine's speculative
+  sampling loop restated (oracle/speculative.py) over seeds, temperatures,
+  top-k, top-p, windows and drafts (other weights, the target's own, none),
+  with its counts of proposals and acceptances; over many seeds the first
+  token follows the target's distribution, and top-p below the leading
+  probability keeps only the leading token (the engine's own checks,
+  backend/tests/test_generation.c:345-387);
 - suppressed tokens are skipped by the device greedy choice;
 - requests outside the plan's limits are refused without retiring it."""
 import pytest
 
 from fyodor_amd import Compute
 from fyodor_amd import model as fm
-from speculative_check import (generation_equals_target_decode, suppressed_tokens_are_skipped,
-                               verify_matches_steps)
+from speculative_check import (first_token_follows_target, generation_equals_target_decode,
+                               sampled_generation_matches_oracle, suppressed_tokens_are_skipped, verify_matches_steps)
 
 PROMPT = [5, 17, 200, 3]
 
@@ -51,6 +58,33 @@ def test_generation_equals_target_decode(mock_rocm, draft):
         # At window 1 the draft only proposes after the swapped token (the
         # round's bonus) and is right; longer windows reach it and are wrong.
         assert any(0 < stats["accepted"] < stats["draft_tokens"] for _, stats in runs), runs
+
+
+SAMPLED_CASES = [(4, 1.0, 1.0, 0, 1), (1, 0.7, 0.9, 0, 7), (3, 1.5, 1.0, 5, 123), (5, 1.0, 0.5, 40, 99),
+                 (2, 2.5, 1.0, 0, 0)]
+
+
+@pytest.mark.parametrize("draft", ["other", "same", "none"])
+def test_sampled_generation_matches_oracle(mock_rocm, draft):
+    runs = sampled_generation_matches_oracle(fm.LlamaShape(context=64, seed=3), draft, PROMPT, 16, SAMPLED_CASES)
+    if draft == "same":
+        # Equal weights give equal distributions: every proposal is accepted.
+        assert all(r["accepted"] == r["draft_tokens"] for r in runs), runs
+    if draft == "other":
+        assert any(r["accepted"] < r["draft_tokens"] for r in runs), runs
+
+
+def test_sampled_stop_token(mock_rocm):
+    sampled_generation_matches_oracle(fm.LlamaShape(context=64, seed=3), "other", PROMPT, 24,
+                                      [(4, 3.0, 1.0, 0, s) for s in (1, 2, 3)], stops=(7, 100, 250))
+
+
+def test_sampled_first_token_distribution(mock_rocm):
+    # A one-token prompt needs no catch-up runs; at p = 3/4, 400 seeds put
+    # the target's distribution and the reversed draft's 23 standard
+    # deviations apart.
+    p, count, accepted = first_token_follows_target(fm.LlamaShape(context=64, seed=3), PROMPT[:1], runs=400)
+    assert abs(p - 0.75) < 0.01, p
 
 
 def test_stop_token_ends_generation(mock_rocm):

@@ -231,6 +231,17 @@ NYA_HIP_EXPORT int nya_hip_matmul_static(uintptr_t w, unsigned type, size_t rows
     return 0;
 }
 
+NYA_HIP_EXPORT int nya_hip_matvec_gated(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t gate,
+    uintptr_t up, uintptr_t y, uintptr_t stream)
+{
+    size_t b;
+    if (!w || !gate || !up || !y || !storage_bytes(type, rows, cols, &b)) return 1;
+    if ((w & 15u) || (gate & 15u) || (up & 15u) || (y & 3u)) return 1;
+    if (!matvec_gated_supported(type, (int)rows, (int)cols)) return 1;
+    return status(launch_matvec_gated(type, (const uint8_t *)w, (const float *)gate, (const float *)up, (float *)y,
+                                      (int)rows, (int)cols, (hipStream_t)stream));
+}
+
 NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_t cols, size_t batch)
 {
     size_t b;

@@ -26,6 +26,13 @@ bool matvec_supported(unsigned type, int rows, int cols);
 const char *matvec_kernel(unsigned type, int rows, int cols);
 hipError_t launch_matvec(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,
     hipStream_t stream);
+// The same product of silu(gate) * up (elementwise, formed as each group of
+// the vector is loaded): the decoder's gated SiLU folded into its down
+// product. Shapes that run on the row-balanced kernel only (up to two tiles
+// per CU for Q4_K); gate and up 16-byte aligned.
+bool matvec_gated_supported(unsigned type, int rows, int cols);
+hipError_t launch_matvec_gated(unsigned type, const uint8_t *w, const float *gate, const float *up, float *y,
+    int rows, int cols, hipStream_t stream);
 // Batches of 2..8 on the same row-balanced layout, the activation digits made
 // inside the kernel (matvec.hip); no workspace. x must be 16-byte aligned.
 bool smalln_rows_supported(unsigned type, int rows, int cols, int batch);

@@ -539,10 +539,27 @@ __device__ __forceinline__ void load_rows_fields(MvStage<T> (&w)[VT], __amdgpu_b
 // lane l holds row l%16 of group 2k + (l/16)%2. A stage whose second group
 // is past the wavefront's last one repeats its first group in those lanes,
 // and their sums are dropped.
-template <unsigned T, int VT, int RING, int KS, int P, bool FULL, bool MULTI>
+// The engine's gated SiLU of one element, silu(g) u = g / (1 + e^-g) u
+// (backend/core/llm_cpu.c:336-341), with the resident step's operations and
+// none of them contracted (the step's file contracts nothing): uncontracted,
+// the product cannot fuse into the block sums that use it either, so the
+// vector is the step's bit for bit.
+__device__ __forceinline__ float gated_silu(float g, float u)
+{
+#pragma clang fp contract(off)
+    return g / (1.0f + expf(-g)) * u;
+}
+__device__ __forceinline__ float4 gated_silu(float4 g, float4 u)
+{
+    return make_float4(gated_silu(g.x, u.x), gated_silu(g.y, u.y), gated_silu(g.z, u.z), gated_silu(g.w, u.w));
+}
+
+// GATED: the vector multiplied is silu(x) * up elementwise (x and up of the
+// same chunk layout), formed as each group is loaded.
+template <unsigned T, int VT, int RING, int KS, int P, bool FULL, bool MULTI, bool GATED>
 __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, const float *__restrict__ x,
-    float *__restrict__ y, int rows, int cols, int base, int live, int g0c, int ngc, int accumulate,
-    uint8_t *sdig, float4 *smeta, float (*red)[VT][64])
+    const float *__restrict__ up, float *__restrict__ y, int rows, int cols, int base, int live, int g0c, int ngc,
+    int accumulate, uint8_t *sdig, float4 *smeta, float (*red)[VT][64])
 {
     static_assert(P == 1 || (P == 2 && VT == 1), "two groups per stage: one 16-row virtual tile");
     constexpr int RT = kTileRows / P;   // rows per virtual tile
@@ -552,7 +569,9 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
     const size_t row_bytes = tiled_row_bytes<T>(cols);
     const int tiles = (rows + kTileRows - 1) / kTileRows, rlast = rows - kTileRows * (tiles - 1);
     const __amdgpu_buffer_rsrc_t wb = buffer_of(w, (uint32_t)((size_t)rows * row_bytes));
-    const __amdgpu_buffer_rsrc_t xb = buffer_of(x, (uint32_t)((g0c + ngc) * kGroupCols <= cols ? ngc : 0) * 1024u);
+    const uint32_t xbytes = (uint32_t)((g0c + ngc) * kGroupCols <= cols ? ngc : 0) * 1024u;
+    const __amdgpu_buffer_rsrc_t xb = buffer_of(x, xbytes);
+    const __amdgpu_buffer_rsrc_t ub = buffer_of(GATED ? up : x, GATED ? xbytes : 0u);
     // Lane offsets per virtual tile; rows past this workgroup's repeat its
     // last row (same addresses: no extra traffic).
     int vq[VT], vs[VT], vd[VT], R[VT];
@@ -606,10 +625,13 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
     //    and the merge waits for the loads, holding back every weight load
     //    behind a full memory round trip.
     auto xgroup = [&](int j) { return wave + KS * (j < ns ? j : ns - 1); };
-    float4 px[P * RING];
+    float4 px[P * RING], pu[P * RING];
 #pragma unroll
-    for (int j = 0; j < P * RING; ++j)
+    for (int j = 0; j < P * RING; ++j) {
         px[j] = __builtin_bit_cast(float4, bload16<false>(xb, 16 * lane + 1024 * (ns > 0 ? xgroup(j) : wave), 0));
+        if constexpr (GATED)
+            pu[j] = __builtin_bit_cast(float4, bload16<false>(ub, 16 * lane + 1024 * (ns > 0 ? xgroup(j) : wave), 0));
+    }
     asm volatile("" ::: "memory");
     if (ns > 0) {
         MvStage<T> st[RING][VT];
@@ -621,12 +643,18 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
 #pragma unroll
         for (int j = 0; j < P * RING; ++j) {
             asm volatile("" : "+v"(px[j].x), "+v"(px[j].y), "+v"(px[j].z), "+v"(px[j].w) :: "memory");
+            if constexpr (GATED) {
+                asm volatile("" : "+v"(pu[j].x), "+v"(pu[j].y), "+v"(pu[j].z), "+v"(pu[j].w) :: "memory");
+                px[j] = gated_silu(px[j], pu[j]);
+            }
             if (j < ns) quantize_group(px[j], xgroup(j), lane, fmul, fcorr, sdig, smeta);
         }
         if constexpr (MULTI)
-            for (int j = P * RING; j < ns; ++j)
-                quantize_group(__builtin_bit_cast(float4, bload16<false>(xb, 16 * lane, 1024 * xgroup(j))), xgroup(j),
-                               lane, fmul, fcorr, sdig, smeta);
+            for (int j = P * RING; j < ns; ++j) {
+                float4 v = __builtin_bit_cast(float4, bload16<false>(xb, 16 * lane, 1024 * xgroup(j)));
+                if constexpr (GATED) v = gated_silu(v, __builtin_bit_cast(float4, bload16<false>(ub, 16 * lane, 1024 * xgroup(j))));
+                quantize_group(v, xgroup(j), lane, fmul, fcorr, sdig, smeta);
+            }
         // Each wave reads back only the groups it wrote.
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -685,9 +713,9 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
     *dst = accumulate ? *dst + sum : sum;
 }
 
-template <unsigned T, int VT, int RING, int KS, int P, bool MULTI>
+template <unsigned T, int VT, int RING, int KS, int P, bool MULTI, bool GATED = false>
 __global__ __launch_bounds__(64 * KS) void matvec_rows(const uint8_t *__restrict__ w, const float *__restrict__ x,
-    float *__restrict__ y, int rows, int cols, int rw, int g0c, int ngc, int accumulate)
+    const float *__restrict__ up, float *__restrict__ y, int rows, int cols, int rw, int g0c, int ngc, int accumulate)
 {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float red[KS][VT][64];
@@ -699,11 +727,11 @@ __global__ __launch_bounds__(64 * KS) void matvec_rows(const uint8_t *__restrict
     // matrix may be shorter): group and field offsets are scalar.
     const int tiles = (rows + kTileRows - 1) / kTileRows;
     if (rows % kTileRows == 0 || base + live <= kTileRows * (tiles - 1))
-        matvec_rows_body<T, VT, RING, KS, P, true, MULTI>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig,
-                                                         smeta, red);
+        matvec_rows_body<T, VT, RING, KS, P, true, MULTI, GATED>(w, x, up, y, rows, cols, base, live, g0c, ngc,
+                                                                accumulate, sdig, smeta, red);
     else
-        matvec_rows_body<T, VT, RING, KS, P, false, MULTI>(w, x, y, rows, cols, base, live, g0c, ngc, accumulate, sdig,
-                                                          smeta, red);
+        matvec_rows_body<T, VT, RING, KS, P, false, MULTI, GATED>(w, x, up, y, rows, cols, base, live, g0c, ngc,
+                                                                 accumulate, sdig, smeta, red);
 }
 
 size_t matvec_lds(int ccols)
@@ -739,32 +767,33 @@ int rows_per_workgroup(int rows)
 }
 
 // One launch of matvec_rows over chunk groups [g0, g0 + ng).
-template <unsigned T, int VT, int RING, int KS, int P = 1>
-void launch_rows_kernel(int wgs, size_t lds, hipStream_t s, const uint8_t *w, const float *xc, float *y, int rows,
-    int cols, int rw, int g0, int ng)
+template <unsigned T, int VT, int RING, int KS, int P = 1, bool GATED = false>
+void launch_rows_kernel(int wgs, size_t lds, hipStream_t s, const uint8_t *w, const float *xc, const float *uc,
+    float *y, int rows, int cols, int rw, int g0, int ng)
 {
     // A chunk has at most kChunkCols / kGroupCols groups: past KS P RING of
     // them no wavefront needs the refill code.
     if constexpr (KS * P * RING < kChunkCols / kGroupCols) {
         if (((ng + KS - 1) / KS + P - 1) / P > RING) {
-            hipLaunchKernelGGL((matvec_rows<T, VT, RING, KS, P, true>), dim3(wgs), dim3(64 * KS), lds, s, w, xc, y, rows,
-                               cols, rw, g0, ng, g0 > 0);
+            hipLaunchKernelGGL((matvec_rows<T, VT, RING, KS, P, true, GATED>), dim3(wgs), dim3(64 * KS), lds, s, w, xc,
+                               uc, y, rows, cols, rw, g0, ng, g0 > 0);
             return;
         }
     }
-    hipLaunchKernelGGL((matvec_rows<T, VT, RING, KS, P, false>), dim3(wgs), dim3(64 * KS), lds, s, w, xc, y, rows, cols,
-                       rw, g0, ng, g0 > 0);
+    hipLaunchKernelGGL((matvec_rows<T, VT, RING, KS, P, false, GATED>), dim3(wgs), dim3(64 * KS), lds, s, w, xc, uc, y,
+                       rows, cols, rw, g0, ng, g0 > 0);
 }
 
-template <unsigned T>
-hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int cols, hipStream_t s)
+template <unsigned T, bool GATED = false>
+hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int cols, hipStream_t s,
+    const float *up = nullptr)
 {
     // Past two tiles per CU (Q6_K only): one workgroup per 32-row tile.
     const int rpw = rows_per_workgroup(rows), rw = rpw > 2 * kTileRows ? kTileRows : rpw;
     const int groups = cols / kGroupCols, wgs = (rows + rw - 1) / rw;
     for (int g0 = 0; g0 < groups; g0 += kChunkCols / kGroupCols) {
         const int ng = groups - g0 < kChunkCols / kGroupCols ? groups - g0 : kChunkCols / kGroupCols;
-        const float *xc = x + (size_t)g0 * kGroupCols;
+        const float *xc = x + (size_t)g0 * kGroupCols, *uc = GATED ? up + (size_t)g0 * kGroupCols : nullptr;
         const size_t lds = matvec_lds(ng * kGroupCols);
         // Up to 16 rows per CU: two groups per stage (P = 2, 4096 x 11008
         // Q4_0: 7.53 -> 7.07 us), and a second stage where a wavefront has
@@ -778,26 +807,26 @@ hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int
         // wavefronts of up to 256 registers.
         if constexpr (T == Q6_K) {
             if (rw <= kTileRows / 2 && deep)
-                launch_rows_kernel<T, 1, 2, 16, 2>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 1, 2, 16, 2, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
             else if (rw <= kTileRows / 2)
-                launch_rows_kernel<T, 1, 1, 16, 2>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 1, 1, 16, 2, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
             else if (rw <= kTileRows && rpw > 2 * kTileRows)   // one tile per workgroup (128256 x 4096: 84.7 -> 72.5 us)
-                launch_rows_kernel<T, 1, 1, 8>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 1, 1, 8, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
             else if (rw <= kTileRows)
-                launch_rows_kernel<T, 1, 1, 16>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 1, 1, 16, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
             else
-                launch_rows_kernel<T, 2, 1, 8>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 2, 1, 8, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
         } else {
             // One stage per wavefront from 17 rows per CU on, also where it
             // has several groups (two stages measured 2-10 % slower).
             if (rw <= kTileRows / 2 && deep)
-                launch_rows_kernel<T, 1, 2, 16, 2>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 1, 2, 16, 2, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
             else if (rw <= kTileRows / 2)
-                launch_rows_kernel<T, 1, 1, 16, 2>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 1, 1, 16, 2, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
             else if (rw <= kTileRows)
-                launch_rows_kernel<T, 1, 1, 16>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 1, 1, 16, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
             else
-                launch_rows_kernel<T, 2, 1, 16>(wgs, lds, s, w, xc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 2, 1, 16, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -1398,6 +1427,21 @@ hipError_t launch_matvec(unsigned type, const uint8_t *w, const float *x, float 
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+bool matvec_gated_supported(unsigned type, int rows, int cols)
+{
+    return matvec_supported(type, rows, cols) && (type != Q4_K || rows_per_workgroup(rows) <= 2 * kTileRows);
+}
+
+hipError_t launch_matvec_gated(unsigned type, const uint8_t *w, const float *gate, const float *up, float *y,
+    int rows, int cols, hipStream_t s)
+{
+    if (!matvec_gated_supported(type, rows, cols)) return hipErrorInvalidValue;
+    if (type == Q4_0) return launch_rows<Q4_0, true>(w, gate, y, rows, cols, s, up);
+    if (type == Q8_0) return launch_rows<Q8_0, true>(w, gate, y, rows, cols, s, up);
+    if (type == Q6_K) return launch_rows<Q6_K, true>(w, gate, y, rows, cols, s, up);
+    return launch_rows<Q4_K, true>(w, gate, y, rows, cols, s, up);
 }
 
 }  // namespace fy

@@ -61,6 +61,8 @@ typedef struct nya_resident_ops {
         size_t, size_t, float, uintptr_t);
     int (*silu_mul)(uintptr_t, size_t, uintptr_t, size_t, uintptr_t, size_t, size_t, uintptr_t);
     int (*greedy)(uintptr_t, size_t, size_t, uintptr_t, uintptr_t, uintptr_t);
+    /* Optional within the set: NULL leaves the gated SiLU a step of its own. */
+    int (*matvec_gated)(uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t);
 } nya_resident_ops;
 
 #define NYA_KERNEL_ABI 1U

@@ -192,6 +192,20 @@ NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t key
 NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, size_t gate_stride, uintptr_t up, size_t up_stride,
     uintptr_t out, size_t n, size_t count, uintptr_t stream);
 
+/* No counterpart in the reference: the decoder's gated SiLU step (as
+ * nya_hip_silu_mul computes it, backend/core/llm_cpu.c:336-341) folded into
+ * the down product of one token. y = W v with v[j] = silu(gate[j]) * up[j],
+ * j < cols, W as for nya_hip_matmul (the library's layout); v is formed as
+ * each group of it is loaded, with the step's own operations, so y equals
+ * nya_hip_silu_mul followed by nya_hip_matmul of one column bit for bit.
+ * For callers that run one decode token (the resident plan): it saves one
+ * launch per block. Returns 1 for shapes the row kernel does not take
+ * (quantized types Q4_K / Q6_K / Q8_0 / Q4_0 only, and for Q4_K at most 64
+ * rows per CU) and for gate / up not 16-byte aligned: the caller runs the
+ * two steps instead. */
+NYA_HIP_EXPORT int nya_hip_matvec_gated(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t gate,
+    uintptr_t up, uintptr_t y, uintptr_t stream);
+
 /* ids[i] = the greedy choice of row i of `count` rows of n fp32 logits
  * (logits + i n), as backend/core/llm_cpu.c:896-904 (nya_llm_sample at
  * temperature 0) picks it after the suppressed tokens are masked

@@ -32,14 +32,16 @@ def test_kernel_library_exports_its_header():
     assert want == {"nya_hip_abi_version", "nya_hip_weight_bytes", "nya_hip_weight_layout", "nya_hip_weight_pack",
                     "nya_hip_workspace_bytes", "nya_hip_matmul", "nya_hip_matmul_static", "nya_hip_kernel_name",
                     "nya_hip_copy", "nya_hip_read", "nya_hip_step", "nya_hip_embed", "nya_hip_rms_norm",
-                    "nya_hip_rope_qkv", "nya_hip_attention", "nya_hip_silu_mul", "nya_hip_greedy"}
+                    "nya_hip_rope_qkv", "nya_hip_attention", "nya_hip_silu_mul", "nya_hip_greedy",
+                    "nya_hip_matvec_gated"}
     assert want <= exported(KERNEL_LIBRARY)
 
 
 def test_provider_library_exports_compute_api():
     want = declared("compute.h") | declared("compute_backend.h")
     assert "nya_rocm_backend" in want and "nya_compute_matmul_typed" in want
-    assert {"nya_compute_plan_verify", "nya_compute_generate_greedy", "nya_rocm_plan_verify"} <= want
+    assert {"nya_compute_plan_verify", "nya_compute_generate_greedy", "nya_compute_generate_sampled",
+            "nya_rocm_plan_verify"} <= want
     missing = want - exported(PROVIDER_LIBRARY)
     assert not missing, missing
 

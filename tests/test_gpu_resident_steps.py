@@ -16,7 +16,11 @@ inputs:
   one query and causal runs of several, lengths from 1 through the LDS limit
   (8192) into the global-scratch path: within 1e-5 (1 + |ref|);
 - silu_mul (fused [gate | up] rows, separate blocks, in place for one
-  token): within 2e-6 (1 + |ref|).
+  token): within 2e-6 (1 + |ref|);
+- matvec_gated (the gated SiLU folded into a one-token down product): bit
+  for bit the output of silu_mul followed by nya_hip_matmul, for every
+  quantized type at down-projection shapes (wide rows, chunked rows, a
+  ragged last tile), and declined (1) where the row kernel does not run.
 The bounds are fp32 rounding over these sums, far inside the engine's own
 inference bounds (logits 5e-4 (1 + |ref|))."""
 import ctypes
@@ -42,6 +46,7 @@ def env():
     L.nya_hip_rope_qkv.argtypes = [_up, _sz, _up, _sz, _up, _sz, _sz, _sz, _sz, _sz, _up, _up, _sz, _up, _up, _up]
     L.nya_hip_attention.argtypes = [_up, _sz, _up, _up, _up, _up, _up, _sz, _sz, _sz, _sz, _sz, _f, _up]
     L.nya_hip_silu_mul.argtypes = [_up, _sz, _up, _sz, _up, _sz, _sz, _up]
+    L.nya_hip_matvec_gated.argtypes = [_up, _u, _sz, _sz, _up, _up, _up, _up]
     stream = rt.stream()
     yield rt, L, stream
     rt.sync(stream)
@@ -283,5 +288,43 @@ def test_silu_mul(env, layout):
         assert scaled_error(dev.get(out, g), ref) <= 2e-6
         if layout != "in-place":
             assert L.nya_hip_silu_mul(gd, gs, ud, us, gd, n, count, stream) == 1   # overlapping output
+    finally:
+        dev.close()
+
+
+@pytest.mark.parametrize("t,rows,cols", [(Q6_K, 4096, 14336), (Q4_K, 4096, 14336), (Q6_K, 2048, 5632),
+                                         (Q4_0, 4096, 11008), (Q8_0, 1000, 4096), (Q4_K, 8192, 28672),
+                                         (Q6_K, 300, 256)])
+def test_matvec_gated_equals_two_steps(env, t, rows, cols):
+    rt, L, stream = env
+    kern = Kernels()
+    rng = np.random.default_rng(rows + cols)
+    g = (4 * rng.standard_normal(cols)).astype(np.float32)
+    u = rng.standard_normal(cols).astype(np.float32)
+    w = kern.device_weights(synth.weights(t, rows, cols, seed=rows), t, rows, cols)
+    dev = Dev(rt)
+    try:
+        wd, gd, ud = dev.put(w), dev.put(g), dev.put(u)
+        v, y1, y2 = dev.empty(4 * cols), dev.empty(4 * rows), dev.empty(4 * rows)
+        print(f"gated {t} {rows}x{cols}", flush=True)
+        assert L.nya_hip_matvec_gated(wd, t, rows, cols, gd, ud, y1, stream) == 0
+        assert L.nya_hip_silu_mul(gd, cols, ud, cols, v, cols, 1, stream) == 0
+        kern.matmul(wd, t, rows, cols, v, y2, 1, 0, 0, stream)
+        rt.sync(stream)
+        a, b = dev.get(y1, np.empty(rows, np.float32)), dev.get(y2, np.empty(rows, np.float32))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    finally:
+        dev.close()
+
+
+def test_matvec_gated_declines(env):
+    rt, L, stream = env
+    dev = Dev(rt)
+    try:
+        p = dev.empty(4 * 8192)
+        assert L.nya_hip_matvec_gated(p, F16, 64, 256, p, p, p, stream) == 1          # dense type
+        assert L.nya_hip_matvec_gated(p, Q4_0, 64, 288, p, p, p, stream) == 1         # short last group
+        assert L.nya_hip_matvec_gated(p, Q4_K, 20480, 256, p, p, p, stream) == 1      # > 64 rows per CU
+        assert L.nya_hip_matvec_gated(p, Q4_K, 64, 256, p + 4, p, p, stream) == 1     # gate not 16-byte aligned
     finally:
         dev.close()

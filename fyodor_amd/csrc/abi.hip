@@ -242,6 +242,17 @@ NYA_HIP_EXPORT int nya_hip_matvec_gated(uintptr_t w, unsigned type, size_t rows,
                                       (int)rows, (int)cols, (hipStream_t)stream));
 }
 
+NYA_HIP_EXPORT int nya_hip_matvec_swiglu(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
+    uintptr_t hidden, uintptr_t stream)
+{
+    size_t b;
+    if (!storage_bytes(type, rows, cols, &b) || !matvec_swiglu_supported(type, (int)rows, (int)cols)) return 1;
+    if (!w) return 0;   // the shape query
+    if (!x || !hidden || (w & 15u) || (x & 15u) || (hidden & 3u)) return 1;
+    return status(launch_matvec_swiglu(type, (const uint8_t *)w, (const float *)x, (float *)hidden, (int)rows,
+                                       (int)cols, (hipStream_t)stream));
+}
+
 NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_t cols, size_t batch)
 {
     size_t b;
@@ -339,6 +350,14 @@ NYA_HIP_EXPORT int nya_hip_greedy(uintptr_t logits, size_t n, size_t count, uint
     if (!vec(logits) || !vec(ids) || (mask & 3u) || !count_ok(n) || !tokens_ok(count)) return 1;
     return status(launch_greedy((const float *)logits, (int)n, (int)count, (const uint32_t *)mask, (uint32_t *)ids,
                                 (hipStream_t)stream));
+}
+
+NYA_HIP_EXPORT int nya_hip_silu_pairs(uintptr_t gu, uintptr_t out, size_t n, size_t count, uintptr_t stream)
+{
+    if (!vec(gu) || !vec(out) || !count_ok(n) || n % 16 || n > (size_t)INT_MAX / 2 || !tokens_ok(count)) return 1;
+    const uintptr_t in_end = gu + 8 * n * count, out_end = out + 4 * n * count;
+    if (gu < out_end && out < in_end) return 1;   // overlapping
+    return status(launch_silu_pairs((const float *)gu, (float *)out, (int)n, (int)count, (hipStream_t)stream));
 }
 
 NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, size_t gate_stride, uintptr_t up, size_t up_stride,

@@ -31,6 +31,13 @@ hipError_t launch_matvec(unsigned type, const uint8_t *w, const float *x, float 
 // product. Shapes that run on the row-balanced kernel only (up to two tiles
 // per CU for Q4_K); gate and up 16-byte aligned.
 bool matvec_gated_supported(unsigned type, int rows, int cols);
+// The gate|up product of one token with rows interleaved in 16-row blocks
+// (gate rows, then their up rows) and silu(gate) * up as its output: Q4_K on
+// the one-workgroup-per-tile kernel (more than 64 rows per CU), one column
+// chunk.
+bool matvec_swiglu_supported(unsigned type, int rows, int cols);
+hipError_t launch_matvec_swiglu(unsigned type, const uint8_t *w, const float *x, float *hidden, int rows, int cols,
+    hipStream_t stream);
 hipError_t launch_matvec_gated(unsigned type, const uint8_t *w, const float *gate, const float *up, float *y,
     int rows, int cols, hipStream_t stream);
 // Batches of 2..8 on the same row-balanced layout, the activation digits made
@@ -88,6 +95,7 @@ hipError_t launch_attention(const float *q, int q_stride, const float *keys, con
     hipStream_t stream);
 hipError_t launch_silu_mul(const float *gate, int gate_stride, const float *up, int up_stride, float *out, int n,
     int count, hipStream_t stream);
+hipError_t launch_silu_pairs(const float *gu, float *out, int n, int count, hipStream_t stream);
 // The greedy choice of each of `count` rows of n logits (first largest among
 // the entries not masked; 0xFFFFFFFF for a row with a NaN or +inf, or
 // without a finite candidate).

@@ -338,7 +338,25 @@ __device__ __forceinline__ void load_q4k(MvStage<Q4_K> &w, __amdgpu_buffer_rsrc_
 // One workgroup per 32-row tile, KS wavefronts splitting its groups
 // [g0c, g0c + ngc) (one column chunk); wavefront w takes chunk groups
 // w, w + KS, ... through a RING-stage register ring.
-template <int KS, int RING>
+// The engine's gated SiLU of one element, silu(g) u = g / (1 + e^-g) u
+// (backend/core/llm_cpu.c:336-341), with the resident step's operations and
+// none of them contracted (the step's file contracts nothing): uncontracted,
+// the product cannot fuse into the block sums that use it either, so the
+// vector is the step's bit for bit.
+__device__ __forceinline__ float gated_silu(float g, float u)
+{
+#pragma clang fp contract(off)
+    return g / (1.0f + expf(-g)) * u;
+}
+__device__ __forceinline__ float4 gated_silu(float4 g, float4 u)
+{
+    return make_float4(gated_silu(g.x, u.x), gated_silu(g.y, u.y), gated_silu(g.z, u.z), gated_silu(g.w, u.w));
+}
+
+// SWIGLU: the rows come in 16-row blocks of gate rows and up rows (tile t
+// holds gate rows 16t .. 16t + 15 as its rows 0..15, their up rows as 16..31)
+// and y receives silu(gate) * up, 16 values per tile at 16 t.
+template <int KS, int RING, bool SWIGLU = false>
 __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) void matvec_q4k(
     const uint8_t *__restrict__ w, const float *__restrict__ x, float *__restrict__ y, int rows, int cols, int g0c,
     int ngc, int accumulate)
@@ -422,6 +440,12 @@ __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) vo
     float v = red[0][lane] + red[0][lane + 32];
 #pragma unroll
     for (int q = 1; q < KS; ++q) v += red[q][lane] + red[q][lane + 32];
+    if constexpr (SWIGLU) {
+        // Every tile is whole (R = 32): lane l < 16 takes its up row from l + 16.
+        const float up = __shfl_down(v, 16, 32);
+        if (lane < 16) y[16 * t + lane] = gated_silu(v, up);
+        return;
+    }
     float *dst = y + kTileRows * t + lane;
     *dst = accumulate ? *dst + v : v;
 }
@@ -539,20 +563,6 @@ __device__ __forceinline__ void load_rows_fields(MvStage<T> (&w)[VT], __amdgpu_b
 // lane l holds row l%16 of group 2k + (l/16)%2. A stage whose second group
 // is past the wavefront's last one repeats its first group in those lanes,
 // and their sums are dropped.
-// The engine's gated SiLU of one element, silu(g) u = g / (1 + e^-g) u
-// (backend/core/llm_cpu.c:336-341), with the resident step's operations and
-// none of them contracted (the step's file contracts nothing): uncontracted,
-// the product cannot fuse into the block sums that use it either, so the
-// vector is the step's bit for bit.
-__device__ __forceinline__ float gated_silu(float g, float u)
-{
-#pragma clang fp contract(off)
-    return g / (1.0f + expf(-g)) * u;
-}
-__device__ __forceinline__ float4 gated_silu(float4 g, float4 u)
-{
-    return make_float4(gated_silu(g.x, u.x), gated_silu(g.y, u.y), gated_silu(g.z, u.z), gated_silu(g.w, u.w));
-}
 
 // GATED: the vector multiplied is silu(x) * up elementwise (x and up of the
 // same chunk layout), formed as each group is loaded.
@@ -1432,6 +1442,22 @@ hipError_t launch_matvec(unsigned type, const uint8_t *w, const float *x, float 
 bool matvec_gated_supported(unsigned type, int rows, int cols)
 {
     return matvec_supported(type, rows, cols) && (type != Q4_K || rows_per_workgroup(rows) <= 2 * kTileRows);
+}
+
+bool matvec_swiglu_supported(unsigned type, int rows, int cols)
+{
+    return type == Q4_K && rows % (2 * 16) == 0 && cols % kGroupCols == 0 && cols <= kChunkCols &&
+           rows_per_workgroup(rows) > 2 * kTileRows;
+}
+
+hipError_t launch_matvec_swiglu(unsigned type, const uint8_t *w, const float *x, float *hidden, int rows, int cols,
+    hipStream_t s)
+{
+    if (!matvec_swiglu_supported(type, rows, cols)) return hipErrorInvalidValue;
+    const int groups = cols / kGroupCols;
+    hipLaunchKernelGGL((matvec_q4k<8, 2, true>), dim3((unsigned)(rows / kTileRows)), dim3(512),
+                       matvec_lds(groups * kGroupCols), s, w, x, hidden, rows, cols, 0, groups, 0);
+    return hipGetLastError();
 }
 
 hipError_t launch_matvec_gated(unsigned type, const uint8_t *w, const float *gate, const float *up, float *y,

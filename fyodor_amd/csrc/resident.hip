@@ -412,6 +412,19 @@ __global__ __launch_bounds__(256) void silu_mul4(const float4 *gate, int gate_st
     }
 }
 
+// The same over rows that hold gate and up in 16-element blocks (row i of
+// 2n values at gu + 2 n i: gate element j at 32 (j / 16) + j % 16, up
+// element j 16 further), out rows of n.
+__global__ __launch_bounds__(256) void silu_pairs(const float *__restrict__ gu, float *__restrict__ out, int n)
+{
+    const float *row = gu + (size_t)blockIdx.y * 2 * n;
+    float *o = out + (size_t)blockIdx.y * n;
+    for (int j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256) {
+        const int at = 32 * (j >> 4) + (j & 15);
+        o[j] = silu_times(row[at], row[at + 16]);
+    }
+}
+
 __global__ __launch_bounds__(256) void silu_mul(const float *gate, int gate_stride, const float *up, int up_stride,
     float *out, int n)
 {
@@ -575,6 +588,12 @@ hipError_t launch_attention(const float *q, int q_stride, const float *keys, con
 hipError_t launch_greedy(const float *logits, int n, int count, const uint32_t *mask, uint32_t *ids, hipStream_t s)
 {
     hipLaunchKernelGGL(greedy, dim3((unsigned)count), dim3(1024), 0, s, logits, n, mask, ids);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_pairs(const float *gu, float *out, int n, int count, hipStream_t s)
+{
+    hipLaunchKernelGGL(silu_pairs, dim3(grid_of(n), (unsigned)count), dim3(256), 0, s, gu, out, n);
     return hipGetLastError();
 }
 

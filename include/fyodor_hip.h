@@ -192,6 +192,29 @@ NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t key
 NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, size_t gate_stride, uintptr_t up, size_t up_stride,
     uintptr_t out, size_t n, size_t count, uintptr_t stream);
 
+/* No counterpart in the reference: the gate|up product of one token with
+ * the gated SiLU as its output. W (rows = 2 n, the library's layout) holds
+ * the feed-forward gate and up rows interleaved in 16-row blocks: rows
+ * 32 b .. 32 b + 15 are gate rows 16 b .. 16 b + 15, rows 32 b + 16 ..
+ * 32 b + 31 their up rows. hidden[j] = silu(g_j) * u_j (as nya_hip_silu_pairs
+ * forms it) with g_j, u_j the products of x with gate and up row j, equal bit
+ * for bit to nya_hip_matmul of one column followed by nya_hip_silu_pairs;
+ * each SiLU is formed once. For callers that lay out the matrix so (the
+ * resident plan): one launch and one pass over the products fewer per block.
+ * w == 0 queries the shape: 0 where it runs, 1 where it does not (Q4_K only,
+ * rows a multiple of 32 and more than 64 per CU, cols a multiple of 256 up to
+ * 16384); then also 1 for x or hidden missing or misaligned. */
+NYA_HIP_EXPORT int nya_hip_matvec_swiglu(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
+    uintptr_t hidden, uintptr_t stream);
+
+/* out[i][j] = silu(g) * u for row i of gu (count rows of 2 n floats holding
+ * gate and up values in 16-element blocks: g = gu[i][32 (j / 16) + j % 16],
+ * u 16 further), out rows of n (n a multiple of 16; out must not overlap gu);
+ * silu(g) * u = g / (1 + e^-g) * u as nya_hip_silu_mul forms it. The
+ * feed-forward step of the gate|up layout of nya_hip_matvec_swiglu for runs
+ * of several tokens. */
+NYA_HIP_EXPORT int nya_hip_silu_pairs(uintptr_t gu, uintptr_t out, size_t n, size_t count, uintptr_t stream);
+
 /* No counterpart in the reference: the decoder's gated SiLU step (as
  * nya_hip_silu_mul computes it, backend/core/llm_cpu.c:336-341) folded into
  * the down product of one token. y = W v with v[j] = silu(gate[j]) * up[j],

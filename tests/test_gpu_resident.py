@@ -111,3 +111,16 @@ def test_decode_graph_replays_match_direct_launches(monkeypatch):
     assert g["kernel_launches"] == d["kernel_launches"] and g["external_matmul_calls"] == d["external_matmul_calls"]
     for i, (a, b) in enumerate(zip(graphed, direct)):
         assert np.array_equal(a, b), f"row {i}"
+
+
+def test_interleaved_gate_up_on_gpu(session_lib, rocm_env, tmp_path):
+    """gate|up above 64 rows per CU: the plan interleaves gate and up rows and
+    one-token runs form the gated SiLU in the product's epilogue
+    (nya_hip_matvec_swiglu), runs of several through nya_hip_silu_pairs."""
+    shape = LlamaShape(hidden=8704, context=24, types={"embedding": Q4_K, "output": Q6_K, "attention": Q4_K,
+                                                        "gate_up": Q4_K, "down": Q6_K})
+    path = tmp_path / "model.gguf"
+    write(path, shape)
+    out = compare(session_lib, path, shape, "rocm", [5, 17, 200, 3, 42, 99, 250, 1, 7, 64])
+    print(out["logit"], out["kv"], flush=True)
+    assert out["execution"] == "resident"

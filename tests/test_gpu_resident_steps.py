@@ -17,6 +17,9 @@ inputs:
   (8192) into the global-scratch path: within 1e-5 (1 + |ref|);
 - silu_mul (fused [gate | up] rows, separate blocks, in place for one
   token): within 2e-6 (1 + |ref|);
+- matvec_swiglu (a one-token gate|up product over 16-row-interleaved gate and
+  up rows with silu(g) * u as output) bit for bit nya_hip_matmul followed by
+  silu_pairs, and silu_pairs within 2e-6 (1 + |ref|) of float64;
 - matvec_gated (the gated SiLU folded into a one-token down product): bit
   for bit the output of silu_mul followed by nya_hip_matmul, for every
   quantized type at down-projection shapes (wide rows, chunked rows, a
@@ -47,6 +50,8 @@ def env():
     L.nya_hip_attention.argtypes = [_up, _sz, _up, _up, _up, _up, _up, _sz, _sz, _sz, _sz, _sz, _f, _up]
     L.nya_hip_silu_mul.argtypes = [_up, _sz, _up, _sz, _up, _sz, _sz, _up]
     L.nya_hip_matvec_gated.argtypes = [_up, _u, _sz, _sz, _up, _up, _up, _up]
+    L.nya_hip_matvec_swiglu.argtypes = [_up, _u, _sz, _sz, _up, _up, _up]
+    L.nya_hip_silu_pairs.argtypes = [_up, _up, _sz, _sz, _up]
     stream = rt.stream()
     yield rt, L, stream
     rt.sync(stream)
@@ -328,3 +333,37 @@ def test_matvec_gated_declines(env):
         assert L.nya_hip_matvec_gated(p, Q4_K, 64, 256, p + 4, p, p, stream) == 1     # gate not 16-byte aligned
     finally:
         dev.close()
+
+
+@pytest.mark.parametrize("rows,cols", [(28672, 4096), (17408, 256), (22528, 2048)])
+def test_matvec_swiglu_equals_two_steps(env, rows, cols):
+    rt, L, stream = env
+    kern = Kernels()
+    assert L.nya_hip_matvec_swiglu(0, Q4_K, rows, cols, 0, 0, stream) == 0
+    rng = np.random.default_rng(rows + cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    w = kern.device_weights(synth.weights(Q4_K, rows, cols, seed=rows), Q4_K, rows, cols)
+    dev = Dev(rt)
+    try:
+        wd, xd = dev.put(w), dev.put(x)
+        y, h1, h2 = dev.empty(4 * rows), dev.empty(2 * rows), dev.empty(2 * rows)
+        print(f"swiglu {rows}x{cols}", flush=True)
+        assert L.nya_hip_matvec_swiglu(wd, Q4_K, rows, cols, xd, h1, stream) == 0
+        kern.matmul(wd, Q4_K, rows, cols, xd, y, 1, 0, 0, stream)
+        assert L.nya_hip_silu_pairs(y, h2, rows // 2, 1, stream) == 0
+        rt.sync(stream)
+        a, b = dev.get(h1, np.empty(rows // 2, np.float32)), dev.get(h2, np.empty(rows // 2, np.float32))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        yv = dev.get(y, np.empty(rows, np.float32)).astype(np.float64).reshape(-1, 2, 16)
+        g, u = yv[:, 0, :].reshape(-1), yv[:, 1, :].reshape(-1)
+        assert scaled_error(b, g / (1 + np.exp(-g)) * u) <= 2e-6
+    finally:
+        dev.close()
+
+
+def test_matvec_swiglu_declines(env):
+    rt, L, stream = env
+    assert L.nya_hip_matvec_swiglu(0, Q4_K, 8192, 4096, 0, 0, stream) == 1     # 32 rows per CU: the row kernel
+    assert L.nya_hip_matvec_swiglu(0, Q6_K, 28672, 4096, 0, 0, stream) == 1    # not Q4_K
+    assert L.nya_hip_matvec_swiglu(0, Q4_K, 28672, 20480, 0, 0, stream) == 1   # more than one column chunk
+    assert L.nya_hip_matvec_swiglu(0, Q4_K, 28688, 4096, 0, 0, stream) == 1    # not whole 32-row blocks

@@ -90,3 +90,17 @@ def test_plan_without_gated_product(session_lib, tmp_path, monkeypatch):
         launches[name] = out["stats"].kernel_launches
     # compare() runs 6 decode tokens, then chunks (5, 1, 1, 7, 1): 9 one-token runs.
     assert launches["ungated"] - launches["gated"] == 9 * shape.blocks, launches
+
+
+def test_interleaved_gate_up(session_lib, tmp_path):
+    """A feed-forward wide enough for the library's one-token SwiGLU product
+    (gate|up above 64 rows per CU): the plan lays gate and up out in 16-row
+    blocks; one-token runs take nya_hip_matvec_swiglu (no separate SiLU
+    step), runs of several nya_hip_silu_pairs; logits and cache still match
+    the engine's reference session."""
+    shape = LlamaShape(hidden=8704, context=16, types={"embedding": Q4_K, "output": Q6_K, "attention": Q4_K,
+                                                        "gate_up": Q4_K, "down": Q6_K})
+    path = tmp_path / "model.gguf"
+    write(path, shape)
+    out = compare(session_lib, path, shape, "rocm", TOKENS[:6])
+    assert out["execution"] == "resident"

@@ -242,6 +242,20 @@ NYA_HIP_EXPORT int nya_hip_matvec_gated(uintptr_t w, unsigned type, size_t rows,
                                       (int)rows, (int)cols, (hipStream_t)stream));
 }
 
+NYA_HIP_EXPORT int nya_hip_matvec_normed(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
+    uintptr_t r, uintptr_t norm, float eps, uintptr_t hout, uintptr_t y, uintptr_t stream)
+{
+    size_t b;
+    if (!storage_bytes(type, rows, cols, &b) || !matvec_normed_supported(type, (int)rows, (int)cols)) return 1;
+    if (!w) return 0;   // the shape query
+    if (!x || !norm || !y || (r && !hout) || ((w | x | r | norm | hout) & 15u) || (y & 3u)) return 1;
+    if (r && hout < r + 4 * cols && r < hout + 4 * cols) return 1;
+    if (r && hout < x + 4 * cols && x < hout + 4 * cols) return 1;
+    return status(launch_matvec_normed(type, (const uint8_t *)w, (const float *)x, (const float *)r,
+                                       (const float *)norm, (float *)hout, eps, (float *)y, (int)rows, (int)cols,
+                                       (hipStream_t)stream));
+}
+
 NYA_HIP_EXPORT int nya_hip_matvec_swiglu(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
     uintptr_t hidden, uintptr_t stream)
 {

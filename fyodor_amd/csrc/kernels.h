@@ -35,6 +35,13 @@ bool matvec_gated_supported(unsigned type, int rows, int cols);
 // (gate rows, then their up rows) and silu(gate) * up as its output: Q4_K on
 // the one-workgroup-per-tile kernel (more than 64 rows per CU), one column
 // chunk.
+// One token's product of the decoder's normalized residual: h = x + r (r
+// may be null), xn = RMS-normalized h times g (the norm step's arithmetic and
+// order), y = W xn, and h written to hout by one workgroup. Up to 32 rows per
+// CU, cols up to 4096.
+bool matvec_normed_supported(unsigned type, int rows, int cols);
+hipError_t launch_matvec_normed(unsigned type, const uint8_t *w, const float *x, const float *r, const float *g,
+    float *hout, float eps, float *y, int rows, int cols, hipStream_t stream);
 bool matvec_swiglu_supported(unsigned type, int rows, int cols);
 hipError_t launch_matvec_swiglu(unsigned type, const uint8_t *w, const float *x, float *hidden, int rows, int cols,
     hipStream_t stream);

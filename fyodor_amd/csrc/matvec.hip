@@ -566,11 +566,60 @@ __device__ __forceinline__ void load_rows_fields(MvStage<T> (&w)[VT], __amdgpu_b
 
 // GATED: the vector multiplied is silu(x) * up elementwise (x and up of the
 // same chunk layout), formed as each group is loaded.
-template <unsigned T, int VT, int RING, int KS, int P, bool FULL, bool MULTI, bool GATED>
+// The residual add and RMS normalization of the decoder folded into the
+// x prologue (one group per wavefront, lane l of wavefront w holding
+// elements 4 (64 w + l) .. + 3, as thread 64 w + l of the norm step):
+// h = x + r (r may be null), xn = h * scale * g with
+// scale = 1 / sqrt(sum h^2 / cols + eps), the sum of squares in double in
+// the norm step's order; workgroup 0 writes h to hout.
+struct NormIn {
+    const float *r, *g;
+    float *hout;
+    float eps;
+};
+
+__device__ __forceinline__ double sq4(float4 h)
+{
+#pragma clang fp contract(off)
+    return (double)h.x * h.x + (double)h.y * h.y + (double)h.z * h.z + (double)h.w * h.w;
+}
+__device__ __forceinline__ float4 add4(float4 a, float4 b)
+{
+#pragma clang fp contract(off)
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+__device__ __forceinline__ float4 scale4(float4 h, float scale, float4 g)
+{
+#pragma clang fp contract(off)
+    return make_float4(h.x * scale * g.x, h.y * scale * g.y, h.z * scale * g.z, h.w * scale * g.w);
+}
+
+// One wavefront's share of the norm (its group in v, r and g loaded, zeros
+// for a wavefront without one): v becomes xn; `writer` (workgroup 0) stores
+// h. Every wavefront of the workgroup calls it once (one barrier).
+__device__ __forceinline__ void norm_group(float4 &v, float4 r, float4 g, const NormIn &nm, int cols, int lane,
+    int wave, bool writer, bool has_group)
+{
+    __shared__ double part[16];
+    const float4 h = nm.r ? add4(v, r) : v;
+    if (writer && has_group && nm.r) ((float4 *)nm.hout)[64 * wave + lane] = h;
+    double s = sq4(h);
+    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+    if (lane == 0) part[wave] = s;
+    __syncthreads();
+    double total = part[0];
+#pragma unroll
+    for (int q = 1; q < 16; ++q) total += part[q];
+    const float scale = (float)(1.0 / sqrt(total / (double)cols + (double)nm.eps));
+    v = scale4(h, scale, g);
+}
+
+template <unsigned T, int VT, int RING, int KS, int P, bool FULL, bool MULTI, bool GATED, bool NORM = false>
 __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, const float *__restrict__ x,
     const float *__restrict__ up, float *__restrict__ y, int rows, int cols, int base, int live, int g0c, int ngc,
-    int accumulate, uint8_t *sdig, float4 *smeta, float (*red)[VT][64])
+    int accumulate, uint8_t *sdig, float4 *smeta, float (*red)[VT][64], const NormIn &nm = NormIn{})
 {
+    static_assert(!NORM || (P == 1 && RING == 1 && KS == 16 && !MULTI && !GATED), "norm: one group per wavefront");
     static_assert(P == 1 || (P == 2 && VT == 1), "two groups per stage: one 16-row virtual tile");
     constexpr int RT = kTileRows / P;   // rows per virtual tile
     const int lane = threadIdx.x & 63;
@@ -642,12 +691,19 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
         if constexpr (GATED)
             pu[j] = __builtin_bit_cast(float4, bload16<false>(ub, 16 * lane + 1024 * (ns > 0 ? xgroup(j) : wave), 0));
     }
+    float4 pr = {}, pg = {};
+    if constexpr (NORM) {
+        const __amdgpu_buffer_rsrc_t rb = buffer_of(nm.r ? nm.r : x, nm.r ? xbytes : 0u), gb = buffer_of(nm.g, xbytes);
+        pr = __builtin_bit_cast(float4, bload16<false>(rb, 16 * lane + 1024 * wave, 0));
+        pg = __builtin_bit_cast(float4, bload16<false>(gb, 16 * lane + 1024 * wave, 0));
+    }
     asm volatile("" ::: "memory");
     if (ns > 0) {
         MvStage<T> st[RING][VT];
 #pragma unroll
         for (int k = 0; k < RING; ++k) stage_load(st[k], k);
 
+        if constexpr (NORM) norm_group(px[0], pr, pg, nm, cols, lane, wave, base == 0, xbytes > 0);
         // 2. Digits of this wave's groups into LDS.
         const float fmul = block_factor<T>(lane), fcorr = block_correction<T>(lane);
 #pragma unroll
@@ -694,6 +750,10 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
         pass(0);
         if constexpr (MULTI)
             for (int i = RING; i < nst; i += RING) pass(i);
+    } else if constexpr (NORM) {
+        // A wavefront without a group still meets the others at the norm's
+        // barrier (its sum is zero).
+        norm_group(px[0], pr, pg, nm, cols, lane, wave, false, false);
     }
 
     // 4. Lane halves and wavefronts, in a fixed order. Wave 0 sums: lane
@@ -742,6 +802,27 @@ __global__ __launch_bounds__(64 * KS) void matvec_rows(const uint8_t *__restrict
     else
         matvec_rows_body<T, VT, RING, KS, P, false, MULTI, GATED>(w, x, up, y, rows, cols, base, live, g0c, ngc,
                                                                  accumulate, sdig, smeta, red);
+}
+
+// One token's product of the normalized residual: matvec_rows with one
+// 256-column group per wavefront (cols <= 4096) and the norm in the x
+// prologue.
+template <unsigned T>
+__global__ __launch_bounds__(1024) void matvec_rows_norm(const uint8_t *__restrict__ w, const float *__restrict__ x,
+    float *__restrict__ y, int rows, int cols, int rw, NormIn nm)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ float red[16][1][64];
+    uint8_t *sdig = lds;
+    float4 *smeta = (float4 *)(lds + (size_t)128 * (cols / 32));
+    const int base = xcd_block() * rw, live = rows - base < rw ? rows - base : rw;
+    const int tiles = (rows + kTileRows - 1) / kTileRows, ngc = cols / kGroupCols;
+    if (rows % kTileRows == 0 || base + live <= kTileRows * (tiles - 1))
+        matvec_rows_body<T, 1, 1, 16, 1, true, false, false, true>(w, x, nullptr, y, rows, cols, base, live, 0, ngc, 0,
+                                                                  sdig, smeta, red, nm);
+    else
+        matvec_rows_body<T, 1, 1, 16, 1, false, false, false, true>(w, x, nullptr, y, rows, cols, base, live, 0, ngc, 0,
+                                                                   sdig, smeta, red, nm);
 }
 
 size_t matvec_lds(int ccols)
@@ -1442,6 +1523,30 @@ hipError_t launch_matvec(unsigned type, const uint8_t *w, const float *x, float 
 bool matvec_gated_supported(unsigned type, int rows, int cols)
 {
     return matvec_supported(type, rows, cols) && (type != Q4_K || rows_per_workgroup(rows) <= 2 * kTileRows);
+}
+
+bool matvec_normed_supported(unsigned type, int rows, int cols)
+{
+    return matvec_supported(type, rows, cols) && cols <= 16 * kGroupCols && rows_per_workgroup(rows) <= kTileRows;
+}
+
+hipError_t launch_matvec_normed(unsigned type, const uint8_t *w, const float *x, const float *r, const float *g,
+    float *hout, float eps, float *y, int rows, int cols, hipStream_t s)
+{
+    if (!matvec_normed_supported(type, rows, cols)) return hipErrorInvalidValue;
+    const int rw = rows_per_workgroup(rows), wgs = (rows + rw - 1) / rw;
+    const NormIn nm{r, g, hout, eps};
+    const size_t lds = matvec_lds(cols);
+#define FY_NORMED(TT) hipLaunchKernelGGL(matvec_rows_norm<TT>, dim3(wgs), dim3(1024), lds, s, w, x, y, rows, cols, rw, nm)
+    switch (type) {
+    case Q4_K: FY_NORMED(Q4_K); break;
+    case Q6_K: FY_NORMED(Q6_K); break;
+    case Q8_0: FY_NORMED(Q8_0); break;
+    case Q4_0: FY_NORMED(Q4_0); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef FY_NORMED
+    return hipGetLastError();
 }
 
 bool matvec_swiglu_supported(unsigned type, int rows, int cols)

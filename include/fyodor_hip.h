@@ -192,6 +192,22 @@ NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t key
 NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, size_t gate_stride, uintptr_t up, size_t up_stride,
     uintptr_t out, size_t n, size_t count, uintptr_t stream);
 
+/* No counterpart in the reference: one token's product of the decoder's
+ * normalized residual, nya_hip_rms_norm folded into the product that reads
+ * it. h = x + r (r = 0: h = x), xn = h * scale * norm with
+ * scale = 1 / sqrt(sum h^2 / cols + eps) (backend/core/llm_cpu.c:83-104, the
+ * sum in double in the norm step's order), y = W xn as nya_hip_matmul of one
+ * column; with r, h is written to hout (cols floats, overlapping neither x nor
+ * r: the norm step writes x in place, which this product cannot while its
+ * other workgroups read x). y and hout equal nya_hip_rms_norm followed by
+ * nya_hip_matmul bit for bit. For callers that run one decode token (the
+ * resident plan): one launch fewer per block. w == 0 queries the shape: 0
+ * where it runs (Q4_K, Q6_K, Q8_0, Q4_0 with cols a multiple of 256 up to
+ * 4096 and at most 32 rows per CU), else 1; then also 1 for missing or
+ * misaligned (16 bytes; y 4) vectors. */
+NYA_HIP_EXPORT int nya_hip_matvec_normed(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
+    uintptr_t r, uintptr_t norm, float eps, uintptr_t hout, uintptr_t y, uintptr_t stream);
+
 /* No counterpart in the reference: the gate|up product of one token with
  * the gated SiLU as its output. W (rows = 2 n, the library's layout) holds
  * the feed-forward gate and up rows interleaved in 16-row blocks: rows

@@ -17,6 +17,11 @@ inputs:
   (8192) into the global-scratch path: within 1e-5 (1 + |ref|);
 - silu_mul (fused [gate | up] rows, separate blocks, in place for one
   token): within 2e-6 (1 + |ref|);
+- matvec_normed (the residual add and RMS norm folded into a one-token
+  product): y and the updated residual bit for bit those of rms_norm
+  followed by nya_hip_matmul, with and without the residual add, for the
+  quantized types at q|k|v shapes; declined (1) past 32 rows per CU or 4096
+  columns;
 - matvec_swiglu (a one-token gate|up product over 16-row-interleaved gate and
   up rows with silu(g) * u as output) bit for bit nya_hip_matmul followed by
   silu_pairs, and silu_pairs within 2e-6 (1 + |ref|) of float64;
@@ -51,6 +56,7 @@ def env():
     L.nya_hip_silu_mul.argtypes = [_up, _sz, _up, _sz, _up, _sz, _sz, _up]
     L.nya_hip_matvec_gated.argtypes = [_up, _u, _sz, _sz, _up, _up, _up, _up]
     L.nya_hip_matvec_swiglu.argtypes = [_up, _u, _sz, _sz, _up, _up, _up]
+    L.nya_hip_matvec_normed.argtypes = [_up, _u, _sz, _sz, _up, _up, _up, _f, _up, _up, _up]
     L.nya_hip_silu_pairs.argtypes = [_up, _up, _sz, _sz, _up]
     stream = rt.stream()
     yield rt, L, stream
@@ -367,3 +373,42 @@ def test_matvec_swiglu_declines(env):
     assert L.nya_hip_matvec_swiglu(0, Q6_K, 28672, 4096, 0, 0, stream) == 1    # not Q4_K
     assert L.nya_hip_matvec_swiglu(0, Q4_K, 28672, 20480, 0, 0, stream) == 1   # more than one column chunk
     assert L.nya_hip_matvec_swiglu(0, Q4_K, 28688, 4096, 0, 0, stream) == 1    # not whole 32-row blocks
+
+
+@pytest.mark.parametrize("t,rows,cols,residual", [(Q4_K, 6144, 4096, True), (Q4_K, 6144, 4096, False),
+                                                  (Q6_K, 2560, 2048, True), (Q8_0, 1000, 4096, True),
+                                                  (Q4_0, 3000, 1024, True), (Q4_K, 8192, 256, True)])
+def test_matvec_normed_equals_two_steps(env, t, rows, cols, residual):
+    rt, L, stream = env
+    kern = Kernels()
+    assert L.nya_hip_matvec_normed(0, t, rows, cols, 0, 0, 0, 1e-5, 0, 0, stream) == 0
+    rng = np.random.default_rng(rows + cols)
+    x = (3 * rng.standard_normal(cols)).astype(np.float32)
+    r = rng.standard_normal(cols).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    w = kern.device_weights(synth.weights(t, rows, cols, seed=rows), t, rows, cols)
+    dev = Dev(rt)
+    try:
+        wd, x1, x2, rd, gd = dev.put(w), dev.put(x), dev.put(x), dev.put(r), dev.put(g)
+        hout, xn = dev.empty(4 * cols), dev.empty(4 * cols)
+        y1, y2 = dev.empty(4 * rows), dev.empty(4 * rows)
+        print(f"normed {t} {rows}x{cols} residual {residual}", flush=True)
+        assert L.nya_hip_matvec_normed(wd, t, rows, cols, x1, rd if residual else 0, gd, 1e-5,
+                                       hout if residual else 0, y1, stream) == 0
+        assert L.nya_hip_rms_norm(x2, rd if residual else 0, gd, xn, cols, 1, 1e-5, stream) == 0
+        kern.matmul(wd, t, rows, cols, xn, y2, 1, 0, 0, stream)
+        rt.sync(stream)
+        bits = lambda p, n: dev.get(p, np.empty(n, np.float32)).view(np.uint32)
+        assert np.array_equal(bits(y1, rows), bits(y2, rows))
+        if residual:
+            assert np.array_equal(bits(hout, cols), bits(x2, cols))   # the norm step's in-place residual
+        assert np.array_equal(bits(x1, cols), x.view(np.uint32))      # x itself untouched
+    finally:
+        dev.close()
+
+
+def test_matvec_normed_declines(env):
+    rt, L, stream = env
+    assert L.nya_hip_matvec_normed(0, Q4_K, 14336, 4096, 0, 0, 0, 1e-5, 0, 0, stream) == 1   # 56 rows per CU
+    assert L.nya_hip_matvec_normed(0, Q4_K, 4096, 8192, 0, 0, 0, 1e-5, 0, 0, stream) == 1    # 8192 columns
+    assert L.nya_hip_matvec_normed(0, F16, 4096, 4096, 0, 0, 0, 1e-5, 0, 0, stream) == 1     # dense type

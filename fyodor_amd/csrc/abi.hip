@@ -358,6 +358,29 @@ NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t key
                                    (int)kv_heads, (int)width, (int)max_length, scale, (hipStream_t)stream));
 }
 
+NYA_HIP_EXPORT int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
+    uintptr_t r, uintptr_t norm, float eps, uintptr_t hout, uintptr_t y, uintptr_t positions, uintptr_t frequencies,
+    size_t heads, size_t kv_heads, size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream)
+{
+    size_t b;
+    if (!storage_bytes(type, rows, cols, &b) || !matvec_normed_rope_supported(type, (int)rows, (int)cols)) return 1;
+    if (!w) return 0;   // the shape query
+    if (!count_ok(heads) || !count_ok(kv_heads) || !count_ok(width) || width % 2 || !count_ok(capacity) ||
+        heads > (size_t)INT_MAX / width || kv_heads > (size_t)INT_MAX / width ||
+        rows != (heads + 2 * kv_heads) * width)
+        return 1;
+    if (!x || !norm || !y || (r && !hout) || !vec(positions) || !vec(frequencies) || !vec(keys) || !vec(values) ||
+        ((w | x | r | norm | hout) & 15u) || (y & 3u))
+        return 1;
+    if (r && hout < r + 4 * cols && r < hout + 4 * cols) return 1;
+    if (r && hout < x + 4 * cols && x < hout + 4 * cols) return 1;
+    return status(launch_matvec_normed_rope(type, (const uint8_t *)w, (const float *)x, (const float *)r,
+                                            (const float *)norm, (float *)hout, eps, (float *)y, (int)rows, (int)cols,
+                                            (const int *)positions, (const float *)frequencies, (float *)keys,
+                                            (float *)values, (int)(heads * width), (int)(kv_heads * width), (int)width,
+                                            (int)capacity, (hipStream_t)stream));
+}
+
 NYA_HIP_EXPORT int nya_hip_greedy(uintptr_t logits, size_t n, size_t count, uintptr_t mask, uintptr_t ids,
     uintptr_t stream)
 {

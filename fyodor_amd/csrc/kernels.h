@@ -42,6 +42,13 @@ bool matvec_gated_supported(unsigned type, int rows, int cols);
 bool matvec_normed_supported(unsigned type, int rows, int cols);
 hipError_t launch_matvec_normed(unsigned type, const uint8_t *w, const float *x, const float *r, const float *g,
     float *hout, float eps, float *y, int rows, int cols, hipStream_t stream);
+// The same over the q|k|v rows with rope_qkv's rotary step in its epilogue:
+// y as rope_qkv leaves it (q rotated), k and v into the cache slot of
+// positions[0]. Rows per CU even.
+bool matvec_normed_rope_supported(unsigned type, int rows, int cols);
+hipError_t launch_matvec_normed_rope(unsigned type, const uint8_t *w, const float *x, const float *r, const float *g,
+    float *hout, float eps, float *y, int rows, int cols, const int *positions, const float *freq, float *keys,
+    float *values, int qd, int kvd, int width, int capacity, hipStream_t stream);
 bool matvec_swiglu_supported(unsigned type, int rows, int cols);
 hipError_t launch_matvec_swiglu(unsigned type, const uint8_t *w, const float *x, float *hidden, int rows, int cols,
     hipStream_t stream);

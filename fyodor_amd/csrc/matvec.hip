@@ -576,7 +576,23 @@ struct NormIn {
     const float *r, *g;
     float *hout;
     float eps;
+    // Rotary step of the q|k|v rows (positions null: none): q rows [0, qd)
+    // rotated in y, k rows [qd, qd + kvd) rotated into keys and v rows into
+    // values at the position's slot, as rope_qkv does.
+    const int *positions;
+    const float *freq;
+    float *keys, *values;
+    int qd, kvd, width, capacity;
 };
+
+// Element e of pair (e & ~1, e | 1) turned by `angle` as rope_qkv turns it:
+// mine is the element's value, other its partner's.
+__device__ __forceinline__ float rotate_element(float mine, float other, bool odd, float angle)
+{
+#pragma clang fp contract(off)
+    const float c = cosf(angle), s = sinf(angle);
+    return odd ? other * s + mine * c : mine * c - other * s;
+}
 
 __device__ __forceinline__ double sq4(float4 h)
 {
@@ -614,11 +630,22 @@ __device__ __forceinline__ void norm_group(float4 &v, float4 r, float4 g, const 
     v = scale4(h, scale, g);
 }
 
-template <unsigned T, int VT, int RING, int KS, int P, bool FULL, bool MULTI, bool GATED, bool NORM = false>
+template <unsigned T, int VT, int RING, int KS, int P, bool FULL, bool MULTI, bool GATED, bool NORM = false,
+    bool ROPE = false>
 __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, const float *__restrict__ x,
     const float *__restrict__ up, float *__restrict__ y, int rows, int cols, int base, int live, int g0c, int ngc,
     int accumulate, uint8_t *sdig, float4 *smeta, float (*red)[VT][64], const NormIn &nm = NormIn{})
 {
+    static_assert(!ROPE || (NORM && VT == 1), "rotary: the normed one-tile product");
+    // The rotary inputs, loaded first (used after the reduction).
+    int rope_position = 0;
+    float rope_freq = 0.f;
+    if constexpr (ROPE) {
+        rope_position = nm.positions[0];
+        const int row = base + (int)(threadIdx.x & 63);
+        const int e = row < nm.qd ? row : row - nm.qd;
+        rope_freq = row < nm.qd + nm.kvd ? nm.freq[(e % nm.width) >> 1] : 0.f;
+    }
     static_assert(!NORM || (P == 1 && RING == 1 && KS == 16 && !MULTI && !GATED), "norm: one group per wavefront");
     static_assert(P == 1 || (P == 2 && VT == 1), "two groups per stage: one 16-row virtual tile");
     constexpr int RT = kTileRows / P;   // rows per virtual tile
@@ -780,6 +807,27 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
 #pragma unroll
     for (int q = 1; q < KS; ++q) sum += p[2 * q] + p[2 * q + 1];
     float *dst = y + base + RT * v + r;
+    if constexpr (ROPE) {
+        // Rows come in pairs within the workgroup (base and live even).
+        const float other = __shfl_xor(sum, 1, 64);
+        const int row = base + r, position = rope_position;
+        if (position >= 0 && position < nm.capacity) {
+            const bool is_q = row < nm.qd, is_k = !is_q && row < nm.qd + nm.kvd;
+            const int e = is_q ? row : row - nm.qd;
+            if (is_q || is_k) {
+                const float out = rotate_element(sum, other, e & 1, (float)position * rope_freq);
+                if (is_q) {
+                    *dst = out;
+                    return;
+                }
+                nm.keys[(size_t)position * nm.kvd + e] = out;
+            } else {
+                nm.values[(size_t)position * nm.kvd + (row - nm.qd - nm.kvd)] = sum;
+            }
+        }
+        *dst = sum;
+        return;
+    }
     *dst = accumulate ? *dst + sum : sum;
 }
 
@@ -807,7 +855,7 @@ __global__ __launch_bounds__(64 * KS) void matvec_rows(const uint8_t *__restrict
 // One token's product of the normalized residual: matvec_rows with one
 // 256-column group per wavefront (cols <= 4096) and the norm in the x
 // prologue.
-template <unsigned T>
+template <unsigned T, bool ROPE = false>
 __global__ __launch_bounds__(1024) void matvec_rows_norm(const uint8_t *__restrict__ w, const float *__restrict__ x,
     float *__restrict__ y, int rows, int cols, int rw, NormIn nm)
 {
@@ -818,11 +866,11 @@ __global__ __launch_bounds__(1024) void matvec_rows_norm(const uint8_t *__restri
     const int base = xcd_block() * rw, live = rows - base < rw ? rows - base : rw;
     const int tiles = (rows + kTileRows - 1) / kTileRows, ngc = cols / kGroupCols;
     if (rows % kTileRows == 0 || base + live <= kTileRows * (tiles - 1))
-        matvec_rows_body<T, 1, 1, 16, 1, true, false, false, true>(w, x, nullptr, y, rows, cols, base, live, 0, ngc, 0,
-                                                                  sdig, smeta, red, nm);
+        matvec_rows_body<T, 1, 1, 16, 1, true, false, false, true, ROPE>(w, x, nullptr, y, rows, cols, base, live, 0,
+                                                                        ngc, 0, sdig, smeta, red, nm);
     else
-        matvec_rows_body<T, 1, 1, 16, 1, false, false, false, true>(w, x, nullptr, y, rows, cols, base, live, 0, ngc, 0,
-                                                                   sdig, smeta, red, nm);
+        matvec_rows_body<T, 1, 1, 16, 1, false, false, false, true, ROPE>(w, x, nullptr, y, rows, cols, base, live, 0,
+                                                                         ngc, 0, sdig, smeta, red, nm);
 }
 
 size_t matvec_lds(int ccols)
@@ -1530,12 +1578,38 @@ bool matvec_normed_supported(unsigned type, int rows, int cols)
     return matvec_supported(type, rows, cols) && cols <= 16 * kGroupCols && rows_per_workgroup(rows) <= kTileRows;
 }
 
+bool matvec_normed_rope_supported(unsigned type, int rows, int cols)
+{
+    return matvec_normed_supported(type, rows, cols) && rows % 2 == 0 && rows_per_workgroup(rows) % 2 == 0;
+}
+
+hipError_t launch_matvec_normed_rope(unsigned type, const uint8_t *w, const float *x, const float *r, const float *g,
+    float *hout, float eps, float *y, int rows, int cols, const int *positions, const float *freq, float *keys,
+    float *values, int qd, int kvd, int width, int capacity, hipStream_t s)
+{
+    if (!matvec_normed_rope_supported(type, rows, cols)) return hipErrorInvalidValue;
+    const int rw = rows_per_workgroup(rows), wgs = (rows + rw - 1) / rw;
+    const NormIn nm{r, g, hout, eps, positions, freq, keys, values, qd, kvd, width, capacity};
+    const size_t lds = matvec_lds(cols);
+#define FY_NORMED(TT) \
+    hipLaunchKernelGGL((matvec_rows_norm<TT, true>), dim3(wgs), dim3(1024), lds, s, w, x, y, rows, cols, rw, nm)
+    switch (type) {
+    case Q4_K: FY_NORMED(Q4_K); break;
+    case Q6_K: FY_NORMED(Q6_K); break;
+    case Q8_0: FY_NORMED(Q8_0); break;
+    case Q4_0: FY_NORMED(Q4_0); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef FY_NORMED
+    return hipGetLastError();
+}
+
 hipError_t launch_matvec_normed(unsigned type, const uint8_t *w, const float *x, const float *r, const float *g,
     float *hout, float eps, float *y, int rows, int cols, hipStream_t s)
 {
     if (!matvec_normed_supported(type, rows, cols)) return hipErrorInvalidValue;
     const int rw = rows_per_workgroup(rows), wgs = (rows + rw - 1) / rw;
-    const NormIn nm{r, g, hout, eps};
+    const NormIn nm{r, g, hout, eps, nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0};
     const size_t lds = matvec_lds(cols);
 #define FY_NORMED(TT) hipLaunchKernelGGL(matvec_rows_norm<TT>, dim3(wgs), dim3(1024), lds, s, w, x, y, rows, cols, rw, nm)
     switch (type) {

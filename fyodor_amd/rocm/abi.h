@@ -66,6 +66,9 @@ typedef struct nya_resident_ops {
     /* Optional: NULL leaves the attention norm a step of its own. */
     int (*matvec_normed)(uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t, uintptr_t, float, uintptr_t,
         uintptr_t, uintptr_t);
+    /* Optional: NULL leaves the rotary step a launch of its own. */
+    int (*matvec_normed_rope)(uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t, uintptr_t, float, uintptr_t,
+        uintptr_t, uintptr_t, uintptr_t, size_t, size_t, size_t, size_t, uintptr_t, uintptr_t, uintptr_t);
     /* Optional as a pair: NULL keeps gate and up in two blocks of rows. */
     int (*matvec_swiglu)(uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t, uintptr_t);
     int (*silu_pairs)(uintptr_t, uintptr_t, size_t, size_t, uintptr_t);

@@ -208,6 +208,20 @@ NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, size_t gate_stride, uintptr_
 NYA_HIP_EXPORT int nya_hip_matvec_normed(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
     uintptr_t r, uintptr_t norm, float eps, uintptr_t hout, uintptr_t y, uintptr_t stream);
 
+/* No counterpart in the reference: nya_hip_matvec_normed of the q|k|v rows
+ * (rows = (heads + 2 kv_heads) width: q, then k, then v) with
+ * nya_hip_rope_qkv's rotary step of one token in its epilogue (frequencies,
+ * positions, capacity, keys and values as there): y is left as the two
+ * steps leave it (q rows rotated, k and v rows as produced) and the key and
+ * value rows go into the cache slot of positions[0], bit for bit, for a
+ * position in [0, capacity); outside it nothing is rotated or stored, as
+ * there. One launch for the attention norm, the q|k|v product and the
+ * rotary step of a decode token. w == 0 queries the shape: as
+ * nya_hip_matvec_normed, with rows and rows per CU even. */
+NYA_HIP_EXPORT int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
+    uintptr_t r, uintptr_t norm, float eps, uintptr_t hout, uintptr_t y, uintptr_t positions, uintptr_t frequencies,
+    size_t heads, size_t kv_heads, size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream);
+
 /* No counterpart in the reference: the gate|up product of one token with
  * the gated SiLU as its output. W (rows = 2 n, the library's layout) holds
  * the feed-forward gate and up rows interleaved in 16-row blocks: rows

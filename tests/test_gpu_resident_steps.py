@@ -22,6 +22,9 @@ inputs:
   followed by nya_hip_matmul, with and without the residual add, for the
   quantized types at q|k|v shapes; declined (1) past 32 rows per CU or 4096
   columns;
+- matvec_normed_rope (the same with rope_qkv in its epilogue): y and the
+  whole key / value cache bit for bit matvec_normed followed by rope_qkv,
+  for a position inside the cache and one past it;
 - matvec_swiglu (a one-token gate|up product over 16-row-interleaved gate and
   up rows with silu(g) * u as output) bit for bit nya_hip_matmul followed by
   silu_pairs, and silu_pairs within 2e-6 (1 + |ref|) of float64;
@@ -57,6 +60,8 @@ def env():
     L.nya_hip_matvec_gated.argtypes = [_up, _u, _sz, _sz, _up, _up, _up, _up]
     L.nya_hip_matvec_swiglu.argtypes = [_up, _u, _sz, _sz, _up, _up, _up]
     L.nya_hip_matvec_normed.argtypes = [_up, _u, _sz, _sz, _up, _up, _up, _f, _up, _up, _up]
+    L.nya_hip_matvec_normed_rope.argtypes = [_up, _u, _sz, _sz, _up, _up, _up, _f, _up, _up, _up, _up, _sz, _sz, _sz,
+                                             _sz, _up, _up, _up]
     L.nya_hip_silu_pairs.argtypes = [_up, _up, _sz, _sz, _up]
     stream = rt.stream()
     yield rt, L, stream
@@ -412,3 +417,42 @@ def test_matvec_normed_declines(env):
     assert L.nya_hip_matvec_normed(0, Q4_K, 14336, 4096, 0, 0, 0, 1e-5, 0, 0, stream) == 1   # 56 rows per CU
     assert L.nya_hip_matvec_normed(0, Q4_K, 4096, 8192, 0, 0, 0, 1e-5, 0, 0, stream) == 1    # 8192 columns
     assert L.nya_hip_matvec_normed(0, F16, 4096, 4096, 0, 0, 0, 1e-5, 0, 0, stream) == 1     # dense type
+
+
+@pytest.mark.parametrize("heads,kv_heads,width,position", [(32, 8, 128, 37), (32, 8, 128, 0), (32, 4, 64, 300),
+                                                           (32, 8, 128, 512)])
+def test_matvec_normed_rope_equals_two_steps(env, heads, kv_heads, width, position):
+    rt, L, stream = env
+    kern = Kernels()
+    cols, capacity = 4096, 512
+    qd, kvd = heads * width, kv_heads * width
+    rows = qd + 2 * kvd
+    assert L.nya_hip_matvec_normed_rope(0, Q4_K, rows, cols, 0, 0, 0, 1e-5, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, stream) == 0
+    rng = np.random.default_rng(rows + position)
+    x = (3 * rng.standard_normal(cols)).astype(np.float32)
+    r = rng.standard_normal(cols).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    cache_k = rng.standard_normal((capacity, kvd)).astype(np.float32)
+    cache_v = rng.standard_normal((capacity, kvd)).astype(np.float32)
+    freq = (10000.0 ** (-np.arange(width // 2) * 2.0 / width)).astype(np.float32)
+    w = kern.device_weights(synth.weights(Q4_K, rows, cols, seed=rows), Q4_K, rows, cols)
+    dev = Dev(rt)
+    try:
+        wd, xd, rd, gd = dev.put(w), dev.put(x), dev.put(r), dev.put(g)
+        k1, v1, k2, v2 = dev.put(cache_k), dev.put(cache_v), dev.put(cache_k), dev.put(cache_v)
+        fd, pd = dev.put(freq), dev.put(np.array([position], np.int32))
+        h1, h2, y1, y2 = dev.empty(4 * cols), dev.empty(4 * cols), dev.empty(4 * rows), dev.empty(4 * rows)
+        print(f"normed_rope {heads}/{kv_heads} width {width} position {position}", flush=True)
+        assert L.nya_hip_matvec_normed_rope(wd, Q4_K, rows, cols, xd, rd, gd, 1e-5, h1, y1, pd, fd, heads, kv_heads,
+                                            width, capacity, k1, v1, stream) == 0
+        assert L.nya_hip_matvec_normed(wd, Q4_K, rows, cols, xd, rd, gd, 1e-5, h2, y2, stream) == 0
+        assert L.nya_hip_rope_qkv(y2, rows, y2 + 4 * qd, rows, y2 + 4 * (qd + kvd), rows, 1, heads, kv_heads, width,
+                                  fd, pd, capacity, k2, v2, stream) == 0
+        rt.sync(stream)
+        bits = lambda p, like: dev.get(p, like).view(np.uint32)
+        assert np.array_equal(bits(y1, np.empty(rows, np.float32)), bits(y2, np.empty(rows, np.float32)))
+        assert np.array_equal(bits(k1, cache_k), bits(k2, cache_k))
+        assert np.array_equal(bits(v1, cache_v), bits(v2, cache_v))
+        assert np.array_equal(bits(h1, np.empty(cols, np.float32)), bits(h2, np.empty(cols, np.float32)))
+    finally:
+        dev.close()

@@ -66,20 +66,23 @@ def test_plan_declined_without_resident_steps(session_lib, tmp_path, monkeypatch
     assert out["execution"] == "cpu-reference"
 
 
-@pytest.mark.parametrize("entry", ["nya_hip_matvec_gated", "nya_hip_matvec_normed"])
-def test_plan_without_fused_step(session_lib, tmp_path, monkeypatch, entry):
+@pytest.mark.parametrize("entries,extra", [(("nya_hip_matvec_gated",), 1), (("nya_hip_matvec_normed_rope",), 1),
+                                           (("nya_hip_matvec_normed", "nya_hip_matvec_normed_rope"), 2)])
+def test_plan_without_fused_step(session_lib, tmp_path, monkeypatch, entries, extra):
     """A kernel library without one of the optional one-token fusions
     (nya_hip_matvec_gated: the gated SiLU in the down product;
-    nya_hip_matvec_normed: the attention norm in the q|k|v product) keeps the
-    resident plan: the step runs apart, with one more launch per block and
-    decode token."""
+    nya_hip_matvec_normed: the attention norm in the q|k|v product;
+    nya_hip_matvec_normed_rope: the rotary step in its epilogue) keeps the
+    resident plan: the steps run apart, with `extra` more launches per block
+    and decode token."""
     lib_dir = tmp_path / "mock"
     lib_dir.mkdir()
     plain = lib_dir / "libnya_mock_ungated.so"
     from conftest import REPO
     src = [str(REPO / "tests/mock/mock_hip.c"), str(REPO / "oracle/quant_oracle.c")]
     subprocess.run(["gcc", "-std=c17", "-O1", "-fPIC", "-shared", "-D_POSIX_C_SOURCE=200809L",
-                    f"-D{entry}=nya_mock_unused_{entry}", *src, "-o", str(plain), "-lm", "-lpthread"], check=True)
+                    *[f"-D{e}=nya_mock_unused_{e}" for e in entries], *src, "-o", str(plain), "-lm", "-lpthread"],
+                   check=True)
     shape = LlamaShape(context=16)
     path = tmp_path / "model.gguf"
     write(path, shape)
@@ -91,7 +94,7 @@ def test_plan_without_fused_step(session_lib, tmp_path, monkeypatch, entry):
         assert out["execution"] == "resident"
         launches[name] = out["stats"].kernel_launches
     # compare() runs 6 decode tokens, then chunks (5, 1, 1, 7, 1): 9 one-token runs.
-    assert launches["unfused"] - launches["fused"] == 9 * shape.blocks, launches
+    assert launches["unfused"] - launches["fused"] == 9 * extra * shape.blocks, launches
 
 
 def test_interleaved_gate_up(session_lib, tmp_path):

@@ -31,10 +31,6 @@ hipError_t launch_matvec(unsigned type, const uint8_t *w, const float *x, float 
 // product. Shapes that run on the row-balanced kernel only (up to two tiles
 // per CU for Q4_K); gate and up 16-byte aligned.
 bool matvec_gated_supported(unsigned type, int rows, int cols);
-// The gate|up product of one token with rows interleaved in 16-row blocks
-// (gate rows, then their up rows) and silu(gate) * up as its output: Q4_K on
-// the one-workgroup-per-tile kernel (more than 64 rows per CU), one column
-// chunk.
 // One token's product of the decoder's normalized residual: h = x + r (r
 // may be null), xn = RMS-normalized h times g (the norm step's arithmetic and
 // order), y = W xn, and h written to hout by one workgroup. Up to 32 rows per
@@ -49,6 +45,10 @@ bool matvec_normed_rope_supported(unsigned type, int rows, int cols);
 hipError_t launch_matvec_normed_rope(unsigned type, const uint8_t *w, const float *x, const float *r, const float *g,
     float *hout, float eps, float *y, int rows, int cols, const int *positions, const float *freq, float *keys,
     float *values, int qd, int kvd, int width, int capacity, hipStream_t stream);
+// The gate|up product of one token with rows interleaved in 16-row blocks
+// (gate rows, then their up rows) and silu(gate) * up as its output: Q4_K on
+// the one-workgroup-per-tile kernel (more than 32 rows per CU), one column
+// chunk.
 bool matvec_swiglu_supported(unsigned type, int rows, int cols);
 hipError_t launch_matvec_swiglu(unsigned type, const uint8_t *w, const float *x, float *hidden, int rows, int cols,
     hipStream_t stream);

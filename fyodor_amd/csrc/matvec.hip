@@ -1626,7 +1626,7 @@ hipError_t launch_matvec_normed(unsigned type, const uint8_t *w, const float *x,
 bool matvec_swiglu_supported(unsigned type, int rows, int cols)
 {
     return type == Q4_K && rows % (2 * 16) == 0 && cols % kGroupCols == 0 && cols <= kChunkCols &&
-           rows_per_workgroup(rows) > 2 * kTileRows;
+           rows_per_workgroup(rows) > kTileRows;
 }
 
 hipError_t launch_matvec_swiglu(unsigned type, const uint8_t *w, const float *x, float *hidden, int rows, int cols,

@@ -232,7 +232,7 @@ NYA_HIP_EXPORT int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t
  * each SiLU is formed once. For callers that lay out the matrix so (the
  * resident plan): one launch and one pass over the products fewer per block.
  * w == 0 queries the shape: 0 where it runs, 1 where it does not (Q4_K only,
- * rows a multiple of 32 and more than 64 per CU, cols a multiple of 256 up to
+ * rows a multiple of 32 and more than 32 per CU, cols a multiple of 256 up to
  * 16384); then also 1 for x or hidden missing or misaligned. */
 NYA_HIP_EXPORT int nya_hip_matvec_swiglu(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
     uintptr_t hidden, uintptr_t stream);

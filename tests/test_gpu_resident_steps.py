@@ -346,7 +346,7 @@ def test_matvec_gated_declines(env):
         dev.close()
 
 
-@pytest.mark.parametrize("rows,cols", [(28672, 4096), (17408, 256), (22528, 2048)])
+@pytest.mark.parametrize("rows,cols", [(28672, 4096), (17408, 256), (22528, 2048), (11264, 2048)])
 def test_matvec_swiglu_equals_two_steps(env, rows, cols):
     rt, L, stream = env
     kern = Kernels()

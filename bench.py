@@ -68,19 +68,110 @@ PREFILL_TOKENS = 512
 MALL_BYTES = 256 * 1024 * 1024
 
 
-TRAFFIC_PROFILE = REPO / "profiles" / "q4k_matvec_14336x4096_traffic.md"
+TRAFFIC_COUNTERS = ("FETCH_SIZE", "WRITE_SIZE")
+CALIBRATION_BYTES = 256 << 20
+PROBE_LAUNCHES = 40
 
 
-def measured_traffic(batch: int):
-    """HBM bytes per launch from the committed rocprofv3 counter summary
-    (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of known size), or None."""
-    try:
-        for line in TRAFFIC_PROFILE.read_text().splitlines():
-            if line.startswith(f"traffic_n{batch}_bytes:"):
-                return int(line.split(":")[1])
-    except OSError:
-        pass
-    return None
+def traffic_probe() -> int:
+    """The launches the traffic counters are read on (run under rocprofv3 by
+    measure_traffic): a 256 MiB copy of known read and write bytes, then the
+    benchmark's N=1 and N=8 matvecs and the plain read, each over the same
+    rotating weight copies as the timed steps."""
+    rt, kern = Runtime(), Kernels()
+    stream = rt.stream()
+    src, dst = rt.malloc(CALIBRATION_BYTES), rt.malloc(CALIBRATION_BYTES)
+    for _ in range(3):
+        kern.copy(dst, src, CALIBRATION_BYTES, stream)
+    rt.sync(stream)
+    rt.free(src)
+    rt.free(dst)
+    wbytes = storage_bytes(Q4_K, ROWS, COLS)
+    copies = max(2, math.ceil(2 * MALL_BYTES / wbytes) + 2)
+    dev_w = kern.device_weights(synth.weights(Q4_K, ROWS, COLS, seed=1234), Q4_K, ROWS, COLS)
+    weights = []
+    for _ in range(copies):
+        p = rt.malloc(wbytes)
+        rt.upload(p, dev_w)
+        weights.append(p)
+    x8 = synth.activations(8, COLS, seed=1234)
+    x_dev, y_dev, sink = rt.malloc(x8.nbytes), rt.malloc(8 * ROWS * 4), rt.malloc(4096)
+    rt.upload(x_dev, x8)
+    for batch in (1, 8):
+        for i in range(PROBE_LAUNCHES):
+            kern.matmul(weights[i % copies], Q4_K, ROWS, COLS, x_dev, y_dev, batch, 0, 0, stream)
+    for i in range(PROBE_LAUNCHES):
+        kern.read(weights[i % copies], wbytes, sink, stream)
+    rt.sync(stream)
+    print(json.dumps({"copy": "copy16", "n1": kern.kernel_name(Q4_K, ROWS, COLS, 1),
+                      "n8": kern.kernel_name(Q4_K, ROWS, COLS, 8), "read": "read16"}), flush=True)
+    return 0
+
+
+def measure_traffic(timeout_s: float = 120.0) -> dict:
+    """HBM bytes per launch, measured in this run: one rocprofv3 pass per
+    counter (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) over
+    traffic_probe() in a child process, each scaled by what it reads on the
+    256 MiB copy (FETCH_SIZE counts half the bytes on gfx950). Run before this
+    process touches the GPU. Returns {"n1": bytes, "n8": bytes, "read": bytes,
+    ...} or {"error": why}."""
+    import csv
+    import shutil
+    import signal
+    import statistics
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3")
+    if not prof:
+        return {"error": "rocprofv3 not found"}
+    medians, kern_names = {}, None
+    for counter in TRAFFIC_COUNTERS:
+        out_dir = tempfile.mkdtemp(prefix="fy_traffic_", dir="/tmp")
+        cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", out_dir, "-o", "run", "--",
+               sys.executable, str(REPO / "bench.py"), "--traffic-probe"]
+        env = dict(os.environ, TMPDIR="/tmp")
+        proc = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                                start_new_session=True)
+        try:
+            out_text, err = proc.communicate(timeout=timeout_s)
+        except subprocess.TimeoutExpired:
+            os.killpg(proc.pid, signal.SIGKILL)
+            proc.wait()
+            shutil.rmtree(out_dir, ignore_errors=True)
+            return {"error": f"rocprofv3 --pmc {counter} did not finish in {timeout_s:.0f} s"}
+        rows = []
+        for path in Path(out_dir).rglob("*counter_collection.csv"):
+            with open(path) as f:
+                rows += list(csv.DictReader(f))
+        shutil.rmtree(out_dir, ignore_errors=True)
+        if not rows:
+            tail = err.decode(errors="replace").strip().splitlines()[-1:] if err else []
+            return {"error": f"rocprofv3 --pmc {counter} exited {proc.returncode} without counters {tail}"}
+        if kern_names is None:
+            names = [l for l in out_text.decode(errors="replace").splitlines() if l.startswith("{")]
+            if not names:
+                return {"error": f"rocprofv3 --pmc {counter}: the probe printed no kernel names"}
+            kern_names = json.loads(names[-1])
+        per_kernel = {}
+        for r in rows:
+            if r.get("Counter_Name") == counter:
+                per_kernel.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        for key, pattern in kern_names.items():
+            vals = [v for name, vs in per_kernel.items()
+                    if pattern in name.replace("(anonymous namespace)", "").split("(")[0] for v in vs]
+            if not vals:
+                return {"error": f"no {counter} dispatches of {pattern}"}
+            medians[(key, counter)] = statistics.median(vals) * 1024.0
+    fetch_scale = CALIBRATION_BYTES / medians[("copy", "FETCH_SIZE")]
+    write_scale = CALIBRATION_BYTES / medians[("copy", "WRITE_SIZE")]
+    out = {key: int(round(medians[(key, "FETCH_SIZE")] * fetch_scale + medians[(key, "WRITE_SIZE")] * write_scale))
+           for key in kern_names if key != "copy"}
+    out["scale"] = {"FETCH_SIZE": round(fetch_scale, 5), "WRITE_SIZE": round(write_scale, 5)}
+    out["source"] = ("median per dispatch of rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE (separate child runs "
+                     f"of bench.py --traffic-probe, {PROBE_LAUNCHES} launches each over the rotating copies), "
+                     f"scaled by the counters on a {CALIBRATION_BYTES >> 20} MiB copy")
+    return out
 
 
 def device(rt) -> str:
@@ -159,7 +250,7 @@ def time_steps(rt, kern, stream, settle, weights, x_dev, y_dev, batch, steps, wa
     return time_launches(rt, stream, settle, launch, steps, warmup, mode, [(p, wbytes) for p in weights])
 
 
-def read_ceiling(rt, kern, stream, settle, weights, steps, warmup, mode, matvec_ms) -> dict:
+def read_ceiling(rt, kern, stream, settle, weights, steps, warmup, mode, matvec_ms, shapes=True, sizes=True) -> dict:
     """The plain streaming read of the same weight bytes, same rotation and
     launch method as the timed matvec steps."""
     wbytes = storage_bytes(Q4_K, ROWS, COLS)
@@ -170,10 +261,80 @@ def read_ceiling(rt, kern, stream, settle, weights, steps, warmup, mode, matvec_
         kern.read(weights[i % copies], wbytes, sink, stream)
 
     ms = time_launches(rt, stream, settle, launch, steps, warmup, mode, [(p, wbytes) for p in weights])
+    out = {"kernel": "read16 (nya_hip_read)", "bytes": wbytes, "us_per_step": round(ms * 1e3, 3),
+           "GBps": round(wbytes / (ms * 1e-3) / 1e9, 2), "frac": round(wbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+           "matvec_over_read": round(matvec_ms / ms, 4)}
+    if shapes:
+        out["structures"] = read_structures(rt, kern, stream, settle, weights, wbytes, sink)
+    if sizes:
+        best = out.get("structures", {}).get("best")
+        out["sizes"] = read_sizes(rt, kern, stream, settle, weights[0], wbytes, sink, best)
     rt.free(sink)
-    return {"kernel": "read16 (nya_hip_read)", "bytes": wbytes, "us_per_step": round(ms * 1e3, 3),
-            "GBps": round(wbytes / (ms * 1e-3) / 1e9, 2), "frac": round(wbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-            "matvec_over_read": round(matvec_ms / ms, 4)}
+    return out
+
+
+# Read structures tried at the matrix's size: (wavefronts per workgroup,
+# 16-byte loads in flight per lane), workgroups per CU, and where the loads
+# land (0 registers, non-temporal; 1 registers, default cache policy; 2 LDS).
+READ_SHAPES = [(4, 32), (4, 16), (8, 16), (8, 8), (16, 8), (16, 4)]
+READ_MODES = {0: "nontemporal", 1: "default", 2: "lds"}
+# Read sizes as multiples of the matrix's bytes (16.5 .. 264 MB).
+READ_SIZE_FACTORS = (0.5, 1, 2, 4, 8)
+
+
+def read_structures(rt, kern, stream, settle, weights, wbytes, sink, steps: int = 200) -> dict:
+    """Every read shape over the same rotating weight copies as the matvec:
+    microseconds per launch, and the fastest."""
+    copies = len(weights)
+    table = []
+    for waves, depth in READ_SHAPES:
+        for per_cu in (1, 2):
+            for mode in READ_MODES:
+                def launch(i, w=waves, d=depth, c=per_cu, m=mode):
+                    kern.read_shaped(weights[i % copies], wbytes, sink, w, d, c, m, stream)
+                ms = time_launches(rt, stream, settle, launch, steps, 10, "stream", [(p, wbytes) for p in weights])
+                table.append({"waves": waves, "depth": depth, "per_cu": per_cu, "loads": READ_MODES[mode],
+                              "us_per_step": round(ms * 1e3, 3),
+                              "frac": round(wbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
+    best = min(table, key=lambda r: r["us_per_step"])
+    return {"bytes": wbytes, "steps": steps, "best": best, "table": table}
+
+
+def read_sizes(rt, kern, stream, settle, src_weights, wbytes, sink, best, steps: int = 200) -> dict:
+    """The plain read (and the fastest structure at the matrix's size) over
+    16.5 .. 264 MB, each size over rotating copies that exceed twice the
+    Infinity Cache, plus a least-squares line us = floor + bytes / rate:
+    the per-dispatch floor and the streaming rate."""
+    sizes = [int(wbytes * f) // 1024 * 1024 for f in READ_SIZE_FACTORS]
+    need = max(s * (math.ceil(2 * MALL_BYTES / s) + 1) for s in sizes)
+    arena = rt.malloc(need)
+    # Fill the arena with the matrix's own bytes (data-dependent power
+    # stays that of the matvec's inputs).
+    for off in range(0, need, wbytes):
+        kern.copy(arena + off, src_weights, min(wbytes, need - off) // 16 * 16, stream)
+    rt.sync(stream)
+    legs = {"read16": lambda p, n: kern.read(p, n, sink, stream)}
+    if best:
+        legs["best"] = lambda p, n: kern.read_shaped(p, n, sink, best["waves"], best["depth"], best["per_cu"],
+                                                    {v: k for k, v in READ_MODES.items()}[best["loads"]], stream)
+    out = {}
+    for name, fn in legs.items():
+        rows = []
+        for s in sizes:
+            copies = math.ceil(2 * MALL_BYTES / s) + 1
+            ptrs = [arena + k * s for k in range(copies)]
+            ms = time_launches(rt, stream, settle, lambda i: fn(ptrs[i % copies], s), steps, 10, "stream",
+                               [(p, s) for p in ptrs])
+            rows.append({"bytes": s, "us_per_step": round(ms * 1e3, 3),
+                         "frac": round(s / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
+        xs = np.array([r["bytes"] for r in rows], dtype=np.float64)
+        ts = np.array([r["us_per_step"] for r in rows], dtype=np.float64)
+        slope, floor = np.polyfit(xs, ts, 1)
+        out[name] = {"table": rows, "fit": {"floor_us": round(float(floor), 3),
+                                            "stream_GBps": round(1e-3 / float(slope), 1),
+                                            "stream_frac": round(1e-3 / float(slope) / PEAK_HBM_GBS, 4)}}
+    rt.free(arena)
+    return out
 
 
 def call_latency(kern, rt, stream, weights, x_dev, y_dev, host_w: np.ndarray, x_host: np.ndarray,
@@ -544,6 +705,11 @@ def main() -> int:
     ap.add_argument("--no-call-latency", action="store_true",
                     help="skip the per-call wall times at the C-ABI and provider boundaries")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the rocprofv3 FETCH_SIZE / WRITE_SIZE child runs that measure HBM bytes per launch")
+    ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--no-read-legs", action="store_true",
+                    help="skip the read structures and read sizes beside the read ceiling")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only the plain 256 MiB device copy used to calibrate HBM byte counters")
     ap.add_argument("--prefill-steps", type=int, default=20, help="timed prefill GEMM calls (0: skip)")
@@ -560,6 +726,12 @@ def main() -> int:
               "sharded across GPUs with no exchange between them). Run with --gpus 1.", file=sys.stderr)
         return 2
 
+    if args.traffic_probe:
+        return traffic_probe()
+    # The counter passes run first: child processes started before this one
+    # touches the GPU.
+    traffic = measure_traffic() if not (args.no_traffic or args.sweep or args.prefill_only or args.resident_only
+                                        or args.calibrate_copy) else {"error": "not measured (--no-traffic)"}
     if args.resident_only:
         print(json.dumps({"resident": resident_legs(args.resident_tg, args.resident_pp, args.resident_blocks or None)}),
               flush=True)
@@ -626,13 +798,15 @@ def main() -> int:
                    "batch": 1, "weight_copies": copies, "launch": args.launch,
                    "kernel": kern.kernel_name(Q4_K, ROWS, COLS, 1), "device": device(rt)},
         "roofline": {"bound": "hbm", "achieved": round(gbs1, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs1 / PEAK_HBM_GBS, 4), "traffic": measured_traffic(1),
+                     "frac": round(gbs1 / PEAK_HBM_GBS, 4), "traffic": traffic.get("n1"),
                      "algorithmic_bytes": bytes1},
         "n8": {"value": round(gbs8, 2), "unit": "GB/s", "ms_per_step": round(ms8, 6),
-               "frac": round(gbs8 / PEAK_HBM_GBS, 4), "algorithmic_bytes": bytes8, "traffic": measured_traffic(8),
+               "frac": round(gbs8 / PEAK_HBM_GBS, 4), "algorithmic_bytes": bytes8, "traffic": traffic.get("n8"),
                "kernel": kern.kernel_name(Q4_K, ROWS, COLS, 8)},
+        "traffic": traffic,
     }
-    line["read_ceiling"] = read_ceiling(rt, kern, stream, settle, weights, args.steps, args.warmup, args.launch, ms1)
+    line["read_ceiling"] = read_ceiling(rt, kern, stream, settle, weights, args.steps, args.warmup, args.launch, ms1,
+                                        shapes=not args.no_read_legs, sizes=not args.no_read_legs)
     if not args.no_call_latency:
         line["call_latency"] = call_latency(kern, rt, stream, weights, x_dev, y_dev, host_w, x8[0].copy())
     if args.prefill_steps > 0:

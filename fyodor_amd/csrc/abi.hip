@@ -210,19 +210,20 @@ NYA_HIP_EXPORT int nya_hip_matmul_static(uintptr_t w, unsigned type, size_t rows
     // (every token is independent of the others): `parts` chunks of nearly
     // equal size, each above half the array's capacity (at least 32 tokens),
     // so every chunk stays on the GEMM and every token gets the same result
-    // as through nya_hip_matmul. Every other path needs at most a few hundred
-    // KiB (the small-N digits of one 16384-column chunk).
+    // as through nya_hip_matmul. Where not even 64 tokens of the GEMM's
+    // workspace fit (rows of about 254k columns and more), the batch runs
+    // as 8-token launches, as nya_hip_matmul does with a short workspace.
+    // Every other path needs at most a few hundred KiB (the small-N digits
+    // of one 16384-column chunk); matmul_impl itself falls back to launches
+    // without scratch where even that would not fit.
     size_t parts = 1;
     if (use_prefill(type, rows, cols, batch)) {
         const size_t fit = static_chunk_tokens(type, cols);
-        if (fit < 64) return NYA_HIP_STATUS_SCRATCH;
+        if (fit < 64) return matmul_impl(w, type, rows, cols, x, y, batch, (uintptr_t)ws, kStaticScratchBytes, stream);
         parts = (batch + fit - 1) / fit;
     }
     for (size_t part = 0, done = 0; part < parts; ++part) {
         const size_t n = batch / parts + (part < batch % parts ? 1 : 0);
-        size_t need = 0;
-        if (nya_hip_workspace_bytes(type, rows, cols, n, &need)) return 1;
-        if (need > kStaticScratchBytes) return NYA_HIP_STATUS_SCRATCH;
         const int st = matmul_impl(w, type, rows, cols, x + done * cols * sizeof(float),
                                    y + done * rows * sizeof(float), n, (uintptr_t)ws, kStaticScratchBytes, stream);
         if (st) return st;
@@ -289,6 +290,15 @@ NYA_HIP_EXPORT int nya_hip_read(uintptr_t src, size_t bytes, uintptr_t sink, uin
 {
     if (!src || !sink || !bytes || (src & 15u) || (sink & 3u) || (bytes & 15u)) return 1;
     return status(launch_read((const uint4 *)src, bytes / 16, (unsigned *)sink, (hipStream_t)stream));
+}
+
+NYA_HIP_EXPORT int nya_hip_read_shaped(uintptr_t src, size_t bytes, uintptr_t sink, int waves, int depth,
+    int per_cu, int mode, uintptr_t stream)
+{
+    if (!src || !sink || !bytes || (src & 15u) || (sink & 3u) || (bytes & 15u)) return 1;
+    const hipError_t e = launch_read_shaped((const uint4 *)src, bytes / 16, (unsigned *)sink, waves, depth, per_cu,
+                                            mode, (hipStream_t)stream);
+    return e == hipErrorInvalidValue ? 1 : status(e);
 }
 
 // ---- resident decoder steps ----------------------------------------------

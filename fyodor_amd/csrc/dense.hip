@@ -154,4 +154,86 @@ hipError_t launch_read(const uint4 *src, size_t count, unsigned *sink, hipStream
     return hipGetLastError();
 }
 
+namespace {
+// The same streaming read in other shapes, to find the fastest plain read of
+// a given size: W wavefronts per workgroup, D 16-byte loads in flight per
+// lane per pass, and the loads either into registers (MODE 0 non-temporal,
+// MODE 1 the default cache policy) or straight into LDS (MODE 2,
+// buffer_load_dwordx4 ... lds: wavefront w's D KiB at LDS offset w D KiB,
+// waited for before the next pass reuses it). A workgroup reads one
+// contiguous share; past it the buffer range check returns zeros.
+template <int W, int D, int MODE>
+__global__ __launch_bounds__(64 * W) void read_shaped(const uint8_t *__restrict__ src, size_t bytes, size_t share,
+    unsigned *__restrict__ sink)
+{
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const size_t begin = (size_t)blockIdx.x * share;
+    const size_t n = begin < bytes ? (bytes - begin < share ? bytes - begin : share) : 0;
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(src + begin), (short)0, (int)n, 0x00020000);
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    if constexpr (MODE == 2) {
+        extern __shared__ __align__(16) uint8_t lds[];
+        for (size_t pass = 0; pass < n; pass += (size_t)1024 * W * D) {
+#pragma unroll
+            for (int u = 0; u < D; ++u)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    r, (__attribute__((address_space(3))) void *)(lds + 1024 * (wave * D + u)), 16, 16 * lane,
+                    (int)(pass + 1024 * (u * W + wave)), 0, 0);
+            // The copies land before the next pass overwrites the same LDS.
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        acc = *(const u32x4 *)(lds + 1024 * wave * D + 16 * lane);
+    } else {
+        for (size_t pass = 0; pass < n; pass += (size_t)1024 * W * D) {
+            u32x4 v[D];
+#pragma unroll
+            for (int u = 0; u < D; ++u)
+                v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           r, (int)(pass + 1024 * (u * W + wave)) + 16 * lane, 0, MODE == 0 ? 2 : 0));
+#pragma unroll
+            for (int u = 0; u < D; ++u) acc ^= v[u];
+        }
+    }
+    const unsigned x = acc.x ^ acc.y ^ acc.z ^ acc.w;
+    if (x == 0x9E3779B9u) sink[blockIdx.x % kReadSinkWords] = x;
+}
+
+template <int W, int D, int MODE>
+hipError_t launch_shaped(const uint8_t *src, size_t bytes, size_t share, unsigned blocks, unsigned *sink,
+    hipStream_t stream)
+{
+    const size_t lds = MODE == 2 ? (size_t)1024 * W * D : 0;
+    hipLaunchKernelGGL((read_shaped<W, D, MODE>), dim3(blocks), dim3(64 * W), lds, stream, src, bytes, share, sink);
+    return hipGetLastError();
+}
+}  // namespace
+
+// (waves, depth) pairs: 4 x 32, 4 x 16, 8 x 16, 8 x 8, 16 x 8, 16 x 4, all
+// at most 128 KiB in flight per workgroup (the LDS form holds them all).
+hipError_t launch_read_shaped(const uint4 *src, size_t count, unsigned *sink, int waves, int depth, int per_cu,
+    int mode, hipStream_t stream)
+{
+    if (mode < 0 || mode > 2 || per_cu < 1 || per_cu > 4) return hipErrorInvalidValue;
+    const unsigned blocks = (unsigned)(device_cu_count() * per_cu);
+    const size_t bytes = count * 16;
+    const size_t share = (bytes + (size_t)1024 * blocks - 1) / ((size_t)1024 * blocks) * 1024;
+    if (share > (size_t)INT32_MAX) return hipErrorInvalidValue;
+    const uint8_t *s = (const uint8_t *)src;
+#define FY_SHAPE(w, d)                                                                                            \
+    if (waves == w && depth == d) {                                                                               \
+        if (mode == 0) return launch_shaped<w, d, 0>(s, bytes, share, blocks, sink, stream);                     \
+        if (mode == 1) return launch_shaped<w, d, 1>(s, bytes, share, blocks, sink, stream);                     \
+        return launch_shaped<w, d, 2>(s, bytes, share, blocks, sink, stream);                                    \
+    }
+    FY_SHAPE(4, 32)
+    FY_SHAPE(4, 16)
+    FY_SHAPE(8, 16)
+    FY_SHAPE(8, 8)
+    FY_SHAPE(16, 8)
+    FY_SHAPE(16, 4)
+#undef FY_SHAPE
+    return hipErrorInvalidValue;
+}
+
 }  // namespace fy

@@ -85,6 +85,11 @@ hipError_t launch_copy(uint4 *dst, const uint4 *src, size_t count, hipStream_t s
 // (dense.hip); `sink` holds kReadSinkWords words.
 constexpr int kReadSinkWords = 1024;
 hipError_t launch_read(const uint4 *src, size_t count, unsigned *sink, hipStream_t stream);
+// The same read in other shapes (dense.hip): `waves` wavefronts per
+// workgroup, `depth` 16-byte loads in flight per lane, `per_cu` workgroups
+// per CU, `mode` 0 non-temporal loads, 1 default cache policy, 2 into LDS.
+hipError_t launch_read_shaped(const uint4 *src, size_t count, unsigned *sink, int waves, int depth, int per_cu,
+    int mode, hipStream_t stream);
 // Vector steps of the resident decoder (resident.hip) over `count` tokens,
 // fp32 device vectors, token i's row at i times the row's stride (floats):
 // the decode step ids written (step[0] token, step[1] position); rows

@@ -116,6 +116,7 @@ class Kernels:
         L.nya_hip_matmul_static.argtypes = [_up, _u, _sz, _sz, _up, _up, _sz, _up]
         L.nya_hip_copy.argtypes = [_up, _up, _sz, _up]
         L.nya_hip_read.argtypes = [_up, _sz, _up, _up]
+        L.nya_hip_read_shaped.argtypes = [_up, _sz, _up, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _up]
         L.nya_hip_kernel_name.restype = ctypes.c_char_p
         L.nya_hip_kernel_name.argtypes = [_u, _sz, _sz, _sz]
 
@@ -161,6 +162,14 @@ class Kernels:
         status = self.lib.nya_hip_read(src, nbytes, sink, stream)
         if status != 0:
             raise HipError(f"nya_hip_read returned {status}")
+
+    def read_shaped(self, src: int, nbytes: int, sink: int, waves: int, depth: int, per_cu: int, mode: int,
+                    stream: int) -> None:
+        """The plain read in another shape (waves x depth, workgroups per CU,
+        0 non-temporal / 1 default policy / 2 into LDS)."""
+        status = self.lib.nya_hip_read_shaped(src, nbytes, sink, waves, depth, per_cu, mode, stream)
+        if status != 0:
+            raise HipError(f"nya_hip_read_shaped returned {status}")
 
     def kernel_name(self, type_id: int, rows: int, cols: int, batch: int) -> str:
         name = self.lib.nya_hip_kernel_name(type_id, rows, cols, batch)

@@ -94,10 +94,13 @@ NYA_HIP_EXPORT int nya_hip_matmul(uintptr_t w, unsigned type, size_t rows, size_
  * scratch is a fixed device array of NYA_HIP_STATIC_SCRATCH_BYTES inside
  * this library, one per GPU, held until the process ends; the call
  * allocates and frees nothing. Prefill batches (above 8 tokens) run in
- * token chunks whose scratch fits the array. Returns 0, 1 when declined
- * (the rules of nya_hip_matmul), NYA_HIP_STATUS_SCRATCH when a request
- * would need more scratch than the array holds (not reachable for rows of
- * at most 2^26 columns), <0 on a HIP failure. Every call on one GPU shares
+ * token chunks whose scratch fits the array; where not even a 64-token
+ * chunk fits (rows of about 254k columns and more) the batch runs as
+ * 8-token launches, which is what nya_hip_matmul does with a workspace
+ * shorter than it asks for (then the results equal that call's, not the
+ * GEMM's). Returns 0, 1 when declined (the rules of nya_hip_matmul), <0 on
+ * a HIP failure; NYA_HIP_STATUS_SCRATCH is kept for callers that test for
+ * it and is not returned. Every call on one GPU shares
  * that GPU's array: calls that overlap on one GPU (other streams, other
  * threads) race and must be serialized by the caller; the array keeps the
  * last call's contents, which no call reads before writing. */
@@ -125,6 +128,16 @@ NYA_HIP_EXPORT int nya_hip_copy(uintptr_t dst, uintptr_t src, size_t bytes, uint
  * a few words and is otherwise left as it is. */
 #define NYA_HIP_READ_SINK_BYTES 4096
 NYA_HIP_EXPORT int nya_hip_read(uintptr_t src, size_t bytes, uintptr_t sink, uintptr_t stream);
+
+/* Diagnostics, no counterpart in the reference: the same plain read in
+ * another shape, to measure which read structure streams a given size
+ * fastest. `waves` wavefronts per workgroup and `depth` 16-byte loads in
+ * flight per lane, as one of the pairs 4x32, 4x16, 8x16, 8x8, 16x8, 16x4;
+ * `per_cu` (1..4) workgroups per compute unit; `mode` 0 non-temporal loads
+ * into registers, 1 loads with the default cache policy, 2 loads straight
+ * into LDS (buffer_load_dwordx4 ... lds). Returns 1 for any other shape. */
+NYA_HIP_EXPORT int nya_hip_read_shaped(uintptr_t src, size_t bytes, uintptr_t sink, int waves, int depth,
+    int per_cu, int mode, uintptr_t stream);
 
 /* The vector steps of the decoder over `count` tokens (1..65535) at once,
  * for a provider that keeps a whole model's token forward on the device (the

@@ -196,7 +196,10 @@ API int nya_hip_workspace_bytes(unsigned type, size_t rows, size_t cols, size_t 
 {
     size_t n;
     if (!out || !batch || nya_hip_weight_bytes(type, rows, cols, &n)) return 1;
-    *out = 0;
+    /* The real library's GEMM asks for scratch above 8 tokens; the stand-in
+     * computes without any, unless a test sets a size to report. */
+    const char *ws = getenv("MOCK_HIP_GEMM_WORKSPACE");
+    *out = ws && batch > 8 ? (size_t)strtoull(ws, NULL, 10) : 0;
     return 0;
 }
 API int nya_hip_matmul(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x, uintptr_t y,

@@ -31,7 +31,7 @@ def test_kernel_library_exports_its_header():
     want = declared("fyodor_hip.h")
     assert want == {"nya_hip_abi_version", "nya_hip_weight_bytes", "nya_hip_weight_layout", "nya_hip_weight_pack",
                     "nya_hip_workspace_bytes", "nya_hip_matmul", "nya_hip_matmul_static", "nya_hip_kernel_name",
-                    "nya_hip_copy", "nya_hip_read", "nya_hip_step", "nya_hip_embed", "nya_hip_rms_norm",
+                    "nya_hip_copy", "nya_hip_read", "nya_hip_read_shaped", "nya_hip_step", "nya_hip_embed", "nya_hip_rms_norm",
                     "nya_hip_rope_qkv", "nya_hip_attention", "nya_hip_silu_mul", "nya_hip_greedy",
                     "nya_hip_matvec_gated", "nya_hip_matvec_swiglu", "nya_hip_silu_pairs",
                     "nya_hip_matvec_normed", "nya_hip_matvec_normed_rope"}

@@ -124,6 +124,12 @@ def test_matvec_stage_shapes(compute, oracle, t, rows, cols):
     check_all(oracle, w, t, x, rows, cols, y)
 
 
+# Worst per-row distance from the exact sums, in units of the contract's
+# bound, allowed against the reference scalar order's own worst on the same
+# outlier inputs.
+OUTLIER_ENVELOPE = 32.0
+
+
 @pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K, Q6_K], ids=lambda t: TYPE_NAMES[t])
 @pytest.mark.parametrize("batch", [1, 8, 40])
 def test_outlier_channels(compute, oracle, t, batch):
@@ -140,8 +146,20 @@ def test_outlier_channels(compute, oracle, t, batch):
     w = synth.weights(t, rows, cols, 92 + t)
     for shift in (12, 14):
         x = outlier_channels(batch, cols, 93 + t + shift, shift)
-        y = compute.matmul_typed(w, rows, cols, t, x, batch)
-        check_rel_l2(oracle, w, t, x, rows, cols, y.reshape(batch, rows))
+        y = compute.matmul_typed(w, rows, cols, t, x, batch).reshape(batch, rows)
+        check_rel_l2(oracle, w, t, x, rows, cols, y)
+        # Per row against the contract's bound 1e-6 (1 + sum |w x|): the
+        # reference's own scalar order leaves it on these inputs too (up to
+        # 6.5 times), so the envelope is stated against that order.
+        s, m = oracle.contract_sums(w, t, x, rows, cols)
+        scalar = oracle.matmul(w, t, x, rows, cols, batch, threads=host_threads())
+        ratio = np.abs(y.astype(np.float64) - s) / (1e-6 * (1 + m))
+        ratio_ref = np.abs(scalar.astype(np.float64) - s) / (1e-6 * (1 + m))
+        print(f"outliers 2^{shift} {TYPE_NAMES[t]} batch {batch}: worst per-row ratio to the contract bound "
+              f"{ratio.max():.3g} (scalar order {ratio_ref.max():.3g}), p99 {np.percentile(ratio, 99):.3g} "
+              f"({np.percentile(ratio_ref, 99):.3g})", flush=True)
+        assert ratio.max() <= OUTLIER_ENVELOPE * max(ratio_ref.max(), 1.0), \
+            f"worst per-row ratio {ratio.max():.3g} against the scalar order's {ratio_ref.max():.3g}"
 
 
 @pytest.mark.parametrize("t", [Q8_0, Q4_0], ids=lambda t: TYPE_NAMES[t])

@@ -60,6 +60,33 @@ def test_resident_plan_on_gpu(session_lib, rocm_env, tmp_path, types):
     assert s.kernel_launches > 0 and s.external_matmul_calls > 0 and s.kv_bytes > 0
 
 
+# The decoder shapes bench.py times (its resident legs): TinyLlama 1.1B and
+# the 8B class, each with its own per-block matrices, head layout,
+# vocabulary and Q4_K/Q6_K mix, at fewer blocks than the real models (the
+# engine's scalar reference session computes every token on one CPU core;
+# every block runs the same kernels). TinyLlama: 4 decode tokens, then a
+# 64-token prompt chunk (the prefill GEMM) and a decode step after it; the
+# 8B class: 4 decode tokens, a 16-token chunk (8-token launches of the
+# small-N kernel) and a decode step.
+BENCH_TYPES = {"embedding": Q4_K, "output": Q6_K, "attention": Q4_K, "gate_up": Q4_K, "down": Q6_K}
+BENCH_SHAPES = {
+    "tinyllama-1.1b": (dict(embedding=2048, heads=32, kv_heads=4, hidden=5632, vocabulary=32000, blocks=2), (64, 1)),
+    "llama-8b": (dict(embedding=4096, heads=32, kv_heads=8, hidden=14336, vocabulary=128256, blocks=1), (16, 1)),
+}
+
+
+@pytest.mark.parametrize("name", list(BENCH_SHAPES))
+def test_benchmarked_shapes_against_engine(session_lib, rocm_env, tmp_path, name):
+    dims, chunks = BENCH_SHAPES[name]
+    shape = LlamaShape(**dims, context=sum(chunks) + 8, types=BENCH_TYPES, seed=13)
+    path = tmp_path / "model.gguf"
+    write(path, shape)
+    print(f"{name}: {dims['blocks']} blocks, decode 4 tokens, chunks {chunks}", flush=True)
+    out = compare(session_lib, path, shape, "rocm", TOKENS[:4], chunks=chunks)
+    print(f"{name}: worst scaled logit error {out['logit']:.3g}, KV {out['kv']:.3g}", flush=True)
+    assert out["execution"] == "resident"
+
+
 def test_python_model_plan_on_gpu(session_lib, rocm_env, tmp_path):
     """The model description built by fyodor_amd.model (no engine loader),
     planned through this repository's own compute API on the GPU, against
@@ -70,7 +97,16 @@ def test_python_model_plan_on_gpu(session_lib, rocm_env, tmp_path):
     print(f"python-built plan: worst scaled logit error {out['logit']:.3g}, KV {out['kv']:.3g}", flush=True)
 
 
-def test_decode_graph_replays_match_direct_launches(monkeypatch):
+# Decode shapes for the graph replay check: one where the plan runs the
+# separate steps, and one where both one-token fusions engage (512 q|k|v
+# rows, two per CU: the normed rotary product; gate|up 17408 rows, past 64
+# per CU: the interleaved SwiGLU product).
+REPLAY_SHAPES = {"separate-steps": dict(embedding=512, heads=8, kv_heads=2, hidden=1024),
+                 "fused-products": dict(embedding=256, heads=4, kv_heads=2, hidden=8704)}
+
+
+@pytest.mark.parametrize("dims", list(REPLAY_SHAPES.values()), ids=list(REPLAY_SHAPES))
+def test_decode_graph_replays_match_direct_launches(monkeypatch, dims):
     """A decode token's launches replayed as a captured HIP graph give the
     same logits, bit for bit, as the same launches issued one by one
     (NYA_ROCM_GRAPHS=0), over many replays of both graphs (with and without
@@ -80,8 +116,17 @@ def test_decode_graph_replays_match_direct_launches(monkeypatch):
     from fyodor_amd import model as fm
     monkeypatch.setenv("NYA_ROCM_KERNEL_LIBRARY", str(KERNEL_LIBRARY))
     monkeypatch.delenv("NYA_ROCM_HIP_LIBRARY", raising=False)
-    shape = fm.LlamaShape(embedding=512, heads=8, kv_heads=2, hidden=1024, blocks=3, context=64, vocabulary=1000,
-                          seed=3)
+    shape = fm.LlamaShape(**dims, blocks=3, context=64, vocabulary=1000, seed=3)
+    if dims["hidden"] == 8704:
+        from fyodor_amd.hip import Kernels
+        L = Kernels().lib
+        up, u, sz = ctypes.c_size_t, ctypes.c_uint, ctypes.c_size_t
+        L.nya_hip_matvec_normed_rope.argtypes = [up, u, sz, sz, up, up, up, ctypes.c_float, up, up, up, up, sz, sz,
+                                                 sz, sz, up, up, up]
+        L.nya_hip_matvec_swiglu.argtypes = [up, u, sz, sz, up, up, up]
+        # Both fused entries take this model's products (shape queries).
+        assert L.nya_hip_matvec_normed_rope(0, Q4_K, 512, 256, 0, 0, 0, 1e-5, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0) == 0
+        assert L.nya_hip_matvec_swiglu(0, Q4_K, 2 * 8704, 256, 0, 0, 0) == 0
     model = fm.LlamaModel(shape)
     tokens = [(i * 37 + 11) % shape.vocabulary for i in range(40)]
 

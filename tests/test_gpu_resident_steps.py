@@ -39,7 +39,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from fyodor_amd import BF16, F16, F32, Q4_0, Q4_K, Q6_K, Q8_0, synth
+from fyodor_amd import BF16, F16, F32, Q4_0, Q4_K, Q6_K, Q8_0, TYPE_NAMES, synth
 from fyodor_amd.hip import Kernels, Runtime
 
 pytestmark = pytest.mark.gpu
@@ -419,15 +419,20 @@ def test_matvec_normed_declines(env):
     assert L.nya_hip_matvec_normed(0, F16, 4096, 4096, 0, 0, 0, 1e-5, 0, 0, stream) == 1     # dense type
 
 
-@pytest.mark.parametrize("heads,kv_heads,width,position", [(32, 8, 128, 37), (32, 8, 128, 0), (32, 4, 64, 300),
-                                                           (32, 8, 128, 512)])
-def test_matvec_normed_rope_equals_two_steps(env, heads, kv_heads, width, position):
+# The plan takes the fused rotary product for every block format of q|k|v.
+NORMED_ROPE = [(Q4_K, 32, 8, 128, 37), (Q4_K, 32, 8, 128, 0), (Q4_K, 32, 4, 64, 300), (Q4_K, 32, 8, 128, 512),
+               (Q6_K, 32, 8, 128, 37), (Q8_0, 32, 8, 128, 200), (Q4_0, 32, 4, 64, 5)]
+
+
+@pytest.mark.parametrize("t,heads,kv_heads,width,position", NORMED_ROPE,
+                         ids=[f"{TYPE_NAMES[c[0]]}-{c[1]}/{c[2]}x{c[3]}-at{c[4]}" for c in NORMED_ROPE])
+def test_matvec_normed_rope_equals_two_steps(env, t, heads, kv_heads, width, position):
     rt, L, stream = env
     kern = Kernels()
     cols, capacity = 4096, 512
     qd, kvd = heads * width, kv_heads * width
     rows = qd + 2 * kvd
-    assert L.nya_hip_matvec_normed_rope(0, Q4_K, rows, cols, 0, 0, 0, 1e-5, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, stream) == 0
+    assert L.nya_hip_matvec_normed_rope(0, t, rows, cols, 0, 0, 0, 1e-5, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, stream) == 0
     rng = np.random.default_rng(rows + position)
     x = (3 * rng.standard_normal(cols)).astype(np.float32)
     r = rng.standard_normal(cols).astype(np.float32)
@@ -435,17 +440,17 @@ def test_matvec_normed_rope_equals_two_steps(env, heads, kv_heads, width, positi
     cache_k = rng.standard_normal((capacity, kvd)).astype(np.float32)
     cache_v = rng.standard_normal((capacity, kvd)).astype(np.float32)
     freq = (10000.0 ** (-np.arange(width // 2) * 2.0 / width)).astype(np.float32)
-    w = kern.device_weights(synth.weights(Q4_K, rows, cols, seed=rows), Q4_K, rows, cols)
+    w = kern.device_weights(synth.weights(t, rows, cols, seed=rows), t, rows, cols)
     dev = Dev(rt)
     try:
         wd, xd, rd, gd = dev.put(w), dev.put(x), dev.put(r), dev.put(g)
         k1, v1, k2, v2 = dev.put(cache_k), dev.put(cache_v), dev.put(cache_k), dev.put(cache_v)
         fd, pd = dev.put(freq), dev.put(np.array([position], np.int32))
         h1, h2, y1, y2 = dev.empty(4 * cols), dev.empty(4 * cols), dev.empty(4 * rows), dev.empty(4 * rows)
-        print(f"normed_rope {heads}/{kv_heads} width {width} position {position}", flush=True)
-        assert L.nya_hip_matvec_normed_rope(wd, Q4_K, rows, cols, xd, rd, gd, 1e-5, h1, y1, pd, fd, heads, kv_heads,
+        print(f"normed_rope {TYPE_NAMES[t]} {heads}/{kv_heads} width {width} position {position}", flush=True)
+        assert L.nya_hip_matvec_normed_rope(wd, t, rows, cols, xd, rd, gd, 1e-5, h1, y1, pd, fd, heads, kv_heads,
                                             width, capacity, k1, v1, stream) == 0
-        assert L.nya_hip_matvec_normed(wd, Q4_K, rows, cols, xd, rd, gd, 1e-5, h2, y2, stream) == 0
+        assert L.nya_hip_matvec_normed(wd, t, rows, cols, xd, rd, gd, 1e-5, h2, y2, stream) == 0
         assert L.nya_hip_rope_qkv(y2, rows, y2 + 4 * qd, rows, y2 + 4 * (qd + kvd), rows, 1, heads, kv_heads, width,
                                   fd, pd, capacity, k2, v2, stream) == 0
         rt.sync(stream)

@@ -66,6 +66,28 @@ def test_plan_declined_without_resident_steps(session_lib, tmp_path, monkeypatch
     assert out["execution"] == "cpu-reference"
 
 
+def test_plan_declined_when_its_workspace_exceeds_the_budget(session_lib, tmp_path, monkeypatch):
+    """The budget check counts the kernels' workspace (sized for the plan's
+    prompt chunks) before allocating anything: a workspace past the budget
+    declines the plan, and the engine runs its reference path."""
+    shape = LlamaShape(context=16)
+    path = tmp_path / "model.gguf"
+    write(path, shape)
+    # What the plan needs without a workspace, then a budget 4 MiB above it.
+    monkeypatch.setenv("MOCK_HIP_GEMM_WORKSPACE", "0")
+    out = compare(session_lib, path, shape, "rocm", TOKENS[:4])
+    assert out["execution"] == "resident"
+    s = out["stats"]
+    mib = (s.weights_bytes + s.kv_bytes + s.scratch_bytes + (1 << 20) - 1 >> 20) + 4
+    monkeypatch.setenv("NYA_ROCM_CACHE_MIB", str(mib))
+    monkeypatch.setenv("MOCK_HIP_GEMM_WORKSPACE", str(2 << 20))
+    assert compare(session_lib, path, shape, "rocm", TOKENS[:4])["execution"] == "resident"
+    # 8 MiB of workspace would still allocate on the stand-in, but it is past
+    # the budget: declined before any upload.
+    monkeypatch.setenv("MOCK_HIP_GEMM_WORKSPACE", str(8 << 20))
+    assert compare(session_lib, path, shape, "rocm", TOKENS[:4])["execution"] == "cpu-reference"
+
+
 @pytest.mark.parametrize("entries,extra", [(("nya_hip_matvec_gated",), 1), (("nya_hip_matvec_normed_rope",), 1),
                                            (("nya_hip_matvec_normed", "nya_hip_matvec_normed_rope"), 2)])
 def test_plan_without_fused_step(session_lib, tmp_path, monkeypatch, entries, extra):

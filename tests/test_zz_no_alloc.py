@@ -7,7 +7,8 @@ the outputs must equal the workspace entry point's bit for bit (same
 kernels on the same tokens). Cases: the fp16 prefill GEMM in one chunk and
 in two (4096 x 14336 at 2048 tokens needs 121 MB of scratch against the
 array's 64 MiB), the int8 Q6_K prefill, the small-N tile kernel's digits
-(the only batch of 2..8 that uses scratch) and the batch-1 matvec.
+(the only batch of 2..8 that uses scratch) and the batch-1 matvec; and
+rows too wide for any GEMM chunk to fit the array.
 """
 import numpy as np
 import pytest
@@ -60,6 +61,40 @@ def test_static_matches_workspace_entry(hip, t, rows, cols, batches):
             finally:
                 for p in (xd, yd, ws):
                     rt.free(p)
+            assert np.all(np.isfinite(got)), f"call {call}: outputs left unwritten"
+            assert np.array_equal(got.view(np.uint32), expected.view(np.uint32)), f"call {call} (batch {batch})"
+    finally:
+        rt.free(wd)
+
+
+def test_static_rows_too_wide_for_a_gemm_chunk(hip):
+    """Q4_K 8192 x 262144: 64 tokens of the GEMM's workspace need about 69 MB,
+    more than the array, so the static entry runs batch 24 (then 9) as
+    8-token launches; nya_hip_matmul without a workspace takes the same
+    launches, so the outputs are equal bit for bit."""
+    rt, kern, stream = hip
+    t, rows, cols = Q4_K, 8192, 262144
+    assert kern.workspace_bytes(t, rows, cols, 64) > SCRATCH
+    w = synth.weights(t, rows, cols, 311)
+    wd = rt.malloc(storage_bytes(t, rows, cols))
+    rt.upload(wd, kern.device_weights(w, t, rows, cols))
+    del w
+    try:
+        for call, batch in enumerate((24, 9)):
+            x = synth.activations(batch, cols, 312 + call)
+            xd, yd = rt.malloc(x.nbytes), rt.malloc(4 * rows * batch)
+            try:
+                rt.upload(xd, x)
+                kern.matmul(wd, t, rows, cols, xd, yd, batch, 0, 0, stream)
+                rt.sync(stream)
+                expected = rt.download(yd, np.empty((batch, rows), dtype=np.float32))
+                rt.upload(yd, np.full((batch, rows), np.nan, dtype=np.float32))
+                kern.matmul_static(wd, t, rows, cols, xd, yd, batch, stream)
+                rt.sync(stream)
+                got = rt.download(yd, np.empty((batch, rows), dtype=np.float32))
+            finally:
+                rt.free(xd)
+                rt.free(yd)
             assert np.all(np.isfinite(got)), f"call {call}: outputs left unwritten"
             assert np.array_equal(got.view(np.uint32), expected.view(np.uint32)), f"call {call} (batch {batch})"
     finally:

@@ -53,7 +53,7 @@ import numpy as np
 REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO))
 
-from fyodor_amd import Q4_0, Q4_K, Q6_K, Q8_0, TYPE_NAMES, storage_bytes, synth  # noqa: E402
+from fyodor_amd import BF16, F16, F32, Q4_0, Q4_K, Q6_K, Q8_0, TYPE_NAMES, storage_bytes, synth  # noqa: E402
 from fyodor_amd.hip import Graph, Kernels, Runtime  # noqa: E402
 
 METRIC = "Q4_K matvec effective HBM GB/s (% of peak), 14336x4096, N=1 and N=8"
@@ -533,7 +533,10 @@ RESIDENT_MODELS = {
 VERIFY_TOKENS = (1, 2, 4, 8, 16, 33)
 
 
-def resident(name: str, tg: int, pp: int, blocks: int | None = None, verify=()) -> dict:
+LONG_CONTEXT = 4096
+
+
+def resident(name: str, tg: int, pp: int, blocks: int | None = None, verify=(), long_tg: int = 0) -> dict:
     """The provider's resident plan on a synthetic model of `name`'s shape:
     tg = tokens/s of `tg` decode steps from position 0 (each with its logits
     downloaded and checked, as llama-bench's tg counts a generated token),
@@ -547,7 +550,10 @@ def resident(name: str, tg: int, pp: int, blocks: int | None = None, verify=()) 
     shape_args = dict(RESIDENT_MODELS[name])
     if blocks:
         shape_args["blocks"] = blocks
-    shape = LlamaShape(**shape_args, context=max(tg, pp) + 8, types=RESIDENT_TYPES, seed=7)
+    context = max(tg, pp) + 8
+    if long_tg:
+        context = max(context, LONG_CONTEXT + long_tg + 8)
+    shape = LlamaShape(**shape_args, context=context, types=RESIDENT_TYPES, seed=7)
     model = LlamaModel(shape, llama_tensors(shape, shared_blocks=True))
     ids = [(7 * i + 11) % shape.vocabulary for i in range(max(tg, pp))]
     out = {"workload": (f"dense LLaMA, embedding {shape.embedding}, {shape.heads} heads / {shape.kv_heads} KV of "
@@ -594,6 +600,24 @@ def resident(name: str, tg: int, pp: int, blocks: int | None = None, verify=()) 
                     if step_us:
                         leg["speedup_vs_serial_steps"] = round(k * step_us / (wall * 1e6), 2)
                     out["verify"][str(k)] = leg
+            if long_tg:
+                # Decode past a 4096-token context (prefilled first): the
+                # attention reads 4096+ cached positions per layer.
+                long_ids = [(7 * i + 11) % shape.vocabulary for i in range(LONG_CONTEXT + long_tg)]
+                t0 = time.perf_counter()
+                plan.prefill(long_ids[:LONG_CONTEXT], 0)
+                prefill_s = time.perf_counter() - t0
+                for i in range(LONG_CONTEXT, LONG_CONTEXT + 4):
+                    plan.token(long_ids[i], i)
+                start = time.perf_counter()
+                for i in range(LONG_CONTEXT + 4, LONG_CONTEXT + long_tg):
+                    plan.token(long_ids[i], i)
+                wall = time.perf_counter() - start
+                n = long_tg - 4
+                out[f"tg_at_{LONG_CONTEXT}"] = {
+                    "tokens_per_s": round(n / wall, 2), "us_per_token": round(wall / n * 1e6, 1),
+                    "positions": [LONG_CONTEXT + 4, LONG_CONTEXT + long_tg - 1],
+                    "prefill_4096_s": round(prefill_s, 3), "logits_finite": bool(np.all(np.isfinite(plan.logits)))}
             if pp:
                 plan.prefill(ids[:pp], 0)
                 start = time.perf_counter()
@@ -608,9 +632,80 @@ def resident(name: str, tg: int, pp: int, blocks: int | None = None, verify=()) 
     return out
 
 
-def resident_legs(tg: int, pp: int, blocks: int | None) -> dict:
+def attention_leg(heads: int = 32, kv_heads: int = 8, width: int = 128, layers: int = 32, steps: int = 200) -> dict:
+    """One decode token's attention of the 8B-class head layout, timed per
+    launch with events over back-to-back launches that rotate through
+    `layers` distinct KV caches (every layer's cache is its own, as in a
+    decode step): one workgroup per query head at 136 and 4096 positions, and
+    the split form (the plan's splits: 512 / KV heads, 8 to 64) at 4096."""
+    from fyodor_amd.hip import Kernels, Runtime
+    rt, kern = Runtime(), Kernels()
+    L = kern.lib
+    up, sz = ctypes.c_uint64, ctypes.c_size_t
+    L.nya_hip_attention.argtypes = [up, sz, up, up, up, up, up, sz, sz, sz, sz, sz, ctypes.c_float, up]
+    L.nya_hip_attention_split.argtypes = [up, sz, up, up, up, up, up, sz, sz, sz, sz, sz, sz, ctypes.c_float, up]
+    stream = rt.stream()
+    max_length = LONG_CONTEXT + 64
+    kv_bytes = max_length * kv_heads * width * 4
+    rng = np.random.default_rng(3)
+    cache = rng.standard_normal(max_length * kv_heads * width).astype(np.float32)
+    keys, values = [], []
+    for _ in range(layers):
+        k, v = rt.malloc(kv_bytes), rt.malloc(kv_bytes)
+        rt.upload(k, cache)
+        rt.upload(v, cache)
+        keys.append(k)
+        values.append(v)
+    q_stride = (heads + 2 * kv_heads) * width
+    qd, od = rt.malloc(4 * q_stride), rt.malloc(4 * heads * width)
+    rt.upload(qd, rng.standard_normal(q_stride).astype(np.float32))
+    splits = min(64, max(8, 512 // kv_heads))
+    part = rt.malloc(4 * heads * splits * (width + 2))
+    pos = rt.malloc(4)
+    scale = 1.0 / math.sqrt(width)
+    out = {"workload": f"{heads} query heads / {kv_heads} KV heads of {width}, one token, {layers} rotating KV caches"}
+
+    def time_it(length, split):
+        rt.upload(pos, np.array([length - 1], dtype=np.int32))
+        def launch(i):
+            if split:
+                st = L.nya_hip_attention_split(qd, q_stride, keys[i % layers], values[i % layers], od, part, pos, 1,
+                                               heads, kv_heads, width, max_length, splits, scale, stream)
+            else:
+                st = L.nya_hip_attention(qd, q_stride, keys[i % layers], values[i % layers], od, 0, pos, 1, heads,
+                                         kv_heads, width, max_length, scale, stream)
+            assert st == 0
+        for i in range(20):
+            launch(i)
+        rt.sync(stream)
+        start, end = rt.event(), rt.event()
+        rt.record(start, stream)
+        for i in range(steps):
+            launch(i)
+        rt.record(end, stream)
+        us = rt.elapsed_ms(start, end) / steps * 1e3
+        rt.sync(stream)
+        return round(us, 2)
+
+    out["per_head_136_us"] = time_it(136, False)
+    out["per_head_4096_us"] = time_it(LONG_CONTEXT, False)
+    out["split_4096_us"] = time_it(LONG_CONTEXT, True)
+    out["by_length"] = {str(n): {"per_head_us": time_it(n, False), "split_us": time_it(n, True)}
+                        for n in (64, 136, 257, 512, 1024, 2048)}
+    out["split_splits"] = splits
+    out["split_4096_over_per_head_136"] = round(out["split_4096_us"] / out["per_head_136_us"], 3)
+    out["kv_bytes_4096"] = 2 * LONG_CONTEXT * kv_heads * width * 4
+    out["split_4096_GBps"] = round(out["kv_bytes_4096"] / (out["split_4096_us"] * 1e-6) / 1e9, 1)
+    for p in keys + values + [qd, od, part, pos]:
+        rt.free(p)
+    return out
+
+
+def resident_legs(tg: int, pp: int, blocks: int | None, long_tg: int = 36) -> dict:
     legs = {name: resident(name, tg, 0 if name == "llama-8b" else pp, blocks,
-                           VERIFY_TOKENS if name == "llama-8b" else ()) for name in RESIDENT_MODELS}
+                           VERIFY_TOKENS if name == "llama-8b" else (),
+                           long_tg if name == "llama-8b" else 0) for name in RESIDENT_MODELS}
+    legs["attention"] = attention_leg()
     legs["reference_published"] = {
         "tinyllama-1.1b": {"tg128": 205.48, "pp512": 1374.38, "hardware": "RTX 5060 Ti",
                            "source": "backend/README.md:796-803 (Stage 2 Fyodor CUDA resident)"}}
@@ -626,6 +721,9 @@ SWEEP_MATVEC = [
     (Q4_0, 4096, 11008, (1, 8)), (Q6_K, 4096, 14336, (1, 8)), (Q6_K, 128256, 4096, (1, 8)),
 ]
 SWEEP_PREFILL = [(t, rows, 4096, m) for t in (Q4_K, Q8_0) for rows in (4096, 14336) for m in (512, 2048)]
+# Dense weights at prefill batches (the fp32-MFMA GEMM): type, rows, cols, tokens.
+SWEEP_DENSE = [(t, 4096, 4096, m) for t in (F32, F16, BF16) for m in (64, 512)]
+PEAK_FP32_MFMA_TFLOPS = 157.3
 
 
 def time_case(rt, kern, stream, settle, t, rows, cols, batch, steps):
@@ -677,6 +775,14 @@ def sweep(rt, kern, stream, settle) -> int:
                           "us_per_call": round(ms * 1e3, 2), "useful_tflops": round(useful, 1),
                           "frac_fp16": round(useful / PEAK_FP16_TFLOPS, 4),
                           "issued_frac_fp16": round(useful * PREFILL_PIECES / PEAK_FP16_TFLOPS, 4)}), flush=True)
+    for t, rows, cols, m in SWEEP_DENSE:
+        ms = time_case(rt, kern, stream, settle, t, rows, cols, m, 20)
+        useful = 2.0 * rows * cols * m / (ms * 1e-3) / 1e12
+        print(json.dumps({"sweep": "dense", "type": TYPE_NAMES[t], "rows": rows, "cols": cols, "tokens": m,
+                          "kernel": kern.kernel_name(t, rows, cols, m), "calls": 20,
+                          "us_per_call": round(ms * 1e3, 2), "tflops": round(useful, 1),
+                          "frac_fp32_mfma": round(useful / PEAK_FP32_MFMA_TFLOPS, 4),
+                          "weight_GBps": round(storage_bytes(t, rows, cols) / (ms * 1e-3) / 1e9, 1)}), flush=True)
     return 0
 
 

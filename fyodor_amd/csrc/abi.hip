@@ -85,6 +85,9 @@ int matmul_impl(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t 
     if (use_prefill(type, rows, cols, batch) && fits && workspace_bytes >= prefill_workspace(type, (int)cols, (int)batch))
         return status(launch_prefill(type, wp, (const float *)x, (float *)y, (int)rows, (int)cols, (int)batch,
                                      (void *)workspace, s));
+    if (dense && dense_gemm_supported(type, (int)rows, (int)cols, (int)batch))
+        return status(launch_dense_gemm(type, wp, (const float *)x, (float *)y, (int)rows, (int)cols, (int)batch,
+                                        fits ? (void *)workspace : nullptr, fits ? workspace_bytes : 0, s));
     for (size_t done = 0; done < batch; done += 8) {
         const int n = (int)(batch - done < 8 ? batch - done : 8);
         const float *xp = (const float *)x + done * cols;
@@ -187,8 +190,12 @@ NYA_HIP_EXPORT int nya_hip_workspace_bytes(unsigned type, size_t rows, size_t co
     if (!bytes || !batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return 1;
     const bool dense = type == F32 || type == F16 || type == BF16;
     const int n = batch < 8 ? (int)batch : 8;
-    *bytes = use_prefill(type, rows, cols, batch) ? prefill_workspace(type, (int)cols, (int)batch)
-           : dense || smalln_rows_supported(type, (int)rows, (int)cols, n) ? 0 : smalln_workspace((int)cols, n);
+    if (dense)
+        *bytes = dense_gemm_supported(type, (int)rows, (int)cols, (int)batch)
+                     ? dense_gemm_workspace((int)rows, (int)cols, (int)batch) : 0;
+    else
+        *bytes = use_prefill(type, rows, cols, batch) ? prefill_workspace(type, (int)cols, (int)batch)
+               : smalln_rows_supported(type, (int)rows, (int)cols, n) ? 0 : smalln_workspace((int)cols, n);
     return 0;
 }
 
@@ -272,7 +279,8 @@ NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_
 {
     size_t b;
     if (!batch || batch > INT_MAX || !storage_bytes(type, rows, cols, &b)) return NULL;
-    if (type == F32 || type == F16 || type == BF16) return "skinny_dense";
+    if (type == F32 || type == F16 || type == BF16)
+        return dense_gemm_supported(type, (int)rows, (int)cols, (int)batch) ? "dense_gemm" : "skinny_dense";
     if (use_prefill(type, rows, cols, batch)) return prefill_kernel(type);
     if (batch == 1 && matvec_supported(type, (int)rows, (int)cols)) return matvec_kernel(type, (int)rows, (int)cols);
     // Batches above 8 outside the GEMM run 8 tokens per launch.
@@ -366,6 +374,28 @@ NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t key
     return status(launch_attention((const float *)q, (int)q_stride, (const float *)keys, (const float *)values,
                                    (float *)out, (float *)scores, (const int *)positions, (int)count, (int)heads,
                                    (int)kv_heads, (int)width, (int)max_length, scale, (hipStream_t)stream));
+}
+
+NYA_HIP_EXPORT int nya_hip_attention_split(uintptr_t q, size_t q_stride, uintptr_t keys, uintptr_t values,
+    uintptr_t out, uintptr_t partials, uintptr_t positions, size_t count, size_t heads, size_t kv_heads, size_t width,
+    size_t max_length, size_t splits, float scale, uintptr_t stream)
+{
+    if (!q)   // the shape query
+        return count_ok(heads) && count_ok(kv_heads) && count_ok(width) && count_ok(max_length) &&
+                       count_ok(splits) && heads <= 4096 && splits <= 4096 && max_length <= (size_t)INT_MAX &&
+                       attention_split_supported((int)heads, (int)kv_heads, (int)width, (int)max_length, (int)splits)
+                   ? 0 : 1;
+    if (!vec(q) || !vec(keys) || !vec(values) || !vec(out) || !vec(positions) || !partials || !tokens_ok(count) ||
+        !count_ok(heads) || !count_ok(kv_heads) || !count_ok(width) || !count_ok(max_length) || !count_ok(splits) ||
+        q_stride < heads * width || q_stride > (size_t)INT_MAX || heads > 4096 || splits > 4096 ||
+        max_length > (size_t)INT_MAX ||
+        !attention_split_supported((int)heads, (int)kv_heads, (int)width, (int)max_length, (int)splits) ||
+        (q_stride & 3u) || ((q | keys | values | partials) & 15u))
+        return 1;
+    return status(launch_attention_split((const float *)q, (int)q_stride, (const float *)keys, (const float *)values,
+                                         (float *)out, (float *)partials, (const int *)positions, (int)count,
+                                         (int)heads, (int)kv_heads, (int)width, (int)max_length, (int)splits, scale,
+                                         (hipStream_t)stream));
 }
 
 NYA_HIP_EXPORT int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,

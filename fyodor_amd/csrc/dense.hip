@@ -81,7 +81,257 @@ hipError_t launch_type(const uint8_t *w, const float *x, float *y, int rows, int
     }
 }
 
+// ---- batches above 8: a GEMM on the fp32 matrix cores ----------------------
+//
+// Y [batch][rows] = X [batch][cols] W^T on v_mfma_f32_32x32x2_f32: every
+// product of an fp32 activation and a weight (F16 and BF16 widen to fp32
+// exactly) is formed and accumulated in fp32, as the reference's CUDA GEMM
+// does (CUDA/gemm.cu:53-96), but on the matrix cores. A workgroup of four
+// wavefronts owns 64 tokens x 128 rows; wavefront w computes the 64 tokens
+// of rows 32 w .. 32 w + 31 as two 32 x 32 tiles, each in two accumulator
+// chains (even and odd column chunks) added at the end. K advances 32
+// columns per step: the workgroup stages the tokens' 64 x 32 and the rows'
+// 128 x 32 fp32 tiles in LDS (rows padded to 36 floats: conflict-free
+// 16-byte reads), and prefetches the next step's tiles into registers while
+// the matrix cores work on the current one. MFMA step s of a 32-column chunk
+// takes column 16 h + s in lane half h, for both operands alike. Tokens past
+// the batch and rows past the matrix read zeros (buffer range checks); the
+// columns of a short last chunk (or of rows not 16-byte aligned) are loaded
+// one by one with their bounds.
+constexpr int kGemmTokens = 64, kGemmRows = 128, kGemmK = 32, kGemmPitch = 36;
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <unsigned T> constexpr int kElem = T == F32 ? 4 : 2;
+
+template <unsigned T>
+__device__ __forceinline__ float widen(uint32_t bits)
+{
+    if constexpr (T == F16) return f16_to_f32(bits & 0xFFFFu);
+    else return bf16_to_f32(bits & 0xFFFFu);
+}
+
+// Thread t's share of a step: W row t/2, columns 16 (t%2) .. +15; X token
+// t/4, columns 8 (t%4) .. +7 (as fp32).
+struct GemmStage {
+    float w[16];
+    float x[8];
+};
+
+template <unsigned T>
+__device__ __forceinline__ void gemm_load(GemmStage &st, __amdgpu_buffer_rsrc_t wb, __amdgpu_buffer_rsrc_t xb,
+    int rows, int cols, int batch, int r0, int t0, int kc, bool fast)
+{
+    const int t = threadIdx.x;
+    const int row = r0 + (t >> 1), wcol = kc + 16 * (t & 1);
+    const int tok = t0 + (t >> 2), xcol = kc + 8 * (t & 3);
+    if (fast) {
+        // Whole chunk, 16-byte aligned rows.
+        const int wo = (int)(((uint32_t)row * (uint32_t)cols + (uint32_t)wcol) * kElem<T>);
+        if constexpr (T == F32) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(wb, wo + 16 * q, 0, 0));
+                st.w[4 * q] = v.x; st.w[4 * q + 1] = v.y; st.w[4 * q + 2] = v.z; st.w[4 * q + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wb, wo + 16 * q, 0, 0));
+                const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    st.w[8 * q + 2 * e] = widen<T>(u[e]);
+                    st.w[8 * q + 2 * e + 1] = widen<T>(u[e] >> 16);
+                }
+            }
+        }
+        const int xo = (int)(((uint32_t)tok * (uint32_t)cols + (uint32_t)xcol) * 4u);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const float4 v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xb, xo + 16 * q, 0, 0));
+            st.x[4 * q] = v.x; st.x[4 * q + 1] = v.y; st.x[4 * q + 2] = v.z; st.x[4 * q + 3] = v.w;
+        }
+    } else {
+        // Element by element, zero past the row's last column.
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int c = wcol + e;
+            const int off = (int)(((uint32_t)row * (uint32_t)cols + (uint32_t)(c < cols ? c : 0)) * kElem<T>);
+            float v;
+            if constexpr (T == F32) v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wb, off, 0, 0));
+            else v = widen<T>(__builtin_amdgcn_raw_buffer_load_b16(wb, off, 0, 0));
+            st.w[e] = c < cols ? v : 0.f;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int c = xcol + e;
+            const float v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                xb, (int)(((uint32_t)tok * (uint32_t)cols + (uint32_t)(c < cols ? c : 0)) * 4u), 0, 0));
+            st.x[e] = c < cols ? v : 0.f;
+        }
+    }
+    (void)rows;
+    (void)batch;
+}
+
+__device__ __forceinline__ void gemm_store(const GemmStage &st, float *__restrict__ sw, float *__restrict__ sx)
+{
+    const int t = threadIdx.x;
+    float *dw = sw + (t >> 1) * kGemmPitch + 16 * (t & 1);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        *(float4 *)(dw + 4 * q) = make_float4(st.w[4 * q], st.w[4 * q + 1], st.w[4 * q + 2], st.w[4 * q + 3]);
+    float *dx = sx + (t >> 2) * kGemmPitch + 8 * (t & 3);
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+        *(float4 *)(dx + 4 * q) = make_float4(st.x[4 * q], st.x[4 * q + 1], st.x[4 * q + 2], st.x[4 * q + 3]);
+}
+
+// Workgroup (row tile, token tile, split z) covers the column chunks
+// [z per, (z + 1) per) of the split count gridDim.z; with one split it
+// writes Y, else its partial sums to part[z][token][row] for dense_combine.
+template <unsigned T>
+__global__ __launch_bounds__(256) void dense_gemm(const uint8_t *__restrict__ w, const float *__restrict__ x,
+    float *__restrict__ y, int rows, int cols, int batch, int per, float *__restrict__ part)
+{
+    __shared__ __align__(16) float sw[kGemmRows * kGemmPitch];
+    __shared__ __align__(16) float sx[kGemmTokens * kGemmPitch];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5;
+    const int r0 = blockIdx.x * kGemmRows, t0 = blockIdx.y * kGemmTokens;
+    const __amdgpu_buffer_rsrc_t wb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(w), (short)0, (int)((size_t)rows * cols * kElem<T>), 0x00020000);
+    const __amdgpu_buffer_rsrc_t xb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(x), (short)0, (int)((size_t)batch * cols * 4), 0x00020000);
+    const bool aligned = (cols * kElem<T>) % 16 == 0;
+    // Two chains per output, even and odd chunks, added at the end (the
+    // reference's CUDA GEMM keeps two as well): partial sums stay half as
+    // long, which keeps sums like 8192 equal products exact.
+    f32x16 acc[2][2] = {};
+    int chain = 0;
+    GemmStage st;
+    const int k0 = blockIdx.z * per * kGemmK, k1 = k0 + per * kGemmK < cols ? k0 + per * kGemmK : cols;
+    if (k0 < k1) gemm_load<T>(st, wb, xb, rows, cols, batch, r0, t0, k0, aligned && k0 + kGemmK <= cols);
+    for (int kc = k0; kc < k1; kc += kGemmK) {
+        __syncthreads();   // the previous step's operand reads are done
+        gemm_store(st, sw, sx);
+        __syncthreads();
+        const int kn = kc + kGemmK;
+        if (kn < k1) gemm_load<T>(st, wb, xb, rows, cols, batch, r0, t0, kn, aligned && kn + kGemmK <= cols);
+        // This lane's operands: row 32 wave + l%32 and tokens l%32, 32 + l%32,
+        // columns 16 h .. 16 h + 15 of the chunk.
+        const float *pw = sw + (32 * wave + (lane & 31)) * kGemmPitch + 16 * h;
+        const float *px0 = sx + (lane & 31) * kGemmPitch + 16 * h;
+        const float *px1 = px0 + 32 * kGemmPitch;
+        float bw[16], a0[16], a1[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 vw = *(const float4 *)(pw + 4 * q), v0 = *(const float4 *)(px0 + 4 * q),
+                         v1 = *(const float4 *)(px1 + 4 * q);
+            bw[4 * q] = vw.x; bw[4 * q + 1] = vw.y; bw[4 * q + 2] = vw.z; bw[4 * q + 3] = vw.w;
+            a0[4 * q] = v0.x; a0[4 * q + 1] = v0.y; a0[4 * q + 2] = v0.z; a0[4 * q + 3] = v0.w;
+            a1[4 * q] = v1.x; a1[4 * q + 1] = v1.y; a1[4 * q + 2] = v1.z; a1[4 * q + 3] = v1.w;
+        }
+        if (chain == 0) {
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], bw[s], acc[0][0], 0, 0, 0);
+                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s], bw[s], acc[1][0], 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], bw[s], acc[0][1], 0, 0, 0);
+                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s], bw[s], acc[1][1], 0, 0, 0);
+            }
+        }
+        chain ^= 1;
+    }
+    // D[token][row]: register i of lane l holds token 8 (i/4) + 4 h + i%4
+    // (of the accumulator's 32), row l%32.
+    const int row = r0 + 32 * wave + (lane & 31);
+    if (row >= rows) return;
+    float *out = gridDim.z == 1 ? y : part + (size_t)blockIdx.z * batch * rows;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int tok = t0 + 32 * a + 8 * (i >> 2) + 4 * h + (i & 3);
+            if (tok < batch) out[(size_t)tok * rows + row] = acc[a][0][i] + acc[a][1][i];
+        }
+}
+
+// y = the splits' partial sums added in split order.
+__global__ __launch_bounds__(256) void dense_combine(const float *__restrict__ part, float *__restrict__ y,
+    size_t n, int splits)
+{
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        float s = part[i];
+        for (int z = 1; z < splits; ++z) s += part[(size_t)z * n + i];
+        y[i] = s;
+    }
+}
+
+template <unsigned T>
+hipError_t launch_gemm(const uint8_t *w, const float *x, float *y, int rows, int cols, int batch, int splits,
+    float *part, hipStream_t s)
+{
+    const int chunks = (cols + kGemmK - 1) / kGemmK, per = (chunks + splits - 1) / splits;
+    const dim3 grid((unsigned)((rows + kGemmRows - 1) / kGemmRows), (unsigned)((batch + kGemmTokens - 1) / kGemmTokens),
+                    (unsigned)splits);
+    hipLaunchKernelGGL((dense_gemm<T>), grid, dim3(256), 0, s, w, x, y, rows, cols, batch, per, part);
+    if (splits > 1) {
+        const size_t n = (size_t)batch * rows;
+        const size_t blocks = (n + 255) / 256;
+        hipLaunchKernelGGL(dense_combine, dim3((unsigned)(blocks < 2048 ? blocks : 2048)), dim3(256), 0, s, part, y, n,
+                           splits);
+    }
+    return hipGetLastError();
+}
+
 }  // namespace
+
+// Column splits of the dense GEMM: where the row and token tiles leave most
+// of the 256 CUs idle (small batches of matrices up to a few thousand rows),
+// the columns are split over up to 8 workgroups (at least 8 chunks of 32
+// columns each), whose partial sums a second launch adds in order.
+int dense_gemm_splits(int rows, int cols, int batch)
+{
+    const long tiles = (long)((rows + kGemmRows - 1) / kGemmRows) * ((batch + kGemmTokens - 1) / kGemmTokens);
+    int splits = 1;
+    while (splits < 8 && tiles * splits < 192 && (cols + kGemmK - 1) / kGemmK >= 16 * splits) splits *= 2;
+    return splits;
+}
+
+size_t dense_gemm_workspace(int rows, int cols, int batch)
+{
+    const int splits = dense_gemm_splits(rows, cols, batch);
+    return splits > 1 ? (size_t)splits * batch * rows * sizeof(float) : 0;
+}
+
+// The whole batch in one GEMM launch (batch > 8). The buffer ranges are
+// 32-bit: W, X and Y each below 2 GiB.
+bool dense_gemm_supported(unsigned type, int rows, int cols, int batch)
+{
+    if (type != F32 && type != F16 && type != BF16) return false;
+    const size_t esize = type == F32 ? 4 : 2;
+    return batch > 8 && rows > 0 && cols > 0 && batch <= 65535 * kGemmTokens &&
+           (size_t)rows * cols * esize <= (size_t)INT32_MAX && (size_t)batch * cols * 4 <= (size_t)INT32_MAX &&
+           (size_t)batch * rows <= (size_t)INT32_MAX;
+}
+
+hipError_t launch_dense_gemm(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,
+    int batch, void *workspace, size_t workspace_bytes, hipStream_t s)
+{
+    if (!dense_gemm_supported(type, rows, cols, batch)) return hipErrorInvalidValue;
+    // Without room for the partial sums, one workgroup per tile covers all
+    // columns.
+    const size_t need = dense_gemm_workspace(rows, cols, batch);
+    const int splits = need && workspace && workspace_bytes >= need ? dense_gemm_splits(rows, cols, batch) : 1;
+    float *part = (float *)workspace;
+    if (type == F32) return launch_gemm<F32>(w, x, y, rows, cols, batch, splits, part, s);
+    if (type == F16) return launch_gemm<F16>(w, x, y, rows, cols, batch, splits, part, s);
+    return launch_gemm<BF16>(w, x, y, rows, cols, batch, splits, part, s);
+}
 
 hipError_t launch_dense(unsigned type, const uint8_t *w, const float *x, float *y,
     int rows, int cols, int batch, hipStream_t s)

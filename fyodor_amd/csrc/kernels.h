@@ -79,6 +79,14 @@ size_t prefill_f16_workspace(int cols, int batch);
 hipError_t launch_prefill_f16(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,
     int batch, void *workspace, hipStream_t stream);
 
+// Dense F32 / F16 / BF16 batches above 8 as one GEMM on the fp32 matrix cores
+// (dense.hip).
+// Batches of matrices with few row tiles split the columns over several
+// workgroups; their partial sums need dense_gemm_workspace bytes.
+bool dense_gemm_supported(unsigned type, int rows, int cols, int batch);
+size_t dense_gemm_workspace(int rows, int cols, int batch);
+hipError_t launch_dense_gemm(unsigned type, const uint8_t *w, const float *x, float *y, int rows, int cols,
+    int batch, void *workspace, size_t workspace_bytes, hipStream_t s);
 // Plain 16-byte-per-thread device copy (dense.hip), for counter calibration.
 hipError_t launch_copy(uint4 *dst, const uint4 *src, size_t count, hipStream_t stream);
 // Plain streaming read of `count` 16-byte elements, one workgroup per CU
@@ -109,6 +117,13 @@ hipError_t launch_rms_norm(float *x, const float *r, const float *w, float *out,
 hipError_t launch_rope_qkv(float *q, int q_stride, const float *k, int k_stride, const float *v, int v_stride,
     int count, int heads, int kv_heads, int width, const float *freq, const int *positions, int capacity, float *keys,
     float *values, hipStream_t stream);
+// Attention split over the cached positions (resident.hip): `splits`
+// workgroups per (KV head, token), then their combination; partials:
+// count * heads * splits * (width + 2) floats.
+bool attention_split_supported(int heads, int kv_heads, int width, int max_length, int splits);
+hipError_t launch_attention_split(const float *q, int q_stride, const float *keys, const float *values, float *out,
+    float *partials, const int *positions, int count, int heads, int kv_heads, int width, int max_length, int splits,
+    float scale, hipStream_t s);
 hipError_t launch_attention(const float *q, int q_stride, const float *keys, const float *values, float *out,
     float *scores, const int *positions, int count, int heads, int kv_heads, int width, int max_length, float scale,
     hipStream_t stream);

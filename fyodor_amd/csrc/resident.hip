@@ -394,6 +394,262 @@ __global__ __launch_bounds__(256) void attention(const float *__restrict__ q, in
     }
 }
 
+// ---- attention split over the cached positions (long contexts) ------------
+//
+// One token's attention reads its KV head's whole history, and one
+// workgroup per (query head, token) leaves most of the chip idle past a few
+// hundred positions. Here workgroup (kv head, split s, token) takes the
+// positions [s C, (s + 1) C) of the token's causal range (C = ceil(length /
+// splits)) for all G query heads that share the KV head, so every cached K
+// and V row is read once per token: per head g the chunk's scores
+// q_g . k_t * scale, their maximum m, e_t = e^(s_t - m), l = sum e_t and
+// o = sum e_t v_t, unnormalized (the engine's order within the chunk,
+// backend/core/llm_cpu.c:491-511). attention_combine then forms
+// out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M), M = max_s m_s. A split
+// past the range writes m = -inf, l = 0, o = 0. Partials: o at
+// partials[((i heads + head) splits + s) W], m and l after all of them
+// ([count][heads][splits][2]).
+constexpr int kSplitMaxChunk = 1024;   // positions per split (scores in LDS)
+
+template <int W, int G>
+__global__ __launch_bounds__(256) void attention_split(const float *__restrict__ q, int q_stride,
+    const float *__restrict__ keys, const float *__restrict__ values, float *__restrict__ partials,
+    const int *__restrict__ positions, int heads, int kv_heads, int max_length, int splits, float scale)
+{
+    constexpr int C = W / 64;          // float4 per lane per row
+    constexpr int U = 4;               // rows per 16 lanes in flight
+    constexpr int NG = 1024 / W;       // output groups of t (W / 4 float4 columns each)
+    static_assert(NG * W <= kSplitMaxChunk, "the groups' partial outputs fit the scores' LDS");
+    __shared__ __align__(16) float sc[G * kSplitMaxChunk];   // scores, then the groups' partial outputs
+    const int kvh = blockIdx.x, sp = blockIdx.y, tok = blockIdx.z, tid = threadIdx.x;
+    const int p = positions[tok];
+    const int length = p < 0 ? 0 : p >= max_length ? max_length : p + 1;
+    const int chunk = (length + splits - 1) / splits;
+    const int c0 = sp * chunk, n = length - c0 < chunk ? length - c0 : chunk;
+    const size_t base = ((size_t)tok * heads + (size_t)kvh * G) * splits + sp;   // partial row of head g: + g splits
+    float *ml = partials + (size_t)gridDim.z * heads * splits * W;
+    if (n <= 0) {
+        // Nothing of the range here: an empty partial.
+        for (int i = tid; i < G * W; i += 256) partials[(base + (size_t)(i / W) * splits) * W + i % W] = 0.f;
+        if (tid < G) {
+            ml[2 * (base + (size_t)tid * splits)] = -INFINITY;
+            ml[2 * (base + (size_t)tid * splits) + 1] = 0.f;
+        }
+        return;
+    }
+    const int kv4 = kv_heads * (W / 4);
+    const int l16 = tid & 15, row = tid >> 4;
+    float4 qr[G][C];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float4 *q4 = (const float4 *)(q + (size_t)tok * q_stride + (size_t)(kvh * G + g) * W);
+#pragma unroll
+        for (int c = 0; c < C; ++c) qr[g][c] = q4[l16 + 16 * c];
+    }
+    const float4 *k4 = (const float4 *)keys + (size_t)kvh * (W / 4);
+    // The output phase's first VU rows per thread (thread (group, float4
+    // column) takes rows group, group + NG, ...), requested now: V does not
+    // wait for the scores.
+    constexpr int VU = 8;
+    const int col = tid % (W / 4), grp = tid / (W / 4);
+    const float4 *v4 = (const float4 *)values + (size_t)kvh * (W / 4) + col;
+    float4 vfirst[VU];
+#pragma unroll
+    for (int u = 0; u < VU; ++u) {
+        const int t = grp + NG * u;
+        vfirst[u] = v4[(size_t)(c0 + (t < n ? t : n - 1)) * kv4];
+    }
+    for (int t0 = 0; t0 < n; t0 += 16 * U) {
+        float4 kr[U][C];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int t = t0 + 16 * u + row, tt = c0 + (t < n ? t : n - 1);
+#pragma unroll
+            for (int c = 0; c < C; ++c) kr[u][c] = k4[(size_t)tt * kv4 + l16 + 16 * c];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int t = t0 + 16 * u + row;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float s = 0.f;
+#pragma unroll
+                for (int c = 0; c < C; ++c)
+                    s += qr[g][c].x * kr[u][c].x + qr[g][c].y * kr[u][c].y + qr[g][c].z * kr[u][c].z +
+                         qr[g][c].w * kr[u][c].w;
+                for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 16);
+                if (t < n && l16 == 0) sc[g * kSplitMaxChunk + t] = s * scale;
+            }
+        }
+    }
+    __syncthreads();
+    // Per head: maximum, e_t and their sum; wavefront w takes heads w, w + 4.
+    __shared__ float mls[2 * G];
+    const int lane = tid & 63, wave = tid >> 6;
+    for (int g = wave; g < G; g += 4) {
+        float *s = sc + g * kSplitMaxChunk;
+        float m = -INFINITY;
+        for (int t = lane; t < n; t += 64) m = fmaxf(m, s[t]);
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        float sum = 0.f;
+        for (int t = lane; t < n; t += 64) {
+            const float e = expf(s[t] - m);
+            s[t] = e;
+            sum += e;
+        }
+        for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+        if (lane == 0) {
+            mls[2 * g] = m;
+            mls[2 * g + 1] = sum;
+        }
+    }
+    __syncthreads();
+    // o_g = sum_t e_t v_t: thread (group, float4 column) over t = group,
+    // group + NG, ...; every V row is read once for all G heads. Eight rows
+    // in flight per thread (each loop trip's loads issue before their first
+    // use; the first trip's were requested with the keys); every thread
+    // adds its rows in increasing t.
+    float4 acc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int t0 = grp; t0 < n; t0 += NG * VU) {
+        float4 v[VU];
+#pragma unroll
+        for (int u = 0; u < VU; ++u) {
+            const int t = t0 + NG * u;
+            v[u] = t0 == grp ? vfirst[u] : v4[(size_t)(c0 + (t < n ? t : n - 1)) * kv4];
+        }
+#pragma unroll
+        for (int u = 0; u < VU; ++u) {
+            const int t = t0 + NG * u;
+            if (t >= n) break;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float e = sc[g * kSplitMaxChunk + t];
+                acc[g].x += e * v[u].x;
+                acc[g].y += e * v[u].y;
+                acc[g].z += e * v[u].z;
+                acc[g].w += e * v[u].w;
+            }
+        }
+    }
+    __syncthreads();   // the e_t are read; their LDS takes the groups' sums
+    float4 *part = (float4 *)sc;   // [g][grp][W / 4]
+#pragma unroll
+    for (int g = 0; g < G; ++g) part[(g * NG + grp) * (W / 4) + col] = acc[g];
+    __syncthreads();
+    for (int i = tid; i < G * (W / 4); i += 256) {
+        const int g = i / (W / 4), c = i % (W / 4);
+        float4 o = part[(g * NG) * (W / 4) + c];
+        for (int k = 1; k < NG; ++k) {
+            const float4 b = part[(g * NG + k) * (W / 4) + c];
+            o = make_float4(o.x + b.x, o.y + b.y, o.z + b.z, o.w + b.w);
+        }
+        ((float4 *)(partials + (base + (size_t)g * splits) * W))[c] = o;
+    }
+    if (tid < G) {
+        ml[2 * (base + (size_t)tid * splits)] = mls[2 * tid];
+        ml[2 * (base + (size_t)tid * splits) + 1] = mls[2 * tid + 1];
+    }
+}
+
+// out[i][head] from the `splits` partials of (token i, head): thread s <
+// splits forms the split's weight f_s = e^(m_s - M) / L (M = max m, L =
+// sum_s l_s e^(m_s - M), an empty split weighs 0), then thread j < width
+// adds f_s o_s[j] over the splits in order, all their loads requested at
+// once (splits <= 256; the ABI's larger counts run in rounds of 256).
+__global__ __launch_bounds__(256) void attention_combine(const float *__restrict__ partials,
+    float *__restrict__ out, const int *__restrict__ positions, int heads, int width, int max_length, int splits)
+{
+    __shared__ float f[256];
+    __shared__ float red[8];
+    const int head = blockIdx.x, tok = blockIdx.y, tid = threadIdx.x;
+    if (positions[tok] < 0 || max_length <= 0) return;
+    const size_t base = ((size_t)tok * heads + head) * splits;
+    const float2 *ml = (const float2 *)(partials + (size_t)gridDim.y * heads * splits * width) + base;
+    float acc = 0.f;
+    for (int s0 = 0; s0 < splits; s0 += 256) {
+        const int ns = splits - s0 < 256 ? splits - s0 : 256;
+        const float2 v = tid < ns ? ml[s0 + tid] : make_float2(-INFINITY, 0.f);
+        // The maximum and the weighted sum of the l over all splits (the
+        // first round covers every split when splits <= 256).
+        float m = v.x;
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if ((tid & 63) == 0) red[tid >> 6] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        if (splits > 256) {
+            // More than one round: the other rounds' maxima too.
+            for (int s = 0; s < splits; ++s)
+                if (s < s0 || s >= s0 + ns) m = fmaxf(m, ml[s].x);
+        }
+        const float e = v.x == -INFINITY ? 0.f : expf(v.x - m);
+        float l = v.y * e;
+        for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
+        __syncthreads();
+        if ((tid & 63) == 0) red[4 + (tid >> 6)] = l;
+        __syncthreads();
+        float total = red[4] + red[5] + red[6] + red[7];
+        if (splits > 256)
+            for (int s = 0; s < splits; ++s)
+                if (s < s0 || s >= s0 + ns) {
+                    const float2 w = ml[s];
+                    if (w.x != -INFINITY) total += w.y * expf(w.x - m);
+                }
+        f[tid] = e / total;
+        __syncthreads();
+        if (tid < width) {
+            const float *po = partials + (base + s0) * width + tid;
+            constexpr int SU = 16;
+            for (int k0 = 0; k0 < ns; k0 += SU) {
+                float pv[SU];
+#pragma unroll
+                for (int u = 0; u < SU; ++u) pv[u] = po[(size_t)(k0 + u < ns ? k0 + u : ns - 1) * width];
+#pragma unroll
+                for (int u = 0; u < SU; ++u)
+                    if (k0 + u < ns) acc += f[k0 + u] * pv[u];
+            }
+        }
+        __syncthreads();
+    }
+    if (tid < width) out[((size_t)tok * heads + head) * width + tid] = acc;
+}
+
+template <int W, int G>
+void launch_split_wg(const float *q, int q_stride, const float *keys, const float *values, float *out,
+    float *partials, const int *positions, int count, int heads, int kv_heads, int max_length, int splits,
+    float scale, hipStream_t s)
+{
+    hipLaunchKernelGGL((attention_split<W, G>), dim3((unsigned)kv_heads, (unsigned)splits, (unsigned)count),
+                       dim3(256), 0, s, q, q_stride, keys, values, partials, positions, heads, kv_heads, max_length,
+                       splits, scale);
+    hipLaunchKernelGGL(attention_combine, dim3((unsigned)heads, (unsigned)count), dim3(256), 0, s, partials, out,
+                       positions, heads, W, max_length, splits);
+}
+
+template <int W>
+hipError_t launch_split_w(const float *q, int q_stride, const float *keys, const float *values, float *out,
+    float *partials, const int *positions, int count, int heads, int kv_heads, int max_length, int splits,
+    float scale, hipStream_t s)
+{
+    switch (heads / kv_heads) {
+    case 1: launch_split_wg<W, 1>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
+                                  max_length, splits, scale, s); break;
+    case 2: launch_split_wg<W, 2>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
+                                  max_length, splits, scale, s); break;
+    case 4: launch_split_wg<W, 4>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
+                                  max_length, splits, scale, s); break;
+    default:
+        if constexpr (W <= 128) {
+            launch_split_wg<W, 8>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
+                                  max_length, splits, scale, s);
+            break;
+        }
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 // out[i][j] = silu(gate[i][j]) * up[i][j] for token i = blockIdx.y (rows at
 // i times their strides), silu(x) = x / (1 + e^-x)
 // (backend/core/llm_cpu.c:336-341); four elements per thread where n and the
@@ -583,6 +839,32 @@ hipError_t launch_attention(const float *q, int q_stride, const float *keys, con
         hipLaunchKernelGGL(attention<false>, grid, dim3(256), 0, s, q, q_stride, keys, values, out, scores, positions,
                            heads, kv_heads, width, max_length, scale);
     return hipGetLastError();
+}
+
+bool attention_split_supported(int heads, int kv_heads, int width, int max_length, int splits)
+{
+    if (heads <= 0 || kv_heads <= 0 || heads % kv_heads || splits < 1 || splits > 4096 || max_length <= 0) return false;
+    const int g = heads / kv_heads;
+    if (width != 64 && width != 128 && width != 256) return false;
+    if (g != 1 && g != 2 && g != 4 && !(g == 8 && width <= 128)) return false;
+    return (max_length + splits - 1) / splits <= kSplitMaxChunk;
+}
+
+hipError_t launch_attention_split(const float *q, int q_stride, const float *keys, const float *values, float *out,
+    float *partials, const int *positions, int count, int heads, int kv_heads, int width, int max_length, int splits,
+    float scale, hipStream_t s)
+{
+    if (!attention_split_supported(heads, kv_heads, width, max_length, splits) || (q_stride & 3) ||
+        (((uintptr_t)q | (uintptr_t)keys | (uintptr_t)values | (uintptr_t)partials) & 15u))
+        return hipErrorInvalidValue;
+    if (width == 128)
+        return launch_split_w<128>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
+                                   max_length, splits, scale, s);
+    if (width == 64)
+        return launch_split_w<64>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
+                                  max_length, splits, scale, s);
+    return launch_split_w<256>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
+                               max_length, splits, scale, s);
 }
 
 hipError_t launch_greedy(const float *logits, int n, int count, const uint32_t *mask, uint32_t *ids, hipStream_t s)

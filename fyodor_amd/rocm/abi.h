@@ -72,6 +72,10 @@ typedef struct nya_resident_ops {
     /* Optional as a pair: NULL keeps gate and up in two blocks of rows. */
     int (*matvec_swiglu)(uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t, uintptr_t);
     int (*silu_pairs)(uintptr_t, uintptr_t, size_t, size_t, uintptr_t);
+    /* Optional: NULL keeps attention one workgroup per query head at every
+     * length. */
+    int (*attention_split)(uintptr_t, size_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, size_t, size_t,
+        size_t, size_t, size_t, size_t, float, uintptr_t);
 } nya_resident_ops;
 
 #define NYA_KERNEL_ABI 1U

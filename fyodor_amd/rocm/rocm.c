@@ -369,6 +369,9 @@ static int bind_all(session *s)
         nya_vendor_symbol(s->kernel_module, "nya_hip_silu_pairs", &s->resident.silu_pairs,
                           sizeof s->resident.silu_pairs))
         s->resident.matvec_swiglu = NULL, s->resident.silu_pairs = NULL;
+    if (nya_vendor_symbol(s->kernel_module, "nya_hip_attention_split", &s->resident.attention_split,
+                          sizeof s->resident.attention_split))
+        s->resident.attention_split = NULL;
     const struct { const char *symbol; void *slot; size_t size; } graphs[] = {
         {"hipStreamBeginCapture", &s->graphs.begin_capture, sizeof s->graphs.begin_capture},
         {"hipStreamEndCapture", &s->graphs.end_capture, sizeof s->graphs.end_capture},

@@ -198,6 +198,24 @@ NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t key
     uintptr_t scores, uintptr_t positions, size_t count, size_t heads, size_t kv_heads, size_t width,
     size_t max_length, float scale, uintptr_t stream);
 
+/* No counterpart in the reference's C engine (the reference's CUDA plan
+ * splits long attention the same way, CUDA/resident.inc:119-133): the
+ * attention of nya_hip_attention for long contexts, split over the cached
+ * positions. `splits` workgroups per (KV head, token) each take a
+ * contiguous share of the token's causal range for all the query heads
+ * that share the KV head (every cached K and V row read once per token),
+ * and a second launch combines their partial maxima, sums and weighted
+ * values (out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M)): the same
+ * softmax, with the exponentials rescaled per split. `partials` is scratch
+ * of count * heads * splits * (width + 2) floats (16-byte aligned). Runs for
+ * width 64, 128 or 256, heads / kv_heads in {1, 2, 4, 8} (8 up to width
+ * 128), ceil(max_length / splits) <= 1024, 16-byte aligned q, keys,
+ * values and q_stride a multiple of 4; else returns 1. q == 0 queries the
+ * shape (heads, kv_heads, width, max_length, splits): 0 where it runs. */
+NYA_HIP_EXPORT int nya_hip_attention_split(uintptr_t q, size_t q_stride, uintptr_t keys, uintptr_t values,
+    uintptr_t out, uintptr_t partials, uintptr_t positions, size_t count, size_t heads, size_t kv_heads, size_t width,
+    size_t max_length, size_t splits, float scale, uintptr_t stream);
+
 /* out[i][j] = g / (1 + e^-g) * u with g = gate[i gate_stride + j],
  * u = up[i up_stride + j], out rows of n (backend/core/llm_cpu.c:336-341,
  * SiLU of the gate times the up product). For one token out may be gate

@@ -410,6 +410,72 @@ API int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t keys, uintptr_
     return 0;
 }
 
+/* The split form: the same result computed through per-split partial
+ * softmaxes, written to `partials` first ([count][heads][splits][width],
+ * then [count][heads][splits][2] maxima and sums) and combined from there,
+ * so the plan's scratch sizing and arguments are exercised. q == 0 is the
+ * shape query. */
+API int nya_hip_attention_split(uintptr_t q, size_t q_stride, uintptr_t keys, uintptr_t values, uintptr_t out,
+    uintptr_t partials, uintptr_t positions, size_t count, size_t heads, size_t kv_heads, size_t width,
+    size_t max_length, size_t splits, float scale, uintptr_t stream)
+{
+    if (!heads || !kv_heads || heads % kv_heads || !width || !max_length || !splits ||
+        (max_length + splits - 1) / splits > 1024)
+        return 1;
+    if (!q) return 0;
+    if (!keys || !values || !out || !partials || !positions || !count || !stream) return 1;
+    if (injected_fault()) return -1;
+    const size_t kvdim = kv_heads * width;
+    float *o = (float *)partials, *ml = o + count * heads * splits * width;
+    for (size_t i = 0; i < count; ++i) {
+        const int p = ((const int *)positions)[i];
+        const size_t length = p < 0 ? 0 : (size_t)p >= max_length ? max_length : (size_t)p + 1;
+        if (!length) continue;
+        const size_t chunk = (length + splits - 1) / splits;
+        for (size_t h = 0; h < heads; ++h) {
+            const float *qh = (const float *)q + i * q_stride + h * width;
+            const size_t kvh = h / (heads / kv_heads);
+            for (size_t sp = 0; sp < splits; ++sp) {
+                const size_t row = (i * heads + h) * splits + sp, c0 = sp * chunk;
+                const size_t c1 = c0 + chunk < length ? c0 + chunk : length;
+                float m = -INFINITY, l = 0.f;
+                for (size_t t = c0; t < c1; ++t) {
+                    const float *k = (const float *)keys + t * kvdim + kvh * width;
+                    float sdot = 0.f;
+                    for (size_t j = 0; j < width; ++j) sdot += qh[j] * k[j];
+                    if (sdot * scale > m) m = sdot * scale;
+                }
+                for (size_t j = 0; j < width; ++j) o[row * width + j] = 0.f;
+                for (size_t t = c0; t < c1; ++t) {
+                    const float *k = (const float *)keys + t * kvdim + kvh * width;
+                    float sdot = 0.f;
+                    for (size_t j = 0; j < width; ++j) sdot += qh[j] * k[j];
+                    const float e = expf(sdot * scale - m);
+                    l += e;
+                    for (size_t j = 0; j < width; ++j) o[row * width + j] += e * ((const float *)values)[t * kvdim + kvh * width + j];
+                }
+                ml[2 * row] = c0 < c1 ? m : -INFINITY;
+                ml[2 * row + 1] = l;
+            }
+            float mx = -INFINITY;
+            for (size_t sp = 0; sp < splits; ++sp)
+                if (ml[2 * ((i * heads + h) * splits + sp)] > mx) mx = ml[2 * ((i * heads + h) * splits + sp)];
+            for (size_t j = 0; j < width; ++j) {
+                float num = 0.f, den = 0.f;
+                for (size_t sp = 0; sp < splits; ++sp) {
+                    const size_t row = (i * heads + h) * splits + sp;
+                    if (ml[2 * row] == -INFINITY) continue;
+                    const float f = expf(ml[2 * row] - mx);
+                    den += ml[2 * row + 1] * f;
+                    num += o[row * width + j] * f;
+                }
+                ((float *)out)[(i * heads + h) * width + j] = num / den;
+            }
+        }
+    }
+    return 0;
+}
+
 API int nya_hip_silu_mul(uintptr_t gate, size_t gate_stride, uintptr_t up, size_t up_stride, uintptr_t out,
     size_t n, size_t count, uintptr_t stream)
 {

@@ -32,7 +32,7 @@ def test_kernel_library_exports_its_header():
     assert want == {"nya_hip_abi_version", "nya_hip_weight_bytes", "nya_hip_weight_layout", "nya_hip_weight_pack",
                     "nya_hip_workspace_bytes", "nya_hip_matmul", "nya_hip_matmul_static", "nya_hip_kernel_name",
                     "nya_hip_copy", "nya_hip_read", "nya_hip_read_shaped", "nya_hip_step", "nya_hip_embed", "nya_hip_rms_norm",
-                    "nya_hip_rope_qkv", "nya_hip_attention", "nya_hip_silu_mul", "nya_hip_greedy",
+                    "nya_hip_rope_qkv", "nya_hip_attention", "nya_hip_attention_split", "nya_hip_silu_mul", "nya_hip_greedy",
                     "nya_hip_matvec_gated", "nya_hip_matvec_swiglu", "nya_hip_silu_pairs",
                     "nya_hip_matvec_normed", "nya_hip_matvec_normed_rope"}
     assert want <= exported(KERNEL_LIBRARY)
@@ -201,7 +201,7 @@ def test_prefill_dispatch_and_workspace():
     matrices the row-balanced small-N kernel takes, which run 8 tokens per
     launch up to a break-even batch (20 tokens from 8192 rows on, else 32;
     Q6_K only on rows wider than 4096 columns, up to 56); dense types need
-    none (nothing is launched)."""
+    none, and run batches above 8 on their own GEMM (nothing is launched)."""
     kern = Kernels()
 
     def pieces(cols, batch):
@@ -235,9 +235,11 @@ def test_prefill_dispatch_and_workspace():
     assert kern.workspace_bytes(Q6_K, 4096, 4096, 9) == 4096 // 32 * 136 * 32
     assert kern.workspace_bytes(Q6_K, 4096, 4096, 512) == 4096 // 32 * 136 * 512
     assert kern.kernel_name(Q6_K, 4096, 4096, 512) == "prefill_mfma"
-    for t in (F32, BF16):
+    for t in (F32, F16, BF16):
         assert kern.workspace_bytes(t, 4096, 4096, 512) == 0
-        assert kern.kernel_name(t, 4096, 4096, 512) == "skinny_dense"
+        assert kern.kernel_name(t, 4096, 4096, 8) == "skinny_dense"
+        assert kern.kernel_name(t, 4096, 4096, 9) == "dense_gemm"
+        assert kern.kernel_name(t, 4096, 4096, 512) == "dense_gemm"
 
 
 def test_model_header_layout_matches_engine(tmp_path):

@@ -87,6 +87,56 @@ def test_benchmarked_shapes_against_engine(session_lib, rocm_env, tmp_path, name
     assert out["execution"] == "resident"
 
 
+def test_long_context_against_engine(session_lib, rocm_env, tmp_path):
+    """Decode past 384 cached positions (the split attention: partial
+    softmaxes per KV head and position range, then their combination) and a
+    20-token run there, against the engine's scalar session."""
+    shape = LlamaShape(embedding=512, heads=8, kv_heads=2, hidden=1024, blocks=2, context=440, vocabulary=1000,
+                       seed=9)
+    path = tmp_path / "model.gguf"
+    write(path, shape)
+    tokens = [(i * 29 + 7) % shape.vocabulary for i in range(400)]
+    out = compare(session_lib, path, shape, "rocm", tokens, chunks=(395, 1, 20, 1))
+    print(f"long context: worst scaled logit error {out['logit']:.3g}, KV {out['kv']:.3g}", flush=True)
+    assert out["execution"] == "resident"
+
+
+def test_long_context_graph_replays_match_direct_launches(monkeypatch):
+    """Decode tokens past 384 positions replayed as the split-attention graph
+    equal direct launches bit for bit, as do the short-context ones before
+    them (both graph variants in one plan)."""
+    import numpy as np
+    from fyodor_amd import Compute
+    from fyodor_amd import model as fm
+    monkeypatch.setenv("NYA_ROCM_KERNEL_LIBRARY", str(KERNEL_LIBRARY))
+    monkeypatch.delenv("NYA_ROCM_HIP_LIBRARY", raising=False)
+    shape = fm.LlamaShape(embedding=256, heads=4, kv_heads=2, hidden=8704, blocks=2, context=440, vocabulary=1000,
+                          seed=4)
+    model = fm.LlamaModel(shape)
+    tokens = [(i * 37 + 11) % shape.vocabulary for i in range(420)]
+
+    def decode(graphs: bool):
+        monkeypatch.setenv("NYA_ROCM_GRAPHS", "1" if graphs else "0")
+        compute = Compute("rocm")
+        plan = fm.Plan(compute, model, shape.context)
+        rows = []
+        try:
+            plan.prefill(tokens[:370], 0)
+            for i in range(370, 420):
+                rows.append(plan.token(tokens[i], i).copy())
+            return rows, plan.stats()
+        finally:
+            plan.close()
+            compute.close()
+
+    graphed, g = decode(True)
+    direct, d = decode(False)
+    assert g["graph_captures"] == 2 and d["graph_replays"] == 0
+    assert g["kernel_launches"] == d["kernel_launches"]
+    for i, (a, b) in enumerate(zip(graphed, direct)):
+        assert np.array_equal(a, b), f"position {370 + i}"
+
+
 def test_python_model_plan_on_gpu(session_lib, rocm_env, tmp_path):
     """The model description built by fyodor_amd.model (no engine loader),
     planned through this repository's own compute API on the GPU, against

@@ -270,6 +270,70 @@ def test_attention(env, heads, kv_heads, width, length, count):
         dev.close()
 
 
+SPLIT_CASES = [(32, 8, 128, 4096, 1, 64), (32, 4, 64, 1000, 1, 16), (8, 8, 128, 300, 1, 8),
+               (16, 8, 128, 2000, 3, 32), (8, 2, 256, 5000, 2, 8), (32, 4, 64, 20000, 1, 32),
+               (32, 8, 128, 5, 1, 64), (32, 8, 128, 257, 33, 8), (8, 2, 128, 600, 2, 300)]
+
+
+@pytest.mark.parametrize("heads,kv_heads,width,length,count,splits", SPLIT_CASES,
+                         ids=[f"{h}/{k}x{w}-len{n}-q{c}-s{s}" for h, k, w, n, c, s in SPLIT_CASES])
+def test_attention_split(env, heads, kv_heads, width, length, count, splits):
+    """The attention split over the cached positions (every query head of a
+    KV head per workgroup, then the combination of the partial softmaxes):
+    against the float64 statement of the engine's step, and beside the
+    one-workgroup-per-head kernel; more splits than positions leave empty
+    partials."""
+    rt, L, stream = env
+    L.nya_hip_attention_split.argtypes = [_up, _sz, _up, _up, _up, _up, _up, _sz, _sz, _sz, _sz, _sz, _sz, _f, _up]
+    rng = np.random.default_rng(length * 11 + width + count + splits)
+    max_length = length + 3
+    q_stride = (heads + 2 * kv_heads) * width
+    q = rng.standard_normal((count, q_stride)).astype(np.float32)
+    keys = rng.standard_normal((max_length, kv_heads * width)).astype(np.float32)
+    values = rng.standard_normal((max_length, kv_heads * width)).astype(np.float32)
+    positions = np.arange(length - count, length, dtype=np.int32)
+    scale = float(1 / np.sqrt(np.float32(width)))
+    ref = np.concatenate([attention_ref(q[i, :heads * width], keys, values, heads, kv_heads, width, int(p) + 1,
+                                        np.float32(scale)) for i, p in enumerate(positions)])
+    dev = Dev(rt)
+    try:
+        qd, kd, vd, pd = dev.put(q), dev.put(keys), dev.put(values), dev.put(positions)
+        od, od2 = dev.empty(4 * count * heads * width), dev.empty(4 * count * heads * width)
+        part = dev.empty(4 * count * heads * splits * (width + 2))
+        sd = dev.empty(4 * count * heads * max_length) if max_length > 8192 else 0
+        print(f"attention_split {heads}/{kv_heads} x {width}, length {length}, {count} queries, {splits} splits",
+              flush=True)
+        assert L.nya_hip_attention_split(qd, q_stride, kd, vd, od, part, pd, count, heads, kv_heads, width,
+                                         max_length, splits, scale, stream) == 0
+        assert L.nya_hip_attention(qd, q_stride, kd, vd, od2, sd, pd, count, heads, kv_heads, width, max_length,
+                                   scale, stream) == 0
+        rt.sync(stream)
+        got = dev.get(od, np.empty(count * heads * width, np.float32))
+        err = scaled_error(got, ref)
+        err2 = scaled_error(got, dev.get(od2, np.empty(count * heads * width, np.float32)).astype(np.float64))
+        print(f"  scaled error {err:.3g} (against the unsplit kernel {err2:.3g})", flush=True)
+        assert err <= 1e-5 and err2 <= 1e-5
+    finally:
+        dev.close()
+
+
+def test_attention_split_declines(env):
+    rt, L, stream = env
+    L.nya_hip_attention_split.argtypes = [_up, _sz, _up, _up, _up, _up, _up, _sz, _sz, _sz, _sz, _sz, _sz, _f, _up]
+    dev = Dev(rt)
+    try:
+        p = dev.empty(4 * 4096)
+        args = lambda heads, kv, width, max_length, splits: (p, (heads + 2 * kv) * width, p, p, p, p, p, 1, heads, kv,
+                                                            width, max_length, splits, 1.0, stream)
+        assert L.nya_hip_attention_split(*args(32, 8, 80, 1000, 8)) == 1      # width 80
+        assert L.nya_hip_attention_split(*args(48, 3, 128, 1000, 8)) == 1     # 16 query heads per KV head
+        assert L.nya_hip_attention_split(*args(32, 4, 256, 1000, 8)) == 1     # 8 heads of width 256
+        assert L.nya_hip_attention_split(*args(32, 8, 128, 9000, 8)) == 1     # 1125 positions per split
+        assert L.nya_hip_attention_split(p + 4, 384, p, p, p, p, p, 1, 2, 1, 128, 100, 4, 1.0, stream) == 1  # q align
+    finally:
+        dev.close()
+
+
 def test_attention_declines(env):
     rt, L, stream = env
     dev = Dev(rt)

@@ -783,8 +783,8 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
         norm_group(px[0], pr, pg, nm, cols, lane, wave, false, false);
     }
 
-    // 4. Lane halves and wavefronts, in a fixed order. Wave 0 sums: lane
-    //    l = RT v + r takes row r of virtual tile v. All 2 KS partials are
+    // 4. Lane halves and wavefronts, in a fixed order. Wave w sums slots
+    //    64 w + l = RT v + r: row r of virtual tile v. All 2 KS partials are
     //    read before the first add, so the reads cost one LDS round trip
     //    (read, wait, add in turn measured 0.1 us slower at the end of every
     //    launch). At P = 2 the two groups of a stage are added first (lanes
@@ -793,8 +793,9 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
 #pragma unroll
     for (int v = 0; v < VT; ++v) red[wave][v][lane] = acc[v];
     __syncthreads();
-    if (wave != 0) return;
-    const int v = lane / RT, r = lane & (RT - 1);
+    // VT RT result rows: wave 0 sums the first 64, wave 1 the next (VT = 3).
+    if (64 * wave >= VT * RT) return;
+    const int v = (64 * wave + lane) / RT, r = lane & (RT - 1);
     if (v >= VT || RT * v + r >= live) return;
     float p[2 * KS];
 #pragma unroll
@@ -928,7 +929,12 @@ hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int
     const float *up = nullptr)
 {
     // Past two tiles per CU (Q6_K only): one workgroup per 32-row tile.
-    const int rpw = rows_per_workgroup(rows), rw = rpw > 2 * kTileRows ? kTileRows : rpw;
+    // Q4_K at 65..80 rows per CU stays row-balanced, three tiles per
+    // workgroup (x 4096 columns against matvec_q4k: 16640 rows 9.13 -> 8.65
+    // us, 20480 rows 9.60 -> 9.13 us; at 96 rows 10.27 -> 10.34 us, and four
+    // tiles spill).
+    const int rpw = rows_per_workgroup(rows);
+    const int rw = T == Q4_K && !GATED && 2 * rpw <= 5 * kTileRows ? rpw : rpw > 2 * kTileRows ? kTileRows : rpw;
     const int groups = cols / kGroupCols, wgs = (rows + rw - 1) / rw;
     for (int g0 = 0; g0 < groups; g0 += kChunkCols / kGroupCols) {
         const int ng = groups - g0 < kChunkCols / kGroupCols ? groups - g0 : kChunkCols / kGroupCols;
@@ -964,8 +970,10 @@ hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int
                 launch_rows_kernel<T, 1, 1, 16, 2, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
             else if (rw <= kTileRows)
                 launch_rows_kernel<T, 1, 1, 16, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
-            else
+            else if (rw <= 2 * kTileRows)
                 launch_rows_kernel<T, 2, 1, 16, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
+            else if constexpr (T == Q4_K && !GATED)
+                launch_rows_kernel<T, 3, 1, 16, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -1014,8 +1022,15 @@ template <int NP> struct RowsSlot {
 // lane j of them takes columns 4 (j % 8) .. +3 of blocks k (L / 8) + j / 8
 // (v[k], k < NP): one load reads 16 L consecutive bytes of the token. SUMS:
 // also the block sums of the quantized values (Q4_K minimums).
-template <bool SUMS, int NP>
-__device__ __forceinline__ void quantize_tokens(const float4 (&v)[NP], int lane, uint8_t *__restrict__ slot)
+struct NoHook {
+    __device__ void operator()(int) const {}
+};
+
+// hook(k) runs after block step k (the caller's weight loads, issued
+// between the steps).
+template <bool SUMS, int NP, typename Hook = NoHook>
+__device__ __forceinline__ void quantize_tokens(const float4 (&v)[NP], int lane, uint8_t *__restrict__ slot,
+    const Hook &hook = Hook{})
 {
     typedef RowsSlot<NP> S;
     typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
@@ -1059,6 +1074,7 @@ __device__ __forceinline__ void quantize_tokens(const float4 (&v)[NP], int lane,
         w[16] = pack_byte(a0 + K2, a1 + K2, a2 + K2, a3 + K2, 2);
         // The four offsets 0x4B400000 wrap away.
         if constexpr (SUMS) part[k] = (int)((a0 + a1) + (a2 + a3) - 4u * 0x4B400000u);
+        hook(k);
     }
     if (lane < 2) *(u32x4 *)(slot + S::kZero + 16 * lane) = (u32x4){0u, 0u, 0u, 0u};
     if constexpr (SUMS) {
@@ -1360,8 +1376,29 @@ __device__ __forceinline__ void smalln_rows_body(const uint8_t *__restrict__ w, 
                 vs[v] = tb + 16 * r;
                 vd[v] = tb + 2 * r;
             }
-            load_rows_fields<T, FULL, VT>(st, wb, vq, vs, R, wave, vd, groups);
-            quantize_tokens<T == Q4_K, NP>(px, lane, slot);
+            if constexpr (T == Q4_K && NP == 8 && VT == 2) {
+                // The scale words, then quant word k/2 of tile k%2 after block
+                // step k of the quantization: a wave's loads wait in the CU's
+                // queue (its sixteen waves request 160 KiB of weights), and a
+                // wave stalled on a load's issue cannot quantize behind it;
+                // interleaved, it quantizes while its later loads wait
+                // (14336 x 4096 N=8 10.0-10.5 -> 9.8-9.9 us).
+#pragma unroll
+                for (int v = 0; v < VT; ++v) load_field<T, FULL>(st[v], wb, vq[v], vs[v], R[v], wave, vd[v], groups, 0);
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_sched_barrier(0);
+                auto hook = [&](int k) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    load_field<T, FULL>(st[k & 1], wb, vq[k & 1], vs[k & 1], R[k & 1], wave, vd[k & 1], groups,
+                                        (k >> 1) + 1);
+                    asm volatile("" ::: "memory");
+                    __builtin_amdgcn_sched_barrier(0);
+                };
+                quantize_tokens<true, NP>(px, lane, slot, hook);
+            } else {
+                load_rows_fields<T, FULL, VT>(st, wb, vq, vs, R, wave, vd, groups);
+                quantize_tokens<T == Q4_K, NP>(px, lane, slot);
+            }
             // Each wave reads back only its own slot.
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
@@ -1527,10 +1564,10 @@ hipError_t launch_smalln_rows(unsigned type, const uint8_t *w, const float *x, f
     return launch_tokens<Q8_0>(w, x, y, rows, cols, batch, s);
 }
 
-// The row-balanced kernel takes up to two 32-row tiles per CU and whole
-// 256-column groups (Q8_0/Q4_0: rows of complete groups); beyond two tiles
-// per CU, Q4_K and Q6_K run one workgroup per tile (matvec_q4k, or the row
-// kernel over single tiles).
+// The row-balanced kernel takes up to two 32-row tiles per CU (Q4_K: up to
+// 80 rows) and whole 256-column groups (Q8_0/Q4_0: rows of complete groups);
+// beyond that, Q4_K and Q6_K run one workgroup per tile (matvec_q4k, or the
+// row kernel over single tiles).
 bool matvec_supported(unsigned type, int rows, int cols)
 {
     if (type != Q4_K && type != Q4_0 && type != Q8_0 && type != Q6_K) return false;
@@ -1542,7 +1579,7 @@ bool matvec_supported(unsigned type, int rows, int cols)
 const char *matvec_kernel(unsigned type, int rows, int cols)
 {
     if (!matvec_supported(type, rows, cols)) return nullptr;
-    if (type == Q4_K && rows_per_workgroup(rows) > 2 * kTileRows) return "matvec_q4k";
+    if (type == Q4_K && 2 * rows_per_workgroup(rows) > 5 * kTileRows) return "matvec_q4k";
     return "matvec_rows";
 }
 
@@ -1553,8 +1590,8 @@ hipError_t launch_matvec(unsigned type, const uint8_t *w, const float *x, float 
     if (type == Q4_0) return launch_rows<Q4_0>(w, x, y, rows, cols, s);
     if (type == Q8_0) return launch_rows<Q8_0>(w, x, y, rows, cols, s);
     if (type == Q6_K) return launch_rows<Q6_K>(w, x, y, rows, cols, s);
-    if (rows_per_workgroup(rows) <= 2 * kTileRows) return launch_rows<Q4_K>(w, x, y, rows, cols, s);
-    // More than two 32-row tiles per CU: one workgroup per tile, eight
+    if (2 * rows_per_workgroup(rows) <= 5 * kTileRows) return launch_rows<Q4_K>(w, x, y, rows, cols, s);
+    // More than 80 rows per CU: one workgroup per 32-row tile, eight
     // wavefronts, two groups each in flight.
     const int groups = cols / kGroupCols;
     const unsigned tiles = (unsigned)((rows + kTileRows - 1) / kTileRows);

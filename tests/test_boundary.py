@@ -97,6 +97,8 @@ def test_queries(kernels):
     assert L.nya_hip_weight_bytes(Q8_0, 1 << 31, 32, ctypes.byref(b)) == 1
     assert L.nya_hip_matmul(0, Q8_0, 3, 32, 16, 16, 1, 0, 0, 0) == 1          # declined, nothing enqueued
     assert kernels.kernel_name(Q4_K, 14336, 4096, 1) == "matvec_rows"          # up to 64 rows per CU
+    assert kernels.kernel_name(Q4_K, 20480, 4096, 1) == "matvec_rows"          # three tiles, up to 80 rows
+    assert kernels.kernel_name(Q4_K, 20481, 4096, 1) == "matvec_q4k"
     assert kernels.kernel_name(Q4_K, 57344, 4096, 1) == "matvec_q4k"           # one workgroup per tile
     assert kernels.kernel_name(Q8_0, 4096, 800, 1) == "smalln_mfma"            # a short last group
     assert kernels.kernel_name(Q4_K, 14336, 4096, 8) == "smalln_rows"          # digits made in the kernel

@@ -55,6 +55,7 @@ CONFIG_SHAPES = [
     (Q8_0, 4096, 4096, 1),
     (Q4_0, 4096, 4096, 1), (Q4_0, 11008, 4096, 1), (Q4_0, 4096, 11008, 1),
     (Q4_K, 4096, 4096, 1), (Q4_K, 1024, 4096, 1), (Q4_K, 14336, 4096, 1),
+    (Q4_K, 20480, 4096, 1), (Q4_K, 24576, 4096, 1), (Q4_K, 28672, 4096, 1),
     (Q6_K, 4096, 14336, 1),
     (Q4_K, 4096, 4096, 2), (Q4_K, 4096, 4096, 4), (Q4_K, 4096, 4096, 8),
     (Q4_K, 14336, 4096, 2), (Q4_K, 14336, 4096, 4), (Q4_K, 14336, 4096, 8),
@@ -72,6 +73,18 @@ def test_config_shapes(compute, oracle, type_id, rows, cols, batch):
     assert np.all(np.isfinite(y))
     err = rel_l2(y, expected)
     assert err <= REL_L2, f"relative L2 {err:.3g}"
+
+
+@pytest.mark.parametrize("rows", [20000, 16400, 20480, 20481])
+def test_q4k_three_tiles(compute, oracle, rows):
+    """Q4_K at 65..80 rows per CU (the row-balanced kernel with three
+    32-row tiles per workgroup): every row within the contract bound, the
+    last workgroup short (20000 = 253 x 79 + 13, 16400 = 252 x 65 + 20),
+    80 rows per CU exactly, and one row past it (matvec_q4k)."""
+    cols = 2048
+    w = synth.weights(Q4_K, rows, cols, rows)
+    x = synth.activations(1, cols, rows + 1)[0]
+    check_rows(oracle, w, Q4_K, x, rows, cols, compute.matvec_typed(w, rows, cols, Q4_K, x))
 
 
 def test_output_head_q6k(compute, oracle):

@@ -245,8 +245,9 @@ __global__ __launch_bounds__(256) void attention_w(const float *__restrict__ q, 
     float scale)
 {
     constexpr int C = W / 64;            // float4 per lane per row
-    constexpr int U = 4;                 // rows per 16 lanes in flight
+    constexpr int U = W <= 128 ? 8 : 4;  // rows per 16 lanes in flight
     constexpr int G = 1024 / W;          // output groups of t (W / 4 float4 columns each)
+    constexpr int VU = 8;                // V rows per thread in flight
     __shared__ float lds_scores[LDS ? kLdsScores : 1];
     __shared__ float4 part[256];
     __shared__ float red[4];
@@ -261,6 +262,16 @@ __global__ __launch_bounds__(256) void attention_w(const float *__restrict__ q, 
 #pragma unroll
     for (int c = 0; c < C; ++c) qr[c] = q4[l16 + 16 * c];
     const float4 *k4 = (const float4 *)keys + (size_t)a.kvh * (W / 4);
+    // The output phase's first VU rows of this thread (rows g, g + G, ...,
+    // column c), requested with the keys: V does not wait for the scores.
+    const int c = tid % (W / 4), g = tid / (W / 4);
+    const float4 *v4 = (const float4 *)values + (size_t)a.kvh * (W / 4) + c;
+    float4 vfirst[VU];
+#pragma unroll
+    for (int u = 0; u < VU; ++u) {
+        const int t = g + G * u;
+        vfirst[u] = v4[(size_t)(t < length ? t : length - 1) * kv4];
+    }
     float m = -INFINITY;
     for (int t0 = 0; t0 < length; t0 += 16 * U) {
         float4 kr[U][C];
@@ -297,20 +308,18 @@ __global__ __launch_bounds__(256) void attention_w(const float *__restrict__ q, 
     sum = block_reduce(sum, red, false);
     for (int t = tid; t < length; t += 256) sc[t] = sc[t] / sum;
     __syncthreads();
-    const int c = tid % (W / 4), g = tid / (W / 4);
-    const float4 *v4 = (const float4 *)values + (size_t)a.kvh * (W / 4) + c;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int t0 = g; t0 < length; t0 += 4 * G) {
-        float4 vr[4];
-        float p[4];
+    for (int t0 = g; t0 < length; t0 += VU * G) {
+        float4 vr[VU];
+        float p[VU];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < VU; ++u) {
             const int t = t0 + G * u, tt = t < length ? t : length - 1;
-            vr[u] = v4[(size_t)tt * kv4];
+            vr[u] = t0 == g ? vfirst[u] : v4[(size_t)tt * kv4];
             p[u] = t < length ? sc[tt] : 0.f;
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < VU; ++u) {
             acc.x += p[u] * vr[u].x;
             acc.y += p[u] * vr[u].y;
             acc.z += p[u] * vr[u].z;

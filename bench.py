@@ -254,7 +254,7 @@ def read_ceiling(rt, kern, stream, settle, weights, steps, warmup, mode, matvec_
     """The plain streaming read of the same weight bytes, same rotation and
     launch method as the timed matvec steps."""
     wbytes = storage_bytes(Q4_K, ROWS, COLS)
-    sink = rt.malloc(4096)
+    sink = rt.malloc(1 << 20)   # the store form writes 256 bytes per workgroup
     copies = len(weights)
 
     def launch(i):
@@ -277,7 +277,7 @@ def read_ceiling(rt, kern, stream, settle, weights, steps, warmup, mode, matvec_
 # 16-byte loads in flight per lane), workgroups per CU, and where the loads
 # land (0 registers, non-temporal; 1 registers, default cache policy; 2 LDS).
 READ_SHAPES = [(4, 32), (4, 16), (8, 16), (8, 8), (16, 8), (16, 4)]
-READ_MODES = {0: "nontemporal", 1: "default", 2: "lds"}
+READ_MODES = {0: "nontemporal", 1: "default", 2: "lds", 3: "nontemporal+store"}
 # Read sizes as multiples of the matrix's bytes (16.5 .. 264 MB).
 READ_SIZE_FACTORS = (0.5, 1, 2, 4, 8)
 
@@ -296,8 +296,9 @@ def read_structures(rt, kern, stream, settle, weights, wbytes, sink, steps: int 
                 table.append({"waves": waves, "depth": depth, "per_cu": per_cu, "loads": READ_MODES[mode],
                               "us_per_step": round(ms * 1e3, 3),
                               "frac": round(wbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
-    best = min(table, key=lambda r: r["us_per_step"])
-    return {"bytes": wbytes, "steps": steps, "best": best, "table": table}
+    best = min((r for r in table if r["loads"] != READ_MODES[3]), key=lambda r: r["us_per_step"])
+    best_store = min((r for r in table if r["loads"] == READ_MODES[3]), key=lambda r: r["us_per_step"])
+    return {"bytes": wbytes, "steps": steps, "best": best, "best_with_store": best_store, "table": table}
 
 
 def read_sizes(rt, kern, stream, settle, src_weights, wbytes, sink, best, steps: int = 200) -> dict:

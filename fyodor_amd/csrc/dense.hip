@@ -6,6 +6,7 @@
 #include "device.h"
 #include "formats.h"
 #include "kernels.h"
+#include "fyodor_hip.h"
 #include <stdint.h>
 
 namespace fy {
@@ -410,7 +411,8 @@ namespace {
 // lane per pass, and the loads either into registers (MODE 0 non-temporal,
 // MODE 1 the default cache policy) or straight into LDS (MODE 2,
 // buffer_load_dwordx4 ... lds: wavefront w's D KiB at LDS offset w D KiB,
-// waited for before the next pass reuses it). A workgroup reads one
+// waited for before the next pass reuses it); MODE 3 is MODE 0 followed by
+// an output store of 56 words per workgroup, as a matvec's y. A workgroup reads one
 // contiguous share; past it the buffer range check returns zeros.
 template <int W, int D, int MODE>
 __global__ __launch_bounds__(64 * W) void read_shaped(const uint8_t *__restrict__ src, size_t bytes, size_t share,
@@ -440,13 +442,19 @@ __global__ __launch_bounds__(64 * W) void read_shaped(const uint8_t *__restrict_
 #pragma unroll
             for (int u = 0; u < D; ++u)
                 v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                           r, (int)(pass + 1024 * (u * W + wave)) + 16 * lane, 0, MODE == 0 ? 2 : 0));
+                           r, (int)(pass + 1024 * (u * W + wave)) + 16 * lane, 0, MODE == 1 ? 0 : 2));
 #pragma unroll
             for (int u = 0; u < D; ++u) acc ^= v[u];
         }
     }
     const unsigned x = acc.x ^ acc.y ^ acc.z ^ acc.w;
-    if (x == 0x9E3779B9u) sink[blockIdx.x % kReadSinkWords] = x;
+    if (MODE == 3) {
+        // An output every real kernel has: wavefront 0 stores 56 words per
+        // workgroup (a 14336-row matvec's y share), unconditionally.
+        if (wave == 0 && lane < 56) sink[(size_t)blockIdx.x * 64 + lane] = x;
+    } else if (x == 0x9E3779B9u) {
+        sink[blockIdx.x % kReadSinkWords] = x;
+    }
 }
 
 template <int W, int D, int MODE>
@@ -464,17 +472,19 @@ hipError_t launch_shaped(const uint8_t *src, size_t bytes, size_t share, unsigne
 hipError_t launch_read_shaped(const uint4 *src, size_t count, unsigned *sink, int waves, int depth, int per_cu,
     int mode, hipStream_t stream)
 {
-    if (mode < 0 || mode > 2 || per_cu < 1 || per_cu > 4) return hipErrorInvalidValue;
+    if (mode < 0 || mode > 3 || per_cu < 1 || per_cu > 4) return hipErrorInvalidValue;
     const unsigned blocks = (unsigned)(device_cu_count() * per_cu);
     const size_t bytes = count * 16;
     const size_t share = (bytes + (size_t)1024 * blocks - 1) / ((size_t)1024 * blocks) * 1024;
     if (share > (size_t)INT32_MAX) return hipErrorInvalidValue;
+    if (mode == 3 && (size_t)blocks * 256 > NYA_HIP_READ_STORE_SINK_BYTES) return hipErrorInvalidValue;
     const uint8_t *s = (const uint8_t *)src;
 #define FY_SHAPE(w, d)                                                                                            \
     if (waves == w && depth == d) {                                                                               \
         if (mode == 0) return launch_shaped<w, d, 0>(s, bytes, share, blocks, sink, stream);                     \
         if (mode == 1) return launch_shaped<w, d, 1>(s, bytes, share, blocks, sink, stream);                     \
-        return launch_shaped<w, d, 2>(s, bytes, share, blocks, sink, stream);                                    \
+        if (mode == 2) return launch_shaped<w, d, 2>(s, bytes, share, blocks, sink, stream);                     \
+        return launch_shaped<w, d, 3>(s, bytes, share, blocks, sink, stream);                                    \
     }
     FY_SHAPE(4, 32)
     FY_SHAPE(4, 16)

@@ -135,7 +135,11 @@ NYA_HIP_EXPORT int nya_hip_read(uintptr_t src, size_t bytes, uintptr_t sink, uin
  * flight per lane, as one of the pairs 4x32, 4x16, 8x16, 8x8, 16x8, 16x4;
  * `per_cu` (1..4) workgroups per compute unit; `mode` 0 non-temporal loads
  * into registers, 1 loads with the default cache policy, 2 loads straight
- * into LDS (buffer_load_dwordx4 ... lds). Returns 1 for any other shape. */
+ * into LDS (buffer_load_dwordx4 ... lds), 3 as 0 followed by an output store
+ * of 56 words per workgroup (the store every real kernel ends with) at
+ * sink + 256 bytes per workgroup: for mode 3 `sink` holds
+ * NYA_HIP_READ_STORE_SINK_BYTES. Returns 1 for any other shape. */
+#define NYA_HIP_READ_STORE_SINK_BYTES ((size_t)1 << 20)
 NYA_HIP_EXPORT int nya_hip_read_shaped(uintptr_t src, size_t bytes, uintptr_t sink, int waves, int depth,
     int per_cu, int mode, uintptr_t stream);
 

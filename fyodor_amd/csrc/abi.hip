@@ -275,6 +275,33 @@ NYA_HIP_EXPORT int nya_hip_matvec_swiglu(uintptr_t w, unsigned type, size_t rows
                                        (int)cols, (hipStream_t)stream));
 }
 
+NYA_HIP_EXPORT int nya_hip_matvec_residual(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
+    uintptr_t res, uintptr_t norm, uintptr_t hn, uintptr_t parts, uintptr_t stream)
+{
+    size_t b;
+    if (!storage_bytes(type, rows, cols, &b) || !matvec_residual_supported(type, (int)rows, (int)cols)) return 1;
+    if (!w) return 0;   // the shape query
+    if (!x || !res || !norm || !hn || !parts || ((w | x) & 15u) || ((res | norm | hn) & 3u) || (parts & 7u)) return 1;
+    // hn and the partial sums are written while other workgroups read x.
+    if (hn < x + 4 * cols && x < hn + 4 * rows) return 1;
+    if (parts < x + 4 * cols && x < parts + 8 * NYA_HIP_NORM_PARTS) return 1;
+    if (hn < res + 4 * rows && res < hn + 4 * rows) return 1;
+    return status(launch_matvec_residual(type, (const uint8_t *)w, (const float *)x, (float *)res,
+                                         (const float *)norm, (float *)hn, (double *)parts, (int)rows, (int)cols,
+                                         (hipStream_t)stream));
+}
+
+NYA_HIP_EXPORT int nya_hip_matvec_swiglu_scaled(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t hn,
+    uintptr_t parts, float eps, uintptr_t hidden, uintptr_t stream)
+{
+    size_t b;
+    if (!storage_bytes(type, rows, cols, &b) || !matvec_swiglu_scaled_supported(type, (int)rows, (int)cols)) return 1;
+    if (!w) return 0;   // the shape query
+    if (!hn || !parts || !hidden || ((w | hn) & 15u) || (parts & 7u) || (hidden & 3u)) return 1;
+    return status(launch_matvec_swiglu_scaled(type, (const uint8_t *)w, (const float *)hn, (const double *)parts,
+                                              eps, (float *)hidden, (int)rows, (int)cols, (hipStream_t)stream));
+}
+
 NYA_HIP_EXPORT const char *nya_hip_kernel_name(unsigned type, size_t rows, size_t cols, size_t batch)
 {
     size_t b;

@@ -52,6 +52,16 @@ hipError_t launch_matvec_normed_rope(unsigned type, const uint8_t *w, const floa
 bool matvec_swiglu_supported(unsigned type, int rows, int cols);
 hipError_t launch_matvec_swiglu(unsigned type, const uint8_t *w, const float *x, float *hidden, int rows, int cols,
     hipStream_t stream);
+// The same of h * g with the norm's scale on the row sums, from the
+// partial sums of squares of launch_matvec_residual.
+bool matvec_swiglu_scaled_supported(unsigned type, int rows, int cols);
+hipError_t launch_matvec_swiglu_scaled(unsigned type, const uint8_t *w, const float *hn, const double *parts,
+    float eps, float *hidden, int rows, int cols, hipStream_t stream);
+// One token's product added into the residual in place, with h * g and the
+// partial sums of squares of h (256 doubles) for the next product.
+bool matvec_residual_supported(unsigned type, int rows, int cols);
+hipError_t launch_matvec_residual(unsigned type, const uint8_t *w, const float *x, float *res, const float *g,
+    float *hn, double *parts, int rows, int cols, hipStream_t stream);
 hipError_t launch_matvec_gated(unsigned type, const uint8_t *w, const float *gate, const float *up, float *y,
     int rows, int cols, hipStream_t stream);
 // Batches of 2..8 on the same row-balanced layout, the activation digits made

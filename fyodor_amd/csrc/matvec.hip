@@ -335,6 +335,102 @@ __device__ __forceinline__ void load_q4k(MvStage<Q4_K> &w, __amdgpu_buffer_rsrc_
     w.sl = bload16<true>(tile, vs + base, 128 * R);
 }
 
+// The residual add and RMS normalization of the decoder folded into the
+// x prologue (lane l holding elements 4 (64 q + l) .. + 3 of 256-column
+// group q, as thread 64 q + l of the norm step):
+// h = x + r (r may be null), xn = h * scale * g with
+// scale = 1 / sqrt(sum h^2 / cols + eps), the sum of squares in double in
+// the norm step's order; workgroup 0 writes h to hout.
+struct NormIn {
+    const float *r, *g;
+    float *hout;
+    float eps;
+    // Rotary step of the q|k|v rows (positions null: none): q rows [0, qd)
+    // rotated in y, k rows [qd, qd + kvd) rotated into keys and v rows into
+    // values at the position's slot, as rope_qkv does.
+    const int *positions;
+    const float *freq;
+    float *keys, *values;
+    int qd, kvd, width, capacity;
+    // Scaled products (x already h * g): the producing product's sums of
+    // squares, kNormParts of them (see ResidOut).
+    const double *parts;
+};
+
+// Sums of squares handed from a product with the residual epilogue to the
+// next product: one double per workgroup of the producer, zeros up to
+// kNormParts.
+constexpr int kNormParts = 256;
+
+// The residual epilogue of one token's product (RESID): y is the residual,
+// h = y + W x is written back in place (the addition the norm step makes),
+// hn = h * g, and parts[j] = the double sum of h^2 over workgroup j's rows
+// (parts[gridDim.x .. kNormParts) = 0).
+struct ResidOut {
+    const float *g;
+    float *hn;
+    double *parts;
+    int block;   // this workgroup's index (set in the kernel)
+};
+
+// Element e of pair (e & ~1, e | 1) turned by `angle` as rope_qkv turns it:
+// mine is the element's value, other its partner's.
+__device__ __forceinline__ float rotate_element(float mine, float other, bool odd, float angle)
+{
+#pragma clang fp contract(off)
+    const float c = cosf(angle), s = sinf(angle);
+    return odd ? other * s + mine * c : mine * c - other * s;
+}
+
+__device__ __forceinline__ double sq4(float4 h)
+{
+#pragma clang fp contract(off)
+    return (double)h.x * h.x + (double)h.y * h.y + (double)h.z * h.z + (double)h.w * h.w;
+}
+__device__ __forceinline__ float4 add4(float4 a, float4 b)
+{
+#pragma clang fp contract(off)
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+__device__ __forceinline__ float4 scale4(float4 h, float scale, float4 g)
+{
+#pragma clang fp contract(off)
+    return make_float4(h.x * scale * g.x, h.y * scale * g.y, h.z * scale * g.z, h.w * scale * g.w);
+}
+
+// A wavefront's sum of one double per lane, lanes l and l ^ o paired for
+// o = 32, 16, .., 1 as the norm step pairs them (every lane ends with the
+// same value).
+__device__ __forceinline__ double wave_sum_pairs(double s)
+{
+    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+    return s;
+}
+
+// The norm step's scale from its 16 wavefronts' sums of squares, in order.
+__device__ __forceinline__ float norm_scale(const double *part, int cols, float eps)
+{
+    double total = part[0];
+#pragma unroll
+    for (int q = 1; q < 16; ++q) total += part[q];
+    return (float)(1.0 / sqrt(total / (double)cols + (double)eps));
+}
+
+// One wavefront's share of the norm (its group in v, r and g loaded, zeros
+// for a wavefront without one): v becomes xn; `writer` (workgroup 0) stores
+// h. Every wavefront of the workgroup calls it once (one barrier).
+__device__ __forceinline__ void norm_group(float4 &v, float4 r, float4 g, const NormIn &nm, int cols, int lane,
+    int wave, bool writer, bool has_group)
+{
+    __shared__ double part[16];
+    const float4 h = nm.r ? add4(v, r) : v;
+    if (writer && has_group && nm.r) ((float4 *)nm.hout)[64 * wave + lane] = h;
+    const double s = wave_sum_pairs(sq4(h));
+    if (lane == 0) part[wave] = s;
+    __syncthreads();
+    v = scale4(h, norm_scale(part, cols, nm.eps), g);
+}
+
 // One workgroup per 32-row tile, KS wavefronts splitting its groups
 // [g0c, g0c + ngc) (one column chunk); wavefront w takes chunk groups
 // w, w + KS, ... through a RING-stage register ring.
@@ -356,11 +452,21 @@ __device__ __forceinline__ float4 gated_silu(float4 g, float4 u)
 // SWIGLU: the rows come in 16-row blocks of gate rows and up rows (tile t
 // holds gate rows 16t .. 16t + 15 as its rows 0..15, their up rows as 16..31)
 // and y receives silu(gate) * up, 16 values per tile at 16 t.
-template <int KS, int RING, bool SWIGLU = false>
+// SCALED: x is h * g of the decoder's residual h and norm weight g, and the
+// row sums are multiplied by the norm's scale 1 / sqrt(sum h^2 / cols + eps)
+// (W xn = scale W (h g)), the sum of squares from the kNormParts partial
+// sums in nm.parts that the producing product's residual epilogue wrote.
+// No workgroup waits for a reduction over the row before its products: the
+// partial sums are added while the weights load and the scale joins at the
+// final barrier. (Normalizing x in every workgroup instead, with the norm
+// step's reduction before the quantization, measured 16.0 us at
+// 28672 x 4096 against 15.3 us for the norm step followed by the product.)
+template <int KS, int RING, bool SWIGLU = false, bool SCALED = false>
 __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) void matvec_q4k(
     const uint8_t *__restrict__ w, const float *__restrict__ x, float *__restrict__ y, int rows, int cols, int g0c,
-    int ngc, int accumulate)
+    int ngc, int accumulate, NormIn nm)
 {
+    static_assert(!SCALED || 64 * KS >= kNormParts, "scaled: one partial sum per lane of the first wavefronts");
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float red[KS][64];
     const int ccols = (g0c + ngc) * kGroupCols < cols ? ngc * kGroupCols : cols - g0c * kGroupCols;
@@ -388,10 +494,22 @@ __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) vo
     // Unconditional: past the chunk the buffer range check returns zeros.
 #pragma unroll
     for (int k = 0; k < RING; ++k) px[k] = xload(wave + KS * k);
+    double pv = 0.0;
+    if constexpr (SCALED) pv = nm.parts[(64 * wave + lane) & (kNormParts - 1)];
     asm volatile("" ::: "memory");
     MvStage<Q4_K> st[RING];
 #pragma unroll
     for (int k = 0; k < RING; ++k) load_q4k(st[k], tile, R, g0c + wave + KS * k, vq, vs);
+    // The partial sums, in the same order in every workgroup: wavefront
+    // w < kNormParts / 64 adds 64 w .. 64 w + 63 (lanes l and l ^ o paired),
+    // wave 0 the wavefronts' sums in turn after the final barrier.
+    __shared__ double part[SCALED ? kNormParts / 64 : 1];
+    if constexpr (SCALED) {
+        if (wave < kNormParts / 64) {
+            pv = wave_sum_pairs(pv);
+            if (lane == 0) part[wave] = pv;
+        }
+    }
 
     // 2. Digits of this wave's groups into LDS.
     const float fmul = block_factor<Q4_K>(lane), fcorr = block_correction<Q4_K>(lane);
@@ -440,6 +558,12 @@ __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) vo
     float v = red[0][lane] + red[0][lane + 32];
 #pragma unroll
     for (int q = 1; q < KS; ++q) v += red[q][lane] + red[q][lane + 32];
+    if constexpr (SCALED) {
+        double total = part[0];
+#pragma unroll
+        for (int q = 1; q < kNormParts / 64; ++q) total += part[q];
+        v *= (float)(1.0 / sqrt(total / (double)cols + (double)nm.eps));
+    }
     if constexpr (SWIGLU) {
         // Every tile is whole (R = 32): lane l < 16 takes its up row from l + 16.
         const float up = __shfl_down(v, 16, 32);
@@ -565,78 +689,27 @@ __device__ __forceinline__ void load_rows_fields(MvStage<T> (&w)[VT], __amdgpu_b
 // and their sums are dropped.
 
 // GATED: the vector multiplied is silu(x) * up elementwise (x and up of the
-// same chunk layout), formed as each group is loaded.
-// The residual add and RMS normalization of the decoder folded into the
-// x prologue (one group per wavefront, lane l of wavefront w holding
-// elements 4 (64 w + l) .. + 3, as thread 64 w + l of the norm step):
-// h = x + r (r may be null), xn = h * scale * g with
-// scale = 1 / sqrt(sum h^2 / cols + eps), the sum of squares in double in
-// the norm step's order; workgroup 0 writes h to hout.
-struct NormIn {
-    const float *r, *g;
-    float *hout;
-    float eps;
-    // Rotary step of the q|k|v rows (positions null: none): q rows [0, qd)
-    // rotated in y, k rows [qd, qd + kvd) rotated into keys and v rows into
-    // values at the position's slot, as rope_qkv does.
-    const int *positions;
-    const float *freq;
-    float *keys, *values;
-    int qd, kvd, width, capacity;
-};
-
-// Element e of pair (e & ~1, e | 1) turned by `angle` as rope_qkv turns it:
-// mine is the element's value, other its partner's.
-__device__ __forceinline__ float rotate_element(float mine, float other, bool odd, float angle)
-{
-#pragma clang fp contract(off)
-    const float c = cosf(angle), s = sinf(angle);
-    return odd ? other * s + mine * c : mine * c - other * s;
-}
-
-__device__ __forceinline__ double sq4(float4 h)
-{
-#pragma clang fp contract(off)
-    return (double)h.x * h.x + (double)h.y * h.y + (double)h.z * h.z + (double)h.w * h.w;
-}
-__device__ __forceinline__ float4 add4(float4 a, float4 b)
-{
-#pragma clang fp contract(off)
-    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
-}
-__device__ __forceinline__ float4 scale4(float4 h, float scale, float4 g)
-{
-#pragma clang fp contract(off)
-    return make_float4(h.x * scale * g.x, h.y * scale * g.y, h.z * scale * g.z, h.w * scale * g.w);
-}
-
-// One wavefront's share of the norm (its group in v, r and g loaded, zeros
-// for a wavefront without one): v becomes xn; `writer` (workgroup 0) stores
-// h. Every wavefront of the workgroup calls it once (one barrier).
-__device__ __forceinline__ void norm_group(float4 &v, float4 r, float4 g, const NormIn &nm, int cols, int lane,
-    int wave, bool writer, bool has_group)
-{
-    __shared__ double part[16];
-    const float4 h = nm.r ? add4(v, r) : v;
-    if (writer && has_group && nm.r) ((float4 *)nm.hout)[64 * wave + lane] = h;
-    double s = sq4(h);
-    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
-    if (lane == 0) part[wave] = s;
-    __syncthreads();
-    double total = part[0];
-#pragma unroll
-    for (int q = 1; q < 16; ++q) total += part[q];
-    const float scale = (float)(1.0 / sqrt(total / (double)cols + (double)nm.eps));
-    v = scale4(h, scale, g);
-}
+// same chunk layout), formed as each group is loaded. NORM: the residual add
+// and norm of NormIn in the x prologue, one group per wavefront.
 
 template <unsigned T, int VT, int RING, int KS, int P, bool FULL, bool MULTI, bool GATED, bool NORM = false,
-    bool ROPE = false>
+    bool ROPE = false, bool RESID = false>
 __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, const float *__restrict__ x,
     const float *__restrict__ up, float *__restrict__ y, int rows, int cols, int base, int live, int g0c, int ngc,
-    int accumulate, uint8_t *sdig, float4 *smeta, float (*red)[VT][64], const NormIn &nm = NormIn{})
+    int accumulate, uint8_t *sdig, float4 *smeta, float (*red)[VT][64], const NormIn &nm = NormIn{},
+    const ResidOut &ro = ResidOut{})
 {
     static_assert(!ROPE || (NORM && VT == 1), "rotary: the normed one-tile product");
+    static_assert(!RESID || (VT * kTileRows / P <= 64 && !NORM && !GATED), "residual: wave 0 holds every row");
+    // The residual epilogue's inputs, loaded first (lane l: row slot l,
+    // clamped into the workgroup's rows; used after the reduction).
+    float res_in = 0.f, g_in = 0.f;
+    if constexpr (RESID) {
+        const int slot = (int)(threadIdx.x & 63), last = (VT * kTileRows / P < live ? VT * kTileRows / P : live) - 1;
+        const int row = base + (slot < last ? slot : last);
+        res_in = y[row];
+        g_in = ro.g[row];
+    }
     // The rotary inputs, loaded first (used after the reduction).
     int rope_position = 0;
     float rope_freq = 0.f;
@@ -796,17 +869,37 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
     // VT RT result rows: wave 0 sums the first 64, wave 1 the next (VT = 3).
     if (64 * wave >= VT * RT) return;
     const int v = (64 * wave + lane) / RT, r = lane & (RT - 1);
-    if (v >= VT || RT * v + r >= live) return;
-    float p[2 * KS];
+    auto row_sum = [&]() {
+        float p[2 * KS];
 #pragma unroll
-    for (int q = 0; q < KS; ++q) {
-        p[2 * q] = red[q][v][r];
-        p[2 * q + 1] = red[q][v][r + 32];
+        for (int q = 0; q < KS; ++q) {
+            p[2 * q] = red[q][v][r];
+            p[2 * q + 1] = red[q][v][r + 32];
+        }
+        asm volatile("" ::: "memory");
+        float sum = p[0] + p[1];
+#pragma unroll
+        for (int q = 1; q < KS; ++q) sum += p[2 * q] + p[2 * q + 1];
+        return sum;
+    };
+    if constexpr (RESID) {
+        // Every lane of wave 0 joins the sum of squares (rows past the
+        // workgroup's add zero), summed as the norm step pairs lanes.
+        double sq = 0.0;
+        if (v < VT && RT * v + r < live) {
+            const float h = res_in + row_sum();
+            y[base + RT * v + r] = h;
+            ro.hn[base + RT * v + r] = h * g_in;
+            sq = (double)h * h;
+        }
+        sq = wave_sum_pairs(sq);
+        if (lane == 0) ro.parts[ro.block] = sq;
+        if (ro.block == 0)
+            for (int i = (int)gridDim.x + lane; i < kNormParts; i += 64) ro.parts[i] = 0.0;
+        return;
     }
-    asm volatile("" ::: "memory");
-    float sum = p[0] + p[1];
-#pragma unroll
-    for (int q = 1; q < KS; ++q) sum += p[2 * q] + p[2 * q + 1];
+    if (v >= VT || RT * v + r >= live) return;
+    const float sum = row_sum();
     float *dst = y + base + RT * v + r;
     if constexpr (ROPE) {
         // Rows come in pairs within the workgroup (base and live even).
@@ -851,6 +944,27 @@ __global__ __launch_bounds__(64 * KS) void matvec_rows(const uint8_t *__restrict
     else
         matvec_rows_body<T, VT, RING, KS, P, false, MULTI, GATED>(w, x, up, y, rows, cols, base, live, g0c, ngc,
                                                                  accumulate, sdig, smeta, red);
+}
+
+// matvec_rows of one column chunk with the residual epilogue (y: the
+// residual, updated in place).
+template <unsigned T, int VT, int RING, int KS, int P, bool MULTI>
+__global__ __launch_bounds__(64 * KS) void matvec_rows_resid(const uint8_t *__restrict__ w,
+    const float *__restrict__ x, float *__restrict__ y, int rows, int cols, int rw, ResidOut ro)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ float red[KS][VT][64];
+    uint8_t *sdig = lds;
+    float4 *smeta = (float4 *)(lds + (size_t)128 * (cols / 32));
+    ro.block = xcd_block();
+    const int base = ro.block * rw, live = rows - base < rw ? rows - base : rw;
+    const int tiles = (rows + kTileRows - 1) / kTileRows, ngc = cols / kGroupCols;
+    if (rows % kTileRows == 0 || base + live <= kTileRows * (tiles - 1))
+        matvec_rows_body<T, VT, RING, KS, P, true, MULTI, false, false, false, true>(
+            w, x, nullptr, y, rows, cols, base, live, 0, ngc, 0, sdig, smeta, red, NormIn{}, ro);
+    else
+        matvec_rows_body<T, VT, RING, KS, P, false, MULTI, false, false, false, true>(
+            w, x, nullptr, y, rows, cols, base, live, 0, ngc, 0, sdig, smeta, red, NormIn{}, ro);
 }
 
 // One token's product of the normalized residual: matvec_rows with one
@@ -907,10 +1021,22 @@ int rows_per_workgroup(int rows)
 }
 
 // One launch of matvec_rows over chunk groups [g0, g0 + ng).
+// ro: the residual epilogue (one chunk, at most 64 rows per workgroup).
 template <unsigned T, int VT, int RING, int KS, int P = 1, bool GATED = false>
 void launch_rows_kernel(int wgs, size_t lds, hipStream_t s, const uint8_t *w, const float *xc, const float *uc,
-    float *y, int rows, int cols, int rw, int g0, int ng)
+    float *y, int rows, int cols, int rw, int g0, int ng, const ResidOut *ro = nullptr)
 {
+    if constexpr (!GATED && VT * kTileRows / P <= 64) {
+        if (ro) {
+            if (((ng + KS - 1) / KS + P - 1) / P > RING)
+                hipLaunchKernelGGL((matvec_rows_resid<T, VT, RING, KS, P, true>), dim3(wgs), dim3(64 * KS), lds, s, w,
+                                   xc, y, rows, cols, rw, *ro);
+            else
+                hipLaunchKernelGGL((matvec_rows_resid<T, VT, RING, KS, P, false>), dim3(wgs), dim3(64 * KS), lds, s,
+                                   w, xc, y, rows, cols, rw, *ro);
+            return;
+        }
+    }
     // A chunk has at most kChunkCols / kGroupCols groups: past KS P RING of
     // them no wavefront needs the refill code.
     if constexpr (KS * P * RING < kChunkCols / kGroupCols) {
@@ -926,7 +1052,7 @@ void launch_rows_kernel(int wgs, size_t lds, hipStream_t s, const uint8_t *w, co
 
 template <unsigned T, bool GATED = false>
 hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int cols, hipStream_t s,
-    const float *up = nullptr)
+    const float *up = nullptr, const ResidOut *ro = nullptr)
 {
     // Past two tiles per CU (Q6_K only): one workgroup per 32-row tile.
     // Q4_K at 65..80 rows per CU stays row-balanced, three tiles per
@@ -952,28 +1078,28 @@ hipError_t launch_rows(const uint8_t *w, const float *x, float *y, int rows, int
         // wavefronts of up to 256 registers.
         if constexpr (T == Q6_K) {
             if (rw <= kTileRows / 2 && deep)
-                launch_rows_kernel<T, 1, 2, 16, 2, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 1, 2, 16, 2, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng, ro);
             else if (rw <= kTileRows / 2)
-                launch_rows_kernel<T, 1, 1, 16, 2, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 1, 1, 16, 2, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng, ro);
             else if (rw <= kTileRows && rpw > 2 * kTileRows)   // one tile per workgroup (128256 x 4096: 84.7 -> 72.5 us)
-                launch_rows_kernel<T, 1, 1, 8, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 1, 1, 8, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng, ro);
             else if (rw <= kTileRows)
-                launch_rows_kernel<T, 1, 1, 16, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 1, 1, 16, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng, ro);
             else
-                launch_rows_kernel<T, 2, 1, 8, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 2, 1, 8, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng, ro);
         } else {
             // One stage per wavefront from 17 rows per CU on, also where it
             // has several groups (two stages measured 2-10 % slower).
             if (rw <= kTileRows / 2 && deep)
-                launch_rows_kernel<T, 1, 2, 16, 2, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 1, 2, 16, 2, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng, ro);
             else if (rw <= kTileRows / 2)
-                launch_rows_kernel<T, 1, 1, 16, 2, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 1, 1, 16, 2, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng, ro);
             else if (rw <= kTileRows)
-                launch_rows_kernel<T, 1, 1, 16, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 1, 1, 16, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng, ro);
             else if (rw <= 2 * kTileRows)
-                launch_rows_kernel<T, 2, 1, 16, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 2, 1, 16, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng, ro);
             else if constexpr (T == Q4_K && !GATED)
-                launch_rows_kernel<T, 3, 1, 16, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng);
+                launch_rows_kernel<T, 3, 1, 16, 1, GATED>(wgs, lds, s, w, xc, uc, y, rows, cols, rw, g0, ng, ro);
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -1598,7 +1724,7 @@ hipError_t launch_matvec(unsigned type, const uint8_t *w, const float *x, float 
     for (int g0 = 0; g0 < groups; g0 += kChunkCols / kGroupCols) {
         const int ng = groups - g0 < kChunkCols / kGroupCols ? groups - g0 : kChunkCols / kGroupCols;
         hipLaunchKernelGGL((matvec_q4k<8, 2>), dim3(tiles), dim3(512), matvec_lds(ng * kGroupCols), s, w,
-                           x + (size_t)g0 * kGroupCols, y, rows, cols, g0, ng, g0 > 0);
+                           x + (size_t)g0 * kGroupCols, y, rows, cols, g0, ng, g0 > 0, NormIn{});
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -1672,8 +1798,49 @@ hipError_t launch_matvec_swiglu(unsigned type, const uint8_t *w, const float *x,
     if (!matvec_swiglu_supported(type, rows, cols)) return hipErrorInvalidValue;
     const int groups = cols / kGroupCols;
     hipLaunchKernelGGL((matvec_q4k<8, 2, true>), dim3((unsigned)(rows / kTileRows)), dim3(512),
-                       matvec_lds(groups * kGroupCols), s, w, x, hidden, rows, cols, 0, groups, 0);
+                       matvec_lds(groups * kGroupCols), s, w, x, hidden, rows, cols, 0, groups, 0, NormIn{});
     return hipGetLastError();
+}
+
+bool matvec_swiglu_scaled_supported(unsigned type, int rows, int cols)
+{
+    return matvec_swiglu_supported(type, rows, cols);
+}
+
+hipError_t launch_matvec_swiglu_scaled(unsigned type, const uint8_t *w, const float *hn, const double *parts,
+    float eps, float *hidden, int rows, int cols, hipStream_t s)
+{
+    if (!matvec_swiglu_scaled_supported(type, rows, cols)) return hipErrorInvalidValue;
+    NormIn nm{};
+    nm.eps = eps;
+    nm.parts = parts;
+    const int groups = cols / kGroupCols;
+    hipLaunchKernelGGL((matvec_q4k<8, 2, true, true>), dim3((unsigned)(rows / kTileRows)), dim3(512),
+                       matvec_lds(groups * kGroupCols), s, w, hn, hidden, rows, cols, 0, groups, 0, nm);
+    return hipGetLastError();
+}
+
+// The residual epilogue: the row-balanced kernel at up to 64 rows per
+// workgroup (wave 0 holds every row), one column chunk, at most kNormParts
+// workgroups.
+bool matvec_residual_supported(unsigned type, int rows, int cols)
+{
+    return matvec_supported(type, rows, cols) && cols <= kChunkCols && rows_per_workgroup(rows) <= 2 * kTileRows &&
+           cu_count() <= kNormParts;
+}
+
+hipError_t launch_matvec_residual(unsigned type, const uint8_t *w, const float *x, float *res, const float *g,
+    float *hn, double *parts, int rows, int cols, hipStream_t s)
+{
+    if (!matvec_residual_supported(type, rows, cols)) return hipErrorInvalidValue;
+    const ResidOut ro{g, hn, parts, 0};
+    switch (type) {
+    case Q4_K: return launch_rows<Q4_K>(w, x, res, rows, cols, s, nullptr, &ro);
+    case Q6_K: return launch_rows<Q6_K>(w, x, res, rows, cols, s, nullptr, &ro);
+    case Q8_0: return launch_rows<Q8_0>(w, x, res, rows, cols, s, nullptr, &ro);
+    case Q4_0: return launch_rows<Q4_0>(w, x, res, rows, cols, s, nullptr, &ro);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_matvec_gated(unsigned type, const uint8_t *w, const float *gate, const float *up, float *y,

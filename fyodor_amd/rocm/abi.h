@@ -72,6 +72,12 @@ typedef struct nya_resident_ops {
     /* Optional as a pair: NULL keeps gate and up in two blocks of rows. */
     int (*matvec_swiglu)(uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t, uintptr_t);
     int (*silu_pairs)(uintptr_t, uintptr_t, size_t, size_t, uintptr_t);
+    /* Optional as a pair (with matvec_swiglu): NULL leaves the feed-forward
+     * norm a step of its own. */
+    int (*matvec_residual)(uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t,
+        uintptr_t, uintptr_t);
+    int (*matvec_swiglu_scaled)(uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t, float, uintptr_t,
+        uintptr_t);
     /* Optional: NULL keeps attention one workgroup per query head at every
      * length. */
     int (*attention_split)(uintptr_t, size_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, size_t, size_t,

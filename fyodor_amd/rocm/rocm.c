@@ -369,6 +369,12 @@ static int bind_all(session *s)
         nya_vendor_symbol(s->kernel_module, "nya_hip_silu_pairs", &s->resident.silu_pairs,
                           sizeof s->resident.silu_pairs))
         s->resident.matvec_swiglu = NULL, s->resident.silu_pairs = NULL;
+    if (!s->resident.matvec_swiglu ||
+        nya_vendor_symbol(s->kernel_module, "nya_hip_matvec_residual", &s->resident.matvec_residual,
+                          sizeof s->resident.matvec_residual) ||
+        nya_vendor_symbol(s->kernel_module, "nya_hip_matvec_swiglu_scaled", &s->resident.matvec_swiglu_scaled,
+                          sizeof s->resident.matvec_swiglu_scaled))
+        s->resident.matvec_residual = NULL, s->resident.matvec_swiglu_scaled = NULL;
     if (nya_vendor_symbol(s->kernel_module, "nya_hip_attention_split", &s->resident.attention_split,
                           sizeof s->resident.attention_split))
         s->resident.attention_split = NULL;

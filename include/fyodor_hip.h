@@ -272,6 +272,43 @@ NYA_HIP_EXPORT int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t
 NYA_HIP_EXPORT int nya_hip_matvec_swiglu(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
     uintptr_t hidden, uintptr_t stream);
 
+/* Partial sums of squares handed from nya_hip_matvec_residual to
+ * nya_hip_matvec_swiglu_scaled: doubles. */
+#define NYA_HIP_NORM_PARTS 256
+
+/* No counterpart in the reference: one decode token's product added into the
+ * decoder's residual, with what the next RMS norm needs, so that the next
+ * product can take the norm without a step of its own. res[i] += (W x)[i] for
+ * i < rows (the residual add of nya_hip_rms_norm, bit for bit: the product is
+ * nya_hip_matmul's of one column), hn[i] = res[i] * norm[i] (the new res),
+ * and parts[0 .. NYA_HIP_NORM_PARTS) the double sums of res[i]^2 over the
+ * kernel's workgroups' rows, zeros past its last (their total is the norm's
+ * sum of squares; the order differs from the norm step's). For callers that
+ * run one decode token (the resident plan): the attention output product
+ * with the feed-forward norm's inputs, read by nya_hip_matvec_swiglu_scaled.
+ * w == 0 queries the shape: 0 where it runs (Q4_K, Q6_K, Q8_0, Q4_0 with
+ * cols a multiple of 256 up to 20480, at most 64 rows per CU, on at most 256
+ * CUs), else 1; then also 1 for missing or misaligned vectors (w, x: 16
+ * bytes; res, norm, hn: 4; parts: 8) or hn or parts overlapping x, or hn
+ * overlapping res. */
+NYA_HIP_EXPORT int nya_hip_matvec_residual(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
+    uintptr_t res, uintptr_t norm, uintptr_t hn, uintptr_t parts, uintptr_t stream);
+
+/* No counterpart in the reference: nya_hip_matvec_swiglu of the decoder's
+ * normalized residual from nya_hip_matvec_residual's outputs, with the RMS
+ * norm's scale s = 1 / sqrt(sum parts / cols + eps) (backend/core/llm_cpu.c:
+ * 83-104) multiplying the gate and up row sums: hidden = silu(g) * u of
+ * g, u = s (W hn), the same in every workgroup. The scale is one number, so
+ * W (hn s) = s (W hn): no workgroup waits for a reduction over the row
+ * before its products. hidden meets the product's error bound as
+ * nya_hip_rms_norm followed by nya_hip_matvec_swiglu does, not bit for bit.
+ * For callers that run one decode token (the resident plan): the
+ * feed-forward norm's launch goes. w == 0 queries the shape: 0 where it runs
+ * (nya_hip_matvec_swiglu's shapes), else 1; then also 1 for missing or
+ * misaligned vectors (hn 16 bytes, parts 8, hidden 4). */
+NYA_HIP_EXPORT int nya_hip_matvec_swiglu_scaled(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t hn,
+    uintptr_t parts, float eps, uintptr_t hidden, uintptr_t stream);
+
 /* out[i][j] = silu(g) * u for row i of gu (count rows of 2 n floats holding
  * gate and up values in 16-element blocks: g = gu[i][32 (j / 16) + j % 16],
  * u 16 further), out rows of n (n a multiple of 16; out must not overlap gu);

@@ -266,6 +266,51 @@ API int nya_hip_matvec_swiglu(uintptr_t w, unsigned type, size_t rows, size_t co
     return rc;
 }
 
+/* One token's product added into the residual, with h * norm and 256 partial
+ * sums of squares (rows in 256 runs of ceil(rows / 256), zeros past the last
+ * run); the shapes the library takes on 256 CUs. w == 0 queries. */
+API int nya_hip_matvec_residual(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x, uintptr_t res,
+    uintptr_t norm, uintptr_t hn, uintptr_t parts, uintptr_t stream)
+{
+    if ((type != 2 && type != 8 && type != 12 && type != 14) || cols % 256 || cols > 20480 || rows > 64 * 256)
+        return 1;
+    if (!w) return 0;
+    if (!x || !res || !norm || !hn || !parts) return 1;
+    float *y = malloc(rows * sizeof(float));
+    if (!y) return -2;
+    const int rc = nya_hip_matmul(w, type, rows, cols, x, (uintptr_t)y, 1, 0, 0, stream);
+    const size_t run = (rows + 255) / 256;
+    double *ps = (double *)parts;
+    for (size_t j = 0; j < 256; ++j) ps[j] = 0.0;
+    for (size_t i = 0; !rc && i < rows; ++i) {
+        float *h = (float *)res + i;
+        *h += y[i];
+        ((float *)hn)[i] = *h * ((const float *)norm)[i];
+        ps[i / run] += (double)*h * *h;
+    }
+    free(y);
+    return rc;
+}
+
+/* The interleaved gate|up product of hn scaled by the norm of the partial
+ * sums: the mock SwiGLU product of hn * scale; its shapes. w == 0 queries. */
+API int nya_hip_matvec_swiglu_scaled(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t hn,
+    uintptr_t parts, float eps, uintptr_t hidden, uintptr_t stream)
+{
+    if (nya_hip_matvec_swiglu(0, type, rows, cols, 0, 0, stream)) return 1;
+    if (!w) return 0;
+    if (!hn || !parts || !hidden) return 1;
+    double total = 0.0;
+    for (size_t j = 0; j < 256; ++j) total += ((const double *)parts)[j];
+    const float scale = (float)(1.0 / sqrt(total / (double)cols + (double)eps));
+    float *xn = malloc(cols * sizeof(float));
+    if (!xn) return -2;
+    for (size_t i = 0; i < cols; ++i) xn[i] = ((const float *)hn)[i] * scale;
+    const int rc = nya_hip_matvec_swiglu(w, type, rows, cols, (uintptr_t)xn, hidden, stream);
+    free(xn);
+    return rc;
+}
+
 API int nya_hip_silu_pairs(uintptr_t gu, uintptr_t out, size_t n, size_t count, uintptr_t stream)
 {
     if (!gu || !out || !n || n % 16 || !count || !stream) return 1;

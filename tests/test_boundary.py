@@ -33,7 +33,8 @@ def test_kernel_library_exports_its_header():
                     "nya_hip_workspace_bytes", "nya_hip_matmul", "nya_hip_matmul_static", "nya_hip_kernel_name",
                     "nya_hip_copy", "nya_hip_read", "nya_hip_read_shaped", "nya_hip_step", "nya_hip_embed", "nya_hip_rms_norm",
                     "nya_hip_rope_qkv", "nya_hip_attention", "nya_hip_attention_split", "nya_hip_silu_mul", "nya_hip_greedy",
-                    "nya_hip_matvec_gated", "nya_hip_matvec_swiglu", "nya_hip_silu_pairs",
+                    "nya_hip_matvec_gated", "nya_hip_matvec_swiglu", "nya_hip_matvec_residual",
+                    "nya_hip_matvec_swiglu_scaled", "nya_hip_silu_pairs",
                     "nya_hip_matvec_normed", "nya_hip_matvec_normed_rope"}
     assert want <= exported(KERNEL_LIBRARY)
 

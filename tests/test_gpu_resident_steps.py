@@ -59,6 +59,8 @@ def env():
     L.nya_hip_silu_mul.argtypes = [_up, _sz, _up, _sz, _up, _sz, _sz, _up]
     L.nya_hip_matvec_gated.argtypes = [_up, _u, _sz, _sz, _up, _up, _up, _up]
     L.nya_hip_matvec_swiglu.argtypes = [_up, _u, _sz, _sz, _up, _up, _up]
+    L.nya_hip_matvec_residual.argtypes = [_up, _u, _sz, _sz, _up, _up, _up, _up, _up, _up]
+    L.nya_hip_matvec_swiglu_scaled.argtypes = [_up, _u, _sz, _sz, _up, _up, _f, _up, _up]
     L.nya_hip_matvec_normed.argtypes = [_up, _u, _sz, _sz, _up, _up, _up, _f, _up, _up, _up]
     L.nya_hip_matvec_normed_rope.argtypes = [_up, _u, _sz, _sz, _up, _up, _up, _f, _up, _up, _up, _up, _sz, _sz, _sz,
                                              _sz, _up, _up, _up]
@@ -442,6 +444,137 @@ def test_matvec_swiglu_declines(env):
     assert L.nya_hip_matvec_swiglu(0, Q6_K, 28672, 4096, 0, 0, stream) == 1    # not Q4_K
     assert L.nya_hip_matvec_swiglu(0, Q4_K, 28672, 20480, 0, 0, stream) == 1   # more than one column chunk
     assert L.nya_hip_matvec_swiglu(0, Q4_K, 28688, 4096, 0, 0, stream) == 1    # not whole 32-row blocks
+
+
+NORM_PARTS = 256
+
+
+@pytest.mark.parametrize("t,rows,cols", [(Q4_K, 4096, 4096), (Q4_K, 2048, 2048), (Q6_K, 4096, 4096),
+                                         (Q8_0, 1000, 4096), (Q4_0, 8192, 1024), (Q4_K, 16384, 256),
+                                         (Q6_K, 5010, 512)])
+def test_matvec_residual(env, t, rows, cols):
+    """The attention output product with the residual epilogue: res + W x in
+    place equals the norm step's residual add of nya_hip_matmul's product bit
+    for bit, hn = res * norm bit for bit, and partial sum j is the double sum
+    of res^2 over workgroup j's rows (ceil(rows / 256) rows each on 256 CUs:
+    16, 8, 4, 32, 64 and 20 rows; at 5010 rows the last of 251 workgroups
+    holds 10, in a short last tile), zeros past the last workgroup."""
+    rt, L, stream = env
+    kern = Kernels()
+    assert L.nya_hip_matvec_residual(0, t, rows, cols, 0, 0, 0, 0, 0, 0) == 0
+    rng = np.random.default_rng(rows + 7 * cols + t)
+    x = rng.standard_normal(cols).astype(np.float32)
+    res = (2 * rng.standard_normal(rows)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(rows)).astype(np.float32)
+    w = kern.device_weights(synth.weights(t, rows, cols, seed=rows + 2), t, rows, cols)
+    dev = Dev(rt)
+    try:
+        wd, xd, r1, r2, gd = dev.put(w), dev.put(x), dev.put(res), dev.put(res), dev.put(g)
+        hn, y, xn = dev.empty(4 * rows), dev.empty(4 * rows), dev.empty(4 * rows)
+        parts = dev.put(np.full(NORM_PARTS, 7.0))   # stale values: every entry is written
+        print(f"residual {TYPE_NAMES[t]} {rows}x{cols}", flush=True)
+        assert L.nya_hip_matvec_residual(wd, t, rows, cols, xd, r1, gd, hn, parts, stream) == 0
+        kern.matmul(wd, t, rows, cols, xd, y, 1, 0, 0, stream)
+        assert L.nya_hip_rms_norm(r2, y, gd, xn, rows, 1, 1e-5, stream) == 0   # r2 += y in place
+        rt.sync(stream)
+        bits = lambda p, n: dev.get(p, np.empty(n, np.float32)).view(np.uint32)
+        h = bits(r1, rows)
+        assert np.array_equal(h, bits(r2, rows))
+        hv = h.view(np.float32)
+        assert np.array_equal(bits(hn, rows), (hv * g).view(np.uint32))
+        ps = dev.get(parts, np.empty(NORM_PARTS, np.float64))
+    finally:
+        dev.close()
+    rw = -(-rows // 256)
+    wgs = -(-rows // rw)
+    want = np.zeros(NORM_PARTS)
+    hd = hv.astype(np.float64) ** 2
+    for j in range(wgs):
+        want[j] = hd[j * rw:(j + 1) * rw].sum()
+    assert np.all(ps[wgs:] == 0.0)
+    assert np.allclose(ps[:wgs], want[:wgs], rtol=1e-12, atol=0)
+
+
+def test_matvec_residual_declines(env):
+    rt, L, stream = env
+    q = lambda t, rows, cols: L.nya_hip_matvec_residual(0, t, rows, cols, 0, 0, 0, 0, 0, 0)
+    assert q(Q4_K, 16384, 4096) == 0      # 64 rows per CU
+    assert q(Q4_K, 16385, 4096) == 1      # 65: three tiles per workgroup
+    assert q(Q4_K, 4096, 20736) == 1      # two column chunks
+    assert q(F16, 4096, 4096) == 1
+    dev = Dev(rt)
+    try:
+        p = dev.empty(1 << 16)   # every call is refused before anything is enqueued
+        assert L.nya_hip_matvec_residual(p, Q4_K, 4096, 4096, p, p, p, p, 0, stream) == 1           # no parts
+        assert L.nya_hip_matvec_residual(p, Q4_K, 4096, 4096, p, p + 16384, p, p + 32768, p + 49156,
+                                         stream) == 1                                                 # parts align
+        assert L.nya_hip_matvec_residual(p, Q4_K, 4096, 4096, p, p, p, p + 64, p + 8, stream) == 1   # hn over x
+    finally:
+        dev.close()
+
+
+@pytest.mark.parametrize("rows,cols", [(28672, 4096), (11264, 2048), (17408, 256), (22528, 3840)])
+def test_matvec_swiglu_scaled(env, oracle, rows, cols):
+    """The gate|up product of hn = h * g with the norm's scale from partial
+    sums of squares (8B and TinyLlama shapes, one group, 15 of 16 groups):
+    within the contract bound 1e-6 (1 + sum |w xn|) on each gate and up sum
+    (backend/tests/test_quant_kernels.c:13-25) of the double-precision norm,
+    carried through silu(g) u (|d/dg| <= 1.1 |u|, |d/du| = |silu(g)|), plus
+    1e-6 of the value for the float SiLU; the norm step followed by
+    nya_hip_matvec_swiglu meets the same bound."""
+    rt, L, stream = env
+    assert L.nya_hip_matvec_swiglu_scaled(0, Q4_K, rows, cols, 0, 0, 1e-5, 0, 0) == 0
+    rng = np.random.default_rng(rows + cols + 3)
+    h = (3 * rng.standard_normal(cols)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    hd = h.astype(np.float64)
+    parts = np.zeros(NORM_PARTS)
+    run = -(-cols // 200)
+    for j in range(0, cols, run):
+        parts[j // run] = float((hd[j:j + run] ** 2).sum())
+    host = synth.weights(Q4_K, rows, cols, seed=rows + 1)
+    w = Kernels().device_weights(host, Q4_K, rows, cols)
+    dev = Dev(rt)
+    try:
+        wd, hnd, pd, xd, gd = dev.put(w), dev.put(h * g), dev.put(parts), dev.put(h), dev.put(g)
+        xn, h1, h2 = dev.empty(4 * cols), dev.empty(2 * rows), dev.empty(2 * rows)
+        print(f"swiglu scaled {rows}x{cols}", flush=True)
+        assert L.nya_hip_matvec_swiglu_scaled(wd, Q4_K, rows, cols, hnd, pd, 1e-5, h1, stream) == 0
+        assert L.nya_hip_rms_norm(xd, 0, gd, xn, cols, 1, 1e-5, stream) == 0
+        assert L.nya_hip_matvec_swiglu(wd, Q4_K, rows, cols, xn, h2, stream) == 0
+        rt.sync(stream)
+        fused = dev.get(h1, np.empty(rows // 2, np.float32))
+        steps = dev.get(h2, np.empty(rows // 2, np.float32))
+    finally:
+        dev.close()
+    xnd = hd / np.sqrt(np.mean(hd * hd) + 1e-5) * g.astype(np.float64)
+    sums, mags = oracle.contract_sums(host, Q4_K, xnd, rows, cols)
+    pick = lambda a, half: a[0].reshape(-1, 2, 16)[:, half, :].reshape(-1)
+    gs, us, gm, um = pick(sums, 0), pick(sums, 1), pick(mags, 0), pick(mags, 1)
+    silu = gs / (1 + np.exp(-gs))
+    want = silu * us
+    bound = 1.1 * np.abs(us) * 1e-6 * (1 + gm) + np.abs(silu) * 1e-6 * (1 + um) + 1e-6 * np.abs(want)
+    for name, got in (("scaled", fused), ("two steps", steps)):
+        err = np.abs(got.astype(np.float64) - want)
+        bad = ~np.isfinite(got) | (err > bound)
+        assert not bad.any(), f"{name}: {int(bad.sum())} outside, worst {float((err / bound).max()):.3g} of the bound"
+        print(f"  {name}: worst {float((err / bound).max()):.3g} of the bound", flush=True)
+
+
+def test_matvec_swiglu_scaled_declines(env):
+    rt, L, stream = env
+    q = lambda t, rows, cols: L.nya_hip_matvec_swiglu_scaled(0, t, rows, cols, 0, 0, 1e-5, 0, 0)
+    assert q(Q4_K, 28672, 4096) == 0
+    assert q(Q4_K, 8192, 4096) == 1      # 32 rows per CU: not the gate|up kernel
+    assert q(Q6_K, 28672, 4096) == 1
+    dev = Dev(rt)
+    try:
+        p = dev.empty(1 << 16)   # every call is refused before anything is enqueued
+        assert L.nya_hip_matvec_swiglu_scaled(p, Q4_K, 28672, 4096, p + 4, p, 1e-5, p, stream) == 1   # hn align
+        assert L.nya_hip_matvec_swiglu_scaled(p, Q4_K, 28672, 4096, p, p + 4, 1e-5, p, stream) == 1   # parts align
+        assert L.nya_hip_matvec_swiglu_scaled(p, Q4_K, 28672, 4096, p, 0, 1e-5, p, stream) == 1       # no parts
+    finally:
+        dev.close()
 
 
 @pytest.mark.parametrize("t,rows,cols,residual", [(Q4_K, 6144, 4096, True), (Q4_K, 6144, 4096, False),

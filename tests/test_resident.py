@@ -108,6 +108,19 @@ def test_plan_declined_when_its_workspace_exceeds_the_budget(session_lib, tmp_pa
     assert compare(session_lib, path, shape, "rocm", TOKENS[:4])["execution"] == "cpu-reference"
 
 
+def mock_without(tmp_path, entries):
+    """The mock kernel library built with `entries` renamed away."""
+    lib_dir = tmp_path / "mock"
+    lib_dir.mkdir()
+    plain = lib_dir / "libnya_mock_without.so"
+    from conftest import REPO
+    src = [str(REPO / "tests/mock/mock_hip.c"), str(REPO / "oracle/quant_oracle.c")]
+    subprocess.run(["gcc", "-std=c17", "-O1", "-fPIC", "-shared", "-D_POSIX_C_SOURCE=200809L",
+                    *[f"-D{e}=nya_mock_unused_{e}" for e in entries], *src, "-o", str(plain), "-lm", "-lpthread"],
+                   check=True)
+    return plain
+
+
 @pytest.mark.parametrize("entries,extra", [(("nya_hip_matvec_gated",), 1), (("nya_hip_matvec_normed_rope",), 1),
                                            (("nya_hip_matvec_normed", "nya_hip_matvec_normed_rope"), 2)])
 def test_plan_without_fused_step(session_lib, tmp_path, monkeypatch, entries, extra):
@@ -117,14 +130,7 @@ def test_plan_without_fused_step(session_lib, tmp_path, monkeypatch, entries, ex
     nya_hip_matvec_normed_rope: the rotary step in its epilogue) keeps the
     resident plan: the steps run apart, with `extra` more launches per block
     and decode token."""
-    lib_dir = tmp_path / "mock"
-    lib_dir.mkdir()
-    plain = lib_dir / "libnya_mock_ungated.so"
-    from conftest import REPO
-    src = [str(REPO / "tests/mock/mock_hip.c"), str(REPO / "oracle/quant_oracle.c")]
-    subprocess.run(["gcc", "-std=c17", "-O1", "-fPIC", "-shared", "-D_POSIX_C_SOURCE=200809L",
-                    *[f"-D{e}=nya_mock_unused_{e}" for e in entries], *src, "-o", str(plain), "-lm", "-lpthread"],
-                   check=True)
+    plain = mock_without(tmp_path, entries)
     shape = LlamaShape(context=16)
     path = tmp_path / "model.gguf"
     write(path, shape)
@@ -139,15 +145,26 @@ def test_plan_without_fused_step(session_lib, tmp_path, monkeypatch, entries, ex
     assert launches["unfused"] - launches["fused"] == 9 * extra * shape.blocks, launches
 
 
-def test_interleaved_gate_up(session_lib, tmp_path):
+def test_interleaved_gate_up(session_lib, tmp_path, monkeypatch):
     """A feed-forward wide enough for the library's one-token SwiGLU product
     (gate|up above 64 rows per CU): the plan lays gate and up out in 16-row
-    blocks; one-token runs take nya_hip_matvec_swiglu (no separate SiLU
-    step), runs of several nya_hip_silu_pairs; logits and cache still match
-    the engine's reference session."""
+    blocks; one-token runs take nya_hip_matvec_residual (the attention
+    output product with the residual add and the feed-forward norm's
+    inputs) and nya_hip_matvec_swiglu_scaled (from a library without the
+    pair: the output product, the norm step and nya_hip_matvec_swiglu, one
+    launch more per block and token), runs of several nya_hip_silu_pairs (no
+    separate SiLU step); logits and cache still match the engine's reference
+    session either way."""
     shape = LlamaShape(hidden=8704, context=16, types={"embedding": Q4_K, "output": Q6_K, "attention": Q4_K,
                                                         "gate_up": Q4_K, "down": Q6_K})
     path = tmp_path / "model.gguf"
     write(path, shape)
-    out = compare(session_lib, path, shape, "rocm", TOKENS[:6])
-    assert out["execution"] == "resident"
+    launches = {}
+    for name, lib in (("fused", None), ("unfused", mock_without(tmp_path, ("nya_hip_matvec_residual", "nya_hip_matvec_swiglu_scaled")))):
+        if lib is not None:
+            monkeypatch.setenv("NYA_ROCM_KERNEL_LIBRARY", str(lib))
+        out = compare(session_lib, path, shape, "rocm", TOKENS[:6])
+        assert out["execution"] == "resident"
+        launches[name] = out["stats"].kernel_launches
+    # 6 decode tokens, then chunks (5, 1, 1, 7, 1): 9 one-token runs.
+    assert launches["unfused"] - launches["fused"] == 9 * shape.blocks, launches

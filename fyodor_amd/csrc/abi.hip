@@ -448,6 +448,27 @@ NYA_HIP_EXPORT int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t
                                             (int)capacity, (hipStream_t)stream));
 }
 
+NYA_HIP_EXPORT int nya_hip_matvec_scaled_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t hn,
+    uintptr_t parts, float eps, uintptr_t y, uintptr_t positions, uintptr_t frequencies, size_t heads, size_t kv_heads,
+    size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream)
+{
+    size_t b;
+    if (!storage_bytes(type, rows, cols, &b) || !matvec_normed_rope_supported(type, (int)rows, (int)cols)) return 1;
+    if (!w) return 0;   // the shape query
+    if (!count_ok(heads) || !count_ok(kv_heads) || !count_ok(width) || width % 2 || !count_ok(capacity) ||
+        heads > (size_t)INT_MAX / width || kv_heads > (size_t)INT_MAX / width ||
+        rows != (heads + 2 * kv_heads) * width)
+        return 1;
+    if (!hn || !parts || !y || !vec(positions) || !vec(frequencies) || !vec(keys) || !vec(values) ||
+        ((w | hn) & 15u) || (parts & 7u) || (y & 3u))
+        return 1;
+    return status(launch_matvec_scaled_rope(type, (const uint8_t *)w, (const float *)hn, (const double *)parts, eps,
+                                            (float *)y, (int)rows, (int)cols, (const int *)positions,
+                                            (const float *)frequencies, (float *)keys, (float *)values,
+                                            (int)(heads * width), (int)(kv_heads * width), (int)width, (int)capacity,
+                                            (hipStream_t)stream));
+}
+
 NYA_HIP_EXPORT int nya_hip_greedy(uintptr_t logits, size_t n, size_t count, uintptr_t mask, uintptr_t ids,
     uintptr_t stream)
 {

@@ -693,13 +693,14 @@ __device__ __forceinline__ void load_rows_fields(MvStage<T> (&w)[VT], __amdgpu_b
 // and norm of NormIn in the x prologue, one group per wavefront.
 
 template <unsigned T, int VT, int RING, int KS, int P, bool FULL, bool MULTI, bool GATED, bool NORM = false,
-    bool ROPE = false, bool RESID = false>
+    bool ROPE = false, bool RESID = false, bool SCALED = false>
 __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, const float *__restrict__ x,
     const float *__restrict__ up, float *__restrict__ y, int rows, int cols, int base, int live, int g0c, int ngc,
     int accumulate, uint8_t *sdig, float4 *smeta, float (*red)[VT][64], const NormIn &nm = NormIn{},
     const ResidOut &ro = ResidOut{})
 {
-    static_assert(!ROPE || (NORM && VT == 1), "rotary: the normed one-tile product");
+    static_assert(!ROPE || ((NORM || SCALED) && VT == 1), "rotary: the normed one-tile product");
+    static_assert(!SCALED || (!NORM && !GATED && KS * 64 >= kNormParts), "scaled: x is already h * g");
     static_assert(!RESID || (VT * kTileRows / P <= 64 && !NORM && !GATED), "residual: wave 0 holds every row");
     // The residual epilogue's inputs, loaded first (lane l: row slot l,
     // clamped into the workgroup's rows; used after the reduction).
@@ -797,13 +798,26 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
         pr = __builtin_bit_cast(float4, bload16<false>(rb, 16 * lane + 1024 * wave, 0));
         pg = __builtin_bit_cast(float4, bload16<false>(gb, 16 * lane + 1024 * wave, 0));
     }
+    // SCALED: the producer's partial sums of squares, added while the
+    // weights load (as in matvec_q4k: wavefront w < kNormParts / 64 adds
+    // 64 w .. 64 w + 63, wave 0 the wavefronts' sums after the barrier).
+    __shared__ double spart[SCALED ? kNormParts / 64 : 1];
+    double pv = 0.0;
+    if constexpr (SCALED) pv = nm.parts[(64 * wave + lane) & (kNormParts - 1)];
     asm volatile("" ::: "memory");
+    auto scaled_parts = [&]() {
+        if (wave < kNormParts / 64) {
+            pv = wave_sum_pairs(pv);
+            if (lane == 0) spart[wave] = pv;
+        }
+    };
     if (ns > 0) {
         MvStage<T> st[RING][VT];
 #pragma unroll
         for (int k = 0; k < RING; ++k) stage_load(st[k], k);
 
         if constexpr (NORM) norm_group(px[0], pr, pg, nm, cols, lane, wave, base == 0, xbytes > 0);
+        if constexpr (SCALED) scaled_parts();   // after this wave's weights are requested
         // 2. Digits of this wave's groups into LDS.
         const float fmul = block_factor<T>(lane), fcorr = block_correction<T>(lane);
 #pragma unroll
@@ -854,6 +868,8 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
         // A wavefront without a group still meets the others at the norm's
         // barrier (its sum is zero).
         norm_group(px[0], pr, pg, nm, cols, lane, wave, false, false);
+    } else if constexpr (SCALED) {
+        scaled_parts();
     }
 
     // 4. Lane halves and wavefronts, in a fixed order. Wave w sums slots
@@ -899,7 +915,13 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
         return;
     }
     if (v >= VT || RT * v + r >= live) return;
-    const float sum = row_sum();
+    float sum = row_sum();
+    if constexpr (SCALED) {
+        double total = spart[0];
+#pragma unroll
+        for (int q = 1; q < kNormParts / 64; ++q) total += spart[q];
+        sum *= (float)(1.0 / sqrt(total / (double)cols + (double)nm.eps));
+    }
     float *dst = y + base + RT * v + r;
     if constexpr (ROPE) {
         // Rows come in pairs within the workgroup (base and live even).
@@ -970,7 +992,9 @@ __global__ __launch_bounds__(64 * KS) void matvec_rows_resid(const uint8_t *__re
 // One token's product of the normalized residual: matvec_rows with one
 // 256-column group per wavefront (cols <= 4096) and the norm in the x
 // prologue.
-template <unsigned T, bool ROPE = false>
+// SCALED: x is h * g with the norm's scale from nm.parts instead (see
+// matvec_q4k), the rotary step after the scale.
+template <unsigned T, bool ROPE = false, bool SCALED = false>
 __global__ __launch_bounds__(1024) void matvec_rows_norm(const uint8_t *__restrict__ w, const float *__restrict__ x,
     float *__restrict__ y, int rows, int cols, int rw, NormIn nm)
 {
@@ -981,11 +1005,11 @@ __global__ __launch_bounds__(1024) void matvec_rows_norm(const uint8_t *__restri
     const int base = xcd_block() * rw, live = rows - base < rw ? rows - base : rw;
     const int tiles = (rows + kTileRows - 1) / kTileRows, ngc = cols / kGroupCols;
     if (rows % kTileRows == 0 || base + live <= kTileRows * (tiles - 1))
-        matvec_rows_body<T, 1, 1, 16, 1, true, false, false, true, ROPE>(w, x, nullptr, y, rows, cols, base, live, 0,
-                                                                        ngc, 0, sdig, smeta, red, nm);
+        matvec_rows_body<T, 1, 1, 16, 1, true, false, false, !SCALED, ROPE, false, SCALED>(
+            w, x, nullptr, y, rows, cols, base, live, 0, ngc, 0, sdig, smeta, red, nm);
     else
-        matvec_rows_body<T, 1, 1, 16, 1, false, false, false, true, ROPE>(w, x, nullptr, y, rows, cols, base, live, 0,
-                                                                         ngc, 0, sdig, smeta, red, nm);
+        matvec_rows_body<T, 1, 1, 16, 1, false, false, false, !SCALED, ROPE, false, SCALED>(
+            w, x, nullptr, y, rows, cols, base, live, 0, ngc, 0, sdig, smeta, red, nm);
 }
 
 size_t matvec_lds(int ccols)
@@ -1764,6 +1788,28 @@ hipError_t launch_matvec_normed_rope(unsigned type, const uint8_t *w, const floa
     default: return hipErrorInvalidValue;
     }
 #undef FY_NORMED
+    return hipGetLastError();
+}
+
+hipError_t launch_matvec_scaled_rope(unsigned type, const uint8_t *w, const float *hn, const double *parts, float eps,
+    float *y, int rows, int cols, const int *positions, const float *freq, float *keys, float *values, int qd, int kvd,
+    int width, int capacity, hipStream_t s)
+{
+    if (!matvec_normed_rope_supported(type, rows, cols)) return hipErrorInvalidValue;
+    const int rw = rows_per_workgroup(rows), wgs = (rows + rw - 1) / rw;
+    NormIn nm{nullptr, nullptr, nullptr, eps, positions, freq, keys, values, qd, kvd, width, capacity};
+    nm.parts = parts;
+    const size_t lds = matvec_lds(cols);
+#define FY_SCALED(TT) \
+    hipLaunchKernelGGL((matvec_rows_norm<TT, true, true>), dim3(wgs), dim3(1024), lds, s, w, hn, y, rows, cols, rw, nm)
+    switch (type) {
+    case Q4_K: FY_SCALED(Q4_K); break;
+    case Q6_K: FY_SCALED(Q6_K); break;
+    case Q8_0: FY_SCALED(Q8_0); break;
+    case Q4_0: FY_SCALED(Q4_0); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef FY_SCALED
     return hipGetLastError();
 }
 

@@ -78,6 +78,10 @@ typedef struct nya_resident_ops {
         uintptr_t, uintptr_t);
     int (*matvec_swiglu_scaled)(uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t, float, uintptr_t,
         uintptr_t);
+    /* Optional (with matvec_residual and matvec_normed_rope): NULL keeps the
+     * attention norm inside every q|k|v workgroup. */
+    int (*matvec_scaled_rope)(uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t, float, uintptr_t,
+        uintptr_t, uintptr_t, size_t, size_t, size_t, size_t, uintptr_t, uintptr_t, uintptr_t);
     /* Optional: NULL keeps attention one workgroup per query head at every
      * length. */
     int (*attention_split)(uintptr_t, size_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, size_t, size_t,

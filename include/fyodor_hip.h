@@ -257,6 +257,22 @@ NYA_HIP_EXPORT int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t
     uintptr_t r, uintptr_t norm, float eps, uintptr_t hout, uintptr_t y, uintptr_t positions, uintptr_t frequencies,
     size_t heads, size_t kv_heads, size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream);
 
+/* No counterpart in the reference: nya_hip_matvec_normed_rope of the decoder's
+ * normalized residual from nya_hip_matvec_residual's outputs (the previous
+ * block's down product): the q|k|v row sums of W hn times the norm's scale
+ * s = 1 / sqrt(sum parts / cols + eps), then nya_hip_rope_qkv's rotary step
+ * and cache store as there. Like nya_hip_matvec_swiglu_scaled, no workgroup
+ * waits for a reduction over the row, and y meets the product's error bound
+ * as nya_hip_rms_norm followed by the product and nya_hip_rope_qkv do, not
+ * bit for bit. For callers that run one decode token (the resident plan):
+ * the attention norm of every block after the first without a reduction in
+ * each workgroup. w == 0 queries the shape: 0 where it runs (the shapes of
+ * nya_hip_matvec_normed_rope), else 1; then also 1 for missing or
+ * misaligned vectors (hn 16 bytes, parts 8, y and the rotary arguments 4). */
+NYA_HIP_EXPORT int nya_hip_matvec_scaled_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t hn,
+    uintptr_t parts, float eps, uintptr_t y, uintptr_t positions, uintptr_t frequencies, size_t heads, size_t kv_heads,
+    size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream);
+
 /* No counterpart in the reference: the gate|up product of one token with
  * the gated SiLU as its output. W (rows = 2 n, the library's layout) holds
  * the feed-forward gate and up rows interleaved in 16-row blocks: rows

@@ -592,3 +592,29 @@ API int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t rows, size
                               positions, capacity, keys, values, stream);
     return rc;
 }
+
+/* The rotary product of hn scaled by the norm of the partial sums: the mock
+ * product of hn * scale and the mock rotary step; the shapes of the normed
+ * rotary product. w == 0 queries. */
+API int nya_hip_matvec_scaled_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t hn,
+    uintptr_t parts, float eps, uintptr_t y, uintptr_t positions, uintptr_t freq, size_t heads, size_t kv_heads,
+    size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream)
+{
+    if (nya_hip_matvec_normed_rope(0, type, rows, cols, 0, 0, 0, eps, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, stream)) return 1;
+    if (!w) return 0;
+    if (!hn || !parts || !y || !heads || !kv_heads || !width || width % 2 || rows != (heads + 2 * kv_heads) * width)
+        return 1;
+    double total = 0.0;
+    for (size_t j = 0; j < 256; ++j) total += ((const double *)parts)[j];
+    const float scale = (float)(1.0 / sqrt(total / (double)cols + (double)eps));
+    float *xn = malloc(cols * sizeof(float));
+    if (!xn) return -2;
+    for (size_t i = 0; i < cols; ++i) xn[i] = ((const float *)hn)[i] * scale;
+    int rc = nya_hip_matmul(w, type, rows, cols, (uintptr_t)xn, y, 1, 0, 0, stream);
+    free(xn);
+    const size_t qd = heads * width, kvd = kv_heads * width;
+    if (!rc)
+        rc = nya_hip_rope_qkv(y, rows, y + 4 * qd, rows, y + 4 * (qd + kvd), rows, 1, heads, kv_heads, width, freq,
+                              positions, capacity, keys, values, stream);
+    return rc;
+}

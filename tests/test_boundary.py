@@ -35,7 +35,7 @@ def test_kernel_library_exports_its_header():
                     "nya_hip_rope_qkv", "nya_hip_attention", "nya_hip_attention_split", "nya_hip_silu_mul", "nya_hip_greedy",
                     "nya_hip_matvec_gated", "nya_hip_matvec_swiglu", "nya_hip_matvec_residual",
                     "nya_hip_matvec_swiglu_scaled", "nya_hip_silu_pairs",
-                    "nya_hip_matvec_normed", "nya_hip_matvec_normed_rope"}
+                    "nya_hip_matvec_normed", "nya_hip_matvec_normed_rope", "nya_hip_matvec_scaled_rope"}
     assert want <= exported(KERNEL_LIBRARY)
 
 

@@ -65,6 +65,8 @@ def env():
     L.nya_hip_matvec_normed_rope.argtypes = [_up, _u, _sz, _sz, _up, _up, _up, _f, _up, _up, _up, _up, _sz, _sz, _sz,
                                              _sz, _up, _up, _up]
     L.nya_hip_silu_pairs.argtypes = [_up, _up, _sz, _sz, _up]
+    L.nya_hip_matvec_scaled_rope.argtypes = [_up, _u, _sz, _sz, _up, _up, _f, _up, _up, _up, _sz, _sz, _sz, _sz, _up,
+                                             _up, _up]
     stream = rt.stream()
     yield rt, L, stream
     rt.sync(stream)
@@ -658,3 +660,66 @@ def test_matvec_normed_rope_equals_two_steps(env, t, heads, kv_heads, width, pos
         assert np.array_equal(bits(h1, np.empty(cols, np.float32)), bits(h2, np.empty(cols, np.float32)))
     finally:
         dev.close()
+
+
+@pytest.mark.parametrize("t,heads,kv_heads,width,position", NORMED_ROPE,
+                         ids=[f"{TYPE_NAMES[c[0]]}-{c[1]}/{c[2]}x{c[3]}-at{c[4]}" for c in NORMED_ROPE])
+def test_matvec_scaled_rope(env, oracle, t, heads, kv_heads, width, position):
+    """The rotary q|k|v product of hn = h * g with the norm's scale from
+    partial sums of squares, against nya_hip_matvec_normed_rope of h (bit for
+    bit the norm step, the product and the rotary step): the two differ only
+    in the row sums, each within the contract bound 1e-6 (1 + sum |w xn|)
+    (backend/tests/test_quant_kernels.c:13-25), so every output (a row sum,
+    or a rotation c a -/+ s b of a pair of them) is within twice the bounds
+    of its rows plus 1e-6 of its value; the cache slot of the position gets
+    the same rows within the same bound and every other slot is untouched
+    (at position 512 = capacity: nothing rotated or stored)."""
+    rt, L, stream = env
+    kern = Kernels()
+    cols, capacity = 4096, 512
+    qd, kvd = heads * width, kv_heads * width
+    rows = qd + 2 * kvd
+    assert L.nya_hip_matvec_scaled_rope(0, t, rows, cols, 0, 0, 1e-5, 0, 0, 0, 0, 0, 0, 0, 0, 0, stream) == 0
+    rng = np.random.default_rng(rows + position + 5)
+    h = (3 * rng.standard_normal(cols)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    hd = h.astype(np.float64)
+    parts = np.zeros(NORM_PARTS)
+    for j in range(0, cols, 16):
+        parts[j // 16] = float((hd[j:j + 16] ** 2).sum())
+    cache_k = rng.standard_normal((capacity, kvd)).astype(np.float32)
+    cache_v = rng.standard_normal((capacity, kvd)).astype(np.float32)
+    freq = (10000.0 ** (-np.arange(width // 2) * 2.0 / width)).astype(np.float32)
+    host = synth.weights(t, rows, cols, seed=rows)
+    w = kern.device_weights(host, t, rows, cols)
+    dev = Dev(rt)
+    try:
+        wd, xd, gd, hnd, prd = dev.put(w), dev.put(h), dev.put(g), dev.put(h * g), dev.put(parts)
+        k1, v1, k2, v2 = dev.put(cache_k), dev.put(cache_v), dev.put(cache_k), dev.put(cache_v)
+        fd, pd = dev.put(freq), dev.put(np.array([position], np.int32))
+        y1, y2 = dev.empty(4 * rows), dev.empty(4 * rows)
+        print(f"scaled_rope {TYPE_NAMES[t]} {heads}/{kv_heads} width {width} position {position}", flush=True)
+        assert L.nya_hip_matvec_scaled_rope(wd, t, rows, cols, hnd, prd, 1e-5, y1, pd, fd, heads, kv_heads, width,
+                                            capacity, k1, v1, stream) == 0
+        assert L.nya_hip_matvec_normed_rope(wd, t, rows, cols, xd, 0, gd, 1e-5, 0, y2, pd, fd, heads, kv_heads,
+                                            width, capacity, k2, v2, stream) == 0
+        rt.sync(stream)
+        got = lambda p, like: dev.get(p, np.empty_like(like))
+        a, b = got(y1, np.empty(rows, np.float32)), got(y2, np.empty(rows, np.float32))
+        ka, kb, va, vb = got(k1, cache_k), got(k2, cache_k), got(v1, cache_v), got(v2, cache_v)
+    finally:
+        dev.close()
+    xnd = hd / np.sqrt(np.mean(hd * hd) + 1e-5) * g.astype(np.float64)
+    _, mags = oracle.contract_sums(host, t, xnd, rows, cols)
+    m = 2e-6 * (1 + mags[0])
+    bound = m + m[np.arange(rows) ^ 1]
+    check = lambda x, y, bd, what: np.all(np.abs(x.astype(np.float64) - y) <= bd + 1e-6 * np.abs(y)) or \
+        pytest.fail(f"{what}: worst {float((np.abs(x.astype(np.float64) - y) / (bd + 1e-6 * np.abs(y))).max()):.3g}")
+    check(a, b, bound, "q|k|v rows")
+    others = np.arange(capacity) != position
+    assert np.array_equal(ka[others], cache_k[others]) and np.array_equal(va[others], cache_v[others])
+    if position < capacity:
+        check(ka[position], kb[position], bound[qd:qd + kvd], "cached key")
+        check(va[position], vb[position], bound[qd + kvd:], "cached value")
+    else:
+        assert np.array_equal(ka, cache_k) and np.array_equal(va, cache_v)

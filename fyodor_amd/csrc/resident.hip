@@ -562,11 +562,14 @@ __global__ __launch_bounds__(256) void attention_split(const float *__restrict__
     }
 }
 
+constexpr int kCombineOnce = 64;   // splits whose partials one thread holds in registers
+
 // out[i][head] from the `splits` partials of (token i, head): thread s <
 // splits forms the split's weight f_s = e^(m_s - M) / L (M = max m, L =
 // sum_s l_s e^(m_s - M), an empty split weighs 0), then thread j < width
 // adds f_s o_s[j] over the splits in order, all their loads requested at
 // once (splits <= 256; the ABI's larger counts run in rounds of 256).
+
 __global__ __launch_bounds__(256) void attention_combine(const float *__restrict__ partials,
     float *__restrict__ out, const int *__restrict__ positions, int heads, int width, int max_length, int splits)
 {
@@ -576,6 +579,37 @@ __global__ __launch_bounds__(256) void attention_combine(const float *__restrict
     if (positions[tok] < 0 || max_length <= 0) return;
     const size_t base = ((size_t)tok * heads + head) * splits;
     const float2 *ml = (const float2 *)(partials + (size_t)gridDim.y * heads * splits * width) + base;
+    if (splits <= kCombineOnce) {
+        // Up to kCombineOnce splits: every load at once (thread j's column of
+        // every split with the splits' m and l), so the combination waits for
+        // one memory round trip; the same arithmetic in the same order as the
+        // rounds below.
+        const float2 v = tid < splits ? ml[tid] : make_float2(-INFINITY, 0.f);
+        const float *po = partials + base * width + (tid < width ? tid : width - 1);
+        float pv[kCombineOnce];
+#pragma unroll
+        for (int u = 0; u < kCombineOnce; ++u) pv[u] = po[(size_t)(u < splits ? u : splits - 1) * width];
+        float m = v.x;
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if ((tid & 63) == 0) red[tid >> 6] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        const float e = v.x == -INFINITY ? 0.f : expf(v.x - m);
+        float l = v.y * e;
+        for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
+        if ((tid & 63) == 0) red[4 + (tid >> 6)] = l;
+        __syncthreads();
+        f[tid] = e / (red[4] + red[5] + red[6] + red[7]);
+        __syncthreads();
+        if (tid < width) {
+            float acc = 0.f;
+#pragma unroll
+            for (int u = 0; u < kCombineOnce; ++u)
+                if (u < splits) acc += f[u] * pv[u];
+            out[((size_t)tok * heads + head) * width + tid] = acc;
+        }
+        return;
+    }
     float acc = 0.f;
     for (int s0 = 0; s0 < splits; s0 += 256) {
         const int ns = splits - s0 < 256 ? splits - s0 : 256;

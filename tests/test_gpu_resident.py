@@ -88,7 +88,7 @@ def test_benchmarked_shapes_against_engine(session_lib, rocm_env, tmp_path, name
 
 
 def test_long_context_against_engine(session_lib, rocm_env, tmp_path):
-    """Decode past 384 cached positions (the split attention: partial
+    """Decode past 320 cached positions (the split attention: partial
     softmaxes per KV head and position range, then their combination) and a
     20-token run there, against the engine's scalar session."""
     shape = LlamaShape(embedding=512, heads=8, kv_heads=2, hidden=1024, blocks=2, context=440, vocabulary=1000,
@@ -102,7 +102,7 @@ def test_long_context_against_engine(session_lib, rocm_env, tmp_path):
 
 
 def test_long_context_graph_replays_match_direct_launches(monkeypatch):
-    """Decode tokens past 384 positions replayed as the split-attention graph
+    """Decode tokens past 320 positions replayed as the split-attention graph
     equal direct launches bit for bit, as do the short-context ones before
     them (both graph variants in one plan)."""
     import numpy as np
@@ -121,8 +121,8 @@ def test_long_context_graph_replays_match_direct_launches(monkeypatch):
         plan = fm.Plan(compute, model, shape.context)
         rows = []
         try:
-            plan.prefill(tokens[:370], 0)
-            for i in range(370, 420):
+            plan.prefill(tokens[:300], 0)
+            for i in range(300, 340):
                 rows.append(plan.token(tokens[i], i).copy())
             return rows, plan.stats()
         finally:
@@ -134,7 +134,7 @@ def test_long_context_graph_replays_match_direct_launches(monkeypatch):
     assert g["graph_captures"] == 2 and d["graph_replays"] == 0
     assert g["kernel_launches"] == d["kernel_launches"]
     for i, (a, b) in enumerate(zip(graphed, direct)):
-        assert np.array_equal(a, b), f"position {370 + i}"
+        assert np.array_equal(a, b), f"position {300 + i}"
 
 
 def test_python_model_plan_on_gpu(session_lib, rocm_env, tmp_path):

@@ -51,7 +51,7 @@ def test_resident_plan_matches_reference_session(session_lib, tmp_path, types):
 
 
 def test_long_context_split_attention(session_lib, tmp_path, monkeypatch):
-    """Past 384 cached positions decode tokens and runs of up to 33 tokens
+    """Past 320 cached positions decode tokens and runs of up to 33 tokens
     take the split attention (nya_hip_attention_split: partial softmaxes
     through the plan's scratch, then their combination); logits and KV still
     match the engine's reference session, and the split adds one launch per
@@ -64,10 +64,10 @@ def test_long_context_split_attention(session_lib, tmp_path, monkeypatch):
     assert split["execution"] == "resident"
     monkeypatch.setenv("NYA_ROCM_ATTENTION_SPLIT", "0")
     plain = compare(session_lib, path, shape, "rocm", tokens, chunks=(390, 1, 20, 1))
-    # The decode tokens at positions 384..389, then (after the reset and the
+    # The decode tokens at positions 320..389, then (after the reset and the
     # unsplit 390-token run) the decode at 390, the 20-token run and the
     # decode after it: one more launch per block each.
-    assert split["stats"].kernel_launches - plain["stats"].kernel_launches == shape.blocks * (6 + 3)
+    assert split["stats"].kernel_launches - plain["stats"].kernel_launches == shape.blocks * (70 + 3)
 
 
 def test_plan_declined_without_resident_steps(session_lib, tmp_path, monkeypatch):

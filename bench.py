@@ -19,7 +19,16 @@ weight matrix; weights and activations are resident in HBM before timing.
   4*rows*N) / average step time.
 - read_ceiling: a plain streaming read of the same weight bytes over the
   same rotation and launch method (nya_hip_read), the time this matvec can
-  approach.
+  approach; `structures` times every read shape of nya_hip_read_shaped
+  (wavefronts, loads in flight, workgroups per CU, load kind, and a read
+  that also stores its output as every kernel does), `sizes` the plain and
+  the fastest read at 16.5 .. 264 MB with a fit of the per-dispatch floor
+  and the streaming rate (--no-read-legs skips both).
+- traffic: HBM bytes per dispatch of the N=1 and N=8 matvecs and the read,
+  from rocprofv3 FETCH_SIZE and WRITE_SIZE passes over child runs of this
+  script (before the parent touches the GPU), scaled by what the same
+  counters read for a 256 MiB copy; roofline.traffic and n8.traffic carry
+  them (--no-traffic skips the passes).
 - cpu_baseline: the reference CPU provider (built from the reference sources
   into oracle/_ref) on the same weights, on this host's cores, at the
   reference's default thread count, at the CPUs this process may use and at
@@ -29,7 +38,12 @@ weight matrix; weights and activations are resident in HBM before timing.
   tokens/s with logits every token, and its weight bytes per token over the
   token time) and TinyLlama 1.1B (tg128 and pp512, the reference's published
   end-to-end metrics); on the 8B-class model also batched verification of
-  k draft tokens (one nya_compute_plan_verify) against k decode steps.
+  k draft tokens (one nya_compute_plan_verify) against k decode steps, and
+  tg_at_4096 (a 4096-token prefill, then decode past it); `attention` times
+  one token's attention of the 8B heads per launch, one workgroup per head
+  against the split over positions, by cached length.
+- --sweep prints one line per configuration instead: the decode, small-N and
+  prefill shapes of the benchmarked models and the dense F32/F16/BF16 GEMM.
 - prefill: the same matrix times 512 tokens through the fp16-MFMA prefill
   GEMM (one call = activation split + GEMM): useful TFLOP/s (2 M N K) against
   the dense fp16 MFMA peak, and the fp16 work the matrix cores issue (two

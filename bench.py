@@ -502,9 +502,8 @@ def cpu_baseline(weights_host: np.ndarray, x: np.ndarray, y_gpu: np.ndarray, sec
     }
 
 
-def prefill(rt, kern, stream, settle, weights, steps: int) -> dict:
-    """Q4_K 14336x4096 times PREFILL_TOKENS tokens on the prefill GEMM."""
-    m = PREFILL_TOKENS
+def prefill(rt, kern, stream, settle, weights, steps: int, m: int = PREFILL_TOKENS) -> dict:
+    """Q4_K 14336x4096 times m tokens on the prefill GEMM."""
     x = synth.activations(m, COLS, seed=99)
     x_dev, y_dev = rt.malloc(x.nbytes), rt.malloc(4 * ROWS * m)
     rt.upload(x_dev, x)
@@ -835,6 +834,8 @@ def main() -> int:
                     help="run only the plain 256 MiB device copy used to calibrate HBM byte counters")
     ap.add_argument("--prefill-steps", type=int, default=20, help="timed prefill GEMM calls (0: skip)")
     ap.add_argument("--prefill-only", action="store_true", help="run only the prefill GEMM measurement")
+    ap.add_argument("--prefill-tokens", type=int, default=PREFILL_TOKENS,
+                    help="tokens of the --prefill-only measurement (the line always uses 512)")
     ap.add_argument("--resident-tg", type=int, default=128, help="timed decode tokens of the resident plans (0: skip)")
     ap.add_argument("--resident-pp", type=int, default=512, help="prompt tokens of the timed resident prefill")
     ap.add_argument("--resident-blocks", type=int, default=0, help="override the resident models' block count")
@@ -882,7 +883,8 @@ def main() -> int:
     work = rt.malloc(max(work_bytes, 16))
 
     if args.prefill_only:
-        print(json.dumps({"prefill": prefill(rt, kern, stream, settle, weights, max(args.prefill_steps, 1))}),
+        print(json.dumps({"prefill": prefill(rt, kern, stream, settle, weights, max(args.prefill_steps, 1),
+                                             args.prefill_tokens)}),
               flush=True)
         for p in weights + [work]:
             rt.free(p)

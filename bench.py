@@ -656,8 +656,8 @@ def attention_leg(heads: int = 32, kv_heads: int = 8, width: int = 128, layers: 
     rt, kern = Runtime(), Kernels()
     L = kern.lib
     up, sz = ctypes.c_uint64, ctypes.c_size_t
-    L.nya_hip_attention.argtypes = [up, sz, up, up, up, up, up, sz, sz, sz, sz, sz, ctypes.c_float, up]
-    L.nya_hip_attention_split.argtypes = [up, sz, up, up, up, up, up, sz, sz, sz, sz, sz, sz, ctypes.c_float, up]
+    L.nya_hip_attention.argtypes = [up, sz, up, up, up, up, up, sz, sz, sz, sz, sz, sz, ctypes.c_float, up]
+    L.nya_hip_attention_split.argtypes = [up, sz, up, up, up, up, up, sz, sz, sz, sz, sz, sz, sz, ctypes.c_float, up]
     stream = rt.stream()
     max_length = LONG_CONTEXT + 64
     kv_bytes = max_length * kv_heads * width * 4
@@ -684,10 +684,10 @@ def attention_leg(heads: int = 32, kv_heads: int = 8, width: int = 128, layers: 
         def launch(i):
             if split:
                 st = L.nya_hip_attention_split(qd, q_stride, keys[i % layers], values[i % layers], od, part, pos, 1,
-                                               heads, kv_heads, width, max_length, splits, scale, stream)
+                                               heads, kv_heads, width, max_length, 0, splits, scale, stream)
             else:
                 st = L.nya_hip_attention(qd, q_stride, keys[i % layers], values[i % layers], od, 0, pos, 1, heads,
-                                         kv_heads, width, max_length, scale, stream)
+                                         kv_heads, width, max_length, 0, scale, stream)
             assert st == 0
         for i in range(20):
             launch(i)

@@ -1,5 +1,6 @@
 // extern "C" entry points of libfyodor_hip.so (declared in include/fyodor_hip.h).
 #include <limits.h>
+#include <math.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -351,15 +352,15 @@ NYA_HIP_EXPORT int nya_hip_step(uintptr_t step, unsigned token, size_t position,
 }
 
 NYA_HIP_EXPORT int nya_hip_embed(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t tokens, size_t count,
-    uintptr_t out, uintptr_t stream)
+    uintptr_t out, float scale, uintptr_t stream)
 {
     format_info f;
     if (!w || !vec(tokens) || !vec(out) || !format_of(type, &f) || !count_ok(rows) || !count_ok(cols) ||
-        cols % f.block || !tokens_ok(count))
+        cols % f.block || !tokens_ok(count) || !isfinite(scale))
         return 1;
     const size_t row_bytes = cols / f.block * f.bytes;
     return status(launch_embed((const uint8_t *)w, type, row_bytes, (int)rows, (const uint32_t *)tokens, (int)count,
-                               (int)cols, (float *)out, (hipStream_t)stream));
+                               (int)cols, (float *)out, scale, (hipStream_t)stream));
 }
 
 NYA_HIP_EXPORT int nya_hip_rms_norm(uintptr_t x, uintptr_t residual, uintptr_t weight, uintptr_t out, size_t n,
@@ -370,6 +371,43 @@ NYA_HIP_EXPORT int nya_hip_rms_norm(uintptr_t x, uintptr_t residual, uintptr_t w
         return 1;
     return status(launch_rms_norm((float *)x, (const float *)residual, (const float *)weight, (float *)out, (int)n,
                                   (int)count, epsilon, (hipStream_t)stream));
+}
+
+NYA_HIP_EXPORT int nya_hip_post_norm(uintptr_t x, uintptr_t residual, uintptr_t post, float output_scale,
+    uintptr_t weight, uintptr_t out, size_t n, size_t count, float epsilon, uintptr_t stream)
+{
+    if (!vec(x) || !vec(out) || (residual & 3u) || (post & 3u) || (post && !residual) || (weight & 3u) ||
+        !count_ok(n) || n > (size_t)kPostNormMax || !tokens_ok(count) || !(epsilon >= 0.f) || !isfinite(output_scale))
+        return 1;
+    return status(launch_post_norm((float *)x, (const float *)residual, (const float *)post, output_scale,
+                                   (const float *)weight, (float *)out, (int)n, (int)count, epsilon,
+                                   (hipStream_t)stream));
+}
+
+NYA_HIP_EXPORT int nya_hip_head_norm_rope(uintptr_t q, size_t q_stride, uintptr_t k, size_t k_stride, uintptr_t v,
+    size_t v_stride, size_t count, size_t heads, size_t kv_heads, size_t width, uintptr_t q_norm, uintptr_t k_norm,
+    float epsilon, uintptr_t frequencies, uintptr_t positions, size_t capacity, uintptr_t keys, uintptr_t values,
+    uintptr_t stream)
+{
+    if (!vec(q) || !vec(q_norm) || !vec(frequencies) || !vec(positions) || !tokens_ok(count) || !count_ok(heads) ||
+        !count_ok(kv_heads) || !count_ok(width) || width % 2 || width > 256 || !count_ok(capacity) ||
+        heads > 65535 || kv_heads > 65535 || heads + 2 * kv_heads > 65535 || !(epsilon >= 0.f) ||
+        q_stride < heads * width || q_stride > (size_t)INT_MAX || capacity > (size_t)INT_MAX / (kv_heads * width))
+        return 1;
+    if (k && (!vec(k) || !vec(v) || !vec(k_norm) || !vec(keys) || !vec(values) || k_stride < kv_heads * width ||
+              v_stride < kv_heads * width || k_stride > (size_t)INT_MAX || v_stride > (size_t)INT_MAX))
+        return 1;
+    return status(launch_head_norm_rope((float *)q, (int)q_stride, (const float *)k, (int)k_stride,
+                                        (const float *)v, (int)v_stride, (int)count, (int)heads, (int)kv_heads,
+                                        (int)width, (const float *)q_norm, (const float *)k_norm, epsilon,
+                                        (const float *)frequencies, (const int *)positions, (int)capacity,
+                                        (float *)keys, (float *)values, (hipStream_t)stream));
+}
+
+NYA_HIP_EXPORT int nya_hip_softcap(uintptr_t x, size_t n, float cap, uintptr_t stream)
+{
+    if (!vec(x) || !n || !(cap > 0.f) || !isfinite(cap)) return 1;
+    return status(launch_softcap((float *)x, n, cap, (hipStream_t)stream));
 }
 
 NYA_HIP_EXPORT int nya_hip_rope_qkv(uintptr_t q, size_t q_stride, uintptr_t k, size_t k_stride, uintptr_t v,
@@ -390,22 +428,23 @@ NYA_HIP_EXPORT int nya_hip_rope_qkv(uintptr_t q, size_t q_stride, uintptr_t k, s
 
 NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t keys, uintptr_t values, uintptr_t out,
     uintptr_t scores, uintptr_t positions, size_t count, size_t heads, size_t kv_heads, size_t width,
-    size_t max_length, float scale, uintptr_t stream)
+    size_t max_length, size_t window, float scale, uintptr_t stream)
 {
     if (!vec(q) || !vec(keys) || !vec(values) || !vec(out) || !vec(positions) || (scores & 3u) ||
         !tokens_ok(count) || !count_ok(heads) || !count_ok(kv_heads) || !count_ok(width) || width > 256 ||
         !count_ok(max_length) || heads % kv_heads || kv_heads > (size_t)INT_MAX / width ||
         q_stride < heads * width || q_stride > (size_t)INT_MAX || (max_length > 8192 && !scores) ||
-        heads > (size_t)INT_MAX / max_length)
+        heads > (size_t)INT_MAX / max_length || window > (size_t)INT_MAX)
         return 1;
     return status(launch_attention((const float *)q, (int)q_stride, (const float *)keys, (const float *)values,
                                    (float *)out, (float *)scores, (const int *)positions, (int)count, (int)heads,
-                                   (int)kv_heads, (int)width, (int)max_length, scale, (hipStream_t)stream));
+                                   (int)kv_heads, (int)width, (int)max_length, (int)window, scale,
+                                   (hipStream_t)stream));
 }
 
 NYA_HIP_EXPORT int nya_hip_attention_split(uintptr_t q, size_t q_stride, uintptr_t keys, uintptr_t values,
     uintptr_t out, uintptr_t partials, uintptr_t positions, size_t count, size_t heads, size_t kv_heads, size_t width,
-    size_t max_length, size_t splits, float scale, uintptr_t stream)
+    size_t max_length, size_t window, size_t splits, float scale, uintptr_t stream)
 {
     if (!q)   // the shape query
         return count_ok(heads) && count_ok(kv_heads) && count_ok(width) && count_ok(max_length) &&
@@ -415,14 +454,14 @@ NYA_HIP_EXPORT int nya_hip_attention_split(uintptr_t q, size_t q_stride, uintptr
     if (!vec(q) || !vec(keys) || !vec(values) || !vec(out) || !vec(positions) || !partials || !tokens_ok(count) ||
         !count_ok(heads) || !count_ok(kv_heads) || !count_ok(width) || !count_ok(max_length) || !count_ok(splits) ||
         q_stride < heads * width || q_stride > (size_t)INT_MAX || heads > 4096 || splits > 4096 ||
-        max_length > (size_t)INT_MAX ||
+        max_length > (size_t)INT_MAX || window > (size_t)INT_MAX ||
         !attention_split_supported((int)heads, (int)kv_heads, (int)width, (int)max_length, (int)splits) ||
         (q_stride & 3u) || ((q | keys | values | partials) & 15u))
         return 1;
     return status(launch_attention_split((const float *)q, (int)q_stride, (const float *)keys, (const float *)values,
                                          (float *)out, (float *)partials, (const int *)positions, (int)count,
-                                         (int)heads, (int)kv_heads, (int)width, (int)max_length, (int)splits, scale,
-                                         (hipStream_t)stream));
+                                         (int)heads, (int)kv_heads, (int)width, (int)max_length, (int)window,
+                                         (int)splits, scale, (hipStream_t)stream));
 }
 
 NYA_HIP_EXPORT int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
@@ -485,19 +524,33 @@ NYA_HIP_EXPORT int nya_hip_silu_pairs(uintptr_t gu, uintptr_t out, size_t n, siz
     return status(launch_silu_pairs((const float *)gu, (float *)out, (int)n, (int)count, (hipStream_t)stream));
 }
 
-NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, size_t gate_stride, uintptr_t up, size_t up_stride,
-    uintptr_t out, size_t n, size_t count, uintptr_t stream)
+// The checks of the gated activations: one token may be rewritten in place
+// (out = gate); across tokens the output must not overlap either input.
+static bool gated_ok(uintptr_t gate, size_t gate_stride, uintptr_t up, size_t up_stride, uintptr_t out, size_t n,
+    size_t count)
 {
     if (!vec(gate) || !vec(up) || !vec(out) || !count_ok(n) || !tokens_ok(count) || gate_stride < n ||
         up_stride < n || gate_stride > (size_t)INT_MAX || up_stride > (size_t)INT_MAX)
-        return 1;
-    // One token may be rewritten in place (out = gate); across tokens the
-    // output must not overlap either input.
+        return false;
     const size_t out_end = out + count * n * sizeof(float);
     const size_t gate_end = gate + ((count - 1) * gate_stride + n) * sizeof(float);
     const size_t up_end = up + ((count - 1) * up_stride + n) * sizeof(float);
-    if (count > 1 && ((out < gate_end && gate < out_end) || (out < up_end && up < out_end))) return 1;
+    return !(count > 1 && ((out < gate_end && gate < out_end) || (out < up_end && up < out_end)));
+}
+
+NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, size_t gate_stride, uintptr_t up, size_t up_stride,
+    uintptr_t out, size_t n, size_t count, uintptr_t stream)
+{
+    if (!gated_ok(gate, gate_stride, up, up_stride, out, n, count)) return 1;
     return status(launch_silu_mul((const float *)gate, (int)gate_stride, (const float *)up, (int)up_stride,
+                                  (float *)out, (int)n, (int)count, (hipStream_t)stream));
+}
+
+NYA_HIP_EXPORT int nya_hip_gelu_mul(uintptr_t gate, size_t gate_stride, uintptr_t up, size_t up_stride,
+    uintptr_t out, size_t n, size_t count, uintptr_t stream)
+{
+    if (!gated_ok(gate, gate_stride, up, up_stride, out, n, count)) return 1;
+    return status(launch_gelu_mul((const float *)gate, (int)gate_stride, (const float *)up, (int)up_stride,
                                   (float *)out, (int)n, (int)count, (hipStream_t)stream));
 }
 

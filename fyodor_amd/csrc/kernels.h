@@ -117,33 +117,46 @@ hipError_t launch_read_shaped(const uint4 *src, size_t count, unsigned *sink, in
 // Vector steps of the resident decoder (resident.hip) over `count` tokens,
 // fp32 device vectors, token i's row at i times the row's stride (floats):
 // the decode step ids written (step[0] token, step[1] position); rows
-// tokens[i] of a GGUF-layout matrix decoded (row_bytes its stored size);
-// x += r (when r is given) then out = RMS-normalized x times w (w may be
-// null); rotary encoding at positions[i] (q rotated in place, k rotated into
-// its slot of `keys`, v copied into `values`, both
-// [capacity][kv_heads * width]); causal attention of each token's `heads`
-// query heads (width <= 256) over positions [0, positions[i]] (scores:
-// count x heads x max_length scratch, used past 8192 positions);
-// out = silu(gate) * up.
+// tokens[i] of a GGUF-layout matrix decoded (row_bytes its stored size)
+// times scale; x += r (when r is given) then out = RMS-normalized x times w
+// (w may be null); the same with r RMS-normalized times post first and x
+// scaled by oscale after the add (n <= kPostNormMax); rotary encoding at
+// positions[i] (q rotated in place, k rotated into its slot of `keys`, v
+// copied into `values`, both [capacity][kv_heads * width]); the Gemma form
+// (per-head RMS norms of q, k and v, then the half-split rotation of q and
+// k; width <= 256; k null: q only); causal attention of each token's
+// `heads` query heads (width <= 256) over positions [0, positions[i]], the
+// last `window` of them when window > 0 (scores: count x heads x max_length
+// scratch, used past 8192 positions); out = silu(gate) * up or
+// gelu(gate) * up; logits x = cap tanh(x / cap).
+constexpr int kPostNormMax = 16384;
 hipError_t launch_set_step(uint32_t *step, uint32_t token, int position, hipStream_t stream);
 hipError_t launch_embed(const uint8_t *w, unsigned type, size_t row_bytes, int rows, const uint32_t *tokens, int count,
-    int cols, float *out, hipStream_t stream);
+    int cols, float *out, float scale, hipStream_t stream);
 hipError_t launch_rms_norm(float *x, const float *r, const float *w, float *out, int n, int count, float eps,
     hipStream_t stream);
+hipError_t launch_post_norm(float *x, const float *r, const float *post, float oscale, const float *w, float *out,
+    int n, int count, float eps, hipStream_t stream);
 hipError_t launch_rope_qkv(float *q, int q_stride, const float *k, int k_stride, const float *v, int v_stride,
     int count, int heads, int kv_heads, int width, const float *freq, const int *positions, int capacity, float *keys,
     float *values, hipStream_t stream);
+hipError_t launch_head_norm_rope(float *q, int q_stride, const float *k, int k_stride, const float *v, int v_stride,
+    int count, int heads, int kv_heads, int width, const float *q_norm, const float *k_norm, float eps,
+    const float *freq, const int *positions, int capacity, float *keys, float *values, hipStream_t stream);
+hipError_t launch_softcap(float *x, size_t n, float cap, hipStream_t stream);
 // Attention split over the cached positions (resident.hip): `splits`
 // workgroups per (KV head, token), then their combination; partials:
 // count * heads * splits * (width + 2) floats.
 bool attention_split_supported(int heads, int kv_heads, int width, int max_length, int splits);
 hipError_t launch_attention_split(const float *q, int q_stride, const float *keys, const float *values, float *out,
-    float *partials, const int *positions, int count, int heads, int kv_heads, int width, int max_length, int splits,
-    float scale, hipStream_t s);
+    float *partials, const int *positions, int count, int heads, int kv_heads, int width, int max_length, int window,
+    int splits, float scale, hipStream_t s);
 hipError_t launch_attention(const float *q, int q_stride, const float *keys, const float *values, float *out,
-    float *scores, const int *positions, int count, int heads, int kv_heads, int width, int max_length, float scale,
-    hipStream_t stream);
+    float *scores, const int *positions, int count, int heads, int kv_heads, int width, int max_length, int window,
+    float scale, hipStream_t stream);
 hipError_t launch_silu_mul(const float *gate, int gate_stride, const float *up, int up_stride, float *out, int n,
+    int count, hipStream_t stream);
+hipError_t launch_gelu_mul(const float *gate, int gate_stride, const float *up, int up_stride, float *out, int n,
     int count, hipStream_t stream);
 hipError_t launch_silu_pairs(const float *gu, float *out, int n, int count, hipStream_t stream);
 // The greedy choice of each of `count` rows of n logits (first largest among

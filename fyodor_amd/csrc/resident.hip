@@ -62,16 +62,16 @@ __device__ float element(const uint8_t *row, unsigned type, int i)
     }
 }
 
-// out[i][c] = element c of row tokens[i] (a token past the matrix gives a
-// zero row; the host checks ids first).
+// out[i][c] = element c of row tokens[i] times scale (a token past the
+// matrix gives a zero row; the host checks ids first).
 __global__ __launch_bounds__(256) void embed(const uint8_t *__restrict__ w, unsigned type, size_t row_bytes,
-    int rows, const uint32_t *__restrict__ tokens, int cols, float *__restrict__ out)
+    int rows, const uint32_t *__restrict__ tokens, int cols, float *__restrict__ out, float scale)
 {
     const uint32_t token = tokens[blockIdx.y];
     float *o = out + (size_t)blockIdx.y * cols;
     const uint8_t *r = w + (size_t)token * row_bytes;
     for (int i = blockIdx.x * 256 + threadIdx.x; i < cols; i += gridDim.x * 256)
-        o[i] = token < (uint32_t)rows ? element(r, type, i) : 0.f;
+        o[i] = token < (uint32_t)rows ? element(r, type, i) * scale : 0.f;
 }
 
 // One workgroup of 1024 per row (token), holding n <= 4096 K elements in
@@ -153,6 +153,137 @@ __global__ __launch_bounds__(256) void rms_norm(float *__restrict__ x, const flo
     for (int i = t; i < n; i += 256) out[i] = x[i] * scale * (w ? w[i] : 1.0f);
 }
 
+// Sum of one double per thread over a workgroup of 64 N threads, the same
+// value in every thread: each wavefront's butterfly, then the wavefronts'
+// sums added in order.
+template <int N>
+__device__ __forceinline__ double group_sum(double s, double *part)
+{
+    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+    __syncthreads();   // an earlier call's reads of part are done
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    double total = part[0];
+#pragma unroll
+    for (int q = 1; q < N; ++q) total += part[q];
+    return total;
+}
+
+// The residual add of a block whose branch output carries its own norm
+// (the engine's Gemma post-attention and post-feed-forward norms,
+// backend/core/llm_cpu.c:514, :531): per token row of n <= 1024 K elements,
+// r' = r * s_r * post (r's RMS scale, the sum of squares in double; post
+// null: r' = r), x = (x + r') * oscale written back (the block's output
+// scale, :544-547; 1 elsewhere), then out = x * s_x * w as the norm step
+// (:83-104). Elements in registers, K per thread; r is not written.
+template <int K>
+__global__ __launch_bounds__(1024) void post_norm(float *__restrict__ x, const float *__restrict__ r,
+    const float *__restrict__ post, float oscale, const float *__restrict__ w, float *__restrict__ out, int n,
+    float eps)
+{
+    __shared__ double part[16];
+    const int t = threadIdx.x;
+    const size_t row = (size_t)blockIdx.x * n;
+    x += row;
+    out += row;
+    if (r) r += row;
+    float v[K], u[K];
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int i = t + 1024 * k;
+        v[k] = i < n ? x[i] : 0.f;
+        u[k] = i < n && r ? r[i] : 0.f;
+        s += (double)u[k] * u[k];
+    }
+    if (r && post) {
+        const float sr = (float)(1.0 / sqrt(group_sum<16>(s, part) / (double)n + (double)eps));
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int i = t + 1024 * k;
+            if (i < n) u[k] = u[k] * sr * post[i];
+        }
+    }
+    s = 0.0;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int i = t + 1024 * k;
+        if (i < n) {
+            if (r) v[k] = v[k] + u[k];
+            v[k] = v[k] * oscale;
+            x[i] = v[k];
+        }
+        s += (double)v[k] * v[k];
+    }
+    const float sx = (float)(1.0 / sqrt(group_sum<16>(s, part) / (double)n + (double)eps));
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int i = t + 1024 * k;
+        if (i < n) out[i] = v[k] * sx * (w ? w[i] : 1.0f);
+    }
+}
+
+constexpr int kHeadWidthMax = 256;   // head width limit of head_norm_rope (one element per thread)
+
+// The query and key steps of the engine's Gemma attention
+// (backend/core/llm_cpu.c:487-500): workgroup (head, token i) takes one head
+// of width <= 256, one element per thread. Heads [0, heads) are q heads (q
+// + i q_stride, normalized in place with q_norm, then rotated); with k,
+// heads [heads, heads + kv_heads) are k heads (normalized with k_norm,
+// rotated, into the key cache slot of positions[i]) and the next kv_heads
+// are v heads (normalized without a weight, into the value cache slot; v may
+// be k itself, the engine's copy of the key for layers without a value
+// matrix). The norm is the engine's RMS norm per head (:360-363, :83-104);
+// the rotation turns the pair (j, j + width / 2) by position * freq[j]
+// (:345-358, angles :429-432). A position outside [0, capacity) leaves
+// everything alone (the host checks first).
+__global__ __launch_bounds__(256) void head_norm_rope(float *__restrict__ q, int q_stride,
+    const float *__restrict__ k, int k_stride, const float *__restrict__ v, int v_stride, int heads, int kv_heads,
+    int width, const float *__restrict__ q_norm, const float *__restrict__ k_norm, float eps,
+    const float *__restrict__ freq, const int *__restrict__ positions, int capacity, float *__restrict__ keys,
+    float *__restrict__ values)
+{
+    __shared__ double part[4];
+    __shared__ float row[kHeadWidthMax];
+    const int position = positions[blockIdx.y];
+    if (position < 0 || position >= capacity) return;
+    const int h = blockIdx.x, j = threadIdx.x, half = width / 2;
+    const int kind = h < heads ? 0 : h < heads + kv_heads ? 1 : 2;   // q, k, v
+    const int hh = kind == 0 ? h : kind == 1 ? h - heads : h - heads - kv_heads;
+    const size_t slot = (size_t)position * kv_heads * width + (size_t)hh * width;
+    const float *src = kind == 0 ? q + (size_t)blockIdx.y * q_stride + (size_t)hh * width
+                     : kind == 1 ? k + (size_t)blockIdx.y * k_stride + (size_t)hh * width
+                                 : v + (size_t)blockIdx.y * v_stride + (size_t)hh * width;
+    float *dst = kind == 0 ? q + (size_t)blockIdx.y * q_stride + (size_t)hh * width
+               : kind == 1 ? keys + slot : values + slot;
+    const float *g = kind == 0 ? q_norm : kind == 1 ? k_norm : nullptr;
+    const float x = j < width ? src[j] : 0.f;
+    const float scale = (float)(1.0 / sqrt(group_sum<4>((double)x * x, part) / (double)width + (double)eps));
+    const float y = x * scale * (g && j < width ? g[j] : 1.0f);
+    if (kind == 2) {
+        if (j < width) dst[j] = y;
+        return;
+    }
+    // q in place: every element was read before group_sum's barriers.
+    if (j < width) row[j] = y;
+    __syncthreads();
+    if (j < half) {
+        const float angle = (float)position * freq[j];
+        const float c = cosf(angle), s = sinf(angle);
+        const float a = row[j], b = row[j + half];
+        dst[j] = a * c - b * s;
+        dst[j + half] = b * c + a * s;
+    }
+}
+
+// Logits squashed as the engine's final soft cap (backend/core/llm_cpu.c:
+// 562-565): x = cap * tanh(x / cap).
+__global__ __launch_bounds__(256) void softcap(float *__restrict__ x, size_t n, float cap)
+{
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        x[i] = cap * tanhf(x[i] / cap);
+}
+
 // The rotary step of token i = blockIdx.y at position positions[i]: its q
 // row (q + i q_stride, heads * width) rotated in place and its k row
 // (k + i k_stride, kv_heads * width) rotated into the key cache slot
@@ -207,22 +338,38 @@ __device__ __forceinline__ float block_reduce(float v, float *red, bool maximum)
 constexpr int kLdsScores = 8192;   // scores kept in LDS up to this length
 constexpr int kMaxWidth = 256;     // head width limit of the attention kernels
 
-// Attention of query token i = blockIdx.y, head blockIdx.x, over the cached
-// positions [0, positions[i]] (clamped to max_length): its q at
-// q + i * q_stride + head * W, its output at out + (i * heads + head) * W.
+// The cached positions [first, first + length) that a token at position p
+// attends: [0, p] clamped to max_length, and with a local window of
+// `window` positions (0: none) the last `window` of them, as the engine
+// bounds a sliding layer's attention (backend/core/llm_cpu.c:486-488).
+struct CausalRange {
+    int first, length;
+};
+
+__device__ __forceinline__ CausalRange causal_range(int p, int max_length, int window)
+{
+    const int end = p < 0 ? -1 : p >= max_length ? max_length - 1 : p;
+    const int first = window > 0 && end >= window ? end - window + 1 : 0;
+    return {first, end < 0 ? 0 : end - first + 1};
+}
+
+// Attention of query token i = blockIdx.y, head blockIdx.x, over its
+// causal range: its q at q + i * q_stride + head * W, its output at
+// out + (i * heads + head) * W.
 struct AttentionRow {
-    int head, kvh, length;
+    int head, kvh, first, length;
     size_t q, out, scores;
 };
 
 __device__ __forceinline__ AttentionRow attention_row(const int *positions, int heads, int kv_heads, int width,
-    int q_stride, int max_length)
+    int q_stride, int max_length, int window)
 {
     AttentionRow a;
     a.head = blockIdx.x;
     a.kvh = a.head / (heads / kv_heads);
-    const int p = positions[blockIdx.y];
-    a.length = p < 0 ? 0 : p >= max_length ? max_length : p + 1;
+    const CausalRange r = causal_range(positions[blockIdx.y], max_length, window);
+    a.first = r.first;
+    a.length = r.length;
     a.q = (size_t)blockIdx.y * q_stride + (size_t)a.head * width;
     a.out = ((size_t)blockIdx.y * heads + a.head) * width;
     a.scores = ((size_t)blockIdx.y * heads + a.head) * max_length;
@@ -242,7 +389,7 @@ template <int W, bool LDS>
 __global__ __launch_bounds__(256) void attention_w(const float *__restrict__ q, int q_stride,
     const float *__restrict__ keys, const float *__restrict__ values, float *__restrict__ out,
     float *__restrict__ scores, const int *__restrict__ positions, int heads, int kv_heads, int max_length,
-    float scale)
+    int window, float scale)
 {
     constexpr int C = W / 64;            // float4 per lane per row
     constexpr int U = W <= 128 ? 8 : 4;  // rows per 16 lanes in flight
@@ -251,10 +398,12 @@ __global__ __launch_bounds__(256) void attention_w(const float *__restrict__ q, 
     __shared__ float lds_scores[LDS ? kLdsScores : 1];
     __shared__ float4 part[256];
     __shared__ float red[4];
-    const AttentionRow a = attention_row(positions, heads, kv_heads, W, q_stride, max_length);
+    const AttentionRow a = attention_row(positions, heads, kv_heads, W, q_stride, max_length, window);
     const int tid = threadIdx.x, length = a.length;
     if (length == 0) return;
     const int kv4 = kv_heads * (W / 4);  // float4 per cached position
+    keys += (size_t)a.first * kv_heads * W;
+    values += (size_t)a.first * kv_heads * W;
     float *sc = LDS ? lds_scores : scores + a.scores;
     const int l16 = tid & 15, row = tid >> 4;
     const float4 *q4 = (const float4 *)(q + a.q);
@@ -347,16 +496,18 @@ template <bool LDS>
 __global__ __launch_bounds__(256) void attention(const float *__restrict__ q, int q_stride,
     const float *__restrict__ keys, const float *__restrict__ values, float *__restrict__ out,
     float *__restrict__ scores, const int *__restrict__ positions, int heads, int kv_heads, int width,
-    int max_length, float scale)
+    int max_length, int window, float scale)
 {
     __shared__ float lds_scores[LDS ? kLdsScores : 1];
     __shared__ float qs[kMaxWidth];
     __shared__ float part[256];
     __shared__ float red[4];
-    const AttentionRow a = attention_row(positions, heads, kv_heads, width, q_stride, max_length);
+    const AttentionRow a = attention_row(positions, heads, kv_heads, width, q_stride, max_length, window);
     const int tid = threadIdx.x, length = a.length;
     if (length == 0) return;
     const size_t kvdim = (size_t)kv_heads * width;
+    keys += (size_t)a.first * kvdim;
+    values += (size_t)a.first * kvdim;
     float *sc = LDS ? lds_scores : scores + a.scores;
     for (int j = tid; j < width; j += 256) qs[j] = q[a.q + j];
     __syncthreads();
@@ -423,7 +574,7 @@ constexpr int kSplitMaxChunk = 1024;   // positions per split (scores in LDS)
 template <int W, int G>
 __global__ __launch_bounds__(256) void attention_split(const float *__restrict__ q, int q_stride,
     const float *__restrict__ keys, const float *__restrict__ values, float *__restrict__ partials,
-    const int *__restrict__ positions, int heads, int kv_heads, int max_length, int splits, float scale)
+    const int *__restrict__ positions, int heads, int kv_heads, int max_length, int window, int splits, float scale)
 {
     constexpr int C = W / 64;          // float4 per lane per row
     constexpr int U = 4;               // rows per 16 lanes in flight
@@ -431,8 +582,10 @@ __global__ __launch_bounds__(256) void attention_split(const float *__restrict__
     static_assert(NG * W <= kSplitMaxChunk, "the groups' partial outputs fit the scores' LDS");
     __shared__ __align__(16) float sc[G * kSplitMaxChunk];   // scores, then the groups' partial outputs
     const int kvh = blockIdx.x, sp = blockIdx.y, tok = blockIdx.z, tid = threadIdx.x;
-    const int p = positions[tok];
-    const int length = p < 0 ? 0 : p >= max_length ? max_length : p + 1;
+    const CausalRange range = causal_range(positions[tok], max_length, window);
+    const int length = range.length;
+    keys += (size_t)range.first * kv_heads * W;
+    values += (size_t)range.first * kv_heads * W;
     const int chunk = (length + splits - 1) / splits;
     const int c0 = sp * chunk, n = length - c0 < chunk ? length - c0 : chunk;
     const size_t base = ((size_t)tok * heads + (size_t)kvh * G) * splits + sp;   // partial row of head g: + g splits
@@ -660,32 +813,32 @@ __global__ __launch_bounds__(256) void attention_combine(const float *__restrict
 
 template <int W, int G>
 void launch_split_wg(const float *q, int q_stride, const float *keys, const float *values, float *out,
-    float *partials, const int *positions, int count, int heads, int kv_heads, int max_length, int splits,
+    float *partials, const int *positions, int count, int heads, int kv_heads, int max_length, int window, int splits,
     float scale, hipStream_t s)
 {
     hipLaunchKernelGGL((attention_split<W, G>), dim3((unsigned)kv_heads, (unsigned)splits, (unsigned)count),
                        dim3(256), 0, s, q, q_stride, keys, values, partials, positions, heads, kv_heads, max_length,
-                       splits, scale);
+                       window, splits, scale);
     hipLaunchKernelGGL(attention_combine, dim3((unsigned)heads, (unsigned)count), dim3(256), 0, s, partials, out,
                        positions, heads, W, max_length, splits);
 }
 
 template <int W>
 hipError_t launch_split_w(const float *q, int q_stride, const float *keys, const float *values, float *out,
-    float *partials, const int *positions, int count, int heads, int kv_heads, int max_length, int splits,
+    float *partials, const int *positions, int count, int heads, int kv_heads, int max_length, int window, int splits,
     float scale, hipStream_t s)
 {
     switch (heads / kv_heads) {
     case 1: launch_split_wg<W, 1>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
-                                  max_length, splits, scale, s); break;
+                                  max_length, window, splits, scale, s); break;
     case 2: launch_split_wg<W, 2>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
-                                  max_length, splits, scale, s); break;
+                                  max_length, window, splits, scale, s); break;
     case 4: launch_split_wg<W, 4>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
-                                  max_length, splits, scale, s); break;
+                                  max_length, window, splits, scale, s); break;
     default:
         if constexpr (W <= 128) {
             launch_split_wg<W, 8>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
-                                  max_length, splits, scale, s);
+                                  max_length, window, splits, scale, s);
             break;
         }
         return hipErrorInvalidValue;
@@ -700,6 +853,17 @@ hipError_t launch_split_w(const float *q, int q_stride, const float *keys, const
 // itself for one token.
 __device__ __forceinline__ float silu_times(float x, float u) { return x / (1.0f + expf(-x)) * u; }
 
+// GELU with the tanh approximation times u, the engine's Gemma gate
+// (backend/core/llm_cpu.c:329-341), in its operation order.
+__device__ __forceinline__ float gelu_times(float x, float u)
+{
+    return 0.5f * x * (1.0f + tanhf(0.7978845608028654f * (x + 0.044715f * x * x * x))) * u;
+}
+
+template <bool GELU>
+__device__ __forceinline__ float gated(float x, float u) { return GELU ? gelu_times(x, u) : silu_times(x, u); }
+
+template <bool GELU>
 __global__ __launch_bounds__(256) void silu_mul4(const float4 *gate, int gate_stride4, const float4 *up,
     int up_stride4, float4 *out, int n4)
 {
@@ -707,7 +871,8 @@ __global__ __launch_bounds__(256) void silu_mul4(const float4 *gate, int gate_st
     float4 *o = out + (size_t)blockIdx.y * n4;
     for (int i = blockIdx.x * 256 + threadIdx.x; i < n4; i += gridDim.x * 256) {
         const float4 a = g[i], b = u[i];
-        o[i] = make_float4(silu_times(a.x, b.x), silu_times(a.y, b.y), silu_times(a.z, b.z), silu_times(a.w, b.w));
+        o[i] = make_float4(gated<GELU>(a.x, b.x), gated<GELU>(a.y, b.y), gated<GELU>(a.z, b.z),
+                           gated<GELU>(a.w, b.w));
     }
 }
 
@@ -724,12 +889,13 @@ __global__ __launch_bounds__(256) void silu_pairs(const float *__restrict__ gu, 
     }
 }
 
+template <bool GELU>
 __global__ __launch_bounds__(256) void silu_mul(const float *gate, int gate_stride, const float *up, int up_stride,
     float *out, int n)
 {
     const float *g = gate + (size_t)blockIdx.y * gate_stride, *u = up + (size_t)blockIdx.y * up_stride;
     float *o = out + (size_t)blockIdx.y * n;
-    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) o[i] = silu_times(g[i], u[i]);
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) o[i] = gated<GELU>(g[i], u[i]);
 }
 
 // step[0] = token, step[1] = position: one decode token's ids, written on
@@ -806,10 +972,10 @@ hipError_t launch_set_step(uint32_t *step, uint32_t token, int position, hipStre
 }
 
 hipError_t launch_embed(const uint8_t *w, unsigned type, size_t row_bytes, int rows, const uint32_t *tokens, int count,
-    int cols, float *out, hipStream_t s)
+    int cols, float *out, float scale, hipStream_t s)
 {
     hipLaunchKernelGGL(embed, dim3(grid_of(cols), (unsigned)count), dim3(256), 0, s, w, type, row_bytes, rows, tokens,
-                       cols, out);
+                       cols, out, scale);
     return hipGetLastError();
 }
 
@@ -834,6 +1000,44 @@ hipError_t launch_rms_norm(float *x, const float *r, const float *w, float *out,
     return hipGetLastError();
 }
 
+hipError_t launch_post_norm(float *x, const float *r, const float *post, float oscale, const float *w, float *out,
+    int n, int count, float eps, hipStream_t s)
+{
+    const dim3 grid((unsigned)count);
+    if (n <= 1024)
+        hipLaunchKernelGGL(post_norm<1>, grid, dim3(1024), 0, s, x, r, post, oscale, w, out, n, eps);
+    else if (n <= 2048)
+        hipLaunchKernelGGL(post_norm<2>, grid, dim3(1024), 0, s, x, r, post, oscale, w, out, n, eps);
+    else if (n <= 4096)
+        hipLaunchKernelGGL(post_norm<4>, grid, dim3(1024), 0, s, x, r, post, oscale, w, out, n, eps);
+    else if (n <= 8192)
+        hipLaunchKernelGGL(post_norm<8>, grid, dim3(1024), 0, s, x, r, post, oscale, w, out, n, eps);
+    else if (n <= kPostNormMax)
+        hipLaunchKernelGGL(post_norm<16>, grid, dim3(1024), 0, s, x, r, post, oscale, w, out, n, eps);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_head_norm_rope(float *q, int q_stride, const float *k, int k_stride, const float *v, int v_stride,
+    int count, int heads, int kv_heads, int width, const float *q_norm, const float *k_norm, float eps,
+    const float *freq, const int *positions, int capacity, float *keys, float *values, hipStream_t s)
+{
+    if (width > kHeadWidthMax || width % 2) return hipErrorInvalidValue;
+    const int rows = heads + (k ? 2 * kv_heads : 0);
+    hipLaunchKernelGGL(head_norm_rope, dim3((unsigned)rows, (unsigned)count), dim3(256), 0, s, q, q_stride, k,
+                       k_stride, v, v_stride, heads, kv_heads, width, q_norm, k_norm, eps, freq, positions, capacity,
+                       keys, values);
+    return hipGetLastError();
+}
+
+hipError_t launch_softcap(float *x, size_t n, float cap, hipStream_t s)
+{
+    hipLaunchKernelGGL(softcap, dim3(grid_of((long)(n < (size_t)1 << 30 ? n : (size_t)1 << 30))), dim3(256), 0, s, x,
+                       n, cap);
+    return hipGetLastError();
+}
+
 hipError_t launch_rope_qkv(float *q, int q_stride, const float *k, int k_stride, const float *v, int v_stride,
     int count, int heads, int kv_heads, int width, const float *freq, const int *positions, int capacity, float *keys,
     float *values, hipStream_t s)
@@ -846,21 +1050,21 @@ hipError_t launch_rope_qkv(float *q, int q_stride, const float *k, int k_stride,
 
 template <int W>
 void launch_attention_w(const float *q, int q_stride, const float *keys, const float *values, float *out,
-    float *scores, const int *positions, int count, int heads, int kv_heads, int max_length, float scale,
+    float *scores, const int *positions, int count, int heads, int kv_heads, int max_length, int window, float scale,
     hipStream_t s)
 {
     const dim3 grid((unsigned)heads, (unsigned)count);
     if (max_length <= kLdsScores)
         hipLaunchKernelGGL((attention_w<W, true>), grid, dim3(256), 0, s, q, q_stride, keys, values, out, scores,
-                           positions, heads, kv_heads, max_length, scale);
+                           positions, heads, kv_heads, max_length, window, scale);
     else
         hipLaunchKernelGGL((attention_w<W, false>), grid, dim3(256), 0, s, q, q_stride, keys, values, out, scores,
-                           positions, heads, kv_heads, max_length, scale);
+                           positions, heads, kv_heads, max_length, window, scale);
 }
 
 hipError_t launch_attention(const float *q, int q_stride, const float *keys, const float *values, float *out,
-    float *scores, const int *positions, int count, int heads, int kv_heads, int width, int max_length, float scale,
-    hipStream_t s)
+    float *scores, const int *positions, int count, int heads, int kv_heads, int width, int max_length, int window,
+    float scale, hipStream_t s)
 {
     if (width > kMaxWidth) return hipErrorInvalidValue;
     const bool aligned = (q_stride & 3) == 0 &&
@@ -868,19 +1072,19 @@ hipError_t launch_attention(const float *q, int q_stride, const float *keys, con
     const dim3 grid((unsigned)heads, (unsigned)count);
     if (aligned && width == 128)
         launch_attention_w<128>(q, q_stride, keys, values, out, scores, positions, count, heads, kv_heads, max_length,
-                                scale, s);
+                                window, scale, s);
     else if (aligned && width == 64)
         launch_attention_w<64>(q, q_stride, keys, values, out, scores, positions, count, heads, kv_heads, max_length,
-                               scale, s);
+                               window, scale, s);
     else if (aligned && width == 256)
         launch_attention_w<256>(q, q_stride, keys, values, out, scores, positions, count, heads, kv_heads, max_length,
-                                scale, s);
+                                window, scale, s);
     else if (max_length <= kLdsScores)
         hipLaunchKernelGGL(attention<true>, grid, dim3(256), 0, s, q, q_stride, keys, values, out, scores, positions,
-                           heads, kv_heads, width, max_length, scale);
+                           heads, kv_heads, width, max_length, window, scale);
     else
         hipLaunchKernelGGL(attention<false>, grid, dim3(256), 0, s, q, q_stride, keys, values, out, scores, positions,
-                           heads, kv_heads, width, max_length, scale);
+                           heads, kv_heads, width, max_length, window, scale);
     return hipGetLastError();
 }
 
@@ -894,20 +1098,20 @@ bool attention_split_supported(int heads, int kv_heads, int width, int max_lengt
 }
 
 hipError_t launch_attention_split(const float *q, int q_stride, const float *keys, const float *values, float *out,
-    float *partials, const int *positions, int count, int heads, int kv_heads, int width, int max_length, int splits,
-    float scale, hipStream_t s)
+    float *partials, const int *positions, int count, int heads, int kv_heads, int width, int max_length, int window,
+    int splits, float scale, hipStream_t s)
 {
     if (!attention_split_supported(heads, kv_heads, width, max_length, splits) || (q_stride & 3) ||
         (((uintptr_t)q | (uintptr_t)keys | (uintptr_t)values | (uintptr_t)partials) & 15u))
         return hipErrorInvalidValue;
     if (width == 128)
         return launch_split_w<128>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
-                                   max_length, splits, scale, s);
+                                   max_length, window, splits, scale, s);
     if (width == 64)
         return launch_split_w<64>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
-                                  max_length, splits, scale, s);
+                                  max_length, window, splits, scale, s);
     return launch_split_w<256>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
-                               max_length, splits, scale, s);
+                               max_length, window, splits, scale, s);
 }
 
 hipError_t launch_greedy(const float *logits, int n, int count, const uint32_t *mask, uint32_t *ids, hipStream_t s)
@@ -922,16 +1126,30 @@ hipError_t launch_silu_pairs(const float *gu, float *out, int n, int count, hipS
     return hipGetLastError();
 }
 
-hipError_t launch_silu_mul(const float *gate, int gate_stride, const float *up, int up_stride, float *out, int n,
+template <bool GELU>
+hipError_t launch_gated(const float *gate, int gate_stride, const float *up, int up_stride, float *out, int n,
     int count, hipStream_t s)
 {
     if (((n | gate_stride | up_stride) & 3) == 0 && (((uintptr_t)gate | (uintptr_t)up | (uintptr_t)out) & 15u) == 0)
-        hipLaunchKernelGGL(silu_mul4, dim3(grid_of(n / 4), (unsigned)count), dim3(256), 0, s, (const float4 *)gate,
-                           gate_stride / 4, (const float4 *)up, up_stride / 4, (float4 *)out, n / 4);
+        hipLaunchKernelGGL(silu_mul4<GELU>, dim3(grid_of(n / 4), (unsigned)count), dim3(256), 0, s,
+                           (const float4 *)gate, gate_stride / 4, (const float4 *)up, up_stride / 4, (float4 *)out,
+                           n / 4);
     else
-        hipLaunchKernelGGL(silu_mul, dim3(grid_of(n), (unsigned)count), dim3(256), 0, s, gate, gate_stride, up,
+        hipLaunchKernelGGL(silu_mul<GELU>, dim3(grid_of(n), (unsigned)count), dim3(256), 0, s, gate, gate_stride, up,
                            up_stride, out, n);
     return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(const float *gate, int gate_stride, const float *up, int up_stride, float *out, int n,
+    int count, hipStream_t s)
+{
+    return launch_gated<false>(gate, gate_stride, up, up_stride, out, n, count, s);
+}
+
+hipError_t launch_gelu_mul(const float *gate, int gate_stride, const float *up, int up_stride, float *out, int n,
+    int count, hipStream_t s)
+{
+    return launch_gated<true>(gate, gate_stride, up, up_stride, out, n, count, s);
 }
 
 }  // namespace fy

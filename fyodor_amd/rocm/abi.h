@@ -53,12 +53,12 @@ typedef struct nya_kernel_library {
  * without them the provider still multiplies matrices and declines plans. */
 typedef struct nya_resident_ops {
     int (*step)(uintptr_t, unsigned, size_t, uintptr_t);
-    int (*embed)(uintptr_t, unsigned, size_t, size_t, uintptr_t, size_t, uintptr_t, uintptr_t);
+    int (*embed)(uintptr_t, unsigned, size_t, size_t, uintptr_t, size_t, uintptr_t, float, uintptr_t);
     int (*rms_norm)(uintptr_t, uintptr_t, uintptr_t, uintptr_t, size_t, size_t, float, uintptr_t);
     int (*rope_qkv)(uintptr_t, size_t, uintptr_t, size_t, uintptr_t, size_t, size_t, size_t, size_t, size_t,
         uintptr_t, uintptr_t, size_t, uintptr_t, uintptr_t, uintptr_t);
     int (*attention)(uintptr_t, size_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, size_t, size_t, size_t,
-        size_t, size_t, float, uintptr_t);
+        size_t, size_t, size_t, float, uintptr_t);
     int (*silu_mul)(uintptr_t, size_t, uintptr_t, size_t, uintptr_t, size_t, size_t, uintptr_t);
     int (*greedy)(uintptr_t, size_t, size_t, uintptr_t, uintptr_t, uintptr_t);
     /* Optional within the set: NULL leaves the gated SiLU a step of its own. */
@@ -85,8 +85,16 @@ typedef struct nya_resident_ops {
     /* Optional: NULL keeps attention one workgroup per query head at every
      * length. */
     int (*attention_split)(uintptr_t, size_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, size_t, size_t,
-        size_t, size_t, size_t, size_t, float, uintptr_t);
+        size_t, size_t, size_t, size_t, size_t, float, uintptr_t);
+    /* Optional as a set: the Gemma steps (per-block post norms and output
+     * scale, per-head q/k/v norms with the half-split rotation, the GELU
+     * gate, the logit soft cap); NULL declines Gemma models. */
+    int (*post_norm)(uintptr_t, uintptr_t, uintptr_t, float, uintptr_t, uintptr_t, size_t, size_t, float, uintptr_t);
+    int (*head_norm_rope)(uintptr_t, size_t, uintptr_t, size_t, uintptr_t, size_t, size_t, size_t, size_t, size_t,
+        uintptr_t, uintptr_t, float, uintptr_t, uintptr_t, size_t, uintptr_t, uintptr_t, uintptr_t);
+    int (*gelu_mul)(uintptr_t, size_t, uintptr_t, size_t, uintptr_t, size_t, size_t, uintptr_t);
+    int (*softcap)(uintptr_t, size_t, float, uintptr_t);
 } nya_resident_ops;
 
-#define NYA_KERNEL_ABI 1U
+#define NYA_KERNEL_ABI 2U
 #endif

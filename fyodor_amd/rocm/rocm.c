@@ -382,6 +382,18 @@ static int bind_all(session *s)
     if (nya_vendor_symbol(s->kernel_module, "nya_hip_attention_split", &s->resident.attention_split,
                           sizeof s->resident.attention_split))
         s->resident.attention_split = NULL;
+    const struct { const char *symbol; void *slot; size_t size; } gemma[] = {
+        {"nya_hip_post_norm", &s->resident.post_norm, sizeof s->resident.post_norm},
+        {"nya_hip_head_norm_rope", &s->resident.head_norm_rope, sizeof s->resident.head_norm_rope},
+        {"nya_hip_gelu_mul", &s->resident.gelu_mul, sizeof s->resident.gelu_mul},
+        {"nya_hip_softcap", &s->resident.softcap, sizeof s->resident.softcap},
+    };
+    bool has_gemma = true;
+    for (size_t i = 0; i < sizeof gemma / sizeof gemma[0]; ++i)
+        if (nya_vendor_symbol(s->kernel_module, gemma[i].symbol, gemma[i].slot, gemma[i].size)) has_gemma = false;
+    if (!has_gemma)
+        s->resident.post_norm = NULL, s->resident.head_norm_rope = NULL, s->resident.gelu_mul = NULL,
+        s->resident.softcap = NULL;
     const struct { const char *symbol; void *slot; size_t size; } graphs[] = {
         {"hipStreamBeginCapture", &s->graphs.begin_capture, sizeof s->graphs.begin_capture},
         {"hipStreamEndCapture", &s->graphs.end_capture, sizeof s->graphs.end_capture},

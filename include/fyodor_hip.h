@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define NYA_HIP_ABI_VERSION 1U
+#define NYA_HIP_ABI_VERSION 2U
 
 /* GGML storage type IDs (backend/core/llm_internal.h:11-19). */
 enum {
@@ -164,11 +164,11 @@ NYA_HIP_EXPORT int nya_hip_step(uintptr_t step, unsigned token, size_t position,
 
 /* out[i][cols] = row tokens[i] of a [rows][cols] matrix of `type` in GGUF
  * storage (not packed), decoded as nya_llm_tensor_value does
- * (backend/core/llm_quant.c:70-142): the token embedding gather
- * (backend/core/llm_cpu.c:71-80, :452-453). An id past the matrix gives a
- * zero row. */
+ * (backend/core/llm_quant.c:70-142), times scale: the token embedding
+ * gather (backend/core/llm_cpu.c:71-80, :452-453; Gemma's scale sqrt(d),
+ * :453, 1 otherwise). An id past the matrix gives a zero row. */
 NYA_HIP_EXPORT int nya_hip_embed(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t tokens,
-    size_t count, uintptr_t out, uintptr_t stream);
+    size_t count, uintptr_t out, float scale, uintptr_t stream);
 
 /* Per token row of n: when residual is nonzero, x += residual first (x is
  * written back); then out = x * s * weight with
@@ -177,6 +177,36 @@ NYA_HIP_EXPORT int nya_hip_embed(uintptr_t w, unsigned type, size_t rows, size_t
  * folded in). */
 NYA_HIP_EXPORT int nya_hip_rms_norm(uintptr_t x, uintptr_t residual, uintptr_t weight, uintptr_t out, size_t n,
     size_t count, float epsilon, uintptr_t stream);
+
+/* The residual add of a block whose branch carries its own norm (Gemma's
+ * post-attention and post-feed-forward norms, backend/core/llm_cpu.c:514,
+ * :531, :544-547), folded into the next norm step: per token row of n
+ * (at most 16384), r' = residual * s_r * post with
+ * s_r = 1 / sqrt(sum residual^2 / n + epsilon) (post 0: r' = residual;
+ * residual 0: no add), x = (x + r') * output_scale written back (the
+ * block's output scale, 1 where it has none), then out = x * s * weight as
+ * nya_hip_rms_norm. The residual rows are read, not written. */
+NYA_HIP_EXPORT int nya_hip_post_norm(uintptr_t x, uintptr_t residual, uintptr_t post, float output_scale,
+    uintptr_t weight, uintptr_t out, size_t n, size_t count, float epsilon, uintptr_t stream);
+
+/* The Gemma form of nya_hip_rope_qkv (backend/core/llm_cpu.c:487-500): each
+ * head of width <= 256 is RMS-normalized on its own (q heads with q_norm,
+ * k heads with k_norm, v heads without a weight; :360-363), then q and k
+ * heads have their halves rotated, the pair (j, j + width / 2) by
+ * p * frequencies[j] (:345-358): q in place, k into the key cache slot of
+ * positions[i], v (normalized only) into the value slot. v may equal k
+ * with the same stride (layers without a value matrix store the key's
+ * projection as the value, :492). k = 0: the q heads only (layers that
+ * read another layer's cache, :488-489); k_norm, keys and values are then
+ * not used. A position outside [0, capacity) leaves everything alone. */
+NYA_HIP_EXPORT int nya_hip_head_norm_rope(uintptr_t q, size_t q_stride, uintptr_t k, size_t k_stride, uintptr_t v,
+    size_t v_stride, size_t count, size_t heads, size_t kv_heads, size_t width, uintptr_t q_norm, uintptr_t k_norm,
+    float epsilon, uintptr_t frequencies, uintptr_t positions, size_t capacity, uintptr_t keys, uintptr_t values,
+    uintptr_t stream);
+
+/* x[i] = cap * tanh(x[i] / cap) over n logits: the final soft cap
+ * (backend/core/llm_cpu.c:562-565). cap > 0. */
+NYA_HIP_EXPORT int nya_hip_softcap(uintptr_t x, size_t n, float cap, uintptr_t stream);
 
 /* The rotary step of each token i at position p = positions[i]: its q row
  * (q + i q_stride floats, `heads` heads of `width`) has the interleaved
@@ -196,11 +226,13 @@ NYA_HIP_EXPORT int nya_hip_rope_qkv(uintptr_t q, size_t q_stride, uintptr_t k, s
  * scores q.k_t * scale over the cached positions t = 0 .. positions[i]
  * (at most max_length) of keys / values ([max_length][kv_heads * width]
  * rows), a softmax, and out[i] = sum_t p_t v_t (backend/core/llm_cpu.c:491-511).
- * `scores` is scratch of count * heads * max_length floats, needed (and
- * used) only when max_length exceeds 8192. */
+ * window > 0 keeps the last `window` of those positions, as the engine
+ * bounds a sliding layer's attention (:486-488); 0 keeps all. `scores` is
+ * scratch of count * heads * max_length floats, needed (and used) only
+ * when max_length exceeds 8192. */
 NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t keys, uintptr_t values, uintptr_t out,
     uintptr_t scores, uintptr_t positions, size_t count, size_t heads, size_t kv_heads, size_t width,
-    size_t max_length, float scale, uintptr_t stream);
+    size_t max_length, size_t window, float scale, uintptr_t stream);
 
 /* No counterpart in the reference's C engine (the reference's CUDA plan
  * splits long attention the same way, CUDA/resident.inc:119-133): the
@@ -218,13 +250,19 @@ NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t key
  * shape (heads, kv_heads, width, max_length, splits): 0 where it runs. */
 NYA_HIP_EXPORT int nya_hip_attention_split(uintptr_t q, size_t q_stride, uintptr_t keys, uintptr_t values,
     uintptr_t out, uintptr_t partials, uintptr_t positions, size_t count, size_t heads, size_t kv_heads, size_t width,
-    size_t max_length, size_t splits, float scale, uintptr_t stream);
+    size_t max_length, size_t window, size_t splits, float scale, uintptr_t stream);
 
 /* out[i][j] = g / (1 + e^-g) * u with g = gate[i gate_stride + j],
  * u = up[i up_stride + j], out rows of n (backend/core/llm_cpu.c:336-341,
  * SiLU of the gate times the up product). For one token out may be gate
  * itself; for several it must not overlap either input. */
 NYA_HIP_EXPORT int nya_hip_silu_mul(uintptr_t gate, size_t gate_stride, uintptr_t up, size_t up_stride,
+    uintptr_t out, size_t n, size_t count, uintptr_t stream);
+
+/* The same with GELU's tanh form in place of SiLU, Gemma's gate
+ * (backend/core/llm_cpu.c:329-341):
+ * out = 0.5 g (1 + tanh(0.7978845608028654 (g + 0.044715 g^3))) u. */
+NYA_HIP_EXPORT int nya_hip_gelu_mul(uintptr_t gate, size_t gate_stride, uintptr_t up, size_t up_stride,
     uintptr_t out, size_t n, size_t count, uintptr_t stream);
 
 /* No counterpart in the reference: one token's product of the decoder's

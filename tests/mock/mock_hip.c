@@ -171,7 +171,7 @@ static int blocks(unsigned type, size_t *block, size_t *bytes)
 static int declined_type = -1;
 API void nya_mock_decline_type(int type) { declined_type = type; }
 
-API unsigned nya_hip_abi_version(void) { return 1; }
+API unsigned nya_hip_abi_version(void) { return 2; }
 API int nya_hip_weight_bytes(unsigned type, size_t rows, size_t cols, size_t *out)
 {
     size_t block, bytes;
@@ -349,17 +349,17 @@ API int nya_hip_step(uintptr_t step, unsigned token, size_t position, uintptr_t 
 }
 
 API int nya_hip_embed(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t tokens, size_t count,
-    uintptr_t out, uintptr_t stream)
+    uintptr_t out, float scale, uintptr_t stream)
 {
-    if (!w || !tokens || !out || !rows || !cols || !count || !stream) return 1;
+    if (!w || !tokens || !out || !rows || !cols || !count || !stream || !isfinite(scale)) return 1;
     if (injected_fault()) return -1;
     const size_t rb = mock_row_bytes(type, cols);
     if (!rb) return 1;
     for (size_t t = 0; t < count; ++t) {
         const uint32_t token = ((const uint32_t *)tokens)[t];
         for (size_t i = 0; i < cols; ++i)
-            ((float *)out)[t * cols + i] = token < rows ? orc_value((const unsigned char *)w + token * rb, type, i)
-                                                        : 0.0f;
+            ((float *)out)[t * cols + i] =
+                token < rows ? orc_value((const unsigned char *)w + token * rb, type, i) * scale : 0.0f;
     }
     return 0;
 }
@@ -413,9 +413,20 @@ API int nya_hip_rope_qkv(uintptr_t q, size_t q_stride, uintptr_t k, size_t k_str
     return 0;
 }
 
+/* The positions [*first, *first + length) a token at p attends: [0, p]
+ * within max_length, the last `window` of them when window > 0. */
+static size_t mock_range(int p, size_t max_length, size_t window, size_t *first)
+{
+    *first = 0;
+    if (p < 0) return 0;
+    const size_t end = (size_t)p >= max_length ? max_length - 1 : (size_t)p;
+    if (window && end >= window) *first = end - window + 1;
+    return end - *first + 1;
+}
+
 API int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t keys, uintptr_t values, uintptr_t out,
     uintptr_t scores, uintptr_t positions, size_t count, size_t heads, size_t kv_heads, size_t width,
-    size_t max_length, float scale, uintptr_t stream)
+    size_t max_length, size_t window, float scale, uintptr_t stream)
 {
     (void)scores;
     if (!q || !keys || !values || !out || !positions || !count || !heads || !kv_heads || heads % kv_heads ||
@@ -426,14 +437,15 @@ API int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t keys, uintptr_
     float *sc = malloc(max_length * sizeof(float));
     if (!sc) return -1;
     for (size_t i = 0; i < count; ++i) {
-        const int p = ((const int *)positions)[i];
-        const size_t length = p < 0 ? 0 : (size_t)p >= max_length ? max_length : (size_t)p + 1;
+        size_t first;
+        const size_t length = mock_range(((const int *)positions)[i], max_length, window, &first);
+        const float *kb = (const float *)keys + first * kvdim, *vb = (const float *)values + first * kvdim;
         for (size_t h = 0; h < heads && length; ++h) {
             const float *qh = (const float *)q + i * q_stride + h * width;
             const size_t kvh = h / (heads / kv_heads);
             float m = -INFINITY, sum = 0.f;
             for (size_t t = 0; t < length; ++t) {
-                const float *k = (const float *)keys + t * kvdim + kvh * width;
+                const float *k = kb + t * kvdim + kvh * width;
                 float s = 0.f;
                 for (size_t j = 0; j < width; ++j) s += qh[j] * k[j];
                 sc[t] = s * scale;
@@ -446,7 +458,7 @@ API int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t keys, uintptr_
             for (size_t t = 0; t < length; ++t) sc[t] /= sum;
             for (size_t j = 0; j < width; ++j) {
                 float acc = 0.f;
-                for (size_t t = 0; t < length; ++t) acc += sc[t] * ((const float *)values)[t * kvdim + kvh * width + j];
+                for (size_t t = 0; t < length; ++t) acc += sc[t] * vb[t * kvdim + kvh * width + j];
                 ((float *)out)[(i * heads + h) * width + j] = acc;
             }
         }
@@ -462,7 +474,7 @@ API int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t keys, uintptr_
  * shape query. */
 API int nya_hip_attention_split(uintptr_t q, size_t q_stride, uintptr_t keys, uintptr_t values, uintptr_t out,
     uintptr_t partials, uintptr_t positions, size_t count, size_t heads, size_t kv_heads, size_t width,
-    size_t max_length, size_t splits, float scale, uintptr_t stream)
+    size_t max_length, size_t window, size_t splits, float scale, uintptr_t stream)
 {
     if (!heads || !kv_heads || heads % kv_heads || !width || !max_length || !splits ||
         (max_length + splits - 1) / splits > 1024)
@@ -473,9 +485,10 @@ API int nya_hip_attention_split(uintptr_t q, size_t q_stride, uintptr_t keys, ui
     const size_t kvdim = kv_heads * width;
     float *o = (float *)partials, *ml = o + count * heads * splits * width;
     for (size_t i = 0; i < count; ++i) {
-        const int p = ((const int *)positions)[i];
-        const size_t length = p < 0 ? 0 : (size_t)p >= max_length ? max_length : (size_t)p + 1;
+        size_t first;
+        const size_t length = mock_range(((const int *)positions)[i], max_length, window, &first);
         if (!length) continue;
+        const float *kb = (const float *)keys + first * kvdim, *vb = (const float *)values + first * kvdim;
         const size_t chunk = (length + splits - 1) / splits;
         for (size_t h = 0; h < heads; ++h) {
             const float *qh = (const float *)q + i * q_stride + h * width;
@@ -485,19 +498,19 @@ API int nya_hip_attention_split(uintptr_t q, size_t q_stride, uintptr_t keys, ui
                 const size_t c1 = c0 + chunk < length ? c0 + chunk : length;
                 float m = -INFINITY, l = 0.f;
                 for (size_t t = c0; t < c1; ++t) {
-                    const float *k = (const float *)keys + t * kvdim + kvh * width;
+                    const float *k = kb + t * kvdim + kvh * width;
                     float sdot = 0.f;
                     for (size_t j = 0; j < width; ++j) sdot += qh[j] * k[j];
                     if (sdot * scale > m) m = sdot * scale;
                 }
                 for (size_t j = 0; j < width; ++j) o[row * width + j] = 0.f;
                 for (size_t t = c0; t < c1; ++t) {
-                    const float *k = (const float *)keys + t * kvdim + kvh * width;
+                    const float *k = kb + t * kvdim + kvh * width;
                     float sdot = 0.f;
                     for (size_t j = 0; j < width; ++j) sdot += qh[j] * k[j];
                     const float e = expf(sdot * scale - m);
                     l += e;
-                    for (size_t j = 0; j < width; ++j) o[row * width + j] += e * ((const float *)values)[t * kvdim + kvh * width + j];
+                    for (size_t j = 0; j < width; ++j) o[row * width + j] += e * vb[t * kvdim + kvh * width + j];
                 }
                 ml[2 * row] = c0 < c1 ? m : -INFINITY;
                 ml[2 * row + 1] = l;
@@ -531,6 +544,97 @@ API int nya_hip_silu_mul(uintptr_t gate, size_t gate_stride, uintptr_t up, size_
             const float x = ((const float *)gate)[t * gate_stride + i], u = ((const float *)up)[t * up_stride + i];
             ((float *)out)[t * n + i] = x / (1.0f + expf(-x)) * u;
         }
+    return 0;
+}
+
+API int nya_hip_gelu_mul(uintptr_t gate, size_t gate_stride, uintptr_t up, size_t up_stride, uintptr_t out,
+    size_t n, size_t count, uintptr_t stream)
+{
+    if (!gate || !up || !out || !n || !count || !stream) return 1;
+    if (injected_fault()) return -1;
+    for (size_t t = 0; t < count; ++t)
+        for (size_t i = 0; i < n; ++i) {
+            const float x = ((const float *)gate)[t * gate_stride + i], u = ((const float *)up)[t * up_stride + i];
+            ((float *)out)[t * n + i] = 0.5f * x * (1.0f + tanhf(0.7978845608028654f * (x + 0.044715f * x * x * x))) * u;
+        }
+    return 0;
+}
+
+/* One row's RMS norm as the engine's (sum of squares in double). */
+static void mock_norm(float *out, const float *in, const float *w, size_t n, float eps)
+{
+    double sum = 0.0;
+    for (size_t i = 0; i < n; ++i) sum += (double)in[i] * in[i];
+    const float scale = (float)(1.0 / sqrt(sum / (double)n + eps));
+    for (size_t i = 0; i < n; ++i) out[i] = in[i] * scale * (w ? w[i] : 1.0f);
+}
+
+API int nya_hip_post_norm(uintptr_t x, uintptr_t residual, uintptr_t post, float output_scale, uintptr_t weight,
+    uintptr_t out, size_t n, size_t count, float eps, uintptr_t stream)
+{
+    if (!x || !out || !n || n > 16384 || !count || !stream || (post && !residual)) return 1;
+    if (injected_fault()) return -1;
+    float *r = malloc(n * sizeof(float));
+    if (!r) return -2;
+    for (size_t t = 0; t < count; ++t) {
+        float *v = (float *)x + t * n;
+        if (residual) {
+            const float *rr = (const float *)residual + t * n;
+            if (post) mock_norm(r, rr, (const float *)post, n, eps);
+            else memcpy(r, rr, n * sizeof(float));
+            for (size_t i = 0; i < n; ++i) v[i] += r[i];
+        }
+        for (size_t i = 0; i < n; ++i) v[i] *= output_scale;
+        mock_norm((float *)out + t * n, v, (const float *)weight, n, eps);
+    }
+    free(r);
+    return 0;
+}
+
+API int nya_hip_head_norm_rope(uintptr_t q, size_t q_stride, uintptr_t k, size_t k_stride, uintptr_t v,
+    size_t v_stride, size_t count, size_t heads, size_t kv_heads, size_t width, uintptr_t q_norm, uintptr_t k_norm,
+    float eps, uintptr_t freq, uintptr_t positions, size_t capacity, uintptr_t keys, uintptr_t values,
+    uintptr_t stream)
+{
+    if (!q || !q_norm || !freq || !positions || !count || !heads || !kv_heads || !width || width % 2 || width > 256 ||
+        !capacity || !stream || (k && (!v || !k_norm || !keys || !values)))
+        return 1;
+    if (injected_fault()) return -1;
+    const size_t kvd = kv_heads * width, half = width / 2;
+    float row[256];
+    for (size_t t = 0; t < count; ++t) {
+        const int position = ((const int *)positions)[t];
+        if (position < 0 || (size_t)position >= capacity) continue;
+        for (size_t h = 0; h < heads + (k ? 2 * kv_heads : 0); ++h) {
+            const int kind = h < heads ? 0 : h < heads + kv_heads ? 1 : 2;
+            const size_t hh = kind == 0 ? h : kind == 1 ? h - heads : h - heads - kv_heads;
+            const float *src = kind == 0 ? (const float *)q + t * q_stride + hh * width
+                             : kind == 1 ? (const float *)k + t * k_stride + hh * width
+                                         : (const float *)v + t * v_stride + hh * width;
+            float *dst = kind == 0 ? (float *)q + t * q_stride + hh * width
+                       : (kind == 1 ? (float *)keys : (float *)values) + (size_t)position * kvd + hh * width;
+            mock_norm(row, src, kind == 0 ? (const float *)q_norm : kind == 1 ? (const float *)k_norm : NULL, width,
+                      eps);
+            if (kind == 2) {
+                memcpy(dst, row, width * sizeof(float));
+                continue;
+            }
+            for (size_t j = 0; j < half; ++j) {
+                const float angle = (float)position * ((const float *)freq)[j];
+                const float c = cosf(angle), s = sinf(angle), a = row[j], b = row[j + half];
+                dst[j] = a * c - b * s;
+                dst[j + half] = b * c + a * s;
+            }
+        }
+    }
+    return 0;
+}
+
+API int nya_hip_softcap(uintptr_t x, size_t n, float cap, uintptr_t stream)
+{
+    if (!x || !n || !(cap > 0.0f) || !stream) return 1;
+    if (injected_fault()) return -1;
+    for (size_t i = 0; i < n; ++i) ((float *)x)[i] = cap * tanhf(((float *)x)[i] / cap);
     return 0;
 }
 

@@ -132,9 +132,16 @@ def check_logits(ref: np.ndarray, got: np.ndarray, where: str):
     return float(scaled.max())
 
 
-def check_kv(ref: Session, got: Session, layers: int, width: int, count: int):
+def kv_widths(shape) -> list[int]:
+    """Floats per cached position of each layer."""
+    if hasattr(shape, "kv_widths"):
+        return shape.kv_widths()
+    return [shape.kv_heads * (shape.embedding // shape.heads)] * shape.blocks
+
+
+def check_kv(ref: Session, got: Session, widths: list[int], count: int):
     worst = 0.0
-    for layer in range(layers):
+    for layer, width in enumerate(widths):
         for a, b in zip(ref.kv(layer, 0, count, width), got.kv(layer, 0, count, width)):
             assert np.all(np.isfinite(b))
             scaled = np.abs(b.astype(np.float64) - a) / (1 + np.abs(a.astype(np.float64)))
@@ -152,14 +159,14 @@ def compare(lib, path: Path, shape, provider: str, tokens: list[int], chunks=(5,
     ref_model, model = Model(lib, path, None), Model(lib, path, provider)
     assert model.provider() == provider
     ref, got = Session(ref_model, shape.context), Session(model, shape.context)
-    width = shape.kv_heads * (shape.embedding // shape.heads)
+    widths = kv_widths(shape)
     out = {"execution": got.execution(), "logit": 0.0, "kv": 0.0}
     try:
         for i, t in enumerate(tokens):
             assert ref.run([t], True) == 0 and got.run([t], True) == 0
             out["logit"] = max(out["logit"], check_logits(ref.logits(shape.vocabulary), got.logits(shape.vocabulary),
                                                           f"decode position {i}"))
-        out["kv"] = check_kv(ref, got, shape.blocks, width, len(tokens))
+        out["kv"] = check_kv(ref, got, widths, len(tokens))
         # Reset, then prefill chunks (the plan's prefill) between decode steps.
         ref.reset()
         got.reset()
@@ -170,7 +177,7 @@ def compare(lib, path: Path, shape, provider: str, tokens: list[int], chunks=(5,
             at += n
             out["logit"] = max(out["logit"], check_logits(ref.logits(shape.vocabulary), got.logits(shape.vocabulary),
                                                           f"chunk ending at {at}"))
-        out["kv"] = max(out["kv"], check_kv(ref, got, shape.blocks, width, at))
+        out["kv"] = max(out["kv"], check_kv(ref, got, widths, at))
         out["stats"] = got.stats()
     finally:
         got.close()

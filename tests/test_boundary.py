@@ -35,7 +35,8 @@ def test_kernel_library_exports_its_header():
                     "nya_hip_rope_qkv", "nya_hip_attention", "nya_hip_attention_split", "nya_hip_silu_mul", "nya_hip_greedy",
                     "nya_hip_matvec_gated", "nya_hip_matvec_swiglu", "nya_hip_matvec_residual",
                     "nya_hip_matvec_swiglu_scaled", "nya_hip_silu_pairs",
-                    "nya_hip_matvec_normed", "nya_hip_matvec_normed_rope", "nya_hip_matvec_scaled_rope"}
+                    "nya_hip_matvec_normed", "nya_hip_matvec_normed_rope", "nya_hip_matvec_scaled_rope",
+                    "nya_hip_post_norm", "nya_hip_head_norm_rope", "nya_hip_gelu_mul", "nya_hip_softcap"}
     assert want <= exported(KERNEL_LIBRARY)
 
 
@@ -85,7 +86,7 @@ def test_unaddressable_block_matrices_decline(kernels, t, block_bytes):
 
 def test_queries(kernels):
     L = kernels.lib
-    assert L.nya_hip_abi_version() == 1
+    assert L.nya_hip_abi_version() == 2
     b = ctypes.c_size_t()
     for t, block, size in [(F32, 1, 4), (F16, 1, 2), (BF16, 1, 2), (Q4_0, 32, 18), (Q8_0, 32, 34),
                            (Q4_K, 256, 144), (Q6_K, 256, 210)]:

@@ -14,8 +14,8 @@ import ctypes
 import pytest
 
 from fyodor_amd import F16, KERNEL_LIBRARY, Q4_0, Q4_K, Q6_K, Q8_0
-from gguf_model import LlamaShape, write
-from resident_check import bind, compare, plan_against_engine
+from gguf_model import GemmaShape, LlamaShape, write, write_gemma
+from resident_check import Model, Session, bind, compare, plan_against_engine
 from conftest import DROPIN_LIBRARY
 
 pytestmark = pytest.mark.gpu
@@ -219,3 +219,77 @@ def test_interleaved_gate_up_on_gpu(session_lib, rocm_env, tmp_path):
     out = compare(session_lib, path, shape, "rocm", [5, 17, 200, 3, 42, 99, 250, 1, 7, 64])
     print(out["logit"], out["kv"], flush=True)
     assert out["execution"] == "resident"
+
+
+# Gemma 4 text models (the engine's is_gemma branch): local layers with an
+# 8..352-position window and global layers of their own head widths, layers
+# reading an earlier layer's cache, keys standing in for values, per-head
+# q/k/v norms with the half-split rotation, post norms, output scales, the
+# GELU gate and a final soft cap.
+GEMMA_GPU = {
+    "widths-128-256": dict(embedding=512, heads=8, kv_heads=4, width=256, local_width=128, hidden=1024,
+                           window=16),
+    "width-80-q8": dict(embedding=512, heads=8, kv_heads=2, width=128, local_width=80, hidden=1536, window=24,
+                        types={"embedding": F16, "output": Q8_0, "attention": Q8_0, "gate_up": Q4_0, "down": Q8_0}),
+    "untied-plain": dict(embedding=768, heads=8, kv_heads=2, width=128, local_width=64, hidden=2048, window=12,
+                         local=(1, 0, 1, 0), shared_kv_layers=0, global_value=True, tied_output=False,
+                         output_scales=(), softcap=0.0),
+}
+
+
+@pytest.mark.parametrize("name", list(GEMMA_GPU))
+def test_gemma_plan_on_gpu(session_lib, rocm_env, tmp_path, name):
+    shape = GemmaShape(**GEMMA_GPU[name], context=64, vocabulary=1000, seed=7)
+    path = tmp_path / "gemma.gguf"
+    write_gemma(path, shape)
+    print(f"gemma {name}", flush=True)
+    out = compare(session_lib, path, shape, "rocm", TOKENS, chunks=(37, 1, 5, 1, 13, 1))
+    print(f"gemma {name}: worst scaled logit error {out['logit']:.3g}, KV {out['kv']:.3g}", flush=True)
+    assert out["execution"] == "resident"
+
+
+def test_gemma_long_context_on_gpu(session_lib, rocm_env, tmp_path):
+    """Past 320 positions: the global layers' split attention, the local
+    layers' split over a 352-position window."""
+    shape = GemmaShape(embedding=512, heads=8, kv_heads=4, width=256, local_width=128, hidden=1024, window=352,
+                       context=440, vocabulary=1000, seed=8)
+    path = tmp_path / "gemma.gguf"
+    write_gemma(path, shape)
+    tokens = [(i * 29 + 7) % shape.vocabulary for i in range(400)]
+    out = compare(session_lib, path, shape, "rocm", tokens, chunks=(395, 1, 20, 1))
+    print(f"gemma long context: worst scaled logit error {out['logit']:.3g}, KV {out['kv']:.3g}", flush=True)
+    assert out["execution"] == "resident"
+
+
+def test_gemma_graph_replays_match_direct_launches(session_lib, rocm_env, tmp_path, monkeypatch):
+    """A Gemma decode token replayed as a captured graph (the embedding
+    scale, head norms, post norms, GELU gate and soft cap among its
+    launches) gives the logits of direct launches bit for bit."""
+    import numpy as np
+    shape = GemmaShape(**GEMMA_GPU["widths-128-256"], context=64, vocabulary=1000, seed=9)
+    path = tmp_path / "gemma.gguf"
+    write_gemma(path, shape)
+
+    def run(graphs: bool):
+        monkeypatch.setenv("NYA_ROCM_GRAPHS", "1" if graphs else "0")
+        model = Model(session_lib, path, "rocm")
+        session = Session(model, shape.context)
+        rows = []
+        try:
+            assert session.run(TOKENS[:5], False) == 0
+            rows.append(session.logits(shape.vocabulary))
+            for t in TOKENS[5:30]:
+                assert session.run([t], True) == 0
+                rows.append(session.logits(shape.vocabulary))
+            assert session.execution() == "resident"
+            return rows, session.stats()
+        finally:
+            session.close()
+            model.close()
+
+    graphed, g = run(True)
+    direct, d = run(False)
+    assert g.graph_replays > 0 and d.graph_replays == 0
+    assert g.kernel_launches == d.kernel_launches
+    for i, (a, b) in enumerate(zip(graphed, direct)):
+        assert np.array_equal(a, b), f"row {i}"

@@ -52,10 +52,17 @@ def env():
     rt, kern = Runtime(), Kernels()
     L = kern.lib
     L.nya_hip_step.argtypes = [_up, _u, _sz, _up]
-    L.nya_hip_embed.argtypes = [_up, _u, _sz, _sz, _up, _sz, _up, _up]
+    L.nya_hip_embed.argtypes = [_up, _u, _sz, _sz, _up, _sz, _up, _f, _up]
     L.nya_hip_rms_norm.argtypes = [_up, _up, _up, _up, _sz, _sz, _f, _up]
     L.nya_hip_rope_qkv.argtypes = [_up, _sz, _up, _sz, _up, _sz, _sz, _sz, _sz, _sz, _up, _up, _sz, _up, _up, _up]
-    L.nya_hip_attention.argtypes = [_up, _sz, _up, _up, _up, _up, _up, _sz, _sz, _sz, _sz, _sz, _f, _up]
+    L.nya_hip_attention.argtypes = [_up, _sz, _up, _up, _up, _up, _up, _sz, _sz, _sz, _sz, _sz, _sz, _f, _up]
+    L.nya_hip_attention_split.argtypes = [_up, _sz, _up, _up, _up, _up, _up, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _f,
+                                          _up]
+    L.nya_hip_post_norm.argtypes = [_up, _up, _up, _f, _up, _up, _sz, _sz, _f, _up]
+    L.nya_hip_head_norm_rope.argtypes = [_up, _sz, _up, _sz, _up, _sz, _sz, _sz, _sz, _sz, _up, _up, _f, _up, _up,
+                                         _sz, _up, _up, _up]
+    L.nya_hip_gelu_mul.argtypes = [_up, _sz, _up, _sz, _up, _sz, _sz, _up]
+    L.nya_hip_softcap.argtypes = [_up, _sz, _f, _up]
     L.nya_hip_silu_mul.argtypes = [_up, _sz, _up, _sz, _up, _sz, _sz, _up]
     L.nya_hip_matvec_gated.argtypes = [_up, _u, _sz, _sz, _up, _up, _up, _up]
     L.nya_hip_matvec_swiglu.argtypes = [_up, _u, _sz, _sz, _up, _up, _up]
@@ -115,22 +122,26 @@ def test_step_slot(env):
 
 
 @pytest.mark.parametrize("type_id", [F32, F16, BF16, Q8_0, Q4_0, Q4_K, Q6_K])
-def test_embed_exact(env, oracle, type_id):
+@pytest.mark.parametrize("scale", [1.0, float(np.sqrt(np.float32(512)))], ids=["plain", "gemma"])
+def test_embed_exact(env, oracle, type_id, scale):
+    """The decoded rows, times Gemma's sqrt(d) (the engine's float
+    product, backend/core/llm_cpu.c:453) where asked: bit for bit."""
     rt, L, stream = env
     rows, cols = 7, 512
     w = synth.weights(type_id, rows, cols, seed=40 + type_id)
-    ref = oracle.dequant(w, type_id, rows, cols).reshape(rows, cols)
+    ref = oracle.dequant(w, type_id, rows, cols).reshape(rows, cols) * np.float32(scale)
     tokens = np.array([3, 0, rows - 1, rows + 5, 3], np.uint32)   # one id past the matrix
     dev = Dev(rt)
     try:
         wd, td, out = dev.put(w), dev.put(tokens), dev.empty(4 * cols * len(tokens))
-        assert L.nya_hip_embed(wd, type_id, rows, cols, td, len(tokens), out, stream) == 0
+        assert L.nya_hip_embed(wd, type_id, rows, cols, td, len(tokens), out, scale, stream) == 0
         rt.sync(stream)
         got = dev.get(out, np.empty((len(tokens), cols), np.float32))
         for i, t in enumerate(tokens):
             want = ref[t] if t < rows else np.zeros(cols, np.float32)
             assert np.array_equal(got[i].view(np.uint32), want.view(np.uint32)), f"token {i} (id {t})"
-        assert L.nya_hip_embed(wd, type_id, rows, cols, td, 0, out, stream) == 1      # no tokens
+        assert L.nya_hip_embed(wd, type_id, rows, cols, td, 0, out, 1.0, stream) == 1      # no tokens
+        assert L.nya_hip_embed(wd, type_id, rows, cols, td, 1, out, float("inf"), stream) == 1
     finally:
         dev.close()
 
@@ -225,10 +236,12 @@ def test_rope_qkv(env, heads, kv_heads, width, layout):
         dev.close()
 
 
-def attention_ref(q, keys, values, heads, kv_heads, width, length, scale):
+def attention_ref(q, keys, values, heads, kv_heads, width, length, scale, window=0):
+    """Positions [0, length), the last `window` of them when window > 0."""
+    first = length - window if 0 < window < length else 0
     q = q.reshape(heads, width).astype(np.float64)
-    k = keys[:length].reshape(length, kv_heads, width).astype(np.float64)
-    v = values[:length].reshape(length, kv_heads, width).astype(np.float64)
+    k = keys[first:length].reshape(length - first, kv_heads, width).astype(np.float64)
+    v = values[first:length].reshape(length - first, kv_heads, width).astype(np.float64)
     group = heads // kv_heads
     out = np.empty((heads, width))
     for h in range(heads):
@@ -239,14 +252,17 @@ def attention_ref(q, keys, values, heads, kv_heads, width, length, scale):
     return out.reshape(-1)
 
 
-@pytest.mark.parametrize("heads,kv_heads,width,length,count", [
-    (32, 8, 128, 1, 1), (32, 8, 128, 37, 1), (32, 8, 128, 1000, 1), (8, 8, 64, 300, 1), (6, 2, 80, 129, 1),
-    (4, 1, 256, 513, 1), (8, 2, 128, 8192, 1), (8, 2, 128, 9000, 1),
-    (32, 4, 64, 64, 64), (8, 2, 128, 300, 5), (6, 2, 80, 40, 7), (4, 2, 128, 8300, 3),
+@pytest.mark.parametrize("heads,kv_heads,width,length,count,window", [
+    (32, 8, 128, 1, 1, 0), (32, 8, 128, 37, 1, 0), (32, 8, 128, 1000, 1, 0), (8, 8, 64, 300, 1, 0),
+    (6, 2, 80, 129, 1, 0), (4, 1, 256, 513, 1, 0), (8, 2, 128, 8192, 1, 0), (8, 2, 128, 9000, 1, 0),
+    (32, 4, 64, 64, 64, 0), (8, 2, 128, 300, 5, 0), (6, 2, 80, 40, 7, 0), (4, 2, 128, 8300, 3, 0),
+    (8, 2, 128, 1000, 1, 64), (4, 1, 256, 513, 3, 100), (6, 2, 80, 129, 7, 20), (8, 4, 64, 40, 12, 32),
+    (8, 2, 128, 9000, 2, 4096), (8, 2, 128, 30, 4, 512),
 ])
-def test_attention(env, heads, kv_heads, width, length, count):
+def test_attention(env, heads, kv_heads, width, length, count, window):
     """`count` causal queries ending at position length - 1, the query rows
-    strided past the fused k|v part as in the plan's buffers."""
+    strided past the fused k|v part as in the plan's buffers; with a window,
+    each query attends its last `window` positions (a sliding layer)."""
     rt, L, stream = env
     rng = np.random.default_rng(length * 7 + width + count)
     max_length = length + 5
@@ -257,38 +273,38 @@ def test_attention(env, heads, kv_heads, width, length, count):
     positions = np.arange(length - count, length, dtype=np.int32)
     scale = float(1 / np.sqrt(np.float32(width)))
     ref = np.concatenate([attention_ref(q[i, :heads * width], keys, values, heads, kv_heads, width, int(p) + 1,
-                                        np.float32(scale)) for i, p in enumerate(positions)])
+                                        np.float32(scale), window) for i, p in enumerate(positions)])
     dev = Dev(rt)
     try:
         qd, kd, vd, pd = dev.put(q), dev.put(keys), dev.put(values), dev.put(positions)
         od = dev.empty(4 * count * heads * width)
         sd = dev.empty(4 * count * heads * max_length) if max_length > 8192 else 0
-        assert L.nya_hip_attention(qd, q_stride, kd, vd, od, sd, pd, count, heads, kv_heads, width, max_length, scale,
-                                   stream) == 0
+        assert L.nya_hip_attention(qd, q_stride, kd, vd, od, sd, pd, count, heads, kv_heads, width, max_length,
+                                   window, scale, stream) == 0
         rt.sync(stream)
         err = scaled_error(dev.get(od, np.empty(count * heads * width, np.float32)), ref)
-        print(f"attention {heads}/{kv_heads} x {width}, length {length}, {count} queries: scaled error {err:.3g}",
-              flush=True)
+        print(f"attention {heads}/{kv_heads} x {width}, length {length}, {count} queries, window {window}: "
+              f"scaled error {err:.3g}", flush=True)
         assert err <= 1e-5
     finally:
         dev.close()
 
 
-SPLIT_CASES = [(32, 8, 128, 4096, 1, 64), (32, 4, 64, 1000, 1, 16), (8, 8, 128, 300, 1, 8),
-               (16, 8, 128, 2000, 3, 32), (8, 2, 256, 5000, 2, 8), (32, 4, 64, 20000, 1, 32),
-               (32, 8, 128, 5, 1, 64), (32, 8, 128, 257, 33, 8), (8, 2, 128, 600, 2, 300)]
+SPLIT_CASES = [(32, 8, 128, 4096, 1, 64, 0), (32, 4, 64, 1000, 1, 16, 0), (8, 8, 128, 300, 1, 8, 0),
+               (16, 8, 128, 2000, 3, 32, 0), (8, 2, 256, 5000, 2, 8, 0), (32, 4, 64, 20000, 1, 32, 0),
+               (32, 8, 128, 5, 1, 64, 0), (32, 8, 128, 257, 33, 8, 0), (8, 2, 128, 600, 2, 300, 0),
+               (32, 8, 128, 4096, 1, 64, 1024), (8, 2, 256, 5000, 2, 8, 700), (16, 8, 128, 2000, 33, 32, 100)]
 
 
-@pytest.mark.parametrize("heads,kv_heads,width,length,count,splits", SPLIT_CASES,
-                         ids=[f"{h}/{k}x{w}-len{n}-q{c}-s{s}" for h, k, w, n, c, s in SPLIT_CASES])
-def test_attention_split(env, heads, kv_heads, width, length, count, splits):
+@pytest.mark.parametrize("heads,kv_heads,width,length,count,splits,window", SPLIT_CASES,
+                         ids=[f"{h}/{k}x{w}-len{n}-q{c}-s{s}-w{win}" for h, k, w, n, c, s, win in SPLIT_CASES])
+def test_attention_split(env, heads, kv_heads, width, length, count, splits, window):
     """The attention split over the cached positions (every query head of a
     KV head per workgroup, then the combination of the partial softmaxes):
     against the float64 statement of the engine's step, and beside the
     one-workgroup-per-head kernel; more splits than positions leave empty
-    partials."""
+    partials; a window splits only the positions it keeps."""
     rt, L, stream = env
-    L.nya_hip_attention_split.argtypes = [_up, _sz, _up, _up, _up, _up, _up, _sz, _sz, _sz, _sz, _sz, _sz, _f, _up]
     rng = np.random.default_rng(length * 11 + width + count + splits)
     max_length = length + 3
     q_stride = (heads + 2 * kv_heads) * width
@@ -298,19 +314,19 @@ def test_attention_split(env, heads, kv_heads, width, length, count, splits):
     positions = np.arange(length - count, length, dtype=np.int32)
     scale = float(1 / np.sqrt(np.float32(width)))
     ref = np.concatenate([attention_ref(q[i, :heads * width], keys, values, heads, kv_heads, width, int(p) + 1,
-                                        np.float32(scale)) for i, p in enumerate(positions)])
+                                        np.float32(scale), window) for i, p in enumerate(positions)])
     dev = Dev(rt)
     try:
         qd, kd, vd, pd = dev.put(q), dev.put(keys), dev.put(values), dev.put(positions)
         od, od2 = dev.empty(4 * count * heads * width), dev.empty(4 * count * heads * width)
         part = dev.empty(4 * count * heads * splits * (width + 2))
         sd = dev.empty(4 * count * heads * max_length) if max_length > 8192 else 0
-        print(f"attention_split {heads}/{kv_heads} x {width}, length {length}, {count} queries, {splits} splits",
-              flush=True)
+        print(f"attention_split {heads}/{kv_heads} x {width}, length {length}, {count} queries, {splits} splits, "
+              f"window {window}", flush=True)
         assert L.nya_hip_attention_split(qd, q_stride, kd, vd, od, part, pd, count, heads, kv_heads, width,
-                                         max_length, splits, scale, stream) == 0
+                                         max_length, window, splits, scale, stream) == 0
         assert L.nya_hip_attention(qd, q_stride, kd, vd, od2, sd, pd, count, heads, kv_heads, width, max_length,
-                                   scale, stream) == 0
+                                   window, scale, stream) == 0
         rt.sync(stream)
         got = dev.get(od, np.empty(count * heads * width, np.float32))
         err = scaled_error(got, ref)
@@ -323,17 +339,16 @@ def test_attention_split(env, heads, kv_heads, width, length, count, splits):
 
 def test_attention_split_declines(env):
     rt, L, stream = env
-    L.nya_hip_attention_split.argtypes = [_up, _sz, _up, _up, _up, _up, _up, _sz, _sz, _sz, _sz, _sz, _sz, _f, _up]
     dev = Dev(rt)
     try:
         p = dev.empty(4 * 4096)
         args = lambda heads, kv, width, max_length, splits: (p, (heads + 2 * kv) * width, p, p, p, p, p, 1, heads, kv,
-                                                            width, max_length, splits, 1.0, stream)
+                                                            width, max_length, 0, splits, 1.0, stream)
         assert L.nya_hip_attention_split(*args(32, 8, 80, 1000, 8)) == 1      # width 80
         assert L.nya_hip_attention_split(*args(48, 3, 128, 1000, 8)) == 1     # 16 query heads per KV head
         assert L.nya_hip_attention_split(*args(32, 4, 256, 1000, 8)) == 1     # 8 heads of width 256
         assert L.nya_hip_attention_split(*args(32, 8, 128, 9000, 8)) == 1     # 1125 positions per split
-        assert L.nya_hip_attention_split(p + 4, 384, p, p, p, p, p, 1, 2, 1, 128, 100, 4, 1.0, stream) == 1  # q align
+        assert L.nya_hip_attention_split(p + 4, 384, p, p, p, p, p, 1, 2, 1, 128, 100, 0, 4, 1.0, stream) == 1  # q align
     finally:
         dev.close()
 
@@ -343,8 +358,8 @@ def test_attention_declines(env):
     dev = Dev(rt)
     try:
         p = dev.empty(4 * 4 * 512)
-        assert L.nya_hip_attention(p, 1024, p, p, p, p, p, 1, 2, 2, 512, 1, 1.0, stream) == 1   # width > 256
-        assert L.nya_hip_attention(p, 256, p, p, p, 0, p, 1, 2, 2, 128, 9000, 1.0, stream) == 1  # scratch needed
+        assert L.nya_hip_attention(p, 1024, p, p, p, p, p, 1, 2, 2, 512, 1, 0, 1.0, stream) == 1   # width > 256
+        assert L.nya_hip_attention(p, 256, p, p, p, 0, p, 1, 2, 2, 128, 9000, 0, 1.0, stream) == 1  # scratch needed
     finally:
         dev.close()
 
@@ -372,6 +387,167 @@ def test_silu_mul(env, layout):
         assert scaled_error(dev.get(out, g), ref) <= 2e-6
         if layout != "in-place":
             assert L.nya_hip_silu_mul(gd, gs, ud, us, gd, n, count, stream) == 1   # overlapping output
+    finally:
+        dev.close()
+
+
+def norm32(x, w, eps):
+    """The engine's RMS norm of each row (backend/core/llm_cpu.c:83-104) in
+    float32 steps: the sum of squares in double, its scale rounded to
+    float32, then x * scale * w."""
+    x = np.asarray(x, np.float32)
+    scale = (1.0 / np.sqrt(np.sum(x.astype(np.float64) ** 2, axis=-1, keepdims=True) / x.shape[-1] +
+                           np.float64(np.float32(eps)))).astype(np.float32)
+    y = x * scale
+    return y * w if w is not None else y
+
+
+@pytest.mark.parametrize("n", [640, 1000, 2560, 5376, 16384])
+@pytest.mark.parametrize("form", ["post", "plain", "no-residual"])
+def test_post_norm(env, n, form):
+    """Gemma's residual add through the branch's post norm, the block's
+    output scale, then the next norm (backend/core/llm_cpu.c:514-515,
+    :531-547): x written back and out against the engine's float32 steps;
+    without a post weight the plain add, without a residual only the scale
+    and the norm."""
+    rt, L, stream = env
+    count, eps, oscale = 3, 1e-6, np.float32(0.8125)
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal((count, n)).astype(np.float32)
+    r = (3 * rng.standard_normal((count, n))).astype(np.float32)
+    post = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    if form == "post":
+        xs = ((x + norm32(r, post, eps)) * oscale).astype(np.float32)
+    elif form == "plain":
+        xs = ((x + r) * oscale).astype(np.float32)
+    else:
+        xs = (x * oscale).astype(np.float32)
+    ref = norm32(xs, w, eps)
+    dev = Dev(rt)
+    try:
+        xd, rd, pd, wd, od = dev.put(x), dev.put(r), dev.put(post), dev.put(w), dev.empty(4 * n * count)
+        rarg, parg = (rd, pd) if form == "post" else (rd, 0) if form == "plain" else (0, 0)
+        assert L.nya_hip_post_norm(xd, rarg, parg, float(oscale), wd, od, n, count, eps, stream) == 0
+        rt.sync(stream)
+        assert scaled_error(dev.get(xd, x), xs.astype(np.float64)) <= 2e-6
+        assert scaled_error(dev.get(od, x), ref.astype(np.float64)) <= 2e-6
+        assert np.array_equal(dev.get(rd, r), r)      # the branch output is read, not written
+        assert L.nya_hip_post_norm(xd, 0, pd, 1.0, wd, od, n, count, eps, stream) == 1       # post without residual
+        assert L.nya_hip_post_norm(xd, rd, pd, 1.0, wd, od, 16385, 1, eps, stream) == 1      # wider than 16384
+    finally:
+        dev.close()
+
+
+def rotate_halves(v, c, s):
+    """Gemma's rotation of one head (backend/core/llm_cpu.c:345-358)."""
+    half = v.shape[-1] // 2
+    a, b = v[..., :half].astype(np.float64), v[..., half:].astype(np.float64)
+    return np.concatenate([a * c - b * s, b * c + a * s], -1)
+
+
+@pytest.mark.parametrize("heads,kv_heads,width", [(8, 4, 256), (4, 2, 128), (6, 2, 80), (2, 1, 64)])
+@pytest.mark.parametrize("form", ["qkv", "key-as-value", "q-only"])
+def test_head_norm_rope(env, heads, kv_heads, width, form):
+    """The Gemma q/k/v step: per-head norms (q and k weighted, v without a
+    weight), the half-split rotation of q (in place) and k (into its cache
+    slot), v into its slot; a key projection standing in for the value; a
+    layer reading another's cache (q only); a position outside the cache
+    leaves everything alone."""
+    rt, L, stream = env
+    count, capacity, eps = 4, 300, 1e-6
+    positions = np.array([17, 18, 250, capacity + 1], np.int32)
+    qd, kvd, half = heads * width, kv_heads * width, width // 2
+    rng = np.random.default_rng(heads * width + len(form))
+    stride = qd + 2 * kvd
+    rows = (2 * rng.standard_normal((count, stride))).astype(np.float32)
+    q_norm = (1 + 0.1 * rng.standard_normal(width)).astype(np.float32)
+    k_norm = (1 + 0.1 * rng.standard_normal(width)).astype(np.float32)
+    freq = (10000.0 ** (-np.arange(half) / half)).astype(np.float32)
+    keys0 = rng.standard_normal((capacity, kvd)).astype(np.float32)
+    values0 = rng.standard_normal((capacity, kvd)).astype(np.float32)
+    dev = Dev(rt)
+    try:
+        rd, qn, kn, fd, pd = dev.put(rows), dev.put(q_norm), dev.put(k_norm), dev.put(freq), dev.put(positions)
+        kd, vd = dev.put(keys0), dev.put(values0)
+        k_at = rd + 4 * qd
+        v_at = k_at if form == "key-as-value" else rd + 4 * (qd + kvd)
+        kp = 0 if form == "q-only" else k_at
+        print(f"head_norm_rope {heads}/{kv_heads} x {width}, {form}", flush=True)
+        assert L.nya_hip_head_norm_rope(rd, stride, kp, stride, v_at, stride, count, heads, kv_heads, width, qn, kn,
+                                        eps, fd, pd, capacity, kd, vd, stream) == 0
+        rt.sync(stream)
+        got = dev.get(rd, rows)
+        keys, values = dev.get(kd, keys0), dev.get(vd, values0)
+        for i, pos in enumerate(positions):
+            if pos >= capacity:
+                assert np.array_equal(got[i], rows[i])
+                continue
+            angle = (np.float32(pos) * freq).astype(np.float64)
+            c, s = np.cos(angle), np.sin(angle)
+            q = norm32(rows[i, :qd].reshape(heads, width), q_norm, eps)
+            assert scaled_error(got[i, :qd], rotate_halves(q, c, s).reshape(-1)) <= 2e-6
+            assert np.array_equal(got[i, qd:], rows[i, qd:])   # k and v rows are read, not written
+            if form == "q-only":
+                continue
+            k = norm32(rows[i, qd:qd + kvd].reshape(kv_heads, width), k_norm, eps)
+            v_src = rows[i, qd:qd + kvd] if form == "key-as-value" else rows[i, qd + kvd:]
+            v = norm32(v_src.reshape(kv_heads, width), None, eps)
+            assert scaled_error(keys[pos], rotate_halves(k, c, s).reshape(-1)) <= 2e-6
+            assert scaled_error(values[pos], v.reshape(-1).astype(np.float64)) <= 2e-6
+        touched = positions[positions < capacity] if form != "q-only" else np.array([], np.int32)
+        untouched = np.setdiff1d(np.arange(capacity), touched)
+        assert np.array_equal(keys[untouched], keys0[untouched])
+        assert np.array_equal(values[untouched], values0[untouched])
+        assert L.nya_hip_head_norm_rope(rd, stride, kp, stride, v_at, stride, count, heads, kv_heads, 258, qn, kn,
+                                        eps, fd, pd, capacity, kd, vd, stream) == 1    # wider than 256
+    finally:
+        dev.close()
+
+
+@pytest.mark.parametrize("layout", ["fused", "split", "in-place"])
+def test_gelu_mul(env, layout):
+    """Gemma's gate (backend/core/llm_cpu.c:329-341) against float64."""
+    rt, L, stream = env
+    rng = np.random.default_rng(6)
+    n = 10240 if layout != "split" else 1001
+    count = 1 if layout == "in-place" else 3
+    g = (4 * rng.standard_normal((count, n))).astype(np.float32)
+    u = rng.standard_normal((count, n)).astype(np.float32)
+    x = g.astype(np.float64)
+    ref = 0.5 * x * (1 + np.tanh(0.7978845608028654 * (x + 0.044715 * x ** 3))) * u
+    dev = Dev(rt)
+    try:
+        if layout == "split":
+            gd, ud = dev.put(g), dev.put(u)
+            gs = us = n
+        else:
+            gu = dev.put(np.concatenate([g, u], axis=1))
+            gd, ud, gs, us = gu, gu + 4 * n, 2 * n, 2 * n
+        out = gd if layout == "in-place" else dev.empty(4 * n * count)
+        assert L.nya_hip_gelu_mul(gd, gs, ud, us, out, n, count, stream) == 0
+        rt.sync(stream)
+        assert scaled_error(dev.get(out, g), ref) <= 2e-6
+        if layout != "in-place":
+            assert L.nya_hip_gelu_mul(gd, gs, ud, us, gd, n, count, stream) == 1   # overlapping output
+    finally:
+        dev.close()
+
+
+def test_softcap(env):
+    """The final soft cap (backend/core/llm_cpu.c:562-565) against float64."""
+    rt, L, stream = env
+    rng = np.random.default_rng(8)
+    x = (40 * rng.standard_normal(3 * 262144 + 5)).astype(np.float32)
+    cap = 30.0
+    ref = cap * np.tanh(x.astype(np.float64) / cap)
+    dev = Dev(rt)
+    try:
+        xd = dev.put(x)
+        assert L.nya_hip_softcap(xd, x.size, cap, stream) == 0
+        rt.sync(stream)
+        assert scaled_error(dev.get(xd, x), ref) <= 2e-6
+        assert L.nya_hip_softcap(xd, x.size, 0.0, stream) == 1
     finally:
         dev.close()
 

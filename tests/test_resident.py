@@ -19,7 +19,7 @@ import subprocess
 import pytest
 
 from fyodor_amd import Q4_0, Q4_K, Q6_K, Q8_0, F16
-from gguf_model import LlamaShape, write
+from gguf_model import GemmaShape, LlamaShape, write, write_gemma
 from resident_check import bind, compare
 
 TOKENS = [5, 17, 200, 3, 42, 99, 250, 1, 7, 64, 128, 33]
@@ -168,3 +168,59 @@ def test_interleaved_gate_up(session_lib, tmp_path, monkeypatch):
         launches[name] = out["stats"].kernel_launches
     # 6 decode tokens, then chunks (5, 1, 1, 7, 1): 9 one-token runs.
     assert launches["unfused"] - launches["fused"] == 9 * shape.blocks, launches
+
+
+GEMMA_VARIANTS = {
+    # Tied output, global layers storing the key as the value, two layers
+    # reading earlier caches, output scales, a soft cap, an 8-position window.
+    "tied-shared": GemmaShape(),
+    # An output matrix of its own, value matrices everywhere, no sharing,
+    # no output scales and no soft cap.
+    "untied-plain": GemmaShape(local=(1, 0, 1, 0), shared_kv_layers=0, global_value=True, tied_output=False,
+                               output_scales=(), softcap=0.0),
+    # Other weight types, local heads as wide as the global ones.
+    "q8-q4-f16": GemmaShape(local_width=128, types={"embedding": F16, "output": Q8_0, "attention": Q8_0,
+                                                    "gate_up": Q4_0, "down": Q8_0}),
+}
+
+
+@pytest.mark.parametrize("variant", list(GEMMA_VARIANTS))
+def test_gemma_plan_matches_reference_session(session_lib, tmp_path, variant):
+    """A Gemma 4 text model (tests/gguf_model.py GemmaShape: the engine's
+    is_gemma branch, backend/core/llm_cpu.c:452-566) runs resident: every
+    decode step's logits and the KV caches of every layer (a shared layer
+    reads its source's) match the engine's reference session, through
+    windows shorter than the sequence and prompt chunks."""
+    shape = GEMMA_VARIANTS[variant]
+    path = tmp_path / "gemma.gguf"
+    write_gemma(path, shape)
+    out = compare(session_lib, path, shape, "rocm", TOKENS)
+    assert out["execution"] == "resident"
+    assert out["stats"].kernel_launches > 0
+
+
+def test_gemma_long_context_split(session_lib, tmp_path):
+    """Past 320 positions the global layers take the split attention and the
+    local layers (a 352-position window, also past the split threshold) split
+    only the window: logits and KV still match the engine."""
+    shape = GemmaShape(context=420, window=352)
+    path = tmp_path / "gemma.gguf"
+    write_gemma(path, shape)
+    tokens = [(i * 29 + 7) % shape.vocabulary for i in range(390)]
+    out = compare(session_lib, path, shape, "rocm", tokens, chunks=(390, 1, 20, 1))
+    assert out["execution"] == "resident"
+
+
+def test_gemma_declined_without_its_steps(session_lib, tmp_path, monkeypatch):
+    """A kernel library without the Gemma steps declines a Gemma model (the
+    engine runs its reference path, same logits) and still runs LLaMA."""
+    plain = mock_without(tmp_path, ("nya_hip_head_norm_rope",))
+    monkeypatch.setenv("NYA_ROCM_KERNEL_LIBRARY", str(plain))
+    shape = GemmaShape()
+    path = tmp_path / "gemma.gguf"
+    write_gemma(path, shape)
+    assert compare(session_lib, path, shape, "rocm", TOKENS[:4])["execution"] == "cpu-reference"
+    llama = LlamaShape(context=16)
+    path = tmp_path / "llama.gguf"
+    write(path, llama)
+    assert compare(session_lib, path, llama, "rocm", TOKENS[:4])["execution"] == "resident"

@@ -390,7 +390,7 @@ NYA_HIP_EXPORT int nya_hip_head_norm_rope(uintptr_t q, size_t q_stride, uintptr_
     uintptr_t stream)
 {
     if (!vec(q) || !vec(q_norm) || !vec(frequencies) || !vec(positions) || !tokens_ok(count) || !count_ok(heads) ||
-        !count_ok(kv_heads) || !count_ok(width) || width % 2 || width > 256 || !count_ok(capacity) ||
+        !count_ok(kv_heads) || !count_ok(width) || width % 2 || width > 512 || !count_ok(capacity) ||
         heads > 65535 || kv_heads > 65535 || heads + 2 * kv_heads > 65535 || !(epsilon >= 0.f) ||
         q_stride < heads * width || q_stride > (size_t)INT_MAX || capacity > (size_t)INT_MAX / (kv_heads * width))
         return 1;
@@ -431,7 +431,7 @@ NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t key
     size_t max_length, size_t window, float scale, uintptr_t stream)
 {
     if (!vec(q) || !vec(keys) || !vec(values) || !vec(out) || !vec(positions) || (scores & 3u) ||
-        !tokens_ok(count) || !count_ok(heads) || !count_ok(kv_heads) || !count_ok(width) || width > 256 ||
+        !tokens_ok(count) || !count_ok(heads) || !count_ok(kv_heads) || !count_ok(width) || width > 512 ||
         !count_ok(max_length) || heads % kv_heads || kv_heads > (size_t)INT_MAX / width ||
         q_stride < heads * width || q_stride > (size_t)INT_MAX || (max_length > 8192 && !scores) ||
         heads > (size_t)INT_MAX / max_length || window > (size_t)INT_MAX)

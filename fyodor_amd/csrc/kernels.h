@@ -124,8 +124,8 @@ hipError_t launch_read_shaped(const uint4 *src, size_t count, unsigned *sink, in
 // positions[i] (q rotated in place, k rotated into its slot of `keys`, v
 // copied into `values`, both [capacity][kv_heads * width]); the Gemma form
 // (per-head RMS norms of q, k and v, then the half-split rotation of q and
-// k; width <= 256; k null: q only); causal attention of each token's
-// `heads` query heads (width <= 256) over positions [0, positions[i]], the
+// k; width <= 512; k null: q only); causal attention of each token's
+// `heads` query heads (width <= 512) over positions [0, positions[i]], the
 // last `window` of them when window > 0 (scores: count x heads x max_length
 // scratch, used past 8192 positions); out = silu(gate) * up or
 // gelu(gate) * up; logits x = cap tanh(x / cap).

@@ -223,11 +223,11 @@ __global__ __launch_bounds__(1024) void post_norm(float *__restrict__ x, const f
     }
 }
 
-constexpr int kHeadWidthMax = 256;   // head width limit of head_norm_rope (one element per thread)
+constexpr int kHeadWidthMax = 512;   // head width limit of head_norm_rope (two elements per thread)
 
 // The query and key steps of the engine's Gemma attention
 // (backend/core/llm_cpu.c:487-500): workgroup (head, token i) takes one head
-// of width <= 256, one element per thread. Heads [0, heads) are q heads (q
+// of width <= 512, elements j and j + 256 in thread j. Heads [0, heads) are q heads (q
 // + i q_stride, normalized in place with q_norm, then rotated); with k,
 // heads [heads, heads + kv_heads) are k heads (normalized with k_norm,
 // rotated, into the key cache slot of positions[i]) and the next kv_heads
@@ -257,15 +257,20 @@ __global__ __launch_bounds__(256) void head_norm_rope(float *__restrict__ q, int
     float *dst = kind == 0 ? q + (size_t)blockIdx.y * q_stride + (size_t)hh * width
                : kind == 1 ? keys + slot : values + slot;
     const float *g = kind == 0 ? q_norm : kind == 1 ? k_norm : nullptr;
-    const float x = j < width ? src[j] : 0.f;
-    const float scale = (float)(1.0 / sqrt(group_sum<4>((double)x * x, part) / (double)width + (double)eps));
-    const float y = x * scale * (g && j < width ? g[j] : 1.0f);
+    const int j1 = j + 256;
+    const float x0 = j < width ? src[j] : 0.f, x1 = j1 < width ? src[j1] : 0.f;
+    const double sq = (double)x0 * x0 + (double)x1 * x1;
+    const float scale = (float)(1.0 / sqrt(group_sum<4>(sq, part) / (double)width + (double)eps));
+    const float y0 = x0 * scale * (g && j < width ? g[j] : 1.0f);
+    const float y1 = x1 * scale * (g && j1 < width ? g[j1] : 1.0f);
     if (kind == 2) {
-        if (j < width) dst[j] = y;
+        if (j < width) dst[j] = y0;
+        if (j1 < width) dst[j1] = y1;
         return;
     }
     // q in place: every element was read before group_sum's barriers.
-    if (j < width) row[j] = y;
+    if (j < width) row[j] = y0;
+    if (j1 < width) row[j1] = y1;
     __syncthreads();
     if (j < half) {
         const float angle = (float)position * freq[j];
@@ -336,7 +341,7 @@ __device__ __forceinline__ float block_reduce(float v, float *red, bool maximum)
 }
 
 constexpr int kLdsScores = 8192;   // scores kept in LDS up to this length
-constexpr int kMaxWidth = 256;     // head width limit of the attention kernels
+constexpr int kMaxWidth = 512;     // head width limit of the attention kernels
 
 // The cached positions [first, first + length) that a token at position p
 // attends: [0, p] clamped to max_length, and with a local window of
@@ -376,7 +381,7 @@ __device__ __forceinline__ AttentionRow attention_row(const int *positions, int 
     return a;
 }
 
-// Head width W (64, 128 or 256; q, keys, values and out 16-byte aligned):
+// Head width W (64, 128, 256 or 512; q, keys, values and out 16-byte aligned):
 // scores q.k_t * scale for t < length, a softmax over them,
 // out = sum_t p_t v_t (backend/core/llm_cpu.c:491-511). Scores: 16 lanes per
 // key row, lane l16 holding float4 columns l16 + 16 c of q and of the row;
@@ -392,7 +397,7 @@ __global__ __launch_bounds__(256) void attention_w(const float *__restrict__ q, 
     int window, float scale)
 {
     constexpr int C = W / 64;            // float4 per lane per row
-    constexpr int U = W <= 128 ? 8 : 4;  // rows per 16 lanes in flight
+    constexpr int U = W <= 128 ? 8 : W <= 256 ? 4 : 2;  // rows per 16 lanes in flight
     constexpr int G = 1024 / W;          // output groups of t (W / 4 float4 columns each)
     constexpr int VU = 8;                // V rows per thread in flight
     __shared__ float lds_scores[LDS ? kLdsScores : 1];
@@ -490,8 +495,9 @@ __global__ __launch_bounds__(256) void attention_w(const float *__restrict__ q, 
 
 // The same for any even width up to kMaxWidth and any 4-byte alignment.
 // Scores: 16 lanes per key row (lanes striding the width), reduced across
-// the 16. Output: 256 / width groups of threads each sum a strided share of
-// t per element, then the groups add up.
+// the 16. Output: up to width 256, 256 / width groups of threads each sum a
+// strided share of t per element, then the groups add up; wider, one thread
+// per element and every t.
 template <bool LDS>
 __global__ __launch_bounds__(256) void attention(const float *__restrict__ q, int q_stride,
     const float *__restrict__ keys, const float *__restrict__ values, float *__restrict__ out,
@@ -539,6 +545,16 @@ __global__ __launch_bounds__(256) void attention(const float *__restrict__ q, in
     sum = block_reduce(sum, red, false);
     for (int t = tid; t < length; t += 256) sc[t] = sc[t] / sum;
     __syncthreads();
+    if (width > 256) {
+        // Wider heads: thread j sums columns j, j + 256 over every t in order.
+        const float *vb = values + (size_t)a.kvh * width;
+        for (int j = tid; j < width; j += 256) {
+            float acc = 0.f;
+            for (int t = 0; t < length; ++t) acc += sc[t] * vb[(size_t)t * kvdim + j];
+            out[a.out + j] = acc;
+        }
+        return;
+    }
     const int groups = 256 / width, g = tid / width, j = tid % width;
     if (g < groups) {
         const float *vb = values + (size_t)a.kvh * width + j;
@@ -1078,6 +1094,9 @@ hipError_t launch_attention(const float *q, int q_stride, const float *keys, con
                                window, scale, s);
     else if (aligned && width == 256)
         launch_attention_w<256>(q, q_stride, keys, values, out, scores, positions, count, heads, kv_heads, max_length,
+                                window, scale, s);
+    else if (aligned && width == 512)
+        launch_attention_w<512>(q, q_stride, keys, values, out, scores, positions, count, heads, kv_heads, max_length,
                                 window, scale, s);
     else if (max_length <= kLdsScores)
         hipLaunchKernelGGL(attention<true>, grid, dim3(256), 0, s, q, q_stride, keys, values, out, scores, positions,

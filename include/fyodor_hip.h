@@ -190,7 +190,7 @@ NYA_HIP_EXPORT int nya_hip_post_norm(uintptr_t x, uintptr_t residual, uintptr_t 
     uintptr_t weight, uintptr_t out, size_t n, size_t count, float epsilon, uintptr_t stream);
 
 /* The Gemma form of nya_hip_rope_qkv (backend/core/llm_cpu.c:487-500): each
- * head of width <= 256 is RMS-normalized on its own (q heads with q_norm,
+ * head of width <= 512 is RMS-normalized on its own (q heads with q_norm,
  * k heads with k_norm, v heads without a weight; :360-363), then q and k
  * heads have their halves rotated, the pair (j, j + width / 2) by
  * p * frequencies[j] (:345-358): q in place, k into the key cache slot of
@@ -222,7 +222,7 @@ NYA_HIP_EXPORT int nya_hip_rope_qkv(uintptr_t q, size_t q_stride, uintptr_t k, s
     uintptr_t positions, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream);
 
 /* Causal attention of each token (its q at q + i q_stride): for each of
- * `heads` heads (grouped onto kv_heads key/value heads, width at most 256),
+ * `heads` heads (grouped onto kv_heads key/value heads, width at most 512),
  * scores q.k_t * scale over the cached positions t = 0 .. positions[i]
  * (at most max_length) of keys / values ([max_length][kv_heads * width]
  * rows), a softmax, and out[i] = sum_t p_t v_t (backend/core/llm_cpu.c:491-511).

@@ -596,12 +596,12 @@ API int nya_hip_head_norm_rope(uintptr_t q, size_t q_stride, uintptr_t k, size_t
     float eps, uintptr_t freq, uintptr_t positions, size_t capacity, uintptr_t keys, uintptr_t values,
     uintptr_t stream)
 {
-    if (!q || !q_norm || !freq || !positions || !count || !heads || !kv_heads || !width || width % 2 || width > 256 ||
+    if (!q || !q_norm || !freq || !positions || !count || !heads || !kv_heads || !width || width % 2 || width > 512 ||
         !capacity || !stream || (k && (!v || !k_norm || !keys || !values)))
         return 1;
     if (injected_fault()) return -1;
     const size_t kvd = kv_heads * width, half = width / 2;
-    float row[256];
+    float row[512];
     for (size_t t = 0; t < count; ++t) {
         const int position = ((const int *)positions)[t];
         if (position < 0 || (size_t)position >= capacity) continue;

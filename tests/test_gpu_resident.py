@@ -229,6 +229,8 @@ def test_interleaved_gate_up_on_gpu(session_lib, rocm_env, tmp_path):
 GEMMA_GPU = {
     "widths-128-256": dict(embedding=512, heads=8, kv_heads=4, width=256, local_width=128, hidden=1024,
                            window=16),
+    "widths-256-512": dict(embedding=512, heads=4, kv_heads=2, width=512, local_width=256, hidden=1024,
+                           window=20),
     "width-80-q8": dict(embedding=512, heads=8, kv_heads=2, width=128, local_width=80, hidden=1536, window=24,
                         types={"embedding": F16, "output": Q8_0, "attention": Q8_0, "gate_up": Q4_0, "down": Q8_0}),
     "untied-plain": dict(embedding=768, heads=8, kv_heads=2, width=128, local_width=64, hidden=2048, window=12,

@@ -258,6 +258,7 @@ def attention_ref(q, keys, values, heads, kv_heads, width, length, scale, window
     (32, 4, 64, 64, 64, 0), (8, 2, 128, 300, 5, 0), (6, 2, 80, 40, 7, 0), (4, 2, 128, 8300, 3, 0),
     (8, 2, 128, 1000, 1, 64), (4, 1, 256, 513, 3, 100), (6, 2, 80, 129, 7, 20), (8, 4, 64, 40, 12, 32),
     (8, 2, 128, 9000, 2, 4096), (8, 2, 128, 30, 4, 512),
+    (8, 4, 512, 700, 1, 0), (4, 2, 512, 300, 6, 64), (4, 1, 320, 257, 3, 0), (2, 2, 512, 9000, 1, 1024),
 ])
 def test_attention(env, heads, kv_heads, width, length, count, window):
     """`count` causal queries ending at position length - 1, the query rows
@@ -358,7 +359,7 @@ def test_attention_declines(env):
     dev = Dev(rt)
     try:
         p = dev.empty(4 * 4 * 512)
-        assert L.nya_hip_attention(p, 1024, p, p, p, p, p, 1, 2, 2, 512, 1, 0, 1.0, stream) == 1   # width > 256
+        assert L.nya_hip_attention(p, 2048, p, p, p, p, p, 1, 2, 2, 1024, 1, 0, 1.0, stream) == 1   # width > 512
         assert L.nya_hip_attention(p, 256, p, p, p, 0, p, 1, 2, 2, 128, 9000, 0, 1.0, stream) == 1  # scratch needed
     finally:
         dev.close()
@@ -446,7 +447,8 @@ def rotate_halves(v, c, s):
     return np.concatenate([a * c - b * s, b * c + a * s], -1)
 
 
-@pytest.mark.parametrize("heads,kv_heads,width", [(8, 4, 256), (4, 2, 128), (6, 2, 80), (2, 1, 64)])
+@pytest.mark.parametrize("heads,kv_heads,width", [(8, 4, 256), (4, 2, 128), (6, 2, 80), (2, 1, 64), (4, 2, 512),
+                                                  (2, 1, 320)])
 @pytest.mark.parametrize("form", ["qkv", "key-as-value", "q-only"])
 def test_head_norm_rope(env, heads, kv_heads, width, form):
     """The Gemma q/k/v step: per-head norms (q and k weighted, v without a
@@ -499,8 +501,8 @@ def test_head_norm_rope(env, heads, kv_heads, width, form):
         untouched = np.setdiff1d(np.arange(capacity), touched)
         assert np.array_equal(keys[untouched], keys0[untouched])
         assert np.array_equal(values[untouched], values0[untouched])
-        assert L.nya_hip_head_norm_rope(rd, stride, kp, stride, v_at, stride, count, heads, kv_heads, 258, qn, kn,
-                                        eps, fd, pd, capacity, kd, vd, stream) == 1    # wider than 256
+        assert L.nya_hip_head_norm_rope(rd, stride, kp, stride, v_at, stride, count, heads, kv_heads, 514, qn, kn,
+                                        eps, fd, pd, capacity, kd, vd, stream) == 1    # wider than 512
     finally:
         dev.close()
 

@@ -39,7 +39,8 @@ weight matrix; weights and activations are resident in HBM before timing.
   token time) and TinyLlama 1.1B (tg128 and pp512, the reference's published
   end-to-end metrics); on the 8B-class model also batched verification of
   k draft tokens (one nya_compute_plan_verify) against k decode steps, and
-  tg_at_4096 (a 4096-token prefill, then decode past it); `attention` times
+  tg_at_4096 (a 4096-token prefill, then decode past it); a 12B-class Gemma
+  layout through the Gemma branch (tg and tg_at_4096); `attention` times
   one token's attention of the 8B heads per launch, one workgroup per head
   against the split over positions, by cached length.
 - --sweep prints one line per configuration instead: the decode, small-N and
@@ -531,16 +532,27 @@ def prefill(rt, kern, stream, settle, weights, steps: int, m: int = PREFILL_TOKE
 
 
 # Resident plan workloads: dense LLaMAs with a Q4_K_M-like type mix (Q4_K
-# attention, gate and up; Q6_K down and output; Q4_K embedding).
+# attention, gate and up; Q6_K down and output; Q4_K embedding), and a
+# Gemma layout.
 # "llama-8b": embedding 4096, 32 heads of 128 with 8 KV heads, feed-forward
 # 14336, 32 blocks, vocabulary 128256. "tinyllama-1.1b": embedding 2048, 32
 # heads of 64 with 4 KV heads, feed-forward 5632, 22 blocks, vocabulary
 # 32000 — the model of the reference's published end-to-end table
 # (backend/README.md:796-803: tg128 and pp512 tokens/s).
 RESIDENT_TYPES = {"embedding": Q4_K, "output": Q6_K, "attention": Q4_K, "gate_up": Q4_K, "down": Q6_K}
+# The tied Gemma embedding is also the vocabulary matrix: Q6_K, as the
+# output matrices here.
+GEMMA_TYPES = {"embedding": Q6_K, "output": Q6_K, "attention": Q4_K, "gate_up": Q4_K, "down": Q6_K}
 RESIDENT_MODELS = {
     "llama-8b": dict(embedding=4096, heads=32, kv_heads=8, hidden=14336, blocks=32, vocabulary=128256),
     "tinyllama-1.1b": dict(embedding=2048, heads=32, kv_heads=4, hidden=5632, blocks=22, vocabulary=32000),
+    # A 12B-class Gemma layout (Gemma 3 12B's published dimensions: 48
+    # blocks of 16 heads / 8 KV heads of 256, five local 1024-position
+    # windows to one global block, feed-forward 15360, 262144 tokens, tied
+    # output), run through the Gemma branch with a final soft cap.
+    "gemma-12b-class": dict(family="gemma", embedding=3840, heads=16, kv_heads=8, width=256, local_width=256,
+                            hidden=15360, local=(1, 1, 1, 1, 1, 0) * 8, window=1024, vocabulary=262144,
+                            shared_kv_layers=0, global_value=True, output_scales=(), softcap=30.0),
 }
 
 
@@ -559,20 +571,33 @@ def resident(name: str, tg: int, pp: int, blocks: int | None = None, verify=(), 
     is warmed first. HBM figure: weight bytes a decode step reads (every
     block's matrices, the output matrix, one embedding row) over its time."""
     from fyodor_amd import Compute
-    from fyodor_amd.model import LlamaModel, LlamaShape, Plan, llama_tensors
+    from fyodor_amd.model import (GemmaModel, GemmaShape, LlamaModel, LlamaShape, Plan, gemma_tensors,
+                                  llama_tensors)
 
     shape_args = dict(RESIDENT_MODELS[name])
-    if blocks:
-        shape_args["blocks"] = blocks
+    gemma = shape_args.pop("family", "llama") == "gemma"
     context = max(tg, pp) + 8
     if long_tg:
         context = max(context, LONG_CONTEXT + long_tg + 8)
-    shape = LlamaShape(**shape_args, context=context, types=RESIDENT_TYPES, seed=7)
-    model = LlamaModel(shape, llama_tensors(shape, shared_blocks=True))
+    if gemma:
+        if blocks:   # the first blocks, the last of them global
+            shape_args["local"] = tuple(shape_args["local"][:blocks - 1]) + (0,)
+        shape = GemmaShape(**shape_args, context=context, types=GEMMA_TYPES, seed=7)
+        model = GemmaModel(shape, gemma_tensors(shape, shared_blocks=True))
+        kinds = f"{sum(shape.local)} local ({shape.window}-position window) + {shape.blocks - sum(shape.local)} global"
+        out = {"workload": (f"Gemma branch, embedding {shape.embedding}, {shape.heads} heads / {shape.kv_heads} KV of "
+                            f"{shape.width}, feed-forward {shape.hidden} (GELU gate), {shape.blocks} blocks "
+                            f"({kinds}), vocabulary {shape.vocabulary} tied, soft cap {shape.softcap}, Q4_K "
+                            f"attention/gate/up + Q6_K down/embedding")}
+    else:
+        if blocks:
+            shape_args["blocks"] = blocks
+        shape = LlamaShape(**shape_args, context=context, types=RESIDENT_TYPES, seed=7)
+        model = LlamaModel(shape, llama_tensors(shape, shared_blocks=True))
+        out = {"workload": (f"dense LLaMA, embedding {shape.embedding}, {shape.heads} heads / {shape.kv_heads} KV "
+                            f"of {shape.embedding // shape.heads}, feed-forward {shape.hidden}, {shape.blocks} "
+                            f"blocks, vocabulary {shape.vocabulary}, Q4_K attention/gate/up + Q6_K down/output")}
     ids = [(7 * i + 11) % shape.vocabulary for i in range(max(tg, pp))]
-    out = {"workload": (f"dense LLaMA, embedding {shape.embedding}, {shape.heads} heads / {shape.kv_heads} KV of "
-                        f"{shape.embedding // shape.heads}, feed-forward {shape.hidden}, {shape.blocks} blocks, "
-                        f"vocabulary {shape.vocabulary}, Q4_K attention/gate/up + Q6_K down/output")}
     compute = Compute("rocm")
     try:
         t0 = time.perf_counter()
@@ -588,9 +613,11 @@ def resident(name: str, tg: int, pp: int, blocks: int | None = None, verify=(), 
                     plan.token(ids[i], i)
                 wall = time.perf_counter() - start
                 launches = (plan.stats()["kernel_launches"] - before) / tg
+                # Every block's matrices and vectors, the output matrix (the
+                # embedding itself when tied) and one embedding row.
                 embd = next(a for a in model.arrays if a[0] == "token_embd.weight")
                 wbytes = sum(a[3].nbytes for a in model.arrays if a[0] != "token_embd.weight") + \
-                    embd[3].nbytes // shape.vocabulary
+                    embd[3].nbytes // shape.vocabulary + (embd[3].nbytes if gemma and shape.tied_output else 0)
                 gbs = wbytes * tg / wall / 1e9
                 out[f"tg{tg}"] = {"tokens_per_s": round(tg / wall, 2), "us_per_token": round(wall / tg * 1e6, 1),
                                   "weight_bytes_per_token": wbytes, "effective_gbs": round(gbs, 1),
@@ -716,9 +743,9 @@ def attention_leg(heads: int = 32, kv_heads: int = 8, width: int = 128, layers: 
 
 
 def resident_legs(tg: int, pp: int, blocks: int | None, long_tg: int = 36) -> dict:
-    legs = {name: resident(name, tg, 0 if name == "llama-8b" else pp, blocks,
+    legs = {name: resident(name, tg, pp if name == "tinyllama-1.1b" else 0, blocks,
                            VERIFY_TOKENS if name == "llama-8b" else (),
-                           long_tg if name == "llama-8b" else 0) for name in RESIDENT_MODELS}
+                           long_tg if name != "tinyllama-1.1b" else 0) for name in RESIDENT_MODELS}
     legs["attention"] = attention_leg()
     legs["reference_published"] = {
         "tinyllama-1.1b": {"tg128": 205.48, "pp512": 1374.38, "hardware": "RTX 5060 Ti",

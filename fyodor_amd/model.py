@@ -150,6 +150,143 @@ def llama_tensors(shape: LlamaShape, shared_blocks: bool = False) -> list[tuple[
     return out
 
 
+@dataclass
+class GemmaShape:
+    """A Gemma 4 text model as the engine's loader binds it
+    (backend/core/llm_gguf.c:852-990): local (sliding-window) and global
+    layers of their own head widths, the last `shared_kv_layers` layers
+    reading the cache of the last earlier layer of their kind, global
+    layers without a value matrix (the key stands in) unless
+    `global_value`, per-head q/k norms, post norms, optional per-layer
+    output scales, rotary factors for the global layers, the output matrix
+    tied to the embedding unless `tied_output` is false, and a final logit
+    soft cap."""
+    embedding: int = 256
+    heads: int = 4
+    kv_heads: int = 2
+    width: int = 128          # global layers' head width
+    local_width: int = 64     # local layers' head width
+    hidden: int = 512
+    local: tuple = (1, 1, 0, 1, 1, 0)
+    shared_kv_layers: int = 2
+    window: int = 8
+    context: int = 64
+    vocabulary: int = 300
+    types: dict = field(default_factory=lambda: {"embedding": Q6_K, "output": Q6_K, "attention": Q4_K,
+                                                 "gate_up": Q4_K, "down": Q6_K})
+    epsilon: float = 1e-6
+    rope_base: float = 1000000.0
+    local_rope_base: float = 10000.0
+    softcap: float = 30.0
+    global_value: bool = False
+    tied_output: bool = True
+    output_scales: tuple = (None, 0.5, None, 1.25, None, 0.75)
+    seed: int = 3
+
+    @property
+    def blocks(self) -> int:
+        return len(self.local)
+
+    def head_width(self, layer: int) -> int:
+        return self.local_width if self.local[layer] else self.width
+
+    def kv_widths(self) -> list[int]:
+        """Floats per cached position of each layer (its source's for a
+        shared layer)."""
+        return [self.kv_heads * self.head_width(i) for i in range(self.blocks)]
+
+    def shared(self, layer: int) -> bool:
+        return layer >= self.blocks - self.shared_kv_layers
+
+    def kv_source(self, layer: int) -> int:
+        """The layer whose cache `layer` reads: itself, or for a shared layer
+        the last earlier unshared layer of its kind (llm_gguf.c:925-930)."""
+        if not self.shared(layer):
+            return layer
+        first_shared = self.blocks - self.shared_kv_layers
+        return max(i for i in range(first_shared) if self.local[i] == self.local[layer])
+
+
+def gemma_tensors(shape: GemmaShape, shared_blocks: bool = False):
+    """(name, type, dims, bytes) of every tensor of `shape` with the engine's
+    Gemma tensor names. With `shared_blocks`, every block reuses the host
+    arrays of the first block of its kind (local or global) wherever the
+    tensors' shapes agree (a many-block model in the time of two)."""
+    d, h, v = shape.embedding, shape.hidden, shape.vocabulary
+    rng = np.random.default_rng(shape.seed)
+    seed = [shape.seed * 1000]
+
+    def matrix(kind: str, rows: int, cols: int):
+        seed[0] += 1
+        t = shape.types[kind]
+        return t, (cols, rows), synth.weights(t, rows, cols, seed[0])
+
+    def norm(n: int, scale: float = 1.0):
+        w = (scale * (1.0 + 0.1 * rng.standard_normal(n))).astype(np.float32)
+        return F32, (n,), w.view(np.uint8)
+
+    out = [("token_embd.weight", *matrix("embedding", v, d)), ("output_norm.weight", *norm(d))]
+    if not shape.tied_output:
+        out.append(("output.weight", *matrix("output", v, d)))
+    # Rotary factors of the global layers: most near 1, a few large (those
+    # pairs barely turn).
+    factors = (1.0 + rng.random(shape.width // 2)).astype(np.float32)
+    factors[-4:] = 1e6
+    out.append(("rope_freqs.weight", F32, (shape.width // 2,), factors.view(np.uint8)))
+    first_of = {}
+    for b in range(shape.blocks):
+        w = shape.head_width(b)
+        q, kv = shape.heads * w, shape.kv_heads * w
+        blk = f"blk.{b}."
+        kind = (shape.local[b], shape.shared(b), shape.local[b] or shape.global_value)
+        if shared_blocks and kind in first_of:
+            src = first_of[kind]
+            out += [(name.replace(src, blk, 1), t, dims, data) for name, t, dims, data in out
+                    if name.startswith(src) and not name.endswith("layer_output_scale.weight")]
+        else:
+            first_of[kind] = blk
+            # Gemma's attention is unscaled: q/k norm weights near
+            # width^(-1/4) keep the scores near unit variance, as a trained
+            # model's norms do (with weights near 1 the random model's
+            # softmax is so peaked that the engine's two CPU paths already
+            # differ past their inference-test bounds).
+            qk = w ** -0.25
+            out += [(blk + "attn_norm.weight", *norm(d)), (blk + "attn_q.weight", *matrix("attention", q, d)),
+                    (blk + "attn_q_norm.weight", *norm(w, qk))]
+            if not shape.shared(b):
+                out += [(blk + "attn_k.weight", *matrix("attention", kv, d)),
+                        (blk + "attn_k_norm.weight", *norm(w, qk))]
+                if shape.local[b] or shape.global_value:
+                    out.append((blk + "attn_v.weight", *matrix("attention", kv, d)))
+            out += [(blk + "attn_output.weight", *matrix("attention", d, q)),
+                    (blk + "post_attention_norm.weight", *norm(d)), (blk + "ffn_norm.weight", *norm(d)),
+                    (blk + "ffn_gate.weight", *matrix("gate_up", h, d)),
+                    (blk + "ffn_up.weight", *matrix("gate_up", h, d)),
+                    (blk + "ffn_down.weight", *matrix("down", d, h)), (blk + "post_ffw_norm.weight", *norm(d))]
+        scale = shape.output_scales[b] if b < len(shape.output_scales) else None
+        if scale is not None:
+            out.append((blk + "layer_output_scale.weight", F32, (1,), np.array([scale], np.float32).view(np.uint8)))
+    for name, t, dims, data in out:
+        rows = dims[1] if len(dims) > 1 else 1
+        assert data.nbytes == storage_bytes(t, rows, dims[0]), name
+    return out
+
+
+def _tensor_table(arrays):
+    n = len(arrays)
+    table = (Tensor * n)()
+    index = {}
+    for i, (name, t, dims, data) in enumerate(arrays):
+        tt = table[i]
+        tt.name = name.encode()
+        tt.type, tt.dimension_count = t, len(dims)
+        for k, v in enumerate(dims):
+            tt.dimensions[k] = v
+        tt.data, tt.data_size, tt.bound = data.ctypes.data, data.nbytes, 1
+        index[name] = ctypes.pointer(tt)
+    return table, index
+
+
 class LlamaModel:
     """A nya_llm_context for a dense LLaMA over `tensors` (kept referenced)."""
 
@@ -157,16 +294,7 @@ class LlamaModel:
         self.shape = shape
         self.arrays = tensors if tensors is not None else llama_tensors(shape)
         n = len(self.arrays)
-        self.tensors = (Tensor * n)()
-        index = {}
-        for i, (name, t, dims, data) in enumerate(self.arrays):
-            tt = self.tensors[i]
-            tt.name = name.encode()
-            tt.type, tt.dimension_count = t, len(dims)
-            for k, v in enumerate(dims):
-                tt.dimensions[k] = v
-            tt.data, tt.data_size, tt.bound = data.ctypes.data, data.nbytes, 1
-            index[name] = ctypes.pointer(tt)
+        self.tensors, index = _tensor_table(self.arrays)
         d, hd = shape.embedding, shape.embedding // shape.heads
         kvd = shape.kv_heads * hd
         self.layers = (Layer * shape.blocks)()
@@ -195,11 +323,76 @@ class LlamaModel:
     def weight_bytes(self) -> int:
         return sum(a[3].nbytes for a in self.arrays)
 
+    def kv_width(self, layer: int) -> int:
+        return self.shape.kv_heads * (self.shape.embedding // self.shape.heads)
+
+
+class GemmaModel:
+    """A nya_llm_context for a Gemma 4 text model over `tensors` (kept
+    referenced), the fields the engine's loader sets
+    (backend/core/llm_gguf.c:852-990, :1496-1497)."""
+
+    def __init__(self, shape: GemmaShape, tensors=None):
+        self.shape = shape
+        self.arrays = tensors if tensors is not None else gemma_tensors(shape)
+        self.tensors, index = _tensor_table(self.arrays)
+        d = shape.embedding
+        self.layers = (Layer * shape.blocks)()
+        cache_width, offsets = 0, []
+        for b in range(shape.blocks):
+            L = self.layers[b]
+            w = shape.head_width(b)
+            get = lambda name: index.get(f"blk.{b}.{name}.weight")
+            for fld, name in [("attention_norm", "attn_norm"), ("query", "attn_q"), ("key", "attn_k"),
+                              ("value", "attn_v"), ("attention_output", "attn_output"), ("feed_forward_norm", "ffn_norm"),
+                              ("feed_forward_gate", "ffn_gate"), ("feed_forward_down", "ffn_down"),
+                              ("feed_forward_up", "ffn_up"), ("query_norm", "attn_q_norm"),
+                              ("key_norm", "attn_k_norm"), ("attention_post_norm", "post_attention_norm"),
+                              ("ffn_post_norm", "post_ffw_norm"), ("output_scale", "layer_output_scale")]:
+                t = get(name)
+                if t is not None:
+                    setattr(L, fld, t)
+            if not shape.local[b]:
+                L.rope_factors = index["rope_freqs.weight"]
+            L.head_count, L.kv_head_count, L.head_dimension = shape.heads, shape.kv_heads, w
+            L.hidden_length, L.sliding_window = shape.hidden, shape.window if shape.local[b] else 0
+            L.kv_source = shape.kv_source(b)
+            if L.kv_source == b:
+                offsets.append(cache_width)
+                cache_width += shape.kv_heads * w
+            else:
+                offsets.append(offsets[L.kv_source])
+            L.cache_offset = offsets[b]
+        c = self.context = Context()
+        c.tensors, c.tensor_count = self.tensors, len(self.arrays)
+        c.layers = self.layers
+        c.tokenizer.vocabulary_size = shape.vocabulary
+        c.token_embedding, c.output_norm = index["token_embd.weight"], index["output_norm.weight"]
+        c.output = index["output.weight"] if not shape.tied_output else c.token_embedding
+        c.embedding_length, c.feed_forward_length, c.block_count = d, shape.hidden, shape.blocks
+        c.head_count, c.key_value_head_count, c.context_length = shape.heads, shape.kv_heads, shape.context
+        c.rope_dimension_count, c.head_dimension = shape.width, shape.width
+        c.sliding_head_dimension, c.sliding_window = shape.local_width, shape.window
+        c.shared_kv_layers = shape.shared_kv_layers
+        c.norm_epsilon, c.rope_frequency_base = shape.epsilon, shape.rope_base
+        c.sliding_rope_base, c.final_logit_softcap = shape.local_rope_base, shape.softcap
+        c.is_gemma = 1
+        c.cache_width = cache_width
+        c.maximum_query_length = shape.heads * max(shape.width, shape.local_width)
+        c.maximum_hidden_length = shape.hidden
+
+    @property
+    def weight_bytes(self) -> int:
+        return sum(a[3].nbytes for a in self.arrays)
+
+    def kv_width(self, layer: int) -> int:
+        return self.shape.kv_heads * self.shape.head_width(layer)
+
 
 class Plan:
     """A resident plan of `model` on `compute` (nya_compute_plan_create)."""
 
-    def __init__(self, compute: Compute, model: LlamaModel, capacity: int):
+    def __init__(self, compute: Compute, model: LlamaModel | GemmaModel, capacity: int):
         lib = compute._lib
         vp_, sz_ = ctypes.c_void_p, ctypes.c_size_t
         lib.nya_compute_plan_create.restype = vp_
@@ -230,8 +423,7 @@ class Plan:
 
     def read_kv(self, layer: int, position: int, count: int) -> tuple[np.ndarray, np.ndarray]:
         """Keys and values of `count` cached positions of `layer`."""
-        s = self.model.shape
-        n = count * s.kv_heads * (s.embedding // s.heads)
+        n = count * self.model.kv_width(layer)
         k, v = np.empty(n, np.float32), np.empty(n, np.float32)
         fp = ctypes.POINTER(ctypes.c_float)
         self.lib.nya_compute_plan_read_kv.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t,

@@ -18,13 +18,9 @@ vocabulary is three control tokens and numbered pieces.
 from __future__ import annotations
 
 import struct
-from dataclasses import dataclass, field
 from pathlib import Path
 
-import numpy as np
-
-from fyodor_amd import F32, Q4_K, Q6_K, storage_bytes, synth
-from fyodor_amd.model import LlamaShape, llama_tensors
+from fyodor_amd.model import GemmaShape, LlamaShape, gemma_tensors, llama_tensors
 
 # GGUF metadata value types.
 U32, I32, F32_META, BOOL, STRING, ARRAY = 4, 5, 6, 7, 8, 9
@@ -78,105 +74,6 @@ def _file(path: Path, meta: list[bytes], ts) -> int:
             f.write(b"\0" * pad)
             at += pad
     return path.stat().st_size
-
-
-@dataclass
-class GemmaShape:
-    """A small Gemma 4 text model as the engine's loader binds it
-    (backend/core/llm_gguf.c:852-990): local (sliding-window) and global
-    layers of their own head widths, the last `shared_kv_layers` layers
-    reading the cache of the last earlier layer of their kind, global
-    layers without a value matrix (the key stands in) unless
-    `global_value`, per-head q/k norms, post norms, optional per-layer
-    output scales, rotary factors for the global layers, the output matrix
-    tied to the embedding unless `tied_output` is false, and a final logit
-    soft cap."""
-    embedding: int = 256
-    heads: int = 4
-    kv_heads: int = 2
-    width: int = 128          # global layers' head width
-    local_width: int = 64     # local layers' head width
-    hidden: int = 512
-    local: tuple = (1, 1, 0, 1, 1, 0)
-    shared_kv_layers: int = 2
-    window: int = 8
-    context: int = 64
-    vocabulary: int = 300
-    types: dict = field(default_factory=lambda: {"embedding": Q6_K, "output": Q6_K, "attention": Q4_K,
-                                                 "gate_up": Q4_K, "down": Q6_K})
-    epsilon: float = 1e-6
-    rope_base: float = 1000000.0
-    local_rope_base: float = 10000.0
-    softcap: float = 30.0
-    global_value: bool = False
-    tied_output: bool = True
-    output_scales: tuple = (None, 0.5, None, 1.25, None, 0.75)
-    seed: int = 3
-
-    @property
-    def blocks(self) -> int:
-        return len(self.local)
-
-    def head_width(self, layer: int) -> int:
-        return self.local_width if self.local[layer] else self.width
-
-    def kv_widths(self) -> list[int]:
-        """Floats per cached position of each layer (its source's for a
-        shared layer)."""
-        return [self.kv_heads * self.head_width(i) for i in range(self.blocks)]
-
-    def shared(self, layer: int) -> bool:
-        return layer >= self.blocks - self.shared_kv_layers
-
-
-def gemma_tensors(shape: GemmaShape):
-    d, h, v = shape.embedding, shape.hidden, shape.vocabulary
-    rng = np.random.default_rng(shape.seed)
-    seed = [shape.seed * 1000]
-
-    def matrix(kind: str, rows: int, cols: int):
-        seed[0] += 1
-        t = shape.types[kind]
-        return t, (cols, rows), synth.weights(t, rows, cols, seed[0])
-
-    def norm(n: int, scale: float = 1.0):
-        w = (scale * (1.0 + 0.1 * rng.standard_normal(n))).astype(np.float32)
-        return F32, (n,), w.view(np.uint8)
-
-    out = [("token_embd.weight", *matrix("embedding", v, d)), ("output_norm.weight", *norm(d))]
-    if not shape.tied_output:
-        out.append(("output.weight", *matrix("output", v, d)))
-    # Rotary factors of the global layers: most near 1, a few large (those
-    # pairs barely turn).
-    factors = (1.0 + rng.random(shape.width // 2)).astype(np.float32)
-    factors[-4:] = 1e6
-    out.append(("rope_freqs.weight", F32, (shape.width // 2,), factors.view(np.uint8)))
-    for b in range(shape.blocks):
-        w = shape.head_width(b)
-        q, kv = shape.heads * w, shape.kv_heads * w
-        blk = f"blk.{b}."
-        # Gemma's attention is unscaled: q/k norm weights near width^(-1/4)
-        # keep the scores near unit variance, as a trained model's norms do
-        # (with weights near 1 the random model's softmax is so peaked that
-        # the engine's two CPU paths already differ past the bounds).
-        qk = w ** -0.25
-        out += [(blk + "attn_norm.weight", *norm(d)), (blk + "attn_q.weight", *matrix("attention", q, d)),
-                (blk + "attn_q_norm.weight", *norm(w, qk))]
-        if not shape.shared(b):
-            out += [(blk + "attn_k.weight", *matrix("attention", kv, d)), (blk + "attn_k_norm.weight", *norm(w, qk))]
-            if shape.local[b] or shape.global_value:
-                out.append((blk + "attn_v.weight", *matrix("attention", kv, d)))
-        out += [(blk + "attn_output.weight", *matrix("attention", d, q)),
-                (blk + "post_attention_norm.weight", *norm(d)), (blk + "ffn_norm.weight", *norm(d)),
-                (blk + "ffn_gate.weight", *matrix("gate_up", h, d)), (blk + "ffn_up.weight", *matrix("gate_up", h, d)),
-                (blk + "ffn_down.weight", *matrix("down", d, h)), (blk + "post_ffw_norm.weight", *norm(d))]
-        scale = shape.output_scales[b] if b < len(shape.output_scales) else None
-        if scale is not None:
-            out.append((blk + "layer_output_scale.weight", F32, (1,), np.array([scale], np.float32).view(np.uint8)))
-    for name, t, dims, data in out:
-        rows = dims[1] if len(dims) > 1 else 1
-        assert data.nbytes == storage_bytes(t, rows, dims[0]), name
-    return out
 
 
 def write_gemma(path: Path, shape: GemmaShape) -> int:

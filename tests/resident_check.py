@@ -194,13 +194,14 @@ def plan_against_engine(lib, tmp_path: Path, shape, tokens: list[int]) -> dict:
     chunk. Returns the worst scaled logit and KV errors."""
     from fyodor_amd import Compute
     from fyodor_amd import model as fm
-    from gguf_model import write
+    from gguf_model import write, write_gemma
     path = tmp_path / "model.gguf"
-    write(path, shape)
+    gemma = isinstance(shape, fm.GemmaShape)
+    (write_gemma if gemma else write)(path, shape)
     ref_model = Model(lib, path, None)
     ref = Session(ref_model, shape.context)
     compute = Compute("rocm")
-    plan = fm.Plan(compute, fm.LlamaModel(shape), shape.context)
+    plan = fm.Plan(compute, fm.GemmaModel(shape) if gemma else fm.LlamaModel(shape), shape.context)
     worst = {"logit": 0.0, "kv": 0.0}
     try:
         for i, t in enumerate(tokens):
@@ -211,9 +212,8 @@ def plan_against_engine(lib, tmp_path: Path, shape, tokens: list[int]) -> dict:
         assert ref.run(chunk, False) == 0
         got = plan.prefill(chunk, len(tokens))
         worst["logit"] = max(worst["logit"], check_logits(ref.logits(shape.vocabulary), got, "prefill chunk"))
-        width = shape.kv_heads * (shape.embedding // shape.heads)
         n = len(tokens) + len(chunk)
-        for layer in range(shape.blocks):
+        for layer, width in enumerate(kv_widths(shape)):
             for a, b in zip(ref.kv(layer, 0, n, width), plan.read_kv(layer, 0, n)):
                 scaled = np.abs(b.astype(np.float64) - a) / (1 + np.abs(a.astype(np.float64)))
                 assert scaled.max() <= KV_BOUND, f"layer {layer}: KV scaled error {scaled.max():.3g}"

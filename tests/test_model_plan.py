@@ -75,6 +75,48 @@ def test_python_model_plan_matches_engine_session(dropin_library, mock_rocm, tmp
     plan_against_engine(bind(dropin_library), tmp_path, shape, TOKENS)
 
 
+def test_gemma_context_matches_the_loader(dropin_library, tmp_path):
+    """fyodor_amd.model's Gemma description equals what the engine's loader
+    makes of the same model written as GGUF (backend/core/llm_gguf.c:852-990):
+    the model fields, and per layer the head shape, window, KV source and
+    cache offset, and which tensors are bound."""
+    from gguf_model import write_gemma
+    from resident_check import Model
+    lib = bind(dropin_library)
+    for shape in (fm.GemmaShape(), fm.GemmaShape(local=(1, 0, 1, 0), shared_kv_layers=0, global_value=True,
+                                                  tied_output=False, output_scales=(), softcap=0.0)):
+        path = tmp_path / "gemma.gguf"
+        write_gemma(path, shape)
+        loaded = Model(lib, path, None)
+        try:
+            want = fm.Context.from_address(loaded.ptr.value)
+            got = fm.GemmaModel(shape).context
+            for f in ("embedding_length", "block_count", "is_gemma", "is_assistant", "cache_width", "sliding_window",
+                      "final_logit_softcap", "sliding_rope_base", "rope_frequency_base", "norm_epsilon",
+                      "expert_count", "per_layer_embedding_length"):
+                assert getattr(got, f) == getattr(want, f), f
+            assert bool(got.output) and (got.output.contents.name == want.output.contents.name)
+            for b in range(shape.blocks):
+                g, w = got.layers[b], want.layers[b]
+                for f in ("head_count", "kv_head_count", "head_dimension", "hidden_length", "sliding_window",
+                          "kv_source", "cache_offset"):
+                    assert getattr(g, f) == getattr(w, f), (b, f)
+                for f, _ in fm.Layer._fields_:
+                    if f in ("head_count", "kv_head_count", "head_dimension", "hidden_length", "expert_hidden_length",
+                             "sliding_window", "kv_source", "cache_offset"):
+                        continue
+                    a, c = getattr(g, f), getattr(w, f)
+                    assert bool(a) == bool(c), (b, f)
+                    if a:
+                        assert a.contents.name == c.contents.name, (b, f)
+        finally:
+            loaded.close()
+
+
+def test_python_gemma_plan_matches_engine_session(dropin_library, mock_rocm, tmp_path):
+    plan_against_engine(bind(dropin_library), tmp_path, fm.GemmaShape(context=32), TOKENS)
+
+
 def test_plan_rejects_out_of_range_calls(mock_rocm):
     shape = fm.LlamaShape(context=8)
     compute = Compute("rocm")

@@ -276,6 +276,17 @@ NYA_HIP_EXPORT int nya_hip_matvec_swiglu(uintptr_t w, unsigned type, size_t rows
                                        (int)cols, (hipStream_t)stream));
 }
 
+NYA_HIP_EXPORT int nya_hip_matvec_geglu(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
+    uintptr_t hidden, uintptr_t stream)
+{
+    size_t b;
+    if (!storage_bytes(type, rows, cols, &b) || !matvec_swiglu_supported(type, (int)rows, (int)cols)) return 1;
+    if (!w) return 0;   // the shape query
+    if (!x || !hidden || (w & 15u) || (x & 15u) || (hidden & 3u)) return 1;
+    return status(launch_matvec_geglu(type, (const uint8_t *)w, (const float *)x, (float *)hidden, (int)rows,
+                                      (int)cols, (hipStream_t)stream));
+}
+
 NYA_HIP_EXPORT int nya_hip_matvec_residual(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
     uintptr_t res, uintptr_t norm, uintptr_t hn, uintptr_t parts, uintptr_t stream)
 {
@@ -516,12 +527,23 @@ NYA_HIP_EXPORT int nya_hip_greedy(uintptr_t logits, size_t n, size_t count, uint
                                 (hipStream_t)stream));
 }
 
+static bool pairs_ok(uintptr_t gu, uintptr_t out, size_t n, size_t count)
+{
+    if (!vec(gu) || !vec(out) || !count_ok(n) || n % 16 || n > (size_t)INT_MAX / 2 || !tokens_ok(count)) return false;
+    const uintptr_t in_end = gu + 8 * n * count, out_end = out + 4 * n * count;
+    return !(gu < out_end && out < in_end);   // not overlapping
+}
+
 NYA_HIP_EXPORT int nya_hip_silu_pairs(uintptr_t gu, uintptr_t out, size_t n, size_t count, uintptr_t stream)
 {
-    if (!vec(gu) || !vec(out) || !count_ok(n) || n % 16 || n > (size_t)INT_MAX / 2 || !tokens_ok(count)) return 1;
-    const uintptr_t in_end = gu + 8 * n * count, out_end = out + 4 * n * count;
-    if (gu < out_end && out < in_end) return 1;   // overlapping
+    if (!pairs_ok(gu, out, n, count)) return 1;
     return status(launch_silu_pairs((const float *)gu, (float *)out, (int)n, (int)count, (hipStream_t)stream));
+}
+
+NYA_HIP_EXPORT int nya_hip_gelu_pairs(uintptr_t gu, uintptr_t out, size_t n, size_t count, uintptr_t stream)
+{
+    if (!pairs_ok(gu, out, n, count)) return 1;
+    return status(launch_gelu_pairs((const float *)gu, (float *)out, (int)n, (int)count, (hipStream_t)stream));
 }
 
 // The checks of the gated activations: one token may be rewritten in place

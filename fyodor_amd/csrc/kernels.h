@@ -58,6 +58,9 @@ hipError_t launch_matvec_scaled_rope(unsigned type, const uint8_t *w, const floa
 bool matvec_swiglu_supported(unsigned type, int rows, int cols);
 hipError_t launch_matvec_swiglu(unsigned type, const uint8_t *w, const float *x, float *hidden, int rows, int cols,
     hipStream_t stream);
+// The same with Gemma's GELU gate (the shapes of matvec_swiglu_supported).
+hipError_t launch_matvec_geglu(unsigned type, const uint8_t *w, const float *x, float *hidden, int rows, int cols,
+    hipStream_t stream);
 // The same of h * g with the norm's scale on the row sums, from the
 // partial sums of squares of launch_matvec_residual.
 bool matvec_swiglu_scaled_supported(unsigned type, int rows, int cols);
@@ -159,6 +162,7 @@ hipError_t launch_silu_mul(const float *gate, int gate_stride, const float *up, 
 hipError_t launch_gelu_mul(const float *gate, int gate_stride, const float *up, int up_stride, float *out, int n,
     int count, hipStream_t stream);
 hipError_t launch_silu_pairs(const float *gu, float *out, int n, int count, hipStream_t stream);
+hipError_t launch_gelu_pairs(const float *gu, float *out, int n, int count, hipStream_t stream);
 // The greedy choice of each of `count` rows of n logits (first largest among
 // the entries not masked; 0xFFFFFFFF for a row with a NaN or +inf, or
 // without a finite candidate).

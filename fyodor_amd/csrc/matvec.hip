@@ -448,10 +448,20 @@ __device__ __forceinline__ float4 gated_silu(float4 g, float4 u)
 {
     return make_float4(gated_silu(g.x, u.x), gated_silu(g.y, u.y), gated_silu(g.z, u.z), gated_silu(g.w, u.w));
 }
+// Gemma's gate, GELU with the tanh approximation (backend/core/llm_cpu.c:
+// 329-341), in the resident step's operation order, uncontracted.
+__device__ __forceinline__ float gated_gelu(float g, float u)
+{
+#pragma clang fp contract(off)
+    return 0.5f * g * (1.0f + tanhf(0.7978845608028654f * (g + 0.044715f * g * g * g))) * u;
+}
 
-// SWIGLU: the rows come in 16-row blocks of gate rows and up rows (tile t
-// holds gate rows 16t .. 16t + 15 as its rows 0..15, their up rows as 16..31)
-// and y receives silu(gate) * up, 16 values per tile at 16 t.
+// The gated activations of the interleaved gate|up products.
+enum : int { kGateNone = 0, kGateSilu = 1, kGateGelu = 2 };
+
+// GATE (SiLU or GELU): the rows come in 16-row blocks of gate rows and up
+// rows (tile t holds gate rows 16t .. 16t + 15 as its rows 0..15, their up
+// rows as 16..31) and y receives act(gate) * up, 16 values per tile at 16 t.
 // SCALED: x is h * g of the decoder's residual h and norm weight g, and the
 // row sums are multiplied by the norm's scale 1 / sqrt(sum h^2 / cols + eps)
 // (W xn = scale W (h g)), the sum of squares from the kNormParts partial
@@ -461,7 +471,7 @@ __device__ __forceinline__ float4 gated_silu(float4 g, float4 u)
 // final barrier. (Normalizing x in every workgroup instead, with the norm
 // step's reduction before the quantization, measured 16.0 us at
 // 28672 x 4096 against 15.3 us for the norm step followed by the product.)
-template <int KS, int RING, bool SWIGLU = false, bool SCALED = false>
+template <int KS, int RING, int GATE = kGateNone, bool SCALED = false>
 __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) void matvec_q4k(
     const uint8_t *__restrict__ w, const float *__restrict__ x, float *__restrict__ y, int rows, int cols, int g0c,
     int ngc, int accumulate, NormIn nm)
@@ -564,10 +574,10 @@ __global__ __launch_bounds__(64 * KS) __attribute__((amdgpu_waves_per_eu(2))) vo
         for (int q = 1; q < kNormParts / 64; ++q) total += part[q];
         v *= (float)(1.0 / sqrt(total / (double)cols + (double)nm.eps));
     }
-    if constexpr (SWIGLU) {
+    if constexpr (GATE != kGateNone) {
         // Every tile is whole (R = 32): lane l < 16 takes its up row from l + 16.
         const float up = __shfl_down(v, 16, 32);
-        if (lane < 16) y[16 * t + lane] = gated_silu(v, up);
+        if (lane < 16) y[16 * t + lane] = GATE == kGateGelu ? gated_gelu(v, up) : gated_silu(v, up);
         return;
     }
     float *dst = y + kTileRows * t + lane;
@@ -1843,7 +1853,17 @@ hipError_t launch_matvec_swiglu(unsigned type, const uint8_t *w, const float *x,
 {
     if (!matvec_swiglu_supported(type, rows, cols)) return hipErrorInvalidValue;
     const int groups = cols / kGroupCols;
-    hipLaunchKernelGGL((matvec_q4k<8, 2, true>), dim3((unsigned)(rows / kTileRows)), dim3(512),
+    hipLaunchKernelGGL((matvec_q4k<8, 2, kGateSilu>), dim3((unsigned)(rows / kTileRows)), dim3(512),
+                       matvec_lds(groups * kGroupCols), s, w, x, hidden, rows, cols, 0, groups, 0, NormIn{});
+    return hipGetLastError();
+}
+
+hipError_t launch_matvec_geglu(unsigned type, const uint8_t *w, const float *x, float *hidden, int rows, int cols,
+    hipStream_t s)
+{
+    if (!matvec_swiglu_supported(type, rows, cols)) return hipErrorInvalidValue;
+    const int groups = cols / kGroupCols;
+    hipLaunchKernelGGL((matvec_q4k<8, 2, kGateGelu>), dim3((unsigned)(rows / kTileRows)), dim3(512),
                        matvec_lds(groups * kGroupCols), s, w, x, hidden, rows, cols, 0, groups, 0, NormIn{});
     return hipGetLastError();
 }
@@ -1861,7 +1881,7 @@ hipError_t launch_matvec_swiglu_scaled(unsigned type, const uint8_t *w, const fl
     nm.eps = eps;
     nm.parts = parts;
     const int groups = cols / kGroupCols;
-    hipLaunchKernelGGL((matvec_q4k<8, 2, true, true>), dim3((unsigned)(rows / kTileRows)), dim3(512),
+    hipLaunchKernelGGL((matvec_q4k<8, 2, kGateSilu, true>), dim3((unsigned)(rows / kTileRows)), dim3(512),
                        matvec_lds(groups * kGroupCols), s, w, hn, hidden, rows, cols, 0, groups, 0, nm);
     return hipGetLastError();
 }

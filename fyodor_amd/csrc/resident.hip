@@ -187,22 +187,23 @@ __global__ __launch_bounds__(1024) void post_norm(float *__restrict__ x, const f
     x += row;
     out += row;
     if (r) r += row;
-    float v[K], u[K];
-    double s = 0.0;
+    // Every input loaded before the first use: one memory round trip.
+    float v[K], u[K], pw[K], g[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
         const int i = t + 1024 * k;
         v[k] = i < n ? x[i] : 0.f;
         u[k] = i < n && r ? r[i] : 0.f;
-        s += (double)u[k] * u[k];
+        pw[k] = i < n && post ? post[i] : 1.f;
+        g[k] = i < n && w ? w[i] : 1.f;
     }
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < K; ++k) s += (double)u[k] * u[k];
     if (r && post) {
         const float sr = (float)(1.0 / sqrt(group_sum<16>(s, part) / (double)n + (double)eps));
 #pragma unroll
-        for (int k = 0; k < K; ++k) {
-            const int i = t + 1024 * k;
-            if (i < n) u[k] = u[k] * sr * post[i];
-        }
+        for (int k = 0; k < K; ++k) u[k] = u[k] * sr * pw[k];
     }
     s = 0.0;
 #pragma unroll
@@ -219,7 +220,7 @@ __global__ __launch_bounds__(1024) void post_norm(float *__restrict__ x, const f
 #pragma unroll
     for (int k = 0; k < K; ++k) {
         const int i = t + 1024 * k;
-        if (i < n) out[i] = v[k] * sx * (w ? w[i] : 1.0f);
+        if (i < n) out[i] = v[k] * sx * g[k];
     }
 }
 
@@ -895,13 +896,14 @@ __global__ __launch_bounds__(256) void silu_mul4(const float4 *gate, int gate_st
 // The same over rows that hold gate and up in 16-element blocks (row i of
 // 2n values at gu + 2 n i: gate element j at 32 (j / 16) + j % 16, up
 // element j 16 further), out rows of n.
+template <bool GELU>
 __global__ __launch_bounds__(256) void silu_pairs(const float *__restrict__ gu, float *__restrict__ out, int n)
 {
     const float *row = gu + (size_t)blockIdx.y * 2 * n;
     float *o = out + (size_t)blockIdx.y * n;
     for (int j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256) {
         const int at = 32 * (j >> 4) + (j & 15);
-        o[j] = silu_times(row[at], row[at + 16]);
+        o[j] = gated<GELU>(row[at], row[at + 16]);
     }
 }
 
@@ -1141,7 +1143,13 @@ hipError_t launch_greedy(const float *logits, int n, int count, const uint32_t *
 
 hipError_t launch_silu_pairs(const float *gu, float *out, int n, int count, hipStream_t s)
 {
-    hipLaunchKernelGGL(silu_pairs, dim3(grid_of(n), (unsigned)count), dim3(256), 0, s, gu, out, n);
+    hipLaunchKernelGGL(silu_pairs<false>, dim3(grid_of(n), (unsigned)count), dim3(256), 0, s, gu, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_gelu_pairs(const float *gu, float *out, int n, int count, hipStream_t s)
+{
+    hipLaunchKernelGGL(silu_pairs<true>, dim3(grid_of(n), (unsigned)count), dim3(256), 0, s, gu, out, n);
     return hipGetLastError();
 }
 

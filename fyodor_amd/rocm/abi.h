@@ -94,6 +94,10 @@ typedef struct nya_resident_ops {
         uintptr_t, uintptr_t, float, uintptr_t, uintptr_t, size_t, uintptr_t, uintptr_t, uintptr_t);
     int (*gelu_mul)(uintptr_t, size_t, uintptr_t, size_t, uintptr_t, size_t, size_t, uintptr_t);
     int (*softcap)(uintptr_t, size_t, float, uintptr_t);
+    /* Optional as a pair (with the Gemma set): NULL keeps Gemma's gate and
+     * up in two blocks of rows and its GELU gate a step of its own. */
+    int (*matvec_geglu)(uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t, uintptr_t);
+    int (*gelu_pairs)(uintptr_t, uintptr_t, size_t, size_t, uintptr_t);
 } nya_resident_ops;
 
 #define NYA_KERNEL_ABI 2U

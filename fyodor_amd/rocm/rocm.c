@@ -394,6 +394,12 @@ static int bind_all(session *s)
     if (!has_gemma)
         s->resident.post_norm = NULL, s->resident.head_norm_rope = NULL, s->resident.gelu_mul = NULL,
         s->resident.softcap = NULL;
+    if (!has_gemma ||
+        nya_vendor_symbol(s->kernel_module, "nya_hip_matvec_geglu", &s->resident.matvec_geglu,
+                          sizeof s->resident.matvec_geglu) ||
+        nya_vendor_symbol(s->kernel_module, "nya_hip_gelu_pairs", &s->resident.gelu_pairs,
+                          sizeof s->resident.gelu_pairs))
+        s->resident.matvec_geglu = NULL, s->resident.gelu_pairs = NULL;
     const struct { const char *symbol; void *slot; size_t size; } graphs[] = {
         {"hipStreamBeginCapture", &s->graphs.begin_capture, sizeof s->graphs.begin_capture},
         {"hipStreamEndCapture", &s->graphs.end_capture, sizeof s->graphs.end_capture},

@@ -363,6 +363,15 @@ NYA_HIP_EXPORT int nya_hip_matvec_residual(uintptr_t w, unsigned type, size_t ro
 NYA_HIP_EXPORT int nya_hip_matvec_swiglu_scaled(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t hn,
     uintptr_t parts, float eps, uintptr_t hidden, uintptr_t stream);
 
+/* No counterpart in the reference: nya_hip_matvec_swiglu with Gemma's GELU
+ * gate (backend/core/llm_cpu.c:329-341) in place of SiLU:
+ * hidden[j] = 0.5 g (1 + tanh(0.7978845608028654 (g + 0.044715 g^3))) u,
+ * as nya_hip_gelu_pairs forms it, bit for bit with nya_hip_matmul of one
+ * column followed by nya_hip_gelu_pairs. The shapes and the shape query of
+ * nya_hip_matvec_swiglu. */
+NYA_HIP_EXPORT int nya_hip_matvec_geglu(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
+    uintptr_t hidden, uintptr_t stream);
+
 /* out[i][j] = silu(g) * u for row i of gu (count rows of 2 n floats holding
  * gate and up values in 16-element blocks: g = gu[i][32 (j / 16) + j % 16],
  * u 16 further), out rows of n (n a multiple of 16; out must not overlap gu);
@@ -370,6 +379,11 @@ NYA_HIP_EXPORT int nya_hip_matvec_swiglu_scaled(uintptr_t w, unsigned type, size
  * feed-forward step of the gate|up layout of nya_hip_matvec_swiglu for runs
  * of several tokens. */
 NYA_HIP_EXPORT int nya_hip_silu_pairs(uintptr_t gu, uintptr_t out, size_t n, size_t count, uintptr_t stream);
+
+/* The same with Gemma's GELU gate as nya_hip_gelu_mul forms it: the
+ * feed-forward step of nya_hip_matvec_geglu's layout for runs of several
+ * tokens. */
+NYA_HIP_EXPORT int nya_hip_gelu_pairs(uintptr_t gu, uintptr_t out, size_t n, size_t count, uintptr_t stream);
 
 /* No counterpart in the reference: the decoder's gated SiLU step (as
  * nya_hip_silu_mul computes it, backend/core/llm_cpu.c:336-341) folded into

@@ -266,6 +266,38 @@ API int nya_hip_matvec_swiglu(uintptr_t w, unsigned type, size_t rows, size_t co
     return rc;
 }
 
+/* The same with Gemma's GELU gate. */
+API int nya_hip_matvec_geglu(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x, uintptr_t hidden,
+    uintptr_t stream)
+{
+    if (nya_hip_matvec_swiglu(0, type, rows, cols, 0, 0, stream)) return 1;
+    if (!w) return 0;
+    if (!x || !hidden) return 1;
+    float *y = malloc(rows * sizeof(float));
+    if (!y) return -2;
+    int rc = nya_hip_matmul(w, type, rows, cols, x, (uintptr_t)y, 1, 0, 0, stream);
+    for (size_t j = 0; !rc && j < rows / 2; ++j) {
+        const float g = y[32 * (j / 16) + j % 16], u = y[32 * (j / 16) + 16 + j % 16];
+        ((float *)hidden)[j] = 0.5f * g * (1.0f + tanhf(0.7978845608028654f * (g + 0.044715f * g * g * g))) * u;
+    }
+    free(y);
+    return rc;
+}
+
+API int nya_hip_gelu_pairs(uintptr_t gu, uintptr_t out, size_t n, size_t count, uintptr_t stream)
+{
+    if (!gu || !out || !n || n % 16 || !count || !stream) return 1;
+    if (injected_fault()) return -1;
+    for (size_t t = 0; t < count; ++t)
+        for (size_t j = 0; j < n; ++j) {
+            const float *row = (const float *)gu + 2 * n * t;
+            const float g = row[32 * (j / 16) + j % 16], u = row[32 * (j / 16) + 16 + j % 16];
+            ((float *)out)[t * n + j] =
+                0.5f * g * (1.0f + tanhf(0.7978845608028654f * (g + 0.044715f * g * g * g))) * u;
+        }
+    return 0;
+}
+
 /* One token's product added into the residual, with h * norm and 256 partial
  * sums of squares (rows in 256 runs of ceil(rows / 256), zeros past the last
  * run); the shapes the library takes on 256 CUs. w == 0 queries. */

@@ -62,6 +62,8 @@ def env():
     L.nya_hip_head_norm_rope.argtypes = [_up, _sz, _up, _sz, _up, _sz, _sz, _sz, _sz, _sz, _up, _up, _f, _up, _up,
                                          _sz, _up, _up, _up]
     L.nya_hip_gelu_mul.argtypes = [_up, _sz, _up, _sz, _up, _sz, _sz, _up]
+    L.nya_hip_matvec_geglu.argtypes = [_up, _u, _sz, _sz, _up, _up, _up]
+    L.nya_hip_gelu_pairs.argtypes = [_up, _up, _sz, _sz, _up]
     L.nya_hip_softcap.argtypes = [_up, _sz, _f, _up]
     L.nya_hip_silu_mul.argtypes = [_up, _sz, _up, _sz, _up, _sz, _sz, _up]
     L.nya_hip_matvec_gated.argtypes = [_up, _u, _sz, _sz, _up, _up, _up, _up]
@@ -614,6 +616,37 @@ def test_matvec_swiglu_equals_two_steps(env, rows, cols):
         yv = dev.get(y, np.empty(rows, np.float32)).astype(np.float64).reshape(-1, 2, 16)
         g, u = yv[:, 0, :].reshape(-1), yv[:, 1, :].reshape(-1)
         assert scaled_error(b, g / (1 + np.exp(-g)) * u) <= 2e-6
+    finally:
+        dev.close()
+
+
+@pytest.mark.parametrize("rows,cols", [(30720, 3840), (17408, 256), (11264, 2048)])
+def test_matvec_geglu_equals_two_steps(env, rows, cols):
+    """Gemma's gate|up product with the GELU gate in its epilogue: bit for
+    bit the product followed by nya_hip_gelu_pairs, which meets the float64
+    gate; several tokens through nya_hip_gelu_pairs."""
+    rt, L, stream = env
+    kern = Kernels()
+    assert L.nya_hip_matvec_geglu(0, Q4_K, rows, cols, 0, 0, stream) == 0
+    rng = np.random.default_rng(rows + cols + 1)
+    x = rng.standard_normal(cols).astype(np.float32)
+    w = kern.device_weights(synth.weights(Q4_K, rows, cols, seed=rows + 1), Q4_K, rows, cols)
+    dev = Dev(rt)
+    try:
+        wd, xd = dev.put(w), dev.put(x)
+        y, h1, h2 = dev.empty(4 * rows), dev.empty(2 * rows), dev.empty(2 * rows)
+        print(f"geglu {rows}x{cols}", flush=True)
+        assert L.nya_hip_matvec_geglu(wd, Q4_K, rows, cols, xd, h1, stream) == 0
+        kern.matmul(wd, Q4_K, rows, cols, xd, y, 1, 0, 0, stream)
+        assert L.nya_hip_gelu_pairs(y, h2, rows // 2, 1, stream) == 0
+        rt.sync(stream)
+        a, b = dev.get(h1, np.empty(rows // 2, np.float32)), dev.get(h2, np.empty(rows // 2, np.float32))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        yv = dev.get(y, np.empty(rows, np.float32)).astype(np.float64).reshape(-1, 2, 16)
+        g, u = yv[:, 0, :].reshape(-1), yv[:, 1, :].reshape(-1)
+        assert scaled_error(b, 0.5 * g * (1 + np.tanh(0.7978845608028654 * (g + 0.044715 * g ** 3))) * u) <= 2e-6
+        assert L.nya_hip_matvec_geglu(0, Q6_K, rows, cols, 0, 0, stream) == 1    # Q4_K only, as SwiGLU
+        assert L.nya_hip_gelu_pairs(y, y, rows // 2, 1, stream) == 1             # overlapping
     finally:
         dev.close()
 

@@ -224,3 +224,24 @@ def test_gemma_declined_without_its_steps(session_lib, tmp_path, monkeypatch):
     path = tmp_path / "llama.gguf"
     write(path, llama)
     assert compare(session_lib, path, llama, "rocm", TOKENS[:4])["execution"] == "resident"
+
+
+def test_gemma_interleaved_gate_up(session_lib, tmp_path, monkeypatch):
+    """A Gemma feed-forward wide enough for the library's one-token gate|up
+    product (gate|up above 32 rows per CU): the plan interleaves gate and up
+    rows, one-token runs form the GELU gate in the product
+    (nya_hip_matvec_geglu), runs of several through nya_hip_gelu_pairs;
+    logits and cache still match the engine; from a library without the
+    product, one launch more per block and one-token run."""
+    shape = GemmaShape(hidden=8704, context=16)
+    path = tmp_path / "gemma.gguf"
+    write_gemma(path, shape)
+    launches = {}
+    for name, lib in (("fused", None), ("unfused", mock_without(tmp_path, ("nya_hip_matvec_geglu",)))):
+        if lib is not None:
+            monkeypatch.setenv("NYA_ROCM_KERNEL_LIBRARY", str(lib))
+        out = compare(session_lib, path, shape, "rocm", TOKENS[:6])
+        assert out["execution"] == "resident"
+        launches[name] = out["stats"].kernel_launches
+    # 6 decode tokens, then chunks (5, 1, 1, 7, 1): 9 one-token runs.
+    assert launches["unfused"] - launches["fused"] == 9 * shape.blocks, launches

@@ -1,10 +1,12 @@
 // The vector operations of the decoder kept on the device (the resident
 // plan of the ROCm provider), each over `count` tokens at once (one token
 // when decoding, a prompt chunk when prefilling): the embedding rows, RMS
-// normalization with the residual add folded in, rotary position encoding
-// with the KV cache store, causal attention over the KV cache and the gated
-// SiLU. Each restates one step of the engine's CPU token forward
-// (backend/core/llm_cpu.c:424-578, LLaMA branch) with the same operation
+// normalization with the residual add folded in (through the branch's post
+// norm for Gemma), rotary position encoding with the KV cache store (after
+// per-head norms for Gemma), causal attention over the KV cache (with a
+// local window), the gated SiLU or GELU and the logit soft cap. Each
+// restates one step of the engine's CPU token forward
+// (backend/core/llm_cpu.c:424-578, LLaMA and Gemma branches) with the same operation
 // order per element where the step is elementwise; arithmetic is not
 // contracted into fused multiply-adds (the reference's C17 build does not
 // contract either). The matrix products between them are the library's

@@ -153,7 +153,7 @@ NYA_HIP_EXPORT int nya_hip_read_shaped(uintptr_t src, size_t bytes, uintptr_t si
  * Each call enqueues one kernel and returns 0, 1 when declined (null or
  * misaligned pointers, zero or out-of-range sizes), <0 on a HIP failure.
  * Each restates one step of the engine's CPU token forward,
- * backend/core/llm_cpu.c:424-578 (LLaMA). */
+ * backend/core/llm_cpu.c:424-578 (its LLaMA and Gemma branches). */
 
 /* step[0] = token (uint32), step[1] = position (int32), written on the
  * stream: the ids of one decode token for the calls below (tokens = step,

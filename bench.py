@@ -742,11 +742,15 @@ def attention_leg(heads: int = 32, kv_heads: int = 8, width: int = 128, layers: 
     return out
 
 
-def resident_legs(tg: int, pp: int, blocks: int | None, long_tg: int = 36) -> dict:
+def resident_legs(tg: int, pp: int, blocks: int | None, long_tg: int = 36, models=None) -> dict:
+    """Every resident model (or the named ones; then without the attention
+    leg and with long_tg as given)."""
+    names = models or list(RESIDENT_MODELS)
     legs = {name: resident(name, tg, pp if name == "tinyllama-1.1b" else 0, blocks,
-                           VERIFY_TOKENS if name == "llama-8b" else (),
-                           long_tg if name != "tinyllama-1.1b" else 0) for name in RESIDENT_MODELS}
-    legs["attention"] = attention_leg()
+                           VERIFY_TOKENS if name == "llama-8b" and not models else (),
+                           long_tg if name != "tinyllama-1.1b" else 0) for name in names}
+    if not models:
+        legs["attention"] = attention_leg()
     legs["reference_published"] = {
         "tinyllama-1.1b": {"tg128": 205.48, "pp512": 1374.38, "hardware": "RTX 5060 Ti",
                            "source": "backend/README.md:796-803 (Stage 2 Fyodor CUDA resident)"}}
@@ -867,6 +871,9 @@ def main() -> int:
     ap.add_argument("--resident-pp", type=int, default=512, help="prompt tokens of the timed resident prefill")
     ap.add_argument("--resident-blocks", type=int, default=0, help="override the resident models' block count")
     ap.add_argument("--resident-only", action="store_true", help="run only the resident plan measurements")
+    ap.add_argument("--resident-models", default="",
+                    help="with --resident-only: comma-separated models to run (" + ", ".join(RESIDENT_MODELS) +
+                         "), decode only")
     ap.add_argument("--sweep", action="store_true",
                     help="time every decode, small-N and prefill configuration instead (one JSON line each)")
     args = ap.parse_args()
@@ -882,8 +889,14 @@ def main() -> int:
     traffic = measure_traffic() if not (args.no_traffic or args.sweep or args.prefill_only or args.resident_only
                                         or args.calibrate_copy) else {"error": "not measured (--no-traffic)"}
     if args.resident_only:
-        print(json.dumps({"resident": resident_legs(args.resident_tg, args.resident_pp, args.resident_blocks or None)}),
-              flush=True)
+        models = [m for m in args.resident_models.split(",") if m]
+        unknown = [m for m in models if m not in RESIDENT_MODELS]
+        if unknown:
+            print(f"unknown resident models: {unknown} (known: {list(RESIDENT_MODELS)})", file=sys.stderr)
+            return 2
+        legs = resident_legs(args.resident_tg, args.resident_pp, args.resident_blocks or None,
+                             0 if models else 36, models or None)
+        print(json.dumps({"resident": legs}), flush=True)
         return 0
     rt = Runtime()
     kern = Kernels()

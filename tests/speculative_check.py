@@ -63,12 +63,19 @@ def check_same_decode(got, ref, ref_rows, where: str):
     return len(got)
 
 
-def verify_matches_steps(shape: fm.LlamaShape, tokens: list[int], chunk: int):
+def model_of(shape, tensors=None):
+    """fyodor_amd.model's description of a LLaMA or Gemma shape."""
+    if isinstance(shape, fm.GemmaShape):
+        return fm.GemmaModel(shape, tensors)
+    return fm.LlamaModel(shape, tensors)
+
+
+def verify_matches_steps(shape, tokens: list[int], chunk: int):
     """plan_verify over chunks of `tokens` against plan_token one at a time:
     the same greedy choices and logits within the engine's bound; a chunk
     run again from an earlier position (a rejected proposal) as well."""
     compute = Compute("rocm")
-    model = fm.LlamaModel(shape)
+    model = model_of(shape)
     serial, batched = fm.Plan(compute, model, shape.context), fm.Plan(compute, model, shape.context)
     worst = 0.0
     try:
@@ -121,7 +128,7 @@ def swapped_output(shape: fm.LlamaShape, tensors, a: int, b: int):
     return out
 
 
-def generation_equals_target_decode(target_shape: fm.LlamaShape, draft_shape: fm.LlamaShape | None, prompt,
+def generation_equals_target_decode(target_shape, draft_shape, prompt,
                                     limit: int, windows=(1, 4), same_draft: bool = False, stop_at: int | None = None,
                                     swap: bool = False):
     """nya_compute_generate_greedy with the draft (or the target's own weights
@@ -129,7 +136,7 @@ def generation_equals_target_decode(target_shape: fm.LlamaShape, draft_shape: fm
     none) at each window emits the serial greedy decode of the target;
     returns (window, counters) of every run."""
     compute = Compute("rocm")
-    target_model = fm.LlamaModel(target_shape)
+    target_model = model_of(target_shape)
     capacity = len(prompt) + limit
     oracle = fm.Plan(compute, target_model, capacity)
     try:
@@ -142,7 +149,7 @@ def generation_equals_target_decode(target_shape: fm.LlamaShape, draft_shape: fm
         draft_model = fm.LlamaModel(target_shape, swapped_output(target_shape, target_model.arrays, a,
                                                                  (a + 1) % target_shape.vocabulary))
     else:
-        draft_model = target_model if same_draft else (fm.LlamaModel(draft_shape) if draft_shape else None)
+        draft_model = target_model if same_draft else (model_of(draft_shape) if draft_shape else None)
     stops = ()
     if stop_at is not None:
         stops = (ref[stop_at],)

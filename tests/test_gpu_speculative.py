@@ -90,3 +90,25 @@ def test_sampled_generation_matches_oracle(draft):
 def test_sampled_first_token_distribution():
     p, count, accepted = first_token_follows_target(fm.LlamaShape(context=64, seed=3), PROMPT[:1], runs=400)
     print(f"p {p:.4f}: {count} of 400 leading, {accepted} accepted", flush=True)
+
+
+GEMMA = dict(embedding=512, heads=8, kv_heads=4, width=256, local_width=128, hidden=1024, window=16, context=96,
+             vocabulary=1000)
+
+
+@pytest.mark.parametrize("chunk", [5, 33])
+def test_gemma_verify_matches_serial_steps(chunk):
+    """A Gemma target's batched verification (soft cap on every row, local
+    windows across the chunk) against one step at a time."""
+    shape = fm.GemmaShape(**GEMMA, seed=3)
+    tokens = [(i * 37 + 11) % shape.vocabulary for i in range(2 * chunk + 3)]
+    worst = verify_matches_steps(shape, tokens, chunk)
+    print(f"gemma chunk {chunk}: worst scaled logit error {worst:.3g}", flush=True)
+
+
+@pytest.mark.parametrize("draft", ["other", "same", "none"])
+def test_gemma_generation_equals_target_decode(draft):
+    target = fm.GemmaShape(**GEMMA, seed=3)
+    other = fm.GemmaShape(**{**GEMMA, "local": (0,)}, shared_kv_layers=0, output_scales=(), seed=11)
+    generation_equals_target_decode(target, other if draft == "other" else None, PROMPT, limit=40,
+                                    same_draft=draft == "same")

@@ -115,3 +115,20 @@ def test_requests_outside_limits_are_refused(mock_rocm):
     finally:
         plan.close()
         compute.close()
+
+
+def test_gemma_verify_matches_serial_steps(mock_rocm):
+    """Batched verification of a Gemma target (its soft cap on every row)
+    against one step at a time."""
+    verify_matches_steps(fm.GemmaShape(context=32, seed=3), [5, 17, 200, 3, 42, 99, 250, 1, 7, 64, 128], chunk=5)
+
+
+@pytest.mark.parametrize("draft", ["none", "same", "other"])
+def test_gemma_generation_equals_target_decode(mock_rocm, draft):
+    """Greedy generation with batched verification on a Gemma target emits
+    its serial greedy decode, with no draft, the target itself, or a
+    one-block Gemma draft."""
+    target = fm.GemmaShape(context=64, seed=3)
+    other = fm.GemmaShape(context=64, seed=11, local=(0,), shared_kv_layers=0, output_scales=())
+    generation_equals_target_decode(target, other if draft == "other" else None, PROMPT, limit=20,
+                                    same_draft=draft == "same")

@@ -475,17 +475,24 @@ NYA_HIP_EXPORT int nya_hip_attention_split(uintptr_t q, size_t q_stride, uintptr
                                          (int)splits, scale, (hipStream_t)stream));
 }
 
-NYA_HIP_EXPORT int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
-    uintptr_t r, uintptr_t norm, float eps, uintptr_t hout, uintptr_t y, uintptr_t positions, uintptr_t frequencies,
-    size_t heads, size_t kv_heads, size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream)
+// A matrix of q|k|v rows [first_row, first_row + rows) of heads + 2 kv_heads
+// heads of width: all of them, or one part (even first row).
+static bool qkv_part_ok(size_t rows, size_t first_row, size_t heads, size_t kv_heads, size_t width)
+{
+    return count_ok(heads) && count_ok(kv_heads) && count_ok(width) && width % 2 == 0 && heads <= 65536 &&
+           kv_heads <= 65536 && (heads + 2 * kv_heads) <= (size_t)INT_MAX / width && first_row % 2 == 0 &&
+           first_row < (heads + 2 * kv_heads) * width && rows <= (heads + 2 * kv_heads) * width - first_row;
+}
+
+NYA_HIP_EXPORT int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, size_t first_row,
+    uintptr_t x, uintptr_t r, uintptr_t norm, float eps, uintptr_t hout, uintptr_t y, uintptr_t positions,
+    uintptr_t frequencies, size_t heads, size_t kv_heads, size_t width, size_t capacity, uintptr_t keys,
+    uintptr_t values, uintptr_t stream)
 {
     size_t b;
     if (!storage_bytes(type, rows, cols, &b) || !matvec_normed_rope_supported(type, (int)rows, (int)cols)) return 1;
     if (!w) return 0;   // the shape query
-    if (!count_ok(heads) || !count_ok(kv_heads) || !count_ok(width) || width % 2 || !count_ok(capacity) ||
-        heads > (size_t)INT_MAX / width || kv_heads > (size_t)INT_MAX / width ||
-        rows != (heads + 2 * kv_heads) * width)
-        return 1;
+    if (!qkv_part_ok(rows, first_row, heads, kv_heads, width) || !count_ok(capacity)) return 1;
     if (!x || !norm || !y || (r && !hout) || !vec(positions) || !vec(frequencies) || !vec(keys) || !vec(values) ||
         ((w | x | r | norm | hout) & 15u) || (y & 3u))
         return 1;
@@ -493,27 +500,24 @@ NYA_HIP_EXPORT int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t
     if (r && hout < x + 4 * cols && x < hout + 4 * cols) return 1;
     return status(launch_matvec_normed_rope(type, (const uint8_t *)w, (const float *)x, (const float *)r,
                                             (const float *)norm, (float *)hout, eps, (float *)y, (int)rows, (int)cols,
-                                            (const int *)positions, (const float *)frequencies, (float *)keys,
-                                            (float *)values, (int)(heads * width), (int)(kv_heads * width), (int)width,
-                                            (int)capacity, (hipStream_t)stream));
+                                            (int)first_row, (const int *)positions, (const float *)frequencies,
+                                            (float *)keys, (float *)values, (int)(heads * width),
+                                            (int)(kv_heads * width), (int)width, (int)capacity, (hipStream_t)stream));
 }
 
-NYA_HIP_EXPORT int nya_hip_matvec_scaled_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t hn,
-    uintptr_t parts, float eps, uintptr_t y, uintptr_t positions, uintptr_t frequencies, size_t heads, size_t kv_heads,
-    size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream)
+NYA_HIP_EXPORT int nya_hip_matvec_scaled_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, size_t first_row,
+    uintptr_t hn, uintptr_t parts, float eps, uintptr_t y, uintptr_t positions, uintptr_t frequencies, size_t heads,
+    size_t kv_heads, size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream)
 {
     size_t b;
     if (!storage_bytes(type, rows, cols, &b) || !matvec_normed_rope_supported(type, (int)rows, (int)cols)) return 1;
     if (!w) return 0;   // the shape query
-    if (!count_ok(heads) || !count_ok(kv_heads) || !count_ok(width) || width % 2 || !count_ok(capacity) ||
-        heads > (size_t)INT_MAX / width || kv_heads > (size_t)INT_MAX / width ||
-        rows != (heads + 2 * kv_heads) * width)
-        return 1;
+    if (!qkv_part_ok(rows, first_row, heads, kv_heads, width) || !count_ok(capacity)) return 1;
     if (!hn || !parts || !y || !vec(positions) || !vec(frequencies) || !vec(keys) || !vec(values) ||
         ((w | hn) & 15u) || (parts & 7u) || (y & 3u))
         return 1;
     return status(launch_matvec_scaled_rope(type, (const uint8_t *)w, (const float *)hn, (const double *)parts, eps,
-                                            (float *)y, (int)rows, (int)cols, (const int *)positions,
+                                            (float *)y, (int)rows, (int)cols, (int)first_row, (const int *)positions,
                                             (const float *)frequencies, (float *)keys, (float *)values,
                                             (int)(heads * width), (int)(kv_heads * width), (int)width, (int)capacity,
                                             (hipStream_t)stream));

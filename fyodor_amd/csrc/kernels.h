@@ -40,17 +40,18 @@ hipError_t launch_matvec_normed(unsigned type, const uint8_t *w, const float *x,
     float *hout, float eps, float *y, int rows, int cols, hipStream_t stream);
 // The same over the q|k|v rows with rope_qkv's rotary step in its epilogue:
 // y as rope_qkv leaves it (q rotated), k and v into the cache slot of
-// positions[0]. Rows per CU even.
+// positions[0]. Rows per CU even. The matrix holds q|k|v rows
+// [row0, row0 + rows) (row0 even): all of them, or one part.
 bool matvec_normed_rope_supported(unsigned type, int rows, int cols);
 hipError_t launch_matvec_normed_rope(unsigned type, const uint8_t *w, const float *x, const float *r, const float *g,
-    float *hout, float eps, float *y, int rows, int cols, const int *positions, const float *freq, float *keys,
-    float *values, int qd, int kvd, int width, int capacity, hipStream_t stream);
+    float *hout, float eps, float *y, int rows, int cols, int row0, const int *positions, const float *freq,
+    float *keys, float *values, int qd, int kvd, int width, int capacity, hipStream_t stream);
 // The same rotary product of h * g with the norm's scale on the row sums,
 // from the partial sums of squares of launch_matvec_residual (before the
 // rotary step); the shapes of matvec_normed_rope_supported.
 hipError_t launch_matvec_scaled_rope(unsigned type, const uint8_t *w, const float *hn, const double *parts, float eps,
-    float *y, int rows, int cols, const int *positions, const float *freq, float *keys, float *values, int qd, int kvd,
-    int width, int capacity, hipStream_t stream);
+    float *y, int rows, int cols, int row0, const int *positions, const float *freq, float *keys, float *values,
+    int qd, int kvd, int width, int capacity, hipStream_t stream);
 // The gate|up product of one token with rows interleaved in 16-row blocks
 // (gate rows, then their up rows) and silu(gate) * up as its output: Q4_K on
 // the one-workgroup-per-tile kernel (more than 32 rows per CU), one column

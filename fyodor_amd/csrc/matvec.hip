@@ -355,6 +355,9 @@ struct NormIn {
     // Scaled products (x already h * g): the producing product's sums of
     // squares, kNormParts of them (see ResidOut).
     const double *parts;
+    // The q|k|v row of the matrix's first row (even): a matrix may hold one
+    // part of the rows (q|k of one weight type, v of another).
+    int row0;
 };
 
 // Sums of squares handed from a product with the residual epilogue to the
@@ -726,7 +729,7 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
     float rope_freq = 0.f;
     if constexpr (ROPE) {
         rope_position = nm.positions[0];
-        const int row = base + (int)(threadIdx.x & 63);
+        const int row = nm.row0 + base + (int)(threadIdx.x & 63);
         const int e = row < nm.qd ? row : row - nm.qd;
         rope_freq = row < nm.qd + nm.kvd ? nm.freq[(e % nm.width) >> 1] : 0.f;
     }
@@ -936,7 +939,7 @@ __device__ __forceinline__ void matvec_rows_body(const uint8_t *__restrict__ w, 
     if constexpr (ROPE) {
         // Rows come in pairs within the workgroup (base and live even).
         const float other = __shfl_xor(sum, 1, 64);
-        const int row = base + r, position = rope_position;
+        const int row = nm.row0 + base + r, position = rope_position;
         if (position >= 0 && position < nm.capacity) {
             const bool is_q = row < nm.qd, is_k = !is_q && row < nm.qd + nm.kvd;
             const int e = is_q ? row : row - nm.qd;
@@ -1781,12 +1784,13 @@ bool matvec_normed_rope_supported(unsigned type, int rows, int cols)
 }
 
 hipError_t launch_matvec_normed_rope(unsigned type, const uint8_t *w, const float *x, const float *r, const float *g,
-    float *hout, float eps, float *y, int rows, int cols, const int *positions, const float *freq, float *keys,
-    float *values, int qd, int kvd, int width, int capacity, hipStream_t s)
+    float *hout, float eps, float *y, int rows, int cols, int row0, const int *positions, const float *freq,
+    float *keys, float *values, int qd, int kvd, int width, int capacity, hipStream_t s)
 {
-    if (!matvec_normed_rope_supported(type, rows, cols)) return hipErrorInvalidValue;
+    if (!matvec_normed_rope_supported(type, rows, cols) || row0 % 2) return hipErrorInvalidValue;
     const int rw = rows_per_workgroup(rows), wgs = (rows + rw - 1) / rw;
-    const NormIn nm{r, g, hout, eps, positions, freq, keys, values, qd, kvd, width, capacity};
+    NormIn nm{r, g, hout, eps, positions, freq, keys, values, qd, kvd, width, capacity};
+    nm.row0 = row0;
     const size_t lds = matvec_lds(cols);
 #define FY_NORMED(TT) \
     hipLaunchKernelGGL((matvec_rows_norm<TT, true>), dim3(wgs), dim3(1024), lds, s, w, x, y, rows, cols, rw, nm)
@@ -1802,13 +1806,14 @@ hipError_t launch_matvec_normed_rope(unsigned type, const uint8_t *w, const floa
 }
 
 hipError_t launch_matvec_scaled_rope(unsigned type, const uint8_t *w, const float *hn, const double *parts, float eps,
-    float *y, int rows, int cols, const int *positions, const float *freq, float *keys, float *values, int qd, int kvd,
-    int width, int capacity, hipStream_t s)
+    float *y, int rows, int cols, int row0, const int *positions, const float *freq, float *keys, float *values,
+    int qd, int kvd, int width, int capacity, hipStream_t s)
 {
-    if (!matvec_normed_rope_supported(type, rows, cols)) return hipErrorInvalidValue;
+    if (!matvec_normed_rope_supported(type, rows, cols) || row0 % 2) return hipErrorInvalidValue;
     const int rw = rows_per_workgroup(rows), wgs = (rows + rw - 1) / rw;
     NormIn nm{nullptr, nullptr, nullptr, eps, positions, freq, keys, values, qd, kvd, width, capacity};
     nm.parts = parts;
+    nm.row0 = row0;
     const size_t lds = matvec_lds(cols);
 #define FY_SCALED(TT) \
     hipLaunchKernelGGL((matvec_rows_norm<TT, true, true>), dim3(wgs), dim3(1024), lds, s, w, hn, y, rows, cols, rw, nm)

@@ -67,8 +67,8 @@ typedef struct nya_resident_ops {
     int (*matvec_normed)(uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t, uintptr_t, float, uintptr_t,
         uintptr_t, uintptr_t);
     /* Optional: NULL leaves the rotary step a launch of its own. */
-    int (*matvec_normed_rope)(uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t, uintptr_t, float, uintptr_t,
-        uintptr_t, uintptr_t, uintptr_t, size_t, size_t, size_t, size_t, uintptr_t, uintptr_t, uintptr_t);
+    int (*matvec_normed_rope)(uintptr_t, unsigned, size_t, size_t, size_t, uintptr_t, uintptr_t, uintptr_t, float,
+        uintptr_t, uintptr_t, uintptr_t, uintptr_t, size_t, size_t, size_t, size_t, uintptr_t, uintptr_t, uintptr_t);
     /* Optional as a pair: NULL keeps gate and up in two blocks of rows. */
     int (*matvec_swiglu)(uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t, uintptr_t);
     int (*silu_pairs)(uintptr_t, uintptr_t, size_t, size_t, uintptr_t);
@@ -80,7 +80,7 @@ typedef struct nya_resident_ops {
         uintptr_t);
     /* Optional (with matvec_residual and matvec_normed_rope): NULL keeps the
      * attention norm inside every q|k|v workgroup. */
-    int (*matvec_scaled_rope)(uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t, float, uintptr_t,
+    int (*matvec_scaled_rope)(uintptr_t, unsigned, size_t, size_t, size_t, uintptr_t, uintptr_t, float, uintptr_t,
         uintptr_t, uintptr_t, size_t, size_t, size_t, size_t, uintptr_t, uintptr_t, uintptr_t);
     /* Optional: NULL keeps attention one workgroup per query head at every
      * length. */

@@ -282,18 +282,23 @@ NYA_HIP_EXPORT int nya_hip_matvec_normed(uintptr_t w, unsigned type, size_t rows
     uintptr_t r, uintptr_t norm, float eps, uintptr_t hout, uintptr_t y, uintptr_t stream);
 
 /* No counterpart in the reference: nya_hip_matvec_normed of the q|k|v rows
- * (rows = (heads + 2 kv_heads) width: q, then k, then v) with
+ * ((heads + 2 kv_heads) width of them: q, then k, then v) with
  * nya_hip_rope_qkv's rotary step of one token in its epilogue (frequencies,
  * positions, capacity, keys and values as there): y is left as the two
  * steps leave it (q rows rotated, k and v rows as produced) and the key and
  * value rows go into the cache slot of positions[0], bit for bit, for a
  * position in [0, capacity); outside it nothing is rotated or stored, as
- * there. One launch for the attention norm, the q|k|v product and the
- * rotary step of a decode token. w == 0 queries the shape: as
- * nya_hip_matvec_normed, with rows and rows per CU even. */
-NYA_HIP_EXPORT int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x,
-    uintptr_t r, uintptr_t norm, float eps, uintptr_t hout, uintptr_t y, uintptr_t positions, uintptr_t frequencies,
-    size_t heads, size_t kv_heads, size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream);
+ * there. W holds the q|k|v rows [first_row, first_row + rows): all of them
+ * (first_row 0), or one part where the rows are stored in two matrices of
+ * different types (q|k and v of a Q4_K_M model), one call per part
+ * (first_row even; y is the part's own rows). One launch for the attention
+ * norm, the q|k|v product and the rotary step of a decode token (one per
+ * part). w == 0 queries the shape: as nya_hip_matvec_normed, with rows and
+ * rows per CU even. */
+NYA_HIP_EXPORT int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, size_t first_row,
+    uintptr_t x, uintptr_t r, uintptr_t norm, float eps, uintptr_t hout, uintptr_t y, uintptr_t positions,
+    uintptr_t frequencies, size_t heads, size_t kv_heads, size_t width, size_t capacity, uintptr_t keys,
+    uintptr_t values, uintptr_t stream);
 
 /* No counterpart in the reference: nya_hip_matvec_normed_rope of the decoder's
  * normalized residual from nya_hip_matvec_residual's outputs (the previous
@@ -304,12 +309,13 @@ NYA_HIP_EXPORT int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t
  * as nya_hip_rms_norm followed by the product and nya_hip_rope_qkv do, not
  * bit for bit. For callers that run one decode token (the resident plan):
  * the attention norm of every block after the first without a reduction in
- * each workgroup. w == 0 queries the shape: 0 where it runs (the shapes of
- * nya_hip_matvec_normed_rope), else 1; then also 1 for missing or
- * misaligned vectors (hn 16 bytes, parts 8, y and the rotary arguments 4). */
-NYA_HIP_EXPORT int nya_hip_matvec_scaled_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t hn,
-    uintptr_t parts, float eps, uintptr_t y, uintptr_t positions, uintptr_t frequencies, size_t heads, size_t kv_heads,
-    size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream);
+ * each workgroup. first_row as there. w == 0 queries the shape: 0 where it
+ * runs (the shapes of nya_hip_matvec_normed_rope), else 1; then also 1 for
+ * missing or misaligned vectors (hn 16 bytes, parts 8, y and the rotary
+ * arguments 4). */
+NYA_HIP_EXPORT int nya_hip_matvec_scaled_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, size_t first_row,
+    uintptr_t hn, uintptr_t parts, float eps, uintptr_t y, uintptr_t positions, uintptr_t frequencies, size_t heads,
+    size_t kv_heads, size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream);
 
 /* No counterpart in the reference: the gate|up product of one token with
  * the gated SiLU as its output. W (rows = 2 n, the library's layout) holds

@@ -711,34 +711,63 @@ API int nya_hip_matvec_normed(uintptr_t w, unsigned type, size_t rows, size_t co
     return rc;
 }
 
-/* The normed q|k|v product with the rotary step: the two mock steps. */
-API int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t x, uintptr_t r,
-    uintptr_t norm, float eps, uintptr_t hout, uintptr_t y, uintptr_t positions, uintptr_t freq, size_t heads,
-    size_t kv_heads, size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream)
+/* The rotary step over q|k|v rows [first_row, first_row + rows) held in y
+ * (y[i] is row first_row + i), as nya_hip_rope_qkv treats those rows. */
+static void mock_rope_part(float *y, size_t first_row, size_t rows, size_t heads, size_t kv_heads, size_t width,
+    const float *freq, int position, size_t capacity, float *keys, float *values)
+{
+    if (position < 0 || (size_t)position >= capacity) return;
+    const size_t qd = heads * width, kvd = kv_heads * width;
+    for (size_t i = 0; i < rows; i += 2) {
+        const size_t row = first_row + i;
+        if (row >= qd + kvd) {
+            values[(size_t)position * kvd + row - qd - kvd] = y[i];
+            values[(size_t)position * kvd + row + 1 - qd - kvd] = y[i + 1];
+            continue;
+        }
+        const size_t e = row < qd ? row : row - qd;
+        const float angle = (float)position * freq[(e % width) / 2];
+        const float c = cosf(angle), sn = sinf(angle), a = y[i], b = y[i + 1];
+        const float o0 = a * c - b * sn, o1 = a * sn + b * c;
+        if (row < qd) {
+            y[i] = o0;
+            y[i + 1] = o1;
+        } else {
+            keys[(size_t)position * kvd + e] = o0;
+            keys[(size_t)position * kvd + e + 1] = o1;
+        }
+    }
+}
+
+/* The normed q|k|v product (or one part of its rows) with the rotary step:
+ * the two mock steps. */
+API int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, size_t first_row, uintptr_t x,
+    uintptr_t r, uintptr_t norm, float eps, uintptr_t hout, uintptr_t y, uintptr_t positions, uintptr_t freq,
+    size_t heads, size_t kv_heads, size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream)
 {
     if (nya_hip_matvec_normed(0, type, rows, cols, 0, 0, 0, eps, 0, 0, stream) || rows % 2 ||
         ((rows + 255) / 256) % 2)
         return 1;
     if (!w) return 0;
-    if (!heads || !kv_heads || !width || width % 2 || rows != (heads + 2 * kv_heads) * width) return 1;
+    if (!heads || !kv_heads || !width || width % 2 || first_row % 2 ||
+        first_row + rows > (heads + 2 * kv_heads) * width)
+        return 1;
     int rc = nya_hip_matvec_normed(w, type, rows, cols, x, r, norm, eps, hout, y, stream);
-    const size_t qd = heads * width, kvd = kv_heads * width;
     if (!rc)
-        rc = nya_hip_rope_qkv(y, rows, y + 4 * qd, rows, y + 4 * (qd + kvd), rows, 1, heads, kv_heads, width, freq,
-                              positions, capacity, keys, values, stream);
+        mock_rope_part((float *)y, first_row, rows, heads, kv_heads, width, (const float *)freq,
+                       ((const int *)positions)[0], capacity, (float *)keys, (float *)values);
     return rc;
 }
 
-/* The rotary product of hn scaled by the norm of the partial sums: the mock
- * product of hn * scale and the mock rotary step; the shapes of the normed
- * rotary product. w == 0 queries. */
-API int nya_hip_matvec_scaled_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, uintptr_t hn,
-    uintptr_t parts, float eps, uintptr_t y, uintptr_t positions, uintptr_t freq, size_t heads, size_t kv_heads,
-    size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream)
+API int nya_hip_matvec_scaled_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, size_t first_row,
+    uintptr_t hn, uintptr_t parts, float eps, uintptr_t y, uintptr_t positions, uintptr_t freq, size_t heads,
+    size_t kv_heads, size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream)
 {
-    if (nya_hip_matvec_normed_rope(0, type, rows, cols, 0, 0, 0, eps, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, stream)) return 1;
+    if (nya_hip_matvec_normed_rope(0, type, rows, cols, 0, 0, 0, 0, eps, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, stream))
+        return 1;
     if (!w) return 0;
-    if (!hn || !parts || !y || !heads || !kv_heads || !width || width % 2 || rows != (heads + 2 * kv_heads) * width)
+    if (!hn || !parts || !y || !heads || !kv_heads || !width || width % 2 || first_row % 2 ||
+        first_row + rows > (heads + 2 * kv_heads) * width)
         return 1;
     double total = 0.0;
     for (size_t j = 0; j < 256; ++j) total += ((const double *)parts)[j];
@@ -748,9 +777,8 @@ API int nya_hip_matvec_scaled_rope(uintptr_t w, unsigned type, size_t rows, size
     for (size_t i = 0; i < cols; ++i) xn[i] = ((const float *)hn)[i] * scale;
     int rc = nya_hip_matmul(w, type, rows, cols, (uintptr_t)xn, y, 1, 0, 0, stream);
     free(xn);
-    const size_t qd = heads * width, kvd = kv_heads * width;
     if (!rc)
-        rc = nya_hip_rope_qkv(y, rows, y + 4 * qd, rows, y + 4 * (qd + kvd), rows, 1, heads, kv_heads, width, freq,
-                              positions, capacity, keys, values, stream);
+        mock_rope_part((float *)y, first_row, rows, heads, kv_heads, width, (const float *)freq,
+                       ((const int *)positions)[0], capacity, (float *)keys, (float *)values);
     return rc;
 }

@@ -171,11 +171,12 @@ def test_decode_graph_replays_match_direct_launches(monkeypatch, dims):
         from fyodor_amd.hip import Kernels
         L = Kernels().lib
         up, u, sz = ctypes.c_size_t, ctypes.c_uint, ctypes.c_size_t
-        L.nya_hip_matvec_normed_rope.argtypes = [up, u, sz, sz, up, up, up, ctypes.c_float, up, up, up, up, sz, sz,
-                                                 sz, sz, up, up, up]
+        L.nya_hip_matvec_normed_rope.argtypes = [up, u, sz, sz, sz, up, up, up, ctypes.c_float, up, up, up, up, sz,
+                                                 sz, sz, sz, up, up, up]
         L.nya_hip_matvec_swiglu.argtypes = [up, u, sz, sz, up, up, up]
         # Both fused entries take this model's products (shape queries).
-        assert L.nya_hip_matvec_normed_rope(0, Q4_K, 512, 256, 0, 0, 0, 1e-5, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0) == 0
+        assert L.nya_hip_matvec_normed_rope(0, Q4_K, 512, 256, 0, 0, 0, 0, 1e-5, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0,
+                                            0) == 0
         assert L.nya_hip_matvec_swiglu(0, Q4_K, 2 * 8704, 256, 0, 0, 0) == 0
     model = fm.LlamaModel(shape)
     tokens = [(i * 37 + 11) % shape.vocabulary for i in range(40)]

@@ -71,11 +71,11 @@ def env():
     L.nya_hip_matvec_residual.argtypes = [_up, _u, _sz, _sz, _up, _up, _up, _up, _up, _up]
     L.nya_hip_matvec_swiglu_scaled.argtypes = [_up, _u, _sz, _sz, _up, _up, _f, _up, _up]
     L.nya_hip_matvec_normed.argtypes = [_up, _u, _sz, _sz, _up, _up, _up, _f, _up, _up, _up]
-    L.nya_hip_matvec_normed_rope.argtypes = [_up, _u, _sz, _sz, _up, _up, _up, _f, _up, _up, _up, _up, _sz, _sz, _sz,
-                                             _sz, _up, _up, _up]
+    L.nya_hip_matvec_normed_rope.argtypes = [_up, _u, _sz, _sz, _sz, _up, _up, _up, _f, _up, _up, _up, _up, _sz,
+                                             _sz, _sz, _sz, _up, _up, _up]
     L.nya_hip_silu_pairs.argtypes = [_up, _up, _sz, _sz, _up]
-    L.nya_hip_matvec_scaled_rope.argtypes = [_up, _u, _sz, _sz, _up, _up, _f, _up, _up, _up, _sz, _sz, _sz, _sz, _up,
-                                             _up, _up]
+    L.nya_hip_matvec_scaled_rope.argtypes = [_up, _u, _sz, _sz, _sz, _up, _up, _f, _up, _up, _up, _sz, _sz, _sz,
+                                             _sz, _up, _up, _up]
     stream = rt.stream()
     yield rt, L, stream
     rt.sync(stream)
@@ -842,7 +842,8 @@ def test_matvec_normed_rope_equals_two_steps(env, t, heads, kv_heads, width, pos
     cols, capacity = 4096, 512
     qd, kvd = heads * width, kv_heads * width
     rows = qd + 2 * kvd
-    assert L.nya_hip_matvec_normed_rope(0, t, rows, cols, 0, 0, 0, 1e-5, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, stream) == 0
+    assert L.nya_hip_matvec_normed_rope(0, t, rows, cols, 0, 0, 0, 0, 1e-5, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0,
+                                        stream) == 0
     rng = np.random.default_rng(rows + position)
     x = (3 * rng.standard_normal(cols)).astype(np.float32)
     r = rng.standard_normal(cols).astype(np.float32)
@@ -858,7 +859,7 @@ def test_matvec_normed_rope_equals_two_steps(env, t, heads, kv_heads, width, pos
         fd, pd = dev.put(freq), dev.put(np.array([position], np.int32))
         h1, h2, y1, y2 = dev.empty(4 * cols), dev.empty(4 * cols), dev.empty(4 * rows), dev.empty(4 * rows)
         print(f"normed_rope {TYPE_NAMES[t]} {heads}/{kv_heads} width {width} position {position}", flush=True)
-        assert L.nya_hip_matvec_normed_rope(wd, t, rows, cols, xd, rd, gd, 1e-5, h1, y1, pd, fd, heads, kv_heads,
+        assert L.nya_hip_matvec_normed_rope(wd, t, rows, cols, 0, xd, rd, gd, 1e-5, h1, y1, pd, fd, heads, kv_heads,
                                             width, capacity, k1, v1, stream) == 0
         assert L.nya_hip_matvec_normed(wd, t, rows, cols, xd, rd, gd, 1e-5, h2, y2, stream) == 0
         assert L.nya_hip_rope_qkv(y2, rows, y2 + 4 * qd, rows, y2 + 4 * (qd + kvd), rows, 1, heads, kv_heads, width,
@@ -871,6 +872,95 @@ def test_matvec_normed_rope_equals_two_steps(env, t, heads, kv_heads, width, pos
         assert np.array_equal(bits(h1, np.empty(cols, np.float32)), bits(h2, np.empty(cols, np.float32)))
     finally:
         dev.close()
+
+
+ROPE_PARTS = [("qk|v", Q4_K, Q6_K, "qk"), ("q|kv", Q4_K, Q8_0, "q")]
+
+
+@pytest.mark.parametrize("name,t0,t1,split", ROPE_PARTS, ids=[c[0] for c in ROPE_PARTS])
+def test_matvec_rope_parts(env, oracle, name, t0, t1, split):
+    """q|k|v rows stored as two matrices of different types (a Q4_K_M
+    model's Q6_K value matrix): one normed rotary product per part, the
+    first adding the residual, the second reading the updated residual,
+    equal bit for bit the normed products of the parts followed by one
+    rotary step over the rows put together; the scaled form per part is
+    within the contract bounds of that (8B heads, position 77)."""
+    rt, L, stream = env
+    kern = Kernels()
+    heads, kv_heads, width, cols, capacity, position = 32, 8, 128, 4096, 512, 77
+    qd, kvd = heads * width, kv_heads * width
+    rows = qd + 2 * kvd
+    cut = qd + kvd if split == "qk" else qd
+    shapes = [(t0, cut, 0), (t1, rows - cut, cut)]
+    rng = np.random.default_rng(cut)
+    x = (3 * rng.standard_normal(cols)).astype(np.float32)
+    r = rng.standard_normal(cols).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    cache_k = rng.standard_normal((capacity, kvd)).astype(np.float32)
+    cache_v = rng.standard_normal((capacity, kvd)).astype(np.float32)
+    freq = (10000.0 ** (-np.arange(width // 2) * 2.0 / width)).astype(np.float32)
+    host = [synth.weights(t, n, cols, seed=n + 3) for t, n, _ in shapes]
+    dev = Dev(rt)
+    try:
+        wd = [dev.put(kern.device_weights(hw, t, n, cols)) for hw, (t, n, _) in zip(host, shapes)]
+        xd, rd, gd = dev.put(x), dev.put(r), dev.put(g)
+        k1, v1, k2, v2 = dev.put(cache_k), dev.put(cache_v), dev.put(cache_k), dev.put(cache_v)
+        k3, v3 = dev.put(cache_k), dev.put(cache_v)
+        fd, pd = dev.put(freq), dev.put(np.array([position], np.int32))
+        h1, h2 = dev.empty(4 * cols), dev.empty(4 * cols)
+        y1, y2, y3 = dev.empty(4 * rows), dev.empty(4 * rows), dev.empty(4 * rows)
+        for (t, n, first), w in zip(shapes, wd):
+            assert L.nya_hip_matvec_normed_rope(0, t, n, cols, 0, 0, 0, 0, 1e-5, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0,
+                                                stream) == 0
+        print(f"rope parts {name}", flush=True)
+        # The parts: the first adds r into x (h to h1), the second reads h1.
+        (t, n, first), w = shapes[0], wd[0]
+        assert L.nya_hip_matvec_normed_rope(w, t, n, cols, first, xd, rd, gd, 1e-5, h1, y1, pd, fd, heads, kv_heads,
+                                            width, capacity, k1, v1, stream) == 0
+        (t, n, first), w = shapes[1], wd[1]
+        assert L.nya_hip_matvec_normed_rope(w, t, n, cols, first, h1, 0, gd, 1e-5, 0, y1 + 4 * first, pd, fd, heads,
+                                            kv_heads, width, capacity, k1, v1, stream) == 0
+        # The separate steps.
+        (t, n, first), w = shapes[0], wd[0]
+        assert L.nya_hip_matvec_normed(w, t, n, cols, xd, rd, gd, 1e-5, h2, y2, stream) == 0
+        (t, n, first), w = shapes[1], wd[1]
+        assert L.nya_hip_matvec_normed(w, t, n, cols, h2, 0, gd, 1e-5, 0, y2 + 4 * first, stream) == 0
+        assert L.nya_hip_rope_qkv(y2, rows, y2 + 4 * qd, rows, y2 + 4 * (qd + kvd), rows, 1, heads, kv_heads, width,
+                                  fd, pd, capacity, k2, v2, stream) == 0
+        # The scaled form of each part, from h * g and its partial sums.
+        hv = (x + r).astype(np.float32)
+        hd = hv.astype(np.float64)
+        parts = np.zeros(NORM_PARTS)
+        for j in range(0, cols, 16):
+            parts[j // 16] = float((hd[j:j + 16] ** 2).sum())
+        hnd, prd = dev.put(hv * g), dev.put(parts)
+        for (t, n, first), w in zip(shapes, wd):
+            assert L.nya_hip_matvec_scaled_rope(w, t, n, cols, first, hnd, prd, 1e-5, y3 + 4 * first, pd, fd, heads,
+                                                kv_heads, width, capacity, k3, v3, stream) == 0
+        assert L.nya_hip_matvec_normed_rope(wd[1], t1, rows - cut, cols, cut + 1, xd, 0, gd, 1e-5, 0, y3, pd, fd,
+                                            heads, kv_heads, width, capacity, k3, v3, stream) == 1   # odd first row
+        assert L.nya_hip_matvec_normed_rope(wd[1], t1, rows - cut, cols, cut + 2, xd, 0, gd, 1e-5, 0, y3, pd, fd,
+                                            heads, kv_heads, width, capacity, k3, v3, stream) == 1   # past the rows
+        rt.sync(stream)
+        bits = lambda p, like: dev.get(p, like).view(np.uint32)
+        assert np.array_equal(bits(y1, np.empty(rows, np.float32)), bits(y2, np.empty(rows, np.float32)))
+        assert np.array_equal(bits(k1, cache_k), bits(k2, cache_k))
+        assert np.array_equal(bits(v1, cache_v), bits(v2, cache_v))
+        assert np.array_equal(bits(h1, np.empty(cols, np.float32)), bits(h2, np.empty(cols, np.float32)))
+        a = dev.get(y3, np.empty(rows, np.float32))
+        b = dev.get(y2, np.empty(rows, np.float32))
+        ka, kb = dev.get(k3, cache_k), dev.get(k2, cache_k)
+        va, vb = dev.get(v3, cache_v), dev.get(v2, cache_v)
+    finally:
+        dev.close()
+    xnd = hd / np.sqrt(np.mean(hd * hd) + 1e-5) * g.astype(np.float64)
+    mags = np.concatenate([oracle.contract_sums(hw, t, xnd, n, cols)[1][0] for hw, (t, n, _) in zip(host, shapes)])
+    m = 2e-6 * (1 + mags)
+    bound = m + m[np.arange(rows) ^ 1]
+    for got, want, bd, what in ((a, b, bound, "rows"), (ka[position], kb[position], bound[qd:qd + kvd], "key"),
+                                (va[position], vb[position], bound[qd + kvd:], "value")):
+        err = np.abs(got.astype(np.float64) - want) / (bd + 1e-6 * np.abs(want))
+        assert err.max() <= 1, f"scaled parts, {what}: worst {err.max():.3g}"
 
 
 @pytest.mark.parametrize("t,heads,kv_heads,width,position", NORMED_ROPE,
@@ -890,7 +980,7 @@ def test_matvec_scaled_rope(env, oracle, t, heads, kv_heads, width, position):
     cols, capacity = 4096, 512
     qd, kvd = heads * width, kv_heads * width
     rows = qd + 2 * kvd
-    assert L.nya_hip_matvec_scaled_rope(0, t, rows, cols, 0, 0, 1e-5, 0, 0, 0, 0, 0, 0, 0, 0, 0, stream) == 0
+    assert L.nya_hip_matvec_scaled_rope(0, t, rows, cols, 0, 0, 0, 1e-5, 0, 0, 0, 0, 0, 0, 0, 0, 0, stream) == 0
     rng = np.random.default_rng(rows + position + 5)
     h = (3 * rng.standard_normal(cols)).astype(np.float32)
     g = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
@@ -910,9 +1000,9 @@ def test_matvec_scaled_rope(env, oracle, t, heads, kv_heads, width, position):
         fd, pd = dev.put(freq), dev.put(np.array([position], np.int32))
         y1, y2 = dev.empty(4 * rows), dev.empty(4 * rows)
         print(f"scaled_rope {TYPE_NAMES[t]} {heads}/{kv_heads} width {width} position {position}", flush=True)
-        assert L.nya_hip_matvec_scaled_rope(wd, t, rows, cols, hnd, prd, 1e-5, y1, pd, fd, heads, kv_heads, width,
+        assert L.nya_hip_matvec_scaled_rope(wd, t, rows, cols, 0, hnd, prd, 1e-5, y1, pd, fd, heads, kv_heads, width,
                                             capacity, k1, v1, stream) == 0
-        assert L.nya_hip_matvec_normed_rope(wd, t, rows, cols, xd, 0, gd, 1e-5, 0, y2, pd, fd, heads, kv_heads,
+        assert L.nya_hip_matvec_normed_rope(wd, t, rows, cols, 0, xd, 0, gd, 1e-5, 0, y2, pd, fd, heads, kv_heads,
                                             width, capacity, k2, v2, stream) == 0
         rt.sync(stream)
         got = lambda p, like: dev.get(p, np.empty_like(like))

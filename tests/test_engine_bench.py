@@ -17,7 +17,7 @@ import subprocess
 import pytest
 
 from conftest import REPO
-from gguf_model import LlamaShape, write
+from gguf_model import GemmaShape, LlamaShape, write, write_gemma
 
 BENCH = REPO / "oracle" / "_ref" / "fyodor-bench"
 
@@ -65,6 +65,18 @@ def test_engine_bench_on_mock_provider(bench_binary, mock_paths, tmp_path):
     # provider operations.
     cpu = run_bench(bench_binary, model, env, "-b", "cpu", "-p", "8", "-n", "8", "-r", "2", "--warmup", "1")
     assert cpu["backend"] == "cpu" and cpu["execution"] == "cpu-optimized"
+
+
+def test_engine_bench_gemma_on_mock_provider(bench_binary, mock_paths, tmp_path):
+    """A Gemma 4 model through the engine's benchmark runs resident too."""
+    import os
+    good, _ = mock_paths
+    model = tmp_path / "gemma.gguf"
+    write_gemma(model, GemmaShape(context=32))
+    env = dict(os.environ, NYA_ROCM_HIP_LIBRARY=str(good), NYA_ROCM_KERNEL_LIBRARY=str(good))
+    env.pop("NYA_ROCM_CACHE_MIB", None)
+    out = run_bench(bench_binary, model, env, "-b", "rocm", "-p", "8", "-n", "8", "-r", "2", "--warmup", "1")
+    check_contract(out, "rocm", "resident")
 
 
 def test_engine_bench_declines_unknown_provider(bench_binary, tmp_path):

@@ -20,7 +20,7 @@ import pytest
 
 from conftest import REPO
 from fyodor_amd import KERNEL_LIBRARY, Q4_K, Q6_K
-from gguf_model import LlamaShape, write
+from gguf_model import GemmaShape, LlamaShape, write, write_gemma
 from test_engine_bench import check_contract
 
 pytestmark = pytest.mark.gpu
@@ -48,6 +48,17 @@ def run(model, env, *args):
 def test_engine_bench_contract_on_gpu(env, tmp_path):
     model = tmp_path / "model.gguf"
     write(model, LlamaShape(embedding=512, heads=8, kv_heads=2, hidden=1024, blocks=3, context=64, vocabulary=1000))
+    out = run(model, env, "-p", "8", "-n", "8", "-r", "2", "--warmup", "1")
+    check_contract(out, "rocm", "resident")
+
+
+def test_engine_bench_gemma_contract_on_gpu(env, tmp_path):
+    """A Gemma 4 model (local and global layers, shared KV, soft cap) through
+    the engine's benchmark on the GPU: resident, with the contract's
+    counters."""
+    model = tmp_path / "gemma.gguf"
+    write_gemma(model, GemmaShape(embedding=512, heads=8, kv_heads=4, width=256, local_width=128, hidden=1024,
+                                  window=16, context=64, vocabulary=1000))
     out = run(model, env, "-p", "8", "-n", "8", "-r", "2", "--warmup", "1")
     check_contract(out, "rocm", "resident")
 

@@ -523,6 +523,36 @@ NYA_HIP_EXPORT int nya_hip_matvec_scaled_rope(uintptr_t w, unsigned type, size_t
                                             (hipStream_t)stream));
 }
 
+NYA_HIP_EXPORT int nya_hip_matvec_rope_pair(uintptr_t w0, unsigned type0, size_t rows0, uintptr_t w1, unsigned type1,
+    size_t rows1, size_t cols, uintptr_t x, uintptr_t r, uintptr_t norm, uintptr_t hout, uintptr_t parts, float eps,
+    uintptr_t y, uintptr_t positions, uintptr_t frequencies, size_t heads, size_t kv_heads, size_t width,
+    size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream)
+{
+    size_t b;
+    if (!storage_bytes(type0, rows0, cols, &b) || !storage_bytes(type1, rows1, cols, &b) ||
+        !matvec_rope_pair_supported(type0, (int)rows0, type1, (int)rows1, (int)cols))
+        return 1;
+    if (!w0) return 0;   // the shape query
+    if (!w1 || !qkv_part_ok(rows0 + rows1, 0, heads, kv_heads, width) ||
+        rows0 + rows1 != (heads + 2 * kv_heads) * width || !count_ok(capacity) || !x || !y || !vec(positions) ||
+        !vec(frequencies) || !vec(keys) || !vec(values) || ((w0 | w1 | x) & 15u) || (y & 3u))
+        return 1;
+    if (parts) {
+        if (parts & 7u) return 1;
+        r = norm = hout = 0;
+    } else {
+        if (!norm || (r && !hout) || ((r | norm | hout) & 15u)) return 1;
+        if (r && hout < r + 4 * cols && r < hout + 4 * cols) return 1;
+        if (r && hout < x + 4 * cols && x < hout + 4 * cols) return 1;
+    }
+    return status(launch_matvec_rope_pair(type0, (const uint8_t *)w0, (int)rows0, type1, (const uint8_t *)w1,
+                                          (int)rows1, (int)cols, (const float *)x, (const float *)r,
+                                          (const float *)norm, (float *)hout, (const double *)parts, eps, (float *)y,
+                                          (const int *)positions, (const float *)frequencies, (float *)keys,
+                                          (float *)values, (int)(heads * width), (int)(kv_heads * width), (int)width,
+                                          (int)capacity, (hipStream_t)stream));
+}
+
 NYA_HIP_EXPORT int nya_hip_greedy(uintptr_t logits, size_t n, size_t count, uintptr_t mask, uintptr_t ids,
     uintptr_t stream)
 {

@@ -52,6 +52,15 @@ hipError_t launch_matvec_normed_rope(unsigned type, const uint8_t *w, const floa
 hipError_t launch_matvec_scaled_rope(unsigned type, const uint8_t *w, const float *hn, const double *parts, float eps,
     float *y, int rows, int cols, int row0, const int *positions, const float *freq, float *keys, float *values,
     int qd, int kvd, int width, int capacity, hipStream_t stream);
+// Both rotary products over q|k|v rows stored as two matrices (q|k of
+// type0, then v of type1: Q4_K and Q6_K) in one launch, the CUs split
+// between them by bytes: the scaled form where parts is given (x = h * g),
+// else the normed form (x the residual, r, g, hout as there).
+bool matvec_rope_pair_supported(unsigned type0, int rows0, unsigned type1, int rows1, int cols);
+hipError_t launch_matvec_rope_pair(unsigned type0, const uint8_t *w0, int rows0, unsigned type1, const uint8_t *w1,
+    int rows1, int cols, const float *x, const float *r, const float *g, float *hout, const double *parts, float eps,
+    float *y, const int *positions, const float *freq, float *keys, float *values, int qd, int kvd, int width,
+    int capacity, hipStream_t stream);
 // The gate|up product of one token with rows interleaved in 16-row blocks
 // (gate rows, then their up rows) and silu(gate) * up as its output: Q4_K on
 // the one-workgroup-per-tile kernel (more than 32 rows per CU), one column

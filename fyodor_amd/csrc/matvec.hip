@@ -427,7 +427,7 @@ __device__ __forceinline__ void norm_group(float4 &v, float4 r, float4 g, const 
 {
     __shared__ double part[16];
     const float4 h = nm.r ? add4(v, r) : v;
-    if (writer && has_group && nm.r) ((float4 *)nm.hout)[64 * wave + lane] = h;
+    if (writer && has_group && nm.r && nm.hout) ((float4 *)nm.hout)[64 * wave + lane] = h;
     const double s = wave_sum_pairs(sq4(h));
     if (lane == 0) part[wave] = s;
     __syncthreads();
@@ -1023,6 +1023,42 @@ __global__ __launch_bounds__(1024) void matvec_rows_norm(const uint8_t *__restri
     else
         matvec_rows_body<T, 1, 1, 16, 1, false, false, false, !SCALED, ROPE, false, SCALED>(
             w, x, nullptr, y, rows, cols, base, live, 0, ngc, 0, sdig, smeta, red, nm);
+}
+
+// The rotary product over q|k|v rows stored as two matrices of types T0
+// (rows [0, rows0)) and T1 (the rest) in one launch: workgroups [0, wgs0)
+// (in xcd_block order) take rw0 rows each of the first, the others rw1 rows
+// of the second, each with matvec_rows_norm's body; only the first part
+// writes the updated residual (nm1.hout null).
+template <unsigned T0, unsigned T1, bool SCALED>
+__global__ __launch_bounds__(1024) void matvec_rows_norm_pair(const uint8_t *__restrict__ w0,
+    const uint8_t *__restrict__ w1, const float *__restrict__ x, float *__restrict__ y, int rows0, int rows1,
+    int cols, int rw0, int rw1, int wgs0, NormIn nm0, NormIn nm1)
+{
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ float red[16][1][64];
+    uint8_t *sdig = lds;
+    float4 *smeta = (float4 *)(lds + (size_t)128 * (cols / 32));
+    const int b = xcd_block(), ngc = cols / kGroupCols;
+    if (b < wgs0) {
+        const int base = b * rw0, live = rows0 - base < rw0 ? rows0 - base : rw0;
+        const int tiles = (rows0 + kTileRows - 1) / kTileRows;
+        if (rows0 % kTileRows == 0 || base + live <= kTileRows * (tiles - 1))
+            matvec_rows_body<T0, 1, 1, 16, 1, true, false, false, !SCALED, true, false, SCALED>(
+                w0, x, nullptr, y, rows0, cols, base, live, 0, ngc, 0, sdig, smeta, red, nm0);
+        else
+            matvec_rows_body<T0, 1, 1, 16, 1, false, false, false, !SCALED, true, false, SCALED>(
+                w0, x, nullptr, y, rows0, cols, base, live, 0, ngc, 0, sdig, smeta, red, nm0);
+    } else {
+        const int base = (b - wgs0) * rw1, live = rows1 - base < rw1 ? rows1 - base : rw1;
+        const int tiles = (rows1 + kTileRows - 1) / kTileRows;
+        if (rows1 % kTileRows == 0 || base + live <= kTileRows * (tiles - 1))
+            matvec_rows_body<T1, 1, 1, 16, 1, true, false, false, !SCALED, true, false, SCALED>(
+                w1, x, nullptr, y + rows0, rows1, cols, base, live, 0, ngc, 0, sdig, smeta, red, nm1);
+        else
+            matvec_rows_body<T1, 1, 1, 16, 1, false, false, false, !SCALED, true, false, SCALED>(
+                w1, x, nullptr, y + rows0, rows1, cols, base, live, 0, ngc, 0, sdig, smeta, red, nm1);
+    }
 }
 
 size_t matvec_lds(int ccols)
@@ -1802,6 +1838,63 @@ hipError_t launch_matvec_normed_rope(unsigned type, const uint8_t *w, const floa
     default: return hipErrorInvalidValue;
     }
 #undef FY_NORMED
+    return hipGetLastError();
+}
+
+// The workgroup split of a two-part rotary product: the CUs shared by the
+// parts' bytes, rows per workgroup even and at most one tile.
+struct RopePair {
+    int rw0, rw1, wgs0, wgs1;
+};
+
+bool rope_pair_split(unsigned type0, int rows0, unsigned type1, int rows1, int cols, RopePair *out)
+{
+    if (type0 != Q4_K || type1 != Q6_K || rows0 <= 0 || rows1 <= 0 || rows0 % 2 || rows1 % 2 ||
+        cols % kGroupCols || cols > 16 * kGroupCols)
+        return false;
+    const int cus = cu_count();
+    const double b0 = (double)rows0 * tiled_row_bytes<Q4_K>(cols), b1 = (double)rows1 * tiled_row_bytes<Q6_K>(cols);
+    int wgs1 = (int)(cus * b1 / (b0 + b1) + 0.5);
+    wgs1 = wgs1 < 1 ? 1 : wgs1 > cus - 1 ? cus - 1 : wgs1;
+    RopePair p;
+    p.rw1 = (rows1 + wgs1 - 1) / wgs1;
+    p.rw1 += p.rw1 % 2;
+    p.wgs1 = (rows1 + p.rw1 - 1) / p.rw1;
+    const int wgs0 = cus - p.wgs1;
+    if (wgs0 < 1) return false;
+    p.rw0 = (rows0 + wgs0 - 1) / wgs0;
+    p.rw0 += p.rw0 % 2;
+    p.wgs0 = (rows0 + p.rw0 - 1) / p.rw0;
+    if (p.rw0 > kTileRows || p.rw1 > kTileRows) return false;
+    *out = p;
+    return true;
+}
+
+bool matvec_rope_pair_supported(unsigned type0, int rows0, unsigned type1, int rows1, int cols)
+{
+    RopePair p;
+    return rope_pair_split(type0, rows0, type1, rows1, cols, &p);
+}
+
+hipError_t launch_matvec_rope_pair(unsigned type0, const uint8_t *w0, int rows0, unsigned type1, const uint8_t *w1,
+    int rows1, int cols, const float *x, const float *r, const float *g, float *hout, const double *parts, float eps,
+    float *y, const int *positions, const float *freq, float *keys, float *values, int qd, int kvd, int width,
+    int capacity, hipStream_t s)
+{
+    RopePair p;
+    if (!rope_pair_split(type0, rows0, type1, rows1, cols, &p)) return hipErrorInvalidValue;
+    NormIn nm0{r, g, hout, eps, positions, freq, keys, values, qd, kvd, width, capacity};
+    nm0.parts = parts;
+    NormIn nm1 = nm0;
+    nm1.hout = nullptr;
+    nm1.row0 = rows0;
+    const dim3 grid((unsigned)(p.wgs0 + p.wgs1));
+    if (parts)
+        hipLaunchKernelGGL((matvec_rows_norm_pair<Q4_K, Q6_K, true>), grid, dim3(1024), matvec_lds(cols), s, w0, w1,
+                           x, y, rows0, rows1, cols, p.rw0, p.rw1, p.wgs0, nm0, nm1);
+    else
+        hipLaunchKernelGGL((matvec_rows_norm_pair<Q4_K, Q6_K, false>), grid, dim3(1024), matvec_lds(cols), s, w0, w1,
+                           x, y, rows0, rows1, cols, p.rw0, p.rw1, p.wgs0, nm0, nm1);
     return hipGetLastError();
 }
 

@@ -82,6 +82,11 @@ typedef struct nya_resident_ops {
      * attention norm inside every q|k|v workgroup. */
     int (*matvec_scaled_rope)(uintptr_t, unsigned, size_t, size_t, size_t, uintptr_t, uintptr_t, float, uintptr_t,
         uintptr_t, uintptr_t, size_t, size_t, size_t, size_t, uintptr_t, uintptr_t, uintptr_t);
+    /* Optional (with matvec_normed_rope): NULL runs q|k|v stored in two
+     * types as one rotary launch per part. */
+    int (*matvec_rope_pair)(uintptr_t, unsigned, size_t, uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t,
+        uintptr_t, uintptr_t, uintptr_t, float, uintptr_t, uintptr_t, uintptr_t, size_t, size_t, size_t, size_t,
+        uintptr_t, uintptr_t, uintptr_t);
     /* Optional: NULL keeps attention one workgroup per query head at every
      * length. */
     int (*attention_split)(uintptr_t, size_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, uintptr_t, size_t, size_t,

@@ -379,6 +379,10 @@ static int bind_all(session *s)
         nya_vendor_symbol(s->kernel_module, "nya_hip_matvec_scaled_rope", &s->resident.matvec_scaled_rope,
                           sizeof s->resident.matvec_scaled_rope))
         s->resident.matvec_scaled_rope = NULL;
+    if (!s->resident.matvec_normed_rope ||
+        nya_vendor_symbol(s->kernel_module, "nya_hip_matvec_rope_pair", &s->resident.matvec_rope_pair,
+                          sizeof s->resident.matvec_rope_pair))
+        s->resident.matvec_rope_pair = NULL;
     if (nya_vendor_symbol(s->kernel_module, "nya_hip_attention_split", &s->resident.attention_split,
                           sizeof s->resident.attention_split))
         s->resident.attention_split = NULL;

@@ -300,6 +300,23 @@ NYA_HIP_EXPORT int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t
     uintptr_t frequencies, size_t heads, size_t kv_heads, size_t width, size_t capacity, uintptr_t keys,
     uintptr_t values, uintptr_t stream);
 
+/* No counterpart in the reference: both parts of q|k|v rows stored as two
+ * matrices — q|k (rows0 rows of type0) and v (rows1 of type1): Q4_K and
+ * Q6_K, a Q4_K_M model's value matrices — through the rotary product in one
+ * launch, the CUs split between the parts by their bytes. With parts
+ * nonzero, the scaled form of nya_hip_matvec_scaled_rope (x = hn; r, norm
+ * and hout unused); else the normed form of nya_hip_matvec_normed_rope (x,
+ * r, norm, hout as there). y receives all rows0 + rows1 = (heads +
+ * 2 kv_heads) width rows and the cache slot of positions[0] the key and
+ * value rows, as the two per-part calls leave them (bit for bit). w0 == 0
+ * queries the shape (type0, rows0, type1, rows1, cols): 0 where it runs
+ * (Q4_K then Q6_K, even row counts, cols a multiple of 256 up to 4096, at
+ * most 32 rows per workgroup of either part), else 1. */
+NYA_HIP_EXPORT int nya_hip_matvec_rope_pair(uintptr_t w0, unsigned type0, size_t rows0, uintptr_t w1, unsigned type1,
+    size_t rows1, size_t cols, uintptr_t x, uintptr_t r, uintptr_t norm, uintptr_t hout, uintptr_t parts, float eps,
+    uintptr_t y, uintptr_t positions, uintptr_t frequencies, size_t heads, size_t kv_heads, size_t width,
+    size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream);
+
 /* No counterpart in the reference: nya_hip_matvec_normed_rope of the decoder's
  * normalized residual from nya_hip_matvec_residual's outputs (the previous
  * block's down product): the q|k|v row sums of W hn times the norm's scale

@@ -759,6 +759,55 @@ API int nya_hip_matvec_normed_rope(uintptr_t w, unsigned type, size_t rows, size
     return rc;
 }
 
+/* Both parts of q|k|v stored in two types (Q4_K then Q6_K) in one call:
+ * the per-part mock steps; the shapes the library takes on 256 CUs (its
+ * workgroup split between the parts by bytes). */
+API int nya_hip_matvec_scaled_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, size_t first_row,
+    uintptr_t hn, uintptr_t parts, float eps, uintptr_t y, uintptr_t positions, uintptr_t freq, size_t heads,
+    size_t kv_heads, size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream);
+
+API int nya_hip_matvec_rope_pair(uintptr_t w0, unsigned type0, size_t rows0, uintptr_t w1, unsigned type1,
+    size_t rows1, size_t cols, uintptr_t x, uintptr_t r, uintptr_t norm, uintptr_t hout, uintptr_t parts, float eps,
+    uintptr_t y, uintptr_t positions, uintptr_t freq, size_t heads, size_t kv_heads, size_t width, size_t capacity,
+    uintptr_t keys, uintptr_t values, uintptr_t stream)
+{
+    if (type0 != 12 || type1 != 14 || !rows0 || !rows1 || rows0 % 2 || rows1 % 2 || cols % 256 || cols > 4096)
+        return 1;
+    /* The stand-in runs the per-part steps: each part must take them. */
+    if (nya_hip_matvec_normed_rope(0, type0, rows0, cols, 0, 0, 0, 0, eps, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, stream) ||
+        nya_hip_matvec_normed_rope(0, type1, rows1, cols, 0, 0, 0, 0, eps, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, stream))
+        return 1;
+    /* The library's split: the 256 CUs shared by the parts' bytes. */
+    const double b0 = (double)rows0 * (cols / 256) * 144, b1 = (double)rows1 * (cols / 256) * 210;
+    size_t wgs1 = (size_t)(256 * b1 / (b0 + b1) + 0.5);
+    wgs1 = wgs1 < 1 ? 1 : wgs1 > 255 ? 255 : wgs1;
+    size_t rw1 = (rows1 + wgs1 - 1) / wgs1;
+    rw1 += rw1 % 2;
+    wgs1 = (rows1 + rw1 - 1) / rw1;
+    const size_t wgs0 = 256 - wgs1;
+    size_t rw0 = (rows0 + wgs0 - 1) / wgs0;
+    rw0 += rw0 % 2;
+    if (rw0 > 32 || rw1 > 32) return 1;
+    if (!w0) return 0;
+    if (!w1 || !x || !y || rows0 + rows1 != (heads + 2 * kv_heads) * width) return 1;
+    if (parts) {
+        for (int k = 0; k < 2; ++k) {
+            const int rc = nya_hip_matvec_scaled_rope(k ? w1 : w0, k ? type1 : type0, k ? rows1 : rows0, cols,
+                                                      k ? rows0 : 0, x, parts, eps, y + (k ? 4 * rows0 : 0),
+                                                      positions, freq, heads, kv_heads, width, capacity, keys, values,
+                                                      stream);
+            if (rc) return rc;
+        }
+        return 0;
+    }
+    int rc = nya_hip_matvec_normed_rope(w0, type0, rows0, cols, 0, x, r, norm, eps, hout, y, positions, freq, heads,
+                                        kv_heads, width, capacity, keys, values, stream);
+    if (!rc)
+        rc = nya_hip_matvec_normed_rope(w1, type1, rows1, cols, rows0, r ? hout : x, 0, norm, eps, 0, y + 4 * rows0,
+                                        positions, freq, heads, kv_heads, width, capacity, keys, values, stream);
+    return rc;
+}
+
 API int nya_hip_matvec_scaled_rope(uintptr_t w, unsigned type, size_t rows, size_t cols, size_t first_row,
     uintptr_t hn, uintptr_t parts, float eps, uintptr_t y, uintptr_t positions, uintptr_t freq, size_t heads,
     size_t kv_heads, size_t width, size_t capacity, uintptr_t keys, uintptr_t values, uintptr_t stream)

@@ -37,7 +37,7 @@ def test_kernel_library_exports_its_header():
                     "nya_hip_matvec_swiglu_scaled", "nya_hip_silu_pairs",
                     "nya_hip_matvec_normed", "nya_hip_matvec_normed_rope", "nya_hip_matvec_scaled_rope",
                     "nya_hip_post_norm", "nya_hip_head_norm_rope", "nya_hip_gelu_mul", "nya_hip_softcap",
-                    "nya_hip_matvec_geglu", "nya_hip_gelu_pairs"}
+                    "nya_hip_matvec_geglu", "nya_hip_gelu_pairs", "nya_hip_matvec_rope_pair"}
     assert want <= exported(KERNEL_LIBRARY)
 
 

@@ -76,6 +76,8 @@ def env():
     L.nya_hip_silu_pairs.argtypes = [_up, _up, _sz, _sz, _up]
     L.nya_hip_matvec_scaled_rope.argtypes = [_up, _u, _sz, _sz, _sz, _up, _up, _f, _up, _up, _up, _sz, _sz, _sz,
                                              _sz, _up, _up, _up]
+    L.nya_hip_matvec_rope_pair.argtypes = [_up, _u, _sz, _up, _u, _sz, _sz, _up, _up, _up, _up, _up, _f, _up, _up, _up,
+                                           _sz, _sz, _sz, _sz, _up, _up, _up]
     stream = rt.stream()
     yield rt, L, stream
     rt.sync(stream)
@@ -884,7 +886,9 @@ def test_matvec_rope_parts(env, oracle, name, t0, t1, split):
     first adding the residual, the second reading the updated residual,
     equal bit for bit the normed products of the parts followed by one
     rotary step over the rows put together; the scaled form per part is
-    within the contract bounds of that (8B heads, position 77)."""
+    within the contract bounds of that (8B heads, position 77). Q4_K then
+    Q6_K: both parts in one launch (nya_hip_matvec_rope_pair, normed and
+    scaled forms) equal the per-part launches bit for bit."""
     rt, L, stream = env
     kern = Kernels()
     heads, kv_heads, width, cols, capacity, position = 32, 8, 128, 4096, 512, 77
@@ -937,6 +941,16 @@ def test_matvec_rope_parts(env, oracle, name, t0, t1, split):
         for (t, n, first), w in zip(shapes, wd):
             assert L.nya_hip_matvec_scaled_rope(w, t, n, cols, first, hnd, prd, 1e-5, y3 + 4 * first, pd, fd, heads,
                                                 kv_heads, width, capacity, k3, v3, stream) == 0
+        pair = L.nya_hip_matvec_rope_pair(0, t0, cut, 0, t1, rows - cut, cols, 0, 0, 0, 0, 0, 1e-5, 0, 0, 0, 0, 0,
+                                          0, 0, 0, 0, stream)
+        assert pair == (0 if (t0, t1) == (Q4_K, Q6_K) else 1)
+        if pair == 0:
+            k4, v4, k5, v5 = dev.put(cache_k), dev.put(cache_v), dev.put(cache_k), dev.put(cache_v)
+            h4, y4, y5 = dev.empty(4 * cols), dev.empty(4 * rows), dev.empty(4 * rows)
+            assert L.nya_hip_matvec_rope_pair(wd[0], t0, cut, wd[1], t1, rows - cut, cols, xd, rd, gd, h4, 0, 1e-5,
+                                              y4, pd, fd, heads, kv_heads, width, capacity, k4, v4, stream) == 0
+            assert L.nya_hip_matvec_rope_pair(wd[0], t0, cut, wd[1], t1, rows - cut, cols, hnd, 0, 0, 0, prd, 1e-5,
+                                              y5, pd, fd, heads, kv_heads, width, capacity, k5, v5, stream) == 0
         assert L.nya_hip_matvec_normed_rope(wd[1], t1, rows - cut, cols, cut + 1, xd, 0, gd, 1e-5, 0, y3, pd, fd,
                                             heads, kv_heads, width, capacity, k3, v3, stream) == 1   # odd first row
         assert L.nya_hip_matvec_normed_rope(wd[1], t1, rows - cut, cols, cut + 2, xd, 0, gd, 1e-5, 0, y3, pd, fd,
@@ -947,6 +961,11 @@ def test_matvec_rope_parts(env, oracle, name, t0, t1, split):
         assert np.array_equal(bits(k1, cache_k), bits(k2, cache_k))
         assert np.array_equal(bits(v1, cache_v), bits(v2, cache_v))
         assert np.array_equal(bits(h1, np.empty(cols, np.float32)), bits(h2, np.empty(cols, np.float32)))
+        if pair == 0:
+            for got, want, like in ((y4, y1, np.empty(rows, np.float32)), (k4, k1, cache_k), (v4, v1, cache_v),
+                                    (h4, h1, np.empty(cols, np.float32)), (y5, y3, np.empty(rows, np.float32)),
+                                    (k5, k3, cache_k), (v5, v3, cache_v)):
+                assert np.array_equal(bits(got, like), bits(want, like))
         a = dev.get(y3, np.empty(rows, np.float32))
         b = dev.get(y2, np.empty(rows, np.float32))
         ka, kb = dev.get(k3, cache_k), dev.get(k2, cache_k)

@@ -250,22 +250,27 @@ def test_gemma_interleaved_gate_up(session_lib, tmp_path, monkeypatch):
 @pytest.mark.parametrize("hidden", [1024, 8704], ids=["normed", "scaled"])
 def test_rotary_products_in_parts(session_lib, tmp_path, monkeypatch, hidden):
     """q|k in Q4_K and v in Q6_K (a Q4_K_M model's value matrices): one-token
-    runs take one rotary product per part (nya_hip_matvec_normed_rope with
-    the part's first row; with the interleaved gate|up, blocks after the
-    first take nya_hip_matvec_scaled_rope per part), against the norm step,
-    two products and the rotary step (a library without the rotary
-    product): two launches fewer per block and one-token run; logits and
-    cache match the engine."""
+    runs take both parts in one rotary launch (nya_hip_matvec_rope_pair; with
+    the interleaved gate|up, blocks after the first take its scaled form);
+    from a library without it, one rotary product per part
+    (nya_hip_matvec_normed_rope / nya_hip_matvec_scaled_rope with the part's
+    first row), one launch more per block and one-token run; without the
+    rotary product, the norm step, two products and the rotary step, two
+    more. Logits and cache match the engine every way."""
     types = {"embedding": Q4_K, "output": Q6_K, "attention": Q4_K, "value": Q6_K, "gate_up": Q4_K, "down": Q6_K}
     shape = LlamaShape(embedding=512, heads=8, kv_heads=8, hidden=hidden, context=16, types=types)
     path = tmp_path / "model.gguf"
     write(path, shape)
     launches = {}
-    for name, lib in (("parts", None), ("separate", mock_without(tmp_path, ("nya_hip_matvec_normed_rope",)))):
-        if lib is not None:
-            monkeypatch.setenv("NYA_ROCM_KERNEL_LIBRARY", str(lib))
+    for name, entries in (("pair", ()), ("parts", ("nya_hip_matvec_rope_pair",)),
+                          ("separate", ("nya_hip_matvec_normed_rope",))):
+        if entries:
+            lib_dir = tmp_path / name
+            lib_dir.mkdir()
+            monkeypatch.setenv("NYA_ROCM_KERNEL_LIBRARY", str(mock_without(lib_dir, entries)))
         out = compare(session_lib, path, shape, "rocm", TOKENS[:6])
         assert out["execution"] == "resident"
         launches[name] = out["stats"].kernel_launches
     # 6 decode tokens, then chunks (5, 1, 1, 7, 1): 9 one-token runs.
+    assert launches["parts"] - launches["pair"] == 9 * shape.blocks, launches
     assert launches["separate"] - launches["parts"] == 2 * 9 * shape.blocks, launches

@@ -742,6 +742,7 @@ constexpr int kCombineOnce = 64;   // splits whose partials one thread holds in 
 // adds f_s o_s[j] over the splits in order, all their loads requested at
 // once (splits <= 256; the ABI's larger counts run in rounds of 256).
 
+template <bool WIDE>
 __global__ __launch_bounds__(256) void attention_combine(const float *__restrict__ partials,
     float *__restrict__ out, const int *__restrict__ positions, int heads, int width, int max_length, int splits)
 {
@@ -780,9 +781,23 @@ __global__ __launch_bounds__(256) void attention_combine(const float *__restrict
                 if (u < splits) acc += f[u] * pv[u];
             out[((size_t)tok * heads + head) * width + tid] = acc;
         }
+        if constexpr (WIDE) {
+            // Heads wider than the workgroup: column tid + 256, same weights.
+            const int c = tid + 256;
+            if (c < width) {
+#pragma unroll
+                for (int u = 0; u < kCombineOnce; ++u)
+                    pv[u] = partials[(base + (u < splits ? u : splits - 1)) * width + c];
+                float acc = 0.f;
+#pragma unroll
+                for (int u = 0; u < kCombineOnce; ++u)
+                    if (u < splits) acc += f[u] * pv[u];
+                out[((size_t)tok * heads + head) * width + c] = acc;
+            }
+        }
         return;
     }
-    float acc = 0.f;
+    float acc = 0.f, acc2 = 0.f;   // columns tid and (wide heads) tid + 256
     for (int s0 = 0; s0 < splits; s0 += 256) {
         const int ns = splits - s0 < 256 ? splits - s0 : 256;
         const float2 v = tid < ns ? ml[s0 + tid] : make_float2(-INFINITY, 0.f);
@@ -825,9 +840,25 @@ __global__ __launch_bounds__(256) void attention_combine(const float *__restrict
                     if (k0 + u < ns) acc += f[k0 + u] * pv[u];
             }
         }
+        if constexpr (WIDE) {
+            if (tid + 256 < width) {
+                const float *po = partials + (base + s0) * width + tid + 256;
+                constexpr int SU = 16;
+                for (int k0 = 0; k0 < ns; k0 += SU) {
+                    float pv[SU];
+#pragma unroll
+                    for (int u = 0; u < SU; ++u) pv[u] = po[(size_t)(k0 + u < ns ? k0 + u : ns - 1) * width];
+#pragma unroll
+                    for (int u = 0; u < SU; ++u)
+                        if (k0 + u < ns) acc2 += f[k0 + u] * pv[u];
+                }
+            }
+        }
         __syncthreads();
     }
     if (tid < width) out[((size_t)tok * heads + head) * width + tid] = acc;
+    if constexpr (WIDE)
+        if (tid + 256 < width) out[((size_t)tok * heads + head) * width + tid + 256] = acc2;
 }
 
 template <int W, int G>
@@ -838,8 +869,8 @@ void launch_split_wg(const float *q, int q_stride, const float *keys, const floa
     hipLaunchKernelGGL((attention_split<W, G>), dim3((unsigned)kv_heads, (unsigned)splits, (unsigned)count),
                        dim3(256), 0, s, q, q_stride, keys, values, partials, positions, heads, kv_heads, max_length,
                        window, splits, scale);
-    hipLaunchKernelGGL(attention_combine, dim3((unsigned)heads, (unsigned)count), dim3(256), 0, s, partials, out,
-                       positions, heads, W, max_length, splits);
+    hipLaunchKernelGGL((attention_combine<(W > 256)>), dim3((unsigned)heads, (unsigned)count), dim3(256), 0, s,
+                       partials, out, positions, heads, W, max_length, splits);
 }
 
 template <int W>
@@ -852,8 +883,13 @@ hipError_t launch_split_w(const float *q, int q_stride, const float *keys, const
                                   max_length, window, splits, scale, s); break;
     case 2: launch_split_wg<W, 2>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
                                   max_length, window, splits, scale, s); break;
-    case 4: launch_split_wg<W, 4>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
-                                  max_length, window, splits, scale, s); break;
+    case 4:
+        if constexpr (W <= 256) {
+            launch_split_wg<W, 4>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
+                                  max_length, window, splits, scale, s);
+            break;
+        }
+        return hipErrorInvalidValue;
     default:
         if constexpr (W <= 128) {
             launch_split_wg<W, 8>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
@@ -1115,8 +1151,9 @@ bool attention_split_supported(int heads, int kv_heads, int width, int max_lengt
 {
     if (heads <= 0 || kv_heads <= 0 || heads % kv_heads || splits < 1 || splits > 4096 || max_length <= 0) return false;
     const int g = heads / kv_heads;
-    if (width != 64 && width != 128 && width != 256) return false;
+    if (width != 64 && width != 128 && width != 256 && width != 512) return false;
     if (g != 1 && g != 2 && g != 4 && !(g == 8 && width <= 128)) return false;
+    if (width == 512 && g > 2) return false;
     return (max_length + splits - 1) / splits <= kSplitMaxChunk;
 }
 
@@ -1133,6 +1170,9 @@ hipError_t launch_attention_split(const float *q, int q_stride, const float *key
     if (width == 64)
         return launch_split_w<64>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
                                   max_length, window, splits, scale, s);
+    if (width == 512)
+        return launch_split_w<512>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
+                                   max_length, window, splits, scale, s);
     return launch_split_w<256>(q, q_stride, keys, values, out, partials, positions, count, heads, kv_heads,
                                max_length, window, splits, scale, s);
 }

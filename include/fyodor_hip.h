@@ -244,8 +244,9 @@ NYA_HIP_EXPORT int nya_hip_attention(uintptr_t q, size_t q_stride, uintptr_t key
  * values (out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M)): the same
  * softmax, with the exponentials rescaled per split. `partials` is scratch
  * of count * heads * splits * (width + 2) floats (16-byte aligned). Runs for
- * width 64, 128 or 256, heads / kv_heads in {1, 2, 4, 8} (8 up to width
- * 128), ceil(max_length / splits) <= 1024, 16-byte aligned q, keys,
+ * width 64, 128 or 256 with heads / kv_heads in {1, 2, 4, 8} (8 up to width
+ * 128), or width 512 with heads / kv_heads in {1, 2};
+ * ceil(max_length / splits) <= 1024, 16-byte aligned q, keys,
  * values and q_stride a multiple of 4; else returns 1. q == 0 queries the
  * shape (heads, kv_heads, width, max_length, splits): 0 where it runs. */
 NYA_HIP_EXPORT int nya_hip_attention_split(uintptr_t q, size_t q_stride, uintptr_t keys, uintptr_t values,

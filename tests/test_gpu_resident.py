@@ -264,6 +264,54 @@ def test_gemma_long_context_on_gpu(session_lib, rocm_env, tmp_path):
     assert out["execution"] == "resident"
 
 
+def test_gemma_split_512_matches_unsplit_on_gpu(session_lib, rocm_env, tmp_path, monkeypatch):
+    """Heads 512 wide (global) and 256 wide (local) past 320 positions: a
+    session whose attention splits against one that never splits
+    (NYA_ROCM_ATTENTION_SPLIT=0), the same model on the same GPU, every
+    decode step's logits and the caches within the engine's bounds. The
+    unsplit kernels meet the engine at these widths elsewhere; against the
+    engine itself this random 512-wide stack is ill-conditioned at single
+    positions before any split (the engine's own reference and optimized CPU
+    sessions differ in layer 2's cache by 3.1e-5 to 3.1e-4 there, seed by
+    seed), which a direct comparison would test instead of the split."""
+    import numpy as np
+    from resident_check import check_kv, check_logits, kv_widths
+    shape = GemmaShape(embedding=512, heads=4, kv_heads=2, width=512, local_width=256, hidden=1024, window=352,
+                       context=440, vocabulary=1000, seed=13)
+    path = tmp_path / "gemma.gguf"
+    write_gemma(path, shape)
+    tokens = [(i * 29 + 7) % shape.vocabulary for i in range(400)]
+
+    def open_session(split: bool):
+        if split:
+            monkeypatch.delenv("NYA_ROCM_ATTENTION_SPLIT", raising=False)
+        else:
+            monkeypatch.setenv("NYA_ROCM_ATTENTION_SPLIT", "0")
+        model = Model(session_lib, path, "rocm")
+        return model, Session(model, shape.context)
+
+    (split_model, split), (plain_model, plain) = open_session(True), open_session(False)
+    monkeypatch.delenv("NYA_ROCM_ATTENTION_SPLIT", raising=False)
+    try:
+        differ, worst = False, 0.0
+        for i, t in enumerate(tokens):
+            assert split.run([t], True) == 0 and plain.run([t], True) == 0
+            a, b = plain.logits(shape.vocabulary), split.logits(shape.vocabulary)
+            worst = max(worst, check_logits(a, b, f"decode position {i}"))
+            differ |= not np.array_equal(a, b)
+        kv = check_kv(plain, split, kv_widths(shape), len(tokens))
+        assert split.execution() == plain.execution() == "resident"
+        # The split sessions' launches add the combine passes past 320 positions.
+        assert split.stats().kernel_launches > plain.stats().kernel_launches
+        assert differ
+        print(f"gemma 512 split vs unsplit: worst scaled logit error {worst:.3g}, KV {kv:.3g}", flush=True)
+    finally:
+        split.close()
+        plain.close()
+        split_model.close()
+        plain_model.close()
+
+
 def test_gemma_graph_replays_match_direct_launches(session_lib, rocm_env, tmp_path, monkeypatch):
     """A Gemma decode token replayed as a captured graph (the embedding
     scale, head norms, post norms, GELU gate and soft cap among its

@@ -298,7 +298,8 @@ def test_attention(env, heads, kv_heads, width, length, count, window):
 SPLIT_CASES = [(32, 8, 128, 4096, 1, 64, 0), (32, 4, 64, 1000, 1, 16, 0), (8, 8, 128, 300, 1, 8, 0),
                (16, 8, 128, 2000, 3, 32, 0), (8, 2, 256, 5000, 2, 8, 0), (32, 4, 64, 20000, 1, 32, 0),
                (32, 8, 128, 5, 1, 64, 0), (32, 8, 128, 257, 33, 8, 0), (8, 2, 128, 600, 2, 300, 0),
-               (32, 8, 128, 4096, 1, 64, 1024), (8, 2, 256, 5000, 2, 8, 700), (16, 8, 128, 2000, 33, 32, 100)]
+               (32, 8, 128, 4096, 1, 64, 1024), (8, 2, 256, 5000, 2, 8, 700), (16, 8, 128, 2000, 33, 32, 100),
+               (2, 2, 512, 5000, 2, 8, 0), (8, 4, 512, 2000, 3, 64, 512), (4, 2, 512, 3000, 1, 300, 0)]
 
 
 @pytest.mark.parametrize("heads,kv_heads,width,length,count,splits,window", SPLIT_CASES,
@@ -353,6 +354,7 @@ def test_attention_split_declines(env):
         assert L.nya_hip_attention_split(*args(48, 3, 128, 1000, 8)) == 1     # 16 query heads per KV head
         assert L.nya_hip_attention_split(*args(32, 4, 256, 1000, 8)) == 1     # 8 heads of width 256
         assert L.nya_hip_attention_split(*args(32, 8, 128, 9000, 8)) == 1     # 1125 positions per split
+        assert L.nya_hip_attention_split(*args(16, 4, 512, 1000, 8)) == 1     # 4 heads of width 512
         assert L.nya_hip_attention_split(p + 4, 384, p, p, p, p, p, 1, 2, 1, 128, 100, 0, 4, 1.0, stream) == 1  # q align
     finally:
         dev.close()

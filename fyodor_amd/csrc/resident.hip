@@ -76,6 +76,84 @@ __global__ __launch_bounds__(256) void embed(const uint8_t *__restrict__ w, unsi
         o[i] = token < (uint32_t)rows ? element(r, type, i) * scale : 0.f;
 }
 
+// Cross-lane reductions without LDS: DPP moves inside a row of 16 lanes
+// (gfx9 controls 0xB1 quad_perm [1,0,3,2], 0x4E quad_perm [2,3,0,1], 0x141
+// row_half_mirror, 0x140 row_mirror; each lane reads a lane of its own
+// row), then v_readlane across the four rows of a wavefront. (A __shfl_xor
+// is a ds_bpermute: one LDS round trip per step, each waited for before the
+// next.) Every lane of the row, or of the wavefront for the wave forms,
+// must be active.
+template <int CTRL>
+__device__ __forceinline__ float row_lane(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+template <int CTRL>
+__device__ __forceinline__ double row_lane(double v)
+{
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, (uint64_t)hi << 32 | lo);
+}
+
+// The sum (MAX: the maximum) over the 16 lanes of an aligned row, the same
+// bits in each of them: pairs, quads, half rows, the row (each step adds two
+// values in either order, which is the same sum).
+template <bool MAX>
+__device__ __forceinline__ float row16_reduce(float v)
+{
+    if constexpr (MAX) {
+        v = fmaxf(v, row_lane<0xB1>(v));
+        v = fmaxf(v, row_lane<0x4E>(v));
+        v = fmaxf(v, row_lane<0x141>(v));
+        return fmaxf(v, row_lane<0x140>(v));
+    } else {
+        v += row_lane<0xB1>(v);
+        v += row_lane<0x4E>(v);
+        v += row_lane<0x141>(v);
+        return v + row_lane<0x140>(v);
+    }
+}
+
+__device__ __forceinline__ double row16_sum(double v)
+{
+    v += row_lane<0xB1>(v);
+    v += row_lane<0x4E>(v);
+    v += row_lane<0x141>(v);
+    return v + row_lane<0x140>(v);
+}
+
+__device__ __forceinline__ float lane_value(float v, int lane)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+__device__ __forceinline__ double lane_value(double v, int lane)
+{
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), lane);
+    return __builtin_bit_cast(double, (uint64_t)hi << 32 | lo);
+}
+
+// Over the wavefront, the same value in every lane: each row's, then the
+// rows' as (r0 . r1) . (r2 . r3).
+template <bool MAX>
+__device__ __forceinline__ float wave_reduce(float v)
+{
+    v = row16_reduce<MAX>(v);
+    const float r0 = lane_value(v, 0), r1 = lane_value(v, 16), r2 = lane_value(v, 32), r3 = lane_value(v, 48);
+    return MAX ? fmaxf(fmaxf(r0, r1), fmaxf(r2, r3)) : (r0 + r1) + (r2 + r3);
+}
+
+__device__ __forceinline__ double wave_sum(double v)
+{
+    v = row16_sum(v);
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+
 // One workgroup of 1024 per row (token), holding n <= 4096 K elements in
 // registers (K float4 per thread; x, r and w all loaded before the first
 // use). x += r first when r is given (written back); then
@@ -112,7 +190,7 @@ __global__ __launch_bounds__(1024) void rms_norm_regs(float4 *__restrict__ x, co
         s += (double)v[k].x * v[k].x + (double)v[k].y * v[k].y + (double)v[k].z * v[k].z +
              (double)v[k].w * v[k].w;
     }
-    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+    s = wave_sum(s);
     if ((t & 63) == 0) part[t >> 6] = s;
     __syncthreads();
     double total = part[0];
@@ -147,7 +225,7 @@ __global__ __launch_bounds__(256) void rms_norm(float *__restrict__ x, const flo
         }
         s += (double)v * v;
     }
-    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+    s = wave_sum(s);
     if ((t & 63) == 0) part[t >> 6] = s;
     __syncthreads();
     const double total = part[0] + part[1] + part[2] + part[3];
@@ -156,12 +234,12 @@ __global__ __launch_bounds__(256) void rms_norm(float *__restrict__ x, const flo
 }
 
 // Sum of one double per thread over a workgroup of 64 N threads, the same
-// value in every thread: each wavefront's butterfly, then the wavefronts'
-// sums added in order.
+// value in every thread: each wavefront's sum (wave_sum), then the
+// wavefronts' sums added in order.
 template <int N>
 __device__ __forceinline__ double group_sum(double s, double *part)
 {
-    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+    s = wave_sum(s);
     __syncthreads();   // an earlier call's reads of part are done
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
     __syncthreads();
@@ -331,10 +409,7 @@ __global__ __launch_bounds__(256) void rope_qkv(float *__restrict__ q, int q_str
 
 __device__ __forceinline__ float block_reduce(float v, float *red, bool maximum)
 {
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float u = __shfl_xor(v, o, 64);
-        v = maximum ? fmaxf(v, u) : v + u;
-    }
+    v = maximum ? wave_reduce<true>(v) : wave_reduce<false>(v);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
@@ -393,7 +468,15 @@ __device__ __forceinline__ AttentionRow attention_row(const int *positions, int 
 // (g, c) sums float4 column c over t = g, g + G, ... (G = 1024 / W groups),
 // then the groups add up in order. Scores in LDS (LDS: max_length <=
 // kLdsScores), else in the global scratch [count][heads][max_length].
-template <int W, bool LDS>
+//
+// Without a window (WIN false) the causal range starts at row 0, so q, the
+// first U key rows per 16 lanes and the first VU value rows per thread are
+// requested before the token's position is known: rows up to max_length - 1
+// (inside the cache), whatever the range. Rows past the range only feed
+// scores that are never kept and values that are replaced by zeros before
+// they are weighed (they may hold anything, NaN included). With a window the
+// first row depends on the position, which is read first.
+template <int W, bool LDS, bool WIN>
 __global__ __launch_bounds__(256) void attention_w(const float *__restrict__ q, int q_stride,
     const float *__restrict__ keys, const float *__restrict__ values, float *__restrict__ out,
     float *__restrict__ scores, const int *__restrict__ positions, int heads, int kv_heads, int max_length,
@@ -406,46 +489,55 @@ __global__ __launch_bounds__(256) void attention_w(const float *__restrict__ q, 
     __shared__ float lds_scores[LDS ? kLdsScores : 1];
     __shared__ float4 part[256];
     __shared__ float red[4];
-    const AttentionRow a = attention_row(positions, heads, kv_heads, W, q_stride, max_length, window);
-    const int tid = threadIdx.x, length = a.length;
-    if (length == 0) return;
-    const int kv4 = kv_heads * (W / 4);  // float4 per cached position
-    keys += (size_t)a.first * kv_heads * W;
-    values += (size_t)a.first * kv_heads * W;
-    float *sc = LDS ? lds_scores : scores + a.scores;
+    const int head = blockIdx.x, kvh = head / (heads / kv_heads), tid = threadIdx.x;
     const int l16 = tid & 15, row = tid >> 4;
-    const float4 *q4 = (const float4 *)(q + a.q);
+    const int c = tid % (W / 4), g = tid / (W / 4);
+    const float4 *q4 = (const float4 *)(q + (size_t)blockIdx.y * q_stride + (size_t)head * W);
     float4 qr[C];
 #pragma unroll
-    for (int c = 0; c < C; ++c) qr[c] = q4[l16 + 16 * c];
-    const float4 *k4 = (const float4 *)keys + (size_t)a.kvh * (W / 4);
+    for (int k = 0; k < C; ++k) qr[k] = q4[l16 + 16 * k];
+    CausalRange range = {0, 0};
+    if constexpr (WIN) {
+        range = causal_range(positions[blockIdx.y], max_length, window);
+        if (range.length == 0) return;
+    }
+    // The rows loaded before the length is known: up to `last`.
+    const int last = WIN ? range.length - 1 : max_length - 1;
+    const int kv4 = kv_heads * (W / 4);  // float4 per cached position
+    const float4 *k4 = (const float4 *)(keys + (size_t)range.first * kv_heads * W) + (size_t)kvh * (W / 4);
     // The output phase's first VU rows of this thread (rows g, g + G, ...,
     // column c), requested with the keys: V does not wait for the scores.
-    const int c = tid % (W / 4), g = tid / (W / 4);
-    const float4 *v4 = (const float4 *)values + (size_t)a.kvh * (W / 4) + c;
+    const float4 *v4 = (const float4 *)(values + (size_t)range.first * kv_heads * W) + (size_t)kvh * (W / 4) + c;
     float4 vfirst[VU];
 #pragma unroll
     for (int u = 0; u < VU; ++u) {
         const int t = g + G * u;
-        vfirst[u] = v4[(size_t)(t < length ? t : length - 1) * kv4];
+        vfirst[u] = v4[(size_t)(t < last ? t : last) * kv4];
     }
+    float4 kr[U][C];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int t = 16 * u + row, tt = t < last ? t : last;
+#pragma unroll
+        for (int k = 0; k < C; ++k) kr[u][k] = k4[(size_t)tt * kv4 + l16 + 16 * k];
+    }
+    if constexpr (!WIN) {
+        // Read after the loads above are issued (no return before them: a
+        // token without positions skips the loops and the store below).
+        __builtin_amdgcn_sched_barrier(0);
+        range = causal_range(positions[blockIdx.y], max_length, 0);
+    }
+    const int length = range.length;
+    float *sc = LDS ? lds_scores : scores + ((size_t)blockIdx.y * heads + head) * max_length;
     float m = -INFINITY;
-    for (int t0 = 0; t0 < length; t0 += 16 * U) {
-        float4 kr[U][C];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int t = t0 + 16 * u + row;
-            const int tt = t < length ? t : length - 1;
-#pragma unroll
-            for (int c = 0; c < C; ++c) kr[u][c] = k4[(size_t)tt * kv4 + l16 + 16 * c];
-        }
+    auto chunk_scores = [&](int t0) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             float s = 0.f;
 #pragma unroll
-            for (int c = 0; c < C; ++c)
-                s += qr[c].x * kr[u][c].x + qr[c].y * kr[u][c].y + qr[c].z * kr[u][c].z + qr[c].w * kr[u][c].w;
-            for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 16);
+            for (int k = 0; k < C; ++k)
+                s += qr[k].x * kr[u][k].x + qr[k].y * kr[u][k].y + qr[k].z * kr[u][k].z + qr[k].w * kr[u][k].w;
+            s = row16_reduce<false>(s);
             const int t = t0 + 16 * u + row;
             if (t < length) {
                 s = s * scale;
@@ -453,6 +545,19 @@ __global__ __launch_bounds__(256) void attention_w(const float *__restrict__ q, 
                 m = fmaxf(m, s);
             }
         }
+    };
+    // The first chunk whatever the length (its rows are loaded; a shorter
+    // range keeps fewer of its scores), so its loads are not held behind a
+    // test of the length.
+    chunk_scores(0);
+    for (int t0 = 16 * U; t0 < length; t0 += 16 * U) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int t = t0 + 16 * u + row, tt = t < length ? t : length - 1;
+#pragma unroll
+            for (int k = 0; k < C; ++k) kr[u][k] = k4[(size_t)tt * kv4 + l16 + 16 * k];
+        }
+        chunk_scores(t0);
     }
     m = block_reduce(m, red, true);
     __syncthreads();   // every score written before any thread reads one
@@ -473,6 +578,7 @@ __global__ __launch_bounds__(256) void attention_w(const float *__restrict__ q, 
         for (int u = 0; u < VU; ++u) {
             const int t = t0 + G * u, tt = t < length ? t : length - 1;
             vr[u] = t0 == g ? vfirst[u] : v4[(size_t)tt * kv4];
+            if (t >= length) vr[u] = make_float4(0.f, 0.f, 0.f, 0.f);
             p[u] = t < length ? sc[tt] : 0.f;
         }
 #pragma unroll
@@ -485,14 +591,14 @@ __global__ __launch_bounds__(256) void attention_w(const float *__restrict__ q, 
     }
     part[tid] = acc;
     __syncthreads();
-    if (tid < W / 4) {
+    if (tid < W / 4 && length > 0) {
         float4 o = part[tid];
 #pragma unroll
         for (int k = 1; k < G; ++k) {
             const float4 b = part[k * (W / 4) + tid];
             o = make_float4(o.x + b.x, o.y + b.y, o.z + b.z, o.w + b.w);
         }
-        ((float4 *)(out + a.out))[tid] = o;
+        ((float4 *)(out + ((size_t)blockIdx.y * heads + head) * W))[tid] = o;
     }
 }
 
@@ -530,7 +636,7 @@ __global__ __launch_bounds__(256) void attention(const float *__restrict__ q, in
             const float *kr = kb + (size_t)t * kvdim;
             for (int j = l16; j < width; j += 16) s += qs[j] * kr[j];
         }
-        for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 16);
+        s = row16_reduce<false>(s);
         if (t < length) {
             s = s * scale;
             if (l16 == 0) sc[t] = s;
@@ -658,7 +764,7 @@ __global__ __launch_bounds__(256) void attention_split(const float *__restrict__
                 for (int c = 0; c < C; ++c)
                     s += qr[g][c].x * kr[u][c].x + qr[g][c].y * kr[u][c].y + qr[g][c].z * kr[u][c].z +
                          qr[g][c].w * kr[u][c].w;
-                for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 16);
+                s = row16_reduce<false>(s);
                 if (t < n && l16 == 0) sc[g * kSplitMaxChunk + t] = s * scale;
             }
         }
@@ -671,14 +777,14 @@ __global__ __launch_bounds__(256) void attention_split(const float *__restrict__
         float *s = sc + g * kSplitMaxChunk;
         float m = -INFINITY;
         for (int t = lane; t < n; t += 64) m = fmaxf(m, s[t]);
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        m = wave_reduce<true>(m);
         float sum = 0.f;
         for (int t = lane; t < n; t += 64) {
             const float e = expf(s[t] - m);
             s[t] = e;
             sum += e;
         }
-        for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+        sum = wave_reduce<false>(sum);
         if (lane == 0) {
             mls[2 * g] = m;
             mls[2 * g + 1] = sum;
@@ -763,13 +869,13 @@ __global__ __launch_bounds__(256) void attention_combine(const float *__restrict
 #pragma unroll
         for (int u = 0; u < kCombineOnce; ++u) pv[u] = po[(size_t)(u < splits ? u : splits - 1) * width];
         float m = v.x;
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        m = wave_reduce<true>(m);
         if ((tid & 63) == 0) red[tid >> 6] = m;
         __syncthreads();
         m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
         const float e = v.x == -INFINITY ? 0.f : expf(v.x - m);
         float l = v.y * e;
-        for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
+        l = wave_reduce<false>(l);
         if ((tid & 63) == 0) red[4 + (tid >> 6)] = l;
         __syncthreads();
         f[tid] = e / (red[4] + red[5] + red[6] + red[7]);
@@ -804,7 +910,7 @@ __global__ __launch_bounds__(256) void attention_combine(const float *__restrict
         // The maximum and the weighted sum of the l over all splits (the
         // first round covers every split when splits <= 256).
         float m = v.x;
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        m = wave_reduce<true>(m);
         if ((tid & 63) == 0) red[tid >> 6] = m;
         __syncthreads();
         m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -815,7 +921,7 @@ __global__ __launch_bounds__(256) void attention_combine(const float *__restrict
         }
         const float e = v.x == -INFINITY ? 0.f : expf(v.x - m);
         float l = v.y * e;
-        for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
+        l = wave_reduce<false>(l);
         __syncthreads();
         if ((tid & 63) == 0) red[4 + (tid >> 6)] = l;
         __syncthreads();
@@ -1110,12 +1216,18 @@ void launch_attention_w(const float *q, int q_stride, const float *keys, const f
     hipStream_t s)
 {
     const dim3 grid((unsigned)heads, (unsigned)count);
-    if (max_length <= kLdsScores)
-        hipLaunchKernelGGL((attention_w<W, true>), grid, dim3(256), 0, s, q, q_stride, keys, values, out, scores,
+    if (max_length <= kLdsScores && window == 0)
+        hipLaunchKernelGGL((attention_w<W, true, false>), grid, dim3(256), 0, s, q, q_stride, keys, values, out, scores,
                            positions, heads, kv_heads, max_length, window, scale);
+    else if (max_length <= kLdsScores)
+        hipLaunchKernelGGL((attention_w<W, true, true>), grid, dim3(256), 0, s, q, q_stride, keys, values, out, scores,
+                           positions, heads, kv_heads, max_length, window, scale);
+    else if (window == 0)
+        hipLaunchKernelGGL((attention_w<W, false, false>), grid, dim3(256), 0, s, q, q_stride, keys, values, out,
+                           scores, positions, heads, kv_heads, max_length, window, scale);
     else
-        hipLaunchKernelGGL((attention_w<W, false>), grid, dim3(256), 0, s, q, q_stride, keys, values, out, scores,
-                           positions, heads, kv_heads, max_length, window, scale);
+        hipLaunchKernelGGL((attention_w<W, false, true>), grid, dim3(256), 0, s, q, q_stride, keys, values, out,
+                           scores, positions, heads, kv_heads, max_length, window, scale);
 }
 
 hipError_t launch_attention(const float *q, int q_stride, const float *keys, const float *values, float *out,

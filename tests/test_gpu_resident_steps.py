@@ -295,6 +295,47 @@ def test_attention(env, heads, kv_heads, width, length, count, window):
         dev.close()
 
 
+@pytest.mark.parametrize("heads,kv_heads,width,length,count", [
+    (32, 8, 128, 1, 1), (32, 8, 128, 37, 3), (8, 8, 64, 5, 2), (4, 1, 256, 20, 1), (4, 2, 512, 9, 2),
+    (32, 8, 128, 200, 1),
+])
+def test_attention_ignores_rows_past_the_range(env, heads, kv_heads, width, length, count):
+    """Without a window the kernel requests the first key and value rows
+    before it reads the position: rows of the cache past the causal range
+    (here NaN and infinities, up to max_length) never reach the output. A
+    query with position -1 leaves its output as it was."""
+    rt, L, stream = env
+    rng = np.random.default_rng(length + width)
+    max_length = 256
+    q_stride = (heads + 2 * kv_heads) * width
+    count += 1   # query 0 has no causal range at all
+    q = rng.standard_normal((count, q_stride)).astype(np.float32)
+    keys = rng.standard_normal((max_length, kv_heads * width)).astype(np.float32)
+    values = rng.standard_normal((max_length, kv_heads * width)).astype(np.float32)
+    keys[length:] = np.nan
+    values[length:] = np.nan
+    values[length::3] = np.inf
+    positions = np.concatenate([[-1], np.arange(length - count + 1, length)]).astype(np.int32)
+    scale = float(1 / np.sqrt(np.float32(width)))
+    sentinel = np.full(heads * width, 7.0, np.float32)
+    dev = Dev(rt)
+    try:
+        qd, kd, vd, pd = dev.put(q), dev.put(keys), dev.put(values), dev.put(positions)
+        od = dev.put(np.tile(sentinel, count))
+        assert L.nya_hip_attention(qd, q_stride, kd, vd, od, 0, pd, count, heads, kv_heads, width, max_length, 0,
+                                   scale, stream) == 0
+        rt.sync(stream)
+        got = dev.get(od, np.empty(count * heads * width, np.float32)).reshape(count, -1)
+        assert np.array_equal(got[0], sentinel)
+        for i in range(1, count):
+            ref = attention_ref(q[i, :heads * width], keys, values, heads, kv_heads, width, int(positions[i]) + 1,
+                                np.float32(scale))
+            assert np.all(np.isfinite(got[i]))
+            assert scaled_error(got[i], ref) <= 1e-5
+    finally:
+        dev.close()
+
+
 SPLIT_CASES = [(32, 8, 128, 4096, 1, 64, 0), (32, 4, 64, 1000, 1, 16, 0), (8, 8, 128, 300, 1, 8, 0),
                (16, 8, 128, 2000, 3, 32, 0), (8, 2, 256, 5000, 2, 8, 0), (32, 4, 64, 20000, 1, 32, 0),
                (32, 8, 128, 5, 1, 64, 0), (32, 8, 128, 257, 33, 8, 0), (8, 2, 128, 600, 2, 300, 0),

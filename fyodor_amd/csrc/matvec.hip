@@ -401,13 +401,11 @@ __device__ __forceinline__ float4 scale4(float4 h, float scale, float4 g)
     return make_float4(h.x * scale * g.x, h.y * scale * g.y, h.z * scale * g.z, h.w * scale * g.w);
 }
 
-// A wavefront's sum of one double per lane, lanes l and l ^ o paired for
-// o = 32, 16, .., 1 as the norm step pairs them (every lane ends with the
-// same value).
+// A wavefront's sum of one double per lane in the norm step's order
+// (wave_sum; every lane ends with the same value).
 __device__ __forceinline__ double wave_sum_pairs(double s)
 {
-    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
-    return s;
+    return wave_sum(s);
 }
 
 // The norm step's scale from its 16 wavefronts' sums of squares, in order.

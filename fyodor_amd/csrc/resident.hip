@@ -14,6 +14,7 @@
 // sequence of launches serves any token (and can be recorded once).
 #include <math.h>
 
+#include "device.h"
 #include "kernels.h"
 
 #pragma clang fp contract(off)
@@ -74,84 +75,6 @@ __global__ __launch_bounds__(256) void embed(const uint8_t *__restrict__ w, unsi
     const uint8_t *r = w + (size_t)token * row_bytes;
     for (int i = blockIdx.x * 256 + threadIdx.x; i < cols; i += gridDim.x * 256)
         o[i] = token < (uint32_t)rows ? element(r, type, i) * scale : 0.f;
-}
-
-// Cross-lane reductions without LDS: DPP moves inside a row of 16 lanes
-// (gfx9 controls 0xB1 quad_perm [1,0,3,2], 0x4E quad_perm [2,3,0,1], 0x141
-// row_half_mirror, 0x140 row_mirror; each lane reads a lane of its own
-// row), then v_readlane across the four rows of a wavefront. (A __shfl_xor
-// is a ds_bpermute: one LDS round trip per step, each waited for before the
-// next.) Every lane of the row, or of the wavefront for the wave forms,
-// must be active.
-template <int CTRL>
-__device__ __forceinline__ float row_lane(float v)
-{
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
-template <int CTRL>
-__device__ __forceinline__ double row_lane(double v)
-{
-    const uint64_t b = __builtin_bit_cast(uint64_t, v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xF, 0xF, false);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, false);
-    return __builtin_bit_cast(double, (uint64_t)hi << 32 | lo);
-}
-
-// The sum (MAX: the maximum) over the 16 lanes of an aligned row, the same
-// bits in each of them: pairs, quads, half rows, the row (each step adds two
-// values in either order, which is the same sum).
-template <bool MAX>
-__device__ __forceinline__ float row16_reduce(float v)
-{
-    if constexpr (MAX) {
-        v = fmaxf(v, row_lane<0xB1>(v));
-        v = fmaxf(v, row_lane<0x4E>(v));
-        v = fmaxf(v, row_lane<0x141>(v));
-        return fmaxf(v, row_lane<0x140>(v));
-    } else {
-        v += row_lane<0xB1>(v);
-        v += row_lane<0x4E>(v);
-        v += row_lane<0x141>(v);
-        return v + row_lane<0x140>(v);
-    }
-}
-
-__device__ __forceinline__ double row16_sum(double v)
-{
-    v += row_lane<0xB1>(v);
-    v += row_lane<0x4E>(v);
-    v += row_lane<0x141>(v);
-    return v + row_lane<0x140>(v);
-}
-
-__device__ __forceinline__ float lane_value(float v, int lane)
-{
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
-}
-
-__device__ __forceinline__ double lane_value(double v, int lane)
-{
-    const uint64_t b = __builtin_bit_cast(uint64_t, v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, lane);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), lane);
-    return __builtin_bit_cast(double, (uint64_t)hi << 32 | lo);
-}
-
-// Over the wavefront, the same value in every lane: each row's, then the
-// rows' as (r0 . r1) . (r2 . r3).
-template <bool MAX>
-__device__ __forceinline__ float wave_reduce(float v)
-{
-    v = row16_reduce<MAX>(v);
-    const float r0 = lane_value(v, 0), r1 = lane_value(v, 16), r2 = lane_value(v, 32), r3 = lane_value(v, 48);
-    return MAX ? fmaxf(fmaxf(r0, r1), fmaxf(r2, r3)) : (r0 + r1) + (r2 + r3);
-}
-
-__device__ __forceinline__ double wave_sum(double v)
-{
-    v = row16_sum(v);
-    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
 // One workgroup of 1024 per row (token), holding n <= 4096 K elements in

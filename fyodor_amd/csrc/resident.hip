@@ -249,35 +249,40 @@ __global__ __launch_bounds__(256) void head_norm_rope(float *__restrict__ q, int
 {
     __shared__ double part[4];
     __shared__ float row[kHeadWidthMax];
-    const int position = positions[blockIdx.y];
-    if (position < 0 || position >= capacity) return;
     const int h = blockIdx.x, j = threadIdx.x, half = width / 2;
     const int kind = h < heads ? 0 : h < heads + kv_heads ? 1 : 2;   // q, k, v
     const int hh = kind == 0 ? h : kind == 1 ? h - heads : h - heads - kv_heads;
-    const size_t slot = (size_t)position * kv_heads * width + (size_t)hh * width;
     const float *src = kind == 0 ? q + (size_t)blockIdx.y * q_stride + (size_t)hh * width
                      : kind == 1 ? k + (size_t)blockIdx.y * k_stride + (size_t)hh * width
                                  : v + (size_t)blockIdx.y * v_stride + (size_t)hh * width;
-    float *dst = kind == 0 ? q + (size_t)blockIdx.y * q_stride + (size_t)hh * width
-               : kind == 1 ? keys + slot : values + slot;
     const float *g = kind == 0 ? q_norm : kind == 1 ? k_norm : nullptr;
     const int j1 = j + 256;
+    // Every load first (none depends on the position; only where k and v
+    // go does), then the position: one memory round trip, not three.
     const float x0 = j < width ? src[j] : 0.f, x1 = j1 < width ? src[j1] : 0.f;
+    const float g0 = g && j < width ? g[j] : 1.0f, g1 = g && j1 < width ? g[j1] : 1.0f;
+    const float f = kind != 2 && j < half ? freq[j] : 0.f;
+    __builtin_amdgcn_sched_barrier(0);
+    const int position = positions[blockIdx.y];
+    const bool stored = position >= 0 && position < capacity;   // else nothing is written
+    const size_t slot = (size_t)(stored ? position : 0) * kv_heads * width + (size_t)hh * width;
+    float *dst = kind == 0 ? q + (size_t)blockIdx.y * q_stride + (size_t)hh * width
+               : kind == 1 ? keys + slot : values + slot;
     const double sq = (double)x0 * x0 + (double)x1 * x1;
     const float scale = (float)(1.0 / sqrt(group_sum<4>(sq, part) / (double)width + (double)eps));
-    const float y0 = x0 * scale * (g && j < width ? g[j] : 1.0f);
-    const float y1 = x1 * scale * (g && j1 < width ? g[j1] : 1.0f);
+    const float y0 = x0 * scale * g0;
+    const float y1 = x1 * scale * g1;
     if (kind == 2) {
-        if (j < width) dst[j] = y0;
-        if (j1 < width) dst[j1] = y1;
+        if (stored && j < width) dst[j] = y0;
+        if (stored && j1 < width) dst[j1] = y1;
         return;
     }
     // q in place: every element was read before group_sum's barriers.
     if (j < width) row[j] = y0;
     if (j1 < width) row[j1] = y1;
     __syncthreads();
-    if (j < half) {
-        const float angle = (float)position * freq[j];
+    if (stored && j < half) {
+        const float angle = (float)position * f;
         const float c = cosf(angle), s = sinf(angle);
         const float a = row[j], b = row[j + half];
         dst[j] = a * c - b * s;

@@ -26,6 +26,9 @@ typedef struct nya_hip_runtime {
     hipError_t (*stream_create)(hipStream_t *, unsigned);
     hipError_t (*stream_destroy)(hipStream_t);
     hipError_t (*stream_wait)(hipStream_t);
+    /* Optional: the device address of mapped pinned memory; NULL leaves the
+     * resident plan downloading its logits with copy_async. */
+    hipError_t (*host_device_pointer)(void **, void *, unsigned);
 } nya_hip_runtime;
 
 /* libamdhip64's stream capture and graphs. Optional: without them the
@@ -103,6 +106,9 @@ typedef struct nya_resident_ops {
      * up in two blocks of rows and its GELU gate a step of its own. */
     int (*matvec_geglu)(uintptr_t, unsigned, size_t, size_t, uintptr_t, uintptr_t, uintptr_t);
     int (*gelu_pairs)(uintptr_t, uintptr_t, size_t, size_t, uintptr_t);
+    /* Optional (with host_device_pointer): the logits written into the
+     * mapped pinned staging by the plan's last launch, no copy call. */
+    int (*copy)(uintptr_t, uintptr_t, size_t, uintptr_t);
 } nya_resident_ops;
 
 #define NYA_KERNEL_ABI 2U

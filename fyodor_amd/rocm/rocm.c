@@ -404,6 +404,10 @@ static int bind_all(session *s)
         nya_vendor_symbol(s->kernel_module, "nya_hip_gelu_pairs", &s->resident.gelu_pairs,
                           sizeof s->resident.gelu_pairs))
         s->resident.matvec_geglu = NULL, s->resident.gelu_pairs = NULL;
+    if (nya_vendor_symbol(s->hip_module, "hipHostGetDevicePointer", &s->hip.host_device_pointer,
+                          sizeof s->hip.host_device_pointer) ||
+        nya_vendor_symbol(s->kernel_module, "nya_hip_copy", &s->resident.copy, sizeof s->resident.copy))
+        s->hip.host_device_pointer = NULL, s->resident.copy = NULL;
     const struct { const char *symbol; void *slot; size_t size; } graphs[] = {
         {"hipStreamBeginCapture", &s->graphs.begin_capture, sizeof s->graphs.begin_capture},
         {"hipStreamEndCapture", &s->graphs.end_capture, sizeof s->graphs.end_capture},

@@ -111,11 +111,22 @@ API hipError_t hipFree(void *ptr)
     return OK;
 }
 
+/* Flags: none, or mapped (0x2) and coherent (0x40000000), alone or
+ * together; anything else is refused. */
 API hipError_t hipHostMalloc(void **ptr, size_t size, unsigned flags)
 {
-    if (injected_fault() || flags) return flags ? INVALID_VALUE : OUT_OF_MEMORY;
+    if (flags & ~(0x2u | 0x40000000u)) return INVALID_VALUE;
+    if (injected_fault()) return OUT_OF_MEMORY;
     *ptr = obtain(size);
     return *ptr ? OK : OUT_OF_MEMORY;
+}
+
+/* Host memory is device memory here: the same address. */
+API hipError_t hipHostGetDevicePointer(void **device, void *host, unsigned flags)
+{
+    if (!device || !host || flags) return INVALID_VALUE;
+    *device = host;
+    return OK;
 }
 
 API hipError_t hipHostFree(void *ptr)
@@ -369,6 +380,15 @@ static size_t mock_row_bytes(unsigned type, size_t cols)
     size_t block, bytes;
     if (blocks(type, &block, &bytes) || cols % block) return 0;
     return cols / block * bytes;
+}
+
+/* nya_hip_copy: 16-byte aligned pointers and a 16-byte multiple. */
+API int nya_hip_copy(uintptr_t dst, uintptr_t src, size_t bytes, uintptr_t stream)
+{
+    (void)stream;
+    if (!dst || !src || (dst & 15u) || (src & 15u) || (bytes & 15u)) return 1;
+    memmove((void *)dst, (const void *)src, bytes);
+    return 0;
 }
 
 API int nya_hip_step(uintptr_t step, unsigned token, size_t position, uintptr_t stream)

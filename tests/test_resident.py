@@ -121,6 +121,26 @@ def mock_without(tmp_path, entries):
     return plain
 
 
+def test_logits_written_into_mapped_staging(session_lib, tmp_path, monkeypatch):
+    """With the runtime's device address of mapped pinned memory and the
+    kernel library's copy, each run's logits reach the host through one more
+    launch at the end of its forward (no copy call after it); a kernel
+    library without nya_hip_copy leaves the plan downloading them with a copy
+    call. The logits meet the engine's either way."""
+    shape = LlamaShape(context=16)
+    path = tmp_path / "model.gguf"
+    write(path, shape)
+    mapped = compare(session_lib, path, shape, "rocm", TOKENS[:6])
+    monkeypatch.setenv("NYA_ROCM_KERNEL_LIBRARY", str(mock_without(tmp_path, ("nya_hip_copy",))))
+    copied = compare(session_lib, path, shape, "rocm", TOKENS[:6])
+    assert mapped["execution"] == copied["execution"] == "resident"
+    s, c = mapped["stats"], copied["stats"]
+    assert s.downloads == c.downloads > 0
+    # One launch per run that returns logits: six decode tokens, then the
+    # five runs of the chunk phase (compare's default chunks).
+    assert s.kernel_launches - c.kernel_launches == 6 + 5
+
+
 @pytest.mark.parametrize("entries,extra", [(("nya_hip_matvec_gated",), 1), (("nya_hip_matvec_normed_rope",), 1),
                                            (("nya_hip_matvec_normed", "nya_hip_matvec_normed_rope"), 2)])
 def test_plan_without_fused_step(session_lib, tmp_path, monkeypatch, entries, extra):

@@ -295,15 +295,17 @@ def test_attention(env, heads, kv_heads, width, length, count, window):
         dev.close()
 
 
-@pytest.mark.parametrize("heads,kv_heads,width,length,count", [
-    (32, 8, 128, 1, 1), (32, 8, 128, 37, 3), (8, 8, 64, 5, 2), (4, 1, 256, 20, 1), (4, 2, 512, 9, 2),
-    (32, 8, 128, 200, 1),
+@pytest.mark.parametrize("heads,kv_heads,width,length,count,window", [
+    (32, 8, 128, 1, 1, 0), (32, 8, 128, 37, 3, 0), (8, 8, 64, 5, 2, 0), (4, 1, 256, 20, 1, 0),
+    (4, 2, 512, 9, 2, 0), (32, 8, 128, 200, 1, 0), (32, 8, 128, 37, 3, 64), (8, 4, 128, 150, 3, 40),
+    (4, 2, 256, 90, 2, 16), (4, 2, 512, 30, 2, 8),
 ])
-def test_attention_ignores_rows_past_the_range(env, heads, kv_heads, width, length, count):
-    """Without a window the kernel requests the first key and value rows
-    before it reads the position: rows of the cache past the causal range
-    (here NaN and infinities, up to max_length) never reach the output. A
-    query with position -1 leaves its output as it was."""
+def test_attention_ignores_rows_past_the_range(env, heads, kv_heads, width, length, count, window):
+    """The kernel requests the first key and value rows from row 0 before it
+    reads the position (and again from the window's start once a window has
+    moved on): rows of the cache outside the causal range (here NaN and
+    infinities, before a window and past the range, up to max_length) never
+    reach the output. A query with position -1 leaves its output as it was."""
     rt, L, stream = env
     rng = np.random.default_rng(length + width)
     max_length = 256
@@ -312,24 +314,29 @@ def test_attention_ignores_rows_past_the_range(env, heads, kv_heads, width, leng
     q = rng.standard_normal((count, q_stride)).astype(np.float32)
     keys = rng.standard_normal((max_length, kv_heads * width)).astype(np.float32)
     values = rng.standard_normal((max_length, kv_heads * width)).astype(np.float32)
+    positions = np.concatenate([[-1], np.arange(length - count + 1, length)]).astype(np.int32)
     keys[length:] = np.nan
     values[length:] = np.nan
     values[length::3] = np.inf
-    positions = np.concatenate([[-1], np.arange(length - count + 1, length)]).astype(np.int32)
+    if window:
+        # Before the earliest query's window.
+        before = max(0, int(positions[1]) + 1 - window)
+        keys[:before] = np.nan
+        values[:before] = -np.inf
     scale = float(1 / np.sqrt(np.float32(width)))
     sentinel = np.full(heads * width, 7.0, np.float32)
     dev = Dev(rt)
     try:
         qd, kd, vd, pd = dev.put(q), dev.put(keys), dev.put(values), dev.put(positions)
         od = dev.put(np.tile(sentinel, count))
-        assert L.nya_hip_attention(qd, q_stride, kd, vd, od, 0, pd, count, heads, kv_heads, width, max_length, 0,
-                                   scale, stream) == 0
+        assert L.nya_hip_attention(qd, q_stride, kd, vd, od, 0, pd, count, heads, kv_heads, width, max_length,
+                                   window, scale, stream) == 0
         rt.sync(stream)
         got = dev.get(od, np.empty(count * heads * width, np.float32)).reshape(count, -1)
         assert np.array_equal(got[0], sentinel)
         for i in range(1, count):
             ref = attention_ref(q[i, :heads * width], keys, values, heads, kv_heads, width, int(positions[i]) + 1,
-                                np.float32(scale))
+                                np.float32(scale), window)
             assert np.all(np.isfinite(got[i]))
             assert scaled_error(got[i], ref) <= 1e-5
     finally:

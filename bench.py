@@ -434,7 +434,7 @@ def cpu_baseline(weights_host: np.ndarray, x: np.ndarray, y_gpu: np.ndarray, sec
     process may run on, and at one thread. The weights rotate over enough
     host copies to exceed twice the host's L3."""
     sys.path.insert(0, str(REPO))
-    from oracle import Oracle, Reference  # the checker; only this leg uses it
+    from oracle import Oracle, Reference  # the oracle; only this leg uses it
 
     host = host_cpu()
     default_threads = min(host["online_cpus"], 64)
@@ -878,7 +878,7 @@ def main() -> int:
                     help="time every decode, small-N and prefill configuration instead (one JSON line each)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (a matrix's rows would be "
+        print("bench.py measures one GPU: this library has no multi-GPU path (a matrix's rows would be "
               "sharded across GPUs with no exchange between them). Run with --gpus 1.", file=sys.stderr)
         return 2
 

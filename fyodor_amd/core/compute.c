@@ -1,6 +1,6 @@
 /* Compute dispatch layer for the ROCm provider (backend/core/compute.c:1-152).
  *
- * The engine's own compute.c lists every compiled provider; this build
+ * The engine's own compute.c lists every compiled provider; this library
  * compiles one, the ROCm provider, so "rocm" is the only name that creates a
  * context. Every entry point forwards through the provider table and yields
  * -1 / NULL when the provider is missing or has failed, which is the signal
@@ -44,7 +44,7 @@ int nya_compute_backend_compiled(const char *provider)
     return provider_named(provider) != NULL;
 }
 
-/* backend/core/compute.c:59-72: NULL selects "cpu", which this build does
+/* backend/core/compute.c:59-72: NULL selects "cpu", which this library does
  * not compile, so the caller keeps its own CPU kernels. */
 nya_compute_context *nya_compute_create_for(const char *selection)
 {
@@ -153,7 +153,7 @@ int nya_compute_plan_read_kv(nya_compute_plan *p, size_t layer, size_t position,
 }
 
 /* ---- batched verification and greedy speculative decoding ----------------
- * Extensions of this build (no slot in the engine's provider table): they
+ * Extensions of this library (no slot in the engine's provider table): they
  * reach the ROCm provider's plan directly. */
 
 static int rocm_plan(const nya_compute_plan *p)

@@ -1,7 +1,7 @@
 /* TEST INFRASTRUCTURE ONLY: the parity oracle of the quantized matrix path.
  *
  * A plain-C restatement of the reference CPU path, used by tests/, by
- * __graft_entry__.smoke() and by bench.py's CPU-baseline leg as the checker.
+ * __graft_entry__.smoke() and by bench.py's CPU-baseline leg as the oracle.
  * Nothing in the product (fyodor_amd/) links, loads or calls it.
  *
  * Each function follows the reference file:line it names, including the

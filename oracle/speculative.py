@@ -1,5 +1,5 @@
 """TEST INFRASTRUCTURE ONLY: the engine's sampler and its speculative
-sampling loop, restated in Python as the checker of
+sampling loop, restated in Python as the oracle of
 nya_compute_generate_sampled. Only tests/ use it; the product never does.
 
 Each function follows the reference lines it names, with the same float /
@@ -10,7 +10,7 @@ the ones the C code gets), and the engine's random stream.
 The loop takes its logits from two callables, so the same rule runs on any
 source of logits: the engine's own scalar sessions (which pins this
 restatement to the engine's nya_llm_generate_draft token for token,
-tests/test_sampling_oracle.py) or a provider's plans (the checker of the
+tests/test_sampling_oracle.py) or a provider's plans (the oracle of the
 batched implementation).
 
 Pinning (tests/test_sampling_oracle.py):

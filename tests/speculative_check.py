@@ -283,7 +283,7 @@ def sampled_generation_matches_oracle(target_shape: fm.LlamaShape, draft: str, p
 
 def first_token_follows_target(target_shape: fm.LlamaShape, prompt, runs: int, window: int = 4):
     """The engine's distribution check (backend/tests/test_generation.c
-    :345-365) on this build: with top-k 2, a temperature giving the leading
+    :345-365) on the ROCm provider's plans: with top-k 2, a temperature giving the leading
     candidate p = 3/4, and a draft favouring the other candidate, the
     first token over `runs` seeds follows the target's two-candidate
     distribution (within five standard deviations), and both acceptance and

@@ -141,6 +141,20 @@ def test_logits_written_into_mapped_staging(session_lib, tmp_path, monkeypatch):
     assert s.kernel_launches - c.kernel_launches == 6 + 5
 
 
+def test_logits_downloaded_when_the_row_is_not_whole_16_bytes(session_lib, tmp_path, monkeypatch):
+    """A vocabulary of 1001 entries (4004 bytes a row, not a multiple of the
+    copy kernel's 16) keeps the copy call: the same launches as a kernel
+    library without nya_hip_copy, and the engine's logits."""
+    shape = LlamaShape(context=16, vocabulary=1001)
+    path = tmp_path / "model.gguf"
+    write(path, shape)
+    plain = compare(session_lib, path, shape, "rocm", TOKENS[:6])
+    monkeypatch.setenv("NYA_ROCM_KERNEL_LIBRARY", str(mock_without(tmp_path, ("nya_hip_copy",))))
+    copied = compare(session_lib, path, shape, "rocm", TOKENS[:6])
+    assert plain["execution"] == copied["execution"] == "resident"
+    assert plain["stats"].kernel_launches == copied["stats"].kernel_launches
+
+
 @pytest.mark.parametrize("entries,extra", [(("nya_hip_matvec_gated",), 1), (("nya_hip_matvec_normed_rope",), 1),
                                            (("nya_hip_matvec_normed", "nya_hip_matvec_normed_rope"), 2)])
 def test_plan_without_fused_step(session_lib, tmp_path, monkeypatch, entries, extra):

@@ -60,6 +60,20 @@ def test_resident_plan_on_gpu(session_lib, rocm_env, tmp_path, types):
     assert s.kernel_launches > 0 and s.external_matmul_calls > 0 and s.kv_bytes > 0
 
 
+def test_logits_copy_call_on_gpu(session_lib, rocm_env, tmp_path):
+    """A vocabulary of 1001 entries (rows of 4004 bytes, not whole 16-byte
+    units for the copy kernel into the mapped staging) takes the logits
+    download with a copy call instead; decode and prompt chunks against the
+    engine, graphs on."""
+    shape = LlamaShape(embedding=512, heads=8, kv_heads=2, hidden=1024, blocks=2, context=64, vocabulary=1001,
+                       seed=5)
+    path = tmp_path / "model.gguf"
+    write(path, shape)
+    out = compare(session_lib, path, shape, "rocm", TOKENS[:20], chunks=(9, 1, 1))
+    print(f"vocabulary 1001: worst scaled logit error {out['logit']:.3g}, KV {out['kv']:.3g}", flush=True)
+    assert out["execution"] == "resident"
+
+
 # The decoder shapes bench.py times (its resident legs): TinyLlama 1.1B and
 # the 8B class, each with its own per-block matrices, head layout,
 # vocabulary and Q4_K/Q6_K mix, at fewer blocks than the real models (the

@@ -33,6 +33,7 @@ enum { STREAM_NON_BLOCKING = 1 };     /* hipStreamNonBlocking */
 float orc_value(const unsigned char *data, unsigned type, size_t index);
 
 static struct {
+    int d2h;            /* device-to-host copy calls so far */
     int outstanding;    /* allocations (device, pinned) and streams not yet released */
     int armed;          /* the armed-th fallible call from now fails (0: none) */
     int fallible;       /* fallible calls made so far */
@@ -63,6 +64,7 @@ static void give_back(void *p)
 API void nya_mock_arm_fault(int n) { state.armed = n; }
 API int nya_mock_outstanding(void) { return state.outstanding; }
 API int nya_mock_calls(void) { return state.fallible; }
+API int nya_mock_d2h_copies(void) { return state.d2h; }
 
 API hipError_t hipInit(unsigned flags)
 {
@@ -139,6 +141,7 @@ API hipError_t hipMemcpyAsync(void *dst, const void *src, size_t bytes, int kind
 {
     if (injected_fault()) return INVALID_VALUE;
     if (!stream || (kind != H2D && kind != D2H)) return INVALID_VALUE;
+    if (kind == D2H) ++state.d2h;
     memcpy(dst, src, bytes);
     return OK;
 }

@@ -121,24 +121,40 @@ def mock_without(tmp_path, entries):
     return plain
 
 
-def test_logits_written_into_mapped_staging(session_lib, tmp_path, monkeypatch):
+@pytest.mark.parametrize("family", ["llama", "gemma"])
+def test_logits_written_into_mapped_staging(session_lib, mock_paths, tmp_path, monkeypatch, family):
     """With the runtime's device address of mapped pinned memory and the
-    kernel library's copy, each run's logits reach the host through one more
-    launch at the end of its forward (no copy call after it); a kernel
-    library without nya_hip_copy leaves the plan downloading them with a copy
-    call. The logits meet the engine's either way."""
-    shape = LlamaShape(context=16)
-    path = tmp_path / "model.gguf"
-    write(path, shape)
+    kernel library's copy, each run's logits reach the host without a copy
+    call: the vocabulary product writes the mapped staging itself (LLaMA),
+    or one copy launch follows Gemma's soft cap. A kernel library without
+    nya_hip_copy leaves the plan downloading them with a copy call. The
+    logits meet the engine's either way."""
+    import ctypes
+    runtime = ctypes.CDLL(str(mock_paths[0]))   # the HIP runtime in both runs
+    if family == "gemma":
+        shape = GemmaShape(context=16)   # the default test model: a soft cap of 30
+        assert shape.softcap > 0
+        path = tmp_path / "gemma.gguf"
+        write_gemma(path, shape)
+    else:
+        shape = LlamaShape(context=16)
+        path = tmp_path / "model.gguf"
+        write(path, shape)
+    before = runtime.nya_mock_d2h_copies()
     mapped = compare(session_lib, path, shape, "rocm", TOKENS[:6])
+    mapped_d2h = runtime.nya_mock_d2h_copies() - before
     monkeypatch.setenv("NYA_ROCM_KERNEL_LIBRARY", str(mock_without(tmp_path, ("nya_hip_copy",))))
+    before = runtime.nya_mock_d2h_copies()
     copied = compare(session_lib, path, shape, "rocm", TOKENS[:6])
+    copied_d2h = runtime.nya_mock_d2h_copies() - before
     assert mapped["execution"] == copied["execution"] == "resident"
     s, c = mapped["stats"], copied["stats"]
     assert s.downloads == c.downloads > 0
-    # One launch per run that returns logits: six decode tokens, then the
-    # five runs of the chunk phase (compare's default chunks).
-    assert s.kernel_launches - c.kernel_launches == 6 + 5
+    # Runs that return logits: six decode tokens, then the five runs of the
+    # chunk phase (compare's default chunks); each is a copy call fewer.
+    runs = 6 + 5
+    assert copied_d2h - mapped_d2h == runs
+    assert s.kernel_launches - c.kernel_launches == (runs if family == "gemma" else 0)
 
 
 def test_logits_downloaded_when_the_row_is_not_whole_16_bytes(session_lib, tmp_path, monkeypatch):
